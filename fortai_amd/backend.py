@@ -1,0 +1,356 @@
+"""ctypes mirror of the gfx950 C ABI (include/fortai_hip_backend.h).
+
+Python counterpart of the reference's iso_c_binding wrapper
+(src/backend/cuda/fortai_backend_cuda.f90): opaque handles with create /
+destroy, and every nonzero return code raised as ``BackendError`` with the
+context's last error message (the wrapper maps them to status_t,
+fortai_backend_cuda.f90:418-431).  There is no CPU fallback: if
+``libfortai_hip.so`` is missing or no GPU is visible, creating a context raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libfortai_hip.so")
+
+OK, INVALID, RUNTIME_ERROR = 0, 1, 2
+
+_vp, _i, _i64, _sz, _f = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
+_fp, _i64p, _u16p = C.POINTER(C.c_float), C.POINTER(C.c_int64), C.POINTER(C.c_uint16)
+_vpp = C.POINTER(C.c_void_p)
+
+# name -> argtypes (all return int unless listed in _RESTYPE)
+_SIGNATURES = {
+    "fortai_hip_q8_context_create": [_i, _vpp],
+    "fortai_hip_q8_context_destroy": [_vp],
+    "fortai_hip_q8_context_set_position": [_vp, _i],
+    "fortai_hip_q8_context_capture_begin": [_vp],
+    "fortai_hip_q8_context_capture_end": [_vp],
+    "fortai_hip_q8_context_graph_launch": [_vp],
+    "fortai_hip_q8_context_synchronize": [_vp],
+    "fortai_hip_q8_weights_upload": [_vp, _vp, _sz, _i, _i, _vpp],
+    "fortai_hip_q8_weights_destroy": [_vp],
+    "fortai_hip_q8_device_buffer_create": [_vp, _sz, _vpp],
+    "fortai_hip_q8_device_buffer_destroy": [_vp, _vp],
+    "fortai_hip_q8_device_buffer_upload": [_vp, _vp, _vp, _sz],
+    "fortai_hip_q8_device_buffer_upload_ptr": [_vp, _vp, _vp, _sz],
+    "fortai_hip_q8_device_buffer_download": [_vp, _vp, _vp, _sz],
+    "fortai_hip_q8_matvec_resident": [_vp, _vp, _vp, _vp, _fp],
+    "fortai_hip_q8_matvec_device_f32": [_vp, _vp, _vp, _sz, _vp, _sz],
+    "fortai_hip_qwen35_embedding_device": [_vp, _vp, _i64, _vp, _sz],
+    "fortai_hip_qwen35_copy_device": [_vp, _vp, _vp, _sz],
+    "fortai_hip_qwen35_add_device": [_vp, _vp, _vp, _vp, _sz],
+    "fortai_hip_qwen35_rms_norm_device": [_vp, _vp, _vp, _vp, _sz, _f],
+    "fortai_hip_q8_matvec_host": [_vp, _vp, _vp, _sz, _vp, _sz, _fp],
+    "fortai_hip_q8_matvec_host_pair": [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp, _sz, _fp],
+    "fortai_hip_q8_matvec_host_triplet": [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _fp],
+    "fortai_hip_q8_matvec_host_triplet_contiguous": [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _fp],
+    "fortai_hip_q8_ffn_host": [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _fp],
+    "fortai_hip_q8_ffn_device": [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz],
+    "fortai_hip_qwen35_recurrent_create": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _vp, _sz, _vp, _sz,
+                                           _vp, _sz, _i, _i, _i, _i, _i, _f, _vpp],
+    "fortai_hip_qwen35_recurrent_destroy": [_vp],
+    "fortai_hip_qwen35_recurrent_reset": [_vp],
+    "fortai_hip_qwen35_recurrent_run": [_vp, _vp, _sz, _vp, _sz, _fp],
+    "fortai_hip_qwen35_recurrent_run_device": [_vp, _vp, _sz, _vp, _sz],
+    "fortai_hip_qwen35_attention_create": [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _i, _i, _i, _i, _i,
+                                           _f, _f, _vpp],
+    "fortai_hip_qwen35_attention_destroy": [_vp],
+    "fortai_hip_qwen35_attention_reset": [_vp],
+    "fortai_hip_qwen35_attention_run_device": [_vp, _vp, _sz, _i, _vp, _sz],
+    "fortai_hip_q8_last_error": [_vp],
+    "fortai_hip_f16_weights_upload": [_vp, _vp, _sz, _i, _i, _vpp],
+    "fortai_hip_f16_weights_destroy": [_vp],
+    "fortai_hip_f16_matvec_device": [_vp, _vp, _vp, _sz, _vp, _sz, _vp],
+    "fortai_hip_qwen35_embedding_f16_device": [_vp, _vp, _i64, _vp, _sz],
+    "fortai_hip_argmax_device": [_vp, _vp, _sz, _vp],
+    "fortai_hip_q8_quantize_device": [_vp, _vp, _sz, _vp, _vp],
+    "fortai_hip_q8_block_dots_device": [_vp, _vp, _vp, _vp],
+    "fortai_hip_qwen35_recurrent_core_device": [_vp, _vp, _vp, _vp, _vp],
+    "fortai_hip_qwen35_recurrent_state_download": [_vp, _vp, _sz, _vp, _sz],
+    "fortai_hip_qwen35_recurrent_state_upload": [_vp, _vp, _sz, _vp, _sz],
+    "fortai_hip_qwen35_attention_core_device": [_vp, _vp, _vp, _vp, _vp],
+    "fortai_hip_qwen35_attention_cache_download": [_vp, _vp, _vp, _i],
+    "fortai_hip_qwen35_attention_cache_upload": [_vp, _vp, _vp, _i],
+    "fortai_hip_qwen35_decoder_create": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,
+                                         _i, _f, _vpp],
+    "fortai_hip_qwen35_decoder_destroy": [_vp],
+    "fortai_hip_qwen35_decoder_reset": [_vp],
+    "fortai_hip_qwen35_decoder_forward": [_vp, _i64, _i, _vp, _vp],
+    "fortai_hip_qwen35_decoder_generate": [_vp, _i64, _i, _i, _vp],
+    "fortai_hip_qwen35_decoder_replay": [_vp, _i],
+    "fortai_hip_qwen35_decoder_logits": [_vp, _vpp],
+}
+_RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p}
+
+_lib: Optional[C.CDLL] = None
+
+
+class BackendError(RuntimeError):
+    def __init__(self, code: int, what: str, message: str = ""):
+        super().__init__(f"{what} failed with code {code}" + (f": {message}" if message else ""))
+        self.code = code
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load libfortai_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is missing: run fortai_amd.build.build() (no CPU fallback exists)")
+    lib = C.CDLL(path)
+    for name, args in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, C.c_int)
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> Sequence[str]:
+    return list(_SIGNATURES)
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data)
+
+
+class Context:
+    """A device context: stream, device position/token, scratch (fortai_cuda_q8_context)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load()
+        h = C.c_void_p()
+        rc = self.lib.fortai_hip_q8_context_create(device, C.byref(h))
+        if rc != OK:
+            raise BackendError(rc, "fortai_hip_q8_context_create (is a GPU visible?)")
+        self.h = h
+
+    def check(self, rc: int, what: str) -> None:
+        if rc != OK:
+            msg = self.lib.fortai_hip_q8_last_error(self.h)
+            raise BackendError(rc, what, msg.decode() if msg else "")
+
+    def call(self, name: str, *args) -> None:
+        self.check(getattr(self.lib, name)(*args), name)
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.fortai_hip_q8_context_destroy(self.h)
+            self.h = None
+
+    def set_position(self, position: int) -> None:
+        self.call("fortai_hip_q8_context_set_position", self.h, position)
+
+    def synchronize(self) -> None:
+        self.call("fortai_hip_q8_context_synchronize", self.h)
+
+    # ---- device buffers
+    def alloc(self, nbytes: int) -> "DeviceBuffer":
+        return DeviceBuffer(self, nbytes)
+
+    def upload_array(self, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = DeviceBuffer(self, max(a.nbytes, 1))
+        buf.upload(a)
+        return buf
+
+
+class DeviceBuffer:
+    def __init__(self, ctx: Context, nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        h = C.c_void_p()
+        ctx.call("fortai_hip_q8_device_buffer_create", ctx.h, self.nbytes, C.byref(h))
+        self.h = h
+
+    @property
+    def ptr(self) -> C.c_void_p:
+        return self.h
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError("upload larger than the buffer")
+        self.ctx.call("fortai_hip_q8_device_buffer_upload", self.ctx.h, self.h, _ptr(a), a.nbytes)
+
+    def download(self, dtype, count: Optional[int] = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype=dtype)
+        self.ctx.call("fortai_hip_q8_device_buffer_download", self.ctx.h, _ptr(out), self.h, out.nbytes)
+        return out
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.fortai_hip_q8_device_buffer_destroy(self.ctx.h, self.h)
+            self.h = None
+
+
+class Q8Weights:
+    """Resident Q8_0 matrix (GGUF bytes [rows][width/32][34])."""
+
+    def __init__(self, ctx: Context, gguf_bytes: np.ndarray, rows: int, width: int):
+        self.ctx, self.rows, self.width = ctx, rows, width
+        data = np.ascontiguousarray(gguf_bytes).view(np.uint8)
+        h = C.c_void_p()
+        ctx.call("fortai_hip_q8_weights_upload", ctx.h, _ptr(data), data.nbytes, rows, width, C.byref(h))
+        self.h = h
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.fortai_hip_q8_weights_destroy(self.h)
+            self.h = None
+
+
+class F16Weights:
+    """Resident fp16 matrix (GGUF F16 row-major [rows][width])."""
+
+    def __init__(self, ctx: Context, bits: np.ndarray, rows: int, width: int):
+        self.ctx, self.rows, self.width = ctx, rows, width
+        data = np.ascontiguousarray(bits).view(np.uint16)
+        h = C.c_void_p()
+        ctx.call("fortai_hip_f16_weights_upload", ctx.h, _ptr(data), data.nbytes, rows, width, C.byref(h))
+        self.h = h
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.fortai_hip_f16_weights_destroy(self.h)
+            self.h = None
+
+
+class Recurrent:
+    """Qwen3.5 Gated DeltaNet layer (fortai_cuda_qwen35_recurrent)."""
+
+    def __init__(self, ctx: Context, qkv: Q8Weights, gate: Q8Weights, alpha: Q8Weights, beta: Q8Weights,
+                 out: Q8Weights, conv_w: np.ndarray, conv_size: int, conv_kernel: int, ssm_a: np.ndarray,
+                 ssm_dt: np.ndarray, ssm_norm: np.ndarray, state_size: int, key_heads: int, value_heads: int,
+                 head_size: int, inner_size: int, eps: float):
+        self.ctx = ctx
+        self.dims = dict(conv_size=conv_size, conv_kernel=conv_kernel, state_size=state_size, key_heads=key_heads,
+                         value_heads=value_heads, head_size=head_size, inner_size=inner_size)
+        arrays = [np.ascontiguousarray(a, dtype=np.float32) for a in (conv_w, ssm_a, ssm_dt, ssm_norm)]
+        h = C.c_void_p()
+        ctx.call("fortai_hip_qwen35_recurrent_create", ctx.h, qkv.h, gate.h, alpha.h, beta.h, out.h,
+                 _ptr(arrays[0]), arrays[0].nbytes, conv_size, conv_kernel, _ptr(arrays[1]), arrays[1].nbytes,
+                 _ptr(arrays[2]), arrays[2].nbytes, _ptr(arrays[3]), arrays[3].nbytes, state_size, key_heads,
+                 value_heads, head_size, inner_size, eps, C.byref(h))
+        self.h = h
+
+    def reset(self) -> None:
+        self.ctx.call("fortai_hip_qwen35_recurrent_reset", self.h)
+
+    def state(self):
+        d = self.dims
+        gdn = np.empty(d["value_heads"] * d["head_size"] ** 2, dtype=np.float32)
+        conv = np.empty((d["conv_kernel"] - 1) * d["conv_size"], dtype=np.float32)
+        self.ctx.call("fortai_hip_qwen35_recurrent_state_download", self.h, _ptr(gdn), gdn.nbytes, _ptr(conv),
+                      conv.nbytes)
+        return gdn, conv
+
+    def set_state(self, gdn: np.ndarray, conv: np.ndarray) -> None:
+        gdn = np.ascontiguousarray(gdn, dtype=np.float32)
+        conv = np.ascontiguousarray(conv, dtype=np.float32)
+        self.ctx.call("fortai_hip_qwen35_recurrent_state_upload", self.h, _ptr(gdn), gdn.nbytes, _ptr(conv),
+                      conv.nbytes)
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.fortai_hip_qwen35_recurrent_destroy(self.h)
+            self.h = None
+
+
+class Attention:
+    """Qwen3.5 gated full-attention layer (fortai_cuda_qwen35_attention)."""
+
+    def __init__(self, ctx: Context, q: Q8Weights, k: Q8Weights, v: Q8Weights, o: Q8Weights, q_norm: np.ndarray,
+                 k_norm: np.ndarray, heads: int, kv_heads: int, head_size: int, value_size: int, max_context: int,
+                 rope_dim: int, rope_base: float, eps: float):
+        self.ctx = ctx
+        self.dims = dict(heads=heads, kv_heads=kv_heads, head_size=head_size, value_size=value_size,
+                         max_context=max_context)
+        qn = np.ascontiguousarray(q_norm, dtype=np.float32)
+        kn = np.ascontiguousarray(k_norm, dtype=np.float32)
+        h = C.c_void_p()
+        ctx.call("fortai_hip_qwen35_attention_create", ctx.h, q.h, k.h, v.h, o.h, _ptr(qn), qn.nbytes, _ptr(kn),
+                 kn.nbytes, heads, kv_heads, head_size, value_size, max_context, rope_dim, rope_base, eps,
+                 C.byref(h))
+        self.h = h
+
+    def reset(self) -> None:
+        self.ctx.call("fortai_hip_qwen35_attention_reset", self.h)
+
+    def cache(self, positions: int):
+        d = self.dims
+        k = np.empty(positions * d["kv_heads"] * d["head_size"], dtype=np.uint16)
+        v = np.empty(positions * d["kv_heads"] * d["value_size"], dtype=np.uint16)
+        self.ctx.call("fortai_hip_qwen35_attention_cache_download", self.h, _ptr(k), _ptr(v), positions)
+        return k, v
+
+    def set_cache(self, k: np.ndarray, v: np.ndarray, positions: int) -> None:
+        k = np.ascontiguousarray(k, dtype=np.uint16)
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        self.ctx.call("fortai_hip_qwen35_attention_cache_upload", self.h, _ptr(k), _ptr(v), positions)
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.fortai_hip_qwen35_attention_destroy(self.h)
+            self.h = None
+
+
+class Decoder:
+    """Fused whole-token decoder (one captured HIP graph per step)."""
+
+    def __init__(self, ctx: Context, recurrent: Sequence[Optional[Recurrent]],
+                 attention: Sequence[Optional[Attention]], ffn_gate: Sequence[Q8Weights],
+                 ffn_up: Sequence[Q8Weights], ffn_down: Sequence[Q8Weights], attn_norm: Sequence[np.ndarray],
+                 post_norm: Sequence[np.ndarray], output_norm: np.ndarray, hidden: int,
+                 embedding, output, max_context: int, eps: float, vocab: int):
+        self.ctx, self.vocab, self.max_context = ctx, vocab, max_context
+        n = len(ffn_gate)
+
+        def harr(items):
+            return (C.c_void_p * n)(*[(x.h if x is not None else None) for x in items])
+
+        self._norms = [np.ascontiguousarray(a, dtype=np.float32) for a in list(attn_norm) + list(post_norm)]
+        an = (C.c_void_p * n)(*[_ptr(a) for a in self._norms[:n]])
+        pn = (C.c_void_p * n)(*[_ptr(a) for a in self._norms[n:]])
+        self._onorm = np.ascontiguousarray(output_norm, dtype=np.float32)
+        e16 = embedding.h if isinstance(embedding, F16Weights) else None
+        e8 = embedding.h if isinstance(embedding, Q8Weights) else None
+        o16 = output.h if isinstance(output, F16Weights) else None
+        o8 = output.h if isinstance(output, Q8Weights) else None
+        h = C.c_void_p()
+        ctx.call("fortai_hip_qwen35_decoder_create", ctx.h, n, harr(recurrent), harr(attention), harr(ffn_gate),
+                 harr(ffn_up), harr(ffn_down), an, pn, _ptr(self._onorm), hidden, e16, e8, o16, o8, max_context,
+                 eps, C.byref(h))
+        self.h = h
+        self.logits = np.zeros(vocab, dtype=np.float32)
+
+    def reset(self) -> None:
+        self.ctx.call("fortai_hip_qwen35_decoder_reset", self.h)
+
+    def forward(self, token: int, position: int, want_logits: bool = True) -> int:
+        nxt = np.zeros(1, dtype=np.int64)
+        self.ctx.call("fortai_hip_qwen35_decoder_forward", self.h, token, position,
+                      _ptr(self.logits) if want_logits else None, _ptr(nxt))
+        return int(nxt[0])
+
+    def generate(self, token: int, position: int, steps: int) -> np.ndarray:
+        trace = np.zeros(steps, dtype=np.int64)
+        self.ctx.call("fortai_hip_qwen35_decoder_generate", self.h, token, position, steps, _ptr(trace))
+        return trace
+
+    def replay(self, steps: int) -> None:
+        self.ctx.call("fortai_hip_qwen35_decoder_replay", self.h, steps)
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.fortai_hip_qwen35_decoder_destroy(self.h)
+            self.h = None

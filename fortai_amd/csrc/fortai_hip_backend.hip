@@ -1,0 +1,1255 @@
+// C ABI of the gfx950 FortAI backend (include/fortai_hip_backend.h).
+//
+// Host orchestration only: handles, validation, device allocation, and the
+// enqueue order of the kernels in q8_kernels.hip, gdn.hip, attention.hip and
+// lm_head.hip.  Entry points follow the reference CUDA ABI
+// (backend/cuda/fortai_cuda_backend.cu:805-1736) in arguments, ownership and
+// return codes; each carries the citation of the function it replaces.
+#include "../../include/fortai_hip_backend.h"
+#include "fortai_hip_internal.h"
+#include "fortai_hip_kernels.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+using namespace fortai_hip;
+
+struct fortai_hip_q8_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
+    int *position = nullptr;    // device: current token position
+    int64_t *token = nullptr;   // device: current token id
+    int8_t *scratch_act = nullptr;
+    size_t scratch_act_bytes = 0;
+    float *scratch_out = nullptr;
+    size_t scratch_out_bytes = 0;
+    float *scratch_aux = nullptr;
+    size_t scratch_aux_bytes = 0;
+    float *argmax_value = nullptr;
+    int32_t *argmax_index = nullptr;
+    unsigned int *argmax_done = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    char error[256] = {};
+};
+
+struct fortai_hip_q8_weights {
+    fortai_hip_q8_context *context = nullptr;
+    int width = 0;
+    Q8Matrix m;
+    uint4 *quants = nullptr;
+    uint2 *scales = nullptr;
+};
+
+struct fortai_hip_f16_weights {
+    fortai_hip_q8_context *context = nullptr;
+    int rows = 0, width = 0;
+    uint16_t *data = nullptr;
+};
+
+struct fortai_hip_qwen35_recurrent {
+    fortai_hip_q8_context *context = nullptr;
+    const fortai_hip_q8_weights *qkv = nullptr, *gate = nullptr, *alpha = nullptr, *beta = nullptr, *out = nullptr;
+    int conv_size = 0, kernel = 0, state_size = 0, key_heads = 0, value_heads = 0, head = 0, inner = 0;
+    float eps = 0.0f;
+    float *conv_w = nullptr, *ssm_a = nullptr, *ssm_dt = nullptr, *ssm_norm = nullptr;
+    float *conv_ring = nullptr, *state = nullptr;
+    float *qkv_out = nullptr, *z_out = nullptr, *alpha_out = nullptr, *beta_out = nullptr, *o_raw = nullptr;
+    int *step = nullptr;
+    unsigned int *done = nullptr;
+};
+
+struct fortai_hip_qwen35_attention {
+    fortai_hip_q8_context *context = nullptr;
+    const fortai_hip_q8_weights *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    int heads = 0, kv_heads = 0, head = 0, value = 0, max_context = 0, rope_dim = 0, chunk = 0;
+    float rope_base = 0.0f, eps = 0.0f;
+    float *q_norm = nullptr, *k_norm = nullptr;
+    float2 *rope = nullptr;
+    uint16_t *kcache = nullptr, *vcache = nullptr;
+    float *q_out = nullptr, *k_out = nullptr, *v_out = nullptr, *attn_out = nullptr, *partial = nullptr;
+    unsigned int *done = nullptr;
+};
+
+struct decoder_layer {
+    fortai_hip_qwen35_recurrent *recurrent = nullptr;
+    fortai_hip_qwen35_attention *attention = nullptr;
+    const fortai_hip_q8_weights *gate = nullptr, *up = nullptr, *down = nullptr;
+    float *attn_norm = nullptr, *post_norm = nullptr;
+};
+
+struct fortai_hip_qwen35_decoder {
+    fortai_hip_q8_context *context = nullptr;
+    std::vector<decoder_layer> layers;
+    int hidden = 0, vocab = 0, ffn = 0, max_context = 0;
+    float eps = 0.0f;
+    const fortai_hip_f16_weights *emb16 = nullptr, *out16 = nullptr;
+    const fortai_hip_q8_weights *emb8 = nullptr, *out8 = nullptr;
+    float *output_norm = nullptr, *x = nullptr, *h = nullptr, *logits = nullptr;
+    float *argmax_value = nullptr;
+    int32_t *argmax_index = nullptr;
+    unsigned int *argmax_done = nullptr;
+    int64_t *trace = nullptr;
+    int next_position = 0;  // host mirror of the device position after the queued steps
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+int fail(fortai_hip_q8_context *ctx, int code, const char *op, hipError_t err = hipSuccess) {
+    if (ctx) {
+        if (err == hipSuccess) std::snprintf(ctx->error, sizeof(ctx->error), "%s", op);
+        else std::snprintf(ctx->error, sizeof(ctx->error), "%s: %s", op, hipGetErrorString(err));
+    }
+    return code;
+}
+
+int done(fortai_hip_q8_context *ctx, hipError_t err, const char *op) {
+    return err == hipSuccess ? FORTAI_HIP_OK : fail(ctx, FORTAI_HIP_RUNTIME_ERROR, op, err);
+}
+
+template <typename T>
+hipError_t alloc(T **ptr, size_t count) {
+    *ptr = nullptr;
+    if (count == 0) return hipSuccess;
+    return hipMalloc(reinterpret_cast<void **>(ptr), count * sizeof(T));
+}
+
+template <typename T>
+void release(T *&ptr) {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+}
+
+hipError_t upload_f32(float **dst, const void *src, size_t count, hipStream_t stream) {
+    hipError_t e = alloc(dst, count);
+    if (e == hipSuccess) e = hipMemcpyAsync(*dst, src, count * sizeof(float), hipMemcpyHostToDevice, stream);
+    return e;
+}
+
+hipError_t ensure(void **buf, size_t *have, size_t need) {
+    if (*have >= need) return hipSuccess;
+    if (*buf) (void)hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
+    const hipError_t e = hipMalloc(buf, need);
+    if (e == hipSuccess) *have = need;
+    return e;
+}
+
+hipError_t ensure_scratch(fortai_hip_q8_context *c, size_t act, size_t out, size_t aux) {
+    hipError_t e = ensure(reinterpret_cast<void **>(&c->scratch_act), &c->scratch_act_bytes, act);
+    if (e == hipSuccess) e = ensure(reinterpret_cast<void **>(&c->scratch_out), &c->scratch_out_bytes, out);
+    if (e == hipSuccess && aux) e = ensure(reinterpret_cast<void **>(&c->scratch_aux), &c->scratch_aux_bytes, aux);
+    return e;
+}
+
+__global__ void set_position_kernel(int *dst, int value) { *dst = value; }
+__global__ void set_token_kernel(int64_t *dst, int64_t value) { *dst = value; }
+
+MatvecSegment segment(const fortai_hip_q8_weights *w, float *out, const float *resid = nullptr,
+    const fortai_hip_q8_weights *w2 = nullptr) {
+    MatvecSegment s;
+    s.w = w->m;
+    if (w2) s.w2 = w2->m;
+    s.out = out;
+    s.resid = resid;
+    return s;
+}
+
+MatvecInput f32_input(const float *x, int width) {
+    MatvecInput in;
+    in.x = x;
+    in.width = width;
+    return in;
+}
+
+MatvecInput q8_input(const int8_t *xq, int width) {
+    MatvecInput in;
+    in.xq = xq;
+    in.width = width;
+    return in;
+}
+
+bool owned(const fortai_hip_q8_context *c, const fortai_hip_q8_weights *w) { return w && w->context == c; }
+
+// enqueue the GDN projection -> step -> gated norm + ssm_out chain
+hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &in, Prologue pro, float *out,
+    const float *resid, hipStream_t stream) {
+    const MatvecSegment segs[4] = {segment(L->qkv, L->qkv_out), segment(L->gate, L->z_out),
+        segment(L->alpha, L->alpha_out), segment(L->beta, L->beta_out)};
+    hipError_t e = launch_q8_matvec(segs, 4, in, pro, Epilogue::STORE, stream);
+    if (e != hipSuccess) return e;
+    GdnParams p;
+    p.qkv = L->qkv_out; p.alpha = L->alpha_out; p.beta = L->beta_out; p.ssm_a = L->ssm_a; p.ssm_dt = L->ssm_dt;
+    p.conv_w = L->conv_w; p.conv_ring = L->conv_ring; p.state = L->state; p.out = L->o_raw;
+    p.step = L->step; p.done = L->done; p.conv_size = L->conv_size; p.kernel = L->kernel;
+    p.state_size = L->state_size; p.key_heads = L->key_heads; p.value_heads = L->value_heads; p.head = L->head;
+    p.eps = L->eps;
+    e = launch_gdn_step(p, stream);
+    if (e != hipSuccess) return e;
+    MatvecInput gin;
+    gin.x = L->o_raw;
+    gin.gate = L->z_out;
+    gin.norm = L->ssm_norm;
+    gin.eps = L->eps;
+    gin.width = L->inner;
+    gin.head = L->head;
+    const MatvecSegment oseg = segment(L->out, out, resid);
+    return launch_q8_matvec(&oseg, 1, gin, Prologue::GATED, resid ? Epilogue::ADD : Epilogue::STORE, stream);
+}
+
+AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q, const float *k, const float *v,
+    float *out) {
+    AttentionParams p;
+    p.q = q; p.k = k; p.v = v; p.q_norm = A->q_norm; p.k_norm = A->k_norm; p.rope = A->rope;
+    p.kcache = A->kcache; p.vcache = A->vcache; p.partial = A->partial; p.done = A->done; p.out = out;
+    p.position = A->context->position; p.heads = A->heads; p.kv_heads = A->kv_heads; p.head = A->head;
+    p.value = A->value; p.max_context = A->max_context; p.rope_dim = A->rope_dim; p.chunk = A->chunk;
+    p.eps = A->eps;
+    return p;
+}
+
+hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &in, Prologue pro, float *out,
+    const float *resid, hipStream_t stream) {
+    const MatvecSegment segs[3] = {segment(A->q, A->q_out), segment(A->k, A->k_out), segment(A->v, A->v_out)};
+    hipError_t e = launch_q8_matvec(segs, 3, in, pro, Epilogue::STORE, stream);
+    if (e != hipSuccess) return e;
+    e = launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream);
+    if (e != hipSuccess) return e;
+    const MatvecSegment oseg = segment(A->o, out, resid);
+    return launch_q8_matvec(&oseg, 1, f32_input(A->attn_out, A->heads * A->value), Prologue::F32,
+        resid ? Epilogue::ADD : Epilogue::STORE, stream);
+}
+
+hipError_t enqueue_ffn(const fortai_hip_q8_weights *gate, const fortai_hip_q8_weights *up,
+    const fortai_hip_q8_weights *down, const MatvecInput &in, Prologue pro, float *h, float *out,
+    const float *resid, hipStream_t stream) {
+    const MatvecSegment pair = segment(gate, h, nullptr, up);
+    hipError_t e = launch_q8_matvec(&pair, 1, in, pro, Epilogue::SILU_PAIR, stream);
+    if (e != hipSuccess) return e;
+    const MatvecSegment dseg = segment(down, out, resid);
+    return launch_q8_matvec(&dseg, 1, f32_input(h, gate->m.rows), Prologue::F32,
+        resid ? Epilogue::ADD : Epilogue::STORE, stream);
+}
+
+bool ffn_shapes_ok(const fortai_hip_q8_weights *g, const fortai_hip_q8_weights *u, const fortai_hip_q8_weights *d) {
+    return g->m.blocks == u->m.blocks && g->m.rows == u->m.rows && g->m.rows == d->m.blocks * kQ8Block &&
+        g->m.rows % kQ8Block == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ------------------------------------------------------------------ context
+// fortai_cuda_backend.cu:805-833
+int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context) {
+    if (!context || device < 0) return FORTAI_HIP_INVALID;
+    *context = nullptr;
+    auto *c = new (std::nothrow) fortai_hip_q8_context;
+    if (!c) return FORTAI_HIP_RUNTIME_ERROR;
+    c->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&c->start);
+    if (e == hipSuccess) e = hipEventCreate(&c->stop);
+    if (e == hipSuccess) e = alloc(&c->position, 1);
+    if (e == hipSuccess) e = alloc(&c->token, 1);
+    if (e == hipSuccess) e = alloc(&c->argmax_value, 1024);
+    if (e == hipSuccess) e = alloc(&c->argmax_index, 1024);
+    if (e == hipSuccess) e = alloc(&c->argmax_done, 1);
+    if (e == hipSuccess) e = hipMemsetAsync(c->position, 0, sizeof(int), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->token, 0, sizeof(int64_t), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(c->argmax_done, 0, sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        fortai_hip_q8_context_destroy(c);
+        return FORTAI_HIP_RUNTIME_ERROR;
+    }
+    *context = c;
+    return FORTAI_HIP_OK;
+}
+
+// fortai_cuda_backend.cu:835-850
+int fortai_hip_q8_context_destroy(fortai_hip_q8_context *c) {
+    if (!c) return FORTAI_HIP_OK;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    release(c->position); release(c->token); release(c->scratch_act); release(c->scratch_out);
+    release(c->scratch_aux); release(c->argmax_value); release(c->argmax_index); release(c->argmax_done);
+    if (c->start) (void)hipEventDestroy(c->start);
+    if (c->stop) (void)hipEventDestroy(c->stop);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return FORTAI_HIP_OK;
+}
+
+// fortai_cuda_backend.cu:852-859.  Written by a one-thread kernel (the value
+// travels as a kernel argument): stream ordered and capturable.
+int fortai_hip_q8_context_set_position(fortai_hip_q8_context *c, int position) {
+    if (!c || !c->position || position < 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
+    return done(c, hipGetLastError(), "set device position");
+}
+
+// fortai_cuda_backend.cu:861-868
+int fortai_hip_q8_context_capture_begin(fortai_hip_q8_context *c) {
+    if (!c || c->graph || c->graph_exec) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeGlobal), "begin HIP graph capture");
+}
+
+// fortai_cuda_backend.cu:870-885
+int fortai_hip_q8_context_capture_end(fortai_hip_q8_context *c) {
+    if (!c) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipStreamEndCapture(c->stream, &c->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&c->graph_exec, c->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+        if (c->graph) (void)hipGraphDestroy(c->graph);
+        c->graph_exec = nullptr;
+        c->graph = nullptr;
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "end HIP graph capture", e);
+    }
+    return FORTAI_HIP_OK;
+}
+
+// fortai_cuda_backend.cu:887-893
+int fortai_hip_q8_context_graph_launch(fortai_hip_q8_context *c) {
+    if (!c || !c->graph_exec) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, hipGraphLaunch(c->graph_exec, c->stream), "launch HIP graph");
+}
+
+int fortai_hip_q8_context_synchronize(fortai_hip_q8_context *c) {
+    if (!c) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, hipStreamSynchronize(c->stream), "stream synchronize");
+}
+
+// ------------------------------------------------------------------ weights
+// fortai_cuda_backend.cu:895-931 (+ the repack to the lane-interleaved layout)
+int fortai_hip_q8_weights_upload(fortai_hip_q8_context *c, const void *host_weights, size_t weight_bytes,
+    int rows, int width, fortai_hip_q8_weights **weights) {
+    if (!c || !host_weights || !weights || rows <= 0 || width <= 0 || width % kQ8Block) return FORTAI_HIP_INVALID;
+    *weights = nullptr;
+    const int blocks = width / kQ8Block;
+    const size_t expected = static_cast<size_t>(rows) * blocks * kQ8Bytes;
+    if (weight_bytes < expected) return FORTAI_HIP_INVALID;
+    auto *w = new (std::nothrow) fortai_hip_q8_weights;
+    if (!w) return FORTAI_HIP_RUNTIME_ERROR;
+    w->context = c;
+    w->width = width;
+    w->m.rows = rows;
+    w->m.blocks = blocks;
+    w->m.chunks = (blocks + 3) / 4;
+    w->m.row_groups = (rows + kRowsPerWave - 1) / kRowsPerWave;
+    (void)hipSetDevice(c->device);
+    uint8_t *staging = nullptr;
+    const size_t groups = static_cast<size_t>(w->m.row_groups) * w->m.chunks;
+    hipError_t e = alloc(&w->quants, groups * 64);
+    if (e == hipSuccess) e = alloc(&w->scales, groups * 8);
+    if (e == hipSuccess) e = alloc(&staging, expected);
+    if (e == hipSuccess) e = hipMemcpyAsync(staging, host_weights, expected, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = launch_q8_repack(staging, rows, blocks, w->quants, w->scales, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    release(staging);
+    if (e != hipSuccess) {
+        release(w->quants);
+        release(w->scales);
+        delete w;
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "weight upload", e);
+    }
+    w->m.quants = w->quants;
+    w->m.scales = w->scales;
+    *weights = w;
+    return FORTAI_HIP_OK;
+}
+
+// fortai_cuda_backend.cu:925-931
+int fortai_hip_q8_weights_destroy(fortai_hip_q8_weights *w) {
+    if (!w) return FORTAI_HIP_OK;
+    if (w->context) (void)hipSetDevice(w->context->device);
+    release(w->quants);
+    release(w->scales);
+    delete w;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_f16_weights_upload(fortai_hip_q8_context *c, const void *host_weights, size_t weight_bytes, int rows,
+    int width, fortai_hip_f16_weights **weights) {
+    if (!c || !host_weights || !weights || rows <= 0 || width <= 0 || width % 64) return FORTAI_HIP_INVALID;
+    *weights = nullptr;
+    const size_t expected = static_cast<size_t>(rows) * width * 2;
+    if (weight_bytes < expected) return FORTAI_HIP_INVALID;
+    auto *w = new (std::nothrow) fortai_hip_f16_weights;
+    if (!w) return FORTAI_HIP_RUNTIME_ERROR;
+    w->context = c;
+    w->rows = rows;
+    w->width = width;
+    (void)hipSetDevice(c->device);
+    hipError_t e = alloc(&w->data, static_cast<size_t>(rows) * width);
+    if (e == hipSuccess) e = hipMemcpyAsync(w->data, host_weights, expected, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        release(w->data);
+        delete w;
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "f16 weight upload", e);
+    }
+    *weights = w;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_f16_weights_destroy(fortai_hip_f16_weights *w) {
+    if (!w) return FORTAI_HIP_OK;
+    if (w->context) (void)hipSetDevice(w->context->device);
+    release(w->data);
+    delete w;
+    return FORTAI_HIP_OK;
+}
+
+// ------------------------------------------------------------------ buffers
+// fortai_cuda_backend.cu:933-990
+int fortai_hip_q8_device_buffer_create(fortai_hip_q8_context *c, size_t bytes, void **buffer) {
+    if (!c || !buffer || bytes == 0) return FORTAI_HIP_INVALID;
+    *buffer = nullptr;
+    (void)hipSetDevice(c->device);
+    return done(c, hipMalloc(buffer, bytes), "device buffer allocation");
+}
+
+int fortai_hip_q8_device_buffer_destroy(fortai_hip_q8_context *c, void *buffer) {
+    if (!c || !buffer) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    return done(c, hipFree(buffer), "device buffer free");
+}
+
+int fortai_hip_q8_device_buffer_upload(fortai_hip_q8_context *c, void *buffer, const void *host, size_t bytes) {
+    if (!c || !buffer || !host || bytes == 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(buffer, host, bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "device upload");
+}
+
+int fortai_hip_q8_device_buffer_upload_ptr(fortai_hip_q8_context *c, void *buffer, const void *host, size_t bytes) {
+    if (!c || !buffer || !host || bytes == 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, hipMemcpyAsync(buffer, host, bytes, hipMemcpyHostToDevice, c->stream), "async device upload");
+}
+
+int fortai_hip_q8_device_buffer_download(fortai_hip_q8_context *c, void *host, const void *buffer, size_t bytes) {
+    if (!c || !buffer || !host || bytes == 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(host, buffer, bytes, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "device download");
+}
+
+// --------------------------------------------------------------- device ops
+// fortai_cuda_backend.cu:992-1012
+int fortai_hip_q8_matvec_resident(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w,
+    const void *device_activation, void *device_output, float *kernel_ms) {
+    if (!c || !owned(c, w) || !device_activation || !device_output || !kernel_ms) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    const MatvecSegment s = segment(w, static_cast<float *>(device_output));
+    hipError_t e = hipEventRecord(c->start, c->stream);
+    if (e == hipSuccess)
+        e = launch_q8_matvec(&s, 1, q8_input(static_cast<const int8_t *>(device_activation), w->width), Prologue::Q8,
+            Epilogue::STORE, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(kernel_ms, c->start, c->stop);
+    return done(c, e, "resident matvec");
+}
+
+// fortai_cuda_backend.cu:1014-1039 (quantize fused into the matvec)
+int fortai_hip_q8_matvec_device_f32(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w,
+    const void *device_activation, size_t activation_elements, void *device_output, size_t output_elements) {
+    if (!c || !owned(c, w) || !device_activation || !device_output ||
+        activation_elements != static_cast<size_t>(w->width) || output_elements < static_cast<size_t>(w->m.rows))
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    const MatvecSegment s = segment(w, static_cast<float *>(device_output));
+    return done(c, launch_q8_matvec(&s, 1, f32_input(static_cast<const float *>(device_activation), w->width),
+        Prologue::F32, Epilogue::STORE, c->stream), "device F32 matvec");
+}
+
+// fortai_cuda_backend.cu:1041-1055
+int fortai_hip_qwen35_embedding_device(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, int64_t token_id,
+    void *device_output, size_t output_elements) {
+    if (!c || !owned(c, w) || !device_output || token_id < 0 || token_id >= w->m.rows ||
+        output_elements < static_cast<size_t>(w->width))
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_q8_embedding(w->m, nullptr, nullptr, token_id, static_cast<float *>(device_output), c->stream),
+        "device Q8 embedding");
+}
+
+int fortai_hip_qwen35_embedding_f16_device(fortai_hip_q8_context *c, const fortai_hip_f16_weights *w,
+    int64_t token_id, void *device_output, size_t output_elements) {
+    if (!c || !w || w->context != c || !device_output || token_id < 0 || token_id >= w->rows ||
+        output_elements < static_cast<size_t>(w->width))
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_f16_embedding(w->data, w->width, nullptr, token_id, static_cast<float *>(device_output),
+        c->stream), "device F16 embedding");
+}
+
+// fortai_cuda_backend.cu:1057-1065
+int fortai_hip_qwen35_copy_device(fortai_hip_q8_context *c, const void *in, void *out, size_t bytes) {
+    if (!c || !in || !out || bytes == 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, hipMemcpyAsync(out, in, bytes, hipMemcpyDeviceToDevice, c->stream), "device copy");
+}
+
+// fortai_cuda_backend.cu:1067-1080
+int fortai_hip_qwen35_add_device(fortai_hip_q8_context *c, const void *left, const void *right, void *out,
+    size_t elements) {
+    if (!c || !left || !right || !out || elements == 0 || elements > static_cast<size_t>(INT32_MAX))
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_add(static_cast<const float *>(left), static_cast<const float *>(right),
+        static_cast<float *>(out), static_cast<int>(elements), c->stream), "device add");
+}
+
+// fortai_cuda_backend.cu:1082-1095
+int fortai_hip_qwen35_rms_norm_device(fortai_hip_q8_context *c, const void *in, const void *weights, void *out,
+    size_t elements, float epsilon) {
+    if (!c || !in || !weights || !out || elements == 0 || elements > static_cast<size_t>(INT32_MAX) ||
+        epsilon <= 0.0f)
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_rms_norm(static_cast<const float *>(in), static_cast<const float *>(weights),
+        static_cast<float *>(out), static_cast<int>(elements), epsilon, c->stream), "device RMS norm");
+}
+
+int fortai_hip_f16_matvec_device(fortai_hip_q8_context *c, const fortai_hip_f16_weights *w,
+    const void *device_activation, size_t activation_elements, void *device_output, size_t output_elements,
+    void *device_token) {
+    if (!c || !w || w->context != c || !device_activation || !device_output ||
+        activation_elements != static_cast<size_t>(w->width) || output_elements < static_cast<size_t>(w->rows))
+        return FORTAI_HIP_INVALID;
+    if (device_token && f16_matvec_workgroups(w->rows) > 1024) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    ArgmaxState st;
+    st.partial_value = c->argmax_value;
+    st.partial_index = c->argmax_index;
+    st.done = c->argmax_done;
+    st.token = static_cast<int64_t *>(device_token);
+    return done(c, launch_f16_matvec(w->data, w->rows, w->width, static_cast<const float *>(device_activation),
+        nullptr, 0.0f, static_cast<float *>(device_output), device_token ? &st : nullptr, c->stream),
+        "device F16 matvec");
+}
+
+int fortai_hip_argmax_device(fortai_hip_q8_context *c, const void *values, size_t elements, void *device_token) {
+    if (!c || !values || !device_token || elements == 0 || elements > static_cast<size_t>(INT32_MAX))
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    ArgmaxState st;
+    st.partial_value = c->argmax_value;
+    st.partial_index = c->argmax_index;
+    st.done = c->argmax_done;
+    st.token = static_cast<int64_t *>(device_token);
+    return done(c, launch_argmax(static_cast<const float *>(values), static_cast<int>(elements), st, c->stream),
+        "device argmax");
+}
+
+int fortai_hip_q8_quantize_device(fortai_hip_q8_context *c, const void *in, size_t elements, void *blocks,
+    void *scales) {
+    if (!c || !in || !blocks || !scales || elements == 0 || elements % kQ8Block ||
+        elements > static_cast<size_t>(INT32_MAX))
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_q8_quantize(static_cast<const float *>(in), static_cast<int>(elements),
+        static_cast<int8_t *>(blocks), static_cast<float *>(scales), c->stream), "device quantize");
+}
+
+int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w,
+    const void *device_activation, void *device_dots) {
+    if (!c || !owned(c, w) || !device_activation || !device_dots) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_q8_block_dots(w->m, static_cast<const int8_t *>(device_activation),
+        static_cast<int32_t *>(device_dots), c->stream), "device block dots");
+}
+
+// ----------------------------------------------------------------- host ops
+namespace {
+struct host_request {
+    const fortai_hip_q8_weights *w;
+    float *host;
+    size_t bytes;
+};
+
+// fortai_cuda_backend.cu host matvec paths (:1097-1187): upload the Q8
+// activation once, evaluate each resident matrix, copy the outputs back.
+int matvec_host_many(fortai_hip_q8_context *c, const host_request *req, int count, const void *host_activation,
+    size_t activation_bytes, float *elapsed_ms, float *contiguous) {
+    if (!c || !host_activation || !elapsed_ms) return FORTAI_HIP_INVALID;
+    size_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        const fortai_hip_q8_weights *w = req[i].w;
+        if (!owned(c, w) || !req[i].host || w->width != req[0].w->width ||
+            req[i].bytes < static_cast<size_t>(w->m.rows) * sizeof(float))
+            return FORTAI_HIP_INVALID;
+        total += static_cast<size_t>(w->m.rows) * sizeof(float);
+    }
+    const size_t act = static_cast<size_t>(req[0].w->m.blocks) * kQ8Bytes;
+    if (activation_bytes < act) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = ensure_scratch(c, act, total, 0);
+    if (e == hipSuccess) e = hipEventRecord(c->start, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->scratch_act, host_activation, act, hipMemcpyHostToDevice, c->stream);
+    MatvecSegment segs[4];
+    size_t offset = 0;
+    for (int i = 0; i < count; ++i) {
+        segs[i] = segment(req[i].w, c->scratch_out + offset);
+        offset += static_cast<size_t>(req[i].w->m.rows);
+    }
+    if (e == hipSuccess)
+        e = launch_q8_matvec(segs, count, q8_input(c->scratch_act, req[0].w->width), Prologue::Q8, Epilogue::STORE,
+            c->stream);
+    if (contiguous) {
+        if (e == hipSuccess) e = hipMemcpyAsync(contiguous, c->scratch_out, total, hipMemcpyDeviceToHost, c->stream);
+    } else {
+        offset = 0;
+        for (int i = 0; i < count && e == hipSuccess; ++i) {
+            const size_t bytes = static_cast<size_t>(req[i].w->m.rows) * sizeof(float);
+            e = hipMemcpyAsync(req[i].host, c->scratch_out + offset, bytes, hipMemcpyDeviceToHost, c->stream);
+            offset += static_cast<size_t>(req[i].w->m.rows);
+        }
+    }
+    if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(elapsed_ms, c->start, c->stop);
+    return done(c, e, "host matvec");
+}
+}  // namespace
+
+int fortai_hip_q8_matvec_host(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *act,
+    size_t act_bytes, float *out, size_t out_bytes, float *ms) {
+    if (!w || !out) return FORTAI_HIP_INVALID;
+    const host_request r[] = {{w, out, out_bytes}};
+    return matvec_host_many(c, r, 1, act, act_bytes, ms, nullptr);
+}
+
+int fortai_hip_q8_matvec_host_pair(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w1,
+    const fortai_hip_q8_weights *w2, const void *act, size_t act_bytes, float *o1, size_t b1, float *o2, size_t b2,
+    float *ms) {
+    if (!w1 || !w2) return FORTAI_HIP_INVALID;
+    const host_request r[] = {{w1, o1, b1}, {w2, o2, b2}};
+    return matvec_host_many(c, r, 2, act, act_bytes, ms, nullptr);
+}
+
+int fortai_hip_q8_matvec_host_triplet(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w1,
+    const fortai_hip_q8_weights *w2, const fortai_hip_q8_weights *w3, const void *act, size_t act_bytes, float *o1,
+    size_t b1, float *o2, size_t b2, float *o3, size_t b3, float *ms) {
+    if (!w1 || !w2 || !w3) return FORTAI_HIP_INVALID;
+    const host_request r[] = {{w1, o1, b1}, {w2, o2, b2}, {w3, o3, b3}};
+    return matvec_host_many(c, r, 3, act, act_bytes, ms, nullptr);
+}
+
+int fortai_hip_q8_matvec_host_triplet_contiguous(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w1,
+    const fortai_hip_q8_weights *w2, const fortai_hip_q8_weights *w3, const void *act, size_t act_bytes, float *out,
+    size_t out_bytes, float *ms) {
+    if (!w1 || !w2 || !w3 || !out) return FORTAI_HIP_INVALID;
+    const size_t n1 = static_cast<size_t>(w1->m.rows), n2 = static_cast<size_t>(w2->m.rows),
+                 n3 = static_cast<size_t>(w3->m.rows);
+    if (out_bytes < (n1 + n2 + n3) * sizeof(float)) return FORTAI_HIP_INVALID;
+    const host_request r[] = {{w1, out, n1 * 4}, {w2, out + n1, n2 * 4}, {w3, out + n1 + n2, n3 * 4}};
+    return matvec_host_many(c, r, 3, act, act_bytes, ms, out);
+}
+
+// fortai_cuda_backend.cu:1189-1245
+int fortai_hip_q8_ffn_host(fortai_hip_q8_context *c, const fortai_hip_q8_weights *gate,
+    const fortai_hip_q8_weights *up, const fortai_hip_q8_weights *down, const void *act, size_t act_bytes, float *out,
+    size_t out_bytes, float *ms) {
+    if (!c || !owned(c, gate) || !owned(c, up) || !owned(c, down) || !act || !out || !ms) return FORTAI_HIP_INVALID;
+    if (!ffn_shapes_ok(gate, up, down)) return FORTAI_HIP_INVALID;
+    const size_t in_bytes = static_cast<size_t>(gate->m.blocks) * kQ8Bytes;
+    const size_t o_bytes = static_cast<size_t>(down->m.rows) * sizeof(float);
+    if (act_bytes < in_bytes || out_bytes < o_bytes) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = ensure_scratch(c, in_bytes, o_bytes, static_cast<size_t>(gate->m.rows) * sizeof(float));
+    if (e == hipSuccess) e = hipEventRecord(c->start, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->scratch_act, act, in_bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess)
+        e = enqueue_ffn(gate, up, down, q8_input(c->scratch_act, gate->width), Prologue::Q8, c->scratch_aux,
+            c->scratch_out, nullptr, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, c->scratch_out, o_bytes, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, c->start, c->stop);
+    return done(c, e, "Qwen FFN host");
+}
+
+// fortai_cuda_backend.cu:1247-1296
+int fortai_hip_q8_ffn_device(fortai_hip_q8_context *c, const fortai_hip_q8_weights *gate,
+    const fortai_hip_q8_weights *up, const fortai_hip_q8_weights *down, const void *act, size_t act_elements,
+    void *out, size_t out_elements) {
+    if (!c || !owned(c, gate) || !owned(c, up) || !owned(c, down) || !act || !out) return FORTAI_HIP_INVALID;
+    if (!ffn_shapes_ok(gate, up, down) || act_elements != static_cast<size_t>(gate->width) ||
+        out_elements < static_cast<size_t>(down->m.rows))
+        return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = ensure_scratch(c, 0, 0, static_cast<size_t>(gate->m.rows) * sizeof(float));
+    if (e == hipSuccess)
+        e = enqueue_ffn(gate, up, down, f32_input(static_cast<const float *>(act), gate->width), Prologue::F32,
+            c->scratch_aux, static_cast<float *>(out), nullptr, c->stream);
+    return done(c, e, "Qwen FFN device");
+}
+
+// --------------------------------------------------------- recurrent layer
+// fortai_cuda_backend.cu:1298-1346
+int fortai_hip_qwen35_recurrent_create(fortai_hip_q8_context *c, const fortai_hip_q8_weights *qkv,
+    const fortai_hip_q8_weights *gate, const fortai_hip_q8_weights *alpha, const fortai_hip_q8_weights *beta,
+    const fortai_hip_q8_weights *outw, const void *conv_weights, size_t conv_weight_bytes, int conv_size,
+    int conv_kernel, const void *ssm_a, size_t ssm_a_bytes, const void *ssm_dt, size_t ssm_dt_bytes,
+    const void *ssm_norm, size_t ssm_norm_bytes, int state_size, int key_heads, int value_heads, int head_size,
+    int inner_size, float norm_epsilon, fortai_hip_qwen35_recurrent **layer) {
+    if (!c || !layer || !qkv || !gate || !alpha || !beta || !outw || !conv_weights || !ssm_a || !ssm_dt ||
+        !ssm_norm || conv_size <= 0 || conv_kernel < 2 || state_size <= 0 || key_heads <= 0 || value_heads <= 0 ||
+        head_size <= 0 || inner_size <= 0 || value_heads % key_heads != 0 || value_heads * head_size != inner_size)
+        return FORTAI_HIP_INVALID;
+    *layer = nullptr;
+    if (!owned(c, qkv) || !owned(c, gate) || !owned(c, alpha) || !owned(c, beta) || !owned(c, outw))
+        return FORTAI_HIP_INVALID;
+    // this backend's step kernel covers the Qwen3.5 geometry: q/k slices of
+    // head_size, power-of-two heads of 64..256
+    if (state_size != head_size || (head_size != 64 && head_size != 128 && head_size != 256) ||
+        conv_size != 2 * state_size * key_heads + inner_size || qkv->m.rows != conv_size ||
+        gate->m.rows != inner_size || alpha->m.rows != value_heads || beta->m.rows != value_heads ||
+        outw->width != inner_size || gate->width != qkv->width || alpha->width != qkv->width ||
+        beta->width != qkv->width)
+        return FORTAI_HIP_INVALID;
+    if (conv_weight_bytes < static_cast<size_t>(conv_size) * conv_kernel * sizeof(float) ||
+        ssm_a_bytes < static_cast<size_t>(value_heads) * sizeof(float) ||
+        ssm_dt_bytes < static_cast<size_t>(value_heads) * sizeof(float) ||
+        ssm_norm_bytes < static_cast<size_t>(head_size) * sizeof(float))
+        return FORTAI_HIP_INVALID;
+    auto *L = new (std::nothrow) fortai_hip_qwen35_recurrent;
+    if (!L) return FORTAI_HIP_RUNTIME_ERROR;
+    L->context = c; L->qkv = qkv; L->gate = gate; L->alpha = alpha; L->beta = beta; L->out = outw;
+    L->conv_size = conv_size; L->kernel = conv_kernel; L->state_size = state_size; L->key_heads = key_heads;
+    L->value_heads = value_heads; L->head = head_size; L->inner = inner_size; L->eps = norm_epsilon;
+    (void)hipSetDevice(c->device);
+    const size_t state_n = static_cast<size_t>(value_heads) * head_size * head_size;
+    hipError_t e = upload_f32(&L->conv_w, conv_weights, static_cast<size_t>(conv_size) * conv_kernel, c->stream);
+    if (e == hipSuccess) e = upload_f32(&L->ssm_a, ssm_a, value_heads, c->stream);
+    if (e == hipSuccess) e = upload_f32(&L->ssm_dt, ssm_dt, value_heads, c->stream);
+    if (e == hipSuccess) e = upload_f32(&L->ssm_norm, ssm_norm, head_size, c->stream);
+    if (e == hipSuccess) e = alloc(&L->conv_ring, static_cast<size_t>(conv_kernel) * conv_size);
+    if (e == hipSuccess) e = alloc(&L->state, state_n);
+    if (e == hipSuccess) e = alloc(&L->qkv_out, conv_size);
+    if (e == hipSuccess) e = alloc(&L->z_out, inner_size);
+    if (e == hipSuccess) e = alloc(&L->alpha_out, value_heads);
+    if (e == hipSuccess) e = alloc(&L->beta_out, value_heads);
+    if (e == hipSuccess) e = alloc(&L->o_raw, inner_size);
+    if (e == hipSuccess) e = alloc(&L->step, 1);
+    if (e == hipSuccess) e = alloc(&L->done, 1);
+    if (e == hipSuccess) e = hipMemsetAsync(L->done, 0, sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        fortai_hip_qwen35_recurrent_destroy(L);
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen recurrent create", e);
+    }
+    const int rc = fortai_hip_qwen35_recurrent_reset(L);
+    if (rc != FORTAI_HIP_OK) {
+        fortai_hip_qwen35_recurrent_destroy(L);
+        return rc;
+    }
+    *layer = L;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_recurrent_destroy(fortai_hip_qwen35_recurrent *L) {
+    if (!L) return FORTAI_HIP_OK;
+    if (L->context) {
+        (void)hipSetDevice(L->context->device);
+        (void)hipStreamSynchronize(L->context->stream);
+    }
+    release(L->conv_w); release(L->ssm_a); release(L->ssm_dt); release(L->ssm_norm); release(L->conv_ring);
+    release(L->state); release(L->qkv_out); release(L->z_out); release(L->alpha_out); release(L->beta_out);
+    release(L->o_raw); release(L->step); release(L->done);
+    delete L;
+    return FORTAI_HIP_OK;
+}
+
+// fortai_cuda_backend.cu:1395-1408
+int fortai_hip_qwen35_recurrent_reset(fortai_hip_qwen35_recurrent *L) {
+    if (!L || !L->context) return FORTAI_HIP_INVALID;
+    auto *c = L->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipMemsetAsync(L->conv_ring, 0, static_cast<size_t>(L->kernel) * L->conv_size * sizeof(float),
+        c->stream);
+    if (e == hipSuccess)
+        e = hipMemsetAsync(L->state, 0, static_cast<size_t>(L->value_heads) * L->head * L->head * sizeof(float),
+            c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(L->step, 0, sizeof(int), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(L->done, 0, sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "Qwen recurrent reset");
+}
+
+// fortai_cuda_backend.cu:1410-1489
+int fortai_hip_qwen35_recurrent_run(fortai_hip_qwen35_recurrent *L, const void *act, size_t act_bytes,
+    float *out, size_t out_bytes, float *ms) {
+    if (!L || !L->context || !act || !out || !ms) return FORTAI_HIP_INVALID;
+    auto *c = L->context;
+    const size_t in_bytes = static_cast<size_t>(L->qkv->m.blocks) * kQ8Bytes;
+    const size_t o_bytes = static_cast<size_t>(L->out->m.rows) * sizeof(float);
+    if (act_bytes < in_bytes || out_bytes < o_bytes) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = ensure_scratch(c, in_bytes, o_bytes, 0);
+    if (e == hipSuccess) e = hipEventRecord(c->start, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->scratch_act, act, in_bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess)
+        e = enqueue_recurrent(L, q8_input(c->scratch_act, L->qkv->width), Prologue::Q8, c->scratch_out, nullptr,
+            c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, c->scratch_out, o_bytes, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, c->start, c->stop);
+    return done(c, e, "Qwen recurrent run");
+}
+
+// fortai_cuda_backend.cu:1491-1562
+int fortai_hip_qwen35_recurrent_run_device(fortai_hip_qwen35_recurrent *L, const void *act, size_t act_elements,
+    void *out, size_t out_elements) {
+    if (!L || !L->context || !act || !out) return FORTAI_HIP_INVALID;
+    if (act_elements != static_cast<size_t>(L->qkv->width) || out_elements < static_cast<size_t>(L->out->m.rows))
+        return FORTAI_HIP_INVALID;
+    auto *c = L->context;
+    (void)hipSetDevice(c->device);
+    return done(c, enqueue_recurrent(L, f32_input(static_cast<const float *>(act), L->qkv->width), Prologue::F32,
+        static_cast<float *>(out), nullptr, c->stream), "Qwen recurrent device run");
+}
+
+int fortai_hip_qwen35_recurrent_core_device(fortai_hip_qwen35_recurrent *L, const void *qkv, const void *alpha,
+    const void *beta, void *out) {
+    if (!L || !L->context || !qkv || !alpha || !beta || !out) return FORTAI_HIP_INVALID;
+    auto *c = L->context;
+    (void)hipSetDevice(c->device);
+    GdnParams p;
+    p.qkv = static_cast<const float *>(qkv); p.alpha = static_cast<const float *>(alpha);
+    p.beta = static_cast<const float *>(beta); p.ssm_a = L->ssm_a; p.ssm_dt = L->ssm_dt; p.conv_w = L->conv_w;
+    p.conv_ring = L->conv_ring; p.state = L->state; p.out = static_cast<float *>(out); p.step = L->step;
+    p.done = L->done; p.conv_size = L->conv_size; p.kernel = L->kernel; p.state_size = L->state_size;
+    p.key_heads = L->key_heads; p.value_heads = L->value_heads; p.head = L->head; p.eps = L->eps;
+    return done(c, launch_gdn_step(p, c->stream), "Qwen recurrent core");
+}
+
+int fortai_hip_qwen35_recurrent_state_download(fortai_hip_qwen35_recurrent *L, float *gdn, size_t gdn_bytes,
+    float *conv, size_t conv_bytes) {
+    if (!L || !L->context) return FORTAI_HIP_INVALID;
+    const int H = L->head, K = L->kernel, C = L->conv_size, cols = H / 8;
+    const size_t sn = static_cast<size_t>(L->value_heads) * H * H;
+    if ((gdn && gdn_bytes < sn * 4) || (conv && conv_bytes < static_cast<size_t>(K - 1) * C * 4))
+        return FORTAI_HIP_INVALID;
+    auto *c = L->context;
+    (void)hipSetDevice(c->device);
+    std::vector<float> st(sn), ring(static_cast<size_t>(K) * C);
+    int t = 0;
+    hipError_t e = hipMemcpyAsync(st.data(), L->state, sn * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(ring.data(), L->conv_ring, ring.size() * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(&t, L->step, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return fail(c, FORTAI_HIP_RUNTIME_ERROR, "recurrent state download", e);
+    if (gdn)
+        for (size_t hr = 0; hr < static_cast<size_t>(L->value_heads) * H; ++hr)
+            for (int l = 0; l < 8; ++l)
+                for (int i = 0; i < cols; ++i) gdn[hr * H + 8 * i + l] = st[(hr * 8 + l) * cols + i];
+    if (conv)
+        for (int s = 0; s < K - 1; ++s) {
+            const int slot = ((t - (K - 1) + s) % K + K) % K;
+            std::memcpy(conv + static_cast<size_t>(s) * C, ring.data() + static_cast<size_t>(slot) * C, C * 4);
+        }
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_recurrent_state_upload(fortai_hip_qwen35_recurrent *L, const float *gdn, size_t gdn_bytes,
+    const float *conv, size_t conv_bytes) {
+    if (!L || !L->context || !gdn || !conv) return FORTAI_HIP_INVALID;
+    const int H = L->head, K = L->kernel, C = L->conv_size, cols = H / 8;
+    const size_t sn = static_cast<size_t>(L->value_heads) * H * H;
+    if (gdn_bytes < sn * 4 || conv_bytes < static_cast<size_t>(K - 1) * C * 4) return FORTAI_HIP_INVALID;
+    std::vector<float> st(sn), ring(static_cast<size_t>(K) * C, 0.0f);
+    for (size_t hr = 0; hr < static_cast<size_t>(L->value_heads) * H; ++hr)
+        for (int l = 0; l < 8; ++l)
+            for (int i = 0; i < cols; ++i) st[(hr * 8 + l) * cols + i] = gdn[hr * H + 8 * i + l];
+    for (int s = 0; s < K - 1; ++s) {  // step counter restarts at 0
+        const int slot = ((0 - (K - 1) + s) % K + K) % K;
+        std::memcpy(ring.data() + static_cast<size_t>(slot) * C, conv + static_cast<size_t>(s) * C, C * 4);
+    }
+    auto *c = L->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(L->state, st.data(), sn * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(L->conv_ring, ring.data(), ring.size() * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(L->step, 0, sizeof(int), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "recurrent state upload");
+}
+
+// --------------------------------------------------------- attention layer
+// fortai_cuda_backend.cu:1564-1621 (+ the RoPE table, computed on the host
+// with the reference's expression, fortai_qwen35_cpu.f90:1487-1490)
+int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hip_q8_weights *q,
+    const fortai_hip_q8_weights *k, const fortai_hip_q8_weights *v, const fortai_hip_q8_weights *o,
+    const void *query_norm, size_t query_norm_bytes, const void *key_norm, size_t key_norm_bytes, int heads,
+    int kv_heads, int head_size, int value_size, int max_context, int rope_dimension, float rope_base,
+    float norm_epsilon, fortai_hip_qwen35_attention **layer) {
+    if (!c || !layer || !q || !k || !v || !o || !query_norm || !key_norm || heads <= 0 || kv_heads <= 0 ||
+        head_size <= 0 || value_size <= 0 || max_context <= 0 || heads % kv_heads != 0 || rope_dimension < 0 ||
+        (rope_dimension > 0 && (rope_dimension > head_size || rope_dimension % 2 != 0)) || rope_base <= 0.0f ||
+        norm_epsilon <= 0.0f)
+        return FORTAI_HIP_INVALID;
+    if (!owned(c, q) || !owned(c, k) || !owned(c, v) || !owned(c, o) || q->m.rows != heads * 2 * head_size ||
+        k->m.rows != kv_heads * head_size || v->m.rows != kv_heads * value_size ||
+        o->width != heads * value_size || query_norm_bytes < static_cast<size_t>(head_size) * sizeof(float) ||
+        key_norm_bytes < static_cast<size_t>(head_size) * sizeof(float) || q->width != k->width ||
+        q->width != v->width)
+        return FORTAI_HIP_INVALID;
+    // this backend's attention kernel: GQA groups of <= 4, head <= 256, value <= 256
+    if (heads / kv_heads > 4 || head_size > 256 || value_size > 256 || head_size % 8 || value_size % 8)
+        return FORTAI_HIP_INVALID;
+    *layer = nullptr;
+    auto *A = new (std::nothrow) fortai_hip_qwen35_attention;
+    if (!A) return FORTAI_HIP_RUNTIME_ERROR;
+    A->context = c; A->q = q; A->k = k; A->v = v; A->o = o; A->heads = heads; A->kv_heads = kv_heads;
+    A->head = head_size; A->value = value_size; A->max_context = max_context; A->rope_dim = rope_dimension;
+    A->rope_base = rope_base; A->eps = norm_epsilon; A->chunk = attention_chunk(max_context);
+    const int half = rope_dimension / 2;
+    std::vector<float2> table(static_cast<size_t>(max_context) * (half > 0 ? half : 1));
+    for (int p = 0; p < max_context; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float angle = static_cast<float>(p) /
+                powf(rope_base, static_cast<float>(2 * i) / static_cast<float>(rope_dimension));
+            table[static_cast<size_t>(p) * half + i] = make_float2(cosf(angle), sinf(angle));
+        }
+    (void)hipSetDevice(c->device);
+    const int group = heads / kv_heads;
+    const int nchunk = (max_context + A->chunk - 1) / A->chunk;
+    const size_t kv_n = static_cast<size_t>(max_context) * kv_heads;
+    hipError_t e = upload_f32(&A->q_norm, query_norm, head_size, c->stream);
+    if (e == hipSuccess) e = upload_f32(&A->k_norm, key_norm, head_size, c->stream);
+    if (e == hipSuccess) e = alloc(&A->rope, table.size());
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(A->rope, table.data(), table.size() * sizeof(float2), hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = alloc(&A->kcache, kv_n * head_size);
+    if (e == hipSuccess) e = alloc(&A->vcache, kv_n * value_size);
+    if (e == hipSuccess) e = alloc(&A->q_out, static_cast<size_t>(heads) * 2 * head_size);
+    if (e == hipSuccess) e = alloc(&A->k_out, static_cast<size_t>(kv_heads) * head_size);
+    if (e == hipSuccess) e = alloc(&A->v_out, static_cast<size_t>(kv_heads) * value_size);
+    if (e == hipSuccess) e = alloc(&A->attn_out, static_cast<size_t>(heads) * value_size);
+    if (e == hipSuccess) e = alloc(&A->partial, static_cast<size_t>(kv_heads) * nchunk * group * (value_size + 2));
+    if (e == hipSuccess) e = alloc(&A->done, kv_heads);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        fortai_hip_qwen35_attention_destroy(A);
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen attention create", e);
+    }
+    const int rc = fortai_hip_qwen35_attention_reset(A);
+    if (rc != FORTAI_HIP_OK) {
+        fortai_hip_qwen35_attention_destroy(A);
+        return rc;
+    }
+    *layer = A;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_attention_destroy(fortai_hip_qwen35_attention *A) {
+    if (!A) return FORTAI_HIP_OK;
+    if (A->context) {
+        (void)hipSetDevice(A->context->device);
+        (void)hipStreamSynchronize(A->context->stream);
+    }
+    release(A->q_norm); release(A->k_norm); release(A->rope); release(A->kcache); release(A->vcache);
+    release(A->q_out); release(A->k_out); release(A->v_out); release(A->attn_out); release(A->partial);
+    release(A->done);
+    delete A;
+    return FORTAI_HIP_OK;
+}
+
+// fortai_cuda_backend.cu:1650-1663
+int fortai_hip_qwen35_attention_reset(fortai_hip_qwen35_attention *A) {
+    if (!A || !A->context) return FORTAI_HIP_INVALID;
+    auto *c = A->context;
+    (void)hipSetDevice(c->device);
+    const size_t kv_n = static_cast<size_t>(A->max_context) * A->kv_heads;
+    hipError_t e = hipMemsetAsync(A->kcache, 0, kv_n * A->head * 2, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(A->vcache, 0, kv_n * A->value * 2, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(A->done, 0, static_cast<size_t>(A->kv_heads) * sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "Qwen attention reset");
+}
+
+// fortai_cuda_backend.cu:1665-1731.  As in the reference, the kernels read the
+// context's device position; `position` is validated against max_context.
+int fortai_hip_qwen35_attention_run_device(fortai_hip_qwen35_attention *A, const void *act, size_t act_elements,
+    int position, void *out, size_t out_elements) {
+    if (!A || !A->context || !act || !out || position < 0 || position >= A->max_context) return FORTAI_HIP_INVALID;
+    if (act_elements != static_cast<size_t>(A->q->width) || out_elements < static_cast<size_t>(A->o->m.rows))
+        return FORTAI_HIP_INVALID;
+    auto *c = A->context;
+    (void)hipSetDevice(c->device);
+    return done(c, enqueue_attention(A, f32_input(static_cast<const float *>(act), A->q->width), Prologue::F32,
+        static_cast<float *>(out), nullptr, c->stream), "Qwen attention device run");
+}
+
+int fortai_hip_qwen35_attention_core_device(fortai_hip_qwen35_attention *A, const void *q, const void *k,
+    const void *v, void *out) {
+    if (!A || !A->context || !q || !k || !v || !out) return FORTAI_HIP_INVALID;
+    auto *c = A->context;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_attention(attention_params(A, static_cast<const float *>(q), static_cast<const float *>(k),
+        static_cast<const float *>(v), static_cast<float *>(out)), c->stream), "Qwen attention core");
+}
+
+int fortai_hip_qwen35_attention_cache_download(fortai_hip_qwen35_attention *A, uint16_t *keys, uint16_t *values,
+    int positions) {
+    if (!A || !A->context || positions <= 0 || positions > A->max_context) return FORTAI_HIP_INVALID;
+    auto *c = A->context;
+    (void)hipSetDevice(c->device);
+    const size_t n = static_cast<size_t>(positions) * A->kv_heads;
+    hipError_t e = hipSuccess;
+    if (keys) e = hipMemcpyAsync(keys, A->kcache, n * A->head * 2, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && values) e = hipMemcpyAsync(values, A->vcache, n * A->value * 2, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "attention cache download");
+}
+
+int fortai_hip_qwen35_attention_cache_upload(fortai_hip_qwen35_attention *A, const uint16_t *keys,
+    const uint16_t *values, int positions) {
+    if (!A || !A->context || !keys || !values || positions <= 0 || positions > A->max_context)
+        return FORTAI_HIP_INVALID;
+    auto *c = A->context;
+    (void)hipSetDevice(c->device);
+    const size_t n = static_cast<size_t>(positions) * A->kv_heads;
+    hipError_t e = hipMemcpyAsync(A->kcache, keys, n * A->head * 2, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(A->vcache, values, n * A->value * 2, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "attention cache upload");
+}
+
+// fortai_cuda_backend.cu:1733-1736
+const char *fortai_hip_q8_last_error(const fortai_hip_q8_context *c) {
+    return c ? c->error : "invalid HIP context";
+}
+
+// ------------------------------------------------------------------ decoder
+namespace {
+hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
+    auto *c = d->context;
+    hipError_t e = d->emb16 ? launch_f16_embedding(d->emb16->data, d->hidden, c->token, 0, d->x, stream)
+                            : launch_q8_embedding(d->emb8->m, nullptr, c->token, 0, d->x, stream);
+    for (size_t i = 0; i < d->layers.size() && e == hipSuccess; ++i) {
+        const decoder_layer &L = d->layers[i];
+        MatvecInput in;
+        in.x = d->x;
+        in.norm = L.attn_norm;
+        in.eps = d->eps;
+        in.width = d->hidden;
+        if (L.recurrent) e = enqueue_recurrent(L.recurrent, in, Prologue::RMSNORM, d->x, d->x, stream);
+        else e = enqueue_attention(L.attention, in, Prologue::RMSNORM, d->x, d->x, stream);
+        if (e != hipSuccess) break;
+        in.norm = L.post_norm;
+        e = enqueue_ffn(L.gate, L.up, L.down, in, Prologue::RMSNORM, d->h, d->x, d->x, stream);
+    }
+    if (e != hipSuccess) return e;
+    ArgmaxState st;
+    st.partial_value = d->argmax_value;
+    st.partial_index = d->argmax_index;
+    st.done = d->argmax_done;
+    st.token = c->token;
+    st.trace = d->trace;
+    st.trace_capacity = d->max_context;
+    st.position = c->position;
+    if (d->out16)
+        return launch_f16_matvec(d->out16->data, d->vocab, d->hidden, d->x, d->output_norm, d->eps, d->logits, &st,
+            stream);
+    MatvecInput in;
+    in.x = d->x;
+    in.norm = d->output_norm;
+    in.eps = d->eps;
+    in.width = d->hidden;
+    const MatvecSegment s = segment(d->out8, d->logits);
+    e = launch_q8_matvec(&s, 1, in, Prologue::RMSNORM, Epilogue::STORE, stream);
+    if (e == hipSuccess) e = launch_argmax(d->logits, d->vocab, st, stream);
+    return e;
+}
+}  // namespace
+
+int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
+    fortai_hip_qwen35_recurrent *const *recurrent, fortai_hip_qwen35_attention *const *attention,
+    const fortai_hip_q8_weights *const *ffn_gate, const fortai_hip_q8_weights *const *ffn_up,
+    const fortai_hip_q8_weights *const *ffn_down, const float *const *attn_norm, const float *const *post_norm,
+    const float *output_norm, int hidden, const fortai_hip_f16_weights *emb16, const fortai_hip_q8_weights *emb8,
+    const fortai_hip_f16_weights *out16, const fortai_hip_q8_weights *out8, int max_context, float eps,
+    fortai_hip_qwen35_decoder **decoder) {
+    if (!c || !decoder || layer_count <= 0 || !recurrent || !attention || !ffn_gate || !ffn_up || !ffn_down ||
+        !attn_norm || !post_norm || !output_norm || hidden <= 0 || hidden % 64 || max_context <= 0 || eps <= 0.0f ||
+        (!emb16 == !emb8) || (!out16 == !out8))
+        return FORTAI_HIP_INVALID;
+    *decoder = nullptr;
+    if ((emb16 && (emb16->context != c || emb16->width != hidden)) || (emb8 && (!owned(c, emb8) || emb8->width != hidden)) ||
+        (out16 && (out16->context != c || out16->width != hidden)) || (out8 && (!owned(c, out8) || out8->width != hidden)))
+        return FORTAI_HIP_INVALID;
+    const int vocab = out16 ? out16->rows : out8->m.rows;
+    if (out16 && f16_matvec_workgroups(vocab) > 1 << 20) return FORTAI_HIP_INVALID;
+    auto *d = new (std::nothrow) fortai_hip_qwen35_decoder;
+    if (!d) return FORTAI_HIP_RUNTIME_ERROR;
+    d->context = c; d->hidden = hidden; d->vocab = vocab; d->max_context = max_context; d->eps = eps;
+    d->emb16 = emb16; d->emb8 = emb8; d->out16 = out16; d->out8 = out8;
+    int ffn = 0;
+    for (int i = 0; i < layer_count; ++i) {
+        decoder_layer L;
+        L.recurrent = recurrent[i];
+        L.attention = attention[i];
+        L.gate = ffn_gate[i]; L.up = ffn_up[i]; L.down = ffn_down[i];
+        const bool ok = (!L.recurrent != !L.attention) && owned(c, L.gate) && owned(c, L.up) && owned(c, L.down) &&
+            ffn_shapes_ok(L.gate, L.up, L.down) && L.gate->width == hidden && L.down->m.rows == hidden &&
+            attn_norm[i] && post_norm[i] &&
+            (L.recurrent ? (L.recurrent->context == c && L.recurrent->qkv->width == hidden && L.recurrent->out->m.rows == hidden)
+                         : (L.attention->context == c && L.attention->q->width == hidden && L.attention->o->m.rows == hidden &&
+                            L.attention->max_context >= max_context));
+        if (!ok) {
+            delete d;
+            return FORTAI_HIP_INVALID;
+        }
+        if (L.gate->m.rows > ffn) ffn = L.gate->m.rows;
+        d->layers.push_back(L);
+    }
+    d->ffn = ffn;
+    (void)hipSetDevice(c->device);
+    const int parts = out16 ? f16_matvec_workgroups(vocab) : 1024;
+    hipError_t e = hipSuccess;
+    for (auto &L : d->layers) {
+        if (e == hipSuccess) e = upload_f32(&L.attn_norm, attn_norm[&L - d->layers.data()], hidden, c->stream);
+        if (e == hipSuccess) e = upload_f32(&L.post_norm, post_norm[&L - d->layers.data()], hidden, c->stream);
+    }
+    if (e == hipSuccess) e = upload_f32(&d->output_norm, output_norm, hidden, c->stream);
+    if (e == hipSuccess) e = alloc(&d->x, hidden);
+    if (e == hipSuccess) e = alloc(&d->h, ffn);
+    if (e == hipSuccess) e = alloc(&d->logits, vocab);
+    if (e == hipSuccess) e = alloc(&d->argmax_value, parts);
+    if (e == hipSuccess) e = alloc(&d->argmax_index, parts);
+    if (e == hipSuccess) e = alloc(&d->argmax_done, 1);
+    if (e == hipSuccess) e = alloc(&d->trace, max_context + 1);
+    if (e == hipSuccess) e = hipMemsetAsync(d->argmax_done, 0, sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(d->trace, 0, (max_context + 1) * sizeof(int64_t), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    // capture one decode step as a graph
+    if (e == hipSuccess) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        const hipError_t ce = enqueue_decoder_step(d, c->stream);
+        e = hipStreamEndCapture(c->stream, &d->graph);
+        if (ce != hipSuccess) e = ce;
+    }
+    if (e == hipSuccess) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        fortai_hip_qwen35_decoder_destroy(d);
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen decoder create", e);
+    }
+    *decoder = d;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *d) {
+    if (!d) return FORTAI_HIP_OK;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    for (auto &L : d->layers) {
+        release(L.attn_norm);
+        release(L.post_norm);
+    }
+    release(d->output_norm); release(d->x); release(d->h); release(d->logits); release(d->argmax_value);
+    release(d->argmax_index); release(d->argmax_done); release(d->trace);
+    delete d;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_decoder_reset(fortai_hip_qwen35_decoder *d) {
+    if (!d) return FORTAI_HIP_INVALID;
+    for (auto &L : d->layers) {
+        const int rc = L.recurrent ? fortai_hip_qwen35_recurrent_reset(L.recurrent)
+                                   : fortai_hip_qwen35_attention_reset(L.attention);
+        if (rc != FORTAI_HIP_OK) return rc;
+    }
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    d->next_position = 0;
+    hipError_t e = hipMemsetAsync(d->trace, 0, (d->max_context + 1) * sizeof(int64_t), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(d->x, 0, d->hidden * sizeof(float), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "decoder reset");
+}
+
+int fortai_hip_qwen35_decoder_forward(fortai_hip_qwen35_decoder *d, int64_t token, int position, float *logits,
+    int64_t *next_token) {
+    if (!d || token < 0 || token >= (d->emb16 ? d->emb16->rows : d->emb8->m.rows) || position < 0 ||
+        position >= d->max_context)
+        return FORTAI_HIP_INVALID;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, c->token, token);
+    hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipGraphLaunch(d->exec, c->stream);
+    d->next_position = position + 1;
+    if (e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, d->logits, static_cast<size_t>(d->vocab) * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && next_token)
+        e = hipMemcpyAsync(next_token, c->token, sizeof(int64_t), hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && (logits || next_token)) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "decoder forward");
+}
+
+int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *d, int64_t token, int position, int steps,
+    int64_t *trace) {
+    if (!d || !trace || steps <= 0 || position < 0 || position + steps > d->max_context || token < 0 ||
+        token >= (d->emb16 ? d->emb16->rows : d->emb8->m.rows))
+        return FORTAI_HIP_INVALID;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, c->token, token);
+    hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
+    hipError_t e = hipGetLastError();
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(d->exec, c->stream);
+    d->next_position = position + steps;
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(trace, d->trace + position, static_cast<size_t>(steps) * sizeof(int64_t),
+            hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "decoder generate");
+}
+
+int fortai_hip_qwen35_decoder_replay(fortai_hip_qwen35_decoder *d, int steps) {
+    if (!d || steps <= 0 || d->next_position + steps > d->max_context) return FORTAI_HIP_INVALID;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipSuccess;
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(d->exec, c->stream);
+    d->next_position += steps;
+    return done(c, e, "decoder replay");
+}
+
+int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits) {
+    if (!d || !logits) return FORTAI_HIP_INVALID;
+    *logits = d->logits;
+    return FORTAI_HIP_OK;
+}
+
+}  // extern "C"

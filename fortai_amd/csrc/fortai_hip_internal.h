@@ -1,0 +1,156 @@
+// Internal types and device helpers of the gfx950 FortAI backend.
+//
+// Numerics conventions (all kernels are compiled with -ffp-contract=off):
+//  * multiply and add are separately rounded unless a fused multiply-add is
+//    written explicitly with __builtin_fmaf, mirroring where the reference CPU
+//    path uses FMA intrinsics (src/backend/cpu/fortai_q8_dot.c:320,377,391,393);
+//  * division and sqrtf are the correctly rounded IEEE operations (HIP's
+//    default for fp32), never the approximate reciprocal;
+//  * reductions that feed a float32 result through a double sum keep the double
+//    accumulator (src/models/qwen35/fortai_qwen35_cpu.f90:1414-1427).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fortai_hip {
+
+constexpr int kQ8Block = 32;       // values per Q8_0 block
+constexpr int kQ8Bytes = 34;       // GGUF bytes per block: fp16 scale + 32 x int8
+constexpr int kRowsPerWave = 8;    // a wave64 holds 8 rows x 8 lanes
+constexpr int kLanesPerRow = 8;    // the 8 fp32 lanes of the reference's AVX2 dot
+
+// ---------------------------------------------------------------- fp16 ----
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// gguf_fp16_to_real (src/fortai_gguf_runtime.f90:770-788): exact for finite
+// halves, exponent 31 decodes to +-huge instead of inf/NaN.
+__device__ __forceinline__ float gguf_half_to_real(uint16_t h) {
+    if ((h & 0x7c00u) == 0x7c00u) return (h & 0x8000u) ? -3.402823466e38f : 3.402823466e38f;
+    return half_bits_to_float(h);
+}
+
+// IEEE round-to-nearest-even binary32 -> binary16 (the F16C conversion the
+// AVX2 quantizer uses for its scale, src/backend/cpu/fortai_q8_dot.c:176).
+__device__ __forceinline__ uint16_t float_to_half_rne(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// The reference's float_to_half (src/backend/cpu/fortai_q8_dot.c:85-113),
+// used for the KV cache store (fortai_qwen35_cpu.f90:1594-1601): it adds one
+// half-ulp whenever bit 12 of the float fraction is set (ties round away from
+// zero); its subnormal branch tests bit 12 of the unshifted fraction.
+__device__ __forceinline__ uint16_t float_to_half_kv(float value) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, value);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    int32_t exponent = static_cast<int32_t>((bits >> 23) & 0xffu) - 127 + 15;
+    uint32_t fraction = bits & 0x007fffffu;
+    if (exponent <= 0) {
+        if (exponent < -10) return static_cast<uint16_t>(sign);
+        fraction = (fraction | 0x00800000u) >> static_cast<uint32_t>(1 - exponent);
+        if (bits & 0x00001000u) fraction += 0x00002000u;
+        return static_cast<uint16_t>(sign | (fraction >> 13));
+    }
+    if (exponent >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    if (fraction & 0x00001000u) {
+        fraction += 0x00002000u;
+        if (fraction & 0x00800000u) {
+            fraction = 0;
+            if (++exponent >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+        }
+    }
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(exponent) << 10) | (fraction >> 13));
+}
+
+// ------------------------------------------------------------- scalars ----
+
+// The vector exp polynomial of the reference SiLU (fortai_q8_dot.c:10-51):
+// Cody-Waite reduction by ln2 (hi/lo split) and a degree-6 Cephes-style
+// polynomial, evaluated with separately rounded multiply and add.
+__device__ __forceinline__ float expf_poly(float value) {
+    value = (value < 88.3762626647949f) ? value : 88.3762626647949f;
+    value = (value > -88.3762626647949f) ? value : -88.3762626647949f;
+    float fx = value * 1.44269504088896341f + 0.5f;
+    int32_t e = static_cast<int32_t>(fx);
+    if (static_cast<float>(e) > fx) e -= 1;
+    fx = static_cast<float>(e);
+    value = value - fx * 0.693359375f;
+    value = value - fx * -2.12194440e-4f;
+    const float z = value * value;
+    float p = 1.9875691500e-4f;
+    p = p * value + 1.3981999507e-3f;
+    p = p * value + 8.3334519073e-3f;
+    p = p * value + 4.1665795894e-2f;
+    p = p * value + 1.6666665459e-1f;
+    p = p * value + 5.0000001201e-1f;
+    p = p * z + value;
+    p = p + 1.0f;
+    return p * __builtin_bit_cast(float, static_cast<uint32_t>(e + 0x7f) << 23);
+}
+
+// One lane of the reference's vector SiLU (fortai_q8_dot.c:450-459).
+__device__ __forceinline__ float silu_poly(float x) {
+    float r = x / (1.0f + expf_poly(0.0f - x));
+    if (x < -20.0f) r = 0.0f;
+    if (x > 20.0f) r = x;
+    return r;
+}
+
+// expf/logf of the reference's Fortran intrinsics (glibc, correctly rounded
+// in practice) evaluated in double and rounded once to float.
+__device__ __forceinline__ float exp_rounded(float v) { return static_cast<float>(exp(static_cast<double>(v))); }
+__device__ __forceinline__ float log_rounded(float v) { return static_cast<float>(log(static_cast<double>(v))); }
+
+// fortai_qwen35_cpu.f90:1506-1514
+__device__ __forceinline__ float sigmoid_ref(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + exp_rounded(-v));
+    const float e = exp_rounded(v);
+    return e / (1.0f + e);
+}
+
+// fortai_qwen35_cpu.f90:1516-1526
+__device__ __forceinline__ float softplus_ref(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return exp_rounded(v);
+    return log_rounded(1.0f + exp_rounded(v));
+}
+
+// ------------------------------------------------------ streaming loads ----
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// Non-temporal 16/8-byte loads for weights that are streamed exactly once.
+__device__ __forceinline__ uint4 load_stream(const uint4 *p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 load_stream(const uint2 *p) {
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
+    return make_uint2(v.x, v.y);
+}
+
+// --------------------------------------------------------- reductions ----
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// Horizontal sum of the 8 row lanes in the AVX2 order of
+// fortai_q8_dot.c:323-330 / :345-353: (l + l^4), then (+ ^2), then (+ ^1).
+// fp32 addition is commutative, so every lane of the group ends with the
+// bit pattern lane 0 of the reference produces.
+__device__ __forceinline__ float row_hsum8(float v) {
+    v = v + __shfl_xor(v, 4);
+    v = v + __shfl_xor(v, 2);
+    v = v + __shfl_xor(v, 1);
+    return v;
+}
+
+}  // namespace fortai_hip

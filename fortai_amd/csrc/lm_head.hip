@@ -1,0 +1,210 @@
+// fp16 LM head (tied token embedding) with a fused greedy argmax.
+//
+// The reference evaluates an F16 matrix row by row with a sequential fp32 dot,
+// value(i) * x(i) accumulated left to right (fortai_gguf_runtime.f90:382-386,
+// :390-422), and no activation quantisation.  Each thread here owns one row
+// and runs exactly that chain, so the logits are bit-identical to the CPU
+// path.  To keep the HBM stream coalesced, a 256-row x 64-column fp16 tile
+// (8 full 128-byte lines per wave load) is staged through LDS with a
+// 144-byte row pitch (36 dwords: eight 16-byte reads of consecutive rows
+// start on distinct 4-bank groups), and the next tile is prefetched into
+// registers while the current one is consumed.
+//
+// The greedy step (maxloc, first maximum; app/fortai_cpu_run.f90:58) is
+// fused: every workgroup reduces its 256 rows to (value, first index), and
+// the last workgroup to finish (device-scope counter) reduces the partials,
+// writes the token, appends it to the trace and advances the device
+// position, so a captured graph can replay decode steps back to back.
+#include "fortai_hip_internal.h"
+#include "fortai_hip_kernels.h"
+
+namespace fortai_hip {
+
+namespace {
+
+constexpr int kRows = 256;      // rows per workgroup (one per thread)
+constexpr int kTileK = 64;      // fp16 columns per tile
+constexpr int kPitch = 72;      // halves per LDS row (64 + 8 pad)
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+// (value, index) first-maximum reduction over the workgroup; result valid in
+// thread 0.
+__device__ __forceinline__ void block_argmax(float &v, int &i, float *sv, int *si) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(v, m);
+        const int oi = __shfl_xor(i, m);
+        if (better(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+    const int tid = static_cast<int>(threadIdx.x);
+    const int waves = static_cast<int>(blockDim.x) >> 6;
+    if ((tid & 63) == 0) { sv[tid >> 6] = v; si[tid >> 6] = i; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < waves; ++w)
+            if (better(sv[w], si[w], v, i)) { v = sv[w]; i = si[w]; }
+    }
+}
+
+// The last workgroup reduces all partials and publishes the greedy token.
+__device__ void finish_argmax(const ArgmaxState &st, float v, int i, float *sv, int *si) {
+    __shared__ bool last;
+    const int tid = static_cast<int>(threadIdx.x);
+    if (tid == 0) {
+        __hip_atomic_store(st.partial_value + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(st.partial_index + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        const unsigned prev = atomicAdd(st.done, 1u);
+        last = (prev == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    for (int w = tid; w < static_cast<int>(gridDim.x); w += static_cast<int>(blockDim.x)) {
+        const float pv = __hip_atomic_load(st.partial_value + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int pi = __hip_atomic_load(st.partial_index + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (better(pv, pi, bv, bi)) { bv = pv; bi = pi; }
+    }
+    __syncthreads();
+    block_argmax(bv, bi, sv, si);
+    if (tid == 0) {
+        const int64_t token = bi;
+        *st.token = token;
+        if (st.position) {
+            const int p = *st.position;
+            if (st.trace && p >= 0 && p < st.trace_capacity) st.trace[p] = token;
+            *st.position = p + 1;
+        }
+        __hip_atomic_store(st.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <bool RMS, bool ARGMAX>
+__global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__restrict__ w, int rows, int width,
+    const float *__restrict__ x, const float *__restrict__ norm, float eps, float *__restrict__ out,
+    ArgmaxState st) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    uint16_t *tile = reinterpret_cast<uint16_t *>(lds);
+    float *xs = reinterpret_cast<float *>(lds + kRows * kPitch * 2);
+    __shared__ double red[kRows / 64];
+    __shared__ float sv[kRows / 64];
+    __shared__ int si[kRows / 64];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int row0 = static_cast<int>(blockIdx.x) * kRows;
+
+    // x (optionally RMS-normalised, fortai_qwen35_cpu.f90:707) into LDS
+    float inv = 1.0f;
+    if constexpr (RMS) {
+        double ss = 0.0;
+        for (int i = tid; i < width; i += kRows) ss += static_cast<double>(x[i]) * static_cast<double>(x[i]);
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        double total = 0.0;
+        for (int i = 0; i < kRows / 64; ++i) total += red[i];
+        inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+    }
+    for (int i = tid; i < width; i += kRows) xs[i] = RMS ? (x[i] * inv) * norm[i] : x[i];
+
+    // tile loader mapping: load j of thread t covers row (t + 256 j) / 8,
+    // 16-byte segment (t + 256 j) % 8 of the 128-byte row slice
+    constexpr int kLoads = kRows * kTileK * 2 / 16 / kRows;  // 8
+    uint4 regs[kLoads];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int li = tid + kRows * j;
+            const int r = li >> 3, seg = li & 7;
+            const int grow = row0 + r;
+            if (grow < rows)
+                regs[j] = load_stream(reinterpret_cast<const uint4 *>(
+                    w + static_cast<size_t>(grow) * width + k0 + seg * 8));
+            else
+                regs[j] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int li = tid + kRows * j;
+            const int r = li >> 3, seg = li & 7;
+            *reinterpret_cast<uint4 *>(tile + r * kPitch + seg * 8) = regs[j];
+        }
+    };
+
+    float acc = 0.0f;
+    fetch(0);
+    for (int k0 = 0; k0 < width; k0 += kTileK) {
+        __syncthreads();  // previous tile consumed (and xs written on the first pass)
+        stash();
+        __syncthreads();
+        if (k0 + kTileK < width) fetch(k0 + kTileK);
+        const uint16_t *mine = tile + tid * kPitch;
+#pragma unroll
+        for (int s = 0; s < kTileK / 8; ++s) {
+            const uint4 h8 = *reinterpret_cast<const uint4 *>(mine + s * 8);
+            const uint32_t hw[4] = {h8.x, h8.y, h8.z, h8.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float a = gguf_half_to_real(static_cast<uint16_t>(hw[q] & 0xffffu));
+                const float b = gguf_half_to_real(static_cast<uint16_t>(hw[q] >> 16));
+                const int k = k0 + s * 8 + q * 2;
+                acc = acc + a * xs[k];
+                acc = acc + b * xs[k + 1];
+            }
+        }
+    }
+    const int row = row0 + tid;
+    if (row < rows) out[row] = acc;
+    if constexpr (ARGMAX) {
+        float v = row < rows ? acc : -__builtin_inff();
+        int i = row < rows ? row : 0x7fffffff;
+        block_argmax(v, i, sv, si);
+        finish_argmax(st, v, i, sv, si);
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float *values, int n, ArgmaxState st) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    float v = -__builtin_inff();
+    int i = 0x7fffffff;
+    for (int k = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); k < n;
+         k += static_cast<int>(gridDim.x * blockDim.x))
+        if (better(values[k], k, v, i)) { v = values[k]; i = k; }
+    block_argmax(v, i, sv, si);
+    finish_argmax(st, v, i, sv, si);
+}
+
+}  // namespace
+
+int f16_matvec_workgroups(int rows) { return (rows + kRows - 1) / kRows; }
+
+hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, const float *x, const float *norm, float eps,
+    float *out, const ArgmaxState *argmax, hipStream_t stream) {
+    if (rows <= 0 || width <= 0 || width % kTileK) return hipErrorInvalidValue;
+    const int grid = f16_matvec_workgroups(rows);
+    const size_t lds = static_cast<size_t>(kRows) * kPitch * 2 + static_cast<size_t>(width) * 4;
+    ArgmaxState st = argmax ? *argmax : ArgmaxState{};
+    if (norm) {
+        if (argmax) hipLaunchKernelGGL((f16_matvec_kernel<true, true>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
+        else hipLaunchKernelGGL((f16_matvec_kernel<true, false>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
+    } else {
+        if (argmax) hipLaunchKernelGGL((f16_matvec_kernel<false, true>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
+        else hipLaunchKernelGGL((f16_matvec_kernel<false, false>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, hipStream_t stream) {
+    int grid = (n + 255) / 256;
+    if (grid > 1024) grid = 1024;
+    hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, stream, values, n, state);
+    return hipGetLastError();
+}
+
+}  // namespace fortai_hip

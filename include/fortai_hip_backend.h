@@ -1,0 +1,272 @@
+/*
+ * fortai_hip_backend.h -- C ABI of the MI355X (gfx950) FortAI backend.
+ *
+ * Drop-in counterpart of the reference's CUDA ABI
+ * (backend/cuda/fortai_cuda_backend.h:22-152): every fortai_cuda_* entry point
+ * exists here as fortai_hip_* with the same arguments, ownership and return
+ * codes, so the reference's iso_c_binding wrapper
+ * (src/backend/cuda/fortai_backend_cuda.f90:67-413) binds it by renaming the
+ * bind(C) names.  Entry points marked [extension] have no reference
+ * counterpart: the fp16 LM head / embedding the CUDA path lacks, parity probes
+ * for the tests, and a fused whole-token decoder.
+ *
+ * Conventions (as the reference, fortai_cuda_backend.cu:42-52,805-893):
+ *  - return 0 OK, 1 INVALID (argument or shape precondition), 2 RUNTIME_ERROR
+ *    (HIP failure; message via fortai_hip_q8_last_error);
+ *  - the backend allocates handles and the caller destroys them; layers and
+ *    weights borrow their context; destroy(NULL) returns OK;
+ *  - one non-blocking stream per context; device ops are asynchronous, ops that
+ *    return host data synchronise;
+ *  - kernels read the token position from device memory written by
+ *    set_position, so a captured graph replays with new positions.
+ */
+#ifndef FORTAI_HIP_BACKEND_H
+#define FORTAI_HIP_BACKEND_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct fortai_hip_q8_context fortai_hip_q8_context;
+typedef struct fortai_hip_q8_weights fortai_hip_q8_weights;
+typedef struct fortai_hip_qwen35_recurrent fortai_hip_qwen35_recurrent;
+typedef struct fortai_hip_qwen35_attention fortai_hip_qwen35_attention;
+typedef struct fortai_hip_f16_weights fortai_hip_f16_weights;          /* [extension] */
+typedef struct fortai_hip_qwen35_decoder fortai_hip_qwen35_decoder;    /* [extension] */
+
+enum {
+    FORTAI_HIP_OK = 0,
+    FORTAI_HIP_INVALID = 1,
+    FORTAI_HIP_RUNTIME_ERROR = 2
+};
+
+/* ---- context (fortai_cuda_backend.h:22-27) ---- */
+int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context);
+int fortai_hip_q8_context_destroy(fortai_hip_q8_context *context);
+int fortai_hip_q8_context_set_position(fortai_hip_q8_context *context, int position);
+int fortai_hip_q8_context_capture_begin(fortai_hip_q8_context *context);
+int fortai_hip_q8_context_capture_end(fortai_hip_q8_context *context);
+int fortai_hip_q8_context_graph_launch(fortai_hip_q8_context *context);
+/* [extension] wait for all work queued on the context's stream */
+int fortai_hip_q8_context_synchronize(fortai_hip_q8_context *context);
+
+/* ---- resident Q8_0 weights (fortai_cuda_backend.h:29-32).  Accepts the raw
+ * GGUF Q8_0 bytes [rows][width/32][34]; they are repacked on the device into a
+ * lane-interleaved int8 plane plus an fp16 scale plane (same 34 B / 32 values). */
+int fortai_hip_q8_weights_upload(fortai_hip_q8_context *context,
+    const void *host_weights, size_t weight_bytes, int rows, int width,
+    fortai_hip_q8_weights **weights);
+int fortai_hip_q8_weights_destroy(fortai_hip_q8_weights *weights);
+
+/* ---- device buffers (fortai_cuda_backend.h:34-45) ---- */
+int fortai_hip_q8_device_buffer_create(fortai_hip_q8_context *context,
+    size_t bytes, void **device_buffer);
+int fortai_hip_q8_device_buffer_destroy(fortai_hip_q8_context *context,
+    void *device_buffer);
+int fortai_hip_q8_device_buffer_upload(fortai_hip_q8_context *context,
+    void *device_buffer, const void *host_data, size_t bytes);
+int fortai_hip_q8_device_buffer_upload_ptr(fortai_hip_q8_context *context,
+    void *device_buffer, const void *host_data, size_t bytes);
+int fortai_hip_q8_device_buffer_download(fortai_hip_q8_context *context,
+    void *host_data, const void *device_buffer, size_t bytes);
+
+/* ---- resident ops (fortai_cuda_backend.h:47-66).  device_activation of
+ * matvec_resident is a device Q8_0 activation in GGUF block layout; kernel_ms
+ * times the kernel only. */
+int fortai_hip_q8_matvec_resident(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_activation,
+    void *device_output, float *kernel_ms);
+int fortai_hip_q8_matvec_device_f32(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_activation,
+    size_t activation_elements, void *device_output, size_t output_elements);
+int fortai_hip_qwen35_embedding_device(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, int64_t token_id, void *device_output,
+    size_t output_elements);
+int fortai_hip_qwen35_copy_device(fortai_hip_q8_context *context,
+    const void *device_input, void *device_output, size_t bytes);
+int fortai_hip_qwen35_add_device(fortai_hip_q8_context *context,
+    const void *device_left, const void *device_right, void *device_output,
+    size_t elements);
+int fortai_hip_qwen35_rms_norm_device(fortai_hip_q8_context *context,
+    const void *device_input, const void *device_weights, void *device_output,
+    size_t elements, float epsilon);
+
+/* ---- host-controlled ops (fortai_cuda_backend.h:68-110): host Q8_0
+ * activation in, host fp32 out; elapsed_ms includes the transfers. */
+int fortai_hip_q8_matvec_host(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *host_activation,
+    size_t activation_bytes, float *host_output, size_t output_bytes,
+    float *elapsed_ms);
+int fortai_hip_q8_matvec_host_pair(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *first_weights,
+    const fortai_hip_q8_weights *second_weights, const void *host_activation,
+    size_t activation_bytes, float *first_output, size_t first_output_bytes,
+    float *second_output, size_t second_output_bytes, float *elapsed_ms);
+int fortai_hip_q8_matvec_host_triplet(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *first_weights,
+    const fortai_hip_q8_weights *second_weights,
+    const fortai_hip_q8_weights *third_weights, const void *host_activation,
+    size_t activation_bytes, float *first_output, size_t first_output_bytes,
+    float *second_output, size_t second_output_bytes, float *third_output,
+    size_t third_output_bytes, float *elapsed_ms);
+int fortai_hip_q8_matvec_host_triplet_contiguous(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *first_weights,
+    const fortai_hip_q8_weights *second_weights,
+    const fortai_hip_q8_weights *third_weights, const void *host_activation,
+    size_t activation_bytes, float *host_output, size_t host_output_bytes,
+    float *elapsed_ms);
+int fortai_hip_q8_ffn_host(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *gate_weights,
+    const fortai_hip_q8_weights *up_weights,
+    const fortai_hip_q8_weights *down_weights, const void *host_activation,
+    size_t activation_bytes, float *host_output, size_t output_bytes,
+    float *elapsed_ms);
+int fortai_hip_q8_ffn_device(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *gate_weights,
+    const fortai_hip_q8_weights *up_weights,
+    const fortai_hip_q8_weights *down_weights, const void *device_activation,
+    size_t activation_elements, void *device_output, size_t output_elements);
+
+/* ---- Qwen3.5 recurrent (Gated DeltaNet) layer (fortai_cuda_backend.h:112-134).
+ * Requires state_size == head_size, head_size in {64,128,256},
+ * value_heads % key_heads == 0, value_heads * head_size == inner_size. */
+int fortai_hip_qwen35_recurrent_create(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *qkv_weights,
+    const fortai_hip_q8_weights *gate_weights,
+    const fortai_hip_q8_weights *alpha_weights,
+    const fortai_hip_q8_weights *beta_weights,
+    const fortai_hip_q8_weights *output_weights,
+    const void *conv_weights, size_t conv_weight_bytes, int conv_size, int conv_kernel,
+    const void *ssm_a, size_t ssm_a_bytes, const void *ssm_dt, size_t ssm_dt_bytes,
+    const void *ssm_norm, size_t ssm_norm_bytes, int state_size, int key_heads,
+    int value_heads, int head_size, int inner_size, float norm_epsilon,
+    fortai_hip_qwen35_recurrent **layer);
+int fortai_hip_qwen35_recurrent_destroy(fortai_hip_qwen35_recurrent *layer);
+int fortai_hip_qwen35_recurrent_reset(fortai_hip_qwen35_recurrent *layer);
+int fortai_hip_qwen35_recurrent_run(fortai_hip_qwen35_recurrent *layer,
+    const void *host_activation, size_t activation_bytes, float *host_output,
+    size_t output_bytes, float *elapsed_ms);
+int fortai_hip_qwen35_recurrent_run_device(fortai_hip_qwen35_recurrent *layer,
+    const void *device_activation, size_t activation_elements,
+    void *device_output, size_t output_elements);
+
+/* ---- Qwen3.5 gated full-attention layer (fortai_cuda_backend.h:136-150).
+ * The KV cache is fp16, [max_context][kv_heads][head_size], written with the
+ * reference CPU path's float_to_half (ties away from zero). */
+int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *query_weights,
+    const fortai_hip_q8_weights *key_weights,
+    const fortai_hip_q8_weights *value_weights,
+    const fortai_hip_q8_weights *output_weights,
+    const void *query_norm, size_t query_norm_bytes,
+    const void *key_norm, size_t key_norm_bytes,
+    int heads, int key_value_heads, int head_size, int value_size,
+    int max_context, int rope_dimension, float rope_base, float norm_epsilon,
+    fortai_hip_qwen35_attention **layer);
+int fortai_hip_qwen35_attention_destroy(fortai_hip_qwen35_attention *layer);
+int fortai_hip_qwen35_attention_reset(fortai_hip_qwen35_attention *layer);
+int fortai_hip_qwen35_attention_run_device(fortai_hip_qwen35_attention *layer,
+    const void *device_activation, size_t activation_elements, int position,
+    void *device_output, size_t output_elements);
+
+const char *fortai_hip_q8_last_error(const fortai_hip_q8_context *context);
+
+/* =================== [extension] entry points ======================== */
+
+/* fp16 matrices (tied token embedding / LM head), GGUF F16 row-major
+ * [rows][width].  The matvec runs the reference's sequential fp32 dot per row
+ * (fortai_gguf_runtime.f90:382-386) and can fuse the first-index argmax
+ * (app/fortai_cpu_run.f90:58): device_token (int64, may be NULL). */
+int fortai_hip_f16_weights_upload(fortai_hip_q8_context *context,
+    const void *host_weights, size_t weight_bytes, int rows, int width,
+    fortai_hip_f16_weights **weights);
+int fortai_hip_f16_weights_destroy(fortai_hip_f16_weights *weights);
+int fortai_hip_f16_matvec_device(fortai_hip_q8_context *context,
+    const fortai_hip_f16_weights *weights, const void *device_activation,
+    size_t activation_elements, void *device_output, size_t output_elements,
+    void *device_token);
+int fortai_hip_qwen35_embedding_f16_device(fortai_hip_q8_context *context,
+    const fortai_hip_f16_weights *weights, int64_t token_id, void *device_output,
+    size_t output_elements);
+/* first-index argmax of a device fp32 vector into a device int64 */
+int fortai_hip_argmax_device(fortai_hip_q8_context *context,
+    const void *device_values, size_t elements, void *device_token);
+
+/* Parity probes: fortai_q8_quantize on device (GGUF block bytes + fp32
+ * scales), and the exact int32 dot of every (row, block) [rows][width/32]. */
+int fortai_hip_q8_quantize_device(fortai_hip_q8_context *context,
+    const void *device_input, size_t elements, void *device_blocks,
+    void *device_scales);
+int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_activation,
+    void *device_dots);
+
+/* Recurrent-layer core step (conv1d + SiLU + L2 norm + decay/beta + delta
+ * rule; no projections, no gated norm): device fp32 qkv [conv_size], alpha and
+ * beta [value_heads] in, raw output [inner_size].  State access uses the
+ * reference layouts: gdn [value_heads][head][head] row-major, conv
+ * [conv_kernel-1][conv_size] oldest first. */
+int fortai_hip_qwen35_recurrent_core_device(fortai_hip_qwen35_recurrent *layer,
+    const void *device_qkv, const void *device_alpha, const void *device_beta,
+    void *device_output);
+int fortai_hip_qwen35_recurrent_state_download(fortai_hip_qwen35_recurrent *layer,
+    float *host_gdn_state, size_t gdn_bytes, float *host_conv_state, size_t conv_bytes);
+int fortai_hip_qwen35_recurrent_state_upload(fortai_hip_qwen35_recurrent *layer,
+    const float *host_gdn_state, size_t gdn_bytes, const float *host_conv_state,
+    size_t conv_bytes);
+
+/* Attention-layer core step at the context's device position: q projection
+ * output [heads][q | gate], k [kv_heads][head], v [kv_heads][value] (device
+ * fp32) -> gated attention output [heads][value].  Cache access in fp16 bits
+ * for positions [0, positions). */
+int fortai_hip_qwen35_attention_core_device(fortai_hip_qwen35_attention *layer,
+    const void *device_query, const void *device_key, const void *device_value,
+    void *device_output);
+int fortai_hip_qwen35_attention_cache_download(fortai_hip_qwen35_attention *layer,
+    uint16_t *host_keys, uint16_t *host_values, int positions);
+int fortai_hip_qwen35_attention_cache_upload(fortai_hip_qwen35_attention *layer,
+    const uint16_t *host_keys, const uint16_t *host_values, int positions);
+
+/* Fused whole-token decoder over already created layers and weights.
+ * Layer i is recurrent[i] (GDN) or attention[i] (full attention); every layer
+ * has ffn_gate/up/down and host fp32 attn_norm/post_norm [hidden].  The token
+ * embedding and LM head are fp16 (tied allowed) or Q8_0.  One decode step is a
+ * single captured HIP graph: embedding, 5 launches per layer, LM head with
+ * the fused argmax; the graph advances the device token and position itself,
+ * so generate() replays it back to back with no host round trip per token. */
+int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *context, int layer_count,
+    fortai_hip_qwen35_recurrent *const *recurrent,
+    fortai_hip_qwen35_attention *const *attention,
+    const fortai_hip_q8_weights *const *ffn_gate,
+    const fortai_hip_q8_weights *const *ffn_up,
+    const fortai_hip_q8_weights *const *ffn_down,
+    const float *const *attn_norm, const float *const *post_norm,
+    const float *output_norm, int hidden_size,
+    const fortai_hip_f16_weights *embedding_f16, const fortai_hip_q8_weights *embedding_q8,
+    const fortai_hip_f16_weights *output_f16, const fortai_hip_q8_weights *output_q8,
+    int max_context, float norm_epsilon, fortai_hip_qwen35_decoder **decoder);
+int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *decoder);
+/* zero every layer state and the token trace */
+int fortai_hip_qwen35_decoder_reset(fortai_hip_qwen35_decoder *decoder);
+/* one step at (token, position): host_logits (vocab floats) and next_token
+ * may be NULL; synchronises only when either is requested */
+int fortai_hip_qwen35_decoder_forward(fortai_hip_qwen35_decoder *decoder, int64_t token,
+    int position, float *host_logits, int64_t *next_token);
+/* greedy decode of `steps` tokens starting from (token, position); the trace
+ * (steps ids) is written to host_trace.  Steps are enqueued back to back. */
+int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *decoder, int64_t token,
+    int position, int steps, int64_t *host_trace);
+/* enqueue `steps` further graph replays continuing from the device token and
+ * position (no host synchronisation; for timing loops) */
+int fortai_hip_qwen35_decoder_replay(fortai_hip_qwen35_decoder *decoder, int steps);
+/* device pointer of the decoder's logits [vocab] */
+int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
