@@ -33,6 +33,8 @@ _SIGNATURES = {
     "fortai_hip_q8_context_capture_end": [_vp],
     "fortai_hip_q8_context_graph_launch": [_vp],
     "fortai_hip_q8_context_synchronize": [_vp],
+    "fortai_hip_q8_context_timer_start": [_vp],
+    "fortai_hip_q8_context_timer_stop": [_vp, _fp],
     "fortai_hip_q8_weights_upload": [_vp, _vp, _sz, _i, _i, _vpp],
     "fortai_hip_q8_weights_destroy": [_vp],
     "fortai_hip_q8_device_buffer_create": [_vp, _sz, _vpp],
@@ -150,6 +152,23 @@ class Context:
 
     def synchronize(self) -> None:
         self.call("fortai_hip_q8_context_synchronize", self.h)
+
+    def timer_start(self) -> None:
+        self.call("fortai_hip_q8_context_timer_start", self.h)
+
+    def timer_stop(self) -> float:
+        ms = C.c_float()
+        self.call("fortai_hip_q8_context_timer_stop", self.h, C.byref(ms))
+        return float(ms.value)
+
+    def capture_begin(self) -> None:
+        self.call("fortai_hip_q8_context_capture_begin", self.h)
+
+    def capture_end(self) -> None:
+        self.call("fortai_hip_q8_context_capture_end", self.h)
+
+    def graph_launch(self) -> None:
+        self.call("fortai_hip_q8_context_graph_launch", self.h)
 
     # ---- device buffers
     def alloc(self, nbytes: int) -> "DeviceBuffer":

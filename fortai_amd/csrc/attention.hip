@@ -5,15 +5,15 @@
 // Reference: forward_attention, fortai_qwen35_cpu.f90:990-1033 (two-pass
 // softmax over positions 0..pos, serial per head).  Here the context is split
 // into chunks across workgroups (flash-decoding); one workgroup serves the
-// whole GQA group of a kv head, so every K/V row is read from HBM once.  The
-// last workgroup of a kv head (device-scope counter) merges the chunk
-// partials with the usual log-sum-exp rescale.
+// whole GQA group of a kv head, so every K/V row is read from HBM once.
 //
 // Bit-exact parts: q/k normalisation (double sum of squares), RoPE from a
 // host-computed table holding the reference's cos/sin values, and the fp16
 // append through the reference's float_to_half (fortai_q8_dot.c:85-113, which
 // rounds ties away from zero).  The softmax and P.V sums are re-associated
-// (fp32, within the 1e-3 relative gate).
+// (fp32, within the 1e-3 relative gate).  The chunk partials are merged by a
+// second small kernel (a cross-workgroup handoff inside one kernel would need
+// a device-scope fence, i.e. an L2 writeback, per workgroup).
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
 
@@ -25,11 +25,12 @@ constexpr int kThreads = 256;
 constexpr int kTile = 64;        // positions per LDS tile
 constexpr int kMaxGroup = 4;     // q heads per kv head handled per workgroup
 constexpr int kMaxHead = 256;
+constexpr int kMaxChunks = 128;  // attention_chunk() keeps the chunk count below this
 
 // RMSNorm with weights over a head slice in LDS (fortai_qwen35_cpu.f90:1434-1453),
 // then RoPE on the first rope_dim values (:1473-1497).  One wave per slice.
-__device__ void norm_rope(float *v, int head, const float *w, float eps, const float2 *rope, int rope_dim,
-    int lane) {
+__device__ __forceinline__ void norm_rope(float *v, int head, const float *w, float eps, const float2 *rope,
+    int rope_dim, int lane) {
     double ss = 0.0;
     for (int i = lane; i < head; i += 64) ss += static_cast<double>(v[i]) * static_cast<double>(v[i]);
     ss = wave_sum(ss);
@@ -47,15 +48,56 @@ __device__ void norm_rope(float *v, int head, const float *w, float eps, const f
     __builtin_amdgcn_wave_barrier();
 }
 
+template <bool FINITE>
+__device__ __forceinline__ float kv_value(uint16_t h) {
+    return FINITE ? half_bits_to_float(h) : gguf_half_to_real(h);
+}
+
+// scores of the 64 positions of a tile: wave g = q head g, lane = position
+template <bool FINITE>
+__device__ __forceinline__ float tile_score(const float *q, const uint16_t *krow, int head) {
+    const float4 *q4 = reinterpret_cast<const float4 *>(q);
+    const uint4 *k8 = reinterpret_cast<const uint4 *>(krow);
+    float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll 4
+    for (int i = 0; i < head / 8; ++i) {
+        const uint4 h8 = k8[i];
+        const float4 qa = q4[2 * i], qb = q4[2 * i + 1];
+        d0 = __builtin_fmaf(qa.x, kv_value<FINITE>(static_cast<uint16_t>(h8.x)), d0);
+        d1 = __builtin_fmaf(qa.y, kv_value<FINITE>(static_cast<uint16_t>(h8.x >> 16)), d1);
+        d2 = __builtin_fmaf(qa.z, kv_value<FINITE>(static_cast<uint16_t>(h8.y)), d2);
+        d3 = __builtin_fmaf(qa.w, kv_value<FINITE>(static_cast<uint16_t>(h8.y >> 16)), d3);
+        d0 = __builtin_fmaf(qb.x, kv_value<FINITE>(static_cast<uint16_t>(h8.z)), d0);
+        d1 = __builtin_fmaf(qb.y, kv_value<FINITE>(static_cast<uint16_t>(h8.z >> 16)), d1);
+        d2 = __builtin_fmaf(qb.z, kv_value<FINITE>(static_cast<uint16_t>(h8.w)), d2);
+        d3 = __builtin_fmaf(qb.w, kv_value<FINITE>(static_cast<uint16_t>(h8.w >> 16)), d3);
+    }
+    return (d0 + d1) + (d2 + d3);
+}
+
+template <bool FINITE>
+__device__ __forceinline__ void tile_pv(float *acc, const float (*prob)[kTile], const uint16_t (*vtile)[kMaxHead],
+    const float *vn, int n, int new_j, int group, int d) {
+#pragma unroll 4
+    for (int j = 0; j < n; ++j) {
+        const float vv = (j == new_j) ? vn[d] : kv_value<FINITE>(vtile[j][d]);
+        for (int g = 0; g < kMaxGroup; ++g)
+            if (g < group) acc[g] = __builtin_fmaf(prob[g][j], vv, acc[g]);
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionParams p) {
-    __shared__ float qh[kMaxGroup][kMaxHead];
-    __shared__ float kn[kMaxHead];
-    __shared__ float vn[kMaxHead];
-    __shared__ uint16_t ktile[kTile][kMaxHead + 8];
-    __shared__ uint16_t vtile[kTile][kMaxHead];
+    __shared__ __align__(16) float qh[kMaxGroup * kMaxHead];
+    __shared__ __align__(16) float kn[kMaxHead];
+    __shared__ __align__(16) float vn[kMaxHead];
+    __shared__ __align__(16) float qw[kMaxHead];
+    __shared__ __align__(16) float kw[kMaxHead];
+    __shared__ __align__(16) float2 rs[kMaxHead / 2];
+    __shared__ __align__(16) uint16_t ktile[kTile][kMaxHead + 8];
+    __shared__ __align__(16) uint16_t vtile[kTile][kMaxHead];
     __shared__ float prob[kMaxGroup][kTile];
     __shared__ float rescale[kMaxGroup];
-    __shared__ bool last;
+    __shared__ int overflow;
 
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = tid >> 6, lane = tid & 63;
@@ -71,34 +113,90 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
     const int head = p.head, value = p.value;
     const int p0 = c * p.chunk;
     const int p1 = (p0 + p.chunk < L) ? p0 + p.chunk : L;
-    const float2 *rope = p.rope + static_cast<size_t>(pos) * (p.rope_dim / 2);
     const bool owns_new = (pos >= p0 && pos < p1);
+    const int h4 = head / 4, v4 = value / 4, half = p.rope_dim / 2;
 
-    // q of the group's heads: normalise + rotate (one wave per head)
-    for (int g = wave; g < group; g += kThreads / 64) {
-        const float *src = p.q + static_cast<size_t>(kvh * group + g) * 2 * head;
-        for (int i = lane; i < head; i += 64) qh[g][i] = src[i];
-        __builtin_amdgcn_wave_barrier();
-        norm_rope(qh[g], head, p.q_norm, p.eps, rope, p.rope_dim, lane);
+    // every prologue load is issued before the first use
+    const int qn = group * h4;
+    float4 qv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), aux = qv, vv4 = qv;
+    float2 rv = make_float2(0.0f, 0.0f);
+    if (tid < qn) {
+        const int g = tid / h4, i = tid % h4;
+        qv = reinterpret_cast<const float4 *>(p.q + static_cast<size_t>(kvh * group + g) * 2 * head)[i];
     }
-    if (owns_new && wave == 0) {
-        for (int i = lane; i < head; i += 64) kn[i] = p.k[static_cast<size_t>(kvh) * head + i];
-        __builtin_amdgcn_wave_barrier();
-        norm_rope(kn, head, p.k_norm, p.eps, rope, p.rope_dim, lane);
-        uint16_t *kdst = p.kcache + (static_cast<size_t>(pos) * p.kv_heads + kvh) * head;
-        uint16_t *vdst = p.vcache + (static_cast<size_t>(pos) * p.kv_heads + kvh) * value;
-        for (int i = lane; i < head; i += 64) {
-            const uint16_t bits = float_to_half_kv(kn[i]);
-            kdst[i] = bits;
-            kn[i] = gguf_half_to_real(bits);
+    if (tid < h4) aux = reinterpret_cast<const float4 *>(p.q_norm)[tid];
+    else if (tid >= 64 && tid - 64 < h4) aux = reinterpret_cast<const float4 *>(p.k_norm)[tid - 64];
+    else if (owns_new && tid >= 192 && tid - 192 < h4)
+        aux = reinterpret_cast<const float4 *>(p.k + static_cast<size_t>(kvh) * head)[tid - 192];
+    if (tid >= 128 && tid - 128 < half) rv = p.rope[static_cast<size_t>(pos) * half + (tid - 128)];
+    if (owns_new && tid < v4) vv4 = reinterpret_cast<const float4 *>(p.v + static_cast<size_t>(kvh) * value)[tid];
+    const int flag = p.cache_flags ? p.cache_flags[kvh] : 1;
+    // first K/V tile (rows contiguous, 16 B per load)
+    const int segs_k = head / 8, segs_v = value / 8;
+    constexpr int kLoads = kTile * (kMaxHead / 8) / kThreads;  // 8
+    uint4 kr[kLoads], vr[kLoads];
+    auto fetch_tile = [&](int t0, int n) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int li = tid + i * kThreads;
+            const int jk = li / segs_k, sk = li % segs_k;
+            const int jv = li / segs_v, sv = li % segs_v;
+            if (jk < n)
+                kr[i] = reinterpret_cast<const uint4 *>(
+                    p.kcache + (static_cast<size_t>(t0 + jk) * p.kv_heads + kvh) * head)[sk];
+            if (jv < n)
+                vr[i] = reinterpret_cast<const uint4 *>(
+                    p.vcache + (static_cast<size_t>(t0 + jv) * p.kv_heads + kvh) * value)[sv];
         }
-        for (int i = lane; i < value; i += 64) {
-            const uint16_t bits = float_to_half_kv(p.v[static_cast<size_t>(kvh) * value + i]);
-            vdst[i] = bits;
-            vn[i] = gguf_half_to_real(bits);
+    };
+    auto stash_tile = [&](int n) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int li = tid + i * kThreads;
+            const int jk = li / segs_k, sk = li % segs_k;
+            const int jv = li / segs_v, sv = li % segs_v;
+            if (jk < n) *reinterpret_cast<uint4 *>(&ktile[jk][sk * 8]) = kr[i];
+            if (jv < n) *reinterpret_cast<uint4 *>(&vtile[jv][sv * 8]) = vr[i];
         }
+    };
+    const int n0 = (p1 - p0 < kTile) ? p1 - p0 : kTile;
+    fetch_tile(p0, n0);
+
+    if (tid < qn) reinterpret_cast<float4 *>(qh)[tid] = qv;
+    if (tid < h4) reinterpret_cast<float4 *>(qw)[tid] = aux;
+    else if (tid >= 64 && tid - 64 < h4) reinterpret_cast<float4 *>(kw)[tid - 64] = aux;
+    else if (owns_new && tid >= 192 && tid - 192 < h4) reinterpret_cast<float4 *>(kn)[tid - 192] = aux;
+    if (tid >= 128 && tid - 128 < half) rs[tid - 128] = rv;
+    if (owns_new && tid < v4) reinterpret_cast<float4 *>(vn)[tid] = vv4;
+    if (tid == 0) overflow = 0;
+    __syncthreads();
+
+    // q heads and the new key: normalise + rotate, one wave per slice
+    for (int sl = wave; sl < group + (owns_new ? 1 : 0); sl += kThreads / 64) {
+        if (sl < group) norm_rope(qh + sl * head, head, qw, p.eps, rs, p.rope_dim, lane);
+        else norm_rope(kn, head, kw, p.eps, rs, p.rope_dim, lane);
     }
     __syncthreads();
+    if (owns_new) {
+        // append at pos with the reference's float_to_half (fortai_qwen35_cpu.f90:1594-1601)
+        uint16_t *kdst = p.kcache + (static_cast<size_t>(pos) * p.kv_heads + kvh) * head;
+        uint16_t *vdst = p.vcache + (static_cast<size_t>(pos) * p.kv_heads + kvh) * value;
+        if (tid < head) {
+            const uint16_t bits = float_to_half_kv(kn[tid]);
+            kdst[tid] = bits;
+            kn[tid] = gguf_half_to_real(bits);
+            if ((bits & 0x7c00u) == 0x7c00u) overflow = 1;
+        }
+        if (tid < value) {
+            const uint16_t bits = float_to_half_kv(vn[tid]);
+            vdst[tid] = bits;
+            vn[tid] = gguf_half_to_real(bits);
+            if ((bits & 0x7c00u) == 0x7c00u) overflow = 1;
+        }
+        __syncthreads();
+        if (tid == 0 && overflow && p.cache_flags) p.cache_flags[kvh] = 1;
+    }
+    const bool finite = flag == 0 && overflow == 0;
 
     const float scale_div = sqrtf(static_cast<float>(head));
     float m_run = -__builtin_inff();  // per wave = per q head (wave g handles head g)
@@ -108,40 +206,20 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
 
     for (int t0 = p0; t0 < p1; t0 += kTile) {
         const int n = (p1 - t0 < kTile) ? p1 - t0 : kTile;
-        // stage K and V rows (16 B per thread per step, rows contiguous)
-        const int segs_k = head / 8, segs_v = value / 8;
-        for (int li = tid; li < n * segs_k; li += kThreads) {
-            const int j = li / segs_k, s = li % segs_k;
-            const uint4 *src = reinterpret_cast<const uint4 *>(
-                p.kcache + (static_cast<size_t>(t0 + j) * p.kv_heads + kvh) * head) + s;
-            *reinterpret_cast<uint4 *>(&ktile[j][s * 8]) = *src;
-        }
-        for (int li = tid; li < n * segs_v; li += kThreads) {
-            const int j = li / segs_v, s = li % segs_v;
-            const uint4 *src = reinterpret_cast<const uint4 *>(
-                p.vcache + (static_cast<size_t>(t0 + j) * p.kv_heads + kvh) * value) + s;
-            *reinterpret_cast<uint4 *>(&vtile[j][s * 8]) = *src;
-        }
+        if (t0 != p0) fetch_tile(t0, n);
+        stash_tile(n);
         __syncthreads();
-        // scores: wave g = q head g, lane j = position t0 + j
         if (wave < group) {
             float sc = -__builtin_inff();
             if (lane < n) {
-                const int pj = t0 + lane;
-                float dot = 0.0f;
-                if (pj == pos) {
-                    for (int i = 0; i < head; ++i) dot = __builtin_fmaf(qh[wave][i], kn[i], dot);
+                float dot;
+                if (t0 + lane == pos) {
+                    float d0 = 0.0f;
+                    for (int i = 0; i < head; ++i) d0 = __builtin_fmaf(qh[wave * head + i], kn[i], d0);
+                    dot = d0;
                 } else {
-                    const uint16_t *kr = &ktile[lane][0];
-                    for (int i = 0; i < head; i += 8) {
-                        const uint4 h8 = *reinterpret_cast<const uint4 *>(kr + i);
-                        const uint32_t hw[4] = {h8.x, h8.y, h8.z, h8.w};
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            dot = __builtin_fmaf(qh[wave][i + 2 * q], gguf_half_to_real(static_cast<uint16_t>(hw[q] & 0xffffu)), dot);
-                            dot = __builtin_fmaf(qh[wave][i + 2 * q + 1], gguf_half_to_real(static_cast<uint16_t>(hw[q] >> 16)), dot);
-                        }
-                    }
+                    dot = finite ? tile_score<true>(qh + wave * head, &ktile[lane][0], head)
+                                 : tile_score<false>(qh + wave * head, &ktile[lane][0], head);
                 }
                 sc = dot / scale_div;
             }
@@ -157,12 +235,12 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
         }
         __syncthreads();
         // P.V: thread d owns value dim d for every head of the group
-        for (int g = 0; g < group; ++g) acc[g] *= rescale[g];
+        for (int g = 0; g < kMaxGroup; ++g)
+            if (g < group) acc[g] *= rescale[g];
         if (tid < value) {
-            for (int j = 0; j < n; ++j) {
-                const float vv = (t0 + j == pos) ? vn[tid] : gguf_half_to_real(vtile[j][tid]);
-                for (int g = 0; g < group; ++g) acc[g] = __builtin_fmaf(prob[g][j], vv, acc[g]);
-            }
+            const int new_j = (pos >= t0 && pos < t0 + n) ? pos - t0 : -1;
+            if (finite) tile_pv<true>(acc, prob, vtile, vn, n, new_j, group, tid);
+            else tile_pv<false>(acc, prob, vtile, vn, n, new_j, group, tid);
         }
         __syncthreads();
     }
@@ -176,40 +254,70 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
     }
     if (tid < value)
         for (int g = 0; g < group; ++g) part[g * stride + 2 + tid] = acc[g];
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(p.done + kvh, 1u);
-        last = (prev == static_cast<unsigned>(active) - 1u);
+}
+
+// Merge the chunk partials of one head (log-sum-exp rescale), apply the
+// sigmoid output gate (fortai_qwen35_cpu.f90:1030-1031) and quantize the
+// result for the o_proj matvec.  One 64-thread workgroup per (head, 64 dims).
+__global__ __launch_bounds__(64) void attention_merge_kernel(const AttentionParams p) {
+    __shared__ float vals[64];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int pos = *p.position;
+    if (pos < 0 || pos >= p.max_context) return;
+    const int slices = p.value / 64;
+    const int h = static_cast<int>(blockIdx.x) / slices;
+    const int d = (static_cast<int>(blockIdx.x) % slices) * 64 + tid;
+    const int group = p.heads / p.kv_heads;
+    const int kvh = h / group, g = h % group;
+    const int nchunk = (p.max_context + p.chunk - 1) / p.chunk;
+    const int active = (pos + 1 + p.chunk - 1) / p.chunk;
+    const size_t stride = static_cast<size_t>(p.value) + 2;
+    const float *base = p.partial + (static_cast<size_t>(kvh) * nchunk * group + g) * stride;
+    // chunk maxima and weights once per workgroup, then the weighted sum of
+    // this thread's dimension; loads are batched so their latencies overlap
+    __shared__ float wts[kMaxChunks];
+    __shared__ float lsums[kMaxChunks];
+    const size_t cstride = static_cast<size_t>(group) * stride;
+    float M = -__builtin_inff();
+    for (int c = tid; c < active; c += 64) M = fmaxf(M, base[c * cstride]);
+    for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
+    for (int c = tid; c < active; c += 64) {
+        const float w = expf(base[c * cstride] - M);
+        wts[c] = w;
+        lsums[c] = base[c * cstride + 1] * w;
     }
     __syncthreads();
-    if (!last) return;
-    __threadfence();
-
-    // merge the active chunks of this kv head, then the output gate
-    if (tid < value) {
-        const float *base = p.partial + static_cast<size_t>(kvh) * nchunk * group * stride;
-        for (int g = 0; g < group; ++g) {
-            float M = -__builtin_inff();
-            for (int cc = 0; cc < active; ++cc)
-                M = fmaxf(M, __hip_atomic_load(base + (static_cast<size_t>(cc) * group + g) * stride,
-                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            float lsum = 0.0f, o = 0.0f;
-            for (int cc = 0; cc < active; ++cc) {
-                const float *pc = base + (static_cast<size_t>(cc) * group + g) * stride;
-                const float m = __hip_atomic_load(pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float l = __hip_atomic_load(pc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float a = __hip_atomic_load(pc + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float w = expf(m - M);
-                lsum = __builtin_fmaf(l, w, lsum);
-                o = __builtin_fmaf(a, w, o);
+    float lsum = 0.0f, o = 0.0f;
+    for (int c0 = 0; c0 < active; c0 += 16) {
+        float a[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a[i] = (c0 + i < active) ? base[(c0 + i) * cstride + 2 + d] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (c0 + i < active) {
+                lsum = lsum + lsums[c0 + i];
+                o = __builtin_fmaf(a[i], wts[c0 + i], o);
             }
-            const int h = kvh * group + g;
-            const float gate = p.q[static_cast<size_t>(h) * 2 * head + head + tid];
-            p.out[static_cast<size_t>(h) * value + tid] = (o / lsum) * sigmoid_ref(gate);
         }
     }
-    if (tid == 0) __hip_atomic_store(p.done + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float gate = p.q[static_cast<size_t>(h) * 2 * p.head + p.head + d];
+    const float y = (o / lsum) * sigmoid_ref(gate);
+    if (p.out) p.out[static_cast<size_t>(h) * p.value + d] = y;
+    if (!p.out_q8l) return;
+    vals[tid] = y;
+    __syncthreads();
+    if (tid < 16) {
+        const float4 v4 = make_float4(vals[4 * tid], vals[4 * tid + 1], vals[4 * tid + 2], vals[4 * tid + 3]);
+        float scale;
+        uint16_t bits;
+        const uint32_t packed = quantize_group(v4, scale, bits);
+        const int gi = (h * p.value + d - tid) / 4 + tid;  // 4-value group index in [heads*value]
+        const int b = gi >> 3, ll = gi & 7;
+        const int chunks = (p.heads * p.value / kQ8Block + 3) / 4;
+        uint32_t *dq = static_cast<uint32_t *>(p.out_q8l);
+        dq[((b >> 2) * 8 + ll) * 4 + (b & 3)] = packed;
+        if (ll == 0) reinterpret_cast<float *>(dq + chunks * 32)[b] = scale;
+    }
 }
 
 }  // namespace
@@ -224,10 +332,13 @@ int attention_chunk(int max_context) {
 hipError_t launch_attention(const AttentionParams &p, hipStream_t stream) {
     const int group = p.kv_heads > 0 ? p.heads / p.kv_heads : 0;
     if (group < 1 || group > kMaxGroup || p.heads % p.kv_heads || p.head > kMaxHead || p.value > kThreads ||
-        p.head % 8 || p.value % 8 || p.rope_dim > p.head || p.rope_dim % 2 || p.chunk < 1)
+        p.head % 8 || p.value % 64 || p.rope_dim > p.head || p.rope_dim % 2 || p.chunk < 1)
         return hipErrorInvalidValue;
     const int nchunk = (p.max_context + p.chunk - 1) / p.chunk;
     hipLaunchKernelGGL(attention_kernel, dim3(p.kv_heads * nchunk), dim3(kThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(p.heads * (p.value / 64)), dim3(64), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -10,6 +10,7 @@
 #include "fortai_hip_kernels.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -31,7 +32,8 @@ struct fortai_hip_q8_context {
     size_t scratch_aux_bytes = 0;
     float *argmax_value = nullptr;
     int32_t *argmax_index = nullptr;
-    unsigned int *argmax_done = nullptr;
+    void *scratch_q8l = nullptr;  // quantized FFN hidden of the ABI FFN paths
+    size_t scratch_q8l_bytes = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     char error[256] = {};
@@ -48,6 +50,7 @@ struct fortai_hip_q8_weights {
 struct fortai_hip_f16_weights {
     fortai_hip_q8_context *context = nullptr;
     int rows = 0, width = 0;
+    bool finite = false;  // no exponent-31 halves: the plain conversion is exact
     uint16_t *data = nullptr;
 };
 
@@ -57,10 +60,9 @@ struct fortai_hip_qwen35_recurrent {
     int conv_size = 0, kernel = 0, state_size = 0, key_heads = 0, value_heads = 0, head = 0, inner = 0;
     float eps = 0.0f;
     float *conv_w = nullptr, *ssm_a = nullptr, *ssm_dt = nullptr, *ssm_norm = nullptr;
-    float *conv_ring = nullptr, *state = nullptr;
-    float *qkv_out = nullptr, *z_out = nullptr, *alpha_out = nullptr, *beta_out = nullptr, *o_raw = nullptr;
-    int *step = nullptr;
-    unsigned int *done = nullptr;
+    float *conv_state = nullptr, *state = nullptr;
+    float *qkv_out = nullptr, *z_out = nullptr, *alpha_out = nullptr, *beta_out = nullptr;
+    void *o_q8l = nullptr;  // gated, quantized GDN output (ssm_out input)
 };
 
 struct fortai_hip_qwen35_attention {
@@ -71,8 +73,9 @@ struct fortai_hip_qwen35_attention {
     float *q_norm = nullptr, *k_norm = nullptr;
     float2 *rope = nullptr;
     uint16_t *kcache = nullptr, *vcache = nullptr;
-    float *q_out = nullptr, *k_out = nullptr, *v_out = nullptr, *attn_out = nullptr, *partial = nullptr;
-    unsigned int *done = nullptr;
+    float *q_out = nullptr, *k_out = nullptr, *v_out = nullptr, *partial = nullptr;
+    int *cache_flags = nullptr;  // per kv head: the cache holds an exponent-31 half
+    void *attn_q8l = nullptr;    // gated, quantized attention output (o_proj input)
 };
 
 struct decoder_layer {
@@ -89,12 +92,13 @@ struct fortai_hip_qwen35_decoder {
     float eps = 0.0f;
     const fortai_hip_f16_weights *emb16 = nullptr, *out16 = nullptr;
     const fortai_hip_q8_weights *emb8 = nullptr, *out8 = nullptr;
-    float *output_norm = nullptr, *x = nullptr, *h = nullptr, *logits = nullptr;
+    float *output_norm = nullptr, *x = nullptr, *logits = nullptr;
+    void *h_q8l = nullptr;  // quantized FFN hidden
     float *argmax_value = nullptr;
     int32_t *argmax_index = nullptr;
-    unsigned int *argmax_done = nullptr;
     int64_t *trace = nullptr;
     int next_position = 0;  // host mirror of the device position after the queued steps
+    bool use_graph = true;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
@@ -142,10 +146,20 @@ hipError_t ensure(void **buf, size_t *have, size_t need) {
     return e;
 }
 
-hipError_t ensure_scratch(fortai_hip_q8_context *c, size_t act, size_t out, size_t aux) {
+hipError_t ensure_scratch(fortai_hip_q8_context *c, size_t act, size_t out, size_t q8l) {
     hipError_t e = ensure(reinterpret_cast<void **>(&c->scratch_act), &c->scratch_act_bytes, act);
     if (e == hipSuccess) e = ensure(reinterpret_cast<void **>(&c->scratch_out), &c->scratch_out_bytes, out);
-    if (e == hipSuccess && aux) e = ensure(reinterpret_cast<void **>(&c->scratch_aux), &c->scratch_aux_bytes, aux);
+    if (e == hipSuccess && q8l > c->scratch_q8l_bytes) {
+        e = ensure(&c->scratch_q8l, &c->scratch_q8l_bytes, q8l);
+        if (e == hipSuccess) e = hipMemsetAsync(c->scratch_q8l, 0, q8l, c->stream);  // padding blocks stay zero
+    }
+    return e;
+}
+
+hipError_t alloc_q8l(void **buf, int width, hipStream_t stream) {
+    const size_t bytes = q8l_bytes(width);
+    hipError_t e = hipMalloc(buf, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(*buf, 0, bytes, stream);
     return e;
 }
 
@@ -153,13 +167,21 @@ __global__ void set_position_kernel(int *dst, int value) { *dst = value; }
 __global__ void set_token_kernel(int64_t *dst, int64_t value) { *dst = value; }
 
 MatvecSegment segment(const fortai_hip_q8_weights *w, float *out, const float *resid = nullptr,
-    const fortai_hip_q8_weights *w2 = nullptr) {
+    const fortai_hip_q8_weights *w2 = nullptr, void *out_q8l = nullptr) {
     MatvecSegment s;
     s.w = w->m;
     if (w2) s.w2 = w2->m;
     s.out = out;
     s.resid = resid;
+    s.out_q8l = out_q8l;
     return s;
+}
+
+MatvecInput q8l_input(const void *xq8l, int width) {
+    MatvecInput in;
+    in.xq8l = xq8l;
+    in.width = width;
+    return in;
 }
 
 MatvecInput f32_input(const float *x, int width) {
@@ -178,37 +200,35 @@ MatvecInput q8_input(const int8_t *xq, int width) {
 
 bool owned(const fortai_hip_q8_context *c, const fortai_hip_q8_weights *w) { return w && w->context == c; }
 
-// enqueue the GDN projection -> step -> gated norm + ssm_out chain
+GdnParams gdn_params(fortai_hip_qwen35_recurrent *L, const float *qkv, const float *alpha, const float *beta,
+    float *out, void *out_q8l) {
+    GdnParams p;
+    p.qkv = qkv; p.z = L->z_out; p.alpha = alpha; p.beta = beta; p.ssm_a = L->ssm_a; p.ssm_dt = L->ssm_dt;
+    p.ssm_norm = L->ssm_norm; p.conv_w = L->conv_w; p.conv_state = L->conv_state; p.state = L->state;
+    p.out = out; p.out_q8l = out_q8l; p.conv_size = L->conv_size; p.kernel = L->kernel;
+    p.state_size = L->state_size; p.key_heads = L->key_heads; p.value_heads = L->value_heads; p.head = L->head;
+    p.eps = L->eps;
+    return p;
+}
+
+// enqueue the GDN projections -> fused step (+ gated norm, quantize) -> ssm_out
 hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &in, Prologue pro, float *out,
     const float *resid, hipStream_t stream) {
     const MatvecSegment segs[4] = {segment(L->qkv, L->qkv_out), segment(L->gate, L->z_out),
         segment(L->alpha, L->alpha_out), segment(L->beta, L->beta_out)};
     hipError_t e = launch_q8_matvec(segs, 4, in, pro, Epilogue::STORE, stream);
+    if (e == hipSuccess) e = launch_gdn_step(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, nullptr, L->o_q8l), stream);
     if (e != hipSuccess) return e;
-    GdnParams p;
-    p.qkv = L->qkv_out; p.alpha = L->alpha_out; p.beta = L->beta_out; p.ssm_a = L->ssm_a; p.ssm_dt = L->ssm_dt;
-    p.conv_w = L->conv_w; p.conv_ring = L->conv_ring; p.state = L->state; p.out = L->o_raw;
-    p.step = L->step; p.done = L->done; p.conv_size = L->conv_size; p.kernel = L->kernel;
-    p.state_size = L->state_size; p.key_heads = L->key_heads; p.value_heads = L->value_heads; p.head = L->head;
-    p.eps = L->eps;
-    e = launch_gdn_step(p, stream);
-    if (e != hipSuccess) return e;
-    MatvecInput gin;
-    gin.x = L->o_raw;
-    gin.gate = L->z_out;
-    gin.norm = L->ssm_norm;
-    gin.eps = L->eps;
-    gin.width = L->inner;
-    gin.head = L->head;
     const MatvecSegment oseg = segment(L->out, out, resid);
-    return launch_q8_matvec(&oseg, 1, gin, Prologue::GATED, resid ? Epilogue::ADD : Epilogue::STORE, stream);
+    return launch_q8_matvec(&oseg, 1, q8l_input(L->o_q8l, L->inner), Prologue::Q8L,
+        resid ? Epilogue::ADD : Epilogue::STORE, stream);
 }
 
 AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q, const float *k, const float *v,
     float *out) {
     AttentionParams p;
     p.q = q; p.k = k; p.v = v; p.q_norm = A->q_norm; p.k_norm = A->k_norm; p.rope = A->rope;
-    p.kcache = A->kcache; p.vcache = A->vcache; p.partial = A->partial; p.done = A->done; p.out = out;
+    p.kcache = A->kcache; p.vcache = A->vcache; p.partial = A->partial; p.cache_flags = A->cache_flags; p.out = out;
     p.position = A->context->position; p.heads = A->heads; p.kv_heads = A->kv_heads; p.head = A->head;
     p.value = A->value; p.max_context = A->max_context; p.rope_dim = A->rope_dim; p.chunk = A->chunk;
     p.eps = A->eps;
@@ -220,21 +240,23 @@ hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &
     const MatvecSegment segs[3] = {segment(A->q, A->q_out), segment(A->k, A->k_out), segment(A->v, A->v_out)};
     hipError_t e = launch_q8_matvec(segs, 3, in, pro, Epilogue::STORE, stream);
     if (e != hipSuccess) return e;
-    e = launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream);
+    AttentionParams ap = attention_params(A, A->q_out, A->k_out, A->v_out, nullptr);
+    ap.out_q8l = A->attn_q8l;
+    e = launch_attention(ap, stream);
     if (e != hipSuccess) return e;
     const MatvecSegment oseg = segment(A->o, out, resid);
-    return launch_q8_matvec(&oseg, 1, f32_input(A->attn_out, A->heads * A->value), Prologue::F32,
+    return launch_q8_matvec(&oseg, 1, q8l_input(A->attn_q8l, A->heads * A->value), Prologue::Q8L,
         resid ? Epilogue::ADD : Epilogue::STORE, stream);
 }
 
 hipError_t enqueue_ffn(const fortai_hip_q8_weights *gate, const fortai_hip_q8_weights *up,
-    const fortai_hip_q8_weights *down, const MatvecInput &in, Prologue pro, float *h, float *out,
+    const fortai_hip_q8_weights *down, const MatvecInput &in, Prologue pro, void *h_q8l, float *out,
     const float *resid, hipStream_t stream) {
-    const MatvecSegment pair = segment(gate, h, nullptr, up);
+    const MatvecSegment pair = segment(gate, nullptr, nullptr, up, h_q8l);
     hipError_t e = launch_q8_matvec(&pair, 1, in, pro, Epilogue::SILU_PAIR, stream);
     if (e != hipSuccess) return e;
     const MatvecSegment dseg = segment(down, out, resid);
-    return launch_q8_matvec(&dseg, 1, f32_input(h, gate->m.rows), Prologue::F32,
+    return launch_q8_matvec(&dseg, 1, q8l_input(h_q8l, gate->m.rows), Prologue::Q8L,
         resid ? Epilogue::ADD : Epilogue::STORE, stream);
 }
 
@@ -263,10 +285,8 @@ int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context) {
     if (e == hipSuccess) e = alloc(&c->token, 1);
     if (e == hipSuccess) e = alloc(&c->argmax_value, 1024);
     if (e == hipSuccess) e = alloc(&c->argmax_index, 1024);
-    if (e == hipSuccess) e = alloc(&c->argmax_done, 1);
     if (e == hipSuccess) e = hipMemsetAsync(c->position, 0, sizeof(int), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->token, 0, sizeof(int64_t), c->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(c->argmax_done, 0, sizeof(unsigned), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         fortai_hip_q8_context_destroy(c);
@@ -284,7 +304,8 @@ int fortai_hip_q8_context_destroy(fortai_hip_q8_context *c) {
     if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
     release(c->position); release(c->token); release(c->scratch_act); release(c->scratch_out);
-    release(c->scratch_aux); release(c->argmax_value); release(c->argmax_index); release(c->argmax_done);
+    release(c->scratch_aux); release(c->argmax_value); release(c->argmax_index);
+    if (c->scratch_q8l) (void)hipFree(c->scratch_q8l);
     if (c->start) (void)hipEventDestroy(c->start);
     if (c->stop) (void)hipEventDestroy(c->stop);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -335,6 +356,21 @@ int fortai_hip_q8_context_synchronize(fortai_hip_q8_context *c) {
     if (!c) return FORTAI_HIP_INVALID;
     (void)hipSetDevice(c->device);
     return done(c, hipStreamSynchronize(c->stream), "stream synchronize");
+}
+
+int fortai_hip_q8_context_timer_start(fortai_hip_q8_context *c) {
+    if (!c) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, hipEventRecord(c->start, c->stream), "timer start");
+}
+
+int fortai_hip_q8_context_timer_stop(fortai_hip_q8_context *c, float *ms) {
+    if (!c || !ms) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipEventRecord(c->stop, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, c->start, c->stop);
+    return done(c, e, "timer stop");
 }
 
 // ------------------------------------------------------------------ weights
@@ -399,8 +435,16 @@ int fortai_hip_f16_weights_upload(fortai_hip_q8_context *c, const void *host_wei
     w->width = width;
     (void)hipSetDevice(c->device);
     hipError_t e = alloc(&w->data, static_cast<size_t>(rows) * width);
+    unsigned int *count = nullptr;
+    unsigned int nonfinite = 1;
+    if (e == hipSuccess) e = alloc(&count, 1);
     if (e == hipSuccess) e = hipMemcpyAsync(w->data, host_weights, expected, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(count, 0, sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = launch_count_nonfinite_halves(w->data, static_cast<size_t>(rows) * width, count, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(&nonfinite, count, sizeof(unsigned), hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    release(count);
+    w->finite = nonfinite == 0;
     if (e != hipSuccess) {
         release(w->data);
         delete w;
@@ -492,7 +536,7 @@ int fortai_hip_qwen35_embedding_device(fortai_hip_q8_context *c, const fortai_hi
         output_elements < static_cast<size_t>(w->width))
         return FORTAI_HIP_INVALID;
     (void)hipSetDevice(c->device);
-    return done(c, launch_q8_embedding(w->m, nullptr, nullptr, token_id, static_cast<float *>(device_output), c->stream),
+    return done(c, launch_q8_embedding(w->m, nullptr, token_id, static_cast<float *>(device_output), c->stream),
         "device Q8 embedding");
 }
 
@@ -545,9 +589,8 @@ int fortai_hip_f16_matvec_device(fortai_hip_q8_context *c, const fortai_hip_f16_
     ArgmaxState st;
     st.partial_value = c->argmax_value;
     st.partial_index = c->argmax_index;
-    st.done = c->argmax_done;
     st.token = static_cast<int64_t *>(device_token);
-    return done(c, launch_f16_matvec(w->data, w->rows, w->width, static_cast<const float *>(device_activation),
+    return done(c, launch_f16_matvec(w->data, w->rows, w->width, w->finite, static_cast<const float *>(device_activation),
         nullptr, 0.0f, static_cast<float *>(device_output), device_token ? &st : nullptr, c->stream),
         "device F16 matvec");
 }
@@ -559,7 +602,6 @@ int fortai_hip_argmax_device(fortai_hip_q8_context *c, const void *values, size_
     ArgmaxState st;
     st.partial_value = c->argmax_value;
     st.partial_index = c->argmax_index;
-    st.done = c->argmax_done;
     st.token = static_cast<int64_t *>(device_token);
     return done(c, launch_argmax(static_cast<const float *>(values), static_cast<int>(elements), st, c->stream),
         "device argmax");
@@ -680,11 +722,11 @@ int fortai_hip_q8_ffn_host(fortai_hip_q8_context *c, const fortai_hip_q8_weights
     const size_t o_bytes = static_cast<size_t>(down->m.rows) * sizeof(float);
     if (act_bytes < in_bytes || out_bytes < o_bytes) return FORTAI_HIP_INVALID;
     (void)hipSetDevice(c->device);
-    hipError_t e = ensure_scratch(c, in_bytes, o_bytes, static_cast<size_t>(gate->m.rows) * sizeof(float));
+    hipError_t e = ensure_scratch(c, in_bytes, o_bytes, q8l_bytes(gate->m.rows));
     if (e == hipSuccess) e = hipEventRecord(c->start, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(c->scratch_act, act, in_bytes, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess)
-        e = enqueue_ffn(gate, up, down, q8_input(c->scratch_act, gate->width), Prologue::Q8, c->scratch_aux,
+        e = enqueue_ffn(gate, up, down, q8_input(c->scratch_act, gate->width), Prologue::Q8, c->scratch_q8l,
             c->scratch_out, nullptr, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(out, c->scratch_out, o_bytes, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
@@ -702,10 +744,10 @@ int fortai_hip_q8_ffn_device(fortai_hip_q8_context *c, const fortai_hip_q8_weigh
         out_elements < static_cast<size_t>(down->m.rows))
         return FORTAI_HIP_INVALID;
     (void)hipSetDevice(c->device);
-    hipError_t e = ensure_scratch(c, 0, 0, static_cast<size_t>(gate->m.rows) * sizeof(float));
+    hipError_t e = ensure_scratch(c, 0, 0, q8l_bytes(gate->m.rows));
     if (e == hipSuccess)
         e = enqueue_ffn(gate, up, down, f32_input(static_cast<const float *>(act), gate->width), Prologue::F32,
-            c->scratch_aux, static_cast<float *>(out), nullptr, c->stream);
+            c->scratch_q8l, static_cast<float *>(out), nullptr, c->stream);
     return done(c, e, "Qwen FFN device");
 }
 
@@ -748,16 +790,13 @@ int fortai_hip_qwen35_recurrent_create(fortai_hip_q8_context *c, const fortai_hi
     if (e == hipSuccess) e = upload_f32(&L->ssm_a, ssm_a, value_heads, c->stream);
     if (e == hipSuccess) e = upload_f32(&L->ssm_dt, ssm_dt, value_heads, c->stream);
     if (e == hipSuccess) e = upload_f32(&L->ssm_norm, ssm_norm, head_size, c->stream);
-    if (e == hipSuccess) e = alloc(&L->conv_ring, static_cast<size_t>(conv_kernel) * conv_size);
+    if (e == hipSuccess) e = alloc(&L->conv_state, static_cast<size_t>(conv_kernel - 1) * conv_size);
     if (e == hipSuccess) e = alloc(&L->state, state_n);
     if (e == hipSuccess) e = alloc(&L->qkv_out, conv_size);
     if (e == hipSuccess) e = alloc(&L->z_out, inner_size);
     if (e == hipSuccess) e = alloc(&L->alpha_out, value_heads);
     if (e == hipSuccess) e = alloc(&L->beta_out, value_heads);
-    if (e == hipSuccess) e = alloc(&L->o_raw, inner_size);
-    if (e == hipSuccess) e = alloc(&L->step, 1);
-    if (e == hipSuccess) e = alloc(&L->done, 1);
-    if (e == hipSuccess) e = hipMemsetAsync(L->done, 0, sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = alloc_q8l(&L->o_q8l, inner_size, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         fortai_hip_qwen35_recurrent_destroy(L);
@@ -778,9 +817,9 @@ int fortai_hip_qwen35_recurrent_destroy(fortai_hip_qwen35_recurrent *L) {
         (void)hipSetDevice(L->context->device);
         (void)hipStreamSynchronize(L->context->stream);
     }
-    release(L->conv_w); release(L->ssm_a); release(L->ssm_dt); release(L->ssm_norm); release(L->conv_ring);
+    release(L->conv_w); release(L->ssm_a); release(L->ssm_dt); release(L->ssm_norm); release(L->conv_state);
     release(L->state); release(L->qkv_out); release(L->z_out); release(L->alpha_out); release(L->beta_out);
-    release(L->o_raw); release(L->step); release(L->done);
+    if (L->o_q8l) (void)hipFree(L->o_q8l);
     delete L;
     return FORTAI_HIP_OK;
 }
@@ -790,13 +829,11 @@ int fortai_hip_qwen35_recurrent_reset(fortai_hip_qwen35_recurrent *L) {
     if (!L || !L->context) return FORTAI_HIP_INVALID;
     auto *c = L->context;
     (void)hipSetDevice(c->device);
-    hipError_t e = hipMemsetAsync(L->conv_ring, 0, static_cast<size_t>(L->kernel) * L->conv_size * sizeof(float),
-        c->stream);
+    hipError_t e = hipMemsetAsync(L->conv_state, 0,
+        static_cast<size_t>(L->kernel - 1) * L->conv_size * sizeof(float), c->stream);
     if (e == hipSuccess)
         e = hipMemsetAsync(L->state, 0, static_cast<size_t>(L->value_heads) * L->head * L->head * sizeof(float),
             c->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(L->step, 0, sizeof(int), c->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(L->done, 0, sizeof(unsigned), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     return done(c, e, "Qwen recurrent reset");
 }
@@ -840,62 +877,46 @@ int fortai_hip_qwen35_recurrent_core_device(fortai_hip_qwen35_recurrent *L, cons
     if (!L || !L->context || !qkv || !alpha || !beta || !out) return FORTAI_HIP_INVALID;
     auto *c = L->context;
     (void)hipSetDevice(c->device);
-    GdnParams p;
-    p.qkv = static_cast<const float *>(qkv); p.alpha = static_cast<const float *>(alpha);
-    p.beta = static_cast<const float *>(beta); p.ssm_a = L->ssm_a; p.ssm_dt = L->ssm_dt; p.conv_w = L->conv_w;
-    p.conv_ring = L->conv_ring; p.state = L->state; p.out = static_cast<float *>(out); p.step = L->step;
-    p.done = L->done; p.conv_size = L->conv_size; p.kernel = L->kernel; p.state_size = L->state_size;
-    p.key_heads = L->key_heads; p.value_heads = L->value_heads; p.head = L->head; p.eps = L->eps;
-    return done(c, launch_gdn_step(p, c->stream), "Qwen recurrent core");
+    return done(c, launch_gdn_step(gdn_params(L, static_cast<const float *>(qkv), static_cast<const float *>(alpha),
+        static_cast<const float *>(beta), static_cast<float *>(out), nullptr), c->stream), "Qwen recurrent core");
 }
 
 int fortai_hip_qwen35_recurrent_state_download(fortai_hip_qwen35_recurrent *L, float *gdn, size_t gdn_bytes,
     float *conv, size_t conv_bytes) {
     if (!L || !L->context) return FORTAI_HIP_INVALID;
-    const int H = L->head, K = L->kernel, C = L->conv_size, cols = H / 8;
+    const int H = L->head, cols = H / 8;
     const size_t sn = static_cast<size_t>(L->value_heads) * H * H;
-    if ((gdn && gdn_bytes < sn * 4) || (conv && conv_bytes < static_cast<size_t>(K - 1) * C * 4))
-        return FORTAI_HIP_INVALID;
+    const size_t cn = static_cast<size_t>(L->kernel - 1) * L->conv_size;
+    if ((gdn && gdn_bytes < sn * 4) || (conv && conv_bytes < cn * 4)) return FORTAI_HIP_INVALID;
     auto *c = L->context;
     (void)hipSetDevice(c->device);
-    std::vector<float> st(sn), ring(static_cast<size_t>(K) * C);
-    int t = 0;
+    std::vector<float> st(sn);
     hipError_t e = hipMemcpyAsync(st.data(), L->state, sn * 4, hipMemcpyDeviceToHost, c->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(ring.data(), L->conv_ring, ring.size() * 4, hipMemcpyDeviceToHost, c->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(&t, L->step, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && conv) e = hipMemcpyAsync(conv, L->conv_state, cn * 4, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) return fail(c, FORTAI_HIP_RUNTIME_ERROR, "recurrent state download", e);
     if (gdn)
         for (size_t hr = 0; hr < static_cast<size_t>(L->value_heads) * H; ++hr)
             for (int l = 0; l < 8; ++l)
                 for (int i = 0; i < cols; ++i) gdn[hr * H + 8 * i + l] = st[(hr * 8 + l) * cols + i];
-    if (conv)
-        for (int s = 0; s < K - 1; ++s) {
-            const int slot = ((t - (K - 1) + s) % K + K) % K;
-            std::memcpy(conv + static_cast<size_t>(s) * C, ring.data() + static_cast<size_t>(slot) * C, C * 4);
-        }
     return FORTAI_HIP_OK;
 }
 
 int fortai_hip_qwen35_recurrent_state_upload(fortai_hip_qwen35_recurrent *L, const float *gdn, size_t gdn_bytes,
     const float *conv, size_t conv_bytes) {
     if (!L || !L->context || !gdn || !conv) return FORTAI_HIP_INVALID;
-    const int H = L->head, K = L->kernel, C = L->conv_size, cols = H / 8;
+    const int H = L->head, cols = H / 8;
     const size_t sn = static_cast<size_t>(L->value_heads) * H * H;
-    if (gdn_bytes < sn * 4 || conv_bytes < static_cast<size_t>(K - 1) * C * 4) return FORTAI_HIP_INVALID;
-    std::vector<float> st(sn), ring(static_cast<size_t>(K) * C, 0.0f);
+    const size_t cn = static_cast<size_t>(L->kernel - 1) * L->conv_size;
+    if (gdn_bytes < sn * 4 || conv_bytes < cn * 4) return FORTAI_HIP_INVALID;
+    std::vector<float> st(sn);
     for (size_t hr = 0; hr < static_cast<size_t>(L->value_heads) * H; ++hr)
         for (int l = 0; l < 8; ++l)
             for (int i = 0; i < cols; ++i) st[(hr * 8 + l) * cols + i] = gdn[hr * H + 8 * i + l];
-    for (int s = 0; s < K - 1; ++s) {  // step counter restarts at 0
-        const int slot = ((0 - (K - 1) + s) % K + K) % K;
-        std::memcpy(ring.data() + static_cast<size_t>(slot) * C, conv + static_cast<size_t>(s) * C, C * 4);
-    }
     auto *c = L->context;
     (void)hipSetDevice(c->device);
     hipError_t e = hipMemcpyAsync(L->state, st.data(), sn * 4, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(L->conv_ring, ring.data(), ring.size() * 4, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(L->step, 0, sizeof(int), c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(L->conv_state, conv, cn * 4, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     return done(c, e, "recurrent state upload");
 }
@@ -920,7 +941,7 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
         q->width != v->width)
         return FORTAI_HIP_INVALID;
     // this backend's attention kernel: GQA groups of <= 4, head <= 256, value <= 256
-    if (heads / kv_heads > 4 || head_size > 256 || value_size > 256 || head_size % 8 || value_size % 8)
+    if (heads / kv_heads > 4 || head_size > 256 || value_size > 256 || head_size % 8 || value_size % 64)
         return FORTAI_HIP_INVALID;
     *layer = nullptr;
     auto *A = new (std::nothrow) fortai_hip_qwen35_attention;
@@ -950,9 +971,9 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
     if (e == hipSuccess) e = alloc(&A->q_out, static_cast<size_t>(heads) * 2 * head_size);
     if (e == hipSuccess) e = alloc(&A->k_out, static_cast<size_t>(kv_heads) * head_size);
     if (e == hipSuccess) e = alloc(&A->v_out, static_cast<size_t>(kv_heads) * value_size);
-    if (e == hipSuccess) e = alloc(&A->attn_out, static_cast<size_t>(heads) * value_size);
+    if (e == hipSuccess) e = alloc_q8l(&A->attn_q8l, heads * value_size, c->stream);
     if (e == hipSuccess) e = alloc(&A->partial, static_cast<size_t>(kv_heads) * nchunk * group * (value_size + 2));
-    if (e == hipSuccess) e = alloc(&A->done, kv_heads);
+    if (e == hipSuccess) e = alloc(&A->cache_flags, kv_heads);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         fortai_hip_qwen35_attention_destroy(A);
@@ -974,8 +995,8 @@ int fortai_hip_qwen35_attention_destroy(fortai_hip_qwen35_attention *A) {
         (void)hipStreamSynchronize(A->context->stream);
     }
     release(A->q_norm); release(A->k_norm); release(A->rope); release(A->kcache); release(A->vcache);
-    release(A->q_out); release(A->k_out); release(A->v_out); release(A->attn_out); release(A->partial);
-    release(A->done);
+    release(A->q_out); release(A->k_out); release(A->v_out); release(A->partial); release(A->cache_flags);
+    if (A->attn_q8l) (void)hipFree(A->attn_q8l);
     delete A;
     return FORTAI_HIP_OK;
 }
@@ -988,7 +1009,7 @@ int fortai_hip_qwen35_attention_reset(fortai_hip_qwen35_attention *A) {
     const size_t kv_n = static_cast<size_t>(A->max_context) * A->kv_heads;
     hipError_t e = hipMemsetAsync(A->kcache, 0, kv_n * A->head * 2, c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(A->vcache, 0, kv_n * A->value * 2, c->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(A->done, 0, static_cast<size_t>(A->kv_heads) * sizeof(unsigned), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(A->cache_flags, 0, static_cast<size_t>(A->kv_heads) * sizeof(int), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     return done(c, e, "Qwen attention reset");
 }
@@ -1035,8 +1056,16 @@ int fortai_hip_qwen35_attention_cache_upload(fortai_hip_qwen35_attention *A, con
     auto *c = A->context;
     (void)hipSetDevice(c->device);
     const size_t n = static_cast<size_t>(positions) * A->kv_heads;
+    // exponent-31 halves force the exact gguf_fp16_to_real decode path
+    std::vector<int> flags(static_cast<size_t>(A->kv_heads), 0);
+    for (size_t i = 0; i < n * A->head; ++i)
+        if ((keys[i] & 0x7c00u) == 0x7c00u) flags[(i / A->head) % A->kv_heads] = 1;
+    for (size_t i = 0; i < n * A->value; ++i)
+        if ((values[i] & 0x7c00u) == 0x7c00u) flags[(i / A->value) % A->kv_heads] = 1;
     hipError_t e = hipMemcpyAsync(A->kcache, keys, n * A->head * 2, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(A->vcache, values, n * A->value * 2, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(A->cache_flags, flags.data(), flags.size() * sizeof(int), hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     return done(c, e, "attention cache upload");
 }
@@ -1051,7 +1080,7 @@ namespace {
 hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     auto *c = d->context;
     hipError_t e = d->emb16 ? launch_f16_embedding(d->emb16->data, d->hidden, c->token, 0, d->x, stream)
-                            : launch_q8_embedding(d->emb8->m, nullptr, c->token, 0, d->x, stream);
+                            : launch_q8_embedding(d->emb8->m, c->token, 0, d->x, stream);
     for (size_t i = 0; i < d->layers.size() && e == hipSuccess; ++i) {
         const decoder_layer &L = d->layers[i];
         MatvecInput in;
@@ -1063,20 +1092,19 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
         else e = enqueue_attention(L.attention, in, Prologue::RMSNORM, d->x, d->x, stream);
         if (e != hipSuccess) break;
         in.norm = L.post_norm;
-        e = enqueue_ffn(L.gate, L.up, L.down, in, Prologue::RMSNORM, d->h, d->x, d->x, stream);
+        e = enqueue_ffn(L.gate, L.up, L.down, in, Prologue::RMSNORM, d->h_q8l, d->x, d->x, stream);
     }
     if (e != hipSuccess) return e;
     ArgmaxState st;
     st.partial_value = d->argmax_value;
     st.partial_index = d->argmax_index;
-    st.done = d->argmax_done;
     st.token = c->token;
     st.trace = d->trace;
     st.trace_capacity = d->max_context;
     st.position = c->position;
     if (d->out16)
-        return launch_f16_matvec(d->out16->data, d->vocab, d->hidden, d->x, d->output_norm, d->eps, d->logits, &st,
-            stream);
+        return launch_f16_matvec(d->out16->data, d->vocab, d->hidden, d->out16->finite, d->x, d->output_norm, d->eps,
+            d->logits, &st, stream);
     MatvecInput in;
     in.x = d->x;
     in.norm = d->output_norm;
@@ -1086,6 +1114,9 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
     e = launch_q8_matvec(&s, 1, in, Prologue::RMSNORM, Epilogue::STORE, stream);
     if (e == hipSuccess) e = launch_argmax(d->logits, d->vocab, st, stream);
     return e;
+}
+hipError_t run_step(fortai_hip_qwen35_decoder *d) {
+    return d->use_graph ? hipGraphLaunch(d->exec, d->context->stream) : enqueue_decoder_step(d, d->context->stream);
 }
 }  // namespace
 
@@ -1139,23 +1170,24 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     }
     if (e == hipSuccess) e = upload_f32(&d->output_norm, output_norm, hidden, c->stream);
     if (e == hipSuccess) e = alloc(&d->x, hidden);
-    if (e == hipSuccess) e = alloc(&d->h, ffn);
+    if (e == hipSuccess) e = alloc_q8l(&d->h_q8l, ffn, c->stream);
     if (e == hipSuccess) e = alloc(&d->logits, vocab);
     if (e == hipSuccess) e = alloc(&d->argmax_value, parts);
     if (e == hipSuccess) e = alloc(&d->argmax_index, parts);
-    if (e == hipSuccess) e = alloc(&d->argmax_done, 1);
     if (e == hipSuccess) e = alloc(&d->trace, max_context + 1);
-    if (e == hipSuccess) e = hipMemsetAsync(d->argmax_done, 0, sizeof(unsigned), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(d->trace, 0, (max_context + 1) * sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    // capture one decode step as a graph
-    if (e == hipSuccess) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
-    if (e == hipSuccess) {
+    // capture one decode step as a graph (FORTAI_HIP_DECODER_GRAPH=0 enqueues
+    // the kernels directly every step instead, e.g. for kernel tracing)
+    const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
+    d->use_graph = !(graph_env && std::strcmp(graph_env, "0") == 0);
+    if (e == hipSuccess && d->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess && d->use_graph) {
         const hipError_t ce = enqueue_decoder_step(d, c->stream);
         e = hipStreamEndCapture(c->stream, &d->graph);
         if (ce != hipSuccess) e = ce;
     }
-    if (e == hipSuccess) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
+    if (e == hipSuccess && d->use_graph) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         fortai_hip_qwen35_decoder_destroy(d);
         return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen decoder create", e);
@@ -1175,8 +1207,9 @@ int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *d) {
         release(L.attn_norm);
         release(L.post_norm);
     }
-    release(d->output_norm); release(d->x); release(d->h); release(d->logits); release(d->argmax_value);
-    release(d->argmax_index); release(d->argmax_done); release(d->trace);
+    release(d->output_norm); release(d->x); release(d->logits); release(d->argmax_value);
+    release(d->argmax_index); release(d->trace);
+    if (d->h_q8l) (void)hipFree(d->h_q8l);
     delete d;
     return FORTAI_HIP_OK;
 }
@@ -1207,7 +1240,7 @@ int fortai_hip_qwen35_decoder_forward(fortai_hip_qwen35_decoder *d, int64_t toke
     hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, c->token, token);
     hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = hipGraphLaunch(d->exec, c->stream);
+    if (e == hipSuccess) e = run_step(d);
     d->next_position = position + 1;
     if (e == hipSuccess && logits)
         e = hipMemcpyAsync(logits, d->logits, static_cast<size_t>(d->vocab) * 4, hipMemcpyDeviceToHost, c->stream);
@@ -1227,7 +1260,7 @@ int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *d, int64_t tok
     hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, c->token, token);
     hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
     hipError_t e = hipGetLastError();
-    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(d->exec, c->stream);
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = run_step(d);
     d->next_position = position + steps;
     if (e == hipSuccess)
         e = hipMemcpyAsync(trace, d->trace + position, static_cast<size_t>(steps) * sizeof(int64_t),
@@ -1241,7 +1274,7 @@ int fortai_hip_qwen35_decoder_replay(fortai_hip_qwen35_decoder *d, int steps) {
     auto *c = d->context;
     (void)hipSetDevice(c->device);
     hipError_t e = hipSuccess;
-    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(d->exec, c->stream);
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = run_step(d);
     d->next_position += steps;
     return done(c, e, "decoder replay");
 }

@@ -153,4 +153,33 @@ __device__ __forceinline__ float row_hsum8(float v) {
     return v;
 }
 
+// ------------------------------------------------------- quantization ----
+
+__device__ __forceinline__ int8_t sat8_rne(float v) {
+    const float r = rintf(v);
+    // cvtps_epi32 gives INT32_MIN for NaN/out of range, which packs to -128
+    if (!(r >= -2147483648.0f && r < 2147483648.0f)) return -128;
+    return static_cast<int8_t>(r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r));
+}
+
+
+// Quantize one 4-value group of a 32-value block held by 8 consecutive lanes
+// (lane l of the block holds values 4l..4l+3).  Returns the packed int8x4 and
+// the block's fp32 scale (f32 of the fp16 RNE scale).
+__device__ __forceinline__ uint32_t quantize_group(float4 y, float &scale_out, uint16_t &scale_bits) {
+    float amax = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const float scale = amax / 127.0f;
+    const float inverse = amax != 0.0f ? 127.0f / amax : 0.0f;
+    scale_bits = float_to_half_rne(scale);
+    scale_out = half_bits_to_float(scale_bits);
+    const uint32_t q0 = static_cast<uint8_t>(sat8_rne(y.x * inverse));
+    const uint32_t q1 = static_cast<uint8_t>(sat8_rne(y.y * inverse));
+    const uint32_t q2 = static_cast<uint8_t>(sat8_rne(y.z * inverse));
+    const uint32_t q3 = static_cast<uint8_t>(sat8_rne(y.w * inverse));
+    return q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
+}
+
 }  // namespace fortai_hip

@@ -1,6 +1,11 @@
 // Host-side launchers of the gfx950 kernels (defined in the *.hip files next
 // to this header).  Every launcher enqueues on the given stream and returns
 // hipGetLastError() of the launch.
+//
+// Cross-workgroup results are handed over only at kernel boundaries: a
+// device-scope fence inside a kernel costs an L2 writeback per workgroup on
+// this part, so every split reduction (attention chunks, argmax partials) is
+// finished by a small follow-up kernel instead.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -19,36 +24,48 @@ struct Q8Matrix {
     int row_groups = 0;             // ceil(rows / 8)
 };
 
+// "Q8L": a quantized activation in the lane layout the matvec consumes, so a
+// consumer copies it to LDS with plain 16-byte loads:
+//   u32[(c * 8 + l) * 4 + j] = int8 x4 of lane l (values 4l..4l+3) of block 4c+j
+//   f32[chunks * 32 + b]     = fp32 scale of block b (fp16-rounded, as the
+//                              reference quantizer stores it)
+// Blocks past the width (up to a multiple of 4) hold zeros.
+__host__ __device__ inline size_t q8l_bytes(int width) {
+    const int chunks = (width / 32 + 3) / 4;
+    return static_cast<size_t>(chunks) * 144;
+}
+
 // How the activation reaches the workgroup before the row dots.
 enum class Prologue : int {
-    Q8 = 0,       // already quantized: GGUF Q8_0 blocks in device memory
+    Q8 = 0,       // GGUF Q8_0 blocks in device memory (host-quantized input)
     F32 = 1,      // f32 vector, quantized in-workgroup (fortai_q8_quantize)
     RMSNORM = 2,  // f32 x -> rms_norm(x, w) -> quantize
-    GATED = 3,    // GDN output: o/rms(o)*ssm_norm*silu(z) per head -> quantize
+    Q8L = 3,      // producer-quantized activation in the Q8L layout
 };
 
 // What happens to each row result.
 enum class Epilogue : int {
     STORE = 0,      // out[row] = dot
     ADD = 1,        // out[row] = dot + resid[row]   (in place allowed)
-    SILU_PAIR = 2,  // out[row] = silu(dot(w)) * dot(w2)  (fortai_silu_product)
+    SILU_PAIR = 2,  // h[row] = silu(dot(w)) * dot(w2)  (fortai_silu_product);
+                    // f32 to out (optional) and Q8L to out_q8l (optional)
 };
 
 struct MatvecSegment {
     Q8Matrix w;
-    Q8Matrix w2;          // second matrix of a SILU_PAIR, same shape as w
+    Q8Matrix w2;             // second matrix of a SILU_PAIR, same shape as w
     float *out = nullptr;
     const float *resid = nullptr;
+    void *out_q8l = nullptr; // SILU_PAIR: quantized h for the next matvec
 };
 
 struct MatvecInput {
-    const float *x = nullptr;     // F32 / RMSNORM: [width]; GATED: o [width]
+    const float *x = nullptr;     // F32 / RMSNORM: [width]
     const int8_t *xq = nullptr;   // Q8: GGUF blocks [blocks][34]
-    const float *norm = nullptr;  // RMSNORM: weights [width]; GATED: ssm_norm [head]
-    const float *gate = nullptr;  // GATED: z [width] (before SiLU)
+    const void *xq8l = nullptr;   // Q8L
+    const float *norm = nullptr;  // RMSNORM: weights [width]
     float eps = 0.0f;
     int width = 0;                // activation elements (multiple of 32)
-    int head = 0;                 // GATED: values per head
 };
 
 // Evaluate up to four matrices that share one activation in one launch.
@@ -67,8 +84,8 @@ hipError_t launch_q8_block_dots(const Q8Matrix &w, const int8_t *xq34, int32_t *
     hipStream_t stream);
 
 // Small elementwise / norm kernels of the reference ABI.
-hipError_t launch_q8_embedding(const Q8Matrix &w, const uint8_t *unused, const int64_t *token,
-    int64_t token_value, float *out, hipStream_t stream);
+hipError_t launch_q8_embedding(const Q8Matrix &w, const int64_t *token, int64_t token_value, float *out,
+    hipStream_t stream);
 hipError_t launch_f16_embedding(const uint16_t *table, int width, const int64_t *token,
     int64_t token_value, float *out, hipStream_t stream);
 hipError_t launch_add(const float *a, const float *b, float *out, int n, hipStream_t stream);
@@ -76,35 +93,39 @@ hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, fl
     hipStream_t stream);
 
 // fp16 matrix x f32 vector with the reference's sequential fp32 dot per row
-// (fortai_gguf_runtime.f90:382-386), optional RMSNorm prologue and a fused
-// first-index argmax whose final reduction is done by the last workgroup.
+// (fortai_gguf_runtime.f90:382-386), optional RMSNorm prologue, and per
+// workgroup first-maximum partials finished by launch_argmax_finish.
 struct ArgmaxState {
     float *partial_value = nullptr;   // [max workgroups]
     int32_t *partial_index = nullptr; // [max workgroups]
-    unsigned int *done = nullptr;     // zero between launches (the last WG resets it)
     int64_t *token = nullptr;         // argmax result (0-based row)
     int64_t *trace = nullptr;         // optional: trace[*position] = token
     int *position = nullptr;          // optional: advanced by one after the trace write
     int trace_capacity = 0;           // entries of trace
 };
-hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, const float *x,
+hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite_halves, const float *x,
     const float *norm, float eps, float *out, const ArgmaxState *argmax, hipStream_t stream);
 int f16_matvec_workgroups(int rows);
 hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, hipStream_t stream);
+// reduce `partials` argmax partials and publish token / trace / position
+hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream);
+// scan an fp16 table for exponent-31 patterns (inf/NaN), counted into *count
+hipError_t launch_count_nonfinite_halves(const uint16_t *w, size_t n, unsigned int *count, hipStream_t stream);
 
 // ---- Gated DeltaNet ------------------------------------------------------
 struct GdnParams {
     const float *qkv = nullptr;       // [conv_size] projection output (pre-conv)
+    const float *z = nullptr;         // [value_heads * head] gate projection (pre-SiLU)
     const float *alpha = nullptr;     // [value_heads]
     const float *beta = nullptr;      // [value_heads]
     const float *ssm_a = nullptr;     // [value_heads]
     const float *ssm_dt = nullptr;    // [value_heads]
+    const float *ssm_norm = nullptr;  // [head]
     const float *conv_w = nullptr;    // [conv_size][kernel]
-    float *conv_ring = nullptr;       // [kernel][conv_size]: x_t lives in slot t % kernel
+    float *conv_state = nullptr;      // [kernel-1][conv_size], oldest first (reference layout)
     float *state = nullptr;           // [value_heads][head][8 lanes][head/8] (lane-major rows)
-    float *out = nullptr;             // [value_heads * head] raw o (before the gated norm)
-    int *step = nullptr;              // device step counter t of this layer
-    unsigned int *done = nullptr;     // workgroup completion counter (self-resetting)
+    float *out = nullptr;             // optional [value_heads * head] raw o (before the gated norm)
+    void *out_q8l = nullptr;          // optional Q8L of the gated output (ssm_out input)
     int conv_size = 0, kernel = 0, state_size = 0, key_heads = 0, value_heads = 0, head = 0;
     float eps = 0.0f;
 };
@@ -121,8 +142,9 @@ struct AttentionParams {
     uint16_t *kcache = nullptr;     // [max_context][kv_heads][head] fp16 bits
     uint16_t *vcache = nullptr;     // [max_context][kv_heads][value] fp16 bits
     float *partial = nullptr;       // [kv_heads][chunks][group][value + 2]
-    unsigned int *done = nullptr;   // [kv_heads] self-resetting counters
-    float *out = nullptr;           // [heads][value]
+    int *cache_flags = nullptr;     // [kv_heads]: 1 once the cache holds an exponent-31 half
+    float *out = nullptr;           // optional [heads][value] gated output
+    void *out_q8l = nullptr;        // optional Q8L of the gated output (o_proj input)
     const int *position = nullptr;  // device position (the new token's index)
     int heads = 0, kv_heads = 0, head = 0, value = 0, max_context = 0, rope_dim = 0;
     int chunk = 0;                  // positions per workgroup

@@ -11,10 +11,11 @@
 // registers while the current one is consumed.
 //
 // The greedy step (maxloc, first maximum; app/fortai_cpu_run.f90:58) is
-// fused: every workgroup reduces its 256 rows to (value, first index), and
-// the last workgroup to finish (device-scope counter) reduces the partials,
-// writes the token, appends it to the trace and advances the device
-// position, so a captured graph can replay decode steps back to back.
+// fused: every workgroup reduces its 256 rows to (value, first index) and a
+// one-workgroup follow-up kernel reduces the partials, writes the token,
+// appends it to the trace and advances the device position, so a captured
+// graph can replay decode steps back to back.  Tables without exponent-31
+// halves (checked once at upload) use the plain hardware conversion.
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
 
@@ -48,28 +49,17 @@ __device__ __forceinline__ void block_argmax(float &v, int &i, float *sv, int *s
     }
 }
 
-// The last workgroup reduces all partials and publishes the greedy token.
-__device__ void finish_argmax(const ArgmaxState &st, float v, int i, float *sv, int *si) {
-    __shared__ bool last;
+// Reduce the per-workgroup (value, first index) partials and publish the
+// greedy token; the trace append and the position advance let a captured
+// graph replay decode steps back to back.
+__global__ __launch_bounds__(256) void argmax_finish_kernel(int partials, ArgmaxState st) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
     const int tid = static_cast<int>(threadIdx.x);
-    if (tid == 0) {
-        __hip_atomic_store(st.partial_value + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(st.partial_index + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence();
-        const unsigned prev = atomicAdd(st.done, 1u);
-        last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
-    for (int w = tid; w < static_cast<int>(gridDim.x); w += static_cast<int>(blockDim.x)) {
-        const float pv = __hip_atomic_load(st.partial_value + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int pi = __hip_atomic_load(st.partial_index + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (better(pv, pi, bv, bi)) { bv = pv; bi = pi; }
-    }
-    __syncthreads();
+    for (int w = tid; w < partials; w += 256)
+        if (better(st.partial_value[w], st.partial_index[w], bv, bi)) { bv = st.partial_value[w]; bi = st.partial_index[w]; }
     block_argmax(bv, bi, sv, si);
     if (tid == 0) {
         const int64_t token = bi;
@@ -79,11 +69,10 @@ __device__ void finish_argmax(const ArgmaxState &st, float v, int i, float *sv, 
             if (st.trace && p >= 0 && p < st.trace_capacity) st.trace[p] = token;
             *st.position = p + 1;
         }
-        __hip_atomic_store(st.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-template <bool RMS, bool ARGMAX>
+template <bool RMS, bool ARGMAX, bool FINITE>
 __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__restrict__ w, int rows, int width,
     const float *__restrict__ x, const float *__restrict__ norm, float eps, float *__restrict__ out,
     ArgmaxState st) {
@@ -150,8 +139,10 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
             const uint32_t hw[4] = {h8.x, h8.y, h8.z, h8.w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float a = gguf_half_to_real(static_cast<uint16_t>(hw[q] & 0xffffu));
-                const float b = gguf_half_to_real(static_cast<uint16_t>(hw[q] >> 16));
+                const float a = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[q] & 0xffffu))
+                                       : gguf_half_to_real(static_cast<uint16_t>(hw[q] & 0xffffu));
+                const float b = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[q] >> 16))
+                                       : gguf_half_to_real(static_cast<uint16_t>(hw[q] >> 16));
                 const int k = k0 + s * 8 + q * 2;
                 acc = acc + a * xs[k];
                 acc = acc + b * xs[k + 1];
@@ -164,7 +155,10 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
         float v = row < rows ? acc : -__builtin_inff();
         int i = row < rows ? row : 0x7fffffff;
         block_argmax(v, i, sv, si);
-        finish_argmax(st, v, i, sv, si);
+        if (tid == 0) {
+            st.partial_value[blockIdx.x] = v;
+            st.partial_index[blockIdx.x] = i;
+        }
     }
 }
 
@@ -177,33 +171,63 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *values, int n,
          k += static_cast<int>(gridDim.x * blockDim.x))
         if (better(values[k], k, v, i)) { v = values[k]; i = k; }
     block_argmax(v, i, sv, si);
-    finish_argmax(st, v, i, sv, si);
+    if (threadIdx.x == 0) {
+        st.partial_value[blockIdx.x] = v;
+        st.partial_index[blockIdx.x] = i;
+    }
+}
+
+__global__ void count_nonfinite_halves_kernel(const uint16_t *w, size_t n, unsigned int *count) {
+    unsigned int local = 0;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        local += (w[i] & 0x7c00u) == 0x7c00u;
+    if (local) atomicAdd(count, local);
 }
 
 }  // namespace
 
 int f16_matvec_workgroups(int rows) { return (rows + kRows - 1) / kRows; }
 
-hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, const float *x, const float *norm, float eps,
-    float *out, const ArgmaxState *argmax, hipStream_t stream) {
+hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite, const float *x, const float *norm,
+    float eps, float *out, const ArgmaxState *argmax, hipStream_t stream) {
     if (rows <= 0 || width <= 0 || width % kTileK) return hipErrorInvalidValue;
     const int grid = f16_matvec_workgroups(rows);
     const size_t lds = static_cast<size_t>(kRows) * kPitch * 2 + static_cast<size_t>(width) * 4;
     ArgmaxState st = argmax ? *argmax : ArgmaxState{};
-    if (norm) {
-        if (argmax) hipLaunchKernelGGL((f16_matvec_kernel<true, true>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
-        else hipLaunchKernelGGL((f16_matvec_kernel<true, false>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
-    } else {
-        if (argmax) hipLaunchKernelGGL((f16_matvec_kernel<false, true>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
-        else hipLaunchKernelGGL((f16_matvec_kernel<false, false>), dim3(grid), dim3(kRows), lds, stream, w, rows, width, x, norm, eps, out, st);
-    }
-    return hipGetLastError();
+#define FORTAI_LM(R, A, F) hipLaunchKernelGGL((f16_matvec_kernel<R, A, F>), dim3(grid), dim3(kRows), lds, stream, \
+        w, rows, width, x, norm, eps, out, st)
+    const bool rms = norm != nullptr, am = argmax != nullptr;
+    if (rms && am && finite) FORTAI_LM(true, true, true);
+    else if (rms && am) FORTAI_LM(true, true, false);
+    else if (rms && finite) FORTAI_LM(true, false, true);
+    else if (rms) FORTAI_LM(true, false, false);
+    else if (am && finite) FORTAI_LM(false, true, true);
+    else if (am) FORTAI_LM(false, true, false);
+    else if (finite) FORTAI_LM(false, false, true);
+    else FORTAI_LM(false, false, false);
+#undef FORTAI_LM
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !argmax) return e;
+    return launch_argmax_finish(grid, st, stream);
 }
 
 hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, hipStream_t stream) {
     int grid = (n + 255) / 256;
     if (grid > 1024) grid = 1024;
     hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, stream, values, n, state);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_argmax_finish(grid, state, stream);
+}
+
+hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, stream, partials, state);
+    return hipGetLastError();
+}
+
+hipError_t launch_count_nonfinite_halves(const uint16_t *w, size_t n, unsigned int *count, hipStream_t stream) {
+    hipLaunchKernelGGL(count_nonfinite_halves_kernel, dim3(1024), dim3(256), 0, stream, w, n, count);
     return hipGetLastError();
 }
 

@@ -17,10 +17,13 @@
 // (8 full 128-byte lines) and 64 contiguous bytes of scales, and every lane
 // receives exactly the operands of its own fp32 accumulator.
 //
-// The activation is quantized inside every workgroup (fortai_q8_quantize,
-// fortai_q8_dot.c:153-198) from the producer's fp32 vector, optionally after
-// the RMSNorm of fortai_qwen35_cpu.f90:1408-1432 or the gated norm of
-// :907-915, and kept in LDS as [chunk][lane][4 blocks] 4-byte groups.
+// Latency structure: a wave first issues every weight load of its 8 rows
+// (the whole row slice, up to 32 chunks, held in VGPRs), then builds the
+// quantized activation in LDS while those loads are in flight.  The
+// activation comes from the producer already quantized (Q8L layout, a
+// 16-byte copy), or is quantized in-workgroup from fp32 (fortai_q8_quantize,
+// fortai_q8_dot.c:153-198), optionally after the RMSNorm of
+// fortai_qwen35_cpu.f90:1408-1432.
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
 
@@ -32,7 +35,7 @@ struct MatvecArgs {
     MatvecSegment seg[4];
     int first_wg[5];
     int count;
-    int chunks;  // activation chunks (ceil(blocks / 4))
+    int chunks;            // activation chunks (ceil(blocks / 4))
     int pair_vector_rows;  // SILU_PAIR: rows below this use the vector SiLU lane
     MatvecInput in;
 };
@@ -43,129 +46,135 @@ __device__ __forceinline__ uint32_t load_u32_unaligned(const int8_t *p) {
         (static_cast<uint32_t>(b[2]) << 16) | (static_cast<uint32_t>(b[3]) << 24);
 }
 
-__device__ __forceinline__ int8_t sat8_rne(float v) {
-    const float r = rintf(v);
-    // cvtps_epi32 gives INT32_MIN for NaN/out of range, which packs to -128
-    if (!(r >= -2147483648.0f && r < 2147483648.0f)) return -128;
-    return static_cast<int8_t>(r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r));
-}
-
-// Quantize one 4-value group of a 32-value block held by 8 consecutive
-// lanes (lane l of the block holds values 4l..4l+3).  Returns the packed
-// int8x4 and the block's fp32 scale (f32 of the fp16 RNE scale).
-__device__ __forceinline__ uint32_t quantize_group(float4 y, float &scale_out, uint16_t &scale_bits) {
-    float amax = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    const float scale = amax / 127.0f;
-    const float inverse = amax != 0.0f ? 127.0f / amax : 0.0f;
-    scale_bits = float_to_half_rne(scale);
-    scale_out = half_bits_to_float(scale_bits);
-    const uint32_t q0 = static_cast<uint8_t>(sat8_rne(y.x * inverse));
-    const uint32_t q1 = static_cast<uint8_t>(sat8_rne(y.y * inverse));
-    const uint32_t q2 = static_cast<uint8_t>(sat8_rne(y.z * inverse));
-    const uint32_t q3 = static_cast<uint8_t>(sat8_rne(y.w * inverse));
-    return q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
-}
-
-// Build the workgroup's LDS copy of the quantized activation.
-//   act32[(c * 8 + l) * 4 + j] = int8x4 of lane l of block 4c+j
-//   act_s[b] = fp32 activation scale of block b
+// Build the workgroup's LDS copy of the quantized activation (Q8L layout).
 template <int THREADS, Prologue PRO>
 __device__ __forceinline__ void build_activation(const MatvecInput &in, int chunks, uint32_t *act32,
     float *act_s, double *red) {
     const int tid = static_cast<int>(threadIdx.x);
     const int groups = in.width / 4;
     const int blocks = in.width / kQ8Block;
-    for (int b = blocks + tid; b < chunks * 4; b += THREADS) {
-        act_s[b] = 0.0f;
-        for (int l = 0; l < kLanesPerRow; ++l) act32[((b >> 2) * 8 + l) * 4 + (b & 3)] = 0u;
-    }
-    if constexpr (PRO == Prologue::Q8) {
-        for (int g = tid; g < groups; g += THREADS) {
-            const int b = g >> 3, l = g & 7;
-            const int8_t *block = in.xq + static_cast<size_t>(b) * kQ8Bytes;
-            act32[((b >> 2) * 8 + l) * 4 + (b & 3)] = load_u32_unaligned(block + 2 + 4 * l);
-            if (l == 0) {
-                const uint8_t *sb = reinterpret_cast<const uint8_t *>(block);
-                act_s[b] = half_bits_to_float(static_cast<uint16_t>(sb[0] | (sb[1] << 8)));
-            }
-        }
+    if constexpr (PRO == Prologue::Q8L) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(in.xq8l);
+        uint4 *dst = reinterpret_cast<uint4 *>(act32);
+        for (int i = tid; i < chunks * 9; i += THREADS) dst[i] = src[i];
         __syncthreads();
         return;
     } else {
-        const float4 *x4 = reinterpret_cast<const float4 *>(in.x);
-        float inverse_rms = 1.0f;
-        if constexpr (PRO == Prologue::RMSNORM) {
-            double ss = 0.0;
-            for (int g = tid; g < groups; g += THREADS) {
-                const float4 v = x4[g];
-                ss += static_cast<double>(v.x) * static_cast<double>(v.x);
-                ss += static_cast<double>(v.y) * static_cast<double>(v.y);
-                ss += static_cast<double>(v.z) * static_cast<double>(v.z);
-                ss += static_cast<double>(v.w) * static_cast<double>(v.w);
-            }
-            ss = wave_sum(ss);
-            if ((tid & 63) == 0) red[tid >> 6] = ss;
-            __syncthreads();
-            double total = 0.0;
-            for (int w = 0; w < THREADS / 64; ++w) total += red[w];
-            const float mean = static_cast<float>(total / static_cast<double>(in.width));
-            inverse_rms = 1.0f / sqrtf(mean + in.eps);
+        for (int b = blocks + tid; b < chunks * 4; b += THREADS) {
+            act_s[b] = 0.0f;
+            for (int l = 0; l < kLanesPerRow; ++l) act32[((b >> 2) * 8 + l) * 4 + (b & 3)] = 0u;
         }
-        const int iterations = (groups + THREADS - 1) / THREADS;
-        for (int it = 0; it < iterations; ++it) {
-            const int g = tid + it * THREADS;
-            const bool valid = g < groups;
-            float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (valid) y = x4[g];
+        if constexpr (PRO == Prologue::Q8) {
+            for (int g = tid; g < groups; g += THREADS) {
+                const int b = g >> 3, l = g & 7;
+                const int8_t *block = in.xq + static_cast<size_t>(b) * kQ8Bytes;
+                act32[((b >> 2) * 8 + l) * 4 + (b & 3)] = load_u32_unaligned(block + 2 + 4 * l);
+                if (l == 0) {
+                    const uint8_t *sb = reinterpret_cast<const uint8_t *>(block);
+                    act_s[b] = half_bits_to_float(static_cast<uint16_t>(sb[0] | (sb[1] << 8)));
+                }
+            }
+            __syncthreads();
+            return;
+        } else {
+            // every x (and norm weight) load of this thread is issued first
+            constexpr int kPre = 8;
+            const float4 *x4 = reinterpret_cast<const float4 *>(in.x);
+            const float4 *w4 = reinterpret_cast<const float4 *>(in.norm);
+            const int iterations = (groups + THREADS - 1) / THREADS;
+            float4 xv[kPre], wv[kPre];
+#pragma unroll
+            for (int it = 0; it < kPre; ++it) {
+                const int g = tid + it * THREADS;
+                xv[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                wv[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (it < iterations && g < groups) {
+                    xv[it] = x4[g];
+                    if constexpr (PRO == Prologue::RMSNORM) wv[it] = w4[g];
+                }
+            }
+            float inverse_rms = 1.0f;
             if constexpr (PRO == Prologue::RMSNORM) {
-                if (valid) {
-                    const float4 w = reinterpret_cast<const float4 *>(in.norm)[g];
+                double ss = 0.0;
+#pragma unroll
+                for (int it = 0; it < kPre; ++it) {
+                    ss += static_cast<double>(xv[it].x) * static_cast<double>(xv[it].x);
+                    ss += static_cast<double>(xv[it].y) * static_cast<double>(xv[it].y);
+                    ss += static_cast<double>(xv[it].z) * static_cast<double>(xv[it].z);
+                    ss += static_cast<double>(xv[it].w) * static_cast<double>(xv[it].w);
+                }
+                for (int g = tid + kPre * THREADS; g < groups; g += THREADS) {
+                    const float4 v = x4[g];
+                    ss += static_cast<double>(v.x) * static_cast<double>(v.x);
+                    ss += static_cast<double>(v.y) * static_cast<double>(v.y);
+                    ss += static_cast<double>(v.z) * static_cast<double>(v.z);
+                    ss += static_cast<double>(v.w) * static_cast<double>(v.w);
+                }
+                ss = wave_sum(ss);
+                if constexpr (THREADS > 64) {
+                    if ((tid & 63) == 0) red[tid >> 6] = ss;
+                    __syncthreads();
+                    ss = 0.0;
+                    for (int w = 0; w < THREADS / 64; ++w) ss += red[w];
+                }
+                const float mean = static_cast<float>(ss / static_cast<double>(in.width));
+                inverse_rms = 1.0f / sqrtf(mean + in.eps);
+            }
+            for (int it = 0; it < iterations; ++it) {
+                const int g = tid + it * THREADS;
+                const bool valid = g < groups;
+                float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f), w = y;
+                if (it < kPre) {
+#pragma unroll
+                    for (int k = 0; k < kPre; ++k)
+                        if (k == it) { y = xv[k]; w = wv[k]; }
+                } else if (valid) {
+                    y = x4[g];
+                    if constexpr (PRO == Prologue::RMSNORM) w = w4[g];
+                }
+                if constexpr (PRO == Prologue::RMSNORM) {
                     y.x = (y.x * inverse_rms) * w.x;
                     y.y = (y.y * inverse_rms) * w.y;
                     y.z = (y.z * inverse_rms) * w.z;
                     y.w = (y.w * inverse_rms) * w.w;
                 }
-            } else if constexpr (PRO == Prologue::GATED) {
-                // rms over the head (head/4 consecutive lanes), double sum
-                double ss = static_cast<double>(y.x) * static_cast<double>(y.x);
-                ss += static_cast<double>(y.y) * static_cast<double>(y.y);
-                ss += static_cast<double>(y.z) * static_cast<double>(y.z);
-                ss += static_cast<double>(y.w) * static_cast<double>(y.w);
-                for (int m = 1; m < in.head / 4; m <<= 1) ss += __shfl_xor(ss, m);
+                float scale;
+                uint16_t bits;
+                const uint32_t packed = quantize_group(y, scale, bits);
                 if (valid) {
-                    const float nf = sqrtf(static_cast<float>(ss / static_cast<double>(in.head)) + in.eps);
-                    const float4 z = reinterpret_cast<const float4 *>(in.gate)[g];
-                    const int j = (4 * g) % in.head;
-                    const float4 w = *reinterpret_cast<const float4 *>(in.norm + j);
-                    y.x = ((y.x / nf) * w.x) * silu_poly(z.x);
-                    y.y = ((y.y / nf) * w.y) * silu_poly(z.y);
-                    y.z = ((y.z / nf) * w.z) * silu_poly(z.z);
-                    y.w = ((y.w / nf) * w.w) * silu_poly(z.w);
+                    const int b = g >> 3, l = g & 7;
+                    act32[((b >> 2) * 8 + l) * 4 + (b & 3)] = packed;
+                    if (l == 0) act_s[b] = scale;
                 }
             }
-            float scale;
-            uint16_t bits;
-            const uint32_t packed = quantize_group(y, scale, bits);
-            if (valid) {
-                const int b = g >> 3, l = g & 7;
-                act32[((b >> 2) * 8 + l) * 4 + (b & 3)] = packed;
-                if (l == 0) act_s[b] = scale;
-            }
+            __syncthreads();
         }
-        __syncthreads();
     }
 }
 
-template <int WAVES, Prologue PRO, Epilogue EPI>
+__device__ __forceinline__ float dot_chunk(uint4 q, uint2 sc, uint4 a, float4 as, float acc) {
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.x), static_cast<int>(a.x), 0, false)), acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.y), static_cast<int>(a.y), 0, false)), acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.z), static_cast<int>(a.z), 0, false)), acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.w), static_cast<int>(a.w), 0, false)), acc);
+    return acc;
+}
+
+// NREG > 0: every chunk of the row slice (<= NREG) is loaded into registers
+// before the activation is built; NREG == 0 streams batches of 8 chunks.
+template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>
 __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs args) {
+    constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
+    constexpr int kRegs = NREG > 0 ? NREG : 1;
     extern __shared__ __align__(16) unsigned char lds[];
     uint32_t *act32 = reinterpret_cast<uint32_t *>(lds);
     float *act_s = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 8 * 16);
-    double *red = reinterpret_cast<double *>(lds + static_cast<size_t>(args.chunks) * (8 * 16 + 16));
-    build_activation<WAVES * 64, PRO>(args.in, args.chunks, act32, act_s, red);
+    double *red = reinterpret_cast<double *>(lds + static_cast<size_t>(args.chunks) * 144);
+    float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 144 + 8 * WAVES);
 
     const int wg = static_cast<int>(blockIdx.x);
     int s = 0;
@@ -174,81 +183,136 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int rg = (wg - args.first_wg[s]) * WAVES + wave;
-    if (rg >= seg.w.row_groups) return;
+    const bool active = rg < seg.w.row_groups;
     const int r = lane >> 3, l = lane & 7;
     const int chunks = seg.w.chunks;
-    const uint4 *qp = seg.w.quants + static_cast<size_t>(rg) * chunks * 64 + lane;
-    const uint2 *sp = seg.w.scales + static_cast<size_t>(rg) * chunks * 8 + r;
-    const uint4 *qp2 = nullptr;
-    const uint2 *sp2 = nullptr;
-    if constexpr (EPI == Epilogue::SILU_PAIR) {
-        qp2 = seg.w2.quants + static_cast<size_t>(rg) * chunks * 64 + lane;
-        sp2 = seg.w2.scales + static_cast<size_t>(rg) * chunks * 8 + r;
+    const uint4 *qp = seg.w.quants + static_cast<size_t>(active ? rg : 0) * chunks * 64 + lane;
+    const uint2 *sp = seg.w.scales + static_cast<size_t>(active ? rg : 0) * chunks * 8 + r;
+    const uint4 *qp2 = kPair ? seg.w2.quants + static_cast<size_t>(active ? rg : 0) * chunks * 64 + lane : nullptr;
+    const uint2 *sp2 = kPair ? seg.w2.scales + static_cast<size_t>(active ? rg : 0) * chunks * 8 + r : nullptr;
+
+    uint4 q[kRegs], q2[kPair ? kRegs : 1];
+    uint2 sc[kRegs], sc2[kPair ? kRegs : 1];
+    if constexpr (NREG > 0) {
+#pragma unroll
+        for (int c = 0; c < NREG; ++c) {
+            if (active && c < chunks) {
+                q[c] = load_stream(qp + static_cast<size_t>(c) * 64);
+                sc[c] = load_stream(sp + static_cast<size_t>(c) * 8);
+                if constexpr (kPair) {
+                    q2[c] = load_stream(qp2 + static_cast<size_t>(c) * 64);
+                    sc2[c] = load_stream(sp2 + static_cast<size_t>(c) * 8);
+                }
+            }
+        }
     }
+    build_activation<WAVES * 64, PRO>(args.in, args.chunks, act32, act_s, red);
+
     const uint4 *act4 = reinterpret_cast<const uint4 *>(act32);
     const float4 *as4 = reinterpret_cast<const float4 *>(act_s);
     float acc = 0.0f, acc2 = 0.0f;
-#pragma unroll 4
-    for (int c = 0; c < chunks; ++c) {
-        const uint4 q = load_stream(qp + static_cast<size_t>(c) * 64);
-        const uint2 sc = load_stream(sp + static_cast<size_t>(c) * 8);
-        const uint4 a = act4[c * 8 + l];
-        const float4 as = as4[c];
-        acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x,
-            static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.x), static_cast<int>(a.x), 0, false)), acc);
-        acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y,
-            static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.y), static_cast<int>(a.y), 0, false)), acc);
-        acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z,
-            static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.z), static_cast<int>(a.z), 0, false)), acc);
-        acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w,
-            static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.w), static_cast<int>(a.w), 0, false)), acc);
-        if constexpr (EPI == Epilogue::SILU_PAIR) {
-            const uint4 q2 = load_stream(qp2 + static_cast<size_t>(c) * 64);
-            const uint2 sc2 = load_stream(sp2 + static_cast<size_t>(c) * 8);
-            acc2 = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc2.x)) * as.x,
-                static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q2.x), static_cast<int>(a.x), 0, false)), acc2);
-            acc2 = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc2.x >> 16)) * as.y,
-                static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q2.y), static_cast<int>(a.y), 0, false)), acc2);
-            acc2 = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc2.y)) * as.z,
-                static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q2.z), static_cast<int>(a.z), 0, false)), acc2);
-            acc2 = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc2.y >> 16)) * as.w,
-                static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q2.w), static_cast<int>(a.w), 0, false)), acc2);
+    if (active) {
+        if constexpr (NREG > 0) {
+#pragma unroll
+            for (int c = 0; c < NREG; ++c) {
+                if (c < chunks) {
+                    const uint4 a = act4[c * 8 + l];
+                    const float4 as = as4[c];
+                    acc = dot_chunk(q[c], sc[c], a, as, acc);
+                    if constexpr (kPair) acc2 = dot_chunk(q2[c], sc2[c], a, as, acc2);
+                }
+            }
+        } else {
+            for (int c0 = 0; c0 < chunks; c0 += 8) {
+                uint4 qb[8], qb2[kPair ? 8 : 1];
+                uint2 sb[8], sb2[kPair ? 8 : 1];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (c0 + i < chunks) {
+                        qb[i] = load_stream(qp + static_cast<size_t>(c0 + i) * 64);
+                        sb[i] = load_stream(sp + static_cast<size_t>(c0 + i) * 8);
+                        if constexpr (kPair) {
+                            qb2[i] = load_stream(qp2 + static_cast<size_t>(c0 + i) * 64);
+                            sb2[i] = load_stream(sp2 + static_cast<size_t>(c0 + i) * 8);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (c0 + i < chunks) {
+                        const uint4 a = act4[(c0 + i) * 8 + l];
+                        const float4 as = as4[c0 + i];
+                        acc = dot_chunk(qb[i], sb[i], a, as, acc);
+                        if constexpr (kPair) acc2 = dot_chunk(qb2[i], sb2[i], a, as, acc2);
+                    }
+                }
+            }
         }
     }
     acc = row_hsum8(acc);
-    if constexpr (EPI == Epilogue::SILU_PAIR) acc2 = row_hsum8(acc2);
+    if constexpr (kPair) acc2 = row_hsum8(acc2);
     const int row = rg * kRowsPerWave + r;
-    if (l != 0 || row >= seg.w.rows) return;
+    const bool writer = active && l == 0 && row < seg.w.rows;
     if constexpr (EPI == Epilogue::STORE) {
-        seg.out[row] = acc;
+        if (writer) seg.out[row] = acc;
     } else if constexpr (EPI == Epilogue::ADD) {
-        seg.out[row] = acc + seg.resid[row];
+        if (writer) seg.out[row] = acc + seg.resid[row];
     } else {
         // fortai_silu_product: vector lanes for the first count/8*8 rows, the
         // libm tail expression for the rest (fortai_q8_dot.c:492-505)
-        if (row < args.pair_vector_rows) seg.out[row] = silu_poly(acc) * acc2;
-        else seg.out[row] = acc / (1.0f + exp_rounded(-acc)) * acc2;
+        const float h = row < args.pair_vector_rows ? silu_poly(acc) * acc2
+                                                    : acc / (1.0f + exp_rounded(-acc)) * acc2;
+        if (writer && seg.out) seg.out[row] = h;
+        if (seg.out_q8l) {
+            // the workgroup's 32 rows form one quantization block of h
+            if (l == 0) epi[wave * 8 + r] = h;
+            __syncthreads();
+            if (threadIdx.x < 8) {
+                const int t = static_cast<int>(threadIdx.x);
+                const float4 y = make_float4(epi[4 * t], epi[4 * t + 1], epi[4 * t + 2], epi[4 * t + 3]);
+                float scale;
+                uint16_t bits;
+                const uint32_t packed = quantize_group(y, scale, bits);
+                const int b = wg - args.first_wg[s];
+                const int hchunks = (seg.w.rows / kQ8Block + 3) / 4;
+                uint32_t *dq = static_cast<uint32_t *>(seg.out_q8l);
+                dq[((b >> 2) * 8 + t) * 4 + (b & 3)] = packed;
+                if (t == 0) reinterpret_cast<float *>(dq + hchunks * 32)[b] = scale;
+            }
+        }
     }
 }
 
-template <int WAVES, Prologue PRO, Epilogue EPI>
+template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>
 hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(args.chunks) * (8 * 16 + 16) + 8 * WAVES;
-    hipLaunchKernelGGL((q8_matvec_kernel<WAVES, PRO, EPI>), dim3(grid), dim3(WAVES * 64), lds, stream, args);
+    const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES;
+    hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI>), dim3(grid), dim3(WAVES * 64), lds, stream, args);
     return hipGetLastError();
 }
 
-template <int WAVES, Prologue PRO>
-hipError_t launch_matvec_epi(const MatvecArgs &args, int grid, Epilogue epi, hipStream_t stream) {
-    switch (epi) {
-    case Epilogue::STORE: return launch_matvec_t<WAVES, PRO, Epilogue::STORE>(args, grid, stream);
-    case Epilogue::ADD: return launch_matvec_t<WAVES, PRO, Epilogue::ADD>(args, grid, stream);
-    case Epilogue::SILU_PAIR: return launch_matvec_t<WAVES, PRO, Epilogue::SILU_PAIR>(args, grid, stream);
+template <int WAVES, Prologue PRO, Epilogue EPI>
+hipError_t launch_matvec_regs(const MatvecArgs &args, int grid, int chunks, hipStream_t stream) {
+    constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
+    if (chunks <= 8) return launch_matvec_t<WAVES, 8, PRO, EPI>(args, grid, stream);
+    if (chunks <= 16) return launch_matvec_t<WAVES, 16, PRO, EPI>(args, grid, stream);
+    if (!kPair && chunks <= 32) return launch_matvec_t<WAVES, kPair ? 0 : 32, PRO, EPI>(args, grid, stream);
+    return launch_matvec_t<WAVES, 0, PRO, EPI>(args, grid, stream);
+}
+
+template <Prologue PRO>
+hipError_t launch_matvec_pro(const MatvecArgs &args, int waves, int grid, int chunks, Epilogue epi,
+    hipStream_t stream) {
+    if (epi == Epilogue::SILU_PAIR) return launch_matvec_regs<4, PRO, Epilogue::SILU_PAIR>(args, grid, chunks, stream);
+    if (epi == Epilogue::STORE) {
+        if (waves == 4) return launch_matvec_regs<4, PRO, Epilogue::STORE>(args, grid, chunks, stream);
+        return launch_matvec_regs<1, PRO, Epilogue::STORE>(args, grid, chunks, stream);
+    }
+    if (epi == Epilogue::ADD) {
+        if (waves == 4) return launch_matvec_regs<4, PRO, Epilogue::ADD>(args, grid, chunks, stream);
+        return launch_matvec_regs<1, PRO, Epilogue::ADD>(args, grid, chunks, stream);
     }
     return hipErrorInvalidValue;
 }
-
-constexpr int kMatvecWaves = 2;
 
 __global__ void q8_repack_kernel(const uint8_t *gguf, int rows, int blocks, int chunks,
     int row_groups, uint4 *quants, uint2 *scales) {
@@ -381,6 +445,16 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const flo
 hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const MatvecInput &in,
     Prologue prologue, Epilogue epilogue, hipStream_t stream) {
     if (count < 1 || count > 4 || in.width <= 0 || in.width % kQ8Block) return hipErrorInvalidValue;
+    // one wave (8 rows) per workgroup keeps the row slices of small matrices
+    // spread over many CUs; large multi-matrix launches use 4 waves so the
+    // activation prologue is built once per 32 rows
+    int total_groups = 0;
+    for (int s = 0; s < count; ++s) total_groups += segments[s].w.row_groups;
+    const int waves = (epilogue == Epilogue::SILU_PAIR || total_groups >= 1024) ? 4 : 1;
+    if (epilogue == Epilogue::SILU_PAIR) {
+        // one workgroup = 32 rows = one quantization block of h
+        if (count != 1 || (segments[0].out_q8l && segments[0].w.rows % kQ8Block)) return hipErrorInvalidValue;
+    }
     MatvecArgs args{};
     args.count = count;
     args.in = in;
@@ -390,19 +464,18 @@ hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const Matv
         args.seg[s] = segments[s];
         args.first_wg[s] = grid;
         if (segments[s].w.chunks != args.chunks) return hipErrorInvalidValue;
-        grid += (segments[s].w.row_groups + kMatvecWaves - 1) / kMatvecWaves;
+        grid += (segments[s].w.row_groups + waves - 1) / waves;
     }
     args.first_wg[count] = grid;
     const int rows = segments[0].w.rows;
     args.pair_vector_rows = rows >= 8 ? (rows / 8) * 8 : 0;
     if (grid == 0) return hipSuccess;
     switch (prologue) {
-    case Prologue::Q8: return launch_matvec_epi<kMatvecWaves, Prologue::Q8>(args, grid, epilogue, stream);
-    case Prologue::F32: return launch_matvec_epi<kMatvecWaves, Prologue::F32>(args, grid, epilogue, stream);
-    case Prologue::RMSNORM: return launch_matvec_epi<kMatvecWaves, Prologue::RMSNORM>(args, grid, epilogue, stream);
-    case Prologue::GATED:
-        if (in.head < 4 || in.head > 256 || (in.head & (in.head - 1)) || in.width % in.head) return hipErrorInvalidValue;
-        return launch_matvec_epi<kMatvecWaves, Prologue::GATED>(args, grid, epilogue, stream);
+    case Prologue::Q8: return launch_matvec_pro<Prologue::Q8>(args, waves, grid, args.chunks, epilogue, stream);
+    case Prologue::F32: return launch_matvec_pro<Prologue::F32>(args, waves, grid, args.chunks, epilogue, stream);
+    case Prologue::RMSNORM:
+        return launch_matvec_pro<Prologue::RMSNORM>(args, waves, grid, args.chunks, epilogue, stream);
+    case Prologue::Q8L: return launch_matvec_pro<Prologue::Q8L>(args, waves, grid, args.chunks, epilogue, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -427,13 +500,13 @@ hipError_t launch_q8_quantize(const float *x, int width, int8_t *out34, float *s
 }
 
 hipError_t launch_q8_block_dots(const Q8Matrix &w, const int8_t *xq34, int32_t *out, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(w.chunks) * (8 * 16 + 16);
+    const size_t lds = static_cast<size_t>(w.chunks) * 144;
     hipLaunchKernelGGL(q8_block_dots_kernel, dim3(w.row_groups), dim3(64), lds, stream, w, xq34, out, w.blocks);
     return hipGetLastError();
 }
 
-hipError_t launch_q8_embedding(const Q8Matrix &w, const uint8_t *, const int64_t *token, int64_t token_value,
-    float *out, hipStream_t stream) {
+hipError_t launch_q8_embedding(const Q8Matrix &w, const int64_t *token, int64_t token_value, float *out,
+    hipStream_t stream) {
     const int n = w.blocks * kQ8Block;
     hipLaunchKernelGGL(q8_embedding_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, w, token, token_value, out);
     return hipGetLastError();

@@ -52,6 +52,11 @@ int fortai_hip_q8_context_capture_end(fortai_hip_q8_context *context);
 int fortai_hip_q8_context_graph_launch(fortai_hip_q8_context *context);
 /* [extension] wait for all work queued on the context's stream */
 int fortai_hip_q8_context_synchronize(fortai_hip_q8_context *context);
+/* [extension] HIP events on the context's stream: timer_start records the
+ * start event; timer_stop records the stop event, waits for it and returns
+ * the elapsed milliseconds of the work enqueued in between. */
+int fortai_hip_q8_context_timer_start(fortai_hip_q8_context *context);
+int fortai_hip_q8_context_timer_stop(fortai_hip_q8_context *context, float *elapsed_ms);
 
 /* ---- resident Q8_0 weights (fortai_cuda_backend.h:29-32).  Accepts the raw
  * GGUF Q8_0 bytes [rows][width/32][34]; they are repacked on the device into a
