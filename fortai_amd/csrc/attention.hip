@@ -76,13 +76,44 @@ __device__ __forceinline__ float tile_score(const float *q, const uint16_t *krow
 }
 
 template <bool FINITE>
-__device__ __forceinline__ void tile_pv(float *acc, const float (*prob)[kTile], const uint16_t (*vtile)[kMaxHead],
-    const float *vn, int n, int new_j, int group, int d) {
+__device__ __forceinline__ void tile_pv(float (&acc)[kMaxGroup], const float (*prob)[kTile],
+    const uint16_t (*vtile)[kMaxHead], int n, int group, int d) {
 #pragma unroll 4
     for (int j = 0; j < n; ++j) {
-        const float vv = (j == new_j) ? vn[d] : kv_value<FINITE>(vtile[j][d]);
+        const float vv = kv_value<FINITE>(vtile[j][d]);
+#pragma unroll
         for (int g = 0; g < kMaxGroup; ++g)
             if (g < group) acc[g] = __builtin_fmaf(prob[g][j], vv, acc[g]);
+    }
+}
+
+constexpr int kLoads = kTile * (kMaxHead / 8) / kThreads;  // 16-byte loads per thread per K (or V) tile
+
+// issue the K and V rows [t0, t0+n) of a kv head (rows contiguous, 16 B per load)
+__device__ __forceinline__ void fetch_tile(const AttentionParams &p, int kvh, int t0, int n, int tid,
+    uint4 (&kr)[kLoads], uint4 (&vr)[kLoads]) {
+    const int segs_k = p.head / 8, segs_v = p.value / 8;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int li = tid + i * kThreads;
+        // rows past the tile re-read row n-1 (always in bounds); stash_tile skips them
+        const int jk = min(li / segs_k, n - 1), sk = li % segs_k;
+        const int jv = min(li / segs_v, n - 1), sv = li % segs_v;
+        kr[i] = reinterpret_cast<const uint4 *>(p.kcache + (static_cast<size_t>(t0 + jk) * p.kv_heads + kvh) * p.head)[sk];
+        vr[i] = reinterpret_cast<const uint4 *>(p.vcache + (static_cast<size_t>(t0 + jv) * p.kv_heads + kvh) * p.value)[sv];
+    }
+}
+
+__device__ __forceinline__ void stash_tile(const AttentionParams &p, int n, int tid, const uint4 (&kr)[kLoads],
+    const uint4 (&vr)[kLoads], uint16_t (*ktile)[kMaxHead + 8], uint16_t (*vtile)[kMaxHead]) {
+    const int segs_k = p.head / 8, segs_v = p.value / 8;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int li = tid + i * kThreads;
+        const int jk = li / segs_k, sk = li % segs_k;
+        const int jv = li / segs_v, sv = li % segs_v;
+        if (jk < n) *reinterpret_cast<uint4 *>(&ktile[jk][sk * 8]) = kr[i];
+        if (jv < n) *reinterpret_cast<uint4 *>(&vtile[jv][sv * 8]) = vr[i];
     }
 }
 
@@ -131,36 +162,6 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
     if (tid >= 128 && tid - 128 < half) rv = p.rope[static_cast<size_t>(pos) * half + (tid - 128)];
     if (owns_new && tid < v4) vv4 = reinterpret_cast<const float4 *>(p.v + static_cast<size_t>(kvh) * value)[tid];
     const int flag = p.cache_flags ? p.cache_flags[kvh] : 1;
-    // first K/V tile (rows contiguous, 16 B per load)
-    const int segs_k = head / 8, segs_v = value / 8;
-    constexpr int kLoads = kTile * (kMaxHead / 8) / kThreads;  // 8
-    uint4 kr[kLoads], vr[kLoads];
-    auto fetch_tile = [&](int t0, int n) {
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-            const int li = tid + i * kThreads;
-            const int jk = li / segs_k, sk = li % segs_k;
-            const int jv = li / segs_v, sv = li % segs_v;
-            if (jk < n)
-                kr[i] = reinterpret_cast<const uint4 *>(
-                    p.kcache + (static_cast<size_t>(t0 + jk) * p.kv_heads + kvh) * head)[sk];
-            if (jv < n)
-                vr[i] = reinterpret_cast<const uint4 *>(
-                    p.vcache + (static_cast<size_t>(t0 + jv) * p.kv_heads + kvh) * value)[sv];
-        }
-    };
-    auto stash_tile = [&](int n) {
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-            const int li = tid + i * kThreads;
-            const int jk = li / segs_k, sk = li % segs_k;
-            const int jv = li / segs_v, sv = li % segs_v;
-            if (jk < n) *reinterpret_cast<uint4 *>(&ktile[jk][sk * 8]) = kr[i];
-            if (jv < n) *reinterpret_cast<uint4 *>(&vtile[jv][sv * 8]) = vr[i];
-        }
-    };
-    const int n0 = (p1 - p0 < kTile) ? p1 - p0 : kTile;
-    fetch_tile(p0, n0);
 
     if (tid < qn) reinterpret_cast<float4 *>(qh)[tid] = qv;
     if (tid < h4) reinterpret_cast<float4 *>(qw)[tid] = aux;
@@ -177,21 +178,21 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
         else norm_rope(kn, head, kw, p.eps, rs, p.rope_dim, lane);
     }
     __syncthreads();
+    // append at pos with the reference's float_to_half (fortai_qwen35_cpu.f90:1594-1601);
+    // the bits also replace the (not yet written) row in the LDS tile below
+    uint16_t kbits = 0, vbits = 0;
     if (owns_new) {
-        // append at pos with the reference's float_to_half (fortai_qwen35_cpu.f90:1594-1601)
         uint16_t *kdst = p.kcache + (static_cast<size_t>(pos) * p.kv_heads + kvh) * head;
         uint16_t *vdst = p.vcache + (static_cast<size_t>(pos) * p.kv_heads + kvh) * value;
         if (tid < head) {
-            const uint16_t bits = float_to_half_kv(kn[tid]);
-            kdst[tid] = bits;
-            kn[tid] = gguf_half_to_real(bits);
-            if ((bits & 0x7c00u) == 0x7c00u) overflow = 1;
+            kbits = float_to_half_kv(kn[tid]);
+            kdst[tid] = kbits;
+            if ((kbits & 0x7c00u) == 0x7c00u) overflow = 1;
         }
         if (tid < value) {
-            const uint16_t bits = float_to_half_kv(vn[tid]);
-            vdst[tid] = bits;
-            vn[tid] = gguf_half_to_real(bits);
-            if ((bits & 0x7c00u) == 0x7c00u) overflow = 1;
+            vbits = float_to_half_kv(vn[tid]);
+            vdst[tid] = vbits;
+            if ((vbits & 0x7c00u) == 0x7c00u) overflow = 1;
         }
         __syncthreads();
         if (tid == 0 && overflow && p.cache_flags) p.cache_flags[kvh] = 1;
@@ -206,21 +207,21 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
 
     for (int t0 = p0; t0 < p1; t0 += kTile) {
         const int n = (p1 - t0 < kTile) ? p1 - t0 : kTile;
-        if (t0 != p0) fetch_tile(t0, n);
-        stash_tile(n);
+        {
+            uint4 kr[kLoads], vr[kLoads];
+            fetch_tile(p, kvh, t0, n, tid, kr, vr);
+            stash_tile(p, n, tid, kr, vr, ktile, vtile);
+        }
+        if (pos >= t0 && pos < t0 + n) {
+            if (tid < head) ktile[pos - t0][tid] = kbits;
+            if (tid < value) vtile[pos - t0][tid] = vbits;
+        }
         __syncthreads();
         if (wave < group) {
             float sc = -__builtin_inff();
             if (lane < n) {
-                float dot;
-                if (t0 + lane == pos) {
-                    float d0 = 0.0f;
-                    for (int i = 0; i < head; ++i) d0 = __builtin_fmaf(qh[wave * head + i], kn[i], d0);
-                    dot = d0;
-                } else {
-                    dot = finite ? tile_score<true>(qh + wave * head, &ktile[lane][0], head)
-                                 : tile_score<false>(qh + wave * head, &ktile[lane][0], head);
-                }
+                const float dot = finite ? tile_score<true>(qh + wave * head, &ktile[lane][0], head)
+                                         : tile_score<false>(qh + wave * head, &ktile[lane][0], head);
                 sc = dot / scale_div;
             }
             float tmax = sc;
@@ -238,9 +239,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const AttentionPara
         for (int g = 0; g < kMaxGroup; ++g)
             if (g < group) acc[g] *= rescale[g];
         if (tid < value) {
-            const int new_j = (pos >= t0 && pos < t0 + n) ? pos - t0 : -1;
-            if (finite) tile_pv<true>(acc, prob, vtile, vn, n, new_j, group, tid);
-            else tile_pv<false>(acc, prob, vtile, vn, n, new_j, group, tid);
+            if (finite) tile_pv<true>(acc, prob, vtile, n, group, tid);
+            else tile_pv<false>(acc, prob, vtile, n, group, tid);
         }
         __syncthreads();
     }
