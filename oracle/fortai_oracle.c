@@ -957,3 +957,41 @@ int orc_threads(void)
     return 1;
 #endif
 }
+
+/* ------------------------------------------------------- parity helpers -- */
+
+/* Exhaustive comparison of orc_float_to_half against another implementation
+ * (the compiled reference's fortai_float_to_half) over the bit patterns
+ * [begin, end); returns the number of mismatches. */
+typedef uint16_t (*f2h_fn)(float);
+int64_t orc_float_to_half_mismatches(void *other, uint64_t begin, uint64_t end)
+{
+    f2h_fn fn = (f2h_fn)other;
+    int64_t bad = 0;
+    #pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (int64_t i = (int64_t)begin; i < (int64_t)end; ++i) {
+        const float f = f_from_bits((uint32_t)i);
+        bad += orc_float_to_half(f) != fn(f);
+    }
+    return bad;
+}
+
+void orc_float_to_half_array(const float *in, uint16_t *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_float_to_half(in[i]);
+}
+
+void orc_f32_to_f16_rne_array(const float *in, uint16_t *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_f16_rne(in[i]);
+}
+
+void orc_half_to_float_array(const uint16_t *in, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_half_to_float(in[i]);
+}
+
+void orc_gguf_fp16_to_real_array(const uint16_t *in, float *out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_gguf_fp16_to_real(in[i]);
+}

@@ -112,6 +112,11 @@ class Oracle:
             "orc_model_kcache": (C.POINTER(C.c_uint16), [_vp, _i64]),
             "orc_model_vcache": (C.POINTER(C.c_uint16), [_vp, _i64]),
             "orc_threads": (C.c_int, []),
+            "orc_float_to_half_mismatches": (_i64, [_vp, C.c_uint64, C.c_uint64]),
+            "orc_float_to_half_array": (None, [_f32p, _u16p, _i64]),
+            "orc_f32_to_f16_rne_array": (None, [_f32p, _u16p, _i64]),
+            "orc_half_to_float_array": (None, [_u16p, _f32p, _i64]),
+            "orc_gguf_fp16_to_real_array": (None, [_u16p, _f32p, _i64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)

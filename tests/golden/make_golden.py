@@ -1,0 +1,137 @@
+"""Write the golden vectors the CPU tests pin the oracle with.
+
+Run in a container that has /root/reference (after ``make -C oracle ref``):
+
+    python tests/golden/make_golden.py
+
+Every expected value here comes from the reference's own CPU code compiled
+from its sources by oracle/Makefile into oracle/_ref (the AVX2 kernels of
+src/backend/cpu/fortai_q8_dot.c and the Fortran decode step of
+src/models/qwen35/fortai_qwen35_cpu.f90 driven by oracle/ref_dump.f90).  The
+inputs are seeded synthetic data; the tiny model is ``fortai_amd.synth``'s
+``qwen35-tiny`` written with its default seed, so the GPU box can regenerate
+it without this script.
+
+Outputs (plain arrays, no pickles):
+  tests/golden/kernels.npz   float_to_half, quantize, q8_dot, gdn_step, silu
+  tests/golden/tiny_model.npz + tiny_model.json   greedy trace, logits of the
+                             first and last step, sha256 of every state buffer
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from fortai_amd import synth  # noqa: E402
+from oracle.oracle import Reference  # noqa: E402
+
+TINY_TOKEN = 17
+TINY_STEPS = 24
+TINY_CONTEXT = 64
+
+
+def f2h_inputs(rng) -> np.ndarray:
+    """Bit patterns that exercise every branch of the conversion."""
+    pats = [rng.integers(0, 1 << 32, 4096, dtype=np.uint64).astype(np.uint32)]
+    # every float exponent with fractions around the round bit (bit 12) and the carry
+    exps = np.arange(256, dtype=np.uint32) << 23
+    fr = np.array([0, 1, 0xfff, 0x1000, 0x1001, 0x1fff, 0x2000, 0x3000, 0x7fefff, 0x7ff000,
+                   0x7fffff, 0x400000, 0x401000], dtype=np.uint32)
+    grid = (exps[:, None] | fr[None, :]).reshape(-1)
+    pats += [grid, grid | 0x80000000]
+    return np.concatenate(pats).astype(np.uint32)
+
+
+def kernels(ref: Reference, rng) -> dict:
+    L = ref.lib
+    g = {}
+    bits = f2h_inputs(rng)
+    g["f2h_in"] = bits
+    g["f2h_out"] = np.array([L.fortai_float_to_half(float(v)) for v in bits.view(np.float32)],
+                            dtype=np.uint16)
+
+    x = (rng.standard_normal(32 * 16) * np.repeat(rng.uniform(0.01, 50, 16), 32)).astype(np.float32)
+    x[32:64] = 0.0            # all-zero block: scale 0, quants 0
+    x[64] = 1e-30             # tiny amax
+    x[96:128] = 1e4           # constant block
+    q = np.zeros(16 * 34, dtype=np.int8)
+    s = np.zeros(16, dtype=np.float32)
+    L.fortai_q8_quantize(x, q, s, x.size)
+    g["quant_in"], g["quant_out"], g["quant_scales"] = x, q, s
+
+    rows, nb = 6, 8
+    w = rng.integers(-128, 128, (rows, nb, 34), dtype=np.int16).astype(np.int8)
+    scales16 = rng.uniform(0.001, 0.1, (rows, nb)).astype(np.float16)
+    w[:, :, :2] = scales16.view(np.int8).reshape(rows, nb, 2)
+    w[0, 0, 2:] = -128        # vpmaddubsw pair saturation: |-128| * -128 twice
+    a = rng.standard_normal(nb * 32).astype(np.float32)
+    a[:32] = -5.0
+    aq = np.zeros(nb * 34, dtype=np.int8)
+    asc = np.zeros(nb, dtype=np.float32)
+    L.fortai_q8_quantize(a, aq, asc, a.size)
+    dots = np.array([L.fortai_q8_dot(np.ascontiguousarray(w[r]).reshape(-1), aq, asc, nb, 0)
+                     for r in range(rows)], dtype=np.float32)
+    g["dot_w"], g["dot_aq"], g["dot_as"], g["dot_out"] = w.reshape(-1), aq, asc, dots
+
+    for head in (2, 16, 64):
+        st = rng.standard_normal(head * head).astype(np.float32)
+        k = rng.standard_normal(head).astype(np.float32)
+        k /= np.float32(np.linalg.norm(k))
+        v = rng.standard_normal(head).astype(np.float32)
+        qv = rng.standard_normal(head).astype(np.float32)
+        out = np.zeros(head, dtype=np.float32)
+        g[f"gdn{head}_in"] = np.concatenate([st, k, v, qv])
+        L.fortai_gdn_step(st, k, v, qv, np.float32(0.93), np.float32(0.4), head,
+                          np.float32(1.0 / np.sqrt(head)), out)
+        g[f"gdn{head}_state"], g[f"gdn{head}_out"] = st, out
+
+    left = np.linspace(-25, 25, 1001).astype(np.float32)
+    right = rng.uniform(0.5, 1.5, left.size).astype(np.float32)
+    g["silu_left"], g["silu_right"] = left.copy(), right
+    L.fortai_silu_product(left, right, left.size)
+    g["silu_out"] = left
+    return g
+
+
+def tiny_model(ref: Reference) -> tuple[dict, dict]:
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "tiny.gguf")
+        synth.write_model(path, synth.CONFIGS["qwen35-tiny"])
+        out = os.path.join(tmp, "dump")
+        res = ref.dump(path, TINY_TOKEN, TINY_STEPS, TINY_CONTEXT, out, state=True, threads=1)
+        hashes = {}
+        for name in sorted(os.listdir(out)):
+            if name.startswith("layer"):
+                with open(os.path.join(out, name), "rb") as f:
+                    hashes[name] = hashlib.sha256(f.read()).hexdigest()
+    arrays = {"tokens": res["tokens"], "logits_first": res["logits"][0],
+              "logits_last": res["logits"][-1]}
+    meta = {"model": "qwen35-tiny", "seed": "fortai_amd.synth default", "token": TINY_TOKEN,
+            "steps": TINY_STEPS, "context": TINY_CONTEXT, "state_sha256": hashes}
+    return arrays, meta
+
+
+def main() -> None:
+    ref = Reference()
+    if not ref.available or not ref.has("ref_dump"):
+        sys.exit("oracle/_ref is not built (make -C oracle ref)")
+    rng = np.random.default_rng(0x60D)
+    np.savez_compressed(os.path.join(HERE, "kernels.npz"), **kernels(ref, rng))
+    arrays, meta = tiny_model(ref)
+    np.savez_compressed(os.path.join(HERE, "tiny_model.npz"), **arrays)
+    with open(os.path.join(HERE, "tiny_model.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+    print("wrote", os.listdir(HERE))
+
+
+if __name__ == "__main__":
+    main()

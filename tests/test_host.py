@@ -1,0 +1,155 @@
+"""Host-side logic that needs no GPU: the GGUF reader/writer, the synthetic
+model generator, layout arithmetic, the bench's byte model, and the C ABI
+library's exports (loaded, never called)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fortai_hip_backend.h")
+LIB = os.path.join(ROOT, "fortai_amd", "lib", "libfortai_hip.so")
+
+
+def header_symbols() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(fortai_hip_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_reference_surface():
+    """Every entry point of backend/cuda/fortai_cuda_backend.h has a
+    fortai_hip_* counterpart (same argument order, hip prefix)."""
+    syms = set(header_symbols())
+    # the entry points of backend/cuda/fortai_cuda_backend.h:22-152
+    mirrored = [
+        "q8_context_capture_begin", "q8_context_capture_end", "q8_context_create", "q8_context_destroy",
+        "q8_context_graph_launch", "q8_context_set_position", "q8_device_buffer_create",
+        "q8_device_buffer_destroy", "q8_device_buffer_download", "q8_device_buffer_upload",
+        "q8_device_buffer_upload_ptr", "q8_ffn_device", "q8_ffn_host", "q8_last_error",
+        "q8_matvec_device_f32", "q8_matvec_host", "q8_matvec_host_pair", "q8_matvec_host_triplet",
+        "q8_matvec_host_triplet_contiguous", "q8_matvec_resident", "q8_weights_destroy",
+        "q8_weights_upload", "qwen35_add_device", "qwen35_attention_create", "qwen35_attention_destroy",
+        "qwen35_attention_reset", "qwen35_attention_run_device", "qwen35_copy_device",
+        "qwen35_embedding_device", "qwen35_recurrent_create", "qwen35_recurrent_destroy",
+        "qwen35_recurrent_reset", "qwen35_recurrent_run", "qwen35_recurrent_run_device",
+        "qwen35_rms_norm_device",
+    ]
+    missing = [m for m in mirrored if "fortai_hip_" + m not in syms]
+    assert not missing, missing
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(LIB):
+        subprocess.run(["python", "-c", "from fortai_amd import build; build.build()"], cwd=ROOT, check=True)
+    lib = ctypes.CDLL(LIB)  # loading initialises no device
+    missing = [s for s in header_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    from fortai_amd import backend
+    assert set(backend.exported_symbols()) <= set(header_symbols())
+    assert set(header_symbols()) <= set(backend.exported_symbols())
+
+
+def test_gguf_roundtrip(tmp_path):
+    from fortai_amd import gguf
+    path = str(tmp_path / "t.gguf")
+    w = gguf.Writer(path)
+    w.add_meta("general.architecture", gguf.GGUF_STRING, "qwen35")
+    w.add_meta("qwen35.block_count", gguf.GGUF_UINT32, 3)
+    w.add_meta("qwen35.rope.freq_base", gguf.GGUF_FLOAT32, 1.0e7)
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((5, 64)).astype(np.float32)
+    b = rng.standard_normal((3, 96)).astype(np.float16)
+    from fortai_amd import synth
+    c = synth.q8_blocks(rng, 7, 64)
+    w.add_tensor("a", (64, 5), gguf.GGML_TYPE_F32)
+    w.add_tensor("b", (96, 3), gguf.GGML_TYPE_F16)
+    w.add_tensor("c", (64, 7), gguf.GGML_TYPE_Q8_0)
+    w.write({"a": a, "b": b, "c": c}.__getitem__)
+    f = gguf.read(path)
+    assert f.meta_int("qwen35.block_count") == 3
+    assert f.meta_real("qwen35.rope.freq_base", 0.0) == np.float32(1.0e7)
+    assert np.array_equal(f.tensor("a").as_f32().reshape(5, 64), a)
+    assert np.array_equal(f.tensor("b").as_f16_bits().reshape(3, 96), b.view(np.uint16))
+    t = f.tensor("c")
+    assert (t.rows, t.width) == (7, 64)
+    assert np.array_equal(np.frombuffer(t.data, dtype=np.uint8)[: c.size], c.reshape(-1))
+
+
+def test_synth_is_deterministic_and_complete(tmp_path):
+    from fortai_amd import gguf, synth, qwen35
+    cfg = synth.CONFIGS["qwen35-tiny"]
+    p1, p2 = str(tmp_path / "1.gguf"), str(tmp_path / "2.gguf")
+    synth.write_model(p1, cfg)
+    synth.write_model(p2, cfg)
+    assert open(p1, "rb").read() == open(p2, "rb").read()
+    f = gguf.read(p1)
+    d = qwen35.read_dims(f)
+    assert (d.hidden, d.layers, d.vocab, d.heads, d.kv_heads) == (cfg.hidden, cfg.layers, cfg.vocab,
+                                                                 cfg.heads, cfg.kv_heads)
+    for name, shape, ggml_type in synth.tensor_specs(cfg):
+        t = f.tensor(name)
+        assert t is not None and tuple(t.shape) == tuple(shape) and t.ggml_type == ggml_type, name
+    assert f.tensor("output.weight") is None  # tied LM head
+    # ssm_a < 0 so every decay factor exp(a * softplus(.)) is below one
+    for layer in range(cfg.layers):
+        if cfg.recurrent(layer):
+            assert np.all(f.tensor(f"blk.{layer}.ssm_a").as_f32() < 0)
+
+
+def test_q8_blocks_distribution():
+    from fortai_amd import synth
+    b = synth.q8_blocks(np.random.default_rng(1), 64, 1024).reshape(64, 32, 34)
+    q = b[:, :, 2:].view(np.int8)
+    assert q.min() >= -127 and q.max() <= 127
+    s = np.abs(b[:, :, :2].copy().view(np.float16).astype(np.float32))
+    assert s.min() >= 1e-3 * 0.999 and s.max() <= 1e-1 * 1.001
+
+
+def test_bytes_per_token_matches_the_byte_model():
+    """1,079.4 MB + 12,288 B per cached position for the 0.8B shape."""
+    import bench
+    from fortai_amd import synth
+    c = synth.CONFIGS["qwen35-0.8b"]
+    d = SimpleNamespace(hidden=c.hidden, layers=c.layers, ffn=c.ffn, heads=c.heads, kv_heads=c.kv_heads,
+                        head_size=c.head_size, value_size=c.value_size, conv_size=c.conv_size,
+                        inner=c.gdn_inner, value_heads=c.gdn_value_heads, gdn_head=c.gdn_head,
+                        conv_kernel=c.conv_kernel, vocab=c.vocab, interval=c.interval)
+    b0 = bench.bytes_per_token(d, 0)
+    assert abs(b0 / 1e6 - 1079.4) < 0.1
+    assert bench.bytes_per_token(d, 4096) - b0 == 12288 * 4096
+
+
+def test_bench_refuses_several_gpus():
+    r = subprocess.run(["python", os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_product_has_no_oracle_dependency():
+    """The shipped package neither imports nor links the parity checker."""
+    pkg = os.path.join(ROOT, "fortai_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for name in files:
+            if name.endswith((".py", ".hip", ".h", ".cpp", ".f90")):
+                text = open(os.path.join(dirpath, name), errors="ignore").read()
+                for needle in ("from oracle", "import oracle", "liboracle", "orc_", "_ref/"):
+                    assert needle not in text, (name, needle)
+                assert "/root/reference" not in text, name
+
+
+def test_backend_load_fails_loudly_without_library(tmp_path):
+    from fortai_amd import backend
+    saved = backend._lib
+    backend._lib = None
+    try:
+        with pytest.raises(FileNotFoundError):
+            backend.load(str(tmp_path / "missing.so"))
+    finally:
+        backend._lib = saved

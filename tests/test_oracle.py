@@ -1,0 +1,379 @@
+"""CPU tests that pin the oracle (oracle/fortai_oracle.c) before it is trusted.
+
+Three kinds of check, chosen so a plausible slip (a dropped term, a wrong
+sign, lane order or rounding mode) fails at least one:
+
+* the reference's own known-answer values (test/test_fortai_smoke.f90);
+* golden vectors from the reference's CPU code compiled from its sources
+  (tests/golden/*.npz, written by tests/golden/make_golden.py), and, where
+  oracle/_ref is built in this container, the compiled reference itself;
+* closed forms and brute force in float64 / exact integers.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def kg():
+    with np.load(os.path.join(GOLDEN, "kernels.npz")) as z:
+        return {k: z[k] for k in z.files}
+
+
+def need_ref(reference):
+    if not reference.available:
+        pytest.skip("oracle/_ref not built (no /root/reference here)")
+
+
+# --------------------------------------------------------------------- fp16
+
+def test_half_to_float_exhaustive(oracle):
+    h = np.arange(65536, dtype=np.uint16)
+    out = np.zeros(65536, dtype=np.float32)
+    oracle.lib.orc_half_to_float_array(h, out, h.size)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(out), nan)
+    assert np.array_equal(out[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_gguf_fp16_to_real(oracle):
+    """fortai_gguf_runtime.f90:770-788: IEEE value for finite halves, +-huge for exponent 31."""
+    h = np.arange(65536, dtype=np.uint16)
+    out = np.zeros(65536, dtype=np.float32)
+    oracle.lib.orc_gguf_fp16_to_real_array(h, out, h.size)
+    e31 = ((h >> 10) & 31) == 31
+    want = h.view(np.float16).astype(np.float32)
+    assert np.array_equal(out[~e31], want[~e31])
+    big = np.finfo(np.float32).max
+    assert np.all(np.abs(out[e31]) == big)
+    assert np.array_equal(np.signbit(out[e31]), (h[e31] & 0x8000) != 0)
+
+
+def test_f32_to_f16_rne_matches_ieee(oracle):
+    rng = np.random.default_rng(1)
+    bits = np.concatenate([
+        rng.integers(0, 1 << 32, 200000, dtype=np.uint64).astype(np.uint32),
+        # every exponent near the half range, fractions around the round bit
+        ((np.arange(96, 160, dtype=np.uint32) << 23)[:, None]
+         | np.array([0, 1, 0xfff, 0x1000, 0x1001, 0x3000, 0x7ff000, 0x7fefff, 0x7fffff],
+                    dtype=np.uint32)[None, :]).reshape(-1),
+    ])
+    bits = np.concatenate([bits, bits | 0x80000000]).astype(np.uint32)
+    f = bits.view(np.float32)
+    out = np.zeros(f.size, dtype=np.uint16)
+    oracle.lib.orc_f32_to_f16_rne_array(f, out, f.size)
+    with np.errstate(over="ignore"):
+        want = f.astype(np.float16)
+    nan = np.isnan(f)
+    assert np.array_equal(out[~nan], want[~nan].view(np.uint16))
+    assert np.all(np.isnan(out[nan].view(np.float16)))
+
+
+def test_float_to_half_golden(oracle, kg):
+    """The reference's truncate-plus-half-ulp conversion (fortai_q8_dot.c:85-113)."""
+    f = kg["f2h_in"].view(np.float32)
+    out = np.zeros(f.size, dtype=np.uint16)
+    oracle.lib.orc_float_to_half_array(f, out, f.size)
+    assert np.array_equal(out, kg["f2h_out"])
+
+
+def test_float_to_half_closed_form(oracle):
+    """Normal range: ties round away from zero; otherwise nearest; overflow -> inf."""
+    rng = np.random.default_rng(2)
+    f = rng.uniform(-60000, 60000, 100000).astype(np.float32)
+    out = np.zeros(f.size, dtype=np.uint16)
+    oracle.lib.orc_float_to_half_array(f, out, f.size)
+    rne = f.astype(np.float16)
+    # away-from-zero tie rule differs from RNE only on exact ties
+    diff = out != rne.view(np.uint16)
+    tie = (f.view(np.uint32) & 0x1fff) == 0x1000
+    assert not np.any(diff & ~tie)
+    assert np.all(np.abs(out[tie].view(np.float16).astype(np.float32)) >= np.abs(f[tie]))
+    big = np.array([65520.0, 1e6, np.inf, -np.inf], dtype=np.float32)
+    ob = np.zeros(4, dtype=np.uint16)
+    oracle.lib.orc_float_to_half_array(big, ob, 4)
+    assert list(ob) == [0x7c00, 0x7c00, 0x7c00, 0xfc00]
+
+
+@pytest.mark.slow
+def test_float_to_half_exhaustive_vs_reference(oracle, reference):
+    need_ref(reference)
+    fn = ctypes.cast(reference.lib.fortai_float_to_half, ctypes.c_void_p)
+    assert oracle.lib.orc_float_to_half_mismatches(fn, 0, 1 << 32) == 0
+
+
+# --------------------------------------------------------------- Q8_0 ops
+
+def test_reference_matvec_known_answers(oracle):
+    """test_fortai_smoke.f90:218-265: scale 1.0, quants 1..32 (x row), ones input."""
+    def row(mult):
+        b = np.zeros(34, dtype=np.uint8)
+        b[0:2] = np.array([0x3c00], dtype=np.uint16).view(np.uint8)
+        b[2:] = (mult * np.arange(1, 33)).astype(np.int8).view(np.uint8)
+        return b
+    ones = np.ones(32, dtype=np.float32)
+    assert oracle.matvec(row(1), 1, 32, ones)[0] == np.float32(527.9677734375)
+    two = np.concatenate([row(1), row(2)])
+    np.testing.assert_array_equal(oracle.matvec(two, 2, 32, ones),
+                                  np.array([527.9677734375, 1055.935546875], np.float32))
+    assert oracle.matvec(row(3), 1, 32, ones)[0] == np.float32(1583.9033203125)
+    deq = np.zeros(32, dtype=np.float32)
+    oracle.lib.orc_q8_dequantize_row(row(1).view(np.int8), deq, 1)
+    np.testing.assert_array_equal(deq, np.arange(1, 33, dtype=np.float32))
+
+
+def test_quantize_golden_and_closed_form(oracle, kg):
+    x = kg["quant_in"]
+    q, s = oracle.quantize(x)
+    assert np.array_equal(q, kg["quant_out"])
+    assert np.array_equal(s, kg["quant_scales"])
+    # closed form: scale = fp16(amax / 127), q = rint(x * 127 / amax)
+    blocks = x.reshape(-1, 32)
+    amax = np.abs(blocks).max(axis=1)
+    np.testing.assert_array_equal(s, (amax / np.float32(127)).astype(np.float16).astype(np.float32))
+    inv = np.where(amax > 0, np.float32(127) / np.where(amax > 0, amax, 1), 0).astype(np.float32)
+    want = np.clip(np.rint(blocks * inv[:, None]), -128, 127).astype(np.int8)
+    assert np.array_equal(q.reshape(-1, 34)[:, 2:], want)
+    assert np.array_equal(q.reshape(-1, 34)[:, :2].copy().view(np.uint16)[:, 0],
+                          (amax / np.float32(127)).astype(np.float16).view(np.uint16))
+
+
+def test_quantize_vs_reference(oracle, reference):
+    need_ref(reference)
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(32 * 512) * 10 ** rng.uniform(-6, 4, 32 * 512)).astype(np.float32)
+    q, s = oracle.quantize(x)
+    rq = np.zeros_like(q)
+    rs = np.zeros_like(s)
+    reference.lib.fortai_q8_quantize(x, rq, rs, x.size)
+    assert np.array_equal(q, rq) and np.array_equal(s, rs)
+
+
+def test_q8_dot_golden(oracle, kg):
+    nb = kg["dot_as"].size
+    w = kg["dot_w"].reshape(-1, nb * 34)
+    got = np.array([oracle.lib.orc_q8_dot(np.ascontiguousarray(w[r]), kg["dot_aq"], kg["dot_as"], nb, 0)
+                    for r in range(w.shape[0])], dtype=np.float32)
+    assert np.array_equal(got, kg["dot_out"])
+
+
+def test_block_dots_brute_force(oracle):
+    """Exact int32 per-block dots.  Quantized activations lie in [-127, 127]
+    (the quantizer rounds x * 127 / amax), so the int16 pair sums of
+    vpmaddubsw (at most 2 * 128 * 127) never saturate."""
+    rng = np.random.default_rng(4)
+    rows, nb = 7, 5
+    w = rng.integers(-128, 128, (rows, nb, 34)).astype(np.int8)
+    a = rng.integers(-127, 128, (nb, 34)).astype(np.int8)
+    got = oracle.block_dots(w.reshape(-1), a.reshape(-1), rows, nb)
+    want = (w[:, :, 2:].astype(np.int64) * a[None, :, 2:].astype(np.int64)).sum(axis=2)
+    assert np.array_equal(got, want)
+    w2 = np.full((1, 1, 34), -128, dtype=np.int8)
+    a2 = np.full((1, 34), -127, dtype=np.int8)
+    assert oracle.block_dots(w2.reshape(-1), a2.reshape(-1), 1, 1)[0, 0] == 32 * 128 * 127
+
+
+def test_q8_matvec_vs_float64(oracle):
+    rng = np.random.default_rng(5)
+    rows, width = 33, 256
+    from fortai_amd import synth
+    w = synth.q8_blocks(rng, rows, width)
+    x = rng.standard_normal(width).astype(np.float32)
+    got = oracle.matvec(w, rows, width, x)
+    q, s = oracle.quantize(x)
+    wb = w.reshape(rows, width // 32, 34)
+    ws = wb[:, :, :2].copy().view(np.float16)[:, :, 0].astype(np.float64)
+    wq = wb[:, :, 2:].view(np.int8).astype(np.float64)
+    xq = q.reshape(-1, 34)[:, 2:].astype(np.float64)
+    want = (ws * s[None, :].astype(np.float64) * (wq * xq[None]).sum(axis=2)).sum(axis=1)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_q8_dot_vs_reference(oracle, reference):
+    need_ref(reference)
+    rng = np.random.default_rng(6)
+    from fortai_amd import synth
+    rows, width = 16, 1024
+    w = synth.q8_blocks(rng, rows, width).view(np.int8).reshape(-1)
+    x = rng.standard_normal(width).astype(np.float32)
+    q, s = oracle.quantize(x)
+    for r in range(rows):
+        a = oracle.lib.orc_q8_dot(w, q, s, r, width // 32)
+        b = reference.lib.fortai_q8_dot(w, q, s, r, width // 32)
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)
+
+
+# ------------------------------------------------------------ GDN / SiLU
+
+def test_gdn_step_known_answer(oracle):
+    """test_fortai_smoke.f90:267-281 (2x2 state, the scalar path)."""
+    st = np.array([1, 2, 3, 4], dtype=np.float32)
+    out = np.zeros(2, dtype=np.float32)
+    oracle.lib.orc_gdn_step(st, np.array([1, 2], np.float32), np.array([5, 6], np.float32),
+                            np.array([2, 1], np.float32), 0.5, 0.25, 2, 1 / np.sqrt(2.0), out)
+    np.testing.assert_allclose(out, np.array([4.5, 5.5]) / np.sqrt(2.0), atol=1e-5)
+    np.testing.assert_allclose(st, [1.125, 2.25, 1.625, 2.25], atol=1e-5)
+
+
+@pytest.mark.parametrize("head", [2, 16, 64])
+def test_gdn_step_golden_and_recurrence(oracle, kg, head):
+    inp = kg[f"gdn{head}_in"]
+    st = inp[:head * head].copy()
+    k, v, q = (inp[head * head + i * head: head * head + (i + 1) * head].copy() for i in range(3))
+    s64 = st.astype(np.float64).reshape(head, head)
+    out = np.zeros(head, dtype=np.float32)
+    oracle.lib.orc_gdn_step(st, k, v, q, np.float32(0.93), np.float32(0.4), head,
+                            np.float32(1.0 / np.sqrt(head)), out)
+    assert np.array_equal(st, kg[f"gdn{head}_state"])
+    assert np.array_equal(out, kg[f"gdn{head}_out"])
+    # float64 delta rule: S = d S; S += beta (v - S k) k^T; o = S q / sqrt(head)
+    s64 *= np.float64(np.float32(0.93))
+    delta = (v.astype(np.float64) - s64 @ k) * np.float64(np.float32(0.4))
+    s64 += np.outer(delta, k)
+    o64 = s64 @ q / np.sqrt(head)
+    np.testing.assert_allclose(st.reshape(head, head), s64, rtol=3e-4, atol=2e-5)
+    np.testing.assert_allclose(out, o64, rtol=3e-4, atol=2e-5)
+
+
+def test_silu_golden_and_bound(oracle, kg):
+    left = kg["silu_left"].copy()
+    right = kg["silu_right"]
+    oracle.lib.orc_silu_product(left, right, left.size)
+    assert np.array_equal(left, kg["silu_out"])
+    x = kg["silu_left"].astype(np.float64)
+    want = x / (1 + np.exp(-x)) * right
+    inner = np.abs(x) <= 20  # the reference's kernel bound (test_fortai_smoke.f90:284-300)
+    assert np.max(np.abs(left[inner] - want[inner])) <= 2e-5 * 1.5
+
+
+def test_expf_poly_relative_error(oracle):
+    xs = np.linspace(-80, 80, 20001).astype(np.float32)
+    got = np.array([oracle.lib.orc_expf_poly(float(v)) for v in xs[::7]], dtype=np.float64)
+    want = np.exp(xs[::7].astype(np.float64))
+    assert np.max(np.abs(got / want - 1)) < 4e-7
+
+
+# ---------------------------------------------------- norms, RoPE, attention
+
+def test_rms_norm_closed_form(oracle):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(1024).astype(np.float32) * 3
+    w = rng.uniform(0.5, 1.5, 1024).astype(np.float32)
+    out = np.zeros_like(x)
+    oracle.lib.orc_rms_norm(x, w, np.float32(1e-6), out, x.size)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt(np.mean(x64 * x64) + 1e-6) * w
+    np.testing.assert_allclose(out, want, rtol=2e-6, atol=1e-7)
+    v = x.copy()
+    oracle.lib.orc_l2_normalize_slice(v, v.size, np.float32(1e-6))
+    np.testing.assert_allclose(v, x64 / np.linalg.norm(x64), rtol=2e-6, atol=1e-8)
+    assert abs(oracle.lib.orc_rms_slice(x, x.size, np.float32(1e-6)) - np.sqrt(np.mean(x64 ** 2) + 1e-6)) < 1e-5
+
+
+def test_rope_closed_form(oracle):
+    rng = np.random.default_rng(8)
+    heads, head, dim, base = 3, 64, 16, 1e7
+    for pos in (0, 1, 7, 100):
+        v = rng.standard_normal(heads * head).astype(np.float32)
+        r = v.copy()
+        oracle.lib.orc_apply_rope(r, heads, head, pos, dim, np.float32(base))
+        half = dim // 2
+        ang = pos / base ** (2 * np.arange(half) / dim)
+        vh, rh = v.reshape(heads, head).astype(np.float64), r.reshape(heads, head)
+        a, b = vh[:, :half], vh[:, half:dim]
+        np.testing.assert_allclose(rh[:, :half], a * np.cos(ang) - b * np.sin(ang), atol=1e-5)
+        np.testing.assert_allclose(rh[:, half:dim], a * np.sin(ang) + b * np.cos(ang), atol=1e-5)
+        np.testing.assert_array_equal(rh[:, dim:], vh[:, dim:].astype(np.float32))
+
+
+def test_attention_apply_brute_force(oracle):
+    rng = np.random.default_rng(9)
+    heads, kvh, head, value = 4, 2, 48, 32
+    for position in (0, 1, 37):
+        n = position + 1
+        kc = rng.standard_normal(n * kvh * head).astype(np.float16).view(np.uint16)
+        vc = rng.standard_normal(n * kvh * value).astype(np.float16).view(np.uint16)
+        qw = rng.standard_normal(heads * 2 * head).astype(np.float32)
+        scores = np.zeros(n, dtype=np.float32)
+        out = np.zeros(heads * value, dtype=np.float32)
+        oracle.lib.orc_attention_apply(qw, kc, vc, heads, kvh, head, value, position, scores, out)
+        K = kc.view(np.float16).astype(np.float64).reshape(n, kvh, head)
+        V = vc.view(np.float16).astype(np.float64).reshape(n, kvh, value)
+        q = qw.astype(np.float64).reshape(heads, 2, head)
+        for h in range(heads):
+            g = h // (heads // kvh)
+            s = K[:, g] @ q[h, 0] / np.sqrt(head)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            want = (p @ V[:, g]) / (1 + np.exp(-q[h, 1, :value]))
+            np.testing.assert_allclose(out[h * value:(h + 1) * value], want, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------- model step
+
+@pytest.fixture(scope="module")
+def tiny_golden():
+    with np.load(os.path.join(GOLDEN, "tiny_model.npz")) as z:
+        arrays = {k: z[k] for k in z.files}
+    with open(os.path.join(GOLDEN, "tiny_model.json")) as f:
+        meta = json.load(f)
+    return arrays, meta
+
+
+def _state_hashes(model) -> dict:
+    from oracle.oracle import Oracle
+    o: Oracle = model.o
+    out = {}
+    d = model.dims
+    for layer in range(d["layers"]):
+        if (layer + 1) % d["interval"] != 0:
+            out[f"layer{layer}.gdn.f32"] = model.gdn_state(layer)
+            out[f"layer{layer}.conv.f32"] = model.conv_state(layer)
+        else:
+            for tag, bits in (("k", model.kcache(layer)), ("v", model.vcache(layer))):
+                f = np.zeros(bits.size, dtype=np.float32)
+                o.lib.orc_gguf_fp16_to_real_array(bits, f, bits.size)
+                out[f"layer{layer}.{tag}.f32"] = f
+    return {k: hashlib.sha256(v.tobytes()).hexdigest() for k, v in out.items()}
+
+
+def test_tiny_model_matches_reference_golden(oracle, tiny_model_path, tiny_golden):
+    """Greedy decode of the synthetic tiny model: logits, token trace and every
+    KV / GDN / conv state buffer bit-identical to the compiled reference."""
+    from oracle.oracle import OracleModel
+    arrays, meta = tiny_golden
+    m = OracleModel(oracle, tiny_model_path, meta["context"])
+    trace, logits = m.greedy(meta["token"], meta["steps"], keep_logits=True)
+    assert trace == list(arrays["tokens"])
+    assert np.array_equal(logits[0], arrays["logits_first"])
+    assert np.array_equal(logits[-1], arrays["logits_last"])
+    assert _state_hashes(m) == meta["state_sha256"]
+    m.close()
+
+
+def test_tiny_model_vs_live_reference(oracle, reference, tiny_model_path, tmp_path):
+    need_ref(reference)
+    if not reference.has("ref_dump"):
+        pytest.skip("ref_dump not built")
+    from oracle.oracle import OracleModel
+    steps = 40
+    res = reference.dump(tiny_model_path, 5, steps, 64, str(tmp_path), state=False, threads=2)
+    m = OracleModel(oracle, tiny_model_path, 64)
+    trace, logits = m.greedy(5, steps, keep_logits=True)
+    assert np.array_equal(logits, res["logits"])
+    assert trace == list(res["tokens"])
+    m.close()
+
+
+def test_argmax_first_maximum(oracle):
+    v = np.array([1, 3, 3, 2], dtype=np.float32)
+    assert oracle.lib.orc_argmax(v, 4) == 1
