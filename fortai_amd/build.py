@@ -36,5 +36,36 @@ def build_library(verbose: bool = False) -> str:
     return LIB
 
 
+FORTRAN = os.path.join(HERE, "fortran")
+FC = os.environ.get("FC_AMD", "/opt/rocm/bin/amdflang")
+SMOKE = os.path.join(HERE, "lib", "hip_abi_smoke")
+
+
+def build_fortran(verbose: bool = False) -> str:
+    """Compile the iso_c_binding module (fortai_backend_hip) with its
+    standalone status module and link the Fortran ABI smoke program against
+    libfortai_hip.so (rpath to this directory)."""
+    out = os.path.join(HERE, "lib", "fortran")
+    os.makedirs(out, exist_ok=True)
+    sources = ["fortai_status.f90", "fortai_backend_hip.f90", "fortai_backend_cuda_on_hip.f90"]
+    objs = []
+    for name in sources:
+        obj = os.path.join(out, name.replace(".f90", ".o"))
+        cmd = [FC, "-O2", "-c", os.path.join(FORTRAN, name), "-o", obj, "-J", out]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"{FC} failed on {name}:\n" + res.stderr)
+        objs.append(obj)
+    cmd = [FC, "-O2", os.path.join(FORTRAN, "hip_abi_smoke.f90"), *objs[:2], "-I", out, "-J", out,
+           "-L", os.path.dirname(LIB), "-lfortai_hip", "-Wl,-rpath,$ORIGIN", "-o", SMOKE]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{FC} failed linking hip_abi_smoke:\n" + res.stderr)
+    if verbose and res.stderr:
+        print(res.stderr)
+    return SMOKE
+
+
 def build(verbose: bool = False) -> None:
     build_library(verbose)
+    build_fortran(verbose)

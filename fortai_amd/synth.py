@@ -47,6 +47,7 @@ class Qwen35Config:
     interval: int = 4
     eps: float = 1.0e-6
     rope_base: float = 1.0e7
+    embedding_q8: bool = False  # tied token_embd as Q8_0 (as llama.cpp Q8_0 exports) instead of F16
 
     @property
     def conv_size(self) -> int:
@@ -75,6 +76,12 @@ CONFIGS: Dict[str, Qwen35Config] = {
                                 kv_heads=2, head_size=64, value_size=64, rope_dim=16,
                                 gdn_key_heads=2, gdn_value_heads=4, gdn_state=64,
                                 gdn_inner=256, conv_kernel=4, vocab=4096),
+    # The tiny model with a Q8_0 tied embedding / LM head: the tensor types the
+    # reference's device pipeline requires (fortai_qwen35_cpu.f90:407-410).
+    "qwen35-tiny-q8emb": Qwen35Config("qwen35-tiny-q8emb", hidden=256, layers=4, ffn=512, heads=4,
+                                      kv_heads=2, head_size=64, value_size=64, rope_dim=16,
+                                      gdn_key_heads=2, gdn_value_heads=4, gdn_state=64,
+                                      gdn_inner=256, conv_kernel=4, vocab=4096, embedding_q8=True),
     # Mid-size: every 0.8B layer shape except the vocabulary and depth.
     "qwen35-0.8b-short": Qwen35Config("qwen35-0.8b-short", hidden=1024, layers=4, ffn=3584,
                                       heads=8, kv_heads=2, head_size=256, value_size=256,
@@ -117,7 +124,7 @@ def _normal(rng: np.random.Generator, n: int, std: float, dtype) -> np.ndarray:
 def tensor_specs(cfg: Qwen35Config) -> Iterator[Tuple[str, Tuple[int, ...], int]]:
     f32, f16, q8 = gguf.GGML_TYPE_F32, gguf.GGML_TYPE_F16, gguf.GGML_TYPE_Q8_0
     h = cfg.hidden
-    yield "token_embd.weight", (h, cfg.vocab), f16
+    yield "token_embd.weight", (h, cfg.vocab), (q8 if cfg.embedding_q8 else f16)
     yield "output_norm.weight", (h,), f32
     for i in range(cfg.layers):
         p = f"blk.{i}."

@@ -10,7 +10,13 @@
 !   <out>/layer<L>.k.f32 / .v.f32   key/value cache of attention layer L after the run
 !   <out>/layer<L>.gdn.f32 / .conv.f32   GDN and conv state of recurrent layer L
 !
-! usage: ref_dump MODEL.gguf TOKEN STEPS CONTEXT OUTDIR [DUMP_STATE(0|1)]
+! usage: ref_dump MODEL.gguf TOKEN STEPS CONTEXT OUTDIR [DUMP_STATE(0|1)] [DEVICE(0|1)]
+!
+! DEVICE=1 calls the model's enable_cuda(0) (fortai_qwen35_cpu.f90:287-384)
+! after open.  In the ref_dump_hip build the reference model is compiled
+! against fortai_amd/fortran/fortai_backend_cuda_on_hip.f90, so that call
+! moves its device pipeline onto libfortai_hip.so; the state dump then reads
+! the CPU-side buffers, which the device pipeline does not update.
 program ref_dump
     use, intrinsic :: iso_fortran_env, only: int64, real32
     use fortai_qwen35_cpu, only: qwen35_cpu_model_t
@@ -23,7 +29,7 @@ program ref_dump
     character(len=1024) :: model_path, out_dir, argument
     integer(int64) :: token, steps, context, position
     integer(int64), allocatable :: trace(:)
-    integer :: unit_logits, unit_tokens, ios, dump_state, layer
+    integer :: unit_logits, unit_tokens, ios, dump_state, layer, device
     character(len=32) :: tag
 
     call get_command_argument(1, model_path)
@@ -37,6 +43,9 @@ program ref_dump
     dump_state = 0
     call get_command_argument(6, argument)
     if (len_trim(argument) > 0) read (argument, *, iostat=ios) dump_state
+    device = 0
+    call get_command_argument(7, argument)
+    if (len_trim(argument) > 0) read (argument, *, iostat=ios) device
     if (len_trim(model_path) == 0 .or. len_trim(out_dir) == 0 .or. steps <= 0) then
         print '(a)', 'usage: ref_dump MODEL.gguf TOKEN STEPS CONTEXT OUTDIR [DUMP_STATE]'
         error stop 2
@@ -46,6 +55,13 @@ program ref_dump
     if (.not. stat%is_ok()) then
         print '(a)', 'open failed: '//stat%message
         error stop 1
+    end if
+    if (device /= 0) then
+        call model%enable_cuda(0, stat)
+        if (.not. stat%is_ok()) then
+            print '(a)', 'enable device failed: '//stat%message
+            error stop 1
+        end if
     end if
     allocate (logits(model%vocabulary_size), trace(steps))
     open (newunit=unit_logits, file=trim(out_dir)//'/logits.f32', access='stream', &

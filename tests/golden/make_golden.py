@@ -14,8 +14,9 @@ it without this script.
 
 Outputs (plain arrays, no pickles):
   tests/golden/kernels.npz   float_to_half, quantize, q8_dot, gdn_step, silu
-  tests/golden/tiny_model.npz + tiny_model.json   greedy trace, logits of the
-                             first and last step, sha256 of every state buffer
+  tests/golden/tiny_model.npz + .json, tiny_q8emb_model.npz + .json
+                             (F16 / Q8_0 tied embedding): greedy trace, logits
+                             of the first and last step, sha256 of every state
 """
 from __future__ import annotations
 
@@ -102,10 +103,10 @@ def kernels(ref: Reference, rng) -> dict:
     return g
 
 
-def tiny_model(ref: Reference) -> tuple[dict, dict]:
+def tiny_model(ref: Reference, config: str) -> tuple[dict, dict]:
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "tiny.gguf")
-        synth.write_model(path, synth.CONFIGS["qwen35-tiny"])
+        synth.write_model(path, synth.CONFIGS[config])
         out = os.path.join(tmp, "dump")
         res = ref.dump(path, TINY_TOKEN, TINY_STEPS, TINY_CONTEXT, out, state=True, threads=1)
         hashes = {}
@@ -115,7 +116,7 @@ def tiny_model(ref: Reference) -> tuple[dict, dict]:
                     hashes[name] = hashlib.sha256(f.read()).hexdigest()
     arrays = {"tokens": res["tokens"], "logits_first": res["logits"][0],
               "logits_last": res["logits"][-1]}
-    meta = {"model": "qwen35-tiny", "seed": "fortai_amd.synth default", "token": TINY_TOKEN,
+    meta = {"model": config, "seed": "fortai_amd.synth default", "token": TINY_TOKEN,
             "steps": TINY_STEPS, "context": TINY_CONTEXT, "state_sha256": hashes}
     return arrays, meta
 
@@ -126,10 +127,11 @@ def main() -> None:
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
     rng = np.random.default_rng(0x60D)
     np.savez_compressed(os.path.join(HERE, "kernels.npz"), **kernels(ref, rng))
-    arrays, meta = tiny_model(ref)
-    np.savez_compressed(os.path.join(HERE, "tiny_model.npz"), **arrays)
-    with open(os.path.join(HERE, "tiny_model.json"), "w") as f:
-        json.dump(meta, f, indent=1, sort_keys=True)
+    for config, stem in (("qwen35-tiny", "tiny_model"), ("qwen35-tiny-q8emb", "tiny_q8emb_model")):
+        arrays, meta = tiny_model(ref, config)
+        np.savez_compressed(os.path.join(HERE, stem + ".npz"), **arrays)
+        with open(os.path.join(HERE, stem + ".json"), "w") as f:
+            json.dump(meta, f, indent=1, sort_keys=True)
     print("wrote", os.listdir(HERE))
 
 

@@ -320,11 +320,10 @@ def test_attention_apply_brute_force(oracle):
 
 # ------------------------------------------------------------- model step
 
-@pytest.fixture(scope="module")
-def tiny_golden():
-    with np.load(os.path.join(GOLDEN, "tiny_model.npz")) as z:
+def load_tiny_golden(stem: str):
+    with np.load(os.path.join(GOLDEN, stem + ".npz")) as z:
         arrays = {k: z[k] for k in z.files}
-    with open(os.path.join(GOLDEN, "tiny_model.json")) as f:
+    with open(os.path.join(GOLDEN, stem + ".json")) as f:
         meta = json.load(f)
     return arrays, meta
 
@@ -346,12 +345,17 @@ def _state_hashes(model) -> dict:
     return {k: hashlib.sha256(v.tobytes()).hexdigest() for k, v in out.items()}
 
 
-def test_tiny_model_matches_reference_golden(oracle, tiny_model_path, tiny_golden):
-    """Greedy decode of the synthetic tiny model: logits, token trace and every
-    KV / GDN / conv state buffer bit-identical to the compiled reference."""
+@pytest.mark.parametrize("stem", ["tiny_model", "tiny_q8emb_model"])
+def test_tiny_model_matches_reference_golden(oracle, tmp_path, stem):
+    """Greedy decode of the synthetic tiny models (F16 and Q8_0 tied
+    embedding): logits, token trace and every KV / GDN / conv state buffer
+    bit-identical to the compiled reference."""
+    from fortai_amd import synth
     from oracle.oracle import OracleModel
-    arrays, meta = tiny_golden
-    m = OracleModel(oracle, tiny_model_path, meta["context"])
+    arrays, meta = load_tiny_golden(stem)
+    path = str(tmp_path / "m.gguf")
+    synth.write_model(path, synth.CONFIGS[meta["model"]])
+    m = OracleModel(oracle, path, meta["context"])
     trace, logits = m.greedy(meta["token"], meta["steps"], keep_logits=True)
     assert trace == list(arrays["tokens"])
     assert np.array_equal(logits[0], arrays["logits_first"])
