@@ -137,6 +137,34 @@ def traffic_from_profile(name: str):
         return json.load(f).get("traffic_bytes_per_launch")
 
 
+def traffic_probe(reps: int = 5) -> None:
+    """Launches for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes that
+    price the LM head's HBM traffic (no model file, no timing):
+    * calibration: fortai_hip_qwen35_add_device over 2^26 floats, algorithmic
+      traffic 512 MiB read + 256 MiB written per launch;
+    * the fp16 LM head with fused argmax over a random 248320 x 1024 table,
+      the dominant kernel's real shape."""
+    import numpy as np
+    from fortai_amd import backend as B
+    ctx = B.Context(0)
+    n = 1 << 26
+    a, b, o = ctx.alloc(4 * n), ctx.alloc(4 * n), ctx.alloc(4 * n)
+    for _ in range(reps):
+        ctx.call("fortai_hip_qwen35_add_device", ctx.h, a.ptr, b.ptr, o.ptr, n)
+    ctx.synchronize()
+    rows, width = 248320, 1024
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal(rows * width, dtype=np.float32) * np.float32(0.02)).astype(np.float16)
+    lm = B.F16Weights(ctx, w, rows, width)
+    del w
+    x = ctx.upload_array(rng.standard_normal(width).astype(np.float32))
+    logits, tok = ctx.alloc(rows * 4), ctx.alloc(8)
+    for _ in range(reps):
+        ctx.call("fortai_hip_f16_matvec_device", ctx.h, lm.h, x.ptr, width, logits.ptr, rows, tok.ptr)
+    ctx.synchronize()
+    log("traffic probe: 5 add launches (2^26 floats) and 5 LM head launches done")
+
+
 def bench_matvec(model, copies: int = 275, reps: int = 4):
     """quantize + Q8_0 GEMV, W 3584x1024, x ~ N(0,1)."""
     import numpy as np
@@ -208,6 +236,8 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the kernels the --pmc traffic passes measure (see traffic_probe)")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue each decode step's kernels directly instead of replaying the HIP graph "
                          "(for kernel tracing)")
@@ -218,6 +248,9 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU only (the decode step is a batch-1 single-GPU path); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
+    if args.traffic_probe:
+        traffic_probe()
+        return 0
     path = model_path(args)
     model, wall_ms, ev_ms = bench_decode(args, path)
     tok_s = args.steps / (wall_ms * 1e-3)
@@ -240,7 +273,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 x int8 -> int32 block dots, fp32 accumulate; fp16 LM head, fp32 accumulate",
+        "dtype": "q8_0: int8 dot4 -> int32, fp32 accumulate (fp16 LM head, fp32 accumulate)",
         "data": "synthetic (seeded random-init Q8_0 weights of the stated shapes; tied fp16 embedding)",
         "config": {"workload": "Qwen3.5-0.8B-shaped Q8_0 greedy decode, batch 1, positions "
                                f"{args.ctx - args.steps}..{args.ctx - 1} of a {args.ctx}-token context "
