@@ -153,3 +153,18 @@ def test_backend_load_fails_loudly_without_library(tmp_path):
             backend.load(str(tmp_path / "missing.so"))
     finally:
         backend._lib = saved
+
+
+def test_weak_stub_covers_the_header(tmp_path):
+    """fortai_hip_stub.c defines every declared entry point (weak) and fails
+    each call with FORTAI_HIP_RUNTIME_ERROR."""
+    so = str(tmp_path / "libstub.so")
+    subprocess.run(["gcc", "-shared", "-fPIC", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "fortai_amd", "fortran", "fortai_hip_stub.c"), "-o", so], check=True)
+    lib = ctypes.CDLL(so)
+    assert all(hasattr(lib, s) for s in header_symbols())
+    lib.fortai_hip_q8_context_create.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]
+    h = ctypes.c_void_p()
+    assert lib.fortai_hip_q8_context_create(0, ctypes.byref(h)) == 2
+    lib.fortai_hip_q8_last_error.restype = ctypes.c_char_p
+    assert b"without the HIP backend" in lib.fortai_hip_q8_last_error(None)
