@@ -87,6 +87,9 @@ _SIGNATURES = {
     "fortai_hip_qwen35_decoder_generate": [_vp, _i64, _i, _i, _vp],
     "fortai_hip_qwen35_decoder_replay": [_vp, _i],
     "fortai_hip_qwen35_decoder_logits": [_vp, _vpp],
+    "fortai_hip_qwen35_decoder_status": [_vp],
+    "fortai_hip_qwen35_decoder_persistent": [_vp],
+    "fortai_hip_qwen35_decoder_phase_times": [_vp, _vp, C.c_size_t],
 }
 _RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p}
 
@@ -368,6 +371,14 @@ class Decoder:
 
     def replay(self, steps: int) -> None:
         self.ctx.call("fortai_hip_qwen35_decoder_replay", self.h, steps)
+
+    def check(self) -> None:
+        """Wait for the queued steps; raise if a persistent step failed."""
+        self.ctx.call("fortai_hip_qwen35_decoder_status", self.h)
+
+    @property
+    def persistent(self) -> bool:
+        return self.ctx.lib.fortai_hip_qwen35_decoder_persistent(self.h) == 1
 
     def free(self) -> None:
         if self.h:

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <string>
 #include <vector>
 
 using namespace fortai_hip;
@@ -68,14 +69,14 @@ struct fortai_hip_qwen35_recurrent {
 struct fortai_hip_qwen35_attention {
     fortai_hip_q8_context *context = nullptr;
     const fortai_hip_q8_weights *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
-    int heads = 0, kv_heads = 0, head = 0, value = 0, max_context = 0, rope_dim = 0, chunk = 0;
+    int heads = 0, kv_heads = 0, head = 0, value = 0, max_context = 0, rope_dim = 0;
     float rope_base = 0.0f, eps = 0.0f;
     float *q_norm = nullptr, *k_norm = nullptr;
     float2 *rope = nullptr;
     uint16_t *kcache = nullptr, *vcache = nullptr;
     float *q_out = nullptr, *k_out = nullptr, *v_out = nullptr, *partial = nullptr;
     int *cache_flags = nullptr;  // per kv head: the cache holds an exponent-31 half
-    void *attn_q8l = nullptr;    // gated, quantized attention output (o_proj input)
+    float *attn_out = nullptr;   // gated attention output (o_proj input)
 };
 
 struct decoder_layer {
@@ -101,6 +102,15 @@ struct fortai_hip_qwen35_decoder {
     bool use_graph = true;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // persistent one-launch-per-token path (decode_persistent.hip)
+    bool persistent = false;
+    int grid = 0;
+    uint64_t *arena = nullptr;               // tagged-word buffers of every phase
+    PersistentLayer *layers_dev = nullptr;
+    PersistentPlan *plan_dev = nullptr;
+    uint32_t *epoch = nullptr;
+    int *status = nullptr;
+    uint64_t *phase_times = nullptr;  // FORTAI_HIP_PHASE_TIMES=1: per-workgroup phase end clocks
 };
 
 namespace {
@@ -230,7 +240,7 @@ AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q,
     p.q = q; p.k = k; p.v = v; p.q_norm = A->q_norm; p.k_norm = A->k_norm; p.rope = A->rope;
     p.kcache = A->kcache; p.vcache = A->vcache; p.partial = A->partial; p.cache_flags = A->cache_flags; p.out = out;
     p.position = A->context->position; p.heads = A->heads; p.kv_heads = A->kv_heads; p.head = A->head;
-    p.value = A->value; p.max_context = A->max_context; p.rope_dim = A->rope_dim; p.chunk = A->chunk;
+    p.value = A->value; p.max_context = A->max_context; p.rope_dim = A->rope_dim;
     p.eps = A->eps;
     return p;
 }
@@ -240,13 +250,13 @@ hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &
     const MatvecSegment segs[3] = {segment(A->q, A->q_out), segment(A->k, A->k_out), segment(A->v, A->v_out)};
     hipError_t e = launch_q8_matvec(segs, 3, in, pro, Epilogue::STORE, stream);
     if (e != hipSuccess) return e;
-    AttentionParams ap = attention_params(A, A->q_out, A->k_out, A->v_out, nullptr);
-    ap.out_q8l = A->attn_q8l;
-    e = launch_attention(ap, stream);
+    e = launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream);
     if (e != hipSuccess) return e;
     const MatvecSegment oseg = segment(A->o, out, resid);
-    return launch_q8_matvec(&oseg, 1, q8l_input(A->attn_q8l, A->heads * A->value), Prologue::Q8L,
-        resid ? Epilogue::ADD : Epilogue::STORE, stream);
+    MatvecInput oin;
+    oin.x = A->attn_out;
+    oin.width = A->heads * A->value;
+    return launch_q8_matvec(&oseg, 1, oin, Prologue::F32, resid ? Epilogue::ADD : Epilogue::STORE, stream);
 }
 
 hipError_t enqueue_ffn(const fortai_hip_q8_weights *gate, const fortai_hip_q8_weights *up,
@@ -940,15 +950,17 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
         key_norm_bytes < static_cast<size_t>(head_size) * sizeof(float) || q->width != k->width ||
         q->width != v->width)
         return FORTAI_HIP_INVALID;
-    // this backend's attention kernel: GQA groups of <= 4, head <= 256, value <= 256
-    if (heads / kv_heads > 4 || head_size > 256 || value_size > 256 || head_size % 8 || value_size % 64)
+    // this backend's attention kernels: GQA groups of <= 4, head <= 256, value <= head (multiple of 16),
+    // the scores of one head held in LDS (context <= 36864)
+    if (heads / kv_heads > 4 || head_size > 256 || value_size > head_size || head_size % 8 || value_size % 16 ||
+        max_context > 36864)
         return FORTAI_HIP_INVALID;
     *layer = nullptr;
     auto *A = new (std::nothrow) fortai_hip_qwen35_attention;
     if (!A) return FORTAI_HIP_RUNTIME_ERROR;
     A->context = c; A->q = q; A->k = k; A->v = v; A->o = o; A->heads = heads; A->kv_heads = kv_heads;
     A->head = head_size; A->value = value_size; A->max_context = max_context; A->rope_dim = rope_dimension;
-    A->rope_base = rope_base; A->eps = norm_epsilon; A->chunk = attention_chunk(max_context);
+    A->rope_base = rope_base; A->eps = norm_epsilon;
     const int half = rope_dimension / 2;
     std::vector<float2> table(static_cast<size_t>(max_context) * (half > 0 ? half : 1));
     for (int p = 0; p < max_context; ++p)
@@ -958,8 +970,6 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
             table[static_cast<size_t>(p) * half + i] = make_float2(cosf(angle), sinf(angle));
         }
     (void)hipSetDevice(c->device);
-    const int group = heads / kv_heads;
-    const int nchunk = (max_context + A->chunk - 1) / A->chunk;
     const size_t kv_n = static_cast<size_t>(max_context) * kv_heads;
     hipError_t e = upload_f32(&A->q_norm, query_norm, head_size, c->stream);
     if (e == hipSuccess) e = upload_f32(&A->k_norm, key_norm, head_size, c->stream);
@@ -971,8 +981,8 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
     if (e == hipSuccess) e = alloc(&A->q_out, static_cast<size_t>(heads) * 2 * head_size);
     if (e == hipSuccess) e = alloc(&A->k_out, static_cast<size_t>(kv_heads) * head_size);
     if (e == hipSuccess) e = alloc(&A->v_out, static_cast<size_t>(kv_heads) * value_size);
-    if (e == hipSuccess) e = alloc_q8l(&A->attn_q8l, heads * value_size, c->stream);
-    if (e == hipSuccess) e = alloc(&A->partial, static_cast<size_t>(kv_heads) * nchunk * group * (value_size + 2));
+    if (e == hipSuccess) e = alloc(&A->attn_out, static_cast<size_t>(heads) * value_size);
+    if (e == hipSuccess) e = alloc(&A->partial, attention_scores_floats(heads, max_context));
     if (e == hipSuccess) e = alloc(&A->cache_flags, kv_heads);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
@@ -996,7 +1006,7 @@ int fortai_hip_qwen35_attention_destroy(fortai_hip_qwen35_attention *A) {
     }
     release(A->q_norm); release(A->k_norm); release(A->rope); release(A->kcache); release(A->vcache);
     release(A->q_out); release(A->k_out); release(A->v_out); release(A->partial); release(A->cache_flags);
-    if (A->attn_q8l) (void)hipFree(A->attn_q8l);
+    release(A->attn_out);
     delete A;
     return FORTAI_HIP_OK;
 }
@@ -1116,7 +1126,188 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
     return e;
 }
 hipError_t run_step(fortai_hip_qwen35_decoder *d) {
+    if (d->persistent) return launch_decode_persistent(d->plan_dev, d->grid, d->context->stream);
     return d->use_graph ? hipGraphLaunch(d->exec, d->context->stream) : enqueue_decoder_step(d, d->context->stream);
+}
+// after a synchronisation: a failed persistent step (a bounded wait expired)
+// is reported once and cleared
+int persistent_status(fortai_hip_qwen35_decoder *d) {
+    if (!d->persistent) return FORTAI_HIP_OK;
+    int st[8 + 2 * 256] = {};
+    if (hipMemcpy(st, d->status, sizeof(st), hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(d->context, FORTAI_HIP_RUNTIME_ERROR, "persistent decode status read");
+    if (st[0] == 0) return FORTAI_HIP_OK;
+    (void)hipMemset(d->status, 0, sizeof(st));
+    if (st[0] & 2) return fail(d->context, FORTAI_HIP_RUNTIME_ERROR, "persistent decode: token or position out of range");
+    int lag = -1;  // the workgroup that failed in the earliest phase
+    for (int b = 0; b < d->grid; ++b)
+        if (st[8 + b] > 0 && (lag < 0 || st[8 + b] < st[8 + lag])) lag = b;
+    char msg[240];
+    std::snprintf(msg, sizeof(msg),
+        "persistent decode: wait timed out in phase %d (workgroup %d, word %d, tag %d, expected %d); earliest "
+        "failing phase %d (workgroup %d, word %d)",
+        st[1] - 1, st[2], st[3], st[4], st[5], lag >= 0 ? st[8 + lag] - 1 : -1, lag, lag >= 0 ? st[8 + 256 + lag] : -1);
+    return fail(d->context, FORTAI_HIP_RUNTIME_ERROR, msg);
+}
+}  // namespace
+
+namespace {
+PersistentMatvec persistent_matvec(std::initializer_list<std::pair<const fortai_hip_q8_weights *, uint64_t *>> segs) {
+    PersistentMatvec m{};
+    m.count = 0;
+    m.first_rg[0] = 0;
+    for (const auto &sgm : segs) {
+        m.w[m.count] = sgm.first->m;
+        m.out[m.count] = sgm.second;
+        m.first_rg[m.count + 1] = m.first_rg[m.count] + sgm.first->m.row_groups;
+        ++m.count;
+    }
+    return m;
+}
+
+// Build the persistent plan; returns "" on success, else why the shapes are
+// not supported (the decoder then keeps the per-op graph path).
+std::string setup_persistent(fortai_hip_qwen35_decoder *d) {
+    auto *c = d->context;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) != hipSuccess || cus <= 0)
+        return "device query";
+    const int grid = cus < 256 ? cus : 256;
+    if (persistent_blocks_per_cu() < 1) return "occupancy";
+    PersistentPlan P{};
+    P.layers = static_cast<int>(d->layers.size());
+    P.hidden = d->hidden; P.ffn = d->ffn; P.vocab = d->vocab; P.max_context = d->max_context; P.eps = d->eps;
+    const fortai_hip_qwen35_recurrent *R0 = nullptr;
+    const fortai_hip_qwen35_attention *A0 = nullptr;
+    for (auto &L : d->layers) {
+        if (L.recurrent && !R0) R0 = L.recurrent;
+        if (L.attention && !A0) A0 = L.attention;
+        if (L.gate->m.rows != d->ffn) return "FFN widths differ between layers";
+        if (L.recurrent && R0 && (L.recurrent->conv_size != R0->conv_size || L.recurrent->kernel != R0->kernel ||
+                                  L.recurrent->key_heads != R0->key_heads || L.recurrent->value_heads != R0->value_heads ||
+                                  L.recurrent->head != R0->head || L.recurrent->inner != R0->inner))
+            return "GDN shapes differ between layers";
+        if (L.attention && A0 && (L.attention->heads != A0->heads || L.attention->kv_heads != A0->kv_heads ||
+                                  L.attention->head != A0->head || L.attention->value != A0->value ||
+                                  L.attention->rope_dim != A0->rope_dim))
+            return "attention shapes differ between layers";
+    }
+    if (R0) {
+        if (R0->state_size != R0->head) return "GDN state size";
+        P.conv_size = R0->conv_size; P.kernel = R0->kernel; P.key_heads = R0->key_heads;
+        P.value_heads = R0->value_heads; P.head = R0->head; P.inner = R0->inner;
+    }
+    if (A0) {
+        P.heads = A0->heads; P.kv_heads = A0->kv_heads; P.head_dim = A0->head; P.value_dim = A0->value;
+        P.rope_dim = A0->rope_dim;
+    }
+    P.emb16 = d->emb16 ? d->emb16->data : nullptr;
+    if (d->emb8) P.emb8 = d->emb8->m;
+    P.out16 = d->out16 ? d->out16->data : nullptr;
+    if (d->out8) P.out8 = d->out8->m;
+    P.out_finite = d->out16 ? (d->out16->finite ? 1 : 0) : 0;
+    const char *why = persistent_unsupported(P, grid);
+    if (*why) return why;
+    for (auto &L : d->layers) {  // projections: at most two row groups per wave
+        const int rg = L.recurrent ? L.recurrent->qkv->m.row_groups + L.recurrent->gate->m.row_groups +
+                                         L.recurrent->alpha->m.row_groups + L.recurrent->beta->m.row_groups
+                                   : L.attention->q->m.row_groups + L.attention->k->m.row_groups +
+                                         L.attention->v->m.row_groups;
+        if (rg > 2 * grid * 4) return "projection rows exceed two row groups per wave";
+    }
+    if (d->out16 && d->hidden % 64) return "LM head width";
+
+    // tagged-word arena: x0, then per layer proj | mid | ao | x1 | h | x2, then the argmax partials
+    size_t words = static_cast<size_t>(d->hidden);
+    std::vector<size_t> offs;
+    for (auto &L : d->layers) {
+        size_t proj, mid, ao = 0;
+        if (L.recurrent) {
+            proj = static_cast<size_t>(P.conv_size) + P.inner + 2 * P.value_heads;
+            mid = P.inner;
+        } else {
+            proj = 2 * static_cast<size_t>(P.heads) * P.head_dim + static_cast<size_t>(P.kv_heads) * (P.head_dim + P.value_dim);
+            mid = static_cast<size_t>(P.heads) * d->max_context;  // scores [head][position]
+            ao = static_cast<size_t>(P.heads) * P.value_dim;
+        }
+        offs.push_back(words);
+        words += proj + mid + ao + 2 * static_cast<size_t>(d->hidden) + d->ffn;
+    }
+    const size_t arg_off = words;
+    words += 2 * static_cast<size_t>(grid);
+    hipError_t e = alloc(&d->arena, words);
+    if (e == hipSuccess) e = hipMemsetAsync(d->arena, 0, words * sizeof(uint64_t), c->stream);
+    if (e == hipSuccess) e = alloc(&d->epoch, 1);
+    if (e == hipSuccess) e = hipMemsetAsync(d->epoch, 0, sizeof(uint32_t), c->stream);
+    if (e == hipSuccess) e = alloc(&d->status, 8 + 2 * 256);
+    if (e == hipSuccess) e = hipMemsetAsync(d->status, 0, (8 + 2 * 256) * sizeof(int), c->stream);
+    if (e != hipSuccess) return "allocation";
+    std::vector<PersistentLayer> host(d->layers.size());
+    for (size_t i = 0; i < d->layers.size(); ++i) {
+        const decoder_layer &L = d->layers[i];
+        PersistentLayer &H = host[i];
+        uint64_t *b = d->arena + offs[i];
+        H.recurrent = L.recurrent ? 1 : 0;
+        H.attn_norm = L.attn_norm;
+        H.post_norm = L.post_norm;
+        H.ll_proj = b;
+        if (L.recurrent) {
+            const auto *R = L.recurrent;
+            H.ll_mid = b + P.conv_size + P.inner + 2 * P.value_heads;
+            H.ll_ao = nullptr;
+            H.ll_x1 = H.ll_mid + P.inner;
+            H.proj = persistent_matvec({{R->qkv, b}, {R->gate, b + P.conv_size}, {R->alpha, b + P.conv_size + P.inner},
+                                        {R->beta, b + P.conv_size + P.inner + P.value_heads}});
+            H.outp = persistent_matvec({{R->out, H.ll_x1}});
+            H.conv_w = R->conv_w; H.ssm_a = R->ssm_a; H.ssm_dt = R->ssm_dt; H.ssm_norm = R->ssm_norm;
+            H.conv_state = R->conv_state; H.state = R->state;
+        } else {
+            const auto *A = L.attention;
+            const size_t qw = 2 * static_cast<size_t>(P.heads) * P.head_dim;
+            const size_t kw = static_cast<size_t>(P.kv_heads) * P.head_dim;
+            const size_t vw = static_cast<size_t>(P.kv_heads) * P.value_dim;
+            H.ll_mid = b + qw + kw + vw;
+            H.ll_ao = H.ll_mid + static_cast<size_t>(P.heads) * d->max_context;
+            H.ll_x1 = H.ll_ao + static_cast<size_t>(P.heads) * P.value_dim;
+            H.proj = persistent_matvec({{A->q, b}, {A->k, b + qw}, {A->v, b + qw + kw}});
+            H.outp = persistent_matvec({{A->o, H.ll_x1}});
+            H.q_norm = A->q_norm; H.k_norm = A->k_norm; H.rope = A->rope;
+            H.kcache = A->kcache; H.vcache = A->vcache; H.cache_flags = A->cache_flags;
+        }
+        H.ll_h = H.ll_x1 + d->hidden;
+        H.ll_x2 = H.ll_h + d->ffn;
+        H.ffn1 = persistent_matvec({{L.gate, H.ll_h}, {L.up, nullptr}});
+        H.ffn2 = persistent_matvec({{L.down, H.ll_x2}});
+    }
+    P.output_norm = d->output_norm;
+    P.logits = d->logits;
+    P.ll_x0 = d->arena;
+    P.ll_arg = d->arena + arg_off;
+    P.token = c->token;
+    P.trace = d->trace;
+    P.position = c->position;
+    P.trace_capacity = d->max_context;
+    P.epoch = d->epoch;
+    P.status = d->status;
+    const char *times_env = std::getenv("FORTAI_HIP_PHASE_TIMES");
+    if (times_env && std::strcmp(times_env, "1") == 0) {
+        const size_t n = static_cast<size_t>(grid) * (P.layers * 6 + 3);
+        if (alloc(&d->phase_times, n) != hipSuccess) return "allocation";
+        (void)hipMemsetAsync(d->phase_times, 0, n * sizeof(uint64_t), c->stream);
+        P.phase_times = d->phase_times;
+    }
+    e = hipMalloc(reinterpret_cast<void **>(&d->layers_dev), host.size() * sizeof(PersistentLayer));
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->layers_dev, host.data(), host.size() * sizeof(PersistentLayer), hipMemcpyHostToDevice,
+            c->stream);
+    P.layer = d->layers_dev;
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&d->plan_dev), sizeof(PersistentPlan));
+    if (e == hipSuccess) e = hipMemcpyAsync(d->plan_dev, &P, sizeof(PersistentPlan), hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return "plan upload";
+    d->grid = grid;
+    d->persistent = true;
+    return "";
 }
 }  // namespace
 
@@ -1177,10 +1368,20 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     if (e == hipSuccess) e = alloc(&d->trace, max_context + 1);
     if (e == hipSuccess) e = hipMemsetAsync(d->trace, 0, (max_context + 1) * sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    // capture one decode step as a graph (FORTAI_HIP_DECODER_GRAPH=0 enqueues
-    // the kernels directly every step instead, e.g. for kernel tracing)
+    // the persistent one-launch step where the shapes allow it
+    // (FORTAI_HIP_DECODER=graph keeps the per-op kernels)
+    const char *path_env = std::getenv("FORTAI_HIP_DECODER");
+    if (e == hipSuccess && !(path_env && std::strcmp(path_env, "graph") == 0)) {
+        const std::string why = setup_persistent(d);
+        if (!why.empty() && path_env && std::strcmp(path_env, "persistent") == 0) {
+            fortai_hip_qwen35_decoder_destroy(d);
+            return fail(c, FORTAI_HIP_INVALID, ("persistent decoder unsupported: " + why).c_str());
+        }
+    }
+    // otherwise capture one per-op decode step as a graph (FORTAI_HIP_DECODER_GRAPH=0
+    // enqueues the kernels directly every step instead, e.g. for kernel tracing)
     const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
-    d->use_graph = !(graph_env && std::strcmp(graph_env, "0") == 0);
+    d->use_graph = !d->persistent && !(graph_env && std::strcmp(graph_env, "0") == 0);
     if (e == hipSuccess && d->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess && d->use_graph) {
         const hipError_t ce = enqueue_decoder_step(d, c->stream);
@@ -1209,6 +1410,8 @@ int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *d) {
     }
     release(d->output_norm); release(d->x); release(d->logits); release(d->argmax_value);
     release(d->argmax_index); release(d->trace);
+    release(d->arena); release(d->layers_dev); release(d->plan_dev); release(d->epoch); release(d->status);
+    release(d->phase_times);
     if (d->h_q8l) (void)hipFree(d->h_q8l);
     delete d;
     return FORTAI_HIP_OK;
@@ -1247,6 +1450,10 @@ int fortai_hip_qwen35_decoder_forward(fortai_hip_qwen35_decoder *d, int64_t toke
     if (e == hipSuccess && next_token)
         e = hipMemcpyAsync(next_token, c->token, sizeof(int64_t), hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess && (logits || next_token)) e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess && (logits || next_token)) {
+        const int rc = persistent_status(d);
+        if (rc != FORTAI_HIP_OK) return rc;
+    }
     return done(c, e, "decoder forward");
 }
 
@@ -1266,6 +1473,10 @@ int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *d, int64_t tok
         e = hipMemcpyAsync(trace, d->trace + position, static_cast<size_t>(steps) * sizeof(int64_t),
             hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) {
+        const int rc = persistent_status(d);
+        if (rc != FORTAI_HIP_OK) return rc;
+    }
     return done(c, e, "decoder generate");
 }
 
@@ -1277,6 +1488,30 @@ int fortai_hip_qwen35_decoder_replay(fortai_hip_qwen35_decoder *d, int steps) {
     for (int s = 0; s < steps && e == hipSuccess; ++s) e = run_step(d);
     d->next_position += steps;
     return done(c, e, "decoder replay");
+}
+
+int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *d) {
+    if (!d) return FORTAI_HIP_INVALID;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    const hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return done(c, e, "decoder status");
+    return persistent_status(d);
+}
+
+int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *d, uint64_t *host_times, size_t count) {
+    if (!d || !host_times || !d->phase_times) return FORTAI_HIP_INVALID;
+    const size_t n = static_cast<size_t>(d->grid) * (d->layers.size() * 6 + 3);
+    if (count < n) return FORTAI_HIP_INVALID;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) e = hipMemcpy(host_times, d->phase_times, n * sizeof(uint64_t), hipMemcpyDeviceToHost);
+    return done(c, e, "decoder phase times");
+}
+
+int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *d) {
+    return d ? (d->persistent ? 1 : 0) : -1;
 }
 
 int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits) {

@@ -100,9 +100,48 @@ __device__ __forceinline__ float silu_poly(float x) {
     return r;
 }
 
-// expf/logf of the reference's Fortran intrinsics (glibc, correctly rounded
-// in practice) evaluated in double and rounded once to float.
-__device__ __forceinline__ float exp_rounded(float v) { return static_cast<float>(exp(static_cast<double>(v))); }
+// expf of the C library the reference CPU path links (the Fortran real32
+// exp intrinsic calls it): glibc's algorithm from ARM optimized-routines
+// (sysdeps/ieee754/flt-32/e_expf.c, x86-64 FMA build).  x * 32/ln2 = k + r,
+// 2^(k/32) from a 32-entry table of 2^(i/32) (exponent field pre-shifted),
+// a cubic for 2^(r/32), all in double with fused multiply-adds, rounded once
+// to float.  glibc's expf is not correctly rounded (about 1 input in 10^4
+// differs from the rounded exact value), so only this sequence reproduces
+// it; on every float of [-103.5, 88] it equals the host expf bit for bit.
+// 2^(i/32) with the exponent field pre-shifted: bits(2^(i/32)) - (i << 47)
+static __constant__ const uint64_t kExpf2Table[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+__device__ __forceinline__ float expf_libm(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return __builtin_inff();
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0), c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0),
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = static_cast<double>(x);
+    const double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = kExpf2Table[ki % 32] + (ki << 47);
+    const double s = __builtin_bit_cast(double, t);
+    const double zz = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(zz, r2, y);
+    return static_cast<float>(y * s);
+}
+__device__ __forceinline__ float exp_rounded(float v) { return expf_libm(v); }
+// logf: evaluated in double and rounded once (glibc's logf differs from this
+// in about 7 of 10^4 arguments near 1; only softplus uses it).
 __device__ __forceinline__ float log_rounded(float v) { return static_cast<float>(log(static_cast<double>(v))); }
 
 // fortai_qwen35_cpu.f90:1506-1514
@@ -181,5 +220,20 @@ __device__ __forceinline__ uint32_t quantize_group(float4 y, float &scale_out, u
     const uint32_t q3 = static_cast<uint8_t>(sat8_rne(y.w * inverse));
     return q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
 }
+
+// One 16-byte Q8L chunk (4 blocks) of a row lane: the reference's per-block
+// acc = fma(f32(w_scale) * a_scale, (float)dot4(w, a), acc), block by block.
+__device__ __forceinline__ float dot_chunk(uint4 q, uint2 sc, uint4 a, float4 as, float acc) {
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.x), static_cast<int>(a.x), 0, false)), acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.y), static_cast<int>(a.y), 0, false)), acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.z), static_cast<int>(a.z), 0, false)), acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w,
+        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.w), static_cast<int>(a.w), 0, false)), acc);
+    return acc;
+}
+
 
 }  // namespace fortai_hip

@@ -141,16 +141,73 @@ struct AttentionParams {
     const float2 *rope = nullptr;   // [max_context][rope_dim/2] (cos, sin)
     uint16_t *kcache = nullptr;     // [max_context][kv_heads][head] fp16 bits
     uint16_t *vcache = nullptr;     // [max_context][kv_heads][value] fp16 bits
-    float *partial = nullptr;       // [kv_heads][chunks][group][value + 2]
+    float *partial = nullptr;       // scores [heads][max_context] (attention_scores_floats)
     int *cache_flags = nullptr;     // [kv_heads]: 1 once the cache holds an exponent-31 half
-    float *out = nullptr;           // optional [heads][value] gated output
-    void *out_q8l = nullptr;        // optional Q8L of the gated output (o_proj input)
+    float *out = nullptr;           // [heads][value] gated output
     const int *position = nullptr;  // device position (the new token's index)
     int heads = 0, kv_heads = 0, head = 0, value = 0, max_context = 0, rope_dim = 0;
-    int chunk = 0;                  // positions per workgroup
     float eps = 0.0f;
 };
 hipError_t launch_attention(const AttentionParams &p, hipStream_t stream);
-int attention_chunk(int max_context);
+size_t attention_scores_floats(int heads, int max_context);
+
+// ---- persistent decoder ------------------------------------------------------
+// One launch per token (decode_persistent.hip).  Activations cross
+// workgroups as 64-bit tagged words (tag << 32 | payload) in per-phase buffers;
+// the tag is the token sequence number + 1.
+struct PersistentMatvec {
+    Q8Matrix w[4];              // segments sharing the activation
+    uint64_t *out[4];           // tagged output words, one per row
+    int first_rg[5];            // cumulative row-group offsets of the segments
+    int count;
+};
+struct PersistentLayer {
+    int recurrent;              // 1 Gated DeltaNet, 0 full attention
+    const float *attn_norm, *post_norm;
+    PersistentMatvec proj;      // GDN: qkv | z | alpha | beta;  attention: q (q|gate per head) | k | v
+    PersistentMatvec outp;      // ssm_out / o_proj -> ll_x1 (+ residual)
+    PersistentMatvec ffn1;      // gate, up (SiLU pair) -> ll_h
+    PersistentMatvec ffn2;      // down -> ll_x2 (+ residual)
+    const float *conv_w, *ssm_a, *ssm_dt, *ssm_norm;
+    float *conv_state, *state;
+    const float *q_norm, *k_norm;
+    const float2 *rope;
+    uint16_t *kcache, *vcache;
+    int *cache_flags;
+    uint64_t *ll_proj;          // projection outputs (segments are views)
+    uint64_t *ll_mid;           // GDN raw output [inner] | attention chunk partials
+    uint64_t *ll_ao;            // attention merged, gated output [heads * value]
+    uint64_t *ll_x1, *ll_h, *ll_x2;  // residual after the mixer, FFN hidden, residual after the FFN
+};
+struct PersistentPlan {
+    int layers, hidden, ffn, vocab, max_context;
+    float eps;
+    int conv_size, kernel, key_heads, value_heads, head, inner;     // GDN
+    int heads, kv_heads, head_dim, value_dim, rope_dim;            // attention
+    const uint16_t *emb16;
+    Q8Matrix emb8;
+    const uint16_t *out16;
+    Q8Matrix out8;
+    int out_finite;
+    const float *output_norm;
+    float *logits;
+    uint64_t *ll_x0;            // embedding row [hidden]
+    uint64_t *ll_arg;           // per-workgroup argmax partials [grid][2]
+    int64_t *token, *trace;
+    int *position;
+    int trace_capacity;
+    uint32_t *epoch;            // tokens decoded by this plan (tag = epoch + 1)
+    int *status;                // non-zero: a wait timed out (every workgroup has exited)
+    uint64_t *phase_times;      // optional [grid][phases]: realtime clock at the end of each phase
+    const PersistentLayer *layer;  // device array [layers]
+};
+// Launch one decode step on `grid` workgroups (one per CU; all must be
+// co-resident); the plan lives in device memory.  persistent_lds_bytes() is
+// the dynamic LDS of a workgroup.
+hipError_t launch_decode_persistent(const PersistentPlan *plan_device, int grid, hipStream_t stream);
+size_t persistent_lds_bytes();
+int persistent_blocks_per_cu();
+// Shape limits of the persistent path ("" when supported, else the reason).
+const char *persistent_unsupported(const PersistentPlan &plan, int grid);
 
 }  // namespace fortai_hip

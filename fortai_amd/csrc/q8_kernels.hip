@@ -152,18 +152,6 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
     }
 }
 
-__device__ __forceinline__ float dot_chunk(uint4 q, uint2 sc, uint4 a, float4 as, float acc) {
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.x), static_cast<int>(a.x), 0, false)), acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.y), static_cast<int>(a.y), 0, false)), acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.z), static_cast<int>(a.z), 0, false)), acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.w), static_cast<int>(a.w), 0, false)), acc);
-    return acc;
-}
-
 // NREG > 0: every chunk of the row slice (<= NREG) is loaded into registers
 // before the activation is built; NREG == 0 streams batches of 8 chunks.
 template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>

@@ -267,6 +267,17 @@ int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *decoder, int64
 /* enqueue `steps` further graph replays continuing from the device token and
  * position (no host synchronisation; for timing loops) */
 int fortai_hip_qwen35_decoder_replay(fortai_hip_qwen35_decoder *decoder, int steps);
+/* wait for the queued steps and report whether every persistent step
+ * completed (RUNTIME_ERROR with the reason in last_error otherwise) */
+int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *decoder);
+/* 1 when the decoder runs the persistent one-launch-per-token kernel, 0 for
+ * the captured per-op graph (FORTAI_HIP_DECODER=graph|persistent selects) */
+int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *decoder);
+/* with FORTAI_HIP_PHASE_TIMES=1 at create: the device realtime clock (100 MHz)
+ * at the end of every phase of the last persistent step, [workgroup][phase],
+ * phases = 6 * layers + 3 (embed, 6 per layer, LM head, final argmax) */
+int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *decoder, uint64_t *host_times,
+    size_t count);
 /* device pointer of the decoder's logits [vocab] */
 int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits);
 

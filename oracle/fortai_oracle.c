@@ -995,3 +995,56 @@ void orc_gguf_fp16_to_real_array(const uint16_t *in, float *out, int64_t n)
 {
     for (int64_t i = 0; i < n; ++i) out[i] = orc_gguf_fp16_to_real(in[i]);
 }
+
+/* The expf sequence the GPU kernels use (fortai_amd/csrc/fortai_hip_internal.h,
+ * expf_libm): glibc's ARM optimized-routines algorithm of
+ * sysdeps/ieee754/flt-32/e_expf.c in its FMA form.  Test infrastructure: it is
+ * compared with the host expf (the function the reference calls) in
+ * tests/test_oracle.py. */
+float orc_expf_restated(float x)
+{
+    static uint64_t tab[32];
+    static int ready = 0;
+    if (!ready) {
+        for (int i = 0; i < 32; ++i) {
+            const double t = (double)exp2l((long double)i / 32.0L);
+            uint64_t b;
+            memcpy(&b, &t, 8);
+            tab[i] = b - ((uint64_t)i << 47);
+        }
+        ready = 1;
+    }
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return INFINITY;
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0), c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0),
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x, z = inv_ln2_n * xd;
+    double kd = z + shift;
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = fma(inv_ln2_n, xd, -kd);
+    const uint64_t t = tab[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double zz = fma(c0, r, c1), r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(zz, r2, y);
+    return (float)(y * s);
+}
+
+/* mismatches of orc_expf_restated against the host expf over every float
+ * bit pattern in [begin, end) */
+int64_t orc_expf_restated_mismatches(uint32_t begin, uint32_t end)
+{
+    int64_t bad = 0;
+    #pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (int64_t b = begin; b < (int64_t)end; ++b) {
+        const float x = f_from_bits((uint32_t)b);
+        const float a = expf(x), c = orc_expf_restated(x);
+        bad += memcmp(&a, &c, 4) != 0;
+    }
+    return bad;
+}

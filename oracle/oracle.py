@@ -30,6 +30,9 @@ q8_dot / block dots    brute-force integer sums; compiled reference floats
 gdn_step               smoke golden (test_fortai_smoke.f90:272-281);
                        compiled reference bit-exact; scalar recurrence of
                        fortai_cuda_gdn_ar_bench.cu:165-197 within 2e-5+3e-4|x|
+expf (device twin)     orc_expf_restated == host expf on every float of
+                       [-103.5, 0] and on samples of (0, 88] (the GPU's
+                       expf_libm is the same sequence)
 silu / silu_product    |x/(1+e^-x) - silu| <= 2e-5 on [-20,20]
                        (test_fortai_smoke.f90:284-300); compiled reference
 rms_norm, l2, rope     closed forms in float64 (tests/test_oracle.py)
@@ -117,6 +120,8 @@ class Oracle:
             "orc_f32_to_f16_rne_array": (None, [_f32p, _u16p, _i64]),
             "orc_half_to_float_array": (None, [_u16p, _f32p, _i64]),
             "orc_gguf_fp16_to_real_array": (None, [_u16p, _f32p, _i64]),
+            "orc_expf_restated": (_f32, [_f32]),
+            "orc_expf_restated_mismatches": (_i64, [C.c_uint32, C.c_uint32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)

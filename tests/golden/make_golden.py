@@ -2,7 +2,8 @@
 
 Run in a container that has /root/reference (after ``make -C oracle ref``):
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py          # kernels + tiny models (seconds)
+    python tests/golden/make_golden.py --full   # + the 0.8B 128-step trace (minutes)
 
 Every expected value here comes from the reference's own CPU code compiled
 from its sources by oracle/Makefile into oracle/_ref (the AVX2 kernels of
@@ -121,6 +122,33 @@ def tiny_model(ref: Reference, config: str) -> tuple[dict, dict]:
     return arrays, meta
 
 
+FULL_TOKEN = 9419   # greedy 128 steps from token 9419
+FULL_STEPS = 128
+FULL_CONTEXT = 4096
+TOPK = 8
+
+
+def full_model(ref: Reference, threads: int = 6) -> tuple[dict, dict]:
+    """The 0.8B-shaped model of BASELINE config 4 (1.1 GB GGUF, written to a
+    temporary directory): the 128-step greedy trace and, per step, the top-8
+    logits (index, value) -- the full logits are 1 MB per step."""
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "m.gguf")
+        synth.write_model(path, synth.CONFIGS["qwen35-0.8b"])
+        res = ref.dump(path, FULL_TOKEN, FULL_STEPS, FULL_CONTEXT, os.path.join(tmp, "out"), threads=threads)
+    return summarize_full(res["tokens"], res["logits"])
+
+
+def summarize_full(tokens, logits):
+    top_i = np.argsort(-logits, axis=1, kind="stable")[:, :TOPK].astype(np.int32)
+    top_v = np.take_along_axis(logits, top_i, axis=1).astype(np.float32)
+    arrays = {"tokens": np.asarray(tokens, dtype=np.int64), "top_index": top_i, "top_value": top_v}
+    meta = {"model": "qwen35-0.8b", "seed": "fortai_amd.synth default", "token": FULL_TOKEN,
+            "steps": FULL_STEPS, "context": FULL_CONTEXT,
+            "min_top2_margin": float(np.min(top_v[:, 0] - top_v[:, 1]))}
+    return arrays, meta
+
+
 def main() -> None:
     ref = Reference()
     if not ref.available or not ref.has("ref_dump"):
@@ -131,6 +159,11 @@ def main() -> None:
         arrays, meta = tiny_model(ref, config)
         np.savez_compressed(os.path.join(HERE, stem + ".npz"), **arrays)
         with open(os.path.join(HERE, stem + ".json"), "w") as f:
+            json.dump(meta, f, indent=1, sort_keys=True)
+    if "--full" in sys.argv:
+        arrays, meta = full_model(ref)
+        np.savez_compressed(os.path.join(HERE, "qwen35_0.8b_trace.npz"), **arrays)
+        with open(os.path.join(HERE, "qwen35_0.8b_trace.json"), "w") as f:
             json.dump(meta, f, indent=1, sort_keys=True)
     print("wrote", os.listdir(HERE))
 

@@ -237,7 +237,8 @@ def test_attention_core(ctx, oracle, L):
     gk, gv = A.cache(L)
     assert np.array_equal(gk, kc[:L * kvh * head]), "K cache after append must be bit-exact"
     assert np.array_equal(gv, vc[:L * kvh * head]), "V cache after append must be bit-exact"
-    assert rel_err(got, want) <= REL
+    # the reference's two-pass softmax with its summation orders: bit-exact
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"max diff {np.max(np.abs(got - want))}"
     A.free()
     for w in ws:
         w.free()

@@ -2,6 +2,8 @@
 (the C restatement, itself bit-exact with the compiled reference on these
 models -- tests/test_oracle.py)."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -18,9 +20,25 @@ def rel_err(got, want):
     return float(np.max(np.abs(np.asarray(got, np.float64) - want) / scale))
 
 
-@pytest.fixture(scope="module")
-def tiny(tiny_model_path):
-    m = Qwen35Hip(tiny_model_path, max_context=64)
+def open_decoder(path, max_context, mode):
+    """mode: "persistent" (one launch per token) or "graph" (captured per-op kernels)."""
+    old = os.environ.get("FORTAI_HIP_DECODER")
+    os.environ["FORTAI_HIP_DECODER"] = mode
+    try:
+        m = Qwen35Hip(path, max_context=max_context)
+    finally:
+        if old is None:
+            del os.environ["FORTAI_HIP_DECODER"]
+        else:
+            os.environ["FORTAI_HIP_DECODER"] = old
+    assert m.decoder.persistent == (mode == "persistent")
+    return m
+
+
+@pytest.fixture(scope="module", params=["persistent", "graph"])
+def tiny(request, tiny_model_path):
+    print(f"decoder path {request.param}", flush=True)
+    m = open_decoder(tiny_model_path, 64, request.param)
     yield m
     m.close()
 
@@ -69,3 +87,79 @@ def test_tiny_generate_trace_and_ops_path(tiny, oracle, tiny_model_path):
         cpu = ref.forward(token, pos)
         assert rel_err(ops, cpu) <= REL, f"ops path step {pos}"
         token = int(np.argmax(cpu))
+
+
+@pytest.fixture(scope="module")
+def tiny_q8emb_path(tmp_path_factory):
+    from fortai_amd import synth
+    path = str(tmp_path_factory.mktemp("models") / "tiny_q8emb.gguf")
+    synth.write_model(path, synth.CONFIGS["qwen35-tiny-q8emb"])
+    return path
+
+
+@pytest.mark.parametrize("mode", ["persistent", "graph"])
+def test_q8_embedding_model_trace(oracle, tiny_q8emb_path, mode):
+    """Q8_0 tied embedding / LM head (the tensor types of llama.cpp Q8_0 exports)."""
+    from oracle.oracle import OracleModel
+    ref = OracleModel(oracle, tiny_q8emb_path, 64)
+    m = open_decoder(tiny_q8emb_path, 64, mode)
+    try:
+        token = 17
+        for pos in range(12):
+            got = m.forward(token, pos).copy()
+            want = ref.forward(token, pos)
+            assert rel_err(got, want) <= REL, f"step {pos}"
+            token = int(np.argmax(want))
+            assert int(np.argmax(got)) == token
+        m.reset()
+        ref.reset()
+        assert m.generate(17, 40).tolist() == ref.greedy(17, 40)
+    finally:
+        m.close()
+
+
+@pytest.fixture(scope="module")
+def short_path(tmp_path_factory):
+    """Every 0.8B layer shape (hidden 1024, FFN 3584, GDN 16x128, attention
+    8/2 heads x 256) with 4 layers and a 16384-token vocabulary."""
+    from fortai_amd import synth
+    path = str(tmp_path_factory.mktemp("models") / "short.gguf")
+    synth.write_model(path, synth.CONFIGS["qwen35-0.8b-short"])
+    return path
+
+
+def test_full_layer_shapes_persistent_long_context(oracle, short_path):
+    """The persistent step at the 0.8B layer shapes over 300 positions: the
+    attention chunking changes as the context grows (16-position chunks at the
+    start, several sub-tiles per chunk later); logits, states and the trace
+    follow the oracle."""
+    from oracle.oracle import OracleModel
+    ctx = 320
+    ref = OracleModel(oracle, short_path, ctx)
+    m = open_decoder(short_path, ctx, "persistent")
+    try:
+        token = 9419 % 16384
+        for pos in range(8):
+            got = m.forward(token, pos).copy()
+            want = ref.forward(token, pos)
+            assert rel_err(got, want) <= REL, f"step {pos}"
+            token = int(np.argmax(want))
+            assert int(np.argmax(got)) == token, f"step {pos}"
+        trace = m.generate(token, 292, start=8)
+        want = ref.greedy(token, 292, start=8)
+        assert trace.tolist() == want
+        for i, layer in enumerate(m.attention):
+            if layer is None:
+                continue
+            k, v = layer.cache(300)
+            assert np.array_equal(k, ref.kcache(i)[:k.size]), f"K cache of layer {i}"
+            assert np.array_equal(v, ref.vcache(i)[:v.size]), f"V cache of layer {i}"
+        for i, layer in enumerate(m.recurrent):
+            if layer is None:
+                continue
+            gdn, conv = layer.state()
+            want_gdn = ref.gdn_state(i)
+            assert np.all(np.abs(gdn - want_gdn) <= 2e-5 + 3e-4 * np.abs(want_gdn)), f"GDN state of layer {i}"
+            assert rel_err(conv, ref.conv_state(i)) <= REL
+    finally:
+        m.close()

@@ -381,3 +381,12 @@ def test_tiny_model_vs_live_reference(oracle, reference, tiny_model_path, tmp_pa
 def test_argmax_first_maximum(oracle):
     v = np.array([1, 3, 3, 2], dtype=np.float32)
     assert oracle.lib.orc_argmax(v, 4) == 1
+
+
+def test_expf_restatement_matches_host_expf(oracle):
+    """The device expf (glibc's algorithm restated) equals the host expf the
+    reference calls on every float of [-103.5, 0] (all softmax arguments) and
+    of [0, 88], including -0x1.f8cbb2p+5 and 0x1.04845ep+5, the two inputs a
+    restatement without the fused r = x * 32/ln2 - k gets wrong."""
+    assert oracle.lib.orc_expf_restated_mismatches(0x80000000, 0xC2CF0001) == 0
+    assert oracle.lib.orc_expf_restated_mismatches(0x00000000, 0x42B00001) == 0
