@@ -81,14 +81,30 @@ __device__ __forceinline__ void softmax_weights(float *s, int n, float *red) {
     for (int p = tid; p < n; p += kThreads) s[p] = expf_libm(s[p] - m);
     __syncthreads();
     if (tid == 0) {
+        // left-to-right sum; LDS reads are issued a batch ahead of the adds
         float z = 0.0f;
         int p = 0;
-        for (; p + 4 <= n; p += 4) {
-            const float4 e = *reinterpret_cast<const float4 *>(s + p);
-            z = z + e.x;
-            z = z + e.y;
-            z = z + e.z;
-            z = z + e.w;
+        float4 cur[8];
+        const int full = n / 32;
+        if (full > 0) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cur[k] = *reinterpret_cast<const float4 *>(s + 4 * k);
+        }
+        for (int b = 0; b < full; ++b, p += 32) {
+            float4 nxt[8];
+            if (b + 1 < full) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) nxt[k] = *reinterpret_cast<const float4 *>(s + p + 32 + 4 * k);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                z = z + cur[k].x;
+                z = z + cur[k].y;
+                z = z + cur[k].z;
+                z = z + cur[k].w;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cur[k] = nxt[k];
         }
         for (; p < n; ++p) z = z + s[p];
         red[4] = z;
@@ -101,43 +117,89 @@ __device__ __forceinline__ void softmax_weights(float *s, int n, float *red) {
 
 // out_j = sum_p w_p * v_p,j left to right for kDims consecutive value dims:
 // lanes 0..kDims-1 of wave 0 run the chains; waves 1..3 write the products
-// fl(w_p * v_p,j) into a double-buffered LDS ring [dim][position].  The
-// value row of position p starts at vbase + p * vstride (fp16 bits).  The
-// result is valid in threads 0..kDims-1.  ring: 2 * kDims * kRingPitch floats.
+// fl(w_p * v_p,j) into a double-buffered LDS ring [dim][position], with the
+// value rows of the next kPrefetch blocks already in their registers (the
+// chains need ~0.2 us per block, a row fetch ~1-2 us).  The value row of
+// position p starts at vbase + p * vstride (fp16 bits, kDims contiguous).
+// The result is valid in threads 0..kDims-1.  ring: 2 * kDims * kRingPitch.
+constexpr int kPrefetch = 8;
+constexpr int kSegs = kRing * kDims / 8;                 // 16-byte value pieces per block
+constexpr int kSegsPerProducer = (kSegs + kThreads - 65) / (kThreads - 64);
+
+template <bool FINITE>
+__device__ __forceinline__ void pv_fetch(const uint16_t *vbase, size_t vstride, int n, int b, int ptid,
+    uint4 (&dst)[kSegsPerProducer]) {
+#pragma unroll
+    for (int i = 0; i < kSegsPerProducer; ++i) {
+        const int c = ptid + i * (kThreads - 64);
+        const int p = b * kRing + c / 2;
+        dst[i] = (c < kSegs && p < n)
+                     ? *reinterpret_cast<const uint4 *>(vbase + static_cast<size_t>(p) * vstride + (c & 1) * 8)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
 template <bool FINITE>
 __device__ __forceinline__ float pv_chains(const float *w, int n, const uint16_t *vbase, size_t vstride,
     float *ring) {
+    static_assert(kDims == 16, "two 16-byte pieces per position");
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks = (n + kRing - 1) / kRing;
-    auto produce = [&](int b, float *buf) {
-        const int p0 = b * kRing;
-        for (int idx = tid - 64; idx < kRing * kDims; idx += kThreads - 64) {
-            const int j = idx / kDims, d = idx % kDims;
-            const int p = p0 + j;
-            if (p < n) buf[d * kRingPitch + j] = w[p] * kv<FINITE>(vbase[static_cast<size_t>(p) * vstride + d]);
+    const int ptid = tid - 64;
+    uint4 pre[kPrefetch][kSegsPerProducer];
+    if (tid >= 64) {
+#pragma unroll
+        for (int k = 0; k < kPrefetch; ++k)
+            if (k < blocks) pv_fetch<FINITE>(vbase, vstride, n, k, ptid, pre[k]);
+    }
+    auto produce = [&](int b, const uint4 (&vr)[kSegsPerProducer], float *buf) {
+#pragma unroll
+        for (int i = 0; i < kSegsPerProducer; ++i) {
+            const int c = ptid + i * (kThreads - 64);
+            const int j = c / 2, d0 = (c & 1) * 8;
+            const int p = b * kRing + j;
+            if (c < kSegs && p < n) {
+                const float wp = w[p];
+                const uint32_t hw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    buf[(d0 + 2 * q) * kRingPitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] & 0xffffu));
+                    buf[(d0 + 2 * q + 1) * kRingPitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] >> 16));
+                }
+            }
         }
     };
-    if (tid >= 64) produce(0, ring);
+    if (tid >= 64) produce(0, pre[0], ring);
     __syncthreads();
     float acc = 0.0f;
-    for (int b = 0; b < blocks; ++b) {
-        float *cur = ring + (b & 1) * kDims * kRingPitch;
-        if (tid >= 64) {
-            if (b + 1 < blocks) produce(b + 1, ring + ((b + 1) & 1) * kDims * kRingPitch);
-        } else if (tid < kDims) {
-            const float *t = cur + tid * kRingPitch;
-            const int cnt = min(kRing, n - b * kRing);
-            int j = 0;
-            for (; j + 4 <= cnt; j += 4) {
-                const float4 t4 = *reinterpret_cast<const float4 *>(t + j);
-                acc = acc + t4.x;
-                acc = acc + t4.y;
-                acc = acc + t4.z;
-                acc = acc + t4.w;
+    for (int b0 = 0; b0 < blocks; b0 += kPrefetch) {
+#pragma unroll
+        for (int s = 0; s < kPrefetch; ++s) {
+            const int b = b0 + s;
+            if (b >= blocks) break;
+            float *cur = ring + (b & 1) * kDims * kRingPitch;
+            if (tid >= 64) {
+                // slot s now feeds block b + kPrefetch; block b + 1 comes from slot s + 1
+                if (b + kPrefetch < blocks) pv_fetch<FINITE>(vbase, vstride, n, b + kPrefetch, ptid, pre[s]);
+                if (b + 1 < blocks) produce(b + 1, pre[(s + 1) % kPrefetch], ring + ((b + 1) & 1) * kDims * kRingPitch);
+            } else if (tid < kDims) {
+                const float *t = cur + tid * kRingPitch;
+                const int cnt = min(kRing, n - b * kRing);
+                int j = 0;
+                for (; j + 16 <= cnt; j += 16) {
+                    const float4 a0 = *reinterpret_cast<const float4 *>(t + j);
+                    const float4 a1 = *reinterpret_cast<const float4 *>(t + j + 4);
+                    const float4 a2 = *reinterpret_cast<const float4 *>(t + j + 8);
+                    const float4 a3 = *reinterpret_cast<const float4 *>(t + j + 12);
+                    acc = acc + a0.x; acc = acc + a0.y; acc = acc + a0.z; acc = acc + a0.w;
+                    acc = acc + a1.x; acc = acc + a1.y; acc = acc + a1.z; acc = acc + a1.w;
+                    acc = acc + a2.x; acc = acc + a2.y; acc = acc + a2.z; acc = acc + a2.w;
+                    acc = acc + a3.x; acc = acc + a3.y; acc = acc + a3.z; acc = acc + a3.w;
+                }
+                for (; j < cnt; ++j) acc = acc + t[j];
             }
-            for (; j < cnt; ++j) acc = acc + t[j];
+            __syncthreads();
         }
-        __syncthreads();
     }
     return acc;
 }

@@ -9,7 +9,8 @@
 // A phase's outputs reach the next phase's workgroups as 64-bit tagged words
 // (tag << 32 | payload), written with device-scope atomic stores into a
 // buffer that only this phase writes, and read with device-scope atomic loads
-// until every word carries the current tag (the token sequence number + 1).
+// until every word carries the current tag (the launch's sequence number,
+// counted by the host and passed as an argument).
 // Each word validates itself, so the handoff needs neither counters nor
 // fences: measured on MI355X, a handoff costs about one load round trip
 // (~1 us), against ~1.7 us for a dependent kernel boundary plus the reload of
@@ -42,9 +43,6 @@ constexpr int kMaxIter = 4;        // activation groups of 4 per thread: width <
 constexpr int kMaxKernel = 8;      // conv1d taps
 constexpr int kMaxGroup = 4;       // q heads per kv head
 constexpr int kMaxHead = 256;      // head_dim / value_dim
-constexpr int kLmRows = 256;       // LM head rows per tile (one per thread)
-constexpr int kLmTileK = 64;
-constexpr int kLmPitch = 72;
 constexpr size_t kLdsBytes = 64 * 1024;  // the largest phase (LM head tile, attention tiles) needs < 48 KiB
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
@@ -63,6 +61,13 @@ __device__ __forceinline__ bool tagged(uint64_t w, uint32_t tag) { return static
 
 // Phase being executed (diagnostics of a failed wait).
 __shared__ int s_phase;
+// optional timing marks of the matvec phases (FORTAI_HIP_PHASE_TIMES=2)
+__shared__ uint64_t *g_marks;
+__shared__ int g_mark_stride;
+__device__ __forceinline__ void mark(int i) {
+    if (g_marks && threadIdx.x == 0)
+        g_marks[(static_cast<size_t>(blockIdx.x) * g_mark_stride + s_phase) * 4 + i] = wall_clock64();
+}
 
 // Load src[idx[k]] for every k (idx < 0: unused) and poll until all carry
 // `tag`.  false: timed out, or another workgroup already failed.  The first
@@ -103,6 +108,23 @@ __device__ __forceinline__ bool ll_wait(const uint64_t *src, const int (&idx)[N]
     }
 }
 
+// Two sources polled together (one round trip instead of two).
+template <int N>
+__device__ __forceinline__ bool ll_wait2(const uint64_t *a, const uint64_t *b, const int (&idx)[N], uint64_t (&va)[N],
+    uint64_t (&vb)[N], uint32_t tag, int *status) {
+    const uint64_t ready = static_cast<uint64_t>(tag) << 32;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        va[k] = idx[k] >= 0 ? ll_load(a + idx[k]) : ready;
+        vb[k] = idx[k] >= 0 ? ll_load(b + idx[k]) : ready;
+    }
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) ok = ok && tagged(va[k], tag) && tagged(vb[k], tag);
+    if (ok) return true;
+    return ll_wait(a, idx, va, tag, status) && ll_wait(b, idx, vb, tag, status);
+}
+
 // every thread of the workgroup agrees on failure (and on LDS reuse)
 __device__ __forceinline__ bool wg_ok(bool ok) { return __syncthreads_count(ok ? 0 : 1) == 0; }
 
@@ -139,11 +161,10 @@ __device__ __forceinline__ bool build_act(const uint64_t *x, const uint64_t *z, 
             w[it] = *reinterpret_cast<const float4 *>(norm + (PRO == Pro::GATED ? (4 * g) % head : 4 * g));
     }
     uint64_t v[N];
-    bool ok = ll_wait(x, ix, v, tag, status);
     uint64_t vz[PRO == Pro::GATED ? N : 1];
-    if constexpr (PRO == Pro::GATED) {
-        if (ok) ok = ll_wait(z, ix, vz, tag, status);
-    }
+    bool ok;
+    if constexpr (PRO == Pro::GATED) ok = ll_wait2(x, z, ix, v, vz, tag, status);
+    else ok = ll_wait(x, ix, v, tag, status);
     if (!wg_ok(ok)) return false;
     for (int b = blocks + tid; b < chunks * 4; b += kT) {
         as[b] = 0.0f;
@@ -271,10 +292,22 @@ __device__ __forceinline__ bool mv_phase(const PersistentMatvec &m, const MvSrc 
             }
         }
     }
+    mark(0);
+    // residual words of this lane's rows (published phases ago): loaded now, checked later
+    uint64_t rres[MAXRG];
+#pragma unroll
+    for (int j = 0; j < MAXRG; ++j) {
+        rres[j] = 0;
+        if constexpr (EPI == Epi::ADD) {
+            const int row = lrg[j] * kRowsPerWave + r;
+            if (seg[j] >= 0 && l == 0 && row < m.w[seg[j]].rows) rres[j] = ll_load(src.resid + row);
+        }
+    }
     uint32_t *aq = reinterpret_cast<uint32_t *>(lds);
     float *as = reinterpret_cast<float *>(lds + static_cast<size_t>(chunks) * 128);
     if (!build_act<PRO>(src.x, src.z, src.norm, src.width, src.head, src.eps, tag, status, aq, as, red))
         return false;
+    mark(1);
 
     const uint4 *act4 = reinterpret_cast<const uint4 *>(aq);
     const float4 *as4 = reinterpret_cast<const float4 *>(as);
@@ -295,15 +328,20 @@ __device__ __forceinline__ bool mv_phase(const PersistentMatvec &m, const MvSrc 
         }
         acc = row_hsum8(acc);
         if constexpr (kPair) acc2 = row_hsum8(acc2);
+        if (j == 0) mark(2);
         const int row = lrg[j] * kRowsPerWave + r;
         if (l != 0 || row >= w.rows) continue;
         if constexpr (EPI == Epi::STORE) {
             ll_putf(m.out[seg[j]] + row, acc, tag);
         } else if constexpr (EPI == Epi::ADD) {
-            const int ix[1] = {row};
-            uint64_t rv[1];
-            if (!ll_wait(src.resid, ix, rv, tag, status)) { ok = false; continue; }
-            ll_putf(m.out[seg[j]] + row, acc + ll_f(rv[0]), tag);
+            uint64_t rv[1] = {rres[j]};
+            if (!tagged(rv[0], tag)) {
+                const int ix[1] = {row};
+                if (!ll_wait(src.resid, ix, rv, tag, status)) { ok = false; continue; }
+            }
+            const float y = acc + ll_f(rv[0]);
+            ll_putf(m.out[seg[j]] + row, y, tag);
+            if (m.plain) m.plain[row] = y;
         } else {
             // fortai_silu_product: vector lanes for the first rows/8*8 rows,
             // the libm expression for the tail (fortai_q8_dot.c:492-505)
@@ -312,7 +350,9 @@ __device__ __forceinline__ bool mv_phase(const PersistentMatvec &m, const MvSrc 
             ll_putf(m.out[0] + row, h, tag);
         }
     }
-    return wg_ok(ok);
+    const bool all = wg_ok(ok);
+    mark(3);
+    return all;
 }
 
 // ------------------------------------------------------------------- embed
@@ -455,27 +495,32 @@ __device__ __forceinline__ bool gdn_phase(const PersistentPlan &P, const Persist
 }
 
 // Shift the conv windows (fortai_qwen35_cpu.f90:870-879) once every GDN unit
-// of the layer has published, i.e. has finished reading them.
-__device__ __forceinline__ bool conv_shift(const PersistentPlan &P, const PersistentLayer &L, uint32_t tag, int *status) {
-    const int C = P.conv_size, K = P.kernel, I = P.inner;
+// of the layer has finished reading them: run during the gate/up phase by
+// the workgroups that have no rows there, after they see the mixer output
+// x1 (published only after every GDN unit did).  Without idle workgroups,
+// every workgroup shifts a share after its rows.
+__device__ __forceinline__ bool conv_shift(const PersistentPlan &P, const PersistentLayer &L, int first, int count,
+    uint32_t tag, int *status) {
+    const int C = P.conv_size, K = P.kernel;
     const int tid = static_cast<int>(threadIdx.x);
-    const int first = static_cast<int>(blockIdx.x) * kT;
-    if (first >= C) return true;
-    constexpr int N = 16;  // inner <= 4096
+    const int me = static_cast<int>(blockIdx.x) - first;
+    if (me < 0 || me * kT >= C) return true;
+    constexpr int N = 4;  // hidden <= 1024
     int ix[N];
 #pragma unroll
-    for (int k = 0; k < N; ++k) ix[k] = tid + k * kT < I ? tid + k * kT : -1;
+    for (int k = 0; k < N; ++k) ix[k] = tid + k * kT < P.hidden ? tid + k * kT : -1;
     uint64_t v[N];
-    if (!wg_ok(ll_wait(L.ll_mid, ix, v, tag, status))) return false;
-    for (int ch = first + tid; ch < C; ch += static_cast<int>(gridDim.x) * kT) {
+    if (!wg_ok(ll_wait(L.ll_x1, ix, v, tag, status))) return false;
+    bool ok = true;
+    for (int ch = me * kT + tid; ch < C; ch += count * kT) {
         const int one[1] = {ch};
         uint64_t xv[1];
-        if (!ll_wait(L.ll_proj, one, xv, tag, status)) break;
+        if (!ll_wait(L.ll_proj, one, xv, tag, status)) { ok = false; break; }
         for (int sl = 0; sl + 1 < K - 1; ++sl)
             L.conv_state[static_cast<size_t>(sl) * C + ch] = L.conv_state[static_cast<size_t>(sl + 1) * C + ch];
         L.conv_state[static_cast<size_t>(K - 2) * C + ch] = ll_f(xv[0]);
     }
-    return wg_ok(__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0);
+    return wg_ok(ok);
 }
 
 // -------------------------------------------------------------- attention
@@ -634,176 +679,31 @@ __device__ __forceinline__ bool att_output_phase(const PersistentPlan &P, const 
     return true;
 }
 
-// ---------------------------------------------------------------- LM head
-
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
-
-__device__ __forceinline__ void wg_argmax(float &v, int &i, float *sv, int *si) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = __shfl_xor(v, m);
-        const int oi = __shfl_xor(i, m);
-        if (better(ov, oi, v, i)) { v = ov; i = oi; }
-    }
-    const int tid = static_cast<int>(threadIdx.x);
-    if ((tid & 63) == 0) { sv[tid >> 6] = v; si[tid >> 6] = i; }
-    __syncthreads();
-    if (tid == 0)
-        for (int w = 1; w < kW; ++w)
-            if (better(sv[w], si[w], v, i)) { v = sv[w]; i = si[w]; }
-}
-
-// Tied fp16 LM head: final RMSNorm fused, one row per thread with the
-// reference's sequential fp32 chain (fortai_gguf_runtime.f90:382-386),
-// 256-row x 64-column tiles staged through LDS; tiles b, b + grid, ...
-template <bool FINITE>
-__device__ __forceinline__ bool lm_head_f16(const PersistentPlan &P, const uint64_t *x, uint32_t tag, int *status, unsigned char *lds,
-    double *red, float &best_v, int &best_i) {
-    const int tid = static_cast<int>(threadIdx.x);
-    const int V = P.vocab, H = P.hidden;
-    uint16_t *tile = reinterpret_cast<uint16_t *>(lds);
-    float *xs = reinterpret_cast<float *>(lds + kLmRows * kLmPitch * 2);
-    const int tiles = (V + kLmRows - 1) / kLmRows;
-    constexpr int kLoads = kLmRows * kLmTileK * 2 / 16 / kLmRows;  // 8
-    uint4 regs[kLoads];
-    auto fetch = [&](int row0, int k0) {
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int li = tid + kLmRows * j;
-            const int rr = li >> 3, seg = li & 7;
-            const int grow = row0 + rr;
-            regs[j] = grow < V ? load_stream(reinterpret_cast<const uint4 *>(P.out16 + static_cast<size_t>(grow) * H +
-                                                                             k0 + seg * 8))
-                               : make_uint4(0u, 0u, 0u, 0u);
-        }
-    };
-    const int t_first = static_cast<int>(blockIdx.x);
-    if (t_first < tiles) fetch(t_first * kLmRows, 0);
-    // x = rms_norm(x, output_norm) into LDS (fortai_qwen35_cpu.f90:707)
-    {
-        constexpr int N = 4;  // hidden <= 1024
-        int ix[N];
-        float wn[N];
-#pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const int i = tid + k * kT;
-            ix[k] = i < H ? i : -1;
-            wn[k] = i < H ? P.output_norm[i] : 0.0f;
-        }
-        uint64_t v[N];
-        if (!wg_ok(ll_wait(x, ix, v, tag, status))) return false;
-        double ss = 0.0;
-#pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const float f = ll_f(v[k]);
-            if (ix[k] >= 0) ss += static_cast<double>(f) * static_cast<double>(f);
-        }
-        ss = wave_sum(ss);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        double total = 0.0;
-        for (int k = 0; k < kW; ++k) total += red[k];
-        const float inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(H)) + P.eps);
-#pragma unroll
-        for (int k = 0; k < N; ++k)
-            if (ix[k] >= 0) xs[ix[k]] = (ll_f(v[k]) * inv) * wn[k];
-    }
-    for (int t = t_first; t < tiles; t += static_cast<int>(gridDim.x)) {
-        const int row0 = t * kLmRows;
-        float acc = 0.0f;
-        for (int k0 = 0; k0 < H; k0 += kLmTileK) {
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < kLoads; ++j) {
-                const int li = tid + kLmRows * j;
-                *reinterpret_cast<uint4 *>(tile + (li >> 3) * kLmPitch + (li & 7) * 8) = regs[j];
-            }
-            __syncthreads();
-            if (k0 + kLmTileK < H) fetch(row0, k0 + kLmTileK);
-            else if (t + static_cast<int>(gridDim.x) < tiles) fetch(row0 + static_cast<int>(gridDim.x) * kLmRows, 0);
-            const uint16_t *mine = tile + tid * kLmPitch;
-#pragma unroll
-            for (int s = 0; s < kLmTileK / 8; ++s) {
-                const uint4 h8 = *reinterpret_cast<const uint4 *>(mine + s * 8);
-                const uint32_t hw[4] = {h8.x, h8.y, h8.z, h8.w};
-#pragma unroll
-                for (int qq = 0; qq < 4; ++qq) {
-                    const float a = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[qq] & 0xffffu))
-                                           : gguf_half_to_real(static_cast<uint16_t>(hw[qq] & 0xffffu));
-                    const float b = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[qq] >> 16))
-                                           : gguf_half_to_real(static_cast<uint16_t>(hw[qq] >> 16));
-                    const int k = k0 + s * 8 + qq * 2;
-                    acc = acc + a * xs[k];
-                    acc = acc + b * xs[k + 1];
-                }
-            }
-        }
-        const int row = row0 + tid;
-        if (row < V) {
-            P.logits[row] = acc;
-            if (better(acc, row, best_v, best_i)) { best_v = acc; best_i = row; }
-        }
-    }
-    return true;
-}
-
-// Q8_0 LM head (Q8_0 tied embedding): row groups gw, gw + waves, ... with the
-// weights of the next group loaded while the current one is reduced.
-__device__ __forceinline__ bool lm_head_q8(const PersistentPlan &P, const uint64_t *x, uint32_t tag, int *status, unsigned char *lds,
-    double *red, float &best_v, int &best_i) {
-    constexpr int NREG = 8;  // hidden <= 1024
-    const Q8Matrix &w = P.out8;
-    const int tid = static_cast<int>(threadIdx.x);
-    const int lane = tid & 63, wave = tid >> 6, r = lane >> 3, l = lane & 7;
-    const int gw = static_cast<int>(blockIdx.x) * kW + wave, nw = static_cast<int>(gridDim.x) * kW;
-    const int chunks = w.chunks;
-    uint4 q[NREG];
-    uint2 sc[NREG];
-    auto fetch = [&](int rg) {
-        const uint4 *qp = w.quants + static_cast<size_t>(rg) * chunks * 64 + lane;
-        const uint2 *sp = w.scales + static_cast<size_t>(rg) * chunks * 8 + r;
-#pragma unroll
-        for (int c = 0; c < NREG; ++c)
-            if (c < chunks) { q[c] = load_stream(qp + static_cast<size_t>(c) * 64); sc[c] = load_stream(sp + static_cast<size_t>(c) * 8); }
-    };
-    if (gw < w.row_groups) fetch(gw);
-    uint32_t *aq = reinterpret_cast<uint32_t *>(lds);
-    float *as = reinterpret_cast<float *>(lds + static_cast<size_t>(chunks) * 128);
-    MvSrc src{};
-    if (!build_act<Pro::RMS>(x, nullptr, P.output_norm, P.hidden, 0, P.eps, tag, status, aq, as, red)) return false;
-    const uint4 *act4 = reinterpret_cast<const uint4 *>(aq);
-    const float4 *as4 = reinterpret_cast<const float4 *>(as);
-    for (int rg = gw; rg < w.row_groups; rg += nw) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NREG; ++c)
-            if (c < chunks) acc = dot_chunk(q[c], sc[c], act4[c * 8 + l], as4[c], acc);
-        if (rg + nw < w.row_groups) fetch(rg + nw);
-        acc = row_hsum8(acc);
-        const int row = rg * kRowsPerWave + r;
-        if (l == 0 && row < w.rows) {
-            P.logits[row] = acc;
-            if (better(acc, row, best_v, best_i)) { best_v = acc; best_i = row; }
-        }
-    }
-    (void)src;
-    return true;
-}
-
 // ------------------------------------------------------------------ kernel
 
-enum Op : int { EMBED, PROJ, GDN64, GDN128, GOUT, SHIFT, ATT, MERGE, AOUT, FFN1, FFN2, LM16F, LM16, LMQ8, DONE };
+enum Op : int { EMBED, PROJ, GDN64, GDN128, GOUT, NOP, ATT, MERGE, AOUT, FFN1, FFN2 };
 
-// The step as a flat list of phases; each case is inlined, so only the loop
-// state is live across phases.
-__global__ __launch_bounds__(kT) void decode_persistent_kernel(const PersistentPlan *__restrict__ plan) {
-    const PersistentPlan &P = *plan;
+// The layers of one step as a flat list of phases (each case inlined, so only
+// the loop state is live across phases).  The plan and the descriptor of the
+// current layer live in LDS: layer li + 1's descriptor is fetched into a
+// register while layer li runs and stored at its end.
+__global__ __launch_bounds__(kT) void decode_persistent_kernel(const PersistentPlan *__restrict__ plan,
+    const uint32_t tag) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ double red[kW];
-    __shared__ float sv[kW];
-    __shared__ int si[kW];
+    constexpr int kPlanWords = sizeof(PersistentPlan) / 4, kLayerWords = sizeof(PersistentLayer) / 4;
+    static_assert(kPlanWords <= kT && kLayerWords <= kT, "one word per thread");
+    __shared__ __align__(16) uint32_t s_plan_words[kPlanWords];
+    __shared__ __align__(16) uint32_t s_layer_words[2][kLayerWords];
+    PersistentPlan &s_plan = *reinterpret_cast<PersistentPlan *>(s_plan_words);
+    PersistentLayer *s_layer = reinterpret_cast<PersistentLayer *>(&s_layer_words[0][0]);
     const int tid = static_cast<int>(threadIdx.x);
+    if (tid < kPlanWords) reinterpret_cast<uint32_t *>(&s_plan)[tid] = reinterpret_cast<const uint32_t *>(plan)[tid];
+    if (tid < kLayerWords)
+        reinterpret_cast<uint32_t *>(&s_layer[0])[tid] = reinterpret_cast<const uint32_t *>(plan->layer)[tid];
+    __syncthreads();
+    const PersistentPlan &P = s_plan;
     int *status = P.status;
-    const uint32_t tag = *P.epoch + 1u;
     const int pos = *P.position;
     const int64_t token = *P.token;
     const int vocab_in = P.emb16 ? P.vocab : P.emb8.rows;
@@ -811,32 +711,33 @@ __global__ __launch_bounds__(kT) void decode_persistent_kernel(const PersistentP
         if (blockIdx.x == 0 && tid == 0) atomicOr(status, 2);
         return;
     }
-    float best_v = -__builtin_inff();
-    int best_i = 0x7fffffff;
-    const int ops = P.layers * 6 + 2;
+    const int ops = P.layers * 6 + 1;
+    if (tid == 0) { g_marks = P.phase_marks; g_mark_stride = ops + 1; }
+    __syncthreads();
+    uint32_t next_word = 0;
     for (int k = 0; k < ops; ++k) {
-        // op k: 0 embed; per layer 6 slots; then the LM head and DONE
-        int op, li = 0;
+        if (tid == 0) s_phase = k;
+        // op k: 0 embed; then 6 slots per layer
+        int op, li = 0, slot = 0;
         if (k == 0) {
             op = EMBED;
-        } else if (k == ops - 1) {
-            op = P.out16 ? (P.out_finite ? LM16F : LM16) : LMQ8;
         } else {
             li = (k - 1) / 6;
-            const int slot = (k - 1) % 6;
-            const bool rec = P.layer[li].recurrent != 0;
+            slot = (k - 1) % 6;
+            const bool rec = s_layer[li & 1].recurrent != 0;
             switch (slot) {
             case 0: op = PROJ; break;
             case 1: op = rec ? (P.head == 64 ? GDN64 : GDN128) : ATT; break;
             case 2: op = rec ? GOUT : MERGE; break;
-            case 3: op = rec ? SHIFT : AOUT; break;
+            case 3: op = rec ? NOP : AOUT; break;
             case 4: op = FFN1; break;
             default: op = FFN2; break;
             }
+            if (slot == 0 && li + 1 < P.layers && tid < kLayerWords)
+                next_word = reinterpret_cast<const uint32_t *>(P.layer + li + 1)[tid];
         }
-        if (tid == 0) s_phase = k;
-        const PersistentLayer &L = P.layer[li];
-        const uint64_t *xin = li == 0 ? P.ll_x0 : P.layer[li - 1].ll_x2;
+        const PersistentLayer &L = s_layer[li & 1];
+        const uint64_t *xin = li == 0 ? P.ll_x0 : s_layer[(li - 1) & 1].ll_x2;
         bool ok = true;
         switch (op) {
         case EMBED: embed_phase(P, token, tag); break;
@@ -855,7 +756,7 @@ __global__ __launch_bounds__(kT) void decode_persistent_kernel(const PersistentP
             ok = mv_phase<16, 1, Pro::GATED, Epi::ADD>(L.outp, mix, tag, status, lds, red);
             break;
         }
-        case SHIFT: ok = conv_shift(P, L, tag, status); break;
+        case NOP: break;  // the conv shift runs inside FFN1 of the recurrent layer
         case ATT: ok = wg_ok(att_scores_phase(P, L, pos, tag, status, lds)); break;
         case MERGE: ok = wg_ok(att_output_phase(P, L, pos, tag, status, lds)); break;
         case AOUT: {
@@ -868,44 +769,27 @@ __global__ __launch_bounds__(kT) void decode_persistent_kernel(const PersistentP
             MvSrc f1{};
             f1.x = L.ll_x1; f1.norm = L.post_norm; f1.width = P.hidden; f1.eps = P.eps;
             ok = mv_phase<8, 1, Pro::RMS, Epi::SILU>(L.ffn1, f1, tag, status, lds, red);
+            if (ok && L.recurrent) {
+                const int busy = (L.ffn1.first_rg[1] + kW - 1) / kW;  // workgroups with gate/up rows
+                const int G = static_cast<int>(gridDim.x);
+                ok = busy < G ? conv_shift(P, L, busy, G - busy, tag, status) : conv_shift(P, L, 0, G, tag, status);
+            }
             break;
         }
-        case FFN2: {
+        default: {
             MvSrc f2{};
             f2.x = L.ll_h; f2.resid = L.ll_x1; f2.width = P.ffn; f2.eps = P.eps;
-            ok = mv_phase<32, 1, Pro::F32, Epi::ADD>(L.ffn2, f2, tag, status, lds, red);
+            ok = mv_phase<28, 1, Pro::F32, Epi::ADD>(L.ffn2, f2, tag, status, lds, red);
             break;
         }
-        case LM16F: ok = lm_head_f16<true>(P, P.layer[P.layers - 1].ll_x2, tag, status, lds, red, best_v, best_i); break;
-        case LM16: ok = lm_head_f16<false>(P, P.layer[P.layers - 1].ll_x2, tag, status, lds, red, best_v, best_i); break;
-        default: ok = lm_head_q8(P, P.layer[P.layers - 1].ll_x2, tag, status, lds, red, best_v, best_i); break;
         }
         if (!ok) return;
+        if (slot == 5 && li + 1 < P.layers) {
+            __syncthreads();  // every thread is done with the old descriptor slot
+            if (tid < kLayerWords) reinterpret_cast<uint32_t *>(&s_layer[(li + 1) & 1])[tid] = next_word;
+            __syncthreads();
+        }
         if (P.phase_times && tid == 0) P.phase_times[static_cast<size_t>(blockIdx.x) * (ops + 1) + k] = wall_clock64();
-    }
-    wg_argmax(best_v, best_i, sv, si);
-    if (tid == 0) {
-        ll_put(P.ll_arg + 2 * blockIdx.x, __float_as_uint(best_v), tag);
-        ll_put(P.ll_arg + 2 * blockIdx.x + 1, static_cast<uint32_t>(best_i), tag);
-    }
-    if (blockIdx.x != 0) return;
-    // greedy maxloc over the workgroup partials; publish token, trace, position
-    // and the next tag for the following launch
-    int ix[2];
-    ix[0] = tid < static_cast<int>(gridDim.x) ? 2 * tid : -1;
-    ix[1] = tid < static_cast<int>(gridDim.x) ? 2 * tid + 1 : -1;
-    uint64_t v[2];
-    if (!wg_ok(ll_wait(P.ll_arg, ix, v, tag, status))) return;
-    float bv = ix[0] >= 0 ? ll_f(v[0]) : -__builtin_inff();
-    int bi = ix[0] >= 0 ? static_cast<int>(static_cast<uint32_t>(v[1])) : 0x7fffffff;
-    __syncthreads();
-    wg_argmax(bv, bi, sv, si);
-    if (tid == 0) {
-        if (P.phase_times) P.phase_times[static_cast<size_t>(blockIdx.x) * (ops + 1) + ops] = wall_clock64();
-        *P.token = bi;
-        if (P.trace && pos < P.trace_capacity) P.trace[pos] = bi;
-        *P.position = pos + 1;
-        *P.epoch = tag;
     }
 }
 
@@ -923,9 +807,8 @@ int persistent_blocks_per_cu() {
 const char *persistent_unsupported(const PersistentPlan &P, int grid) {
     if (grid <= 0 || grid > kT) return "grid must be 1..256 workgroups";
     if (P.hidden % 64 || P.hidden > 1024) return "hidden size must be a multiple of 64, at most 1024";
-    if (P.ffn % kQ8Block || P.ffn > 4096 || P.ffn / 8 > grid * kW) return "FFN width out of range";
+    if (P.ffn % kQ8Block || P.ffn > 3584 || P.ffn / 8 > grid * kW) return "FFN width out of range";
     if (P.hidden / 8 > grid * kW) return "hidden rows exceed one row group per wave";
-    if (P.out16 == nullptr && P.out8.row_groups <= 0) return "no LM head";
     if (sizeof(ScoreLds) > kLdsBytes) return "attention LDS";
     if (P.heads > 0 && P.max_context > 24 * kT) return "context longer than the persistent output phase holds";
     if (P.heads > 0 && (P.max_context + 8 + 2 * exact_attention::kDims * exact_attention::kRingPitch) * sizeof(float) >
@@ -953,8 +836,8 @@ const char *persistent_unsupported(const PersistentPlan &P, int grid) {
     return "";
 }
 
-hipError_t launch_decode_persistent(const PersistentPlan *plan_device, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL(decode_persistent_kernel, dim3(grid), dim3(kT), kLdsBytes, stream, plan_device);
+hipError_t launch_decode_persistent(const PersistentPlan *plan_device, uint32_t tag, int grid, hipStream_t stream) {
+    hipLaunchKernelGGL(decode_persistent_kernel, dim3(grid), dim3(kT), kLdsBytes, stream, plan_device, tag);
     return hipGetLastError();
 }
 

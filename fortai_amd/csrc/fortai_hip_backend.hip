@@ -108,7 +108,7 @@ struct fortai_hip_qwen35_decoder {
     uint64_t *arena = nullptr;               // tagged-word buffers of every phase
     PersistentLayer *layers_dev = nullptr;
     PersistentPlan *plan_dev = nullptr;
-    uint32_t *epoch = nullptr;
+    uint32_t next_tag = 1;                   // tag of the next persistent launch
     int *status = nullptr;
     uint64_t *phase_times = nullptr;  // FORTAI_HIP_PHASE_TIMES=1: per-workgroup phase end clocks
 };
@@ -1087,6 +1087,7 @@ const char *fortai_hip_q8_last_error(const fortai_hip_q8_context *c) {
 
 // ------------------------------------------------------------------ decoder
 namespace {
+hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream);
 hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     auto *c = d->context;
     hipError_t e = d->emb16 ? launch_f16_embedding(d->emb16->data, d->hidden, c->token, 0, d->x, stream)
@@ -1105,6 +1106,13 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
         e = enqueue_ffn(L.gate, L.up, L.down, in, Prologue::RMSNORM, d->h_q8l, d->x, d->x, stream);
     }
     if (e != hipSuccess) return e;
+    return enqueue_lm_head(d, stream);
+}
+// final RMSNorm + LM head + greedy argmax from d->x; advances token, trace
+// and position for the next step
+hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
+    auto *c = d->context;
+    hipError_t e = hipSuccess;
     ArgmaxState st;
     st.partial_value = d->argmax_value;
     st.partial_index = d->argmax_index;
@@ -1126,7 +1134,10 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
     return e;
 }
 hipError_t run_step(fortai_hip_qwen35_decoder *d) {
-    if (d->persistent) return launch_decode_persistent(d->plan_dev, d->grid, d->context->stream);
+    if (d->persistent) {
+        hipError_t e = launch_decode_persistent(d->plan_dev, d->next_tag++, d->grid, d->context->stream);
+        return e == hipSuccess ? enqueue_lm_head(d, d->context->stream) : e;
+    }
     return d->use_graph ? hipGraphLaunch(d->exec, d->context->stream) : enqueue_decoder_step(d, d->context->stream);
 }
 // after a synchronisation: a failed persistent step (a bounded wait expired)
@@ -1151,10 +1162,12 @@ int persistent_status(fortai_hip_qwen35_decoder *d) {
 }
 }  // namespace
 
+extern "C++" {
 namespace {
 PersistentMatvec persistent_matvec(std::initializer_list<std::pair<const fortai_hip_q8_weights *, uint64_t *>> segs) {
     PersistentMatvec m{};
     m.count = 0;
+    m.plain = nullptr;
     m.first_rg[0] = 0;
     for (const auto &sgm : segs) {
         m.w[m.count] = sgm.first->m;
@@ -1203,9 +1216,6 @@ std::string setup_persistent(fortai_hip_qwen35_decoder *d) {
     }
     P.emb16 = d->emb16 ? d->emb16->data : nullptr;
     if (d->emb8) P.emb8 = d->emb8->m;
-    P.out16 = d->out16 ? d->out16->data : nullptr;
-    if (d->out8) P.out8 = d->out8->m;
-    P.out_finite = d->out16 ? (d->out16->finite ? 1 : 0) : 0;
     const char *why = persistent_unsupported(P, grid);
     if (*why) return why;
     for (auto &L : d->layers) {  // projections: at most two row groups per wave
@@ -1217,7 +1227,7 @@ std::string setup_persistent(fortai_hip_qwen35_decoder *d) {
     }
     if (d->out16 && d->hidden % 64) return "LM head width";
 
-    // tagged-word arena: x0, then per layer proj | mid | ao | x1 | h | x2, then the argmax partials
+    // tagged-word arena: x0, then per layer proj | mid | ao | x1 | h | x2
     size_t words = static_cast<size_t>(d->hidden);
     std::vector<size_t> offs;
     for (auto &L : d->layers) {
@@ -1233,12 +1243,8 @@ std::string setup_persistent(fortai_hip_qwen35_decoder *d) {
         offs.push_back(words);
         words += proj + mid + ao + 2 * static_cast<size_t>(d->hidden) + d->ffn;
     }
-    const size_t arg_off = words;
-    words += 2 * static_cast<size_t>(grid);
     hipError_t e = alloc(&d->arena, words);
     if (e == hipSuccess) e = hipMemsetAsync(d->arena, 0, words * sizeof(uint64_t), c->stream);
-    if (e == hipSuccess) e = alloc(&d->epoch, 1);
-    if (e == hipSuccess) e = hipMemsetAsync(d->epoch, 0, sizeof(uint32_t), c->stream);
     if (e == hipSuccess) e = alloc(&d->status, 8 + 2 * 256);
     if (e == hipSuccess) e = hipMemsetAsync(d->status, 0, (8 + 2 * 256) * sizeof(int), c->stream);
     if (e != hipSuccess) return "allocation";
@@ -1278,23 +1284,20 @@ std::string setup_persistent(fortai_hip_qwen35_decoder *d) {
         H.ll_x2 = H.ll_h + d->ffn;
         H.ffn1 = persistent_matvec({{L.gate, H.ll_h}, {L.up, nullptr}});
         H.ffn2 = persistent_matvec({{L.down, H.ll_x2}});
+        if (i + 1 == d->layers.size()) H.ffn2.plain = d->x;  // the LM head's input
     }
-    P.output_norm = d->output_norm;
-    P.logits = d->logits;
     P.ll_x0 = d->arena;
-    P.ll_arg = d->arena + arg_off;
     P.token = c->token;
-    P.trace = d->trace;
     P.position = c->position;
-    P.trace_capacity = d->max_context;
-    P.epoch = d->epoch;
     P.status = d->status;
     const char *times_env = std::getenv("FORTAI_HIP_PHASE_TIMES");
-    if (times_env && std::strcmp(times_env, "1") == 0) {
-        const size_t n = static_cast<size_t>(grid) * (P.layers * 6 + 3);
-        if (alloc(&d->phase_times, n) != hipSuccess) return "allocation";
-        (void)hipMemsetAsync(d->phase_times, 0, n * sizeof(uint64_t), c->stream);
+    if (times_env && (std::strcmp(times_env, "1") == 0 || std::strcmp(times_env, "2") == 0)) {
+        const size_t n = static_cast<size_t>(grid) * (P.layers * 6 + 2);
+        const size_t n_all = times_env[0] == '2' ? 5 * n : n;  // times, then 4 marks per phase
+        if (alloc(&d->phase_times, n_all) != hipSuccess) return "allocation";
+        (void)hipMemsetAsync(d->phase_times, 0, n_all * sizeof(uint64_t), c->stream);
         P.phase_times = d->phase_times;
+        if (times_env[0] == '2') P.phase_marks = d->phase_times + n;
     }
     e = hipMalloc(reinterpret_cast<void **>(&d->layers_dev), host.size() * sizeof(PersistentLayer));
     if (e == hipSuccess)
@@ -1310,6 +1313,7 @@ std::string setup_persistent(fortai_hip_qwen35_decoder *d) {
     return "";
 }
 }  // namespace
+}  // extern "C++"
 
 int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     fortai_hip_qwen35_recurrent *const *recurrent, fortai_hip_qwen35_attention *const *attention,
@@ -1410,7 +1414,7 @@ int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *d) {
     }
     release(d->output_norm); release(d->x); release(d->logits); release(d->argmax_value);
     release(d->argmax_index); release(d->trace);
-    release(d->arena); release(d->layers_dev); release(d->plan_dev); release(d->epoch); release(d->status);
+    release(d->arena); release(d->layers_dev); release(d->plan_dev); release(d->status);
     release(d->phase_times);
     if (d->h_q8l) (void)hipFree(d->h_q8l);
     delete d;
@@ -1501,7 +1505,9 @@ int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *d) {
 
 int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *d, uint64_t *host_times, size_t count) {
     if (!d || !host_times || !d->phase_times) return FORTAI_HIP_INVALID;
-    const size_t n = static_cast<size_t>(d->grid) * (d->layers.size() * 6 + 3);
+    size_t n = static_cast<size_t>(d->grid) * (d->layers.size() * 6 + 2);
+    const char *times_env = std::getenv("FORTAI_HIP_PHASE_TIMES");
+    if (times_env && times_env[0] == '2' && count >= 5 * n) n *= 5;  // marks follow the times
     if (count < n) return FORTAI_HIP_INVALID;
     auto *c = d->context;
     (void)hipSetDevice(c->device);

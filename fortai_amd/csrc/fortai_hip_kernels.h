@@ -160,6 +160,7 @@ struct PersistentMatvec {
     uint64_t *out[4];           // tagged output words, one per row
     int first_rg[5];            // cumulative row-group offsets of the segments
     int count;
+    float *plain;               // optional plain fp32 copy of the outputs (read after the launch)
 };
 struct PersistentLayer {
     int recurrent;              // 1 Gated DeltaNet, 0 full attention
@@ -186,25 +187,20 @@ struct PersistentPlan {
     int heads, kv_heads, head_dim, value_dim, rope_dim;            // attention
     const uint16_t *emb16;
     Q8Matrix emb8;
-    const uint16_t *out16;
-    Q8Matrix out8;
-    int out_finite;
-    const float *output_norm;
-    float *logits;
     uint64_t *ll_x0;            // embedding row [hidden]
-    uint64_t *ll_arg;           // per-workgroup argmax partials [grid][2]
-    int64_t *token, *trace;
-    int *position;
-    int trace_capacity;
-    uint32_t *epoch;            // tokens decoded by this plan (tag = epoch + 1)
+    const int64_t *token;
+    const int *position;
     int *status;                // non-zero: a wait timed out (every workgroup has exited)
     uint64_t *phase_times;      // optional [grid][phases]: realtime clock at the end of each phase
+    uint64_t *phase_marks;      // optional [grid][phases][4]: matvec phases' internal marks
     const PersistentLayer *layer;  // device array [layers]
 };
-// Launch one decode step on `grid` workgroups (one per CU; all must be
-// co-resident); the plan lives in device memory.  persistent_lds_bytes() is
-// the dynamic LDS of a workgroup.
-hipError_t launch_decode_persistent(const PersistentPlan *plan_device, int grid, hipStream_t stream);
+// Launch the layers of one decode step on `grid` workgroups (one per CU; all
+// must be co-resident); the plan lives in device memory.  The last layer's
+// residual is left in plain fp32 (ffn2.plain of the last layer) for the LM
+// head, which runs as its own kernels.  persistent_lds_bytes() is the
+// dynamic LDS of a workgroup.
+hipError_t launch_decode_persistent(const PersistentPlan *plan_device, uint32_t tag, int grid, hipStream_t stream);
 size_t persistent_lds_bytes();
 int persistent_blocks_per_cu();
 // Shape limits of the persistent path ("" when supported, else the reason).

@@ -274,8 +274,8 @@ int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *decoder);
  * the captured per-op graph (FORTAI_HIP_DECODER=graph|persistent selects) */
 int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *decoder);
 /* with FORTAI_HIP_PHASE_TIMES=1 at create: the device realtime clock (100 MHz)
- * at the end of every phase of the last persistent step, [workgroup][phase],
- * phases = 6 * layers + 3 (embed, 6 per layer, LM head, final argmax) */
+ * at the end of every phase of the last persistent step, [workgroup][slot],
+ * slots = 6 * layers + 2 (embed, 6 per layer, one unused) */
 int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *decoder, uint64_t *host_times,
     size_t count);
 /* device pointer of the decoder's logits [vocab] */
