@@ -5,7 +5,7 @@
 //
 // Two kernels: scores (one workgroup per kv head x 64 positions; the one
 // that holds the new position also appends it) and output (one workgroup per
-// head x 16 value dims: softmax weights, the P.V chains and the sigmoid gate).
+// head x 8 value dims: softmax weights, the P.V chains and the sigmoid gate).
 #include "attention_exact.h"
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
@@ -110,23 +110,23 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * ea::kDims;
     const int kvh = h / group;
     float *sw = lds;
-    float *red = sw + p.max_context;
-    float *ring = red + 8;
+    float *work = sw + ea::sw_floats(p.max_context);
     const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
     for (int i = tid; i < positions; i += ea::kThreads) sw[i] = sc[i];
     const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
     const int flag = p.cache_flags[kvh];
-    __syncthreads();
-    ea::softmax_weights(sw, positions, red);
     const uint16_t *vbase = p.vcache + static_cast<size_t>(kvh) * VD + d0;
     const size_t vstride = static_cast<size_t>(NKV) * VD;
-    const float acc = flag == 0 ? ea::pv_chains<true>(sw, positions, vbase, vstride, ring)
-                                : ea::pv_chains<false>(sw, positions, vbase, vstride, ring);
+    ea::ValuePieces v;
+    ea::value_prefetch(vbase, vstride, positions, v);
+    __syncthreads();
+    const float acc = flag == 0 ? ea::attend<true>(sw, positions, vbase, vstride, work, v)
+                                : ea::attend<false>(sw, positions, vbase, vstride, work, v);
     if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * sigmoid_ref(gate);
 }
 
 size_t output_lds_bytes(int max_context) {
-    return (static_cast<size_t>(max_context) + 8 + 2 * ea::kDims * ea::kRingPitch) * sizeof(float);
+    return ea::output_lds_floats(max_context) * sizeof(float);
 }
 
 }  // namespace

@@ -8,20 +8,21 @@
 // Q8_0, so a one-ulp change of an output flips an int8 now and then and the
 // trace drifts.  The parallel parts (the score of each position, e_p, e_p/Z,
 // every product) run on many lanes; only the left-to-right sums are chains.
-// The P.V chains are fed by producer waves through an LDS ring, so the chain
-// lane issues one add per position.
+// The chains run from registers, handed from wave to wave (attend below).
 #pragma once
 
 #include "fortai_hip_internal.h"
+
+#ifndef FORTAI_ATT_MARK
+#define FORTAI_ATT_MARK(i)
+#endif
 
 namespace fortai_hip {
 namespace exact_attention {
 
 constexpr int kThreads = 256;
 constexpr int kPosBlock = 64;   // positions per score unit
-constexpr int kDims = 16;       // value dims per output unit
-constexpr int kRing = 128;      // positions per ring block
-constexpr int kRingPitch = kRing + 4;
+constexpr int kDims = 8;        // value dims per output unit
 
 template <bool FINITE>
 __device__ __forceinline__ float kv(uint16_t h) { return FINITE ? half_bits_to_float(h) : gguf_half_to_real(h); }
@@ -67,140 +68,216 @@ __device__ __forceinline__ float score(const float *q, const uint16_t *krow, int
     return acc / sqrt_head;
 }
 
-// s[0..n) (LDS, the scores of one head) -> w[p] = expf(s_p - max) / Z in
-// place, with Z summed left to right by one lane (fortai_qwen35_cpu.f90:
-// 1016-1020).  red: >= 8 floats of LDS.  All threads of the block call it.
-__device__ __forceinline__ void softmax_weights(float *s, int n, float *red) {
-    const int tid = static_cast<int>(threadIdx.x);
-    float m = -3.402823466e38f;  // -huge(1.0_real32)
-    for (int p = tid; p < n; p += kThreads) m = fmaxf(m, s[p]);
-    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = tid; p < n; p += kThreads) s[p] = expf_libm(s[p] - m);
-    __syncthreads();
-    if (tid == 0) {
-        // left-to-right sum; LDS reads are issued a batch ahead of the adds
-        float z = 0.0f;
-        int p = 0;
-        float4 cur[8];
-        const int full = n / 32;
-        if (full > 0) {
+// ------------------------------------------------------------ fp32 chains
+// A left-to-right fp32 sum is a chain of dependent adds: one add issues every
+// ~4.7 cycles on gfx950, and any other instruction of the summing wave takes
+// an issue slot from the chain.  So a chain is cut into segments of kSeg
+// positions that the four waves take in turn: segment k is summed by wave
+// k % 4 from registers only, while the other three waves compute the values
+// of their next segments (expf, or e/Z times the value row) and load them into
+// their registers.  The running sum passes from wave to wave through a tagged
+// 64-bit LDS word per chain (tag = index of the segment it starts).
+
+constexpr int kWaves = kThreads / 64;
+constexpr int kSeg = 256;            // positions per chain segment
+constexpr int kSegVec = kSeg / 4;    // 16-byte registers per lane per segment
+constexpr int kStagePitch = kSeg + 4;
+constexpr int kTurnSpin = 1 << 22;   // polls of a handoff word before giving up
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+
+// A segment's values into registers.  The reads are ordinary loads, so the
+// compiler tracks them; seg_held() then makes the compiler complete them at
+// that point (an empty asm that uses every value), before the wave waits for
+// its turn, instead of sinking each read next to its first add inside the
+// chain.
+__device__ __forceinline__ void seg_read(f4 (&r)[kSegVec], const float *src) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) cur[k] = *reinterpret_cast<const float4 *>(s + 4 * k);
-        }
-        for (int b = 0; b < full; ++b, p += 32) {
-            float4 nxt[8];
-            if (b + 1 < full) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) nxt[k] = *reinterpret_cast<const float4 *>(s + p + 32 + 4 * k);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                z = z + cur[k].x;
-                z = z + cur[k].y;
-                z = z + cur[k].z;
-                z = z + cur[k].w;
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) cur[k] = nxt[k];
-        }
-        for (; p < n; ++p) z = z + s[p];
-        red[4] = z;
-    }
-    __syncthreads();
-    const float z = red[4];
-    for (int p = tid; p < n; p += kThreads) s[p] = s[p] / z;
-    __syncthreads();
+    for (int c = 0; c < kSegVec; ++c) r[c] = *reinterpret_cast<const f4 *>(src + 4 * c);
 }
 
-// out_j = sum_p w_p * v_p,j left to right for kDims consecutive value dims:
-// lanes 0..kDims-1 of wave 0 run the chains; waves 1..3 write the products
-// fl(w_p * v_p,j) into a double-buffered LDS ring [dim][position], with the
-// value rows of the next kPrefetch blocks already in their registers (the
-// chains need ~0.2 us per block, a row fetch ~1-2 us).  The value row of
-// position p starts at vbase + p * vstride (fp16 bits, kDims contiguous).
-// The result is valid in threads 0..kDims-1.  ring: 2 * kDims * kRingPitch.
-constexpr int kPrefetch = 8;
-constexpr int kSegs = kRing * kDims / 8;                 // 16-byte value pieces per block
-constexpr int kSegsPerProducer = (kSegs + kThreads - 65) / (kThreads - 64);
+template <int C>
+__device__ __forceinline__ void seg_held(f4 (&r)[kSegVec]) {
+    if constexpr (C < kSegVec) {
+        asm volatile(""
+                     : "+v"(r[C]), "+v"(r[C + 1]), "+v"(r[C + 2]), "+v"(r[C + 3]), "+v"(r[C + 4]), "+v"(r[C + 5]),
+                       "+v"(r[C + 6]), "+v"(r[C + 7]), "+v"(r[C + 8]), "+v"(r[C + 9]), "+v"(r[C + 10]),
+                       "+v"(r[C + 11]), "+v"(r[C + 12]), "+v"(r[C + 13]), "+v"(r[C + 14]), "+v"(r[C + 15]));
+        seg_held<C + 16>(r);
+    }
+}
 
-template <bool FINITE>
-__device__ __forceinline__ void pv_fetch(const uint16_t *vbase, size_t vstride, int n, int b, int ptid,
-    uint4 (&dst)[kSegsPerProducer]) {
+// acc + r[0].x + r[0].y + ..., left to right, over the first cnt values
+// rounded up to 16.  The values past cnt are -0.0f, which leaves any sum as
+// it is (x + -0 = x for every x), so a partial segment needs no guards.
+__device__ __forceinline__ float seg_chain(const f4 (&r)[kSegVec], int cnt, float acc) {
+    if (cnt >= kSeg) {
 #pragma unroll
-    for (int i = 0; i < kSegsPerProducer; ++i) {
-        const int c = ptid + i * (kThreads - 64);
-        const int p = b * kRing + c / 2;
-        dst[i] = (c < kSegs && p < n)
-                     ? *reinterpret_cast<const uint4 *>(vbase + static_cast<size_t>(p) * vstride + (c & 1) * 8)
+        for (int i = 0; i < kSegVec; ++i) {
+            acc = acc + r[i].x;
+            acc = acc + r[i].y;
+            acc = acc + r[i].z;
+            acc = acc + r[i].w;
+        }
+        return acc;
+    }
+#pragma unroll
+    for (int c = 0; c < kSegVec; c += 4) {
+        if (4 * c < cnt) {
+#pragma unroll
+            for (int i = c; i < c + 4; ++i) {
+                acc = acc + r[i].x;
+                acc = acc + r[i].y;
+                acc = acc + r[i].z;
+                acc = acc + r[i].w;
+            }
+        }
+    }
+    return acc;
+}
+
+// The running sum entering segment k (0 for k = 0), from the chain's handoff
+// word.  Only this workgroup writes the word, and every wave of it is
+// resident, so the wait ends; the bound only guards against a broken caller.
+__device__ __forceinline__ float take_turn(const uint64_t *word, int k) {
+    if (k == 0) return 0.0f;
+    uint64_t w;
+    int spins = 0;
+    do {
+        w = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } while (static_cast<int>(w >> 32) != k && ++spins < kTurnSpin);
+    return __uint_as_float(static_cast<uint32_t>(w));
+}
+
+__device__ __forceinline__ void pass_turn(uint64_t *word, int k_next, float acc) {
+    __hip_atomic_store(word, (static_cast<uint64_t>(k_next) << 32) | __float_as_uint(acc), __ATOMIC_RELAXED,
+        __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// LDS of the output step, in floats: scores/weights sw[max_context rounded up
+// to kSeg], then 8 reduction slots, kDims handoff words, and one stage of
+// kDims x kSeg products per wave.
+__host__ __device__ constexpr size_t sw_floats(int max_context) {
+    return static_cast<size_t>((max_context + kSeg - 1) / kSeg * kSeg);
+}
+__host__ __device__ constexpr size_t output_lds_floats(int max_context) {
+    return sw_floats(max_context) + 8 + 2 * kDims + static_cast<size_t>(kWaves) * kDims * kStagePitch;
+}
+
+// The value pieces (kDims fp16 = 16 bytes) a lane multiplies for its wave's
+// first segment: positions wave*kSeg + lane + 64 i.
+constexpr int kPieces = kSeg / 64;
+typedef uint4 ValuePieces[kPieces];
+
+__device__ __forceinline__ void value_fetch(const uint16_t *vbase, size_t vstride, int n, int k, ValuePieces &v) {
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+        const int p = k * kSeg + lane + 64 * i;
+        v[i] = p < n ? *reinterpret_cast<const uint4 *>(vbase + static_cast<size_t>(p) * vstride)
                      : make_uint4(0u, 0u, 0u, 0u);
     }
 }
 
+__device__ __forceinline__ void value_prefetch(const uint16_t *vbase, size_t vstride, int n, ValuePieces &v) {
+    value_fetch(vbase, vstride, n, static_cast<int>(threadIdx.x) >> 6, v);
+}
+
+// Softmax weights and P.V of kDims value dims over n positions
+// (fortai_qwen35_cpu.f90:1016-1029):
+//   m = max_p s_p;  e_p = expf(s_p - m);  Z = e_0 + e_1 + ... (left to right)
+//   out_j = (e_0/Z) v_0,j + (e_1/Z) v_1,j + ... (left to right, each product
+//   rounded).
+// sw: the n scores (LDS, sw_floats(max_context) floats); work: the rest of
+// output_lds_floats.  The value row of position p starts at vbase + p *
+// vstride (fp16 bits, kDims contiguous); v: value_prefetch of it.  All threads
+// call it; the result is valid in threads 0..kDims-1.
 template <bool FINITE>
-__device__ __forceinline__ float pv_chains(const float *w, int n, const uint16_t *vbase, size_t vstride,
-    float *ring) {
-    static_assert(kDims == 16, "two 16-byte pieces per position");
-    const int tid = static_cast<int>(threadIdx.x);
-    const int blocks = (n + kRing - 1) / kRing;
-    const int ptid = tid - 64;
-    uint4 pre[kPrefetch][kSegsPerProducer];
-    if (tid >= 64) {
+__device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase, size_t vstride, float *work,
+    ValuePieces &v) {
+    static_assert(kDims == 8, "one 16-byte value piece per position");
+    const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+    float *red = work;
+    uint64_t *hand = reinterpret_cast<uint64_t *>(work + 8);
+    float *stage = work + 8 + 2 * kDims + wave * kDims * kStagePitch;
+    const int nseg = (n + kSeg - 1) / kSeg;
+    if (tid < kDims) hand[tid] = 0;
+
+    // max (any order gives the same value)
+    constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
+    constexpr int kUnroll = 8;
+    float m = kLowest;
+    for (int p0 = tid; p0 < n; p0 += kThreads * kUnroll) {
+        float x[kUnroll];
 #pragma unroll
-        for (int k = 0; k < kPrefetch; ++k)
-            if (k < blocks) pv_fetch<FINITE>(vbase, vstride, n, k, ptid, pre[k]);
+        for (int k = 0; k < kUnroll; ++k) x[k] = p0 + k * kThreads < n ? sw[p0 + k * kThreads] : kLowest;
+#pragma unroll
+        for (int k = 0; k < kUnroll; ++k) m = fmaxf(m, x[k]);
     }
-    auto produce = [&](int b, const uint4 (&vr)[kSegsPerProducer], float *buf) {
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    FORTAI_ATT_MARK(1);
+
+    // Z: each wave turns its segments' scores into e_p (kept in sw for the
+    // weights) and sums them when its turn comes
+    f4 r[kSegVec];
+    for (int k = wave; k < nseg; k += kWaves) {
+        const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
 #pragma unroll
-        for (int i = 0; i < kSegsPerProducer; ++i) {
-            const int c = ptid + i * (kThreads - 64);
-            const int j = c / 2, d0 = (c & 1) * 8;
-            const int p = b * kRing + j;
-            if (c < kSegs && p < n) {
-                const float wp = w[p];
-                const uint32_t hw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+        for (int i = 0; i < kPieces; ++i) {
+            const int p = p0 + lane + 64 * i;
+            sw[p] = p < n ? expf_libm(sw[p] - m) : -0.0f;
+        }
+        seg_read(r, sw + p0);
+        seg_held<0>(r);
+        float acc = take_turn(hand, k);
+        acc = seg_chain(r, cnt, acc);
+        if (lane == 0) pass_turn(hand, k + 1, acc);
+    }
+    __syncthreads();
+    const float z = __uint_as_float(static_cast<uint32_t>(hand[0]));
+    FORTAI_ATT_MARK(2);
+    __syncthreads();
+    if (tid < kDims) hand[tid] = 0;
+    __syncthreads();
+
+    // P.V: each wave writes its segment's products fl(fl(e_p/Z) v_p,j) to its
+    // stage [dim][position], fetches the value pieces of its next segment, and
+    // lanes 0..kDims-1 sum their dim's row when the turn comes
+    float acc = 0.0f;
+    for (int k = wave; k < nseg; k += kWaves) {
+        const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+            const int j = lane + 64 * i, p = p0 + j;
+            if (p < n) {
+                const float wp = sw[p] / z;
+                const uint32_t hw[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    buf[(d0 + 2 * q) * kRingPitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] & 0xffffu));
-                    buf[(d0 + 2 * q + 1) * kRingPitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] >> 16));
+                    stage[(2 * q) * kStagePitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] & 0xffffu));
+                    stage[(2 * q + 1) * kStagePitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] >> 16));
                 }
+            } else {
+#pragma unroll
+                for (int d = 0; d < kDims; ++d) stage[d * kStagePitch + j] = -0.0f;
             }
         }
-    };
-    if (tid >= 64) produce(0, pre[0], ring);
-    __syncthreads();
-    float acc = 0.0f;
-    for (int b0 = 0; b0 < blocks; b0 += kPrefetch) {
-#pragma unroll
-        for (int s = 0; s < kPrefetch; ++s) {
-            const int b = b0 + s;
-            if (b >= blocks) break;
-            float *cur = ring + (b & 1) * kDims * kRingPitch;
-            if (tid >= 64) {
-                // slot s now feeds block b + kPrefetch; block b + 1 comes from slot s + 1
-                if (b + kPrefetch < blocks) pv_fetch<FINITE>(vbase, vstride, n, b + kPrefetch, ptid, pre[s]);
-                if (b + 1 < blocks) produce(b + 1, pre[(s + 1) % kPrefetch], ring + ((b + 1) & 1) * kDims * kRingPitch);
-            } else if (tid < kDims) {
-                const float *t = cur + tid * kRingPitch;
-                const int cnt = min(kRing, n - b * kRing);
-                int j = 0;
-                for (; j + 16 <= cnt; j += 16) {
-                    const float4 a0 = *reinterpret_cast<const float4 *>(t + j);
-                    const float4 a1 = *reinterpret_cast<const float4 *>(t + j + 4);
-                    const float4 a2 = *reinterpret_cast<const float4 *>(t + j + 8);
-                    const float4 a3 = *reinterpret_cast<const float4 *>(t + j + 12);
-                    acc = acc + a0.x; acc = acc + a0.y; acc = acc + a0.z; acc = acc + a0.w;
-                    acc = acc + a1.x; acc = acc + a1.y; acc = acc + a1.z; acc = acc + a1.w;
-                    acc = acc + a2.x; acc = acc + a2.y; acc = acc + a2.z; acc = acc + a2.w;
-                    acc = acc + a3.x; acc = acc + a3.y; acc = acc + a3.z; acc = acc + a3.w;
-                }
-                for (; j < cnt; ++j) acc = acc + t[j];
-            }
-            __syncthreads();
+        if (k + kWaves < nseg) value_fetch(vbase, vstride, n, k + kWaves, v);
+        if (lane < kDims) {
+            seg_read(r, stage + lane * kStagePitch);
+            seg_held<0>(r);
+            float a = take_turn(hand + lane, k);
+            a = seg_chain(r, cnt, a);
+            pass_turn(hand + lane, k + 1, a);
         }
     }
+    __syncthreads();
+    if (tid < kDims) acc = __uint_as_float(static_cast<uint32_t>(hand[tid]));
+    __syncthreads();  // hand and stage are free again when this returns
     return acc;
 }
 

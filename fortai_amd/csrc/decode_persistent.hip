@@ -30,6 +30,13 @@
 // practice) and attention is split over chunks with an online softmax.
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
+
+namespace fortai_hip {
+namespace {
+__device__ __forceinline__ void mark(int i);
+}
+}  // namespace fortai_hip
+#define FORTAI_ATT_MARK(i) mark(i)
 #include "attention_exact.h"
 
 namespace fortai_hip {
@@ -636,7 +643,7 @@ __device__ __forceinline__ bool att_scores_phase(const PersistentPlan &P, const 
     return true;
 }
 
-// Softmax weights and the P.V chains of one head x 16 value dims
+// Softmax weights and the P.V chains of one head x 8 value dims
 // (exact_attention::softmax_weights / pv_chains), then the sigmoid gate
 // (fortai_qwen35_cpu.f90:1030-1031).
 __device__ __forceinline__ bool att_output_phase(const PersistentPlan &P, const PersistentLayer &L, int pos,
@@ -645,9 +652,8 @@ __device__ __forceinline__ bool att_output_phase(const PersistentPlan &P, const 
     const int slices = VD / ea::kDims, units = NH * slices;
     const int positions = pos + 1;
     const int tid = static_cast<int>(threadIdx.x);
-    float *sw = reinterpret_cast<float *>(lds);                        // [max_context]
-    float *red = sw + P.max_context;                                    // [8]
-    float *ring = red + 8;                                              // [2][kDims][kRingPitch]
+    float *sw = reinterpret_cast<float *>(lds);
+    float *work = sw + ea::sw_floats(P.max_context);
     for (int u = static_cast<int>(blockIdx.x); u < units; u += static_cast<int>(gridDim.x)) {
         const int h = u / slices, d0 = (u % slices) * ea::kDims, kvh = h / group;
         constexpr int N = 24;  // positions <= 6144
@@ -667,12 +673,15 @@ __device__ __forceinline__ bool att_output_phase(const PersistentPlan &P, const 
         for (int k = 0; k < N; ++k)
             if (ix[k] >= 0) sw[tid + k * kT] = ll_f(v[k]);
         const int flag = __hip_atomic_load(L.cache_flags + kvh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        ea::softmax_weights(sw, positions, red);
         const uint16_t *vbase = L.vcache + static_cast<size_t>(kvh) * VD + d0;
         const size_t vstride = static_cast<size_t>(NKV) * VD;
-        const float acc = flag == 0 ? ea::pv_chains<true>(sw, positions, vbase, vstride, ring)
-                                    : ea::pv_chains<false>(sw, positions, vbase, vstride, ring);
+        ea::ValuePieces vp;
+        ea::value_prefetch(vbase, vstride, positions, vp);
+        __syncthreads();
+        mark(0);
+        const float acc = flag == 0 ? ea::attend<true>(sw, positions, vbase, vstride, work, vp)
+                                    : ea::attend<false>(sw, positions, vbase, vstride, work, vp);
+        mark(3);
         if (tid < ea::kDims) ll_putf(L.ll_ao + h * VD + d0 + tid, acc * sigmoid_ref(ll_f(gv[0])), tag);
         __syncthreads();
     }
@@ -811,8 +820,7 @@ const char *persistent_unsupported(const PersistentPlan &P, int grid) {
     if (P.hidden / 8 > grid * kW) return "hidden rows exceed one row group per wave";
     if (sizeof(ScoreLds) > kLdsBytes) return "attention LDS";
     if (P.heads > 0 && P.max_context > 24 * kT) return "context longer than the persistent output phase holds";
-    if (P.heads > 0 && (P.max_context + 8 + 2 * exact_attention::kDims * exact_attention::kRingPitch) * sizeof(float) >
-                           kLdsBytes)
+    if (P.heads > 0 && exact_attention::output_lds_floats(P.max_context) * sizeof(float) > kLdsBytes)
         return "attention output LDS";
     for (int li = 0; li < P.layers; ++li) {
         (void)li;
