@@ -223,15 +223,20 @@ __device__ __forceinline__ uint32_t quantize_group(float4 y, float &scale_out, u
 
 // One 16-byte Q8L chunk (4 blocks) of a row lane: the reference's per-block
 // acc = fma(f32(w_scale) * a_scale, (float)dot4(w, a), acc), block by block.
+// sum of the four int8 products of a and b
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), 0, false);
+}
+
 __device__ __forceinline__ float dot_chunk(uint4 q, uint2 sc, uint4 a, float4 as, float acc) {
     acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.x), static_cast<int>(a.x), 0, false)), acc);
+        static_cast<float>(sdot4(q.x, a.x)), acc);
     acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.y), static_cast<int>(a.y), 0, false)), acc);
+        static_cast<float>(sdot4(q.y, a.y)), acc);
     acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.z), static_cast<int>(a.z), 0, false)), acc);
+        static_cast<float>(sdot4(q.z, a.z)), acc);
     acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w,
-        static_cast<float>(__builtin_amdgcn_sdot4(static_cast<int>(q.w), static_cast<int>(a.w), 0, false)), acc);
+        static_cast<float>(sdot4(q.w, a.w)), acc);
     return acc;
 }
 

@@ -27,6 +27,10 @@
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
 
+#ifndef FORTAI_MV_MARK
+#define FORTAI_MV_MARK(i)
+#endif
+
 namespace fortai_hip {
 
 namespace {
@@ -47,16 +51,64 @@ __device__ __forceinline__ uint32_t load_u32_unaligned(const int8_t *p) {
 }
 
 // Build the workgroup's LDS copy of the quantized activation (Q8L layout).
+// The activation of a matvec is read before the weights, into registers
+// (act_fetch), and stored to LDS after the weight loads are issued
+// (act_store): the compiler's in-order vmcnt waits for the activation then do
+// not wait for the weights.
+constexpr int kMaxChunks = 96;  // Q8L activations up to 12288 wide
+
 template <int THREADS, Prologue PRO>
-__device__ __forceinline__ void build_activation(const MatvecInput &in, int chunks, uint32_t *act32,
-    float *act_s, double *red) {
+struct ActShape {
+    static constexpr int kQ8L = (kMaxChunks * 9 + THREADS - 1) / THREADS;  // 16-byte pieces per thread
+    static constexpr int kPre = 8;                                          // float4 groups per thread
+    static constexpr int kQ = PRO == Prologue::Q8L ? kQ8L : 1;
+    static constexpr int kX = PRO == Prologue::F32 || PRO == Prologue::RMSNORM ? kPre : 1;
+    static constexpr int kW = PRO == Prologue::RMSNORM ? kPre : 1;
+};
+
+template <int THREADS, Prologue PRO, int NQ, int NX, int NW>
+__device__ __forceinline__ void act_fetch(const MatvecInput &in, int chunks, u32x4_t (&q8l)[NQ], float4 (&xr)[NX],
+    float4 (&wr)[NW]) {
+    using A = ActShape<THREADS, PRO>;
+    const int tid = static_cast<int>(threadIdx.x);
+    if constexpr (PRO == Prologue::Q8L) {
+        const u32x4_t *src = reinterpret_cast<const u32x4_t *>(in.xq8l);
+        // clamped: every load is in bounds; the trip count is uniform
+        const int last = chunks * 9 - 1, iters = (last + THREADS) / THREADS;
+#pragma unroll
+        for (int k = 0; k < A::kQ8L; ++k)
+            if (k < iters) q8l[k] = src[min(tid + k * THREADS, last)];
+    } else if constexpr (PRO == Prologue::F32 || PRO == Prologue::RMSNORM) {
+        const int groups = in.width / 4;
+        const float4 *x4 = reinterpret_cast<const float4 *>(in.x);
+        const float4 *w4 = reinterpret_cast<const float4 *>(in.norm);
+        const int iters = (groups + THREADS - 1) / THREADS;  // uniform
+#pragma unroll
+        for (int k = 0; k < A::kPre; ++k) {
+            if (k < iters) {
+                const int g = min(tid + k * THREADS, groups - 1);  // clamped; duplicates are masked below
+                xr[k] = x4[g];
+                if constexpr (PRO == Prologue::RMSNORM) wr[k] = w4[g];
+            }
+        }
+    }
+}
+
+template <int THREADS, Prologue PRO, int NQ, int NX, int NW>
+__device__ __forceinline__ void act_store(const MatvecInput &in, int chunks, const u32x4_t (&q8l)[NQ],
+    const float4 (&xr)[NX], const float4 (&wr)[NW], uint32_t *act32, float *act_s, double *red) {
+    using A = ActShape<THREADS, PRO>;
     const int tid = static_cast<int>(threadIdx.x);
     const int groups = in.width / 4;
     const int blocks = in.width / kQ8Block;
     if constexpr (PRO == Prologue::Q8L) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(in.xq8l);
-        uint4 *dst = reinterpret_cast<uint4 *>(act32);
-        for (int i = tid; i < chunks * 9; i += THREADS) dst[i] = src[i];
+        u32x4_t *dst = reinterpret_cast<u32x4_t *>(act32);
+        const int iters = (chunks * 9 + THREADS - 1) / THREADS;
+#pragma unroll
+        for (int k = 0; k < A::kQ8L; ++k) {
+            const int i = tid + k * THREADS;
+            if (k < iters && i < chunks * 9) dst[i] = q8l[k];
+        }
         __syncthreads();
         return;
     } else {
@@ -77,38 +129,19 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
             __syncthreads();
             return;
         } else {
-            // every x (and norm weight) load of this thread is issued first
-            constexpr int kPre = 8;
-            const float4 *x4 = reinterpret_cast<const float4 *>(in.x);
-            const float4 *w4 = reinterpret_cast<const float4 *>(in.norm);
-            const int iterations = (groups + THREADS - 1) / THREADS;
-            float4 xv[kPre], wv[kPre];
-#pragma unroll
-            for (int it = 0; it < kPre; ++it) {
-                const int g = tid + it * THREADS;
-                xv[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                wv[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                if (it < iterations && g < groups) {
-                    xv[it] = x4[g];
-                    if constexpr (PRO == Prologue::RMSNORM) wv[it] = w4[g];
-                }
-            }
+            // widths up to kPre * THREADS * 4 are held in registers
             float inverse_rms = 1.0f;
             if constexpr (PRO == Prologue::RMSNORM) {
                 double ss = 0.0;
+                const int iters = (groups + THREADS - 1) / THREADS;
 #pragma unroll
-                for (int it = 0; it < kPre; ++it) {
-                    ss += static_cast<double>(xv[it].x) * static_cast<double>(xv[it].x);
-                    ss += static_cast<double>(xv[it].y) * static_cast<double>(xv[it].y);
-                    ss += static_cast<double>(xv[it].z) * static_cast<double>(xv[it].z);
-                    ss += static_cast<double>(xv[it].w) * static_cast<double>(xv[it].w);
-                }
-                for (int g = tid + kPre * THREADS; g < groups; g += THREADS) {
-                    const float4 v = x4[g];
-                    ss += static_cast<double>(v.x) * static_cast<double>(v.x);
-                    ss += static_cast<double>(v.y) * static_cast<double>(v.y);
-                    ss += static_cast<double>(v.z) * static_cast<double>(v.z);
-                    ss += static_cast<double>(v.w) * static_cast<double>(v.w);
+                for (int k = 0; k < A::kPre; ++k) {
+                    if (k >= iters) break;
+                    double t = static_cast<double>(xr[k].x) * static_cast<double>(xr[k].x);
+                    t += static_cast<double>(xr[k].y) * static_cast<double>(xr[k].y);
+                    t += static_cast<double>(xr[k].z) * static_cast<double>(xr[k].z);
+                    t += static_cast<double>(xr[k].w) * static_cast<double>(xr[k].w);
+                    ss += tid + k * THREADS < groups ? t : 0.0;
                 }
                 ss = wave_sum(ss);
                 if constexpr (THREADS > 64) {
@@ -120,28 +153,22 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
                 const float mean = static_cast<float>(ss / static_cast<double>(in.width));
                 inverse_rms = 1.0f / sqrtf(mean + in.eps);
             }
-            for (int it = 0; it < iterations; ++it) {
-                const int g = tid + it * THREADS;
-                const bool valid = g < groups;
-                float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f), w = y;
-                if (it < kPre) {
+            const int iters = (groups + THREADS - 1) / THREADS;
 #pragma unroll
-                    for (int k = 0; k < kPre; ++k)
-                        if (k == it) { y = xv[k]; w = wv[k]; }
-                } else if (valid) {
-                    y = x4[g];
-                    if constexpr (PRO == Prologue::RMSNORM) w = w4[g];
-                }
+            for (int k = 0; k < A::kPre; ++k) {
+                if (k >= iters) break;
+                const int g = tid + k * THREADS;
+                float4 y = xr[k];
                 if constexpr (PRO == Prologue::RMSNORM) {
-                    y.x = (y.x * inverse_rms) * w.x;
-                    y.y = (y.y * inverse_rms) * w.y;
-                    y.z = (y.z * inverse_rms) * w.z;
-                    y.w = (y.w * inverse_rms) * w.w;
+                    y.x = (y.x * inverse_rms) * wr[k].x;
+                    y.y = (y.y * inverse_rms) * wr[k].y;
+                    y.z = (y.z * inverse_rms) * wr[k].z;
+                    y.w = (y.w * inverse_rms) * wr[k].w;
                 }
                 float scale;
                 uint16_t bits;
                 const uint32_t packed = quantize_group(y, scale, bits);
-                if (valid) {
+                if (g < groups) {
                     const int b = g >> 3, l = g & 7;
                     act32[((b >> 2) * 8 + l) * 4 + (b & 3)] = packed;
                     if (l == 0) act_s[b] = scale;
@@ -154,6 +181,19 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
 
 // NREG > 0: every chunk of the row slice (<= NREG) is loaded into registers
 // before the activation is built; NREG == 0 streams batches of 8 chunks.
+template <int THREADS, Prologue PRO>
+__device__ __forceinline__ void build_activation(const MatvecInput &in, int chunks, uint32_t *act32, float *act_s,
+    double *red) {
+    using A = ActShape<THREADS, PRO>;
+    u32x4_t q8l[A::kQ];
+    float4 xr[A::kX], wr[A::kW];
+    act_fetch<THREADS, PRO>(in, chunks, q8l, xr, wr);
+    act_store<THREADS, PRO>(in, chunks, q8l, xr, wr, act32, act_s, red);
+}
+
+// One wave per 8-row group, eight lanes per row.
+// NREG > 0: the matrix has exactly NREG chunks per row, all held in
+// registers; NREG = 0: any width, weights streamed in batches of 8 chunks.
 template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>
 __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs args) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
@@ -172,29 +212,40 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int rg = (wg - args.first_wg[s]) * WAVES + wave;
     const bool active = rg < seg.w.row_groups;
+    const int rgc = active ? rg : seg.w.row_groups - 1;  // excess waves re-read the last group, write nothing
     const int r = lane >> 3, l = lane & 7;
     const int chunks = seg.w.chunks;
-    const uint4 *qp = seg.w.quants + static_cast<size_t>(active ? rg : 0) * chunks * 64 + lane;
-    const uint2 *sp = seg.w.scales + static_cast<size_t>(active ? rg : 0) * chunks * 8 + r;
-    const uint4 *qp2 = kPair ? seg.w2.quants + static_cast<size_t>(active ? rg : 0) * chunks * 64 + lane : nullptr;
-    const uint2 *sp2 = kPair ? seg.w2.scales + static_cast<size_t>(active ? rg : 0) * chunks * 8 + r : nullptr;
+    const uint4 *qp = seg.w.quants + static_cast<size_t>(rgc) * chunks * 64 + lane;
+    const uint2 *sp = seg.w.scales + static_cast<size_t>(rgc) * chunks * 8 + r;
+    const uint4 *qp2 = kPair ? seg.w2.quants + static_cast<size_t>(rgc) * chunks * 64 + lane : nullptr;
+    const uint2 *sp2 = kPair ? seg.w2.scales + static_cast<size_t>(rgc) * chunks * 8 + r : nullptr;
 
+    FORTAI_MV_MARK(0);
+    using AS = ActShape<WAVES * 64, PRO>;
+    u32x4_t act_q[AS::kQ];
+    float4 act_x[AS::kX], act_w[AS::kW];
+    act_fetch<WAVES * 64, PRO>(args.in, args.chunks, act_q, act_x, act_w);
     uint4 q[kRegs], q2[kPair ? kRegs : 1];
     uint2 sc[kRegs], sc2[kPair ? kRegs : 1];
     if constexpr (NREG > 0) {
 #pragma unroll
         for (int c = 0; c < NREG; ++c) {
-            if (active && c < chunks) {
-                q[c] = load_stream(qp + static_cast<size_t>(c) * 64);
-                sc[c] = load_stream(sp + static_cast<size_t>(c) * 8);
-                if constexpr (kPair) {
-                    q2[c] = load_stream(qp2 + static_cast<size_t>(c) * 64);
-                    sc2[c] = load_stream(sp2 + static_cast<size_t>(c) * 8);
-                }
+            q[c] = load_stream(qp + static_cast<size_t>(c) * 64);
+            sc[c] = load_stream(sp + static_cast<size_t>(c) * 8);
+            if constexpr (kPair) {
+                q2[c] = load_stream(qp2 + static_cast<size_t>(c) * 64);
+                sc2[c] = load_stream(sp2 + static_cast<size_t>(c) * 8);
             }
         }
     }
-    build_activation<WAVES * 64, PRO>(args.in, args.chunks, act32, act_s, red);
+    const int row = rg * kRowsPerWave + r;
+    const bool writer = active && l == 0 && row < seg.w.rows;
+    float resid = 0.0f;  // loaded now, used after the dot
+    if constexpr (EPI == Epilogue::ADD)
+        if (writer) resid = seg.resid[row];
+    FORTAI_MV_MARK(1);
+    act_store<WAVES * 64, PRO>(args.in, args.chunks, act_q, act_x, act_w, act32, act_s, red);
+    FORTAI_MV_MARK(2);
 
     const uint4 *act4 = reinterpret_cast<const uint4 *>(act32);
     const float4 *as4 = reinterpret_cast<const float4 *>(act_s);
@@ -203,12 +254,10 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
         if constexpr (NREG > 0) {
 #pragma unroll
             for (int c = 0; c < NREG; ++c) {
-                if (c < chunks) {
-                    const uint4 a = act4[c * 8 + l];
-                    const float4 as = as4[c];
-                    acc = dot_chunk(q[c], sc[c], a, as, acc);
-                    if constexpr (kPair) acc2 = dot_chunk(q2[c], sc2[c], a, as, acc2);
-                }
+                const uint4 a = act4[c * 8 + l];
+                const float4 as = as4[c];
+                acc = dot_chunk(q[c], sc[c], a, as, acc);
+                if constexpr (kPair) acc2 = dot_chunk(q2[c], sc2[c], a, as, acc2);
             }
         } else {
             for (int c0 = 0; c0 < chunks; c0 += 8) {
@@ -237,14 +286,14 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
             }
         }
     }
+    FORTAI_MV_MARK(3);
     acc = row_hsum8(acc);
     if constexpr (kPair) acc2 = row_hsum8(acc2);
-    const int row = rg * kRowsPerWave + r;
-    const bool writer = active && l == 0 && row < seg.w.rows;
     if constexpr (EPI == Epilogue::STORE) {
         if (writer) seg.out[row] = acc;
     } else if constexpr (EPI == Epilogue::ADD) {
-        if (writer) seg.out[row] = acc + seg.resid[row];
+        if (writer) seg.out[row] = acc + resid;
+        FORTAI_MV_MARK(4);
     } else {
         // fortai_silu_product: vector lanes for the first count/8*8 rows, the
         // libm tail expression for the rest (fortai_q8_dot.c:492-505)
@@ -271,6 +320,8 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     }
 }
 
+constexpr int kMatvecWaves = 4;  // large launches; small ones use one wave per workgroup
+
 template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>
 hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES;
@@ -281,9 +332,10 @@ hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream)
 template <int WAVES, Prologue PRO, Epilogue EPI>
 hipError_t launch_matvec_regs(const MatvecArgs &args, int grid, int chunks, hipStream_t stream) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
-    if (chunks <= 8) return launch_matvec_t<WAVES, 8, PRO, EPI>(args, grid, stream);
-    if (chunks <= 16) return launch_matvec_t<WAVES, 16, PRO, EPI>(args, grid, stream);
-    if (!kPair && chunks <= 32) return launch_matvec_t<WAVES, kPair ? 0 : 32, PRO, EPI>(args, grid, stream);
+    if (chunks == 8) return launch_matvec_t<WAVES, 8, PRO, EPI>(args, grid, stream);
+    if (chunks == 16) return launch_matvec_t<WAVES, 16, PRO, EPI>(args, grid, stream);
+    if (!kPair && chunks == 28) return launch_matvec_t<WAVES, kPair ? 0 : 28, PRO, EPI>(args, grid, stream);
+    if (!kPair && chunks == 32) return launch_matvec_t<WAVES, kPair ? 0 : 32, PRO, EPI>(args, grid, stream);
     return launch_matvec_t<WAVES, 0, PRO, EPI>(args, grid, stream);
 }
 
@@ -433,12 +485,18 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const flo
 hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const MatvecInput &in,
     Prologue prologue, Epilogue epilogue, hipStream_t stream) {
     if (count < 1 || count > 4 || in.width <= 0 || in.width % kQ8Block) return hipErrorInvalidValue;
-    // one wave (8 rows) per workgroup keeps the row slices of small matrices
-    // spread over many CUs; large multi-matrix launches use 4 waves so the
-    // activation prologue is built once per 32 rows
+    // activation widths the register prologues hold
+    if (prologue == Prologue::Q8L && (in.width / kQ8Block + 3) / 4 > kMaxChunks) return hipErrorInvalidValue;
+    constexpr int kPre = ActShape<64, Prologue::F32>::kPre;  // float4 groups per thread
+    const bool f32_in = prologue == Prologue::F32 || prologue == Prologue::RMSNORM;
+    if (f32_in && in.width / 4 > kPre * kMatvecWaves * 64) return hipErrorInvalidValue;
+    // small matrices: one wave per workgroup keeps their row groups spread
+    // over many CUs (each CU's memory pipeline serves one wave's loads); large
+    // multi-matrix launches use 4 (one activation per 32 rows)
     int total_groups = 0;
     for (int s = 0; s < count; ++s) total_groups += segments[s].w.row_groups;
-    const int waves = (epilogue == Epilogue::SILU_PAIR || total_groups >= 1024) ? 4 : 1;
+    const int waves = (epilogue == Epilogue::SILU_PAIR || total_groups >= 1024 ||
+                          (f32_in && in.width / 4 > kPre * 64)) ? 4 : 1;
     if (epilogue == Epilogue::SILU_PAIR) {
         // one workgroup = 32 rows = one quantization block of h
         if (count != 1 || (segments[0].out_q8l && segments[0].w.rows % kQ8Block)) return hipErrorInvalidValue;
