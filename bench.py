@@ -257,6 +257,7 @@ def main() -> int:
     roof = lm_head_roofline(model)
     mv = None if args.no_matvec else bench_matvec(model)
     d = model.d
+    decoder = "persistent (one launch per token)" if model.decoder.persistent else "HIP graph of per-op kernels"
     step_bytes = bytes_per_token(d, args.ctx - args.steps // 2)
     decode_gbps = step_bytes * tok_s / 1e9
     model.close()
@@ -279,7 +280,7 @@ def main() -> int:
                                f"{args.ctx - args.steps}..{args.ctx - 1} of a {args.ctx}-token context "
                                "(BASELINE config 4)",
                    "hidden": d.hidden, "layers": d.layers, "ffn": d.ffn, "vocab": d.vocab,
-                   "context": args.ctx, "batch": 1},
+                   "context": args.ctx, "batch": 1, "decoder": decoder},
         "decode_hbm": {"algorithmic_bytes_per_token": int(step_bytes), "gbps": round(decode_gbps, 1),
                        "frac_of_8TBps": round(decode_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": roof,

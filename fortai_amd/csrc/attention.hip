@@ -19,6 +19,7 @@ namespace ea = exact_attention;
 constexpr int kMaxGroup = 4;
 constexpr int kMaxHead = 256;
 constexpr int kLoads = ea::kPosBlock * (kMaxHead / 8) / ea::kThreads;
+constexpr int kQLoads = kMaxGroup * kMaxHead / ea::kThreads;
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
@@ -32,6 +33,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     __shared__ __align__(16) uint16_t ktile[ea::kPosBlock][kMaxHead + 8];
     __shared__ int overflow;
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+    FORTAI_ATT_MARK(8);
     const int pos = *p.position;
     if (pos < 0 || pos >= p.max_context) return;  // never index past the cache
     const int positions = pos + 1, nblk_max = (p.max_context + ea::kPosBlock - 1) / ea::kPosBlock;
@@ -50,17 +52,32 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
         const int j = min(li / segs, n - 1), sg = li % segs;  // rows past n re-read row n-1 (in bounds)
         kr[i] = reinterpret_cast<const v4u *>(p.kcache + (static_cast<size_t>(p0 + j) * NKV + kvh) * HD)[sg];
     }
-    for (int i = tid; i < group * HD; i += ea::kThreads)
-        qh[i] = p.q[static_cast<size_t>(kvh * group + i / HD) * 2 * HD + i % HD];
-    if (tid < HD) {
-        qw[tid] = p.q_norm[tid];
-        kw[tid] = p.k_norm[tid];
-        if (owns_new) kn[tid] = p.k[static_cast<size_t>(kvh) * HD + tid];
+    // every other input in the same round trip (indices clamped in bounds),
+    // then the LDS stores
+    float qv[kQLoads];
+#pragma unroll
+    for (int i = 0; i < kQLoads; ++i) {
+        const int e = min(tid + i * ea::kThreads, group * HD - 1);
+        qv[i] = p.q[static_cast<size_t>(kvh * group + e / HD) * 2 * HD + e % HD];
     }
-    if (owns_new && tid < VD) vn[tid] = p.v[static_cast<size_t>(kvh) * VD + tid];
-    if (tid < half) rs[tid] = p.rope[static_cast<size_t>(pos) * half + tid];
-    if (tid == 0) overflow = 0;
+    const int th = min(tid, HD - 1), tv = min(tid, VD - 1);
+    const float qwv = p.q_norm[th], kwv = p.k_norm[th];
+    const float knv = p.k[static_cast<size_t>(kvh) * HD + th];
+    const float vnv = p.v[static_cast<size_t>(kvh) * VD + tv];
+    const float2 rsv = half > 0 ? p.rope[static_cast<size_t>(pos) * half + min(tid, half - 1)] : make_float2(0.0f, 0.0f);
     const int flag = p.cache_flags[kvh];
+#pragma unroll
+    for (int i = 0; i < kQLoads; ++i)
+        if (tid + i * ea::kThreads < group * HD) qh[tid + i * ea::kThreads] = qv[i];
+    if (tid < HD) {
+        qw[tid] = qwv;
+        kw[tid] = kwv;
+        kn[tid] = knv;
+    }
+    if (tid < VD) vn[tid] = vnv;
+    if (tid < half) rs[tid] = rsv;
+    if (tid == 0) overflow = 0;
+    FORTAI_ATT_MARK(9);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int li = tid + i * ea::kThreads;
@@ -73,6 +90,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
         else ea::norm_rope(kn, HD, kw, p.eps, rs, p.rope_dim, lane);
     }
     __syncthreads();
+    FORTAI_ATT_MARK(10);
     if (owns_new) {
         // append at pos (fortai_qwen35_cpu.f90:1594-1601)
         if (tid < HD) {
@@ -97,11 +115,13 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
                                 : ea::score<false>(qh + gi * HD, &ktile[j][0], HD, sqrt_head);
         p.partial[static_cast<size_t>(kvh * group + gi) * p.max_context + p0 + j] = sc;
     }
+    FORTAI_ATT_MARK(11);
 }
 
 __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const AttentionParams p) {
     extern __shared__ __align__(16) float lds[];
     const int tid = static_cast<int>(threadIdx.x);
+    FORTAI_ATT_MARK(0);
     const int pos = *p.position;
     if (pos < 0 || pos >= p.max_context) return;
     const int positions = pos + 1;
@@ -111,18 +131,29 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     const int kvh = h / group;
     float *sw = lds;
     float *work = sw + ea::sw_floats(p.max_context);
-    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
-    for (int i = tid; i < positions; i += ea::kThreads) sw[i] = sc[i];
-    const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
-    const int flag = p.cache_flags[kvh];
     const uint16_t *vbase = p.vcache + static_cast<size_t>(kvh) * VD + d0;
     const size_t vstride = static_cast<size_t>(NKV) * VD;
     ea::ValuePieces v;
     ea::value_prefetch(vbase, vstride, positions, v);
+    const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
+    const int flag = p.cache_flags[kvh];
+    // the scores, eight loads in flight per thread
+    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
+    constexpr int kBatch = 8;
+    for (int i0 = tid; i0 < positions; i0 += ea::kThreads * kBatch) {
+        float x[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) x[k] = sc[min(i0 + k * ea::kThreads, positions - 1)];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k)
+            if (i0 + k * ea::kThreads < positions) sw[i0 + k * ea::kThreads] = x[k];
+    }
     __syncthreads();
+    FORTAI_ATT_MARK(3);
     const float acc = flag == 0 ? ea::attend<true>(sw, positions, vbase, vstride, work, v)
                                 : ea::attend<false>(sw, positions, vbase, vstride, work, v);
     if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * sigmoid_ref(gate);
+    FORTAI_ATT_MARK(4);
 }
 
 size_t output_lds_bytes(int max_context) {

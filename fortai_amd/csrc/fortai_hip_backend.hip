@@ -1372,17 +1372,18 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     if (e == hipSuccess) e = alloc(&d->trace, max_context + 1);
     if (e == hipSuccess) e = hipMemsetAsync(d->trace, 0, (max_context + 1) * sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    // the persistent one-launch step where the shapes allow it
-    // (FORTAI_HIP_DECODER=graph keeps the per-op kernels)
+    // FORTAI_HIP_DECODER=persistent: the one-launch step (all layers in one
+    // kernel, phases handed over through tagged words).  The default is the
+    // captured graph of per-op kernels, which measures faster on MI355X.
     const char *path_env = std::getenv("FORTAI_HIP_DECODER");
-    if (e == hipSuccess && !(path_env && std::strcmp(path_env, "graph") == 0)) {
+    if (e == hipSuccess && path_env && std::strcmp(path_env, "persistent") == 0) {
         const std::string why = setup_persistent(d);
-        if (!why.empty() && path_env && std::strcmp(path_env, "persistent") == 0) {
+        if (!why.empty()) {
             fortai_hip_qwen35_decoder_destroy(d);
             return fail(c, FORTAI_HIP_INVALID, ("persistent decoder unsupported: " + why).c_str());
         }
     }
-    // otherwise capture one per-op decode step as a graph (FORTAI_HIP_DECODER_GRAPH=0
+    // the per-op decode step captured as a graph (FORTAI_HIP_DECODER_GRAPH=0
     // enqueues the kernels directly every step instead, e.g. for kernel tracing)
     const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
     d->use_graph = !d->persistent && !(graph_env && std::strcmp(graph_env, "0") == 0);
