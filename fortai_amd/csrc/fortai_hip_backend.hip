@@ -63,7 +63,7 @@ struct fortai_hip_qwen35_recurrent {
     float *conv_w = nullptr, *ssm_a = nullptr, *ssm_dt = nullptr, *ssm_norm = nullptr;
     float *conv_state = nullptr, *state = nullptr;
     float *qkv_out = nullptr, *z_out = nullptr, *alpha_out = nullptr, *beta_out = nullptr;
-    void *o_q8l = nullptr;  // gated, quantized GDN output (ssm_out input)
+    float *o_raw = nullptr;  // GDN output before the gated norm (ssm_out input)
 };
 
 struct fortai_hip_qwen35_attention {
@@ -221,17 +221,29 @@ GdnParams gdn_params(fortai_hip_qwen35_recurrent *L, const float *qkv, const flo
     return p;
 }
 
-// enqueue the GDN projections -> fused step (+ gated norm, quantize) -> ssm_out
+// enqueue the GDN projections (the qkv rows through conv1d + SiLU in the
+// epilogue) -> delta rule -> ssm_out with the gated RMSNorm as its prologue
 hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &in, Prologue pro, float *out,
     const float *resid, hipStream_t stream) {
-    const MatvecSegment segs[4] = {segment(L->qkv, L->qkv_out), segment(L->gate, L->z_out),
+    MatvecSegment segs[4] = {segment(L->qkv, L->qkv_out), segment(L->gate, L->z_out),
         segment(L->alpha, L->alpha_out), segment(L->beta, L->beta_out)};
+    segs[0].conv_w = L->conv_w;
+    segs[0].conv_state = L->conv_state;
+    segs[0].conv_size = L->conv_size;
+    segs[0].kernel = L->kernel;
+    segs[1].silu = true;  // the gate is only used through SiLU
     hipError_t e = launch_q8_matvec(segs, 4, in, pro, Epilogue::STORE, stream);
-    if (e == hipSuccess) e = launch_gdn_step(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, nullptr, L->o_q8l), stream);
+    if (e == hipSuccess) e = launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw, nullptr), stream);
     if (e != hipSuccess) return e;
+    MatvecInput gated;
+    gated.x = L->o_raw;
+    gated.z = L->z_out;
+    gated.norm = L->ssm_norm;
+    gated.eps = L->eps;
+    gated.head = L->head;
+    gated.width = L->inner;
     const MatvecSegment oseg = segment(L->out, out, resid);
-    return launch_q8_matvec(&oseg, 1, q8l_input(L->o_q8l, L->inner), Prologue::Q8L,
-        resid ? Epilogue::ADD : Epilogue::STORE, stream);
+    return launch_q8_matvec(&oseg, 1, gated, Prologue::GATED, resid ? Epilogue::ADD : Epilogue::STORE, stream);
 }
 
 AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q, const float *k, const float *v,
@@ -806,7 +818,7 @@ int fortai_hip_qwen35_recurrent_create(fortai_hip_q8_context *c, const fortai_hi
     if (e == hipSuccess) e = alloc(&L->z_out, inner_size);
     if (e == hipSuccess) e = alloc(&L->alpha_out, value_heads);
     if (e == hipSuccess) e = alloc(&L->beta_out, value_heads);
-    if (e == hipSuccess) e = alloc_q8l(&L->o_q8l, inner_size, c->stream);
+    if (e == hipSuccess) e = alloc(&L->o_raw, inner_size);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         fortai_hip_qwen35_recurrent_destroy(L);
@@ -829,7 +841,7 @@ int fortai_hip_qwen35_recurrent_destroy(fortai_hip_qwen35_recurrent *L) {
     }
     release(L->conv_w); release(L->ssm_a); release(L->ssm_dt); release(L->ssm_norm); release(L->conv_state);
     release(L->state); release(L->qkv_out); release(L->z_out); release(L->alpha_out); release(L->beta_out);
-    if (L->o_q8l) (void)hipFree(L->o_q8l);
+    release(L->o_raw);
     delete L;
     return FORTAI_HIP_OK;
 }

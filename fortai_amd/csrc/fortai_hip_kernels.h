@@ -41,6 +41,9 @@ enum class Prologue : int {
     F32 = 1,      // f32 vector, quantized in-workgroup (fortai_q8_quantize)
     RMSNORM = 2,  // f32 x -> rms_norm(x, w) -> quantize
     Q8L = 3,      // producer-quantized activation in the Q8L layout
+    GATED = 4,    // raw GDN output x with the gate already through SiLU (z):
+                  // per-head gated RMSNorm ((x / rms(x)) * norm) * z
+                  // (fortai_qwen35_cpu.f90:907-915)
 };
 
 // What happens to each row result.
@@ -57,13 +60,22 @@ struct MatvecSegment {
     float *out = nullptr;
     const float *resid = nullptr;
     void *out_q8l = nullptr; // SILU_PAIR: quantized h for the next matvec
+    // STORE with conv_w: the causal conv1d + SiLU of each row's channel over
+    // its window conv_state[kernel-1][conv_size] (oldest first), which the
+    // row's thread then shifts (fortai_qwen35_cpu.f90:856-879)
+    const float *conv_w = nullptr;  // [rows][kernel]
+    float *conv_state = nullptr;
+    int conv_size = 0, kernel = 0;
+    bool silu = false;              // STORE without conv: out[row] = silu(dot)
 };
 
 struct MatvecInput {
     const float *x = nullptr;     // F32 / RMSNORM: [width]
     const int8_t *xq = nullptr;   // Q8: GGUF blocks [blocks][34]
     const void *xq8l = nullptr;   // Q8L
-    const float *norm = nullptr;  // RMSNORM: weights [width]
+    const float *norm = nullptr;  // RMSNORM: weights [width]; GATED: [head]
+    const float *z = nullptr;     // GATED: silu(gate) [width]
+    int head = 0;                 // GATED: head size (the norm's span)
     float eps = 0.0f;
     int width = 0;                // activation elements (multiple of 32)
 };
@@ -130,6 +142,11 @@ struct GdnParams {
     float eps = 0.0f;
 };
 hipError_t launch_gdn_step(const GdnParams &p, hipStream_t stream);
+// The delta-rule part alone, 16 state rows per workgroup: qkv holds the
+// conv + SiLU outputs (the projection epilogue computed them and shifted the
+// window); writes the raw output o to p.out (the gated norm is the ssm_out
+// prologue).  z, conv_w, conv_state and out_q8l are not used.
+hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream);
 
 // ---- attention -------------------------------------------------------------
 struct AttentionParams {

@@ -183,6 +183,93 @@ __global__ __launch_bounds__(kThreads) void gdn_group_kernel(const GdnParams p) 
     }
 }
 
+// The delta rule of 16 state rows of one value head per workgroup (128
+// threads, 8 lanes per row): the L2 norms of the head's q and k (waves 0 and
+// 1, the same sums as gdn_group_kernel), beta and the decay, the row updates
+// and the raw output.  qkv already holds conv + SiLU.
+constexpr int kDeltaRows = 16;
+constexpr int kDeltaThreads = kDeltaRows * 8;
+
+template <int HEAD>
+__global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParams p) {
+    constexpr int kCols = HEAD / 8;
+    __shared__ __align__(16) float qs[HEAD];
+    __shared__ __align__(16) float ks[HEAD];
+    __shared__ double red[2];
+    __shared__ float hs[2];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int blocks_per_head = HEAD / kDeltaRows;
+    const int h = static_cast<int>(blockIdx.x) / blocks_per_head;
+    const int r0 = (static_cast<int>(blockIdx.x) % blocks_per_head) * kDeltaRows;
+    const int kh = h / (p.value_heads / p.key_heads);
+    const int r8 = tid >> 3, l = tid & 7, row = r0 + r8;
+    // every load first: the state row, q and k of the key head, v, the scalars
+    float s[kCols];
+    float4 *srow = reinterpret_cast<float4 *>(p.state + ((static_cast<size_t>(h) * HEAD + row) * 8 + l) * kCols);
+#pragma unroll
+    for (int i = 0; i < kCols / 4; ++i) {
+        const float4 f = srow[i];
+        s[4 * i] = f.x; s[4 * i + 1] = f.y; s[4 * i + 2] = f.z; s[4 * i + 3] = f.w;
+    }
+    constexpr int kPer = (2 * HEAD + kDeltaThreads - 1) / kDeltaThreads;  // q|k values per thread
+    float qk[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = min(tid + k * kDeltaThreads, 2 * HEAD - 1);
+        qk[k] = p.qkv[i < HEAD ? kh * HEAD + i : p.state_size * p.key_heads + kh * HEAD + (i - HEAD)];
+    }
+    const float vrow = p.qkv[2 * p.state_size * p.key_heads + h * HEAD + row];
+    float beta = 0.0f, decay = 0.0f;
+    if (tid == 0) {
+        // fortai_qwen35_cpu.f90:890-894
+        beta = sigmoid_ref(p.beta[h]);
+        decay = exp_rounded(p.ssm_a[h] * softplus_ref(p.alpha[h] + p.ssm_dt[h]));
+        hs[0] = beta;
+        hs[1] = decay;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = tid + k * kDeltaThreads;
+        if (i < HEAD) qs[i] = qk[k];
+        else if (i < 2 * HEAD) ks[i - HEAD] = qk[k];
+    }
+    __syncthreads();
+    // L2 norms of q (wave 0) and k (wave 1), fortai_qwen35_cpu.f90:1455-1471
+    {
+        const float *v = (tid < 64) ? qs : ks;
+        double ss = 0.0;
+        for (int i = tid & 63; i < HEAD; i += 64) ss += static_cast<double>(v[i]) * static_cast<double>(v[i]);
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+    }
+    __syncthreads();
+    const float qinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[0])), p.eps);
+    const float kinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[1])), p.eps);
+    beta = hs[0];
+    decay = hs[1];
+    // delta rule (fortai_q8_dot.c:363-396), the normalized q and k read from LDS
+    float kd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) {
+        const float d = s[i] * decay;
+        s[i] = d;
+        kd = __builtin_fmaf(d, ks[8 * i + l] * kinv, kd);
+    }
+    kd = row_hsum8(kd);
+    const float delta = (vrow - kd) * beta;
+    float qd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) {
+        const float u = __builtin_fmaf(delta, ks[8 * i + l] * kinv, s[i]);
+        s[i] = u;
+        qd = __builtin_fmaf(u, qs[8 * i + l] * qinv, qd);
+    }
+    qd = row_hsum8(qd);
+#pragma unroll
+    for (int i = 0; i < kCols / 4; ++i) srow[i] = make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
+    if (l == 0) p.out[h * HEAD + row] = qd * (1.0f / sqrtf(static_cast<float>(HEAD)));
+}
+
 }  // namespace
 
 hipError_t launch_gdn_step(const GdnParams &p, hipStream_t stream) {
@@ -197,6 +284,18 @@ hipError_t launch_gdn_step(const GdnParams &p, hipStream_t stream) {
     case 64: hipLaunchKernelGGL(gdn_group_kernel<64>, dim3(p.key_heads), dim3(kThreads), lds, stream, p); break;
     case 128: hipLaunchKernelGGL(gdn_group_kernel<128>, dim3(p.key_heads), dim3(kThreads), lds, stream, p); break;
     case 256: hipLaunchKernelGGL(gdn_group_kernel<256>, dim3(p.key_heads), dim3(kThreads), lds, stream, p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream) {
+    if (p.key_heads <= 0 || p.value_heads % p.key_heads || p.state_size != p.head || !p.out) return hipErrorInvalidValue;
+    const dim3 grid(p.value_heads * (p.head / kDeltaRows));
+    switch (p.head) {
+    case 64: hipLaunchKernelGGL(gdn_delta_kernel<64>, grid, dim3(kDeltaThreads), 0, stream, p); break;
+    case 128: hipLaunchKernelGGL(gdn_delta_kernel<128>, grid, dim3(kDeltaThreads), 0, stream, p); break;
+    case 256: hipLaunchKernelGGL(gdn_delta_kernel<256>, grid, dim3(kDeltaThreads), 0, stream, p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -56,19 +56,22 @@ __device__ __forceinline__ uint32_t load_u32_unaligned(const int8_t *p) {
 // (act_store): the compiler's in-order vmcnt waits for the activation then do
 // not wait for the weights.
 constexpr int kMaxChunks = 96;  // Q8L activations up to 12288 wide
+constexpr int kConvMax = 8;     // conv epilogue: kernel width limit
 
 template <int THREADS, Prologue PRO>
 struct ActShape {
     static constexpr int kQ8L = (kMaxChunks * 9 + THREADS - 1) / THREADS;  // 16-byte pieces per thread
     static constexpr int kPre = 8;                                          // float4 groups per thread
+    static constexpr bool kF32 = PRO == Prologue::F32 || PRO == Prologue::RMSNORM || PRO == Prologue::GATED;
     static constexpr int kQ = PRO == Prologue::Q8L ? kQ8L : 1;
-    static constexpr int kX = PRO == Prologue::F32 || PRO == Prologue::RMSNORM ? kPre : 1;
-    static constexpr int kW = PRO == Prologue::RMSNORM ? kPre : 1;
+    static constexpr int kX = kF32 ? kPre : 1;
+    static constexpr int kW = PRO == Prologue::RMSNORM || PRO == Prologue::GATED ? kPre : 1;
+    static constexpr int kZ = PRO == Prologue::GATED ? kPre : 1;
 };
 
-template <int THREADS, Prologue PRO, int NQ, int NX, int NW>
+template <int THREADS, Prologue PRO, int NQ, int NX, int NW, int NZ>
 __device__ __forceinline__ void act_fetch(const MatvecInput &in, int chunks, u32x4_t (&q8l)[NQ], float4 (&xr)[NX],
-    float4 (&wr)[NW]) {
+    float4 (&wr)[NW], float4 (&zr)[NZ]) {
     using A = ActShape<THREADS, PRO>;
     const int tid = static_cast<int>(threadIdx.x);
     if constexpr (PRO == Prologue::Q8L) {
@@ -78,10 +81,11 @@ __device__ __forceinline__ void act_fetch(const MatvecInput &in, int chunks, u32
 #pragma unroll
         for (int k = 0; k < A::kQ8L; ++k)
             if (k < iters) q8l[k] = src[min(tid + k * THREADS, last)];
-    } else if constexpr (PRO == Prologue::F32 || PRO == Prologue::RMSNORM) {
+    } else if constexpr (A::kF32) {
         const int groups = in.width / 4;
         const float4 *x4 = reinterpret_cast<const float4 *>(in.x);
         const float4 *w4 = reinterpret_cast<const float4 *>(in.norm);
+        const float4 *z4 = reinterpret_cast<const float4 *>(in.z);
         const int iters = (groups + THREADS - 1) / THREADS;  // uniform
 #pragma unroll
         for (int k = 0; k < A::kPre; ++k) {
@@ -89,14 +93,19 @@ __device__ __forceinline__ void act_fetch(const MatvecInput &in, int chunks, u32
                 const int g = min(tid + k * THREADS, groups - 1);  // clamped; duplicates are masked below
                 xr[k] = x4[g];
                 if constexpr (PRO == Prologue::RMSNORM) wr[k] = w4[g];
+                if constexpr (PRO == Prologue::GATED) {
+                    wr[k] = w4[g % (in.head / 4)];
+                    zr[k] = z4[g];
+                }
             }
         }
     }
 }
 
-template <int THREADS, Prologue PRO, int NQ, int NX, int NW>
+template <int THREADS, Prologue PRO, int NQ, int NX, int NW, int NZ>
 __device__ __forceinline__ void act_store(const MatvecInput &in, int chunks, const u32x4_t (&q8l)[NQ],
-    const float4 (&xr)[NX], const float4 (&wr)[NW], uint32_t *act32, float *act_s, double *red) {
+    const float4 (&xr)[NX], const float4 (&wr)[NW], const float4 (&zr)[NZ], uint32_t *act32, float *act_s,
+    double *red) {
     using A = ActShape<THREADS, PRO>;
     const int tid = static_cast<int>(threadIdx.x);
     const int groups = in.width / 4;
@@ -164,6 +173,19 @@ __device__ __forceinline__ void act_store(const MatvecInput &in, int chunks, con
                     y.y = (y.y * inverse_rms) * wr[k].y;
                     y.z = (y.z * inverse_rms) * wr[k].z;
                     y.w = (y.w * inverse_rms) * wr[k].w;
+                } else if constexpr (PRO == Prologue::GATED) {
+                    // a head is head/4 consecutive lanes (aligned): its sum of
+                    // squares in double over those lanes, then the gate
+                    double ss = static_cast<double>(y.x) * static_cast<double>(y.x);
+                    ss += static_cast<double>(y.y) * static_cast<double>(y.y);
+                    ss += static_cast<double>(y.z) * static_cast<double>(y.z);
+                    ss += static_cast<double>(y.w) * static_cast<double>(y.w);
+                    for (int m = 1; m < in.head / 4; m <<= 1) ss += __shfl_xor(ss, m);
+                    const float nf = sqrtf(static_cast<float>(ss / static_cast<double>(in.head)) + in.eps);
+                    y.x = ((y.x / nf) * wr[k].x) * zr[k].x;
+                    y.y = ((y.y / nf) * wr[k].y) * zr[k].y;
+                    y.z = ((y.z / nf) * wr[k].z) * zr[k].z;
+                    y.w = ((y.w / nf) * wr[k].w) * zr[k].w;
                 }
                 float scale;
                 uint16_t bits;
@@ -186,9 +208,9 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
     double *red) {
     using A = ActShape<THREADS, PRO>;
     u32x4_t q8l[A::kQ];
-    float4 xr[A::kX], wr[A::kW];
-    act_fetch<THREADS, PRO>(in, chunks, q8l, xr, wr);
-    act_store<THREADS, PRO>(in, chunks, q8l, xr, wr, act32, act_s, red);
+    float4 xr[A::kX], wr[A::kW], zr[A::kZ];
+    act_fetch<THREADS, PRO>(in, chunks, q8l, xr, wr, zr);
+    act_store<THREADS, PRO>(in, chunks, q8l, xr, wr, zr, act32, act_s, red);
 }
 
 // One wave per 8-row group, eight lanes per row.
@@ -223,8 +245,8 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     FORTAI_MV_MARK(0);
     using AS = ActShape<WAVES * 64, PRO>;
     u32x4_t act_q[AS::kQ];
-    float4 act_x[AS::kX], act_w[AS::kW];
-    act_fetch<WAVES * 64, PRO>(args.in, args.chunks, act_q, act_x, act_w);
+    float4 act_x[AS::kX], act_w[AS::kW], act_z[AS::kZ];
+    act_fetch<WAVES * 64, PRO>(args.in, args.chunks, act_q, act_x, act_w, act_z);
     uint4 q[kRegs], q2[kPair ? kRegs : 1];
     uint2 sc[kRegs], sc2[kPair ? kRegs : 1];
     if constexpr (NREG > 0) {
@@ -243,8 +265,19 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     float resid = 0.0f;  // loaded now, used after the dot
     if constexpr (EPI == Epilogue::ADD)
         if (writer) resid = seg.resid[row];
+    // STORE with a conv: the row's window and taps, loaded now
+    float win[kConvMax - 1], taps[kConvMax];
+    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr;
+    const int ck = conv ? seg.kernel : 0;
+    if (conv && writer) {
+#pragma unroll
+        for (int t = 0; t < kConvMax; ++t) {
+            if (t < ck - 1) win[t] = seg.conv_state[static_cast<size_t>(t) * seg.conv_size + row];
+            if (t < ck) taps[t] = seg.conv_w[static_cast<size_t>(row) * ck + t];
+        }
+    }
     FORTAI_MV_MARK(1);
-    act_store<WAVES * 64, PRO>(args.in, args.chunks, act_q, act_x, act_w, act32, act_s, red);
+    act_store<WAVES * 64, PRO>(args.in, args.chunks, act_q, act_x, act_w, act_z, act32, act_s, red);
     FORTAI_MV_MARK(2);
 
     const uint4 *act4 = reinterpret_cast<const uint4 *>(act32);
@@ -290,7 +323,26 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     acc = row_hsum8(acc);
     if constexpr (kPair) acc2 = row_hsum8(acc2);
     if constexpr (EPI == Epilogue::STORE) {
-        if (writer) seg.out[row] = acc;
+        if (conv && writer) {
+            // fortai_qwen35_cpu.f90:856-879: oldest slot first, the current value
+            // last; then the window moves by one (only this thread touches it)
+            float a = 0.0f;
+#pragma unroll
+            for (int t = 0; t < kConvMax - 1; ++t)
+                if (t < ck - 1) a = a + taps[t] * win[t];
+            float last = 0.0f;
+#pragma unroll
+            for (int t = 0; t < kConvMax; ++t)
+                if (t == ck - 1) last = taps[t];
+            a = a + last * acc;
+            seg.out[row] = silu_poly(a);
+#pragma unroll
+            for (int t = 0; t + 1 < kConvMax - 1; ++t)
+                if (t + 1 < ck - 1) seg.conv_state[static_cast<size_t>(t) * seg.conv_size + row] = win[t + 1];
+            seg.conv_state[static_cast<size_t>(ck - 2) * seg.conv_size + row] = acc;
+        } else if (writer) {
+            seg.out[row] = seg.silu ? silu_poly(acc) : acc;
+        }
     } else if constexpr (EPI == Epilogue::ADD) {
         if (writer) seg.out[row] = acc + resid;
         FORTAI_MV_MARK(4);
@@ -488,14 +540,25 @@ hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const Matv
     // activation widths the register prologues hold
     if (prologue == Prologue::Q8L && (in.width / kQ8Block + 3) / 4 > kMaxChunks) return hipErrorInvalidValue;
     constexpr int kPre = ActShape<64, Prologue::F32>::kPre;  // float4 groups per thread
-    const bool f32_in = prologue == Prologue::F32 || prologue == Prologue::RMSNORM;
+    const bool f32_in = prologue == Prologue::F32 || prologue == Prologue::RMSNORM || prologue == Prologue::GATED;
+    if (prologue == Prologue::GATED) {
+        // a head must be an aligned power-of-two run of lanes
+        const int hl = in.head / 4;
+        if (in.head <= 0 || in.head % 4 || hl > 64 || (hl & (hl - 1)) || in.width % in.head || !in.z || !in.norm)
+            return hipErrorInvalidValue;
+    }
+    for (int s = 0; s < count; ++s)
+        if (segments[s].conv_w && (epilogue != Epilogue::STORE || segments[s].kernel < 2 ||
+                                     segments[s].kernel > kConvMax || segments[s].conv_size < segments[s].w.rows))
+            return hipErrorInvalidValue;
     if (f32_in && in.width / 4 > kPre * kMatvecWaves * 64) return hipErrorInvalidValue;
     // small matrices: one wave per workgroup keeps their row groups spread
     // over many CUs (each CU's memory pipeline serves one wave's loads); large
     // multi-matrix launches use 4 (one activation per 32 rows)
     int total_groups = 0;
     for (int s = 0; s < count; ++s) total_groups += segments[s].w.row_groups;
-    const int waves = (epilogue == Epilogue::SILU_PAIR || total_groups >= 1024 ||
+    // (the gated prologue's per-value divisions are spread over 4 waves too)
+    const int waves = (epilogue == Epilogue::SILU_PAIR || total_groups >= 1024 || prologue == Prologue::GATED ||
                           (f32_in && in.width / 4 > kPre * 64)) ? 4 : 1;
     if (epilogue == Epilogue::SILU_PAIR) {
         // one workgroup = 32 rows = one quantization block of h
@@ -522,6 +585,7 @@ hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const Matv
     case Prologue::RMSNORM:
         return launch_matvec_pro<Prologue::RMSNORM>(args, waves, grid, args.chunks, epilogue, stream);
     case Prologue::Q8L: return launch_matvec_pro<Prologue::Q8L>(args, waves, grid, args.chunks, epilogue, stream);
+    case Prologue::GATED: return launch_matvec_pro<Prologue::GATED>(args, waves, grid, args.chunks, epilogue, stream);
     }
     return hipErrorInvalidValue;
 }
