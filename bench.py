@@ -226,6 +226,38 @@ def cpu_baseline(path, ctx_len: int, steps: int):
             "sample": f"{steps} greedy decode steps at positions 0..{steps - 1} with oracle/liboracle.so"}
 
 
+def trace_summary(directory: str, steps: int = 64) -> None:
+    """Per-kernel time of the last `steps` decode steps of a rocprofv3
+    --kernel-trace CSV (a step starts at its embedding kernel)."""
+    import csv
+    import glob
+    from collections import defaultdict
+    paths = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no kernel_trace.csv under {directory}")
+    rows = []
+    with open(paths[0]) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    starts = [i for i, r in enumerate(rows) if "embedding" in r[2]]
+    if len(starts) < steps + 1:
+        raise SystemExit(f"only {len(starts)} decode steps in the trace")
+    sel = rows[starts[-steps - 1]:starts[-1]]
+    agg = defaultdict(lambda: [0, 0])
+    for s0, s1, name in sel:
+        key = name.replace("(anonymous namespace)::", "").replace("fortai_hip::", "").replace("void ", "")
+        key = key.replace("(Prologue)", "P").replace("(Epilogue)", "E").split("(")[0]
+        agg[key][0] += 1
+        agg[key][1] += s1 - s0
+    busy = sum(v[1] for v in agg.values()) / steps / 1e3
+    print(f"| kernel | calls/step | avg us | us/step | % of busy |")
+    print(f"|---|---:|---:|---:|---:|")
+    for k, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"| `{k}` | {c / steps:.0f} | {t / c / 1e3:.2f} | {t / steps / 1e3:.1f} | {100 * t / steps / 1e3 / busy:.1f} |")
+    print(f"\nkernel busy time per step: {busy:.1f} us over {len(sel) / steps:.0f} dispatches")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -241,7 +273,13 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue each decode step's kernels directly instead of replaying the HIP graph "
                          "(for kernel tracing)")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="print the per-kernel table of the last --steps decode steps of a rocprofv3 "
+                         "--kernel-trace CSV under DIR, then exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.steps)
+        return 0
     if args.no_graph:
         os.environ["FORTAI_HIP_DECODER_GRAPH"] = "0"
     if args.gpus != 1:
