@@ -129,36 +129,22 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     const int slices = VD / ea::kDims;
     const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * ea::kDims;
     const int kvh = h / group;
-    float *sw = lds;
-    float *work = sw + ea::sw_floats(p.max_context);
+    float *work = lds;
     const uint16_t *vbase = p.vcache + static_cast<size_t>(kvh) * VD + d0;
     const size_t vstride = static_cast<size_t>(NKV) * VD;
     ea::ValuePieces v;
     ea::value_prefetch(vbase, vstride, positions, v);
     const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
     const int flag = p.cache_flags[kvh];
-    // the scores, eight loads in flight per thread
-    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
-    constexpr int kBatch = 8;
-    for (int i0 = tid; i0 < positions; i0 += ea::kThreads * kBatch) {
-        float x[kBatch];
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) x[k] = sc[min(i0 + k * ea::kThreads, positions - 1)];
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k)
-            if (i0 + k * ea::kThreads < positions) sw[i0 + k * ea::kThreads] = x[k];
-    }
-    __syncthreads();
+    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;  // read in place
     FORTAI_ATT_MARK(3);
-    const float acc = flag == 0 ? ea::attend<true>(sw, positions, vbase, vstride, work, v)
-                                : ea::attend<false>(sw, positions, vbase, vstride, work, v);
+    const float acc = flag == 0 ? ea::attend<true>(sc, positions, vbase, vstride, work, v)
+                                : ea::attend<false>(sc, positions, vbase, vstride, work, v);
     if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * sigmoid_ref(gate);
     FORTAI_ATT_MARK(4);
 }
 
-size_t output_lds_bytes(int max_context) {
-    return ea::output_lds_floats(max_context) * sizeof(float);
-}
+size_t output_lds_bytes() { return ea::work_floats() * sizeof(float); }
 
 }  // namespace
 
@@ -169,15 +155,7 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream) {
     if (group < 1 || group > kMaxGroup || p.heads % p.kv_heads || p.head > kMaxHead || p.head % 8 ||
         p.value % ea::kDims || p.value > p.head || p.rope_dim > p.head || p.rope_dim % 2 || !p.out || !p.partial)
         return hipErrorInvalidValue;
-    const size_t lds = output_lds_bytes(p.max_context);
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
-    static bool raised = false;  // dynamic LDS beyond 64 KiB needs the attribute once per process
-    if (lds > 64 * 1024 && !raised) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(attention_output_kernel),
-            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        raised = true;
-    }
+    const size_t lds = output_lds_bytes();  // independent of the context length
     const int nblk_max = (p.max_context + ea::kPosBlock - 1) / ea::kPosBlock;
     hipLaunchKernelGGL(attention_scores_kernel, dim3(p.kv_heads * nblk_max), dim3(ea::kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();

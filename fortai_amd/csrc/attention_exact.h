@@ -155,14 +155,17 @@ __device__ __forceinline__ void pass_turn(uint64_t *word, int k_next, float acc)
         __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// LDS of the output step, in floats: scores/weights sw[max_context rounded up
-// to kSeg], then 8 reduction slots, kDims handoff words, and one stage of
-// kDims x kSeg products per wave.
+// LDS of the output step, in floats: 8 reduction slots, kDims handoff words
+// and one stage of kDims x kSeg values per wave (work_floats); a caller that
+// keeps the scores in LDS adds sw_floats(max_context) in front.
+__host__ __device__ constexpr size_t work_floats() {
+    return 8 + 2 * kDims + static_cast<size_t>(kWaves) * kDims * kStagePitch;
+}
 __host__ __device__ constexpr size_t sw_floats(int max_context) {
-    return static_cast<size_t>((max_context + kSeg - 1) / kSeg * kSeg);
+    return static_cast<size_t>((max_context + 3) / 4 * 4);
 }
 __host__ __device__ constexpr size_t output_lds_floats(int max_context) {
-    return sw_floats(max_context) + 8 + 2 * kDims + static_cast<size_t>(kWaves) * kDims * kStagePitch;
+    return sw_floats(max_context) + work_floats();
 }
 
 // The value pieces (kDims fp16 = 16 bytes) a lane multiplies for its wave's
@@ -189,13 +192,14 @@ __device__ __forceinline__ void value_prefetch(const uint16_t *vbase, size_t vst
 //   m = max_p s_p;  e_p = expf(s_p - m);  Z = e_0 + e_1 + ... (left to right)
 //   out_j = (e_0/Z) v_0,j + (e_1/Z) v_1,j + ... (left to right, each product
 //   rounded).
-// sw: the n scores (LDS, sw_floats(max_context) floats); work: the rest of
-// output_lds_floats.  The value row of position p starts at vbase + p *
-// vstride (fp16 bits, kDims contiguous); v: value_prefetch of it.  All threads
-// call it; the result is valid in threads 0..kDims-1.
+// scores: the n scores (global memory or LDS; only read).  e_p is evaluated
+// twice, for Z and for the weights (the same value both times).  work:
+// work_floats() floats of LDS.  The value row of position p starts at
+// vbase + p * vstride (fp16 bits, kDims contiguous); v: value_prefetch of it.
+// All threads call it; the result is valid in threads 0..kDims-1.
 template <bool FINITE>
-__device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase, size_t vstride, float *work,
-    ValuePieces &v) {
+__device__ __forceinline__ float attend(const float *scores, int n, const uint16_t *vbase, size_t vstride,
+    float *work, ValuePieces &v) {
     static_assert(kDims == 8, "one 16-byte value piece per position");
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     float *red = work;
@@ -203,6 +207,13 @@ __device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase,
     float *stage = work + 8 + 2 * kDims + wave * kDims * kStagePitch;
     const int nseg = (n + kSeg - 1) / kSeg;
     if (tid < kDims) hand[tid] = 0;
+    // the scores of the wave's next segment, a round ahead (clamped in bounds)
+    float s4[kPieces];
+    auto load_scores = [&](int k) {
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) s4[i] = scores[min(k * kSeg + lane + 64 * i, n - 1)];
+    };
+    if (wave < nseg) load_scores(wave);
 
     // max (any order gives the same value)
     constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
@@ -211,9 +222,9 @@ __device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase,
     for (int p0 = tid; p0 < n; p0 += kThreads * kUnroll) {
         float x[kUnroll];
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k) x[k] = p0 + k * kThreads < n ? sw[p0 + k * kThreads] : kLowest;
+        for (int k = 0; k < kUnroll; ++k) x[k] = scores[min(p0 + k * kThreads, n - 1)];
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k) m = fmaxf(m, x[k]);
+        for (int k = 0; k < kUnroll; ++k) m = fmaxf(m, x[k]);  // clamped duplicates change nothing
     }
     for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
     if (lane == 0) red[wave] = m;
@@ -221,17 +232,18 @@ __device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase,
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     FORTAI_ATT_MARK(1);
 
-    // Z: each wave turns its segments' scores into e_p (kept in sw for the
-    // weights) and sums them when its turn comes
+    // Z: each wave turns its segments' scores into e_p in its stage and sums
+    // them when its turn comes
     f4 r[kSegVec];
     for (int k = wave; k < nseg; k += kWaves) {
         const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
+        float e[kPieces];
 #pragma unroll
-        for (int i = 0; i < kPieces; ++i) {
-            const int p = p0 + lane + 64 * i;
-            sw[p] = p < n ? expf_libm(sw[p] - m) : -0.0f;
-        }
-        seg_read(r, sw + p0);
+        for (int i = 0; i < kPieces; ++i) e[i] = p0 + lane + 64 * i < n ? expf_libm(s4[i] - m) : -0.0f;
+        if (k + kWaves < nseg) load_scores(k + kWaves);
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) stage[lane + 64 * i] = e[i];
+        seg_read(r, stage);
         seg_held<0>(r);
         float acc = take_turn(hand, k);
         acc = seg_chain(r, cnt, acc);
@@ -242,11 +254,12 @@ __device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase,
     FORTAI_ATT_MARK(2);
     __syncthreads();
     if (tid < kDims) hand[tid] = 0;
+    if (wave < nseg) load_scores(wave);
     __syncthreads();
 
     // P.V: each wave writes its segment's products fl(fl(e_p/Z) v_p,j) to its
-    // stage [dim][position], fetches the value pieces of its next segment, and
-    // lanes 0..kDims-1 sum their dim's row when the turn comes
+    // stage [dim][position], fetches the scores and value pieces of its next
+    // segment, and lanes 0..kDims-1 sum their dim's row when the turn comes
     float acc = 0.0f;
     for (int k = wave; k < nseg; k += kWaves) {
         const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
@@ -254,7 +267,7 @@ __device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase,
         for (int i = 0; i < kPieces; ++i) {
             const int j = lane + 64 * i, p = p0 + j;
             if (p < n) {
-                const float wp = sw[p] / z;
+                const float wp = expf_libm(s4[i] - m) / z;
                 const uint32_t hw[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -266,7 +279,10 @@ __device__ __forceinline__ float attend(float *sw, int n, const uint16_t *vbase,
                 for (int d = 0; d < kDims; ++d) stage[d * kStagePitch + j] = -0.0f;
             }
         }
-        if (k + kWaves < nseg) value_fetch(vbase, vstride, n, k + kWaves, v);
+        if (k + kWaves < nseg) {
+            load_scores(k + kWaves);
+            value_fetch(vbase, vstride, n, k + kWaves, v);
+        }
         if (lane < kDims) {
             seg_read(r, stage + lane * kStagePitch);
             seg_held<0>(r);

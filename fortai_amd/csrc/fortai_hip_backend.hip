@@ -962,10 +962,10 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
         key_norm_bytes < static_cast<size_t>(head_size) * sizeof(float) || q->width != k->width ||
         q->width != v->width)
         return FORTAI_HIP_INVALID;
-    // this backend's attention kernels: GQA groups of <= 4, head <= 256, value <= head (multiple of 16),
-    // the scores of one head held in LDS (context <= 36864)
-    if (heads / kv_heads > 4 || head_size > 256 || value_size > head_size || head_size % 8 || value_size % 16 ||
-        max_context > 36864)
+    // this backend's attention kernels: GQA groups of <= 4, head <= 256, value <= head (multiple of 8);
+    // the scores live in global memory, so the context only bounds the buffers' sizes
+    if (heads / kv_heads > 4 || head_size > 256 || value_size > head_size || head_size % 8 || value_size % 8 ||
+        max_context > (1 << 20))
         return FORTAI_HIP_INVALID;
     *layer = nullptr;
     auto *A = new (std::nothrow) fortai_hip_qwen35_attention;

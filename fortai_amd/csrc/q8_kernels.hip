@@ -345,7 +345,6 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
         }
     } else if constexpr (EPI == Epilogue::ADD) {
         if (writer) seg.out[row] = acc + resid;
-        FORTAI_MV_MARK(4);
     } else {
         // fortai_silu_product: vector lanes for the first count/8*8 rows, the
         // libm tail expression for the rest (fortai_q8_dot.c:492-505)
@@ -370,6 +369,7 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
             }
         }
     }
+    FORTAI_MV_MARK(4);
 }
 
 constexpr int kMatvecWaves = 4;  // large launches; small ones use one wave per workgroup

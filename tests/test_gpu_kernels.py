@@ -205,9 +205,10 @@ def test_gdn_core_128_steps(ctx, oracle):
         w.free()
 
 
-@pytest.mark.parametrize("L", [1, 70, 1024, 4096])
+@pytest.mark.parametrize("L", [1, 70, 1024, 4096, 32768])
 def test_attention_core(ctx, oracle, L):
-    """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7, append + attend at position L-1."""
+    """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7, append + attend at position L-1
+    (L up to 32768: the output kernel reads the scores in place, its LDS does not grow with L)."""
     rng = np.random.default_rng(L)
     heads, kvh, head, H = 8, 2, 256, 1024
     mk = lambda rows, width: B.Q8Weights(ctx, synth.q8_blocks(rng, rows, width), rows, width)
