@@ -196,6 +196,113 @@ def bench_matvec(model, copies: int = 275, reps: int = 4):
             "frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
+def _q8(ctx, rng, rows, width):
+    from fortai_amd import backend as B
+    from fortai_amd import synth
+    return B.Q8Weights(ctx, synth.q8_blocks(rng, rows, width), rows, width)
+
+
+def bench_gdn(steps: int = 128, reps: int = 8):
+    """one Gated DeltaNet layer (16 heads x 128, conv K=4
+    over 6144 channels), state ~ N(0, 0.02), 128 autoregressive steps of
+    resident inputs through fortai_hip_qwen35_recurrent_core_device (the
+    conv1d+SiLU kernel and the decoder's delta-rule kernel), replayed from a
+    captured graph."""
+    import ctypes as C
+    import numpy as np
+    from fortai_amd import backend as B
+    ctx = B.Context(0)  # one captured graph per context
+    rng = np.random.default_rng(0x35A08B)
+    H, heads, head, kernel = 1024, 16, 128, 4
+    inner = heads * head
+    conv = 2 * head * heads + inner
+    ws = [_q8(ctx, rng, conv, H), _q8(ctx, rng, inner, H), _q8(ctx, rng, heads, H), _q8(ctx, rng, heads, H),
+          _q8(ctx, rng, H, inner)]
+    layer = B.Recurrent(ctx, *ws, (rng.standard_normal(conv * kernel) * 0.1).astype(np.float32), conv, kernel,
+                        -np.exp(rng.standard_normal(heads) * 0.5).astype(np.float32),
+                        rng.standard_normal(heads).astype(np.float32), np.ones(head, np.float32), head, heads, heads,
+                        head, inner, 1e-6)
+    layer.set_state((rng.standard_normal(heads * head * head) * 0.02).astype(np.float32),
+                    np.zeros((kernel - 1) * conv, np.float32))
+    qkv = ctx.upload_array(rng.standard_normal(steps * conv).astype(np.float32))
+    ab = ctx.upload_array(rng.standard_normal(steps * 2 * heads).astype(np.float32))
+    out = ctx.alloc(inner * 4)
+    ctx.capture_begin()
+    for t in range(steps):
+        at = lambda buf, nbytes: C.c_void_p(buf.ptr.value + nbytes)
+        ctx.call("fortai_hip_qwen35_recurrent_core_device", layer.h, at(qkv, t * conv * 4),
+                 at(ab, t * 2 * heads * 4), at(ab, (t * 2 + 1) * heads * 4), out.ptr)
+    ctx.capture_end()
+    ctx.graph_launch()
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        ctx.graph_launch()
+    us = ctx.timer_stop() * 1e3 / (reps * steps)
+    # state r+w + conv state r+w + conv weights + qkv in + o out + alpha/beta (survey section 8(d), config 2)
+    algo = 2 * heads * head * head * 4 + 2 * (kernel - 1) * conv * 4 + conv * kernel * 4 + conv * 4 + inner * 4 + 2 * heads * 4
+    for b in (qkv, ab, out):
+        b.free()
+    layer.free()
+    for w in ws:
+        w.free()
+    ctx.close()
+    gbps = algo / (us * 1e-6) / 1e9
+    return {"config": f"GDN layer 16x128, conv 4x6144, {steps} autoregressive steps (conv1d+SiLU + delta rule kernels), "
+                      "graph replay", "us_per_step": round(us, 3), "algorithmic_bytes": algo, "gbps": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
+def bench_attention(lengths=(1024, 4096, 32768), calls: int = 16, reps: int = 4):
+    """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7; one K/V
+    append at position L-1, then attention over 0..L-1, through
+    fortai_hip_qwen35_attention_core_device (scores kernel + exact two-pass
+    output kernel), replayed from a captured graph (one context per L)."""
+    import numpy as np
+    from fortai_amd import backend as B
+    heads, kvh, head, H = 8, 2, 256, 1024
+    results = []
+    for L in lengths:
+        ctx = B.Context(0)
+        rng = np.random.default_rng(L)
+        ws = [_q8(ctx, rng, heads * 2 * head, H), _q8(ctx, rng, kvh * head, H), _q8(ctx, rng, kvh * head, H),
+              _q8(ctx, rng, H, heads * head)]
+        A = B.Attention(ctx, *ws, (1 + 0.05 * rng.standard_normal(head)).astype(np.float32),
+                        (1 + 0.05 * rng.standard_normal(head)).astype(np.float32), heads, kvh, head, head, L, 64,
+                        1.0e7, 1e-6)
+        n = L * kvh * head
+        A.set_cache(rng.standard_normal(n).astype(np.float16).view(np.uint16),
+                    rng.standard_normal(n).astype(np.float16).view(np.uint16), L)
+        dq = ctx.upload_array(rng.standard_normal(heads * 2 * head).astype(np.float32))
+        dk = ctx.upload_array(rng.standard_normal(kvh * head).astype(np.float32))
+        dv = ctx.upload_array(rng.standard_normal(kvh * head).astype(np.float32))
+        do = ctx.alloc(heads * head * 4)
+        ctx.set_position(L - 1)
+        ctx.capture_begin()
+        for _ in range(calls):
+            ctx.call("fortai_hip_qwen35_attention_core_device", A.h, dq.ptr, dk.ptr, dv.ptr, do.ptr)
+        ctx.capture_end()
+        ctx.graph_launch()
+        ctx.synchronize()
+        ctx.timer_start()
+        for _ in range(reps):
+            ctx.graph_launch()
+        us = ctx.timer_stop() * 1e3 / (reps * calls)
+        # KV read 2048 B per position + the append + q/k/v in and the output (survey section 8(d), config 3)
+        algo = 2048 * L + 2048 + (heads * 2 * head + 2 * kvh * head + heads * head) * 4
+        gbps = algo / (us * 1e-6) / 1e9
+        results.append({"L": L, "us_per_step": round(us, 2), "algorithmic_bytes": algo, "gbps": round(gbps, 1),
+                        "frac": round(gbps / HBM_PEAK_GBPS, 4)})
+        for b in (dq, dk, dv, do):
+            b.free()
+        A.free()
+        for w in ws:
+            w.free()
+        ctx.close()
+    return {"config": "8 q / 2 kv heads x 256, fp16 KV, append + exact attention at position L-1, graph replay",
+            "lengths": results}
+
+
 def cpu_baseline(path, ctx_len: int, steps: int):
     """The reference CPU decode (oracle/_ref/fortai_cpu_run) on this host."""
     exe = os.path.join(ROOT, "oracle", "_ref", "fortai_cpu_run")
@@ -268,6 +375,7 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the config 2 (GDN) and config 3 (attention) figures")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the kernels the --pmc traffic passes measure (see traffic_probe)")
     ap.add_argument("--no-graph", action="store_true",
@@ -294,6 +402,9 @@ def main() -> int:
     tok_s = args.steps / (wall_ms * 1e-3)
     roof = lm_head_roofline(model)
     mv = None if args.no_matvec else bench_matvec(model)
+    kernels = None
+    if not args.no_kernels:
+        kernels = {"gdn_step": bench_gdn(), "attention": bench_attention()}
     d = model.d
     decoder = "persistent (one launch per token)" if model.decoder.persistent else "HIP graph of per-op kernels"
     step_bytes = bytes_per_token(d, args.ctx - args.steps // 2)
@@ -323,6 +434,7 @@ def main() -> int:
                        "frac_of_8TBps": round(decode_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": roof,
         "matvec": mv,
+        "kernels": kernels,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -211,11 +211,10 @@ MatvecInput q8_input(const int8_t *xq, int width) {
 bool owned(const fortai_hip_q8_context *c, const fortai_hip_q8_weights *w) { return w && w->context == c; }
 
 GdnParams gdn_params(fortai_hip_qwen35_recurrent *L, const float *qkv, const float *alpha, const float *beta,
-    float *out, void *out_q8l) {
+    float *out) {
     GdnParams p;
-    p.qkv = qkv; p.z = L->z_out; p.alpha = alpha; p.beta = beta; p.ssm_a = L->ssm_a; p.ssm_dt = L->ssm_dt;
-    p.ssm_norm = L->ssm_norm; p.conv_w = L->conv_w; p.conv_state = L->conv_state; p.state = L->state;
-    p.out = out; p.out_q8l = out_q8l; p.conv_size = L->conv_size; p.kernel = L->kernel;
+    p.qkv = qkv; p.alpha = alpha; p.beta = beta; p.ssm_a = L->ssm_a; p.ssm_dt = L->ssm_dt;
+    p.state = L->state; p.out = out;
     p.state_size = L->state_size; p.key_heads = L->key_heads; p.value_heads = L->value_heads; p.head = L->head;
     p.eps = L->eps;
     return p;
@@ -233,7 +232,7 @@ hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &
     segs[0].kernel = L->kernel;
     segs[1].silu = true;  // the gate is only used through SiLU
     hipError_t e = launch_q8_matvec(segs, 4, in, pro, Epilogue::STORE, stream);
-    if (e == hipSuccess) e = launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw, nullptr), stream);
+    if (e == hipSuccess) e = launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw), stream);
     if (e != hipSuccess) return e;
     MatvecInput gated;
     gated.x = L->o_raw;
@@ -899,8 +898,13 @@ int fortai_hip_qwen35_recurrent_core_device(fortai_hip_qwen35_recurrent *L, cons
     if (!L || !L->context || !qkv || !alpha || !beta || !out) return FORTAI_HIP_INVALID;
     auto *c = L->context;
     (void)hipSetDevice(c->device);
-    return done(c, launch_gdn_step(gdn_params(L, static_cast<const float *>(qkv), static_cast<const float *>(alpha),
-        static_cast<const float *>(beta), static_cast<float *>(out), nullptr), c->stream), "Qwen recurrent core");
+    // conv1d + SiLU into the layer's qkv buffer (the caller's qkv is only read), then the delta rule
+    hipError_t e = launch_conv_silu(static_cast<const float *>(qkv), L->conv_w, L->conv_state, L->qkv_out, L->conv_size,
+        L->kernel, c->stream);
+    if (e == hipSuccess)
+        e = launch_gdn_delta(gdn_params(L, L->qkv_out, static_cast<const float *>(alpha),
+            static_cast<const float *>(beta), static_cast<float *>(out)), c->stream);
+    return done(c, e, "Qwen recurrent core");
 }
 
 int fortai_hip_qwen35_recurrent_state_download(fortai_hip_qwen35_recurrent *L, float *gdn, size_t gdn_bytes,

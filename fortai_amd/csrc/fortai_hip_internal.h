@@ -100,6 +100,25 @@ __device__ __forceinline__ float silu_poly(float x) {
     return r;
 }
 
+// Causal conv1d + SiLU of one channel (fortai_qwen35_cpu.f90:856-867): the
+// window's K-1 values oldest first, then the current value x last, each
+// product added in order; slots at or past K-1 (window) or K (taps) are
+// unused.  The caller shifts the window (:870-879).
+constexpr int kConvMax = 8;
+__device__ __forceinline__ float conv_silu(const float (&win)[kConvMax - 1], const float (&taps)[kConvMax], int K,
+    float x) {
+    float a = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kConvMax - 1; ++t)
+        if (t < K - 1) a = a + taps[t] * win[t];
+    float last = 0.0f;
+#pragma unroll
+    for (int t = 0; t < kConvMax; ++t)
+        if (t == K - 1) last = taps[t];
+    a = a + last * x;
+    return silu_poly(a);
+}
+
 // expf of the C library the reference CPU path links (the Fortran real32
 // exp intrinsic calls it): glibc's algorithm from ARM optimized-routines
 // (sysdeps/ieee754/flt-32/e_expf.c, x86-64 FMA build).  x * 32/ln2 = k + r,

@@ -126,27 +126,22 @@ hipError_t launch_count_nonfinite_halves(const uint16_t *w, size_t n, unsigned i
 
 // ---- Gated DeltaNet ------------------------------------------------------
 struct GdnParams {
-    const float *qkv = nullptr;       // [conv_size] projection output (pre-conv)
-    const float *z = nullptr;         // [value_heads * head] gate projection (pre-SiLU)
+    const float *qkv = nullptr;       // [conv_size] conv + SiLU outputs (q | k | v channels)
     const float *alpha = nullptr;     // [value_heads]
     const float *beta = nullptr;      // [value_heads]
     const float *ssm_a = nullptr;     // [value_heads]
     const float *ssm_dt = nullptr;    // [value_heads]
-    const float *ssm_norm = nullptr;  // [head]
-    const float *conv_w = nullptr;    // [conv_size][kernel]
-    float *conv_state = nullptr;      // [kernel-1][conv_size], oldest first (reference layout)
     float *state = nullptr;           // [value_heads][head][8 lanes][head/8] (lane-major rows)
-    float *out = nullptr;             // optional [value_heads * head] raw o (before the gated norm)
-    void *out_q8l = nullptr;          // optional Q8L of the gated output (ssm_out input)
-    int conv_size = 0, kernel = 0, state_size = 0, key_heads = 0, value_heads = 0, head = 0;
+    float *out = nullptr;             // [value_heads * head] raw o (before the gated norm)
+    int state_size = 0, key_heads = 0, value_heads = 0, head = 0;
     float eps = 0.0f;
 };
-hipError_t launch_gdn_step(const GdnParams &p, hipStream_t stream);
-// The delta-rule part alone, 16 state rows per workgroup: qkv holds the
-// conv + SiLU outputs (the projection epilogue computed them and shifted the
-// window); writes the raw output o to p.out (the gated norm is the ssm_out
-// prologue).  z, conv_w, conv_state and out_q8l are not used.
+// The delta rule, 16 state rows per workgroup: writes the raw output o.
 hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream);
+// Causal conv1d + SiLU of every channel of x, shifting the windows
+// conv_state[K-1][channels] (oldest first).
+hipError_t launch_conv_silu(const float *x, const float *conv_w, float *conv_state, float *out, int channels, int K,
+    hipStream_t stream);
 
 // ---- attention -------------------------------------------------------------
 struct AttentionParams {

@@ -56,7 +56,6 @@ __device__ __forceinline__ uint32_t load_u32_unaligned(const int8_t *p) {
 // (act_store): the compiler's in-order vmcnt waits for the activation then do
 // not wait for the weights.
 constexpr int kMaxChunks = 96;  // Q8L activations up to 12288 wide
-constexpr int kConvMax = 8;     // conv epilogue: kernel width limit
 
 template <int THREADS, Prologue PRO>
 struct ActShape {
@@ -324,18 +323,8 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     if constexpr (kPair) acc2 = row_hsum8(acc2);
     if constexpr (EPI == Epilogue::STORE) {
         if (conv && writer) {
-            // fortai_qwen35_cpu.f90:856-879: oldest slot first, the current value
-            // last; then the window moves by one (only this thread touches it)
-            float a = 0.0f;
-#pragma unroll
-            for (int t = 0; t < kConvMax - 1; ++t)
-                if (t < ck - 1) a = a + taps[t] * win[t];
-            float last = 0.0f;
-#pragma unroll
-            for (int t = 0; t < kConvMax; ++t)
-                if (t == ck - 1) last = taps[t];
-            a = a + last * acc;
-            seg.out[row] = silu_poly(a);
+            // the window then moves by one (only this thread touches it)
+            seg.out[row] = conv_silu(win, taps, ck, acc);
 #pragma unroll
             for (int t = 0; t + 1 < kConvMax - 1; ++t)
                 if (t + 1 < ck - 1) seg.conv_state[static_cast<size_t>(t) * seg.conv_size + row] = win[t + 1];
