@@ -19,6 +19,10 @@
 
 using namespace fortai_hip;
 
+// per-workgroup (value, index) partials of a fused argmax held by a context
+// (the fp16 LM head uses one per 128 rows: vocabularies up to 524,288)
+constexpr int kArgmaxParts = 4096;
+
 struct fortai_hip_q8_context {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -304,8 +308,8 @@ int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context) {
     if (e == hipSuccess) e = hipEventCreate(&c->stop);
     if (e == hipSuccess) e = alloc(&c->position, 1);
     if (e == hipSuccess) e = alloc(&c->token, 1);
-    if (e == hipSuccess) e = alloc(&c->argmax_value, 1024);
-    if (e == hipSuccess) e = alloc(&c->argmax_index, 1024);
+    if (e == hipSuccess) e = alloc(&c->argmax_value, kArgmaxParts);
+    if (e == hipSuccess) e = alloc(&c->argmax_index, kArgmaxParts);
     if (e == hipSuccess) e = hipMemsetAsync(c->position, 0, sizeof(int), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->token, 0, sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -605,7 +609,7 @@ int fortai_hip_f16_matvec_device(fortai_hip_q8_context *c, const fortai_hip_f16_
     if (!c || !w || w->context != c || !device_activation || !device_output ||
         activation_elements != static_cast<size_t>(w->width) || output_elements < static_cast<size_t>(w->rows))
         return FORTAI_HIP_INVALID;
-    if (device_token && f16_matvec_workgroups(w->rows) > 1024) return FORTAI_HIP_INVALID;
+    if (device_token && f16_matvec_workgroups(w->rows) > kArgmaxParts) return FORTAI_HIP_INVALID;
     (void)hipSetDevice(c->device);
     ArgmaxState st;
     st.partial_value = c->argmax_value;
