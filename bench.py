@@ -253,23 +253,34 @@ def bench_gdn(steps: int = 128, reps: int = 8):
             "frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
-def bench_attention(lengths=(1024, 4096, 32768), calls: int = 16, reps: int = 4):
+def bench_attention(cases=((1024, None), (4096, None), (32768, None), (32768, 1 << 20)), calls: int = 16,
+                    reps: int = 4):
     """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7; one K/V
     append at position L-1, then attention over 0..L-1, through
     fortai_hip_qwen35_attention_core_device (scores kernel + exact two-pass
-    output kernel), replayed from a captured graph (one context per L)."""
+    output kernel up to FORTAI_HIP_EXACT_ATTENTION_MAX positions, split-K
+    beyond), replayed from a captured graph (one context per case).  A case
+    is (L, exact_max); exact_max None is the default (8192)."""
     import numpy as np
     from fortai_amd import backend as B
     heads, kvh, head, H = 8, 2, 256, 1024
     results = []
-    for L in lengths:
+    for L, exact_max in cases:
         ctx = B.Context(0)
         rng = np.random.default_rng(L)
         ws = [_q8(ctx, rng, heads * 2 * head, H), _q8(ctx, rng, kvh * head, H), _q8(ctx, rng, kvh * head, H),
               _q8(ctx, rng, H, heads * head)]
+        saved = os.environ.get("FORTAI_HIP_EXACT_ATTENTION_MAX")
+        if exact_max is not None:
+            os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = str(exact_max)
         A = B.Attention(ctx, *ws, (1 + 0.05 * rng.standard_normal(head)).astype(np.float32),
                         (1 + 0.05 * rng.standard_normal(head)).astype(np.float32), heads, kvh, head, head, L, 64,
                         1.0e7, 1e-6)
+        if saved is None:
+            os.environ.pop("FORTAI_HIP_EXACT_ATTENTION_MAX", None)
+        else:
+            os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = saved
+        path = "exact two-pass" if L <= (8192 if exact_max is None else exact_max) else "split-K (1e-3)"
         n = L * kvh * head
         A.set_cache(rng.standard_normal(n).astype(np.float16).view(np.uint16),
                     rng.standard_normal(n).astype(np.float16).view(np.uint16), L)
@@ -291,8 +302,8 @@ def bench_attention(lengths=(1024, 4096, 32768), calls: int = 16, reps: int = 4)
         # KV read 2048 B per position + the append + q/k/v in and the output (survey section 8(d), config 3)
         algo = 2048 * L + 2048 + (heads * 2 * head + 2 * kvh * head + heads * head) * 4
         gbps = algo / (us * 1e-6) / 1e9
-        results.append({"L": L, "us_per_step": round(us, 2), "algorithmic_bytes": algo, "gbps": round(gbps, 1),
-                        "frac": round(gbps / HBM_PEAK_GBPS, 4)})
+        results.append({"L": L, "path": path, "us_per_step": round(us, 2), "algorithmic_bytes": algo,
+                        "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)})
         for b in (dq, dk, dv, do):
             b.free()
         A.free()

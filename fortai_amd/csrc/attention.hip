@@ -125,6 +125,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     const int pos = *p.position;
     if (pos < 0 || pos >= p.max_context) return;
     const int positions = pos + 1;
+    if (positions > p.exact_max) return;  // the split-K kernels cover this position
     const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
     const int slices = VD / ea::kDims;
     const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * ea::kDims;
@@ -146,12 +147,223 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
 
 size_t output_lds_bytes() { return ea::work_floats() * sizeof(float); }
 
+// ---------------------------------------------------------------- split-K
+// Beyond exact_max positions: each workgroup takes one kv head and a chunk of
+// kChunk positions for the whole GQA group: the chunk's max m_c, Z_c =
+// sum exp(s - m_c) and o_c = sum exp(s - m_c) v, which the merge kernel
+// combines per head: M = max m_c, Z = sum Z_c e^(m_c - M),
+// out = (sum o_c e^(m_c - M)) / Z * sigmoid(gate) (flash-decoding).  The
+// scores are the scores kernel's (the reference's per-position dots).
+constexpr int kChunk = 256;
+
+__device__ __forceinline__ float block_max256(float v, float *red) {
+    for (int k = 32; k >= 1; k >>= 1) v = fmaxf(v, __shfl_xor(v, k));
+    const int tid = static_cast<int>(threadIdx.x);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+    for (int k = 32; k >= 1; k >>= 1) v += __shfl_xor(v, k);
+    const int tid = static_cast<int>(threadIdx.x);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Per-workgroup split-K partials of one kv head and chunk for the GQA group.
+// Thread t takes the 8-dim value slice t % 32 of positions t / 32 + 8 i (all
+// 32 of its 16-byte value loads in flight at once), then the 8 position
+// groups are summed through LDS.
+constexpr int kSplitSlices = 32;                    // 8-dim slices: value dims <= 256
+constexpr int kSplitGroups = 256 / kSplitSlices;    // position groups
+constexpr int kSplitPer = kChunk / kSplitGroups;    // positions per thread
+static_assert(kChunk <= 256 && kChunk % kSplitGroups == 0, "one score per thread; whole position groups");
+
+struct SplitLds {
+    float e[kMaxGroup][kChunk];
+    float red4[kMaxGroup][4];
+    float part[kMaxGroup][kSplitGroups][kSplitSlices * 8];
+};
+
+template <bool FINITE>
+__device__ __forceinline__ void split_chunk(const AttentionParams &p, int kvh, int c, int nmax, int p0, int n,
+    SplitLds &L) {
+    const int tid = static_cast<int>(threadIdx.x);
+    const int group = p.heads / p.kv_heads, VD = p.value, NKV = p.kv_heads;
+    const int slice = tid % kSplitSlices, pg = tid / kSplitSlices;
+    // the scores of every head, then the value loads (the in-order wait for
+    // the scores then does not include the values)
+    float sc[kMaxGroup], m[kMaxGroup], z[kMaxGroup];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+        sc[g] = g < group ? p.partial[static_cast<size_t>(kvh * group + g) * p.max_context + p0 + min(tid, n - 1)]
+                          : 0.0f;
+    // slices past VD re-read slice 0
+    const int d0 = (slice * 8 < VD ? slice : 0) * 8;
+    const uint16_t *vb = p.vcache + (static_cast<size_t>(p0) * NKV + kvh) * VD + d0;
+    const size_t vs = static_cast<size_t>(NKV) * VD;
+    uint4 vv[kSplitPer];
+#pragma unroll
+    for (int i = 0; i < kSplitPer; ++i)
+        vv[i] = *reinterpret_cast<const uint4 *>(vb + static_cast<size_t>(min(pg + kSplitGroups * i, n - 1)) * vs);
+    FORTAI_ATT_MARK(12);
+    // the four heads' max and sum, reduced together
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        m[g] = tid < n ? sc[g] : -__builtin_inff();
+        for (int k = 32; k >= 1; k >>= 1) m[g] = fmaxf(m[g], __shfl_xor(m[g], k));
+    }
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) L.red4[g][tid >> 6] = m[g];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        m[g] = fmaxf(fmaxf(L.red4[g][0], L.red4[g][1]), fmaxf(L.red4[g][2], L.red4[g][3]));
+        const float ev = (g < group && tid < n) ? expf_libm(sc[g] - m[g]) : 0.0f;
+        if (tid < kChunk) L.e[g][tid] = ev;
+        z[g] = ev;
+        for (int k = 32; k >= 1; k >>= 1) z[g] += __shfl_xor(z[g], k);
+    }
+    __syncthreads();  // every wave has read red4
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) L.red4[g][tid >> 6] = z[g];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) z[g] = (L.red4[g][0] + L.red4[g][1]) + (L.red4[g][2] + L.red4[g][3]);
+    FORTAI_ATT_MARK(13);
+    float acc[kMaxGroup][8];
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[g][d] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSplitPer; ++i) {
+        const int j = pg + kSplitGroups * i;
+        if (j >= n) continue;
+        const uint32_t hw[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+        float v8[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v8[2 * q] = ea::kv<FINITE>(static_cast<uint16_t>(hw[q] & 0xffffu));
+            v8[2 * q + 1] = ea::kv<FINITE>(static_cast<uint16_t>(hw[q] >> 16));
+        }
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            if (g >= group) break;
+            const float ej = L.e[g][j];
+#pragma unroll
+            for (int d = 0; d < 8; ++d) acc[g][d] = __builtin_fmaf(ej, v8[d], acc[g][d]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= group) break;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) L.part[g][pg][slice * 8 + d] = acc[g][d];
+    }
+    __syncthreads();
+    FORTAI_ATT_MARK(14);
+    if (tid >= VD) return;
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g) {
+        if (g >= group) break;
+        float o = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kSplitGroups; ++k) o += L.part[g][k][tid];
+        float *dst = p.split + (static_cast<size_t>(kvh * group + g) * nmax + c) * (VD + 2);
+        dst[tid] = o;
+        if (tid == 0) {
+            dst[VD] = m[g];
+            dst[VD + 1] = z[g];
+        }
+    }
+}
+
+__global__ __launch_bounds__(ea::kThreads) void attention_split_kernel(const AttentionParams p) {
+    __shared__ SplitLds L;
+    const int pos = *p.position;
+    if (pos < 0 || pos >= p.max_context) return;
+    const int positions = pos + 1;
+    if (positions <= p.exact_max) return;  // the exact kernel covers this position
+    const int nmax = (p.max_context + kChunk - 1) / kChunk;
+    const int kvh = static_cast<int>(blockIdx.x) / nmax, c = static_cast<int>(blockIdx.x) % nmax;
+    const int p0 = c * kChunk;
+    if (p0 >= positions) return;
+    const int n = min(kChunk, positions - p0);
+    if (p.cache_flags[kvh] == 0) split_chunk<true>(p, kvh, c, nmax, p0, n, L);
+    else split_chunk<false>(p, kvh, c, nmax, p0, n, L);
+}
+
+// Per head and 64 value dims: the chunks' scale factors e^(m_c - M) once into
+// LDS, then each dim's chunk partials summed by four threads (a quarter of the
+// chunks each, 32 loads in flight) and combined through LDS.
+constexpr int kMaxSplitChunks = 4096;  // contexts up to 1M positions
+constexpr int kMergeDims = 64;
+constexpr int kMergeParts = ea::kThreads / kMergeDims;
+constexpr int kMergeBatch = 32;
+
+__global__ __launch_bounds__(ea::kThreads) void attention_merge_kernel(const AttentionParams p) {
+    __shared__ float f[kMaxSplitChunks];
+    __shared__ float red[4];
+    __shared__ float part[kMergeParts][kMergeDims];
+    const int pos = *p.position;
+    if (pos < 0 || pos >= p.max_context) return;
+    const int positions = pos + 1;
+    if (positions <= p.exact_max) return;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int VD = p.value, HD = p.head;
+    const int slices = (VD + kMergeDims - 1) / kMergeDims;
+    const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * kMergeDims;
+    const int nmax = (p.max_context + kChunk - 1) / kChunk, chunks = (positions + kChunk - 1) / kChunk;
+    const float *base = p.split + static_cast<size_t>(h) * nmax * (VD + 2);
+    float mx = -__builtin_inff();
+    for (int c = tid; c < chunks; c += ea::kThreads) mx = fmaxf(mx, base[static_cast<size_t>(c) * (VD + 2) + VD]);
+    mx = block_max256(mx, red);
+    float zp = 0.0f;
+    for (int c = tid; c < chunks; c += ea::kThreads) {
+        const float *row = base + static_cast<size_t>(c) * (VD + 2);
+        const float fc = expf_libm(row[VD] - mx);
+        f[c] = fc;
+        zp = __builtin_fmaf(row[VD + 1], fc, zp);
+    }
+    const float z = block_sum256(zp, red);  // (its barriers also publish f)
+    const int dl = tid % kMergeDims, q = tid / kMergeDims, d = min(d0 + dl, VD - 1);
+    const int per = (chunks + kMergeParts - 1) / kMergeParts, c0 = q * per, c1 = min(chunks, c0 + per);
+    float o = 0.0f;
+    for (int cb = c0; cb < c1; cb += kMergeBatch) {
+        float x[kMergeBatch];
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) x[u] = base[static_cast<size_t>(min(cb + u, c1 - 1)) * (VD + 2) + d];
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+            if (cb + u < c1) o = __builtin_fmaf(x[u], f[cb + u], o);
+    }
+    part[q][dl] = o;
+    __syncthreads();
+    if (q != 0 || d0 + dl >= VD) return;
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMergeParts; ++k) sum += part[k][dl];
+    const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + dl];
+    p.out[static_cast<size_t>(h) * VD + d0 + dl] = (sum / z) * sigmoid_ref(gate);
+}
+
 }  // namespace
 
 size_t attention_scores_floats(int heads, int max_context) { return static_cast<size_t>(heads) * max_context; }
 
+int attention_split_chunks(int max_context) { return (max_context + kChunk - 1) / kChunk; }
+
 hipError_t launch_attention(const AttentionParams &p, hipStream_t stream) {
     const int group = p.kv_heads > 0 ? p.heads / p.kv_heads : 0;
+    if (p.max_context > p.exact_max && (!p.split || attention_split_chunks(p.max_context) > kMaxSplitChunks))
+        return hipErrorInvalidValue;
     if (group < 1 || group > kMaxGroup || p.heads % p.kv_heads || p.head > kMaxHead || p.head % 8 ||
         p.value % ea::kDims || p.value > p.head || p.rope_dim > p.head || p.rope_dim % 2 || !p.out || !p.partial)
         return hipErrorInvalidValue;
@@ -161,6 +373,15 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims)), dim3(ea::kThreads), lds, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess || p.max_context <= p.exact_max) return e;
+    // long contexts: the split-K pair (each kernel picks its regime from the device position)
+    hipLaunchKernelGGL(attention_split_kernel, dim3(p.kv_heads * attention_split_chunks(p.max_context)),
+        dim3(ea::kThreads), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(p.heads * ((p.value + kMergeDims - 1) / kMergeDims)),
+        dim3(ea::kThreads), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -81,6 +81,8 @@ struct fortai_hip_qwen35_attention {
     float *q_out = nullptr, *k_out = nullptr, *v_out = nullptr, *partial = nullptr;
     int *cache_flags = nullptr;  // per kv head: the cache holds an exponent-31 half
     float *attn_out = nullptr;   // gated attention output (o_proj input)
+    int exact_max = 0;           // positions with the bit-exact two-pass softmax; split-K beyond
+    float *split = nullptr;      // split-K partials (allocated when max_context > exact_max)
 };
 
 struct decoder_layer {
@@ -256,7 +258,7 @@ AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q,
     p.kcache = A->kcache; p.vcache = A->vcache; p.partial = A->partial; p.cache_flags = A->cache_flags; p.out = out;
     p.position = A->context->position; p.heads = A->heads; p.kv_heads = A->kv_heads; p.head = A->head;
     p.value = A->value; p.max_context = A->max_context; p.rope_dim = A->rope_dim;
-    p.eps = A->eps;
+    p.eps = A->eps; p.exact_max = A->exact_max; p.split = A->split;
     return p;
 }
 
@@ -1003,6 +1005,13 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
     if (e == hipSuccess) e = alloc(&A->v_out, static_cast<size_t>(kv_heads) * value_size);
     if (e == hipSuccess) e = alloc(&A->attn_out, static_cast<size_t>(heads) * value_size);
     if (e == hipSuccess) e = alloc(&A->partial, attention_scores_floats(heads, max_context));
+    // FORTAI_HIP_EXACT_ATTENTION_MAX: the positions up to which the attention
+    // output keeps the reference's summation orders (default 8192); beyond
+    // them the split-K path (within 1e-3 relative) takes over
+    A->exact_max = 8192;
+    if (const char *env = std::getenv("FORTAI_HIP_EXACT_ATTENTION_MAX")) A->exact_max = std::max(0, std::atoi(env));
+    if (e == hipSuccess && max_context > A->exact_max)
+        e = alloc(&A->split, static_cast<size_t>(heads) * attention_split_chunks(max_context) * (value_size + 2));
     if (e == hipSuccess) e = alloc(&A->cache_flags, kv_heads);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
@@ -1026,7 +1035,7 @@ int fortai_hip_qwen35_attention_destroy(fortai_hip_qwen35_attention *A) {
     }
     release(A->q_norm); release(A->k_norm); release(A->rope); release(A->kcache); release(A->vcache);
     release(A->q_out); release(A->k_out); release(A->v_out); release(A->partial); release(A->cache_flags);
-    release(A->attn_out);
+    release(A->attn_out); release(A->split);
     delete A;
     return FORTAI_HIP_OK;
 }

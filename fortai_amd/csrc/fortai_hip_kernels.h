@@ -159,7 +159,14 @@ struct AttentionParams {
     const int *position = nullptr;  // device position (the new token's index)
     int heads = 0, kv_heads = 0, head = 0, value = 0, max_context = 0, rope_dim = 0;
     float eps = 0.0f;
+    // Up to exact_max positions the output is the reference's two-pass softmax
+    // with its summation orders (bit-exact); beyond, split-K over chunks of
+    // the context with an online-softmax merge (within 1e-3 relative).  The
+    // split-K kernels are launched only when max_context > exact_max.
+    int exact_max = 1 << 30;
+    float *split = nullptr;         // [heads][attention_split_chunks][value + 2]
 };
+int attention_split_chunks(int max_context);
 hipError_t launch_attention(const AttentionParams &p, hipStream_t stream);
 size_t attention_scores_floats(int heads, int max_context);
 

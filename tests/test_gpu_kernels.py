@@ -6,6 +6,8 @@ reproduces the reference's lane order exactly (Q8 matvec, GDN step, F16 LM
 head) the tests demand bit-identical floats, which is stricter.
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -205,10 +207,13 @@ def test_gdn_core_128_steps(ctx, oracle):
         w.free()
 
 
-@pytest.mark.parametrize("L", [1, 70, 1024, 4096, 32768])
-def test_attention_core(ctx, oracle, L):
-    """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7, append + attend at position L-1
-    (L up to 32768: the output kernel reads the scores in place, its LDS does not grow with L)."""
+@pytest.mark.parametrize("L,exact_max", [(1, None), (70, None), (1024, None), (4096, None), (32768, None),
+                                         (32768, 1 << 20), (70, 0), (1024, 0), (4095, 0)])
+def test_attention_core(ctx, oracle, L, exact_max):
+    """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7, append + attend at position L-1.
+    Up to FORTAI_HIP_EXACT_ATTENTION_MAX positions (default 8192) the output keeps the reference's two-pass
+    summation orders and is bit-exact; beyond it, split-K with an online-softmax merge, within the north
+    star's 1e-3 relative.  exact_max None: the default; 1 << 20: exact at 32768; 0: split-K at every L."""
     rng = np.random.default_rng(L)
     heads, kvh, head, H = 8, 2, 256, 1024
     mk = lambda rows, width: B.Q8Weights(ctx, synth.q8_blocks(rng, rows, width), rows, width)
@@ -216,7 +221,16 @@ def test_attention_core(ctx, oracle, L):
     qn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     kn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     maxc = max(L, 64)
-    A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
+    saved = os.environ.get("FORTAI_HIP_EXACT_ATTENTION_MAX")
+    if exact_max is not None:
+        os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = str(exact_max)  # read when the layer is created
+    try:
+        A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
+    finally:
+        if saved is None:
+            os.environ.pop("FORTAI_HIP_EXACT_ATTENTION_MAX", None)
+        else:
+            os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = saved
     kc = np.zeros(maxc * kvh * head, np.uint16)
     vc = np.zeros(maxc * kvh * head, np.uint16)
     n = (L - 1) * kvh * head
@@ -238,8 +252,13 @@ def test_attention_core(ctx, oracle, L):
     gk, gv = A.cache(L)
     assert np.array_equal(gk, kc[:L * kvh * head]), "K cache after append must be bit-exact"
     assert np.array_equal(gv, vc[:L * kvh * head]), "V cache after append must be bit-exact"
-    # the reference's two-pass softmax with its summation orders: bit-exact
-    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"max diff {np.max(np.abs(got - want))}"
+    limit = 8192 if exact_max is None else exact_max
+    if L <= limit:
+        # the reference's two-pass softmax with its summation orders: bit-exact
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"max diff {np.max(np.abs(got - want))}"
+    else:
+        assert rel_err(got, want) <= REL, f"split-K attention off by {rel_err(got, want)}"
+        assert not np.array_equal(got, np.zeros_like(got))
     A.free()
     for w in ws:
         w.free()
