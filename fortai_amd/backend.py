@@ -73,6 +73,10 @@ _SIGNATURES = {
     "fortai_hip_argmax_device": [_vp, _vp, _sz, _vp],
     "fortai_hip_q8_quantize_device": [_vp, _vp, _sz, _vp, _vp],
     "fortai_hip_q8_block_dots_device": [_vp, _vp, _vp, _vp],
+    "fortai_hip_q8_tokens_bytes": [_i, _i],
+    "fortai_hip_q8_quantize_tokens_device": [_vp, _vp, _i, _i, _vp],
+    "fortai_hip_q8_mmq_device": [_vp, _vp, _vp, _i, _vp, _vp, _fp],
+    "fortai_hip_q8_mmq_block_dots": [_vp, _vp, _vp, _i, _vp],
     "fortai_hip_qwen35_recurrent_core_device": [_vp, _vp, _vp, _vp, _vp],
     "fortai_hip_qwen35_recurrent_state_download": [_vp, _vp, _sz, _vp, _sz],
     "fortai_hip_qwen35_recurrent_state_upload": [_vp, _vp, _sz, _vp, _sz],
@@ -91,7 +95,7 @@ _SIGNATURES = {
     "fortai_hip_qwen35_decoder_persistent": [_vp],
     "fortai_hip_qwen35_decoder_phase_times": [_vp, _vp, C.c_size_t],
 }
-_RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p}
+_RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p, "fortai_hip_q8_tokens_bytes": C.c_size_t}
 
 _lib: Optional[C.CDLL] = None
 

@@ -652,6 +652,49 @@ int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *c, const fortai_hip_q
         static_cast<int32_t *>(device_dots), c->stream), "device block dots");
 }
 
+// ------------------------------------------------------ token blocks (MFMA)
+size_t fortai_hip_q8_tokens_bytes(int tokens, int width) {
+    if (tokens <= 0 || width <= 0 || width % kQ8Block) return 0;
+    return q8_tokens_bytes(tokens, width);
+}
+
+int fortai_hip_q8_quantize_tokens_device(fortai_hip_q8_context *c, const void *x, int tokens, int width, void *x8) {
+    if (!c || !x || !x8 || tokens <= 0 || width <= 0 || width % kQ8Block) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    return done(c, launch_q8_quantize_tokens(static_cast<const float *>(x), tokens, width, width, x8, c->stream),
+        "quantize tokens");
+}
+
+int fortai_hip_q8_mmq_device(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x8, int tokens,
+    void *out, const void *resid, float *kernel_ms) {
+    if (!c || !owned(c, w) || !x8 || !out || tokens <= 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipSuccess;
+    if (kernel_ms) e = hipEventRecord(c->start, c->stream);
+    if (e == hipSuccess)
+        e = launch_q8_mmq(w->m, x8, tokens, static_cast<float *>(out), w->m.rows, static_cast<const float *>(resid),
+            nullptr, c->stream);
+    if (kernel_ms) {
+        if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+        if (e == hipSuccess) e = hipEventElapsedTime(kernel_ms, c->start, c->stop);
+    }
+    return done(c, e, "token-block matmul");
+}
+
+int fortai_hip_q8_mmq_block_dots(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x8,
+    int tokens, void *dots) {
+    if (!c || !owned(c, w) || !x8 || !dots || tokens <= 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    float *scratch = nullptr;
+    hipError_t e = hipMalloc(&scratch, static_cast<size_t>(tokens) * w->m.rows * sizeof(float));
+    if (e == hipSuccess)
+        e = launch_q8_mmq(w->m, x8, tokens, scratch, w->m.rows, nullptr, static_cast<int32_t *>(dots), c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (scratch) (void)hipFree(scratch);
+    return done(c, e, "token-block dots");
+}
+
 // ----------------------------------------------------------------- host ops
 namespace {
 struct host_request {

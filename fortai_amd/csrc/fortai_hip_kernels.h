@@ -124,6 +124,17 @@ hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStrea
 // scan an fp16 table for exponent-31 patterns (inf/NaN), counted into *count
 hipError_t launch_count_nonfinite_halves(const uint16_t *w, size_t n, unsigned int *count, hipStream_t stream);
 
+// ---- token blocks on the i8 matrix cores (mmq.hip) --------------------------
+// X8 token activations: [blocks_pad][ld][32] int8 then [blocks_pad][ld] f32
+// scales, ld = q8_tokens_ld(tokens), blocks_pad = 4 * ceil(width / 128).
+int q8_tokens_ld(int tokens);
+size_t q8_tokens_bytes(int tokens, int width);
+hipError_t launch_q8_quantize_tokens(const float *x, int tokens, int width, int ld_x, void *x8, hipStream_t stream);
+// out[t * ld_out + row] = W . x_t (+ resid at the same index); optional
+// int32 block dots [tokens][rows][blocks]
+hipError_t launch_q8_mmq(const Q8Matrix &w, const void *x8, int tokens, float *out, int ld_out, const float *resid,
+    int32_t *dots, hipStream_t stream);
+
 // ---- Gated DeltaNet ------------------------------------------------------
 struct GdnParams {
     const float *qkv = nullptr;       // [conv_size] conv + SiLU outputs (q | k | v channels)

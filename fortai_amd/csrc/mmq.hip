@@ -1,0 +1,295 @@
+// Q8_0 x Q8_0 matrix-matrix product on the i8 matrix cores (prefill / batched
+// token blocks).
+//
+// The reference has no prefill: every token runs the matvec of
+// fortai_gguf_runtime.f90:424-465, i.e. per row and block the exact int32 dot
+// of 32 int8 products, scaled by f32(w_scale) * a_scale and accumulated in
+// fp32 (fortai_q8_dot.c:262-284 scalar, :287-331 AVX2).  Here the int32 block
+// dot of 32 tokens x 32 rows is one v_mfma_i32_32x32x32_i8 (exact: integer
+// arithmetic), and the scale-and-accumulate of every (token, row, block) runs
+// on the vector ALUs: acc = fma(f32(w_scale) * x_scale, f32(dot), acc), the
+// scalar reference's form.  The AVX2 reference splits each block dot into
+// eight 4-product lane partials before the fp32 accumulation, so results
+// agree with it to fp32 rounding (relative 1e-5 class), not bit for bit; the
+// per-block int32 dots are bit-exact and exported for testing.
+//
+// Token activations ("X8", written by q8_quantize_tokens_kernel):
+//   q[(b * ld + t) * 32 + k]   int8 value k of block b of token t
+//   s[b * ld + t]              f32 scale (the fp16-rounded reference scale)
+// with ld = tokens rounded up to 128 and blocks padded to a multiple of 4;
+// padding holds zeros.  The int8 part precedes the scales in one buffer of
+// q8_tokens_bytes() bytes.
+//
+// Weights stay in the decode layout (q8_kernels.hip): lanes 4h..4h+3 of a
+// row's 16-byte pieces hold its bytes 16h..16h+15 of four consecutive blocks,
+// so a lane that loads those four pieces holds the B operand of four MFMAs
+// with no shuffling.  Both operands present their 16 bytes in natural order,
+// so the products pair up whatever k order the instruction uses internally.
+#include "fortai_hip_internal.h"
+#include "fortai_hip_kernels.h"
+
+
+namespace fortai_hip {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kTokTile = 128;  // tokens per workgroup
+constexpr int kRowTile = 128;  // rows per workgroup
+constexpr int kMmqThreads = 256;
+
+__device__ __forceinline__ v4i as_v4i(uint4 u) {
+    v4i r;
+    r.x = static_cast<int>(u.x); r.y = static_cast<int>(u.y);
+    r.z = static_cast<int>(u.z); r.w = static_cast<int>(u.w);
+    return r;
+}
+
+__device__ __forceinline__ uint32_t comp(const uint4 &u, int j) {
+    return j == 0 ? u.x : (j == 1 ? u.y : (j == 2 ? u.z : u.w));
+}
+
+// LDS stage of one chunk (four blocks) of a 128-token x 128-row tile.
+// Operand rows are 32 bytes; the two 16-byte halves of row n are stored
+// swapped when bit 3 of n is set, so the 16-byte reads of 16 consecutive
+// rows fall on distinct banks.
+struct MmqStage {
+    uint4 a[4][kTokTile][2];   // token bytes per block
+    uint4 b[4][kRowTile][2];   // row bytes per block
+    float as[4][kTokTile];     // token scales
+    float bs[4][kRowTile];     // row scales (f32 of the fp16)
+};
+
+__device__ __forceinline__ int half_slot(int n, int h) { return h ^ ((n >> 3) & 1); }
+
+// One workgroup: 128 tokens x 128 rows; wave w covers tokens 64 (w & 1) and
+// rows 64 (w >> 1) as 2 x 2 MFMA tiles of 32 x 32.  Chunk c + 1 is loaded
+// into registers while chunk c is consumed from LDS, then stored to the other
+// stage (one barrier per chunk).
+//   EPI 0: out[t * ld_out + row] = acc;  EPI 1: out = acc + resid (same index)
+//   DOTS: also write every int32 block dot to dots[(t * rows + row) * blocks + b]
+template <int EPI, bool DOTS>
+__global__ __launch_bounds__(kMmqThreads, 2) void q8_mmq_kernel(Q8Matrix w, const int8_t *__restrict__ xq,
+    const float *__restrict__ xs, int tokens, int ld, float *__restrict__ out, int ld_out,
+    const float *__restrict__ resid, int32_t *__restrict__ dots) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    MmqStage *stage = reinterpret_cast<MmqStage *>(lds_raw);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 31, h = lane >> 5;
+    const int t0 = static_cast<int>(blockIdx.y) * kTokTile;
+    const int r0 = static_cast<int>(blockIdx.x) * kRowTile;
+    const int twl = (wave & 1) * 64;   // wave's first token within the tile
+    const int rwl = (wave >> 1) * 64;  // wave's first row within the tile
+    const int chunks = w.chunks;
+    const size_t bstride = static_cast<size_t>(ld) * 32;  // bytes per block of X8
+
+    // global sources of this thread's share of a chunk:
+    //  tokens: 4 blocks x 128 tokens x 2 halves = 1024 pieces, 4 per thread
+    //  rows:   16 row groups x 64 lanes          = 1024 pieces, 4 per thread
+    //  token scales: 512 floats, 2 per thread;  row scales: 128 x uint2, threads < 128
+    const int g_last = w.row_groups - 1;
+    u32x4_t ra[4], rb[4];  // plain vectors (arrays of the uint4 class stay in scratch)
+    float rs[2];
+    uint2 rws = make_uint2(0u, 0u);
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int p = tid + k * kMmqThreads;          // 0..1023
+            const int j = p >> 8, t = (p >> 1) & 127, hh = p & 1;
+            ra[k] = *reinterpret_cast<const u32x4_t *>(xq + static_cast<size_t>(4 * c + j) * bstride +
+                static_cast<size_t>(t0 + t) * 32 + hh * 16);
+            const int g = min((r0 >> 3) + (p >> 6), g_last);  // clamped; rows past the end are not stored
+            // cached loads: every token tile of the launch re-reads these rows
+            rb[k] = reinterpret_cast<const u32x4_t *>(w.quants)[(static_cast<size_t>(g) * chunks + c) * 64 + (p & 63)];
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = tid + k * kMmqThreads;  // 0..511
+            rs[k] = xs[static_cast<size_t>(4 * c + (p >> 7)) * ld + t0 + (p & 127)];
+        }
+        if (tid < kRowTile) {
+            const int g = min((r0 >> 3) + (tid >> 3), g_last);
+            rws = w.scales[(static_cast<size_t>(g) * chunks + c) * 8 + (tid & 7)];
+        }
+    };
+    auto stash = [&](MmqStage &st) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int p = tid + k * kMmqThreads;
+            const int j = p >> 8, t = (p >> 1) & 127, hh = p & 1;
+            *reinterpret_cast<u32x4_t *>(&st.a[j][t][half_slot(t, hh)]) = ra[k];
+        }
+        // row piece: row (p >> 6) * 8 + r, bytes 4l..4l+3 of the four blocks
+        uint32_t *dst = reinterpret_cast<uint32_t *>(&st.b[0][0][0]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int p = tid + k * kMmqThreads;
+            const int q = p & 63, r = q >> 3, l = q & 7;
+            const int row = (p >> 6) * 8 + r;
+            const int base = (row * 2 + half_slot(row, l >> 2)) * 4 + (l & 3);
+            dst[base] = rb[k].x;
+            dst[base + kRowTile * 8] = rb[k].y;
+            dst[base + 2 * kRowTile * 8] = rb[k].z;
+            dst[base + 3 * kRowTile * 8] = rb[k].w;
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = tid + k * kMmqThreads;
+            st.as[p >> 7][p & 127] = rs[k];
+        }
+        if (tid < kRowTile) {
+            st.bs[0][tid] = half_bits_to_float(static_cast<uint16_t>(rws.x & 0xffffu));
+            st.bs[1][tid] = half_bits_to_float(static_cast<uint16_t>(rws.x >> 16));
+            st.bs[2][tid] = half_bits_to_float(static_cast<uint16_t>(rws.y & 0xffffu));
+            st.bs[3][tid] = half_bits_to_float(static_cast<uint16_t>(rws.y >> 16));
+        }
+    };
+
+    float acc[2][2][16];
+#pragma unroll
+    for (int ta = 0; ta < 2; ++ta)
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[ta][f][v] = 0.0f;
+
+    fetch(0);
+    stash(stage[0]);
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+        const MmqStage &st = stage[c & 1];
+        if (c + 1 < chunks) fetch(c + 1);
+        // one block at a time (unrolled, the compiler hoists all 16 MFMAs of
+        // the chunk and spills)
+#pragma unroll 1
+        for (int j = 0; j < 4; ++j) {
+            uint4 af[2], bf[2];
+            float wsc[2];
+#pragma unroll
+            for (int ta = 0; ta < 2; ++ta) {
+                const int t = twl + 32 * ta + i;
+                af[ta] = st.a[j][t][half_slot(t, h)];
+            }
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                const int row = rwl + 32 * f + i;
+                bf[f] = st.b[j][row][half_slot(row, h)];
+                wsc[f] = st.bs[j][row];
+            }
+#pragma unroll
+            for (int ta = 0; ta < 2; ++ta) {
+                // this lane's 16 tokens: twl + 32 ta + 8 (v / 4) + 4 h + v % 4
+                float tsc[16];
+                const float4 *s4 = reinterpret_cast<const float4 *>(&st.as[j][twl + 32 * ta + 4 * h]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 s = s4[2 * q];
+                    tsc[4 * q] = s.x; tsc[4 * q + 1] = s.y; tsc[4 * q + 2] = s.z; tsc[4 * q + 3] = s.w;
+                }
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                    const v16i zero = {};
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(as_v4i(af[ta]), as_v4i(bf[f]), zero, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        acc[ta][f][v] = __builtin_fmaf(wsc[f] * tsc[v], static_cast<float>(d[v]), acc[ta][f][v]);
+                    // keep one MFMA result live at a time (the other wave of
+                    // the SIMD covers the MFMA latency)
+                    __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (DOTS) {
+                        const int row = r0 + rwl + 32 * f + i, blk = 4 * c + j;
+                        if (row < w.rows && blk < w.blocks) {
+#pragma unroll
+                            for (int v = 0; v < 16; ++v) {
+                                const int t = t0 + twl + 32 * ta + 8 * (v >> 2) + 4 * h + (v & 3);
+                                if (t < tokens) dots[(static_cast<size_t>(t) * w.rows + row) * w.blocks + blk] = d[v];
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        if (c + 1 < chunks) stash(stage[(c + 1) & 1]);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int ta = 0; ta < 2; ++ta) {
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const int row = r0 + rwl + 32 * f + i;
+            if (row >= w.rows) continue;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int t = t0 + twl + 32 * ta + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (t >= tokens) continue;
+                const size_t o = static_cast<size_t>(t) * ld_out + row;
+                if constexpr (EPI == 1) out[o] = acc[ta][f][v] + resid[o];
+                else out[o] = acc[ta][f][v];
+            }
+        }
+    }
+}
+
+// fortai_q8_quantize (fortai_q8_dot.c:153-198) of every token into X8: one
+// thread per 4 values, 8 consecutive threads per block.
+__global__ __launch_bounds__(256) void q8_quantize_tokens_kernel(const float *__restrict__ x, int tokens, int width,
+    int ld_x, int ld, int blocks_pad, int8_t *__restrict__ xq, float *__restrict__ xs) {
+    const size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int groups_pad = blocks_pad * 8;
+    const int t = static_cast<int>(idx / groups_pad), g = static_cast<int>(idx % groups_pad);
+    if (t >= ld) return;  // whole 8-lane blocks exit together (groups_pad % 8 == 0)
+    float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < tokens && g < width / 4) y = reinterpret_cast<const float4 *>(x + static_cast<size_t>(t) * ld_x)[g];
+    float scale;
+    uint16_t bits;
+    const uint32_t packed = quantize_group(y, scale, bits);
+    const int b = g >> 3, l = g & 7;
+    reinterpret_cast<uint32_t *>(xq + (static_cast<size_t>(b) * ld + t) * 32)[l] = packed;
+    if (l == 0) xs[static_cast<size_t>(b) * ld + t] = scale;
+}
+
+}  // namespace
+
+int q8_tokens_ld(int tokens) { return (tokens + kTokTile - 1) / kTokTile * kTokTile; }
+
+size_t q8_tokens_bytes(int tokens, int width) {
+    const size_t blocks_pad = static_cast<size_t>((width / kQ8Block + 3) / 4) * 4;
+    return static_cast<size_t>(q8_tokens_ld(tokens)) * blocks_pad * (32 + 4);
+}
+
+hipError_t launch_q8_quantize_tokens(const float *x, int tokens, int width, int ld_x, void *x8, hipStream_t stream) {
+    if (tokens <= 0 || width <= 0 || width % kQ8Block || ld_x < width || ld_x % 4) return hipErrorInvalidValue;
+    const int ld = q8_tokens_ld(tokens);
+    const int blocks_pad = (width / kQ8Block + 3) / 4 * 4;
+    int8_t *xq = static_cast<int8_t *>(x8);
+    float *xs = reinterpret_cast<float *>(xq + static_cast<size_t>(ld) * blocks_pad * 32);
+    const size_t threads = static_cast<size_t>(ld) * blocks_pad * 8;
+    hipLaunchKernelGGL(q8_quantize_tokens_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+        stream, x, tokens, width, ld_x, ld, blocks_pad, xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_mmq(const Q8Matrix &w, const void *x8, int tokens, float *out, int ld_out, const float *resid,
+    int32_t *dots, hipStream_t stream) {
+    if (tokens <= 0 || ld_out < w.rows || w.rows <= 0) return hipErrorInvalidValue;
+    const int ld = q8_tokens_ld(tokens);
+    const int8_t *xq = static_cast<const int8_t *>(x8);
+    const float *xs = reinterpret_cast<const float *>(xq + static_cast<size_t>(ld) * w.chunks * 4 * 32);
+    const dim3 grid((w.rows + kRowTile - 1) / kRowTile, ld / kTokTile);
+    const size_t lds = 2 * sizeof(MmqStage);
+    if (dots)
+        hipLaunchKernelGGL((q8_mmq_kernel<0, true>), grid, dim3(kMmqThreads), lds, stream, w, xq, xs, tokens, ld, out,
+            ld_out, resid, dots);
+    else if (resid)
+        hipLaunchKernelGGL((q8_mmq_kernel<1, false>), grid, dim3(kMmqThreads), lds, stream, w, xq, xs, tokens, ld, out,
+            ld_out, resid, dots);
+    else
+        hipLaunchKernelGGL((q8_mmq_kernel<0, false>), grid, dim3(kMmqThreads), lds, stream, w, xq, xs, tokens, ld, out,
+            ld_out, resid, dots);
+    return hipGetLastError();
+}
+
+}  // namespace fortai_hip

@@ -209,6 +209,30 @@ int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *context,
     const fortai_hip_q8_weights *weights, const void *device_activation,
     void *device_dots);
 
+/* Token blocks (prefill, batches) on the i8 matrix cores.  The reference runs
+ * every token through the matvec of fortai_gguf_runtime.f90:424-465; these
+ * compute the same product for `tokens` activations at once.
+ * quantize_tokens: device fp32 x [tokens][width] (row pitch `width`) ->
+ * fortai_q8_quantize (fortai_q8_dot.c:153-198) of every token into a device
+ * buffer of fortai_hip_q8_tokens_bytes(tokens, width) bytes.
+ * mmq: out[t][rows] (fp32) = W . x_t for every token, plus device_residual
+ * [tokens][rows] when it is not NULL (may alias the output).  The int32 block
+ * dots are exact; the fp32 accumulation is the scalar reference's
+ * result += scale * dot per block (fortai_q8_dot.c:262-284), so results
+ * agree with the AVX2 path to fp32 rounding.  kernel_ms (may be NULL):
+ * event-timed kernel duration, synchronising.
+ * mmq_block_dots: the exact int32 dot of every (token, row, block), device
+ * int32 [tokens][rows][width/32] (parity probe). */
+size_t fortai_hip_q8_tokens_bytes(int tokens, int width);
+int fortai_hip_q8_quantize_tokens_device(fortai_hip_q8_context *context,
+    const void *device_x, int tokens, int width, void *device_tokens);
+int fortai_hip_q8_mmq_device(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_tokens, int tokens,
+    void *device_output, const void *device_residual, float *kernel_ms);
+int fortai_hip_q8_mmq_block_dots(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_tokens, int tokens,
+    void *device_dots);
+
 /* Recurrent-layer core step (conv1d + SiLU + L2 norm + decay/beta + delta
  * rule; no projections, no gated norm): device fp32 qkv [conv_size], alpha and
  * beta [value_heads] in, raw output [inner_size].  State access uses the
