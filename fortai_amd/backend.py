@@ -94,6 +94,14 @@ _SIGNATURES = {
     "fortai_hip_qwen35_decoder_status": [_vp],
     "fortai_hip_qwen35_decoder_persistent": [_vp],
     "fortai_hip_qwen35_decoder_phase_times": [_vp, _vp, C.c_size_t],
+    "fortai_hip_qwen35_batch_create": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp,
+                                       _vp, _i, _f, _vpp],
+    "fortai_hip_qwen35_batch_destroy": [_vp],
+    "fortai_hip_qwen35_batch_reset": [_vp],
+    "fortai_hip_qwen35_batch_forward": [_vp, _vp, _vp, _vp, _vp],
+    "fortai_hip_qwen35_batch_generate": [_vp, _vp, _vp, _i, _vp],
+    "fortai_hip_qwen35_batch_replay": [_vp, _i],
+    "fortai_hip_qwen35_batch_logits": [_vp, _vpp],
 }
 _RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p, "fortai_hip_q8_tokens_bytes": C.c_size_t}
 
@@ -387,4 +395,66 @@ class Decoder:
     def free(self) -> None:
         if self.h:
             self.ctx.lib.fortai_hip_qwen35_decoder_destroy(self.h)
+            self.h = None
+
+
+class BatchDecoder:
+    """``batch`` independent sequences over one set of layers and weights (one
+    captured graph per step, every weight read once for all sequences)."""
+
+    def __init__(self, ctx: Context, batch: int, recurrent: Sequence[Optional[Recurrent]],
+                 attention: Sequence[Optional[Attention]], ffn_gate: Sequence[Q8Weights],
+                 ffn_up: Sequence[Q8Weights], ffn_down: Sequence[Q8Weights], attn_norm: Sequence[np.ndarray],
+                 post_norm: Sequence[np.ndarray], output_norm: np.ndarray, hidden: int,
+                 embedding, output, max_context: int, eps: float, vocab: int):
+        self.ctx, self.batch, self.vocab, self.max_context = ctx, batch, vocab, max_context
+        n = len(ffn_gate)
+
+        def harr(items):
+            return (C.c_void_p * n)(*[(x.h if x is not None else None) for x in items])
+
+        self._norms = [np.ascontiguousarray(a, dtype=np.float32) for a in list(attn_norm) + list(post_norm)]
+        an = (C.c_void_p * n)(*[_ptr(a) for a in self._norms[:n]])
+        pn = (C.c_void_p * n)(*[_ptr(a) for a in self._norms[n:]])
+        self._onorm = np.ascontiguousarray(output_norm, dtype=np.float32)
+        e16 = embedding.h if isinstance(embedding, F16Weights) else None
+        e8 = embedding.h if isinstance(embedding, Q8Weights) else None
+        o16 = output.h if isinstance(output, F16Weights) else None
+        o8 = output.h if isinstance(output, Q8Weights) else None
+        h = C.c_void_p()
+        ctx.call("fortai_hip_qwen35_batch_create", ctx.h, batch, n, harr(recurrent), harr(attention),
+                 harr(ffn_gate), harr(ffn_up), harr(ffn_down), an, pn, _ptr(self._onorm), hidden, e16, e8, o16, o8,
+                 max_context, eps, C.byref(h))
+        self.h = h
+        self.logits = np.zeros((batch, vocab), dtype=np.float32)
+
+    def _inputs(self, tokens, positions):
+        t = np.ascontiguousarray(tokens, dtype=np.int64)
+        p = np.ascontiguousarray(positions, dtype=np.int32)
+        if t.shape != (self.batch,) or p.shape != (self.batch,):
+            raise ValueError(f"need {self.batch} tokens and positions")
+        return t, p
+
+    def reset(self) -> None:
+        self.ctx.call("fortai_hip_qwen35_batch_reset", self.h)
+
+    def forward(self, tokens, positions, want_logits: bool = True) -> np.ndarray:
+        t, p = self._inputs(tokens, positions)
+        nxt = np.zeros(self.batch, dtype=np.int64)
+        self.ctx.call("fortai_hip_qwen35_batch_forward", self.h, _ptr(t), _ptr(p),
+                      _ptr(self.logits) if want_logits else None, _ptr(nxt))
+        return nxt
+
+    def generate(self, tokens, positions, steps: int) -> np.ndarray:
+        t, p = self._inputs(tokens, positions)
+        trace = np.zeros((self.batch, steps), dtype=np.int64)
+        self.ctx.call("fortai_hip_qwen35_batch_generate", self.h, _ptr(t), _ptr(p), steps, _ptr(trace))
+        return trace
+
+    def replay(self, steps: int) -> None:
+        self.ctx.call("fortai_hip_qwen35_batch_replay", self.h, steps)
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.fortai_hip_qwen35_batch_destroy(self.h)
             self.h = None

@@ -23,7 +23,27 @@ constexpr int kQLoads = kMaxGroup * kMaxHead / ea::kThreads;
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const AttentionParams p) {
+constexpr int kChunk = 256;  // positions per split-K chunk (long contexts)
+
+// Sequence s of a batch (blockIdx.y): every per-sequence buffer is laid out
+// [batch][...] with the single-sequence size, and position[s] is its own.
+__device__ __forceinline__ AttentionParams attention_seq(AttentionParams p, int s) {
+    const size_t nmax = (static_cast<size_t>(p.max_context) + kChunk - 1) / kChunk;
+    p.q += static_cast<size_t>(s) * p.heads * 2 * p.head;
+    p.k += static_cast<size_t>(s) * p.kv_heads * p.head;
+    p.v += static_cast<size_t>(s) * p.kv_heads * p.value;
+    p.kcache += static_cast<size_t>(s) * p.max_context * p.kv_heads * p.head;
+    p.vcache += static_cast<size_t>(s) * p.max_context * p.kv_heads * p.value;
+    p.partial += static_cast<size_t>(s) * p.heads * p.max_context;
+    p.cache_flags += static_cast<size_t>(s) * p.kv_heads;
+    p.out += static_cast<size_t>(s) * p.heads * p.value;
+    p.position += s;
+    if (p.split) p.split += static_cast<size_t>(s) * p.heads * nmax * (p.value + 2);
+    return p;
+}
+
+__global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const AttentionParams p_batch) {
+    const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     __shared__ __align__(16) float qh[kMaxGroup * kMaxHead];
     __shared__ __align__(16) float kn[kMaxHead];
     __shared__ __align__(16) float vn[kMaxHead];
@@ -118,7 +138,8 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     FORTAI_ATT_MARK(11);
 }
 
-__global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const AttentionParams p) {
+__global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const AttentionParams p_batch) {
+    const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     extern __shared__ __align__(16) float lds[];
     const int tid = static_cast<int>(threadIdx.x);
     FORTAI_ATT_MARK(0);
@@ -154,7 +175,6 @@ size_t output_lds_bytes() { return ea::work_floats() * sizeof(float); }
 // combines per head: M = max m_c, Z = sum Z_c e^(m_c - M),
 // out = (sum o_c e^(m_c - M)) / Z * sigmoid(gate) (flash-decoding).  The
 // scores are the scores kernel's (the reference's per-position dots).
-constexpr int kChunk = 256;
 
 __device__ __forceinline__ float block_max256(float v, float *red) {
     for (int k = 32; k >= 1; k >>= 1) v = fmaxf(v, __shfl_xor(v, k));
@@ -285,7 +305,8 @@ __device__ __forceinline__ void split_chunk(const AttentionParams &p, int kvh, i
     }
 }
 
-__global__ __launch_bounds__(ea::kThreads) void attention_split_kernel(const AttentionParams p) {
+__global__ __launch_bounds__(ea::kThreads) void attention_split_kernel(const AttentionParams p_batch) {
+    const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     __shared__ SplitLds L;
     const int pos = *p.position;
     if (pos < 0 || pos >= p.max_context) return;
@@ -308,7 +329,8 @@ constexpr int kMergeDims = 64;
 constexpr int kMergeParts = ea::kThreads / kMergeDims;
 constexpr int kMergeBatch = 32;
 
-__global__ __launch_bounds__(ea::kThreads) void attention_merge_kernel(const AttentionParams p) {
+__global__ __launch_bounds__(ea::kThreads) void attention_merge_kernel(const AttentionParams p_batch) {
+    const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     __shared__ float f[kMaxSplitChunks];
     __shared__ float red[4];
     __shared__ float part[kMergeParts][kMergeDims];
@@ -360,7 +382,8 @@ size_t attention_scores_floats(int heads, int max_context) { return static_cast<
 
 int attention_split_chunks(int max_context) { return (max_context + kChunk - 1) / kChunk; }
 
-hipError_t launch_attention(const AttentionParams &p, hipStream_t stream) {
+hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int batch) {
+    if (batch < 1) return hipErrorInvalidValue;
     const int group = p.kv_heads > 0 ? p.heads / p.kv_heads : 0;
     if (p.max_context > p.exact_max && (!p.split || attention_split_chunks(p.max_context) > kMaxSplitChunks))
         return hipErrorInvalidValue;
@@ -369,18 +392,18 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream) {
         return hipErrorInvalidValue;
     const size_t lds = output_lds_bytes();  // independent of the context length
     const int nblk_max = (p.max_context + ea::kPosBlock - 1) / ea::kPosBlock;
-    hipLaunchKernelGGL(attention_scores_kernel, dim3(p.kv_heads * nblk_max), dim3(ea::kThreads), 0, stream, p);
+    hipLaunchKernelGGL(attention_scores_kernel, dim3(p.kv_heads * nblk_max, batch), dim3(ea::kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims)), dim3(ea::kThreads), lds, stream, p);
+    hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads), lds, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess || p.max_context <= p.exact_max) return e;
     // long contexts: the split-K pair (each kernel picks its regime from the device position)
-    hipLaunchKernelGGL(attention_split_kernel, dim3(p.kv_heads * attention_split_chunks(p.max_context)),
+    hipLaunchKernelGGL(attention_split_kernel, dim3(p.kv_heads * attention_split_chunks(p.max_context), batch),
         dim3(ea::kThreads), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_merge_kernel, dim3(p.heads * ((p.value + kMergeDims - 1) / kMergeDims)),
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(p.heads * ((p.value + kMergeDims - 1) / kMergeDims), batch),
         dim3(ea::kThreads), 0, stream, p);
     return hipGetLastError();
 }

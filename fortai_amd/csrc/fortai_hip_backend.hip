@@ -9,6 +9,7 @@
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstdio>
@@ -117,6 +118,42 @@ struct fortai_hip_qwen35_decoder {
     uint32_t next_tag = 1;                   // tag of the next persistent launch
     int *status = nullptr;
     uint64_t *phase_times = nullptr;  // FORTAI_HIP_PHASE_TIMES=1: per-workgroup phase end clocks
+};
+
+// Batched decoder: `batch` independent sequences over one set of layers and
+// weights.  The layer objects supply weights and constants; every sequence
+// has its own conv/GDN state and KV cache, all [batch][single size].
+struct batch_layer {
+    fortai_hip_qwen35_recurrent *rec = nullptr;
+    fortai_hip_qwen35_attention *att = nullptr;
+    const fortai_hip_q8_weights *gate = nullptr, *up = nullptr, *down = nullptr;
+    float *attn_norm = nullptr, *post_norm = nullptr;
+    // recurrent
+    float *conv_state = nullptr, *state = nullptr, *qkv = nullptr, *z = nullptr, *alpha = nullptr, *beta = nullptr,
+          *o_raw = nullptr;
+    // attention
+    uint16_t *kcache = nullptr, *vcache = nullptr;
+    float *q = nullptr, *k = nullptr, *v = nullptr, *partial = nullptr, *attn_out = nullptr, *split = nullptr;
+    int *flags = nullptr;
+};
+
+struct fortai_hip_qwen35_batch {
+    fortai_hip_q8_context *context = nullptr;
+    int batch = 0, hidden = 0, vocab = 0, ffn = 0, max_context = 0, parts = 0, act_width = 0;
+    float eps = 0.0f;
+    std::vector<batch_layer> layers;
+    const fortai_hip_f16_weights *emb16 = nullptr, *out16 = nullptr;
+    const fortai_hip_q8_weights *emb8 = nullptr, *out8 = nullptr;
+    float *output_norm = nullptr, *x = nullptr, *logits = nullptr;
+    void *act = nullptr;     // quantized activations [batch][q8l_bytes(act_width)]
+    void *h_q8l = nullptr;   // quantized FFN hidden [batch][q8l_bytes(ffn)]
+    float *argmax_value = nullptr;
+    int32_t *argmax_index = nullptr;
+    int64_t *tokens = nullptr, *trace = nullptr;  // trace [batch][max_context]
+    int *positions = nullptr;
+    std::vector<int> next_positions;  // host mirror after the queued steps
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 namespace {
@@ -1599,4 +1636,330 @@ int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits
     return FORTAI_HIP_OK;
 }
 
+// ------------------------------------------------------------ batched decoder
+namespace {
+hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
+    const int B = b->batch, H = b->hidden;
+    hipError_t e = b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->tokens, 0, b->x, stream, B)
+                            : launch_q8_embedding(b->emb8->m, b->tokens, 0, b->x, stream, B);
+    for (size_t i = 0; i < b->layers.size() && e == hipSuccess; ++i) {
+        batch_layer &L = b->layers[i];
+        MatvecInput in;
+        in.x = b->x;
+        in.norm = L.attn_norm;
+        in.eps = b->eps;
+        in.width = H;
+        e = launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream);
+        if (e != hipSuccess) break;
+        if (L.rec) {
+            auto *R = L.rec;
+            MatvecSegment segs[4] = {segment(R->qkv, L.qkv), segment(R->gate, L.z), segment(R->alpha, L.alpha),
+                segment(R->beta, L.beta)};
+            segs[0].conv_w = R->conv_w;
+            segs[0].conv_state = L.conv_state;
+            segs[0].conv_size = R->conv_size;
+            segs[0].kernel = R->kernel;
+            segs[1].silu = true;
+            e = launch_q8_batch_matvec(segs, 4, b->act, H, B, Epilogue::STORE, stream);
+            GdnParams gp = gdn_params(R, L.qkv, L.alpha, L.beta, L.o_raw);
+            gp.state = L.state;
+            if (e == hipSuccess) e = launch_gdn_delta(gp, stream, B);
+            MatvecInput gated;
+            gated.x = L.o_raw;
+            gated.z = L.z;
+            gated.norm = R->ssm_norm;
+            gated.eps = R->eps;
+            gated.head = R->head;
+            gated.width = R->inner;
+            if (e == hipSuccess) e = launch_q8l_prep(gated, Prologue::GATED, b->act, B, stream);
+            const MatvecSegment oseg = segment(R->out, b->x, b->x);
+            if (e == hipSuccess) e = launch_q8_batch_matvec(&oseg, 1, b->act, R->inner, B, Epilogue::ADD, stream);
+        } else {
+            auto *A = L.att;
+            const MatvecSegment segs[3] = {segment(A->q, L.q), segment(A->k, L.k), segment(A->v, L.v)};
+            e = launch_q8_batch_matvec(segs, 3, b->act, H, B, Epilogue::STORE, stream);
+            AttentionParams ap = attention_params(A, L.q, L.k, L.v, L.attn_out);
+            ap.kcache = L.kcache; ap.vcache = L.vcache; ap.partial = L.partial; ap.cache_flags = L.flags;
+            ap.split = L.split; ap.position = b->positions; ap.max_context = b->max_context;
+            if (e == hipSuccess) e = launch_attention(ap, stream, B);
+            MatvecInput oin;
+            oin.x = L.attn_out;
+            oin.width = A->heads * A->value;
+            if (e == hipSuccess) e = launch_q8l_prep(oin, Prologue::F32, b->act, B, stream);
+            const MatvecSegment oseg = segment(A->o, b->x, b->x);
+            if (e == hipSuccess) e = launch_q8_batch_matvec(&oseg, 1, b->act, oin.width, B, Epilogue::ADD, stream);
+        }
+        if (e != hipSuccess) break;
+        in.norm = L.post_norm;
+        e = launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream);
+        const MatvecSegment pair = segment(L.gate, nullptr, nullptr, L.up, b->h_q8l);
+        if (e == hipSuccess) e = launch_q8_batch_matvec(&pair, 1, b->act, H, B, Epilogue::SILU_PAIR, stream);
+        const MatvecSegment dseg = segment(L.down, b->x, b->x);
+        if (e == hipSuccess) e = launch_q8_batch_matvec(&dseg, 1, b->h_q8l, L.gate->m.rows, B, Epilogue::ADD, stream);
+    }
+    if (e != hipSuccess) return e;
+    ArgmaxState st;
+    st.partial_value = b->argmax_value;
+    st.partial_index = b->argmax_index;
+    st.token = b->tokens;
+    st.trace = b->trace;
+    st.trace_capacity = b->max_context;
+    st.position = b->positions;
+    if (b->out16)
+        return launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm, b->eps,
+            b->logits, st, stream);
+    // Q8_0 LM head: the batched matvec, then the argmax of each sequence
+    MatvecInput in;
+    in.x = b->x;
+    in.norm = b->output_norm;
+    in.eps = b->eps;
+    in.width = H;
+    e = launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream);
+    const MatvecSegment s8 = segment(b->out8, b->logits);
+    if (e == hipSuccess) e = launch_q8_batch_matvec(&s8, 1, b->act, H, B, Epilogue::STORE, stream);
+    for (int q = 0; q < B && e == hipSuccess; ++q) {
+        ArgmaxState sq = st;
+        sq.partial_value += static_cast<size_t>(q) * b->parts;
+        sq.partial_index += static_cast<size_t>(q) * b->parts;
+        sq.token += q;
+        sq.trace += static_cast<size_t>(q) * b->max_context;
+        sq.position += q;
+        e = launch_argmax(b->logits + static_cast<size_t>(q) * b->vocab, b->vocab, sq, stream);
+    }
+    return e;
+}
+
+hipError_t batch_zero_state(fortai_hip_qwen35_batch *b, hipStream_t stream) {
+    const size_t B = static_cast<size_t>(b->batch);
+    hipError_t e = hipSuccess;
+    for (auto &L : b->layers) {
+        if (L.rec) {
+            const auto *R = L.rec;
+            if (e == hipSuccess)
+                e = hipMemsetAsync(L.conv_state, 0, B * (R->kernel - 1) * R->conv_size * sizeof(float), stream);
+            if (e == hipSuccess)
+                e = hipMemsetAsync(L.state, 0, B * R->value_heads * R->head * R->head * sizeof(float), stream);
+        } else {
+            const auto *A = L.att;
+            const size_t cache = B * b->max_context * A->kv_heads;
+            if (e == hipSuccess) e = hipMemsetAsync(L.kcache, 0, cache * A->head * sizeof(uint16_t), stream);
+            if (e == hipSuccess) e = hipMemsetAsync(L.vcache, 0, cache * A->value * sizeof(uint16_t), stream);
+            if (e == hipSuccess) e = hipMemsetAsync(L.flags, 0, B * A->kv_heads * sizeof(int), stream);
+        }
+    }
+    if (e == hipSuccess) e = hipMemsetAsync(b->trace, 0, B * b->max_context * sizeof(int64_t), stream);
+    if (e == hipSuccess) e = hipMemsetAsync(b->x, 0, B * b->hidden * sizeof(float), stream);
+    return e;
+}
+
+int batch_set_inputs(fortai_hip_qwen35_batch *b, const int64_t *tokens, const int *positions, int steps) {
+    const int rows = b->emb16 ? b->emb16->rows : b->emb8->m.rows;
+    for (int q = 0; q < b->batch; ++q)
+        if (tokens[q] < 0 || tokens[q] >= rows || positions[q] < 0 || positions[q] + steps > b->max_context)
+            return FORTAI_HIP_INVALID;
+    auto *c = b->context;
+    hipError_t e = hipMemcpyAsync(b->tokens, tokens, b->batch * sizeof(int64_t), hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(b->positions, positions, b->batch * sizeof(int), hipMemcpyHostToDevice, c->stream);
+    // the host arrays are borrowed for the call only
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    for (int q = 0; q < b->batch; ++q) b->next_positions[q] = positions[q];
+    return done(c, e, "batch inputs");
+}
+}  // namespace
+
+int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *c, int batch, int layer_count,
+    fortai_hip_qwen35_recurrent *const *recurrent, fortai_hip_qwen35_attention *const *attention,
+    const fortai_hip_q8_weights *const *ffn_gate, const fortai_hip_q8_weights *const *ffn_up,
+    const fortai_hip_q8_weights *const *ffn_down, const float *const *attn_norm, const float *const *post_norm,
+    const float *output_norm, int hidden, const fortai_hip_f16_weights *emb16, const fortai_hip_q8_weights *emb8,
+    const fortai_hip_f16_weights *out16, const fortai_hip_q8_weights *out8, int max_context, float eps,
+    fortai_hip_qwen35_batch **out) {
+    if (!c || !out || batch < 1 || batch > 8 || layer_count <= 0 || !recurrent || !attention || !ffn_gate ||
+        !ffn_up || !ffn_down || !attn_norm || !post_norm || !output_norm || hidden <= 0 || hidden % 64 ||
+        max_context <= 0 || eps <= 0.0f || (!emb16 == !emb8) || (!out16 == !out8))
+        return FORTAI_HIP_INVALID;
+    *out = nullptr;
+    if ((emb16 && (emb16->context != c || emb16->width != hidden)) || (emb8 && (!owned(c, emb8) || emb8->width != hidden)) ||
+        (out16 && (out16->context != c || out16->width != hidden)) || (out8 && (!owned(c, out8) || out8->width != hidden)))
+        return FORTAI_HIP_INVALID;
+    auto *b = new (std::nothrow) fortai_hip_qwen35_batch;
+    if (!b) return FORTAI_HIP_RUNTIME_ERROR;
+    b->context = c; b->batch = batch; b->hidden = hidden; b->max_context = max_context; b->eps = eps;
+    b->emb16 = emb16; b->emb8 = emb8; b->out16 = out16; b->out8 = out8;
+    b->vocab = out16 ? out16->rows : out8->m.rows;
+    b->parts = out16 ? f16_batch_lm_head_workgroups(b->vocab) : (b->vocab + 255) / 256;
+    b->next_positions.assign(batch, 0);
+    int ffn = 0, width = hidden;
+    for (int i = 0; i < layer_count; ++i) {
+        batch_layer L;
+        L.rec = recurrent[i];
+        L.att = attention[i];
+        L.gate = ffn_gate[i]; L.up = ffn_up[i]; L.down = ffn_down[i];
+        const bool ok = (!L.rec != !L.att) && owned(c, L.gate) && owned(c, L.up) && owned(c, L.down) &&
+            ffn_shapes_ok(L.gate, L.up, L.down) && L.gate->width == hidden && L.down->m.rows == hidden &&
+            attn_norm[i] && post_norm[i] &&
+            (L.rec ? (L.rec->context == c && L.rec->qkv->width == hidden && L.rec->out->m.rows == hidden)
+                   : (L.att->context == c && L.att->q->width == hidden && L.att->o->m.rows == hidden &&
+                      L.att->max_context >= max_context));
+        if (!ok) {
+            delete b;
+            return FORTAI_HIP_INVALID;
+        }
+        ffn = std::max(ffn, L.gate->m.rows);
+        width = std::max(width, L.rec ? L.rec->inner : L.att->heads * L.att->value);
+        b->layers.push_back(L);
+    }
+    b->ffn = ffn;
+    b->act_width = width;
+    (void)hipSetDevice(c->device);
+    const size_t B = static_cast<size_t>(batch);
+    hipError_t e = hipSuccess;
+    for (size_t i = 0; i < b->layers.size(); ++i) {
+        batch_layer &L = b->layers[i];
+        if (e == hipSuccess) e = upload_f32(&L.attn_norm, attn_norm[i], hidden, c->stream);
+        if (e == hipSuccess) e = upload_f32(&L.post_norm, post_norm[i], hidden, c->stream);
+        if (L.rec) {
+            const auto *R = L.rec;
+            if (e == hipSuccess) e = alloc(&L.conv_state, B * (R->kernel - 1) * R->conv_size);
+            if (e == hipSuccess) e = alloc(&L.state, B * R->value_heads * R->head * R->head);
+            if (e == hipSuccess) e = alloc(&L.qkv, B * R->conv_size);
+            if (e == hipSuccess) e = alloc(&L.z, B * R->inner);
+            if (e == hipSuccess) e = alloc(&L.alpha, B * R->value_heads);
+            if (e == hipSuccess) e = alloc(&L.beta, B * R->value_heads);
+            if (e == hipSuccess) e = alloc(&L.o_raw, B * R->inner);
+        } else {
+            const auto *A = L.att;
+            const size_t cache = B * max_context * A->kv_heads;
+            if (e == hipSuccess) e = alloc(&L.kcache, cache * A->head);
+            if (e == hipSuccess) e = alloc(&L.vcache, cache * A->value);
+            if (e == hipSuccess) e = alloc(&L.q, B * A->heads * 2 * A->head);
+            if (e == hipSuccess) e = alloc(&L.k, B * A->kv_heads * A->head);
+            if (e == hipSuccess) e = alloc(&L.v, B * A->kv_heads * A->value);
+            if (e == hipSuccess) e = alloc(&L.partial, B * attention_scores_floats(A->heads, max_context));
+            if (e == hipSuccess) e = alloc(&L.attn_out, B * A->heads * A->value);
+            if (e == hipSuccess) e = alloc(&L.flags, B * A->kv_heads);
+            if (e == hipSuccess && max_context > A->exact_max)
+                e = alloc(&L.split, B * A->heads * attention_split_chunks(max_context) * (A->value + 2));
+        }
+    }
+    if (e == hipSuccess) e = upload_f32(&b->output_norm, output_norm, hidden, c->stream);
+    if (e == hipSuccess) e = alloc(&b->x, B * hidden);
+    if (e == hipSuccess) e = hipMalloc(&b->act, B * q8l_bytes(width));
+    if (e == hipSuccess) e = hipMemsetAsync(b->act, 0, B * q8l_bytes(width), c->stream);
+    if (e == hipSuccess) e = hipMalloc(&b->h_q8l, B * q8l_bytes(ffn));
+    if (e == hipSuccess) e = hipMemsetAsync(b->h_q8l, 0, B * q8l_bytes(ffn), c->stream);
+    if (e == hipSuccess) e = alloc(&b->logits, B * b->vocab);
+    if (e == hipSuccess) e = alloc(&b->argmax_value, B * b->parts);
+    if (e == hipSuccess) e = alloc(&b->argmax_index, B * b->parts);
+    if (e == hipSuccess) e = alloc(&b->tokens, B);
+    if (e == hipSuccess) e = alloc(&b->positions, B);
+    if (e == hipSuccess) e = alloc(&b->trace, B * max_context);
+    if (e == hipSuccess) e = hipMemsetAsync(b->tokens, 0, B * sizeof(int64_t), c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(b->positions, 0, B * sizeof(int), c->stream);
+    if (e == hipSuccess) e = batch_zero_state(b, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    // one step captured as a graph (state, tokens and positions are device-side)
+    if (e == hipSuccess) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        const hipError_t ce = enqueue_batch_step(b, c->stream);
+        e = hipStreamEndCapture(c->stream, &b->graph);
+        if (ce != hipSuccess) e = ce;
+    }
+    if (e == hipSuccess) e = hipGraphInstantiate(&b->exec, b->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        fortai_hip_qwen35_batch_destroy(b);
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen batch create", e);
+    }
+    *out = b;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_batch_destroy(fortai_hip_qwen35_batch *b) {
+    if (!b) return FORTAI_HIP_OK;
+    auto *c = b->context;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    if (b->exec) (void)hipGraphExecDestroy(b->exec);
+    if (b->graph) (void)hipGraphDestroy(b->graph);
+    for (auto &L : b->layers) {
+        release(L.attn_norm); release(L.post_norm);
+        release(L.conv_state); release(L.state); release(L.qkv); release(L.z); release(L.alpha); release(L.beta);
+        release(L.o_raw);
+        release(L.kcache); release(L.vcache); release(L.q); release(L.k); release(L.v); release(L.partial);
+        release(L.attn_out); release(L.split); release(L.flags);
+    }
+    release(b->output_norm); release(b->x); release(b->logits); release(b->argmax_value); release(b->argmax_index);
+    release(b->tokens); release(b->positions); release(b->trace);
+    if (b->act) (void)hipFree(b->act);
+    if (b->h_q8l) (void)hipFree(b->h_q8l);
+    delete b;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_batch_reset(fortai_hip_qwen35_batch *b) {
+    if (!b) return FORTAI_HIP_INVALID;
+    auto *c = b->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = batch_zero_state(b, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    b->next_positions.assign(b->batch, 0);
+    return done(c, e, "batch reset");
+}
+
+int fortai_hip_qwen35_batch_forward(fortai_hip_qwen35_batch *b, const int64_t *tokens, const int *positions,
+    float *logits, int64_t *next_tokens) {
+    if (!b || !tokens || !positions) return FORTAI_HIP_INVALID;
+    auto *c = b->context;
+    (void)hipSetDevice(c->device);
+    const int rc = batch_set_inputs(b, tokens, positions, 1);
+    if (rc != FORTAI_HIP_OK) return rc;
+    hipError_t e = hipGraphLaunch(b->exec, c->stream);
+    for (auto &p : b->next_positions) ++p;
+    if (e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, b->logits, static_cast<size_t>(b->batch) * b->vocab * sizeof(float),
+            hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && next_tokens)
+        e = hipMemcpyAsync(next_tokens, b->tokens, b->batch * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && (logits || next_tokens)) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "batch forward");
+}
+
+int fortai_hip_qwen35_batch_generate(fortai_hip_qwen35_batch *b, const int64_t *tokens, const int *positions,
+    int steps, int64_t *trace) {
+    if (!b || !tokens || !positions || !trace || steps <= 0) return FORTAI_HIP_INVALID;
+    auto *c = b->context;
+    (void)hipSetDevice(c->device);
+    const int rc = batch_set_inputs(b, tokens, positions, steps);
+    if (rc != FORTAI_HIP_OK) return rc;
+    hipError_t e = hipSuccess;
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(b->exec, c->stream);
+    for (int q = 0; q < b->batch && e == hipSuccess; ++q) {
+        e = hipMemcpyAsync(trace + static_cast<size_t>(q) * steps,
+            b->trace + static_cast<size_t>(q) * b->max_context + positions[q], steps * sizeof(int64_t),
+            hipMemcpyDeviceToHost, c->stream);
+        b->next_positions[q] = positions[q] + steps;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "batch generate");
+}
+
+int fortai_hip_qwen35_batch_replay(fortai_hip_qwen35_batch *b, int steps) {
+    if (!b || steps <= 0) return FORTAI_HIP_INVALID;
+    for (int q = 0; q < b->batch; ++q)
+        if (b->next_positions[q] + steps > b->max_context) return FORTAI_HIP_INVALID;
+    auto *c = b->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipSuccess;
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(b->exec, c->stream);
+    for (auto &p : b->next_positions) p += steps;
+    return done(c, e, "batch replay");
+}
+
+int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *b, void **logits) {
+    if (!b || !logits) return FORTAI_HIP_INVALID;
+    *logits = b->logits;
+    return FORTAI_HIP_OK;
+}
+
 }  // extern "C"
+

@@ -84,6 +84,15 @@ struct MatvecInput {
 hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const MatvecInput &in,
     Prologue prologue, Epilogue epilogue, hipStream_t stream);
 
+// Batches of up to 8 sequences.  launch_q8l_prep builds each sequence's
+// quantized activation (F32, RMSNORM or GATED prologue; x and z [batch][width])
+// into q8l [batch][q8l_bytes(width)]; launch_q8_batch_matvec evaluates the
+// segments for every sequence from it, outputs [batch][rows] (SILU_PAIR's
+// out_q8l [batch][q8l_bytes(rows)], conv windows [batch][kernel-1][conv_size]).
+hipError_t launch_q8l_prep(const MatvecInput &in, Prologue prologue, void *q8l, int batch, hipStream_t stream);
+hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, const void *q8l, int width, int batch,
+    Epilogue epilogue, hipStream_t stream);
+
 // Repack GGUF Q8_0 bytes [rows][blocks][34] (device) into the Q8Matrix planes.
 hipError_t launch_q8_repack(const uint8_t *gguf, int rows, int blocks, uint4 *quants,
     uint2 *scales, hipStream_t stream);
@@ -96,10 +105,11 @@ hipError_t launch_q8_block_dots(const Q8Matrix &w, const int8_t *xq34, int32_t *
     hipStream_t stream);
 
 // Small elementwise / norm kernels of the reference ABI.
+// batch > 1 (device tokens only): token[s] -> out + s * width
 hipError_t launch_q8_embedding(const Q8Matrix &w, const int64_t *token, int64_t token_value, float *out,
-    hipStream_t stream);
+    hipStream_t stream, int batch = 1);
 hipError_t launch_f16_embedding(const uint16_t *table, int width, const int64_t *token,
-    int64_t token_value, float *out, hipStream_t stream);
+    int64_t token_value, float *out, hipStream_t stream, int batch = 1);
 hipError_t launch_add(const float *a, const float *b, float *out, int n, hipStream_t stream);
 hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, float eps,
     hipStream_t stream);
@@ -118,9 +128,17 @@ struct ArgmaxState {
 hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite_halves, const float *x,
     const float *norm, float eps, float *out, const ArgmaxState *argmax, hipStream_t stream);
 int f16_matvec_workgroups(int rows);
+// The fp16 LM head for `batch` (<= 8) sequences at once: final RMSNorm
+// (norm required), x [batch][width] -> out [batch][rows], argmax partials
+// [batch][f16_batch_lm_head_workgroups(rows)], then the per-sequence finish.
+hipError_t launch_f16_batch_lm_head(const uint16_t *w, int rows, int width, bool finite, int batch, const float *x,
+    const float *norm, float eps, float *out, const ArgmaxState &argmax, hipStream_t stream);
+int f16_batch_lm_head_workgroups(int rows);
 hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, hipStream_t stream);
 // reduce `partials` argmax partials and publish token / trace / position
-hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream);
+// batch > 1: sequence s reduces partials [s * partials, (s + 1) * partials)
+// into token[s], trace[s * trace_capacity + position[s]], position[s]
+hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream, int batch = 1);
 // scan an fp16 table for exponent-31 patterns (inf/NaN), counted into *count
 hipError_t launch_count_nonfinite_halves(const uint16_t *w, size_t n, unsigned int *count, hipStream_t stream);
 
@@ -148,7 +166,8 @@ struct GdnParams {
     float eps = 0.0f;
 };
 // The delta rule, 16 state rows per workgroup: writes the raw output o.
-hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream);
+// batch > 1: sequences along blockIdx.y, every buffer [batch][single size]
+hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream, int batch = 1);
 // Causal conv1d + SiLU of every channel of x, shifting the windows
 // conv_state[K-1][channels] (oldest first).
 hipError_t launch_conv_silu(const float *x, const float *conv_w, float *conv_state, float *out, int channels, int K,
@@ -178,7 +197,9 @@ struct AttentionParams {
     float *split = nullptr;         // [heads][attention_split_chunks][value + 2]
 };
 int attention_split_chunks(int max_context);
-hipError_t launch_attention(const AttentionParams &p, hipStream_t stream);
+// batch > 1: sequences along blockIdx.y, every buffer [batch][single size],
+// position[batch]
+hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int batch = 1);
 size_t attention_scores_floats(int heads, int max_context);
 
 // ---- persistent decoder ------------------------------------------------------

@@ -50,8 +50,21 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const float *__restrict_
 constexpr int kDeltaRows = 16;
 constexpr int kDeltaThreads = kDeltaRows * 8;
 
+// Sequence s of a batch (blockIdx.y): buffers laid out [batch][...] with the
+// single-sequence sizes.
+__device__ __forceinline__ GdnParams gdn_seq(GdnParams p, int s) {
+    const size_t conv = static_cast<size_t>(2) * p.state_size * p.key_heads + static_cast<size_t>(p.value_heads) * p.head;
+    p.qkv += s * conv;
+    p.alpha += static_cast<size_t>(s) * p.value_heads;
+    p.beta += static_cast<size_t>(s) * p.value_heads;
+    p.state += static_cast<size_t>(s) * p.value_heads * p.head * p.head;
+    p.out += static_cast<size_t>(s) * p.value_heads * p.head;
+    return p;
+}
+
 template <int HEAD>
-__global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParams p) {
+__global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParams p_batch) {
+    const GdnParams p = gdn_seq(p_batch, static_cast<int>(blockIdx.y));
     constexpr int kCols = HEAD / 8;
     __shared__ __align__(16) float qs[HEAD];
     __shared__ __align__(16) float ks[HEAD];
@@ -140,9 +153,9 @@ hipError_t launch_conv_silu(const float *x, const float *conv_w, float *conv_sta
     return hipGetLastError();
 }
 
-hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream) {
-    if (p.key_heads <= 0 || p.value_heads % p.key_heads || p.state_size != p.head || !p.out) return hipErrorInvalidValue;
-    const dim3 grid(p.value_heads * (p.head / kDeltaRows));
+hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream, int batch) {
+    if (batch < 1 || p.key_heads <= 0 || p.value_heads % p.key_heads || p.state_size != p.head || !p.out) return hipErrorInvalidValue;
+    const dim3 grid(p.value_heads * (p.head / kDeltaRows), batch);
     switch (p.head) {
     case 64: hipLaunchKernelGGL(gdn_delta_kernel<64>, grid, dim3(kDeltaThreads), 0, stream, p); break;
     case 128: hipLaunchKernelGGL(gdn_delta_kernel<128>, grid, dim3(kDeltaThreads), 0, stream, p); break;

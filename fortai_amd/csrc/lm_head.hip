@@ -53,6 +53,12 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(int partials, Argmax
     __shared__ float sv[4];
     __shared__ int si[4];
     const int tid = static_cast<int>(threadIdx.x);
+    const int seq = static_cast<int>(blockIdx.y);  // batch: sequence seq's partials, token, trace, position
+    st.partial_value += static_cast<size_t>(seq) * partials;
+    st.partial_index += static_cast<size_t>(seq) * partials;
+    st.token += seq;
+    if (st.trace) st.trace += static_cast<size_t>(seq) * st.trace_capacity;
+    if (st.position) st.position += seq;
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
     for (int w = tid; w < partials; w += 256)
@@ -172,6 +178,141 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
     }
 }
 
+// Batched LM head: the fp16 table is read once for `batch` sequences.  Each
+// thread owns one row and runs, for every sequence, the same sequential chain
+// as f16_matvec_kernel (same tile order, same mul-then-add), and the final
+// RMSNorm of each sequence uses that kernel's reduction layout (128 strided
+// partial sums, then the two wave sums in order), so each sequence's logits
+// equal the single-sequence kernel's bit for bit.  256 rows x 64 columns per
+// tile; x of every sequence in LDS; per-sequence argmax partials.
+constexpr int kBatchRows = 256;
+constexpr int kBatchTile = 64;
+constexpr int kMaxBatch = 8;
+
+template <bool FINITE>
+__global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uint16_t *__restrict__ w, int rows,
+    int width, int batch, const float *__restrict__ x, const float *__restrict__ norm, float eps,
+    float *__restrict__ out, ArgmaxState st) {
+    constexpr int kPitch = kBatchTile + 8;
+    extern __shared__ __align__(16) unsigned char lds[];
+    uint16_t *tile = reinterpret_cast<uint16_t *>(lds);
+    float *xs = reinterpret_cast<float *>(lds + kBatchRows * kPitch * 2);  // [batch][width]
+    __shared__ double red[kMaxBatch][2];
+    __shared__ float sv[kBatchRows / 64];
+    __shared__ int si[kBatchRows / 64];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int row0 = static_cast<int>(blockIdx.x) * kBatchRows;
+
+    constexpr int kSegs = kBatchTile / 8;
+    constexpr int kLoads = kBatchTile * 2 / 16;  // 16-byte loads per thread and tile (one row's worth)
+    uint4 ra[kLoads], rb[kLoads];
+    auto fetch = [&](int k0, uint4 (&regs)[kLoads]) {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int li = tid + kBatchRows * j;
+            const int r = li / kSegs, seg = li % kSegs;
+            const int grow = min(row0 + r, rows - 1);
+            regs[j] = load_stream(reinterpret_cast<const uint4 *>(w + static_cast<size_t>(grow) * width + k0 + seg * 8));
+        }
+    };
+    auto stash = [&](const uint4 (&regs)[kLoads]) {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int li = tid + kBatchRows * j;
+            const int r = li / kSegs, seg = li % kSegs;
+            *reinterpret_cast<uint4 *>(tile + r * kPitch + seg * 8) = regs[j];
+        }
+    };
+    const int tiles = width / kBatchTile;
+    fetch(0, ra);
+    if (tiles > 1) fetch(kBatchTile, rb);
+
+    // RMSNorm of every sequence (fortai_qwen35_cpu.f90:707): threads 0-127
+    // take the even sequences, 128-255 the odd ones, each with the
+    // single-sequence kernel's partition of the sum
+    const int half = tid >> 7, ht = tid & 127;
+    for (int s0 = 0; s0 < batch; s0 += 2) {
+        const int s = s0 + half;
+        if (s < batch) {
+            const float *xq = x + static_cast<size_t>(s) * width;
+            double ss = 0.0;
+            for (int i = ht; i < width; i += 128) ss += static_cast<double>(xq[i]) * static_cast<double>(xq[i]);
+            ss = wave_sum(ss);
+            if ((ht & 63) == 0) red[s][ht >> 6] = ss;
+        }
+    }
+    __syncthreads();
+    for (int s = 0; s < batch; ++s) {
+        double total = 0.0;
+        total += red[s][0];
+        total += red[s][1];
+        const float inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+        const float *xq = x + static_cast<size_t>(s) * width;
+        for (int i = tid; i < width; i += kBatchRows) xs[s * width + i] = (xq[i] * inv) * norm[i];
+    }
+
+    float acc[kMaxBatch];
+#pragma unroll
+    for (int s = 0; s < kMaxBatch; ++s) acc[s] = 0.0f;
+    auto consume = [&](int k0) {
+        const uint16_t *mine = tile + tid * kPitch;
+#pragma unroll 2
+        for (int sg = 0; sg < kBatchTile / 8; ++sg) {
+            const uint4 h8 = *reinterpret_cast<const uint4 *>(mine + sg * 8);
+            const uint32_t hw[4] = {h8.x, h8.y, h8.z, h8.w};
+            float a[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a[2 * q] = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[q] & 0xffffu))
+                                  : gguf_half_to_real(static_cast<uint16_t>(hw[q] & 0xffffu));
+                a[2 * q + 1] = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[q] >> 16))
+                                      : gguf_half_to_real(static_cast<uint16_t>(hw[q] >> 16));
+            }
+            const int k = k0 + sg * 8;
+#pragma unroll
+            for (int s = 0; s < kMaxBatch; ++s) {
+                if (s < batch) {
+                    const float4 x0 = *reinterpret_cast<const float4 *>(xs + s * width + k);
+                    const float4 x1 = *reinterpret_cast<const float4 *>(xs + s * width + k + 4);
+                    float v = acc[s];
+                    v = v + a[0] * x0.x; v = v + a[1] * x0.y; v = v + a[2] * x0.z; v = v + a[3] * x0.w;
+                    v = v + a[4] * x1.x; v = v + a[5] * x1.y; v = v + a[6] * x1.z; v = v + a[7] * x1.w;
+                    acc[s] = v;
+                }
+            }
+        }
+    };
+    for (int t = 0; t < tiles; t += 2) {
+        __syncthreads();
+        stash(ra);
+        __syncthreads();
+        if (t + 2 < tiles) fetch((t + 2) * kBatchTile, ra);
+        consume(t * kBatchTile);
+        if (t + 1 >= tiles) break;
+        __syncthreads();
+        stash(rb);
+        __syncthreads();
+        if (t + 3 < tiles) fetch((t + 3) * kBatchTile, rb);
+        consume((t + 1) * kBatchTile);
+    }
+    const int row = row0 + tid;
+    const int parts = static_cast<int>(gridDim.x);
+#pragma unroll
+    for (int s = 0; s < kMaxBatch; ++s) {
+        if (s < batch) {
+            if (row < rows) out[static_cast<size_t>(s) * rows + row] = acc[s];
+            float v = row < rows ? acc[s] : -__builtin_inff();
+            int i = row < rows ? row : 0x7fffffff;
+            block_argmax(v, i, sv, si);
+            if (tid == 0) {
+                st.partial_value[static_cast<size_t>(s) * parts + blockIdx.x] = v;
+                st.partial_index[static_cast<size_t>(s) * parts + blockIdx.x] = i;
+            }
+            __syncthreads();  // sv / si are reused by the next sequence
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void argmax_kernel(const float *values, int n, ArgmaxState st) {
     __shared__ float sv[4];
     __shared__ int si[4];
@@ -230,6 +371,24 @@ hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite
     return launch_argmax_finish(grid, st, stream);
 }
 
+int f16_batch_lm_head_workgroups(int rows) { return (rows + kBatchRows - 1) / kBatchRows; }
+
+hipError_t launch_f16_batch_lm_head(const uint16_t *w, int rows, int width, bool finite, int batch, const float *x,
+    const float *norm, float eps, float *out, const ArgmaxState &argmax, hipStream_t stream) {
+    if (rows <= 0 || width <= 0 || width % kBatchTile || batch < 1 || batch > kMaxBatch || !norm) return hipErrorInvalidValue;
+    const int grid = f16_batch_lm_head_workgroups(rows);
+    const size_t lds = static_cast<size_t>(kBatchRows) * (kBatchTile + 8) * 2 + static_cast<size_t>(batch) * width * 4;
+    if (finite)
+        hipLaunchKernelGGL(f16_batch_lm_head_kernel<true>, dim3(grid), dim3(kBatchRows), lds, stream, w, rows, width,
+            batch, x, norm, eps, out, argmax);
+    else
+        hipLaunchKernelGGL(f16_batch_lm_head_kernel<false>, dim3(grid), dim3(kBatchRows), lds, stream, w, rows, width,
+            batch, x, norm, eps, out, argmax);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_argmax_finish(grid, argmax, stream, batch);
+}
+
 hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, hipStream_t stream) {
     int grid = (n + 255) / 256;
     if (grid > 1024) grid = 1024;
@@ -239,8 +398,9 @@ hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, h
     return launch_argmax_finish(grid, state, stream);
 }
 
-hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, stream, partials, state);
+hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream, int batch) {
+    if (batch < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(1, batch), dim3(256), 0, stream, partials, state);
     return hipGetLastError();
 }
 

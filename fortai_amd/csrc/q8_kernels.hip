@@ -395,6 +395,231 @@ hipError_t launch_matvec_pro(const MatvecArgs &args, int waves, int grid, int ch
     return hipErrorInvalidValue;
 }
 
+// ---- batches of sequences ----------------------------------------------------
+// The activation of each sequence is built once per step by q8l_prep_kernel
+// (one workgroup per sequence, the same code as the single-sequence
+// prologues, into the Q8L layout in device memory); the batched matvec then
+// streams every weight once for all sequences.  Per (row, sequence) it runs
+// the single-sequence kernel's eight lane chains, horizontal sum and
+// epilogue, so each sequence's outputs are bit-identical to batch 1.
+constexpr int kMaxBatch = 8;
+constexpr int kBatchThreads = 256;
+
+template <Prologue PRO>
+__global__ __launch_bounds__(kBatchThreads) void q8l_prep_kernel(MatvecInput in, void *q8l) {
+    __shared__ double red[kBatchThreads / 64];
+    const int seq = static_cast<int>(blockIdx.x);
+    const int chunks = (in.width / kQ8Block + 3) / 4;
+    in.x += static_cast<size_t>(seq) * in.width;
+    if (in.z) in.z += static_cast<size_t>(seq) * in.width;
+    unsigned char *base = static_cast<unsigned char *>(q8l) + static_cast<size_t>(seq) * q8l_bytes(in.width);
+    build_activation<kBatchThreads, PRO>(in, chunks, reinterpret_cast<uint32_t *>(base),
+        reinterpret_cast<float *>(base + static_cast<size_t>(chunks) * 128), red);
+}
+
+struct BatchMatvecArgs {
+    MatvecSegment seg[4];  // outputs [batch][rows]; conv windows [batch][kernel-1][conv_size]
+    int first_wg[5];
+    int count;
+    int chunks;            // activation chunks
+    int batch;
+    int split;             // waves sharing one row group (each takes every split-th sequence)
+    int pair_vector_rows;
+    const void *act;       // Q8L [batch][q8l_bytes(width)]
+};
+
+__device__ __forceinline__ float dot_chunk_f(uint4 q, const float (&ws)[4], uint4 a, float4 as, float acc) {
+    acc = __builtin_fmaf(ws[0] * as.x, static_cast<float>(sdot4(q.x, a.x)), acc);
+    acc = __builtin_fmaf(ws[1] * as.y, static_cast<float>(sdot4(q.y, a.y)), acc);
+    acc = __builtin_fmaf(ws[2] * as.z, static_cast<float>(sdot4(q.z, a.z)), acc);
+    acc = __builtin_fmaf(ws[3] * as.w, static_cast<float>(sdot4(q.w, a.w)), acc);
+    return acc;
+}
+
+__device__ __forceinline__ void scales_f(uint2 sc, float (&ws)[4]) {
+    ws[0] = half_bits_to_float(static_cast<uint16_t>(sc.x));
+    ws[1] = half_bits_to_float(static_cast<uint16_t>(sc.x >> 16));
+    ws[2] = half_bits_to_float(static_cast<uint16_t>(sc.y));
+    ws[3] = half_bits_to_float(static_cast<uint16_t>(sc.y >> 16));
+}
+
+// Four waves per workgroup; wave w takes row group slot w / split and the
+// sequences w % split, w % split + split, ...  Weights stream in batches of
+// 8 chunks (the next batch in flight while one is consumed).
+template <Epilogue EPI>
+__global__ __launch_bounds__(kBatchThreads) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
+    constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
+    constexpr int kPieces = 28;  // 16-byte activation pieces per thread (8 sequences x 96 chunks)
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int seq_bytes = args.chunks * 144;
+    float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.batch) * seq_bytes);  // [8][32]
+
+    const int wg = static_cast<int>(blockIdx.x);
+    int sgi = 0;
+    while (sgi + 1 < args.count && wg >= args.first_wg[sgi + 1]) ++sgi;
+    const MatvecSegment &seg = args.seg[sgi];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int split = args.split, slot = wave / split, sub = wave % split;
+    const int rg = (wg - args.first_wg[sgi]) * (4 / split) + slot;
+    const bool active = rg < seg.w.row_groups;
+    const int rgc = active ? rg : seg.w.row_groups - 1;
+    const int r = lane >> 3, l = lane & 7;
+    const int chunks = seg.w.chunks;
+    const uint4 *qp = seg.w.quants + static_cast<size_t>(rgc) * chunks * 64 + lane;
+    const uint2 *sp = seg.w.scales + static_cast<size_t>(rgc) * chunks * 8 + r;
+    const uint4 *qp2 = kPair ? seg.w2.quants + static_cast<size_t>(rgc) * chunks * 64 + lane : nullptr;
+    const uint2 *sp2 = kPair ? seg.w2.scales + static_cast<size_t>(rgc) * chunks * 8 + r : nullptr;
+    const int ns = (args.batch - sub + split - 1) / split;  // sequences of this wave
+
+    // first weight batch, then the activations of every sequence
+    uint4 qa[8], qa2[kPair ? 8 : 1];
+    uint2 sa[8], sa2[kPair ? 8 : 1];
+    auto fetch = [&](int c0, uint4 (&q)[8], uint2 (&sc)[8], uint4 (&q2)[kPair ? 8 : 1], uint2 (&sc2)[kPair ? 8 : 1]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = min(c0 + i, chunks - 1);  // clamped: uniform trip count
+            q[i] = load_stream(qp + static_cast<size_t>(c) * 64);
+            sc[i] = load_stream(sp + static_cast<size_t>(c) * 8);
+            if constexpr (kPair) {
+                q2[i] = load_stream(qp2 + static_cast<size_t>(c) * 64);
+                sc2[i] = load_stream(sp2 + static_cast<size_t>(c) * 8);
+            }
+        }
+    };
+    fetch(0, qa, sa, qa2, sa2);
+    {
+        const int pieces = args.batch * seq_bytes / 16;
+        const int iters = (pieces + kBatchThreads - 1) / kBatchThreads;
+        const u32x4_t *src = static_cast<const u32x4_t *>(args.act);
+        u32x4_t *dst = reinterpret_cast<u32x4_t *>(lds);
+        u32x4_t v[kPieces];
+#pragma unroll
+        for (int k = 0; k < kPieces; ++k)
+            if (k < iters) v[k] = src[min(tid + k * kBatchThreads, pieces - 1)];
+#pragma unroll
+        for (int k = 0; k < kPieces; ++k) {
+            const int i = tid + k * kBatchThreads;
+            if (k < iters && i < pieces) dst[i] = v[k];
+        }
+    }
+    const int row = rg * kRowsPerWave + r;
+    const bool writer = active && l == 0 && row < seg.w.rows;
+    // per-sequence residuals and conv windows, loaded now
+    float resid[kMaxBatch], win[kMaxBatch][kConvMax - 1], taps[kConvMax];
+    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr;
+    const int ck = conv ? seg.kernel : 0;
+#pragma unroll
+    for (int k = 0; k < kMaxBatch; ++k) {
+        const int sq = sub + k * split;
+        resid[k] = 0.0f;
+        if constexpr (EPI == Epilogue::ADD)
+            if (writer && k < ns) resid[k] = seg.resid[static_cast<size_t>(sq) * seg.w.rows + row];
+        if (conv && writer && k < ns) {
+#pragma unroll
+            for (int t = 0; t < kConvMax - 1; ++t)
+                if (t < ck - 1)
+                    win[k][t] = seg.conv_state[(static_cast<size_t>(sq) * (ck - 1) + t) * seg.conv_size + row];
+        }
+    }
+    if (conv && writer) {
+#pragma unroll
+        for (int t = 0; t < kConvMax; ++t)
+            if (t < ck) taps[t] = seg.conv_w[static_cast<size_t>(row) * ck + t];
+    }
+    __syncthreads();
+
+    float acc[kMaxBatch], acc2[kMaxBatch];
+#pragma unroll
+    for (int k = 0; k < kMaxBatch; ++k) { acc[k] = 0.0f; acc2[k] = 0.0f; }
+    auto consume = [&](int c0, const uint4 (&q)[8], const uint2 (&sc)[8], const uint4 (&q2)[kPair ? 8 : 1],
+                       const uint2 (&sc2)[kPair ? 8 : 1]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = c0 + i;
+            if (c < chunks) {
+                float ws[4], ws2[4];
+                scales_f(sc[i], ws);
+                if constexpr (kPair) scales_f(sc2[i], ws2);
+#pragma unroll
+                for (int k = 0; k < kMaxBatch; ++k) {
+                    if (k < ns) {
+                        const unsigned char *sb = lds + static_cast<size_t>(sub + k * split) * seq_bytes;
+                        const uint4 a = reinterpret_cast<const uint4 *>(sb)[c * 8 + l];
+                        const float4 as = reinterpret_cast<const float4 *>(sb + static_cast<size_t>(args.chunks) * 128)[c];
+                        acc[k] = dot_chunk_f(q[i], ws, a, as, acc[k]);
+                        if constexpr (kPair) acc2[k] = dot_chunk_f(q2[i], ws2, a, as, acc2[k]);
+                    }
+                }
+            }
+        }
+    };
+    uint4 qb[8], qb2[kPair ? 8 : 1];
+    uint2 sb[8], sb2[kPair ? 8 : 1];
+    if (active) {
+        for (int c0 = 0; c0 < chunks; c0 += 16) {
+            if (c0 + 8 < chunks) fetch(c0 + 8, qb, sb, qb2, sb2);
+            consume(c0, qa, sa, qa2, sa2);
+            if (c0 + 8 >= chunks) break;
+            if (c0 + 16 < chunks) fetch(c0 + 16, qa, sa, qa2, sa2);
+            consume(c0 + 8, qb, sb, qb2, sb2);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxBatch; ++k) {
+        if (k < ns) {
+            acc[k] = row_hsum8(acc[k]);
+            if constexpr (kPair) acc2[k] = row_hsum8(acc2[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxBatch; ++k) {
+        if (k >= ns) continue;
+        const int sq = sub + k * split;
+        float *out = seg.out ? seg.out + static_cast<size_t>(sq) * seg.w.rows : nullptr;
+        if constexpr (EPI == Epilogue::STORE) {
+            if (conv && writer) {
+                float *cs = seg.conv_state + static_cast<size_t>(sq) * (ck - 1) * seg.conv_size;
+                out[row] = conv_silu(win[k], taps, ck, acc[k]);
+#pragma unroll
+                for (int t = 0; t + 1 < kConvMax - 1; ++t)
+                    if (t + 1 < ck - 1) cs[static_cast<size_t>(t) * seg.conv_size + row] = win[k][t + 1];
+                cs[static_cast<size_t>(ck - 2) * seg.conv_size + row] = acc[k];
+            } else if (writer) {
+                out[row] = seg.silu ? silu_poly(acc[k]) : acc[k];
+            }
+        } else if constexpr (EPI == Epilogue::ADD) {
+            if (writer) out[row] = acc[k] + resid[k];
+        } else {
+            const float h = row < args.pair_vector_rows ? silu_poly(acc[k]) * acc2[k]
+                                                        : acc[k] / (1.0f + exp_rounded(-acc[k])) * acc2[k];
+            if (writer && out) out[row] = h;
+            if (seg.out_q8l && l == 0) epi[sq * 32 + wave * 8 + r] = h;
+        }
+    }
+    if constexpr (kPair) {
+        if (seg.out_q8l) {
+            // split == 1: the workgroup's 32 rows form one quantization block of
+            // every sequence's h
+            __syncthreads();
+            const int t = tid & 7, sq = tid >> 3;
+            if (sq < args.batch) {
+                const float *e = epi + sq * 32;
+                const float4 y = make_float4(e[4 * t], e[4 * t + 1], e[4 * t + 2], e[4 * t + 3]);
+                float scale;
+                uint16_t bits;
+                const uint32_t packed = quantize_group(y, scale, bits);
+                const int b = wg - args.first_wg[sgi];
+                const int hchunks = (seg.w.rows / kQ8Block + 3) / 4;
+                uint32_t *dq = reinterpret_cast<uint32_t *>(static_cast<unsigned char *>(seg.out_q8l) +
+                    static_cast<size_t>(sq) * q8l_bytes(seg.w.rows));
+                dq[((b >> 2) * 8 + t) * 4 + (b & 3)] = packed;
+                if (t == 0) reinterpret_cast<float *>(dq + hchunks * 32)[b] = scale;
+            }
+        }
+    }
+}
+
 __global__ void q8_repack_kernel(const uint8_t *gguf, int rows, int blocks, int chunks,
     int row_groups, uint4 *quants, uint2 *scales) {
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -480,7 +705,9 @@ __global__ void q8_block_dots_kernel(Q8Matrix w, const int8_t *xq, int32_t *out,
 __global__ void q8_embedding_kernel(Q8Matrix w, const int64_t *token, int64_t token_value, float *out) {
     const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= w.blocks * kQ8Block) return;
-    const int64_t t = token ? *token : token_value;
+    const int seq = static_cast<int>(blockIdx.y);  // batch: token[seq] -> row seq of out
+    out += static_cast<size_t>(seq) * w.blocks * kQ8Block;
+    const int64_t t = token ? token[seq] : token_value;
     const int g = static_cast<int>(t >> 3), r = static_cast<int>(t & 7);
     const int b = i / kQ8Block, within = i % kQ8Block, l = within >> 2, byte = within & 3;
     const int c = b >> 2, j = b & 3;
@@ -496,7 +723,9 @@ __global__ void f16_embedding_kernel(const uint16_t *table, int width, const int
     int64_t token_value, float *out) {
     const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= width) return;
-    const int64_t t = token ? *token : token_value;
+    const int seq = static_cast<int>(blockIdx.y);  // batch: token[seq] -> row seq of out
+    out += static_cast<size_t>(seq) * width;
+    const int64_t t = token ? token[seq] : token_value;
     out[i] = gguf_half_to_real(table[t * width + i]);
 }
 
@@ -579,6 +808,84 @@ hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const Matv
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_q8l_prep(const MatvecInput &in, Prologue prologue, void *q8l, int batch, hipStream_t stream) {
+    constexpr int kPre = ActShape<kBatchThreads, Prologue::F32>::kPre;
+    if (batch < 1 || batch > kMaxBatch || in.width <= 0 || in.width % kQ8Block || in.width / 4 > kPre * kBatchThreads)
+        return hipErrorInvalidValue;
+    switch (prologue) {
+    case Prologue::F32:
+        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::F32>, dim3(batch), dim3(kBatchThreads), 0, stream, in, q8l);
+        break;
+    case Prologue::RMSNORM:
+        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::RMSNORM>, dim3(batch), dim3(kBatchThreads), 0, stream, in, q8l);
+        break;
+    case Prologue::GATED: {
+        const int hl = in.head / 4;
+        if (in.head <= 0 || in.head % 4 || hl > 64 || (hl & (hl - 1)) || in.width % in.head || !in.z || !in.norm)
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::GATED>, dim3(batch), dim3(kBatchThreads), 0, stream, in, q8l);
+        break;
+    }
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, const void *q8l, int width, int batch,
+    Epilogue epilogue, hipStream_t stream) {
+    const int chunks = (width / kQ8Block + 3) / 4;
+    if (count < 1 || count > 4 || width <= 0 || width % kQ8Block || batch < 1 || batch > kMaxBatch ||
+        batch * chunks * 9 > 28 * kBatchThreads)
+        return hipErrorInvalidValue;
+    int total_groups = 0;
+    for (int s = 0; s < count; ++s) {
+        if (segments[s].w.chunks != chunks) return hipErrorInvalidValue;
+        if (segments[s].conv_w && (epilogue != Epilogue::STORE || segments[s].kernel < 2 ||
+                                     segments[s].kernel > kConvMax || segments[s].conv_size < segments[s].w.rows))
+            return hipErrorInvalidValue;
+        total_groups += segments[s].w.row_groups;
+    }
+    // enough waves for the chip: sequences spread over up to 4 waves per row
+    // group when the matrices are small (the quantized-h epilogue needs all
+    // sequences of 32 rows in one workgroup)
+    int split = total_groups >= 1024 ? 1 : (total_groups >= 512 ? 2 : 4);
+    if (epilogue == Epilogue::SILU_PAIR) {
+        if (count != 1 || (segments[0].out_q8l && segments[0].w.rows % kQ8Block)) return hipErrorInvalidValue;
+        if (segments[0].out_q8l) split = 1;
+    }
+    BatchMatvecArgs args{};
+    args.count = count;
+    args.chunks = chunks;
+    args.batch = batch;
+    args.split = split;
+    args.act = q8l;
+    int grid = 0;
+    const int per_wg = 4 / split;
+    for (int s = 0; s < count; ++s) {
+        args.seg[s] = segments[s];
+        args.first_wg[s] = grid;
+        grid += (segments[s].w.row_groups + per_wg - 1) / per_wg;
+    }
+    args.first_wg[count] = grid;
+    const int rows = segments[0].w.rows;
+    args.pair_vector_rows = rows >= 8 ? (rows / 8) * 8 : 0;
+    if (grid == 0) return hipSuccess;
+    const size_t lds = static_cast<size_t>(batch) * chunks * 144 + kMaxBatch * 32 * 4;
+    switch (epilogue) {
+    case Epilogue::STORE:
+        hipLaunchKernelGGL(q8_batch_matvec_kernel<Epilogue::STORE>, dim3(grid), dim3(kBatchThreads), lds, stream, args);
+        break;
+    case Epilogue::ADD:
+        hipLaunchKernelGGL(q8_batch_matvec_kernel<Epilogue::ADD>, dim3(grid), dim3(kBatchThreads), lds, stream, args);
+        break;
+    case Epilogue::SILU_PAIR:
+        hipLaunchKernelGGL(q8_batch_matvec_kernel<Epilogue::SILU_PAIR>, dim3(grid), dim3(kBatchThreads), lds, stream,
+            args);
+        break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_q8_repack(const uint8_t *gguf, int rows, int blocks, uint4 *quants, uint2 *scales,
     hipStream_t stream) {
     const int chunks = (blocks + 3) / 4;
@@ -605,15 +912,17 @@ hipError_t launch_q8_block_dots(const Q8Matrix &w, const int8_t *xq34, int32_t *
 }
 
 hipError_t launch_q8_embedding(const Q8Matrix &w, const int64_t *token, int64_t token_value, float *out,
-    hipStream_t stream) {
+    hipStream_t stream, int batch) {
+    if (batch < 1 || (batch > 1 && !token)) return hipErrorInvalidValue;
     const int n = w.blocks * kQ8Block;
-    hipLaunchKernelGGL(q8_embedding_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, w, token, token_value, out);
+    hipLaunchKernelGGL(q8_embedding_kernel, dim3((n + 255) / 256, batch), dim3(256), 0, stream, w, token, token_value, out);
     return hipGetLastError();
 }
 
 hipError_t launch_f16_embedding(const uint16_t *table, int width, const int64_t *token, int64_t token_value,
-    float *out, hipStream_t stream) {
-    hipLaunchKernelGGL(f16_embedding_kernel, dim3((width + 255) / 256), dim3(256), 0, stream, table, width, token,
+    float *out, hipStream_t stream, int batch) {
+    if (batch < 1 || (batch > 1 && !token)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(f16_embedding_kernel, dim3((width + 255) / 256, batch), dim3(256), 0, stream, table, width, token,
         token_value, out);
     return hipGetLastError();
 }

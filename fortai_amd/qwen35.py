@@ -81,7 +81,7 @@ def read_dims(f: gguf.GGUFFile) -> Qwen35Dims:
 
 
 class Qwen35Hip:
-    def __init__(self, path: str, max_context: int = 256, device: int = 0, fused: bool = True):
+    def __init__(self, path: str, max_context: int = 256, device: int = 0, fused: bool = True, batch: int = 0):
         self.file = gguf.read(path)
         self.d = d = read_dims(self.file)
         self.max_context = max_context
@@ -126,6 +126,15 @@ class Qwen35Hip:
         if fused:
             self.decoder = B.Decoder(
                 self.ctx, self.recurrent, self.attention,
+                [self.q8[f"blk.{i}.ffn_gate.weight"] for i in range(d.layers)],
+                [self.q8[f"blk.{i}.ffn_up.weight"] for i in range(d.layers)],
+                [self.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
+                [n["attn"] for n in self.norms], [n["post"] for n in self.norms], self.output_norm, d.hidden,
+                self.embedding, self.output, max_context, d.eps, d.vocab)
+        self.batch: Optional[B.BatchDecoder] = None
+        if batch:
+            self.batch = B.BatchDecoder(
+                self.ctx, batch, self.recurrent, self.attention,
                 [self.q8[f"blk.{i}.ffn_gate.weight"] for i in range(d.layers)],
                 [self.q8[f"blk.{i}.ffn_up.weight"] for i in range(d.layers)],
                 [self.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
@@ -203,6 +212,8 @@ class Qwen35Hip:
         return b["logits"].download(np.float32, d.vocab)
 
     def close(self) -> None:
+        if self.batch:
+            self.batch.free()
         if self.decoder:
             self.decoder.free()
         if self._ops:

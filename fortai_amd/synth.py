@@ -88,6 +88,19 @@ CONFIGS: Dict[str, Qwen35Config] = {
                                       rope_dim=64, gdn_key_heads=16, gdn_value_heads=16,
                                       gdn_state=128, gdn_inner=2048, conv_kernel=4,
                                       vocab=16384),
+    # BASELINE config 5 (Qwen3.5-4B shape): hidden 2560, 32 layers (24 GDN /
+    # 8 attention), FFN 9216, 16 q / 4 kv heads of 256.  BASELINE leaves the
+    # GDN heads open; 16 key / 32 value heads of 128 (value_heads % key_heads
+    # == 0, fortai_qwen35_cpu.f90:231-235) give conv channels 8192, inner 4096.
+    "qwen35-4b": Qwen35Config("qwen35-4b", hidden=2560, layers=32, ffn=9216, heads=16, kv_heads=4,
+                              head_size=256, value_size=256, rope_dim=64, gdn_key_heads=16,
+                              gdn_value_heads=32, gdn_state=128, gdn_inner=4096, conv_kernel=4,
+                              vocab=248320),
+    # Every 4B layer shape with 4 layers and a small vocabulary (fast parity).
+    "qwen35-4b-short": Qwen35Config("qwen35-4b-short", hidden=2560, layers=4, ffn=9216, heads=16,
+                                    kv_heads=4, head_size=256, value_size=256, rope_dim=64,
+                                    gdn_key_heads=16, gdn_value_heads=32, gdn_state=128,
+                                    gdn_inner=4096, conv_kernel=4, vocab=16384),
 }
 
 

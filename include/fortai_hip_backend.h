@@ -36,6 +36,7 @@ typedef struct fortai_hip_qwen35_recurrent fortai_hip_qwen35_recurrent;
 typedef struct fortai_hip_qwen35_attention fortai_hip_qwen35_attention;
 typedef struct fortai_hip_f16_weights fortai_hip_f16_weights;          /* [extension] */
 typedef struct fortai_hip_qwen35_decoder fortai_hip_qwen35_decoder;    /* [extension] */
+typedef struct fortai_hip_qwen35_batch fortai_hip_qwen35_batch;        /* [extension] */
 
 enum {
     FORTAI_HIP_OK = 0,
@@ -304,6 +305,43 @@ int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *decoder, ui
     size_t count);
 /* device pointer of the decoder's logits [vocab] */
 int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits);
+
+/* [extension] Batched decoder: `batch` (1..8) independent sequences over the
+ * same layers and weights as fortai_hip_qwen35_decoder_create (same
+ * arguments).  The layer objects supply weights and constants only: the batch
+ * object holds every sequence's conv/GDN state and KV cache (max_context
+ * positions each).  One step is one captured graph that reads every weight
+ * once for all sequences; each sequence's logits and tokens are bit-identical
+ * to the single-sequence decoder's.  The reference decodes one sequence at a
+ * time (app/fortai_cpu_run.f90:50-64); sequence s here is that loop on its own
+ * token and position. */
+int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *context, int batch, int layer_count,
+    fortai_hip_qwen35_recurrent *const *recurrent,
+    fortai_hip_qwen35_attention *const *attention,
+    const fortai_hip_q8_weights *const *ffn_gate,
+    const fortai_hip_q8_weights *const *ffn_up,
+    const fortai_hip_q8_weights *const *ffn_down,
+    const float *const *attn_norm, const float *const *post_norm,
+    const float *output_norm, int hidden_size,
+    const fortai_hip_f16_weights *embedding_f16, const fortai_hip_q8_weights *embedding_q8,
+    const fortai_hip_f16_weights *output_f16, const fortai_hip_q8_weights *output_q8,
+    int max_context, float norm_epsilon, fortai_hip_qwen35_batch **batch_decoder);
+int fortai_hip_qwen35_batch_destroy(fortai_hip_qwen35_batch *batch_decoder);
+/* zero every sequence's state, cache and trace */
+int fortai_hip_qwen35_batch_reset(fortai_hip_qwen35_batch *batch_decoder);
+/* one step of every sequence at (tokens[s], positions[s]); host_logits
+ * [batch][vocab] and next_tokens [batch] may be NULL */
+int fortai_hip_qwen35_batch_forward(fortai_hip_qwen35_batch *batch_decoder, const int64_t *tokens,
+    const int *positions, float *host_logits, int64_t *next_tokens);
+/* greedy decode of `steps` tokens per sequence from (tokens[s], positions[s]);
+ * host_trace [batch][steps] */
+int fortai_hip_qwen35_batch_generate(fortai_hip_qwen35_batch *batch_decoder, const int64_t *tokens,
+    const int *positions, int steps, int64_t *host_trace);
+/* enqueue `steps` further steps from the device tokens and positions (no
+ * synchronisation; for timing loops) */
+int fortai_hip_qwen35_batch_replay(fortai_hip_qwen35_batch *batch_decoder, int steps);
+/* device pointer of the logits [batch][vocab] */
+int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batch_decoder, void **device_logits);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,89 @@
+"""Batched decode (independent sequences sharing one set of
+weights) through the C ABI.
+
+The reference decodes one sequence at a time (app/fortai_cpu_run.f90:50-64),
+so the bar is per sequence: the batched step must give every sequence exactly
+the single-sequence decoder's logits and greedy tokens (bit-identical; the
+single-sequence decoder is itself checked against the oracle in
+test_gpu_model.py), and one sequence is also checked against the oracle here
+directly.
+"""
+
+import numpy as np
+import pytest
+
+from fortai_amd import synth
+from fortai_amd.qwen35 import Qwen35Hip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def model_paths(tmp_path_factory):
+    out = {}
+    d = tmp_path_factory.mktemp("batch_models")
+    for name in ("qwen35-tiny", "qwen35-tiny-q8emb", "qwen35-0.8b-short", "qwen35-4b-short"):
+        path = str(d / f"{name}.gguf")
+        synth.write_model(path, synth.CONFIGS[name])
+        out[name] = path
+    return out
+
+
+def run_single(m, token, position, steps):
+    """Logits and tokens of the single-sequence decoder from (token, position)."""
+    m.decoder.reset()
+    logits, toks = [], []
+    for k in range(steps):
+        nxt = m.decoder.forward(token, position + k)
+        logits.append(m.decoder.logits.copy())
+        toks.append(nxt)
+        token = nxt
+    return np.stack(logits), toks
+
+
+@pytest.mark.parametrize("name,batch,steps", [("qwen35-tiny", 3, 12), ("qwen35-tiny-q8emb", 8, 8),
+                                              ("qwen35-0.8b-short", 8, 6), ("qwen35-4b-short", 8, 4)])
+def test_batch_matches_single_sequence(model_paths, name, batch, steps):
+    m = Qwen35Hip(model_paths[name], max_context=64, batch=batch)
+    try:
+        rng = np.random.default_rng(batch * 7 + steps)
+        tokens = rng.integers(0, m.d.vocab, size=batch)
+        positions = rng.integers(0, 32, size=batch)  # independent positions (empty caches before them)
+        m.batch.reset()
+        cur = tokens.copy()
+        got_logits, got_tokens = [], []
+        for k in range(steps):
+            nxt = m.batch.forward(cur, positions + k)
+            got_logits.append(m.batch.logits.copy())
+            got_tokens.append(nxt.copy())
+            cur = nxt
+        got_logits = np.stack(got_logits)        # [steps][batch][vocab]
+        got_tokens = np.stack(got_tokens)        # [steps][batch]
+        for s in range(batch):
+            print(f"{name} sequence {s}: token {tokens[s]} position {positions[s]}", flush=True)
+            want_logits, want_tokens = run_single(m, int(tokens[s]), int(positions[s]), steps)
+            assert np.array_equal(got_logits[:, s].view(np.uint32), want_logits.view(np.uint32)), f"sequence {s}"
+            assert got_tokens[:, s].tolist() == want_tokens
+    finally:
+        m.close()
+
+
+def test_batch_generate_trace_matches_oracle(model_paths, oracle):
+    from oracle.oracle import OracleModel
+    path = model_paths["qwen35-tiny"]
+    m = Qwen35Hip(path, max_context=64, batch=4)
+    try:
+        starts = [9, 100, 4000, 9]
+        m.batch.reset()
+        got = m.batch.generate(starts, [0, 0, 0, 0], 40)
+        ref = OracleModel(oracle, path, 64)
+        for s, t in enumerate(starts):
+            ref.reset()
+            assert got[s].tolist() == ref.greedy(t, 40), f"sequence {s}"
+        assert got[0].tolist() == got[3].tolist()  # same start, independent state
+        # continuing after a reset reproduces the same traces
+        m.batch.reset()
+        again = m.batch.generate(starts, [0, 0, 0, 0], 40)
+        assert np.array_equal(again, got)
+    finally:
+        m.close()
