@@ -152,6 +152,7 @@ struct fortai_hip_qwen35_batch {
     int64_t *tokens = nullptr, *trace = nullptr;  // trace [batch][max_context]
     int *positions = nullptr;
     std::vector<int> next_positions;  // host mirror after the queued steps
+    bool use_graph = true;            // FORTAI_HIP_DECODER_GRAPH=0: enqueue the kernels every step
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
@@ -687,6 +688,26 @@ int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *c, const fortai_hip_q
     (void)hipSetDevice(c->device);
     return done(c, launch_q8_block_dots(w->m, static_cast<const int8_t *>(device_activation),
         static_cast<int32_t *>(device_dots), c->stream), "device block dots");
+}
+
+// ------------------------------------------------------ batched matvec
+int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x,
+    int batch, void *out, float *kernel_ms) {
+    if (!c || !owned(c, w) || !x || !out || batch < 1 || batch > 8) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    const size_t q8l = static_cast<size_t>(batch) * q8l_bytes(w->width);
+    hipError_t e = ensure(&c->scratch_q8l, &c->scratch_q8l_bytes, q8l);
+    if (e == hipSuccess && kernel_ms) e = hipEventRecord(c->start, c->stream);
+    MatvecInput in = f32_input(static_cast<const float *>(x), w->width);
+    if (e == hipSuccess) e = launch_q8l_prep(in, Prologue::F32, c->scratch_q8l, batch, c->stream);
+    const MatvecSegment seg = segment(w, static_cast<float *>(out));
+    if (e == hipSuccess) e = launch_q8_batch_matvec(&seg, 1, c->scratch_q8l, w->width, batch, Epilogue::STORE, c->stream);
+    if (kernel_ms) {
+        if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+        if (e == hipSuccess) e = hipEventElapsedTime(kernel_ms, c->start, c->stop);
+    }
+    return done(c, e, "batched matvec");
 }
 
 // ------------------------------------------------------ token blocks (MFMA)
@@ -1729,6 +1750,10 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
     return e;
 }
 
+hipError_t batch_step(fortai_hip_qwen35_batch *b) {
+    return b->use_graph ? hipGraphLaunch(b->exec, b->context->stream) : enqueue_batch_step(b, b->context->stream);
+}
+
 hipError_t batch_zero_state(fortai_hip_qwen35_batch *b, hipStream_t stream) {
     const size_t B = static_cast<size_t>(b->batch);
     hipError_t e = hipSuccess;
@@ -1858,14 +1883,17 @@ int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *c, int batch, int laye
     if (e == hipSuccess) e = hipMemsetAsync(b->positions, 0, B * sizeof(int), c->stream);
     if (e == hipSuccess) e = batch_zero_state(b, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    // one step captured as a graph (state, tokens and positions are device-side)
-    if (e == hipSuccess) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
-    if (e == hipSuccess) {
+    // one step captured as a graph (state, tokens and positions are device-side);
+    // FORTAI_HIP_DECODER_GRAPH=0 enqueues the kernels directly (kernel tracing)
+    const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
+    b->use_graph = !(graph_env && std::strcmp(graph_env, "0") == 0);
+    if (e == hipSuccess && b->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess && b->use_graph) {
         const hipError_t ce = enqueue_batch_step(b, c->stream);
         e = hipStreamEndCapture(c->stream, &b->graph);
         if (ce != hipSuccess) e = ce;
     }
-    if (e == hipSuccess) e = hipGraphInstantiate(&b->exec, b->graph, nullptr, nullptr, 0);
+    if (e == hipSuccess && b->use_graph) e = hipGraphInstantiate(&b->exec, b->graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         fortai_hip_qwen35_batch_destroy(b);
         return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen batch create", e);
@@ -1913,7 +1941,7 @@ int fortai_hip_qwen35_batch_forward(fortai_hip_qwen35_batch *b, const int64_t *t
     (void)hipSetDevice(c->device);
     const int rc = batch_set_inputs(b, tokens, positions, 1);
     if (rc != FORTAI_HIP_OK) return rc;
-    hipError_t e = hipGraphLaunch(b->exec, c->stream);
+    hipError_t e = batch_step(b);
     for (auto &p : b->next_positions) ++p;
     if (e == hipSuccess && logits)
         e = hipMemcpyAsync(logits, b->logits, static_cast<size_t>(b->batch) * b->vocab * sizeof(float),
@@ -1932,7 +1960,7 @@ int fortai_hip_qwen35_batch_generate(fortai_hip_qwen35_batch *b, const int64_t *
     const int rc = batch_set_inputs(b, tokens, positions, steps);
     if (rc != FORTAI_HIP_OK) return rc;
     hipError_t e = hipSuccess;
-    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(b->exec, c->stream);
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = batch_step(b);
     for (int q = 0; q < b->batch && e == hipSuccess; ++q) {
         e = hipMemcpyAsync(trace + static_cast<size_t>(q) * steps,
             b->trace + static_cast<size_t>(q) * b->max_context + positions[q], steps * sizeof(int64_t),
@@ -1950,7 +1978,7 @@ int fortai_hip_qwen35_batch_replay(fortai_hip_qwen35_batch *b, int steps) {
     auto *c = b->context;
     (void)hipSetDevice(c->device);
     hipError_t e = hipSuccess;
-    for (int s = 0; s < steps && e == hipSuccess; ++s) e = hipGraphLaunch(b->exec, c->stream);
+    for (int s = 0; s < steps && e == hipSuccess; ++s) e = batch_step(b);
     for (auto &p : b->next_positions) p += steps;
     return done(c, e, "batch replay");
 }

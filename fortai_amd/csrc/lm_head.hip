@@ -251,6 +251,11 @@ __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uin
         for (int i = tid; i < width; i += kBatchRows) xs[s * width + i] = (xq[i] * inv) * norm[i];
     }
 
+    // every sequence slot is computed (slots past the batch repeat the last
+    // sequence and are not written): no per-sequence branch in the inner loop
+    int xo[kMaxBatch];
+#pragma unroll
+    for (int s = 0; s < kMaxBatch; ++s) xo[s] = min(s, batch - 1) * width;
     float acc[kMaxBatch];
 #pragma unroll
     for (int s = 0; s < kMaxBatch; ++s) acc[s] = 0.0f;
@@ -260,6 +265,13 @@ __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uin
         for (int sg = 0; sg < kBatchTile / 8; ++sg) {
             const uint4 h8 = *reinterpret_cast<const uint4 *>(mine + sg * 8);
             const uint32_t hw[4] = {h8.x, h8.y, h8.z, h8.w};
+            const int k = k0 + sg * 8;
+            float4 x0[kMaxBatch], x1[kMaxBatch];
+#pragma unroll
+            for (int s = 0; s < kMaxBatch; ++s) {
+                x0[s] = *reinterpret_cast<const float4 *>(xs + xo[s] + k);
+                x1[s] = *reinterpret_cast<const float4 *>(xs + xo[s] + k + 4);
+            }
             float a[8];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -268,17 +280,12 @@ __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uin
                 a[2 * q + 1] = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[q] >> 16))
                                       : gguf_half_to_real(static_cast<uint16_t>(hw[q] >> 16));
             }
-            const int k = k0 + sg * 8;
 #pragma unroll
             for (int s = 0; s < kMaxBatch; ++s) {
-                if (s < batch) {
-                    const float4 x0 = *reinterpret_cast<const float4 *>(xs + s * width + k);
-                    const float4 x1 = *reinterpret_cast<const float4 *>(xs + s * width + k + 4);
-                    float v = acc[s];
-                    v = v + a[0] * x0.x; v = v + a[1] * x0.y; v = v + a[2] * x0.z; v = v + a[3] * x0.w;
-                    v = v + a[4] * x1.x; v = v + a[5] * x1.y; v = v + a[6] * x1.z; v = v + a[7] * x1.w;
-                    acc[s] = v;
-                }
+                float v = acc[s];
+                v = v + a[0] * x0[s].x; v = v + a[1] * x0[s].y; v = v + a[2] * x0[s].z; v = v + a[3] * x0[s].w;
+                v = v + a[4] * x1[s].x; v = v + a[5] * x1[s].y; v = v + a[6] * x1[s].z; v = v + a[7] * x1[s].w;
+                acc[s] = v;
             }
         }
     };

@@ -405,15 +405,17 @@ hipError_t launch_matvec_pro(const MatvecArgs &args, int waves, int grid, int ch
 constexpr int kMaxBatch = 8;
 constexpr int kBatchThreads = 256;
 
+constexpr int kPrepThreads = 512;  // activations up to 16384 wide
+
 template <Prologue PRO>
-__global__ __launch_bounds__(kBatchThreads) void q8l_prep_kernel(MatvecInput in, void *q8l) {
-    __shared__ double red[kBatchThreads / 64];
+__global__ __launch_bounds__(kPrepThreads) void q8l_prep_kernel(MatvecInput in, void *q8l) {
+    __shared__ double red[kPrepThreads / 64];
     const int seq = static_cast<int>(blockIdx.x);
     const int chunks = (in.width / kQ8Block + 3) / 4;
     in.x += static_cast<size_t>(seq) * in.width;
     if (in.z) in.z += static_cast<size_t>(seq) * in.width;
     unsigned char *base = static_cast<unsigned char *>(q8l) + static_cast<size_t>(seq) * q8l_bytes(in.width);
-    build_activation<kBatchThreads, PRO>(in, chunks, reinterpret_cast<uint32_t *>(base),
+    build_activation<kPrepThreads, PRO>(in, chunks, reinterpret_cast<uint32_t *>(base),
         reinterpret_cast<float *>(base + static_cast<size_t>(chunks) * 128), red);
 }
 
@@ -443,16 +445,21 @@ __device__ __forceinline__ void scales_f(uint2 sc, float (&ws)[4]) {
     ws[3] = half_bits_to_float(static_cast<uint16_t>(sc.y >> 16));
 }
 
-// Four waves per workgroup; wave w takes row group slot w / split and the
-// sequences w % split, w % split + split, ...  Weights stream in batches of
-// 8 chunks (the next batch in flight while one is consumed).
-template <Epilogue EPI>
-__global__ __launch_bounds__(kBatchThreads) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
+// Four waves per workgroup; wave w takes row group slot w / SPLIT and the
+// sequences w % SPLIT, w % SPLIT + SPLIT, ... (8 / SPLIT of them; indices past
+// the batch repeat its last sequence and write nothing).  The activations of
+// every sequence are copied to LDS by direct global-to-LDS loads; weights
+// stream in groups of G chunks (G divides the chunk count), two groups in
+// flight while one is consumed.  Every load is unconditional (clamped), so
+// the compiler's in-order load counters never wait for a prefetch.
+template <Epilogue EPI, int SPLIT, int G>
+__global__ __launch_bounds__(kBatchThreads, 2) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
-    constexpr int kPieces = 28;  // 16-byte activation pieces per thread (8 sequences x 96 chunks)
+    constexpr int NS = kMaxBatch / SPLIT;
     extern __shared__ __align__(16) unsigned char lds[];
     const int seq_bytes = args.chunks * 144;
-    float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.batch) * seq_bytes);  // [8][32]
+    const int act_bytes = (args.batch * seq_bytes + 1023) / 1024 * 1024;  // whole 1 KiB load blocks
+    float *epi = reinterpret_cast<float *>(lds + act_bytes);  // [8][32]
 
     const int wg = static_cast<int>(blockIdx.x);
     int sgi = 0;
@@ -460,8 +467,8 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_matvec_kernel(const Ba
     const MatvecSegment &seg = args.seg[sgi];
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63, wave = tid >> 6;
-    const int split = args.split, slot = wave / split, sub = wave % split;
-    const int rg = (wg - args.first_wg[sgi]) * (4 / split) + slot;
+    const int slot = wave / SPLIT, sub = wave % SPLIT;
+    const int rg = (wg - args.first_wg[sgi]) * (4 / SPLIT) + slot;
     const bool active = rg < seg.w.row_groups;
     const int rgc = active ? rg : seg.w.row_groups - 1;
     const int r = lane >> 3, l = lane & 7;
@@ -470,141 +477,147 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_matvec_kernel(const Ba
     const uint2 *sp = seg.w.scales + static_cast<size_t>(rgc) * chunks * 8 + r;
     const uint4 *qp2 = kPair ? seg.w2.quants + static_cast<size_t>(rgc) * chunks * 64 + lane : nullptr;
     const uint2 *sp2 = kPair ? seg.w2.scales + static_cast<size_t>(rgc) * chunks * 8 + r : nullptr;
-    const int ns = (args.batch - sub + split - 1) / split;  // sequences of this wave
-
-    // first weight batch, then the activations of every sequence
-    uint4 qa[8], qa2[kPair ? 8 : 1];
-    uint2 sa[8], sa2[kPair ? 8 : 1];
-    auto fetch = [&](int c0, uint4 (&q)[8], uint2 (&sc)[8], uint4 (&q2)[kPair ? 8 : 1], uint2 (&sc2)[kPair ? 8 : 1]) {
+    int sq[NS];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = min(c0 + i, chunks - 1);  // clamped: uniform trip count
-            q[i] = load_stream(qp + static_cast<size_t>(c) * 64);
-            sc[i] = load_stream(sp + static_cast<size_t>(c) * 8);
+    for (int k = 0; k < NS; ++k) sq[k] = min(sub + k * SPLIT, args.batch - 1);
+
+    // a ring of three operand groups: two in flight while one is consumed
+    uint4 qa[G], qa2[kPair ? G : 1], qb[G], qb2[kPair ? G : 1], qc[G], qc2[kPair ? G : 1];
+    uint2 sa[G], sa2[kPair ? G : 1], sb[G], sb2[kPair ? G : 1], sc_[G], sc2_[kPair ? G : 1];
+    auto fetch = [&](int c0, uint4 (&q)[G], uint2 (&sc)[G], uint4 (&q2)[kPair ? G : 1], uint2 (&sc2)[kPair ? G : 1]) {
+        c0 = min(c0, chunks - G);  // past the end: the last group again (cached, unused)
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            q[i] = load_stream(qp + static_cast<size_t>(c0 + i) * 64);
+            sc[i] = load_stream(sp + static_cast<size_t>(c0 + i) * 8);
             if constexpr (kPair) {
-                q2[i] = load_stream(qp2 + static_cast<size_t>(c) * 64);
-                sc2[i] = load_stream(sp2 + static_cast<size_t>(c) * 8);
+                q2[i] = load_stream(qp2 + static_cast<size_t>(c0 + i) * 64);
+                sc2[i] = load_stream(sp2 + static_cast<size_t>(c0 + i) * 8);
             }
         }
     };
     fetch(0, qa, sa, qa2, sa2);
+    fetch(G, qb, sb, qb2, sb2);
     {
+        // activations of every sequence: 1 KiB blocks, wave w takes blocks w, w + 4, ...
         const int pieces = args.batch * seq_bytes / 16;
-        const int iters = (pieces + kBatchThreads - 1) / kBatchThreads;
+        const int blocks = act_bytes / 1024;
         const u32x4_t *src = static_cast<const u32x4_t *>(args.act);
-        u32x4_t *dst = reinterpret_cast<u32x4_t *>(lds);
-        u32x4_t v[kPieces];
-#pragma unroll
-        for (int k = 0; k < kPieces; ++k)
-            if (k < iters) v[k] = src[min(tid + k * kBatchThreads, pieces - 1)];
-#pragma unroll
-        for (int k = 0; k < kPieces; ++k) {
-            const int i = tid + k * kBatchThreads;
-            if (k < iters && i < pieces) dst[i] = v[k];
-        }
+        for (int b = wave; b < blocks; b += 4)
+            __builtin_amdgcn_global_load_lds(src + min(b * 64 + lane, pieces - 1),
+                reinterpret_cast<u32x4_t *>(lds) + b * 64, 16, 0, 0);
     }
     const int row = rg * kRowsPerWave + r;
+    const int rowc = min(row, seg.w.rows - 1);
     const bool writer = active && l == 0 && row < seg.w.rows;
-    // per-sequence residuals and conv windows, loaded now
-    float resid[kMaxBatch], win[kMaxBatch][kConvMax - 1], taps[kConvMax];
+    // per-sequence residuals and conv windows, loaded now (clamped, unconditional)
+    float resid[NS], win[NS][kConvMax - 1], taps[kConvMax];
     const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr;
     const int ck = conv ? seg.kernel : 0;
 #pragma unroll
-    for (int k = 0; k < kMaxBatch; ++k) {
-        const int sq = sub + k * split;
+    for (int k = 0; k < NS; ++k) {
         resid[k] = 0.0f;
-        if constexpr (EPI == Epilogue::ADD)
-            if (writer && k < ns) resid[k] = seg.resid[static_cast<size_t>(sq) * seg.w.rows + row];
-        if (conv && writer && k < ns) {
+        if constexpr (EPI == Epilogue::ADD) resid[k] = seg.resid[static_cast<size_t>(sq[k]) * seg.w.rows + rowc];
+    }
+    if (conv) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
 #pragma unroll
             for (int t = 0; t < kConvMax - 1; ++t)
-                if (t < ck - 1)
-                    win[k][t] = seg.conv_state[(static_cast<size_t>(sq) * (ck - 1) + t) * seg.conv_size + row];
-        }
-    }
-    if (conv && writer) {
+                win[k][t] = t < ck - 1
+                    ? seg.conv_state[(static_cast<size_t>(sq[k]) * (ck - 1) + t) * seg.conv_size + rowc] : 0.0f;
 #pragma unroll
-        for (int t = 0; t < kConvMax; ++t)
-            if (t < ck) taps[t] = seg.conv_w[static_cast<size_t>(row) * ck + t];
+        for (int t = 0; t < kConvMax; ++t) taps[t] = t < ck ? seg.conv_w[static_cast<size_t>(rowc) * ck + t] : 0.0f;
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's direct-to-LDS loads have landed
     __syncthreads();
 
-    float acc[kMaxBatch], acc2[kMaxBatch];
+    float acc[NS], acc2[NS];
 #pragma unroll
-    for (int k = 0; k < kMaxBatch; ++k) { acc[k] = 0.0f; acc2[k] = 0.0f; }
-    auto consume = [&](int c0, const uint4 (&q)[8], const uint2 (&sc)[8], const uint4 (&q2)[kPair ? 8 : 1],
-                       const uint2 (&sc2)[kPair ? 8 : 1]) {
+    for (int k = 0; k < NS; ++k) { acc[k] = 0.0f; acc2[k] = 0.0f; }
+    // per group: the weight scales once, then two sequences at a time with all
+    // of their activation reads for the group issued before the dots (each
+    // sequence's chain still runs chunk by chunk in order)
+    auto consume = [&](int c0, const uint4 (&q)[G], const uint2 (&sc)[G], const uint4 (&q2)[kPair ? G : 1],
+                       const uint2 (&sc2)[kPair ? G : 1]) {
+        float ws[G][4], ws2[kPair ? G : 1][4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = c0 + i;
-            if (c < chunks) {
-                float ws[4], ws2[4];
-                scales_f(sc[i], ws);
-                if constexpr (kPair) scales_f(sc2[i], ws2);
+        for (int i = 0; i < G; ++i) {
+            scales_f(sc[i], ws[i]);
+            if constexpr (kPair) scales_f(sc2[i], ws2[i]);
+        }
 #pragma unroll
-                for (int k = 0; k < kMaxBatch; ++k) {
-                    if (k < ns) {
-                        const unsigned char *sb = lds + static_cast<size_t>(sub + k * split) * seq_bytes;
-                        const uint4 a = reinterpret_cast<const uint4 *>(sb)[c * 8 + l];
-                        const float4 as = reinterpret_cast<const float4 *>(sb + static_cast<size_t>(args.chunks) * 128)[c];
-                        acc[k] = dot_chunk_f(q[i], ws, a, as, acc[k]);
-                        if constexpr (kPair) acc2[k] = dot_chunk_f(q2[i], ws2, a, as, acc2[k]);
-                    }
+        for (int k0 = 0; k0 < NS; k0 += 2) {
+            constexpr int kP = NS >= 2 ? 2 : 1;
+            uint4 a[kP][G];
+            float4 as[kP][G];
+#pragma unroll
+            for (int kk = 0; kk < kP; ++kk) {
+                const unsigned char *sbase = lds + static_cast<size_t>(sq[k0 + kk]) * seq_bytes;
+#pragma unroll
+                for (int i = 0; i < G; ++i) {
+                    a[kk][i] = reinterpret_cast<const uint4 *>(sbase)[(c0 + i) * 8 + l];
+                    as[kk][i] = reinterpret_cast<const float4 *>(sbase + static_cast<size_t>(args.chunks) * 128)[c0 + i];
+                }
+            }
+#pragma unroll
+            for (int kk = 0; kk < kP; ++kk) {
+#pragma unroll
+                for (int i = 0; i < G; ++i) {
+                    acc[k0 + kk] = dot_chunk_f(q[i], ws[i], a[kk][i], as[kk][i], acc[k0 + kk]);
+                    if constexpr (kPair) acc2[k0 + kk] = dot_chunk_f(q2[i], ws2[i], a[kk][i], as[kk][i], acc2[k0 + kk]);
                 }
             }
         }
     };
-    uint4 qb[8], qb2[kPair ? 8 : 1];
-    uint2 sb[8], sb2[kPair ? 8 : 1];
-    if (active) {
-        for (int c0 = 0; c0 < chunks; c0 += 16) {
-            if (c0 + 8 < chunks) fetch(c0 + 8, qb, sb, qb2, sb2);
-            consume(c0, qa, sa, qa2, sa2);
-            if (c0 + 8 >= chunks) break;
-            if (c0 + 16 < chunks) fetch(c0 + 16, qa, sa, qa2, sa2);
-            consume(c0 + 8, qb, sb, qb2, sb2);
-        }
+    for (int c0 = 0;; c0 += 3 * G) {
+        fetch(c0 + 2 * G, qc, sc_, qc2, sc2_);
+        consume(c0, qa, sa, qa2, sa2);
+        if (c0 + G >= chunks) break;
+        fetch(c0 + 3 * G, qa, sa, qa2, sa2);
+        consume(c0 + G, qb, sb, qb2, sb2);
+        if (c0 + 2 * G >= chunks) break;
+        fetch(c0 + 4 * G, qb, sb, qb2, sb2);
+        consume(c0 + 2 * G, qc, sc_, qc2, sc2_);
+        if (c0 + 3 * G >= chunks) break;
     }
 #pragma unroll
-    for (int k = 0; k < kMaxBatch; ++k) {
-        if (k < ns) {
-            acc[k] = row_hsum8(acc[k]);
-            if constexpr (kPair) acc2[k] = row_hsum8(acc2[k]);
-        }
+    for (int k = 0; k < NS; ++k) {
+        acc[k] = row_hsum8(acc[k]);
+        if constexpr (kPair) acc2[k] = row_hsum8(acc2[k]);
     }
 #pragma unroll
-    for (int k = 0; k < kMaxBatch; ++k) {
-        if (k >= ns) continue;
-        const int sq = sub + k * split;
-        float *out = seg.out ? seg.out + static_cast<size_t>(sq) * seg.w.rows : nullptr;
+    for (int k = 0; k < NS; ++k) {
+        const bool mine = sub + k * SPLIT < args.batch;
+        float *out = seg.out ? seg.out + static_cast<size_t>(sq[k]) * seg.w.rows : nullptr;
         if constexpr (EPI == Epilogue::STORE) {
-            if (conv && writer) {
-                float *cs = seg.conv_state + static_cast<size_t>(sq) * (ck - 1) * seg.conv_size;
+            if (conv && writer && mine) {
+                float *cs = seg.conv_state + static_cast<size_t>(sq[k]) * (ck - 1) * seg.conv_size;
                 out[row] = conv_silu(win[k], taps, ck, acc[k]);
 #pragma unroll
                 for (int t = 0; t + 1 < kConvMax - 1; ++t)
                     if (t + 1 < ck - 1) cs[static_cast<size_t>(t) * seg.conv_size + row] = win[k][t + 1];
                 cs[static_cast<size_t>(ck - 2) * seg.conv_size + row] = acc[k];
-            } else if (writer) {
+            } else if (writer && mine) {
                 out[row] = seg.silu ? silu_poly(acc[k]) : acc[k];
             }
         } else if constexpr (EPI == Epilogue::ADD) {
-            if (writer) out[row] = acc[k] + resid[k];
+            if (writer && mine) out[row] = acc[k] + resid[k];
         } else {
             const float h = row < args.pair_vector_rows ? silu_poly(acc[k]) * acc2[k]
                                                         : acc[k] / (1.0f + exp_rounded(-acc[k])) * acc2[k];
-            if (writer && out) out[row] = h;
-            if (seg.out_q8l && l == 0) epi[sq * 32 + wave * 8 + r] = h;
+            if (writer && mine && out) out[row] = h;
+            if (seg.out_q8l && l == 0 && mine) epi[sq[k] * 32 + wave * 8 + r] = h;
         }
     }
     if constexpr (kPair) {
         if (seg.out_q8l) {
-            // split == 1: the workgroup's 32 rows form one quantization block of
+            // SPLIT == 1: the workgroup's 32 rows form one quantization block of
             // every sequence's h
             __syncthreads();
-            const int t = tid & 7, sq = tid >> 3;
-            if (sq < args.batch) {
-                const float *e = epi + sq * 32;
+            const int t = tid & 7, q = tid >> 3;
+            if (q < args.batch) {
+                const float *e = epi + q * 32;
                 const float4 y = make_float4(e[4 * t], e[4 * t + 1], e[4 * t + 2], e[4 * t + 3]);
                 float scale;
                 uint16_t bits;
@@ -612,12 +625,162 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_matvec_kernel(const Ba
                 const int b = wg - args.first_wg[sgi];
                 const int hchunks = (seg.w.rows / kQ8Block + 3) / 4;
                 uint32_t *dq = reinterpret_cast<uint32_t *>(static_cast<unsigned char *>(seg.out_q8l) +
-                    static_cast<size_t>(sq) * q8l_bytes(seg.w.rows));
+                    static_cast<size_t>(q) * q8l_bytes(seg.w.rows));
                 dq[((b >> 2) * 8 + t) * 4 + (b & 3)] = packed;
                 if (t == 0) reinterpret_cast<float *>(dq + hchunks * 32)[b] = scale;
             }
         }
     }
+}
+
+// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
+
+constexpr int kRingG = 4;  // chunks per ring group
+
+// Store/add matvec of a batch with the weights fetched once per workgroup.
+// One workgroup per 8-row group; its four waves take two sequences each
+// (w and w + 4).  Every wave loads one chunk of each group of four (1 KiB) and
+// the group's row scales into a register ring R groups deep, so R groups are
+// in flight per wave; just before a group is consumed the four waves put it
+// into one of two LDS slots and, after one barrier, all read it from there.
+// Per (row, sequence) the chain is the single-sequence kernel's.
+template <Epilogue EPI, int GROUPS>
+__global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const BatchMatvecArgs args) {
+    constexpr int NS = 2;
+    constexpr int R = GROUPS < 8 ? GROUPS : 8;  // groups in flight per wave
+    constexpr int kSlot = kRingG * 1024 + kRingG * 64;  // quants then scales of one group
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int seq_bytes = args.chunks * 144;
+    const int act_bytes = (args.batch * seq_bytes + 1023) / 1024 * 1024;
+    unsigned char *slots = lds + act_bytes;  // [2][kSlot]
+
+    const int wg = static_cast<int>(blockIdx.x);
+    int sgi = 0;
+    while (sgi + 1 < args.count && wg >= args.first_wg[sgi + 1]) ++sgi;
+    const MatvecSegment &seg = args.seg[sgi];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int rg = wg - args.first_wg[sgi];
+    const int r = lane >> 3, l = lane & 7;
+    constexpr int chunks = GROUPS * kRingG, groups = GROUPS;
+    const u32x4_t *qsrc = reinterpret_cast<const u32x4_t *>(seg.w.quants) + static_cast<size_t>(rg) * chunks * 64;
+    const uint32_t *ssrc = reinterpret_cast<const uint32_t *>(seg.w.scales) + static_cast<size_t>(rg) * chunks * 16;
+    int sq[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) sq[k] = min(wave + 4 * k, args.batch - 1);
+
+    u32x4_t rq[R];
+    uint32_t rs[R];
+    // group g -> register slot g % R: this wave's chunk and one scale word
+    auto fetch = [&](int g, u32x4_t &q, uint32_t &sw) {
+        const int gc = min(g, groups - 1);  // past the end: the last group again (never consumed)
+        q = __builtin_nontemporal_load(qsrc + (static_cast<size_t>(gc) * kRingG + wave) * 64 + lane);
+        sw = __builtin_nontemporal_load(ssrc + static_cast<size_t>(gc) * kRingG * 16 + lane);
+    };
+#pragma unroll
+    for (int g = 0; g < R; ++g) fetch(g, rq[g], rs[g]);
+    {
+        const int pieces = args.batch * seq_bytes / 16;
+        const int blocks = act_bytes / 1024;
+        const u32x4_t *src = static_cast<const u32x4_t *>(args.act);
+        for (int b = wave; b < blocks; b += 4)
+            __builtin_amdgcn_global_load_lds(src + min(b * 64 + lane, pieces - 1),
+                reinterpret_cast<u32x4_t *>(lds) + b * 64, 16, 0, 0);
+    }
+    const int row = rg * kRowsPerWave + r;
+    const int rowc = min(row, seg.w.rows - 1);
+    const bool writer = l == 0 && row < seg.w.rows;
+    float resid[NS], win[NS][kConvMax - 1], taps[kConvMax];
+    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr;
+    const int ck = conv ? seg.kernel : 0;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        resid[k] = 0.0f;
+        if constexpr (EPI == Epilogue::ADD) resid[k] = seg.resid[static_cast<size_t>(sq[k]) * seg.w.rows + rowc];
+    }
+    if (conv) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+#pragma unroll
+            for (int t = 0; t < kConvMax - 1; ++t)
+                win[k][t] = t < ck - 1
+                    ? seg.conv_state[(static_cast<size_t>(sq[k]) * (ck - 1) + t) * seg.conv_size + rowc] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < kConvMax; ++t) taps[t] = t < ck ? seg.conv_w[static_cast<size_t>(rowc) * ck + t] : 0.0f;
+    }
+
+    float acc[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) acc[k] = 0.0f;
+    // one group: into LDS slot g & 1, barrier, refill the register slot with
+    // group g + R, then the dots from LDS
+    auto step = [&](int g, u32x4_t &q, uint32_t &sw) {
+        unsigned char *slot = slots + (g & 1) * kSlot;
+        reinterpret_cast<u32x4_t *>(slot + wave * 1024)[lane] = q;
+        if (wave == 0) reinterpret_cast<uint32_t *>(slot + kRingG * 1024)[lane] = sw;
+        __syncthreads();  // the group is in LDS (and, the first time, the activations: see below)
+        if (g + R < GROUPS) fetch(g + R, q, sw);
+#pragma unroll
+        for (int i = 0; i < kRingG; ++i) {
+            const int c = g * kRingG + i;
+            const uint4 qq = reinterpret_cast<const uint4 *>(slot + i * 1024)[lane];
+            const uint2 sc = reinterpret_cast<const uint2 *>(slot + kRingG * 1024 + i * 64)[r];
+            float ws[4];
+            scales_f(sc, ws);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                const unsigned char *sbase = lds + static_cast<size_t>(sq[k]) * seq_bytes;
+                const uint4 a = reinterpret_cast<const uint4 *>(sbase)[c * 8 + l];
+                const float4 as = reinterpret_cast<const float4 *>(sbase + static_cast<size_t>(args.chunks) * 128)[c];
+                acc[k] = dot_chunk_f(qq, ws, a, as, acc[k]);
+            }
+        }
+    };
+    // the activations' direct-to-LDS copies were issued after the first R
+    // groups: waiting for all of this wave's loads once covers both
+    __builtin_amdgcn_s_waitcnt(0);
+    // fully unrolled (the group count is a template parameter): the compiler's
+    // load counters then know that group g is the oldest load in flight
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g) step(g, rq[g % R], rs[g % R]);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) acc[k] = row_hsum8(acc[k]);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const bool mine = wave + 4 * k < args.batch;
+        if (!(writer && mine)) continue;
+        float *out = seg.out + static_cast<size_t>(sq[k]) * seg.w.rows;
+        if constexpr (EPI == Epilogue::STORE) {
+            if (conv) {
+                float *cs = seg.conv_state + static_cast<size_t>(sq[k]) * (ck - 1) * seg.conv_size;
+                out[row] = conv_silu(win[k], taps, ck, acc[k]);
+#pragma unroll
+                for (int t = 0; t + 1 < kConvMax - 1; ++t)
+                    if (t + 1 < ck - 1) cs[static_cast<size_t>(t) * seg.conv_size + row] = win[k][t + 1];
+                cs[static_cast<size_t>(ck - 2) * seg.conv_size + row] = acc[k];
+            } else {
+                out[row] = seg.silu ? silu_poly(acc[k]) : acc[k];
+            }
+        } else {
+            out[row] = acc[k] + resid[k];
+        }
+    }
+}
+
+template <Epilogue EPI, int SPLIT>
+hipError_t launch_batch_g(const BatchMatvecArgs &args, int grid, size_t lds, hipStream_t stream) {
+    // groups of at most 4 chunks (with three groups in registers, larger
+    // groups exceed the register budget of two workgroups per CU)
+    const int c = args.chunks;
+    const int g = c % 4 == 0 ? 4 : (c % 2 == 0 ? 2 : 1);
+    switch (g) {
+    case 4: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 4>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
+    case 2: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 2>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
+    default: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 1>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
+    }
+    return hipGetLastError();
 }
 
 __global__ void q8_repack_kernel(const uint8_t *gguf, int rows, int blocks, int chunks,
@@ -809,21 +972,22 @@ hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const Matv
 }
 
 hipError_t launch_q8l_prep(const MatvecInput &in, Prologue prologue, void *q8l, int batch, hipStream_t stream) {
-    constexpr int kPre = ActShape<kBatchThreads, Prologue::F32>::kPre;
-    if (batch < 1 || batch > kMaxBatch || in.width <= 0 || in.width % kQ8Block || in.width / 4 > kPre * kBatchThreads)
+    constexpr int kPre = ActShape<kPrepThreads, Prologue::F32>::kPre;
+    if (batch < 1 || batch > kMaxBatch || in.width <= 0 || in.width % kQ8Block || in.width / 4 > kPre * kPrepThreads ||
+        (in.width / kQ8Block + 3) / 4 > kMaxChunks)
         return hipErrorInvalidValue;
     switch (prologue) {
     case Prologue::F32:
-        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::F32>, dim3(batch), dim3(kBatchThreads), 0, stream, in, q8l);
+        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::F32>, dim3(batch), dim3(kPrepThreads), 0, stream, in, q8l);
         break;
     case Prologue::RMSNORM:
-        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::RMSNORM>, dim3(batch), dim3(kBatchThreads), 0, stream, in, q8l);
+        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::RMSNORM>, dim3(batch), dim3(kPrepThreads), 0, stream, in, q8l);
         break;
     case Prologue::GATED: {
         const int hl = in.head / 4;
         if (in.head <= 0 || in.head % 4 || hl > 64 || (hl & (hl - 1)) || in.width % in.head || !in.z || !in.norm)
             return hipErrorInvalidValue;
-        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::GATED>, dim3(batch), dim3(kBatchThreads), 0, stream, in, q8l);
+        hipLaunchKernelGGL(q8l_prep_kernel<Prologue::GATED>, dim3(batch), dim3(kPrepThreads), 0, stream, in, q8l);
         break;
     }
     default: return hipErrorInvalidValue;
@@ -835,7 +999,7 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
     Epilogue epilogue, hipStream_t stream) {
     const int chunks = (width / kQ8Block + 3) / 4;
     if (count < 1 || count > 4 || width <= 0 || width % kQ8Block || batch < 1 || batch > kMaxBatch ||
-        batch * chunks * 9 > 28 * kBatchThreads)
+        static_cast<size_t>(batch) * chunks * 144 > 120 * 1024)
         return hipErrorInvalidValue;
     int total_groups = 0;
     for (int s = 0; s < count; ++s) {
@@ -851,7 +1015,7 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
     int split = total_groups >= 1024 ? 1 : (total_groups >= 512 ? 2 : 4);
     if (epilogue == Epilogue::SILU_PAIR) {
         if (count != 1 || (segments[0].out_q8l && segments[0].w.rows % kQ8Block)) return hipErrorInvalidValue;
-        if (segments[0].out_q8l) split = 1;
+        split = 1;  // one workgroup = 32 rows of every sequence (one quantization block of h)
     }
     BatchMatvecArgs args{};
     args.count = count;
@@ -870,20 +1034,53 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
     const int rows = segments[0].w.rows;
     args.pair_vector_rows = rows >= 8 ? (rows / 8) * 8 : 0;
     if (grid == 0) return hipSuccess;
-    const size_t lds = static_cast<size_t>(batch) * chunks * 144 + kMaxBatch * 32 * 4;
-    switch (epilogue) {
-    case Epilogue::STORE:
-        hipLaunchKernelGGL(q8_batch_matvec_kernel<Epilogue::STORE>, dim3(grid), dim3(kBatchThreads), lds, stream, args);
-        break;
-    case Epilogue::ADD:
-        hipLaunchKernelGGL(q8_batch_matvec_kernel<Epilogue::ADD>, dim3(grid), dim3(kBatchThreads), lds, stream, args);
-        break;
-    case Epilogue::SILU_PAIR:
-        hipLaunchKernelGGL(q8_batch_matvec_kernel<Epilogue::SILU_PAIR>, dim3(grid), dim3(kBatchThreads), lds, stream,
-            args);
-        break;
+    const size_t act = (static_cast<size_t>(batch) * chunks * 144 + 1023) / 1024 * 1024;
+    const size_t lds = act + kMaxBatch * 32 * 4;
+    const int ring_groups = chunks % kRingG == 0 ? chunks / kRingG : 0;
+    const bool ring = epilogue != Epilogue::SILU_PAIR && (ring_groups == 2 || ring_groups == 4 || ring_groups == 5 ||
+        ring_groups == 7 || ring_groups == 8 || ring_groups == 16 || ring_groups == 18);
+    if (ring) {
+        // weights fetched once per workgroup (a register ring of up to 8
+        // groups per wave, shared through LDS): one workgroup per row group
+        int ring_grid = 0;
+        for (int s = 0; s < count; ++s) {
+            args.first_wg[s] = ring_grid;
+            ring_grid += segments[s].w.row_groups;
+        }
+        args.first_wg[count] = ring_grid;
+        constexpr size_t kSlot = kRingG * 1024 + kRingG * 64;
+        const size_t ring_lds = act + 2 * kSlot;
+        if (ring_lds > 160 * 1024) return hipErrorInvalidValue;
+#define FORTAI_RING(E, G) hipLaunchKernelGGL((q8_batch_ring_kernel<E, G>), dim3(ring_grid), dim3(kBatchThreads), \
+        ring_lds, stream, args)
+#define FORTAI_RING_E(E)                                 \
+        switch (ring_groups) {                           \
+        case 2: FORTAI_RING(E, 2); break;                \
+        case 4: FORTAI_RING(E, 4); break;                \
+        case 5: FORTAI_RING(E, 5); break;                \
+        case 7: FORTAI_RING(E, 7); break;                \
+        case 8: FORTAI_RING(E, 8); break;                \
+        case 16: FORTAI_RING(E, 16); break;              \
+        default: FORTAI_RING(E, 18); break;              \
+        }
+        if (epilogue == Epilogue::STORE) { FORTAI_RING_E(Epilogue::STORE) }
+        else { FORTAI_RING_E(Epilogue::ADD) }
+#undef FORTAI_RING_E
+#undef FORTAI_RING
+        return hipGetLastError();
     }
-    return hipGetLastError();
+    if (epilogue == Epilogue::SILU_PAIR) return launch_batch_g<Epilogue::SILU_PAIR, 1>(args, grid, lds, stream);
+    if (epilogue == Epilogue::STORE) {
+        if (split == 1) return launch_batch_g<Epilogue::STORE, 1>(args, grid, lds, stream);
+        if (split == 2) return launch_batch_g<Epilogue::STORE, 2>(args, grid, lds, stream);
+        return launch_batch_g<Epilogue::STORE, 4>(args, grid, lds, stream);
+    }
+    if (epilogue == Epilogue::ADD) {
+        if (split == 1) return launch_batch_g<Epilogue::ADD, 1>(args, grid, lds, stream);
+        if (split == 2) return launch_batch_g<Epilogue::ADD, 2>(args, grid, lds, stream);
+        return launch_batch_g<Epilogue::ADD, 4>(args, grid, lds, stream);
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_q8_repack(const uint8_t *gguf, int rows, int blocks, uint4 *quants, uint2 *scales,

@@ -210,6 +210,14 @@ int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *context,
     const fortai_hip_q8_weights *weights, const void *device_activation,
     void *device_dots);
 
+/* Batched matvec: device fp32 x [batch][width] (batch 1..8) -> out
+ * [batch][rows], every weight read once for all rows of x; each output row
+ * is bit-identical to fortai_hip_q8_matvec_device_f32 of that x.  kernel_ms
+ * (may be NULL): event-timed duration, synchronising. */
+int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_x, int batch,
+    void *device_output, float *kernel_ms);
+
 /* Token blocks (prefill, batches) on the i8 matrix cores.  The reference runs
  * every token through the matvec of fortai_gguf_runtime.f90:424-465; these
  * compute the same product for `tokens` activations at once.
