@@ -103,6 +103,7 @@ _SIGNATURES = {
     "fortai_hip_qwen35_batch_generate": [_vp, _vp, _vp, _i, _vp],
     "fortai_hip_qwen35_batch_replay": [_vp, _i],
     "fortai_hip_qwen35_batch_logits": [_vp, _vpp],
+    "fortai_hip_qwen35_batch_prefill": [_vp, _vp, _i, _vp, _vp, _fp],
 }
 _RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p, "fortai_hip_q8_tokens_bytes": C.c_size_t}
 
@@ -454,6 +455,18 @@ class BatchDecoder:
 
     def replay(self, steps: int) -> None:
         self.ctx.call("fortai_hip_qwen35_batch_replay", self.h, steps)
+
+    def prefill(self, tokens, want_logits: bool = True):
+        """Prompt tokens [batch][T] from position 0; returns (next tokens,
+        prefill milliseconds); logits of the last prompt token in .logits."""
+        t = np.ascontiguousarray(tokens, dtype=np.int64)
+        if t.ndim != 2 or t.shape[0] != self.batch:
+            raise ValueError(f"need tokens [{self.batch}][T]")
+        nxt = np.zeros(self.batch, dtype=np.int64)
+        ms = C.c_float()
+        self.ctx.call("fortai_hip_qwen35_batch_prefill", self.h, _ptr(t), t.shape[1], _ptr(nxt),
+                      _ptr(self.logits) if want_logits else None, C.byref(ms))
+        return nxt, ms.value
 
     def free(self) -> None:
         if self.h:

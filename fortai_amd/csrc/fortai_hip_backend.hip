@@ -152,6 +152,14 @@ struct fortai_hip_qwen35_batch {
     int64_t *tokens = nullptr, *trace = nullptr;  // trace [batch][max_context]
     int *positions = nullptr;
     std::vector<int> next_positions;  // host mirror after the queued steps
+    // prompt prefill buffers, rows = batch * T (grown on demand)
+    int prefill_rows = 0;
+    float *px = nullptr;                                   // residual stream [rows][hidden]
+    void *px8 = nullptr;                                   // quantized tokens of the widest input
+    float *pa = nullptr, *pb = nullptr, *pc = nullptr, *pd = nullptr;  // projections / stage outputs
+    float *palpha = nullptr, *pbeta = nullptr, *pqinv = nullptr, *pkinv = nullptr, *pbt = nullptr, *pdt = nullptr;
+    int64_t *ptokens = nullptr;
+    void *pq8l = nullptr;                                  // exact mode: 8 tokens in the matvec layout
     bool use_graph = true;            // FORTAI_HIP_DECODER_GRAPH=0: enqueue the kernels every step
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -1907,6 +1915,11 @@ int fortai_hip_qwen35_batch_destroy(fortai_hip_qwen35_batch *b) {
     auto *c = b->context;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    release(b->px); release(b->pa); release(b->pb); release(b->pc); release(b->pd); release(b->palpha);
+    release(b->pbeta); release(b->pqinv); release(b->pkinv); release(b->pbt); release(b->pdt); release(b->ptokens);
+    if (b->px8) (void)hipFree(b->px8);
+    if (b->pq8l) (void)hipFree(b->pq8l);
+    b->pq8l = nullptr;
     if (b->exec) (void)hipGraphExecDestroy(b->exec);
     if (b->graph) (void)hipGraphDestroy(b->graph);
     for (auto &L : b->layers) {
@@ -1981,6 +1994,193 @@ int fortai_hip_qwen35_batch_replay(fortai_hip_qwen35_batch *b, int steps) {
     for (int s = 0; s < steps && e == hipSuccess; ++s) e = batch_step(b);
     for (auto &p : b->next_positions) p += steps;
     return done(c, e, "batch replay");
+}
+
+namespace {
+// widths of the prefill buffers
+struct prefill_widths {
+    int x8 = 0, a = 0, b = 0, c = 0, d = 0, vh = 0, kh = 0;
+};
+prefill_widths batch_prefill_widths(const fortai_hip_qwen35_batch *b) {
+    prefill_widths w;
+    w.x8 = std::max(b->hidden, b->ffn);
+    w.a = w.b = b->ffn;
+    for (const auto &L : b->layers) {
+        if (L.rec) {
+            const auto *R = L.rec;
+            w.x8 = std::max(w.x8, R->inner);
+            w.a = std::max(w.a, R->conv_size);
+            w.b = std::max(w.b, R->inner);
+            w.c = std::max(w.c, R->conv_size);
+            w.d = std::max(w.d, R->inner);
+            w.vh = std::max(w.vh, R->value_heads);
+            w.kh = std::max(w.kh, R->key_heads);
+        } else {
+            const auto *A = L.att;
+            w.x8 = std::max(w.x8, A->heads * A->value);
+            w.a = std::max(w.a, A->heads * 2 * A->head);
+            w.b = std::max(w.b, A->kv_heads * A->head);
+            w.c = std::max(w.c, A->kv_heads * A->value);
+            w.d = std::max(w.d, A->heads * A->value);
+        }
+    }
+    return w;
+}
+
+hipError_t batch_prefill_buffers(fortai_hip_qwen35_batch *b, int rows) {
+    if (rows <= b->prefill_rows) return hipSuccess;
+    release(b->px); release(b->pa); release(b->pb); release(b->pc); release(b->pd); release(b->palpha);
+    release(b->pbeta); release(b->pqinv); release(b->pkinv); release(b->pbt); release(b->pdt); release(b->ptokens);
+    if (b->px8) (void)hipFree(b->px8);
+    if (b->pq8l) (void)hipFree(b->pq8l);
+    b->pq8l = nullptr;
+    b->px8 = nullptr;
+    b->prefill_rows = 0;
+    const prefill_widths w = batch_prefill_widths(b);
+    const size_t n = static_cast<size_t>(rows);
+    hipError_t e = alloc(&b->px, n * b->hidden);
+    if (e == hipSuccess) e = hipMalloc(&b->px8, q8_tokens_bytes(rows, w.x8));
+    if (e == hipSuccess) e = alloc(&b->pa, n * w.a);
+    if (e == hipSuccess) e = alloc(&b->pb, n * w.b);
+    if (e == hipSuccess) e = alloc(&b->pc, n * std::max(w.c, 1));
+    if (e == hipSuccess) e = alloc(&b->pd, n * w.d);
+    if (e == hipSuccess) e = alloc(&b->palpha, n * std::max(w.vh, 1));
+    if (e == hipSuccess) e = alloc(&b->pbeta, n * std::max(w.vh, 1));
+    if (e == hipSuccess) e = alloc(&b->pbt, n * std::max(w.vh, 1));
+    if (e == hipSuccess) e = alloc(&b->pdt, n * std::max(w.vh, 1));
+    if (e == hipSuccess) e = alloc(&b->pqinv, n * std::max(w.kh, 1));
+    if (e == hipSuccess) e = alloc(&b->pkinv, n * std::max(w.kh, 1));
+    if (e == hipSuccess) e = alloc(&b->ptokens, n);
+    if (e == hipSuccess) e = hipMalloc(&b->pq8l, 8 * q8l_bytes(w.x8));
+    if (e == hipSuccess) b->prefill_rows = rows;
+    return e;
+}
+
+// Every layer over batch * T prompt tokens (positions 0..T-1), then the LM
+// head on each sequence's last token, which leaves tokens / positions / trace
+// as after T decode steps.
+// exact: every projection through the bit-exact batched matvec, 8 tokens at a
+// time (the reference's lane order; for validating the prefill kernels)
+hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, hipStream_t stream) {
+    const int B = b->batch, H = b->hidden, N = B * T;
+    hipError_t e = b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->ptokens, 0, b->px, stream, N)
+                            : launch_q8_embedding(b->emb8->m, b->ptokens, 0, b->px, stream, N);
+    auto mmq = [&](const fortai_hip_q8_weights *w, float *out, const float *resid) {
+        if (!exact) return launch_q8_mmq(w->m, b->px8, N, out, w->m.rows, resid, nullptr, stream);
+        hipError_t r = hipSuccess;
+        for (int r0 = 0; r0 < N && r == hipSuccess; r0 += 8) {
+            const int cnt = std::min(8, N - r0);
+            r = launch_x8_to_q8l(b->px8, N, w->width, r0, cnt, b->pq8l, stream);
+            MatvecSegment sg = segment(w, out + static_cast<size_t>(r0) * w->m.rows,
+                resid ? resid + static_cast<size_t>(r0) * w->m.rows : nullptr);
+            if (r == hipSuccess)
+                r = launch_q8_batch_matvec(&sg, 1, b->pq8l, w->width, cnt, resid ? Epilogue::ADD : Epilogue::STORE,
+                    stream);
+        }
+        return r;
+    };
+    for (size_t i = 0; i < b->layers.size() && e == hipSuccess; ++i) {
+        batch_layer &L = b->layers[i];
+        e = launch_rms_quantize_tokens(b->px, N, H, L.attn_norm, b->eps, b->px8, stream);
+        if (L.rec) {
+            const auto *R = L.rec;
+            if (e == hipSuccess) e = mmq(R->qkv, b->pa, nullptr);
+            if (e == hipSuccess) e = mmq(R->gate, b->pb, nullptr);
+            if (e == hipSuccess) e = mmq(R->alpha, b->palpha, nullptr);
+            if (e == hipSuccess) e = mmq(R->beta, b->pbeta, nullptr);
+            if (e == hipSuccess)
+                e = launch_conv_silu_tokens(b->pa, R->conv_w, L.conv_state, b->pc, B, T, R->conv_size, R->kernel, stream);
+            GdnParams gp = gdn_params(const_cast<fortai_hip_qwen35_recurrent *>(R), b->pc, b->palpha, b->pbeta, b->pd);
+            gp.state = L.state;
+            if (e == hipSuccess) e = launch_gdn_prefill(gp, B, T, b->pqinv, b->pkinv, b->pbt, b->pdt, stream);
+            if (e == hipSuccess)
+                e = launch_gated_quantize_tokens(b->pd, b->pb, R->ssm_norm, R->eps, N, R->inner, R->head, b->px8, stream);
+            if (e == hipSuccess) e = mmq(R->out, b->px, b->px);
+        } else {
+            const auto *A = L.att;
+            if (e == hipSuccess) e = mmq(A->q, b->pa, nullptr);
+            if (e == hipSuccess) e = mmq(A->k, b->pb, nullptr);
+            if (e == hipSuccess) e = mmq(A->v, b->pc, nullptr);
+            AttentionParams ap = attention_params(const_cast<fortai_hip_qwen35_attention *>(A), b->pa, b->pb, b->pc, b->pd);
+            ap.kcache = L.kcache; ap.vcache = L.vcache; ap.cache_flags = L.flags; ap.max_context = b->max_context;
+            if (e == hipSuccess) e = launch_attention_prefill(ap, B, T, b->pd, stream);
+            if (e == hipSuccess) e = launch_rms_quantize_tokens(b->pd, N, A->heads * A->value, nullptr, 0.0f, b->px8, stream);
+            if (e == hipSuccess) e = mmq(A->o, b->px, b->px);
+        }
+        if (e == hipSuccess) e = launch_rms_quantize_tokens(b->px, N, H, L.post_norm, b->eps, b->px8, stream);
+        if (e == hipSuccess) e = mmq(L.gate, b->pa, nullptr);
+        if (e == hipSuccess) e = mmq(L.up, b->pb, nullptr);
+        if (e == hipSuccess) e = launch_silu_product_quantize(b->pa, b->pb, N, L.gate->m.rows, b->px8, stream);
+        if (e == hipSuccess) e = mmq(L.down, b->px, b->px);
+    }
+    if (e != hipSuccess) return e;
+    // each sequence's last token -> x [batch][hidden]; the LM head then
+    // writes trace[T - 1] and advances the positions to T
+    e = hipMemcpy2DAsync(b->x, H * sizeof(float), b->px + static_cast<size_t>(T - 1) * H, static_cast<size_t>(T) * H * sizeof(float),
+        H * sizeof(float), B, hipMemcpyDeviceToDevice, stream);
+    if (e != hipSuccess) return e;
+    ArgmaxState st;
+    st.partial_value = b->argmax_value;
+    st.partial_index = b->argmax_index;
+    st.token = b->tokens;
+    st.trace = b->trace;
+    st.trace_capacity = b->max_context;
+    st.position = b->positions;
+    if (b->out16)
+        return launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm, b->eps,
+            b->logits, st, stream);
+    MatvecInput in;
+    in.x = b->x;
+    in.norm = b->output_norm;
+    in.eps = b->eps;
+    in.width = H;
+    e = launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream);
+    const MatvecSegment s8 = segment(b->out8, b->logits);
+    if (e == hipSuccess) e = launch_q8_batch_matvec(&s8, 1, b->act, H, B, Epilogue::STORE, stream);
+    for (int q = 0; q < B && e == hipSuccess; ++q) {
+        ArgmaxState sq = st;
+        sq.partial_value += static_cast<size_t>(q) * b->parts;
+        sq.partial_index += static_cast<size_t>(q) * b->parts;
+        sq.token += q;
+        sq.trace += static_cast<size_t>(q) * b->max_context;
+        sq.position += q;
+        e = launch_argmax(b->logits + static_cast<size_t>(q) * b->vocab, b->vocab, sq, stream);
+    }
+    return e;
+}
+}  // namespace
+
+int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *b, const int64_t *tokens, int T, int64_t *next_tokens,
+    float *logits, float *kernel_ms) {
+    if (!b || !tokens || T < 1 || T > b->max_context) return FORTAI_HIP_INVALID;
+    const int rows = b->emb16 ? b->emb16->rows : b->emb8->m.rows;
+    const size_t N = static_cast<size_t>(b->batch) * T;
+    for (size_t i = 0; i < N; ++i)
+        if (tokens[i] < 0 || tokens[i] >= rows) return FORTAI_HIP_INVALID;
+    auto *c = b->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = batch_prefill_buffers(b, static_cast<int>(N));
+    if (e == hipSuccess) e = hipMemcpyAsync(b->ptokens, tokens, N * sizeof(int64_t), hipMemcpyHostToDevice, c->stream);
+    // the LM head of the last prompt token writes trace[T - 1] and moves to T
+    std::vector<int> last(b->batch, T - 1);
+    if (e == hipSuccess) e = hipMemcpyAsync(b->positions, last.data(), b->batch * sizeof(int), hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);  // the host arrays are borrowed for the call
+    if (e == hipSuccess && kernel_ms) e = hipEventRecord(c->start, c->stream);
+    // FORTAI_HIP_PREFILL_EXACT=1: the projections in the reference's lane
+    // order (slow; validates the rest of the prefill against decoding)
+    const char *exact_env = std::getenv("FORTAI_HIP_PREFILL_EXACT");
+    const bool exact = exact_env && std::strcmp(exact_env, "1") == 0;
+    if (e == hipSuccess) e = enqueue_batch_prefill(b, T, exact, c->stream);
+    if (e == hipSuccess && kernel_ms) e = hipEventRecord(c->stop, c->stream);
+    if (e == hipSuccess && logits)
+        e = hipMemcpyAsync(logits, b->logits, static_cast<size_t>(b->batch) * b->vocab * sizeof(float),
+            hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess && next_tokens)
+        e = hipMemcpyAsync(next_tokens, b->tokens, b->batch * sizeof(int64_t), hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess && kernel_ms) e = hipEventElapsedTime(kernel_ms, c->start, c->stop);
+    b->next_positions.assign(b->batch, T);
+    return done(c, e, "batch prefill");
 }
 
 int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *b, void **logits) {

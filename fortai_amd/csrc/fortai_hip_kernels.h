@@ -202,6 +202,32 @@ int attention_split_chunks(int max_context);
 hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int batch = 1);
 size_t attention_scores_floats(int heads, int max_context);
 
+// ---- prompt prefill (prefill.hip): rows are tokens, row s * T + t ---------------
+// rows [r0, r0 + count) of an X8 buffer -> Q8L [count][q8l_bytes(width)]
+hipError_t launch_x8_to_q8l(const void *x8, int tokens, int width, int r0, int count, void *q8l, hipStream_t stream);
+// x [rows][width] -> optional RMSNorm -> X8 (q8_tokens_bytes(rows, width))
+hipError_t launch_rms_quantize_tokens(const float *x, int rows, int width, const float *norm, float eps, void *x8,
+    hipStream_t stream);
+// GDN o and raw gate z [rows][width] -> per-head gated RMSNorm -> X8
+hipError_t launch_gated_quantize_tokens(const float *o, const float *z, const float *norm, float eps, int rows,
+    int width, int head, void *x8, hipStream_t stream);
+// silu(gate) * up [rows][width] -> X8
+hipError_t launch_silu_product_quantize(const float *gate, const float *up, int rows, int width, void *x8,
+    hipStream_t stream);
+// causal conv1d + SiLU over T tokens of every sequence, continuing conv_state
+hipError_t launch_conv_silu_tokens(const float *x, const float *conv_w, float *conv_state, float *out, int batch, int T,
+    int C, int K, hipStream_t stream);
+// the delta rule over T tokens (p.qkv: conv outputs [rows][C], p.alpha/beta
+// raw projections [rows][value_heads], p.out [rows][inner], p.state
+// [batch][...] as the decode kernel keeps it); scratch [rows][key_heads] x 2
+// and [rows][value_heads] x 2
+hipError_t launch_gdn_prefill(const GdnParams &p, int batch, int T, float *qinv, float *kinv, float *beta_t,
+    float *decay_t, hipStream_t stream);
+// q/k norm + RoPE, fp16 K/V append at positions 0..T-1 and causal attention:
+// p.q [rows][heads][2 head] (normalized in place), p.k/p.v [rows][kv_heads][head],
+// caches and flags [batch][...]; out [rows][heads][head]
+hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream);
+
 // ---- persistent decoder ------------------------------------------------------
 // One launch per token (decode_persistent.hip).  Activations cross
 // workgroups as 64-bit tagged words (tag << 32 | payload) in per-phase buffers;

@@ -1,0 +1,511 @@
+// Prompt prefill of a batch of sequences: T tokens per sequence in one pass.
+//
+// The reference has no prefill: it runs every prompt token through the decode
+// step (fortai_qwen35_cpu.f90:591-711).  Here the projections of all
+// batch x T tokens are token-block products on the i8 matrix cores
+// (mmq.hip), and the parts that are sequential in time run as one kernel per
+// layer that loops over the tokens: the causal conv1d (per channel,
+// :856-879), the delta rule (per value head and 16 state rows, :880-906) and
+// causal attention (per query block, online softmax).  Results agree with the
+// per-token decode within fp32 rounding (the block dots are exact; the fp32
+// accumulation orders differ), not bit for bit.  Rows are token-major: row
+// n = s * T + t is token t of sequence s, at position t.
+#include "attention_exact.h"
+#include "fortai_hip_internal.h"
+#include "fortai_hip_kernels.h"
+
+namespace fortai_hip {
+
+namespace {
+
+namespace ea = exact_attention;
+
+constexpr int kRowThreads = 256;
+
+// x [rows][width] (row pitch ld_x) -> optional RMSNorm (fortai_qwen35_cpu.f90:
+// 1408-1432) -> fortai_q8_quantize of every row into X8.  One workgroup per row.
+__global__ __launch_bounds__(kRowThreads) void rms_quantize_tokens_kernel(const float *__restrict__ x, int ld_x,
+    int width, const float *__restrict__ norm, float eps, int ld, int blocks_pad, int8_t *__restrict__ xq,
+    float *__restrict__ xs) {
+    __shared__ double red[kRowThreads / 64];
+    const int n = static_cast<int>(blockIdx.x), tid = static_cast<int>(threadIdx.x);
+    const float *row = x + static_cast<size_t>(n) * ld_x;
+    float inv = 1.0f;
+    if (norm) {
+        double ss = 0.0;
+        for (int i = tid; i < width; i += kRowThreads) ss += static_cast<double>(row[i]) * static_cast<double>(row[i]);
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        double total = 0.0;
+        for (int w = 0; w < kRowThreads / 64; ++w) total += red[w];
+        inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+    }
+    for (int g = tid; g < blocks_pad * 8; g += kRowThreads) {
+        float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (g < width / 4) {
+            y = reinterpret_cast<const float4 *>(row)[g];
+            if (norm) {
+                const float4 w4 = reinterpret_cast<const float4 *>(norm)[g];
+                y.x = (y.x * inv) * w4.x; y.y = (y.y * inv) * w4.y; y.z = (y.z * inv) * w4.z; y.w = (y.w * inv) * w4.w;
+            }
+        }
+        float scale;
+        uint16_t bits;
+        const uint32_t packed = quantize_group(y, scale, bits);
+        const int b = g >> 3, l = g & 7;
+        reinterpret_cast<uint32_t *>(xq + (static_cast<size_t>(b) * ld + n) * 32)[l] = packed;
+        if (l == 0) xs[static_cast<size_t>(b) * ld + n] = scale;
+    }
+}
+
+// GDN output o with the gate: per head ((o / rms(o)) * ssm_norm) * silu(z)
+// (fortai_qwen35_cpu.f90:907-915), quantized into X8.  One workgroup per row;
+// a head is head/4 consecutive threads (aligned power of two).
+__global__ __launch_bounds__(kRowThreads) void gated_quantize_tokens_kernel(const float *__restrict__ o,
+    const float *__restrict__ z, const float *__restrict__ norm, float eps, int width, int head, int ld,
+    int blocks_pad, int8_t *__restrict__ xq, float *__restrict__ xs) {
+    const int n = static_cast<int>(blockIdx.x), tid = static_cast<int>(threadIdx.x);
+    const float *orow = o + static_cast<size_t>(n) * width;
+    const float *zrow = z + static_cast<size_t>(n) * width;
+    const int hl = head / 4;
+    for (int g0 = 0; g0 < blocks_pad * 8; g0 += kRowThreads) {
+        const int g = g0 + tid;
+        const bool in = g < width / 4;
+        float4 y = in ? reinterpret_cast<const float4 *>(orow)[g] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        double ss = static_cast<double>(y.x) * y.x + static_cast<double>(y.y) * y.y +
+            static_cast<double>(y.z) * y.z + static_cast<double>(y.w) * y.w;
+        for (int m = 1; m < hl; m <<= 1) ss += __shfl_xor(ss, m);
+        if (in) {
+            const float nf = sqrtf(static_cast<float>(ss / static_cast<double>(head)) + eps);
+            const float4 w4 = reinterpret_cast<const float4 *>(norm)[g % hl];
+            const float4 z4 = reinterpret_cast<const float4 *>(zrow)[g];
+            y.x = ((y.x / nf) * w4.x) * silu_poly(z4.x);
+            y.y = ((y.y / nf) * w4.y) * silu_poly(z4.y);
+            y.z = ((y.z / nf) * w4.z) * silu_poly(z4.z);
+            y.w = ((y.w / nf) * w4.w) * silu_poly(z4.w);
+        }
+        float scale;
+        uint16_t bits;
+        const uint32_t packed = quantize_group(y, scale, bits);
+        if (g < blocks_pad * 8) {
+            const int b = g >> 3, l = g & 7;
+            reinterpret_cast<uint32_t *>(xq + (static_cast<size_t>(b) * ld + n) * 32)[l] = packed;
+            if (l == 0) xs[static_cast<size_t>(b) * ld + n] = scale;
+        }
+    }
+}
+
+// FFN hidden silu(gate) * up (fortai_silu_product) quantized into X8.
+__global__ __launch_bounds__(kRowThreads) void silu_product_quantize_kernel(const float *__restrict__ gate,
+    const float *__restrict__ up, int width, int ld, int blocks_pad, int8_t *__restrict__ xq, float *__restrict__ xs) {
+    const int n = static_cast<int>(blockIdx.x), tid = static_cast<int>(threadIdx.x);
+    const float4 *g4 = reinterpret_cast<const float4 *>(gate + static_cast<size_t>(n) * width);
+    const float4 *u4 = reinterpret_cast<const float4 *>(up + static_cast<size_t>(n) * width);
+    for (int g = tid; g < blocks_pad * 8; g += kRowThreads) {
+        float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (g < width / 4) {
+            const float4 a = g4[g], b = u4[g];
+            y = make_float4(silu_poly(a.x) * b.x, silu_poly(a.y) * b.y, silu_poly(a.z) * b.z, silu_poly(a.w) * b.w);
+        }
+        float scale;
+        uint16_t bits;
+        const uint32_t packed = quantize_group(y, scale, bits);
+        const int b = g >> 3, l = g & 7;
+        reinterpret_cast<uint32_t *>(xq + (static_cast<size_t>(b) * ld + n) * 32)[l] = packed;
+        if (l == 0) xs[static_cast<size_t>(b) * ld + n] = scale;
+    }
+}
+
+// Causal conv1d + SiLU over time: one thread per (sequence, channel), the
+// window in registers, continuing from and returning conv_state
+// [batch][K-1][C] (oldest first).  x: raw projections [batch*T][C].
+__global__ __launch_bounds__(256) void conv_silu_tokens_kernel(const float *__restrict__ x,
+    const float *__restrict__ conv_w, float *__restrict__ conv_state, float *__restrict__ out, int T, int C, int K) {
+    const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    const int s = static_cast<int>(blockIdx.y);
+    if (c >= C) return;
+    float win[kConvMax - 1], taps[kConvMax];
+    float *cs = conv_state + static_cast<size_t>(s) * (K - 1) * C;
+#pragma unroll
+    for (int t = 0; t < kConvMax - 1; ++t) win[t] = t < K - 1 ? cs[static_cast<size_t>(t) * C + c] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < kConvMax; ++t) taps[t] = t < K ? conv_w[static_cast<size_t>(c) * K + t] : 0.0f;
+    const float *xs = x + static_cast<size_t>(s) * T * C + c;
+    float *os = out + static_cast<size_t>(s) * T * C + c;
+#pragma unroll 8
+    for (int t = 0; t < T; ++t) {
+        const float v = xs[static_cast<size_t>(t) * C];
+        os[static_cast<size_t>(t) * C] = conv_silu(win, taps, K, v);
+#pragma unroll
+        for (int i = 0; i + 1 < kConvMax - 1; ++i)
+            if (i + 1 < K - 1) win[i] = win[i + 1];
+#pragma unroll
+        for (int i = 0; i < kConvMax - 1; ++i)
+            if (i == K - 2) win[i] = v;
+    }
+#pragma unroll
+    for (int t = 0; t < kConvMax - 1; ++t)
+        if (t < K - 1) cs[static_cast<size_t>(t) * C + c] = win[t];
+}
+
+// Per token: the L2 norms of every key head's q and k (1 / max(|x|, eps),
+// fortai_qwen35_cpu.f90:1455-1471) and every value head's beta and decay
+// (:890-894).  One workgroup per token; wave w takes key heads w, w + 4, ...
+__global__ __launch_bounds__(256) void gdn_token_prep_kernel(const float *__restrict__ qkv, const float *__restrict__ alpha,
+    const float *__restrict__ beta, const float *__restrict__ ssm_a, const float *__restrict__ ssm_dt, int C,
+    int key_heads, int value_heads, int head, int state_size, float eps, float *__restrict__ qinv,
+    float *__restrict__ kinv, float *__restrict__ beta_out, float *__restrict__ decay_out) {
+    const int n = static_cast<int>(blockIdx.x), tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6;
+    const float *row = qkv + static_cast<size_t>(n) * C;
+    for (int kh = wave; kh < key_heads; kh += 4) {
+        const float *q = row + kh * head, *k = row + state_size * key_heads + kh * head;
+        double sq = 0.0, sk = 0.0;
+        for (int i = lane; i < head; i += 64) {
+            sq += static_cast<double>(q[i]) * q[i];
+            sk += static_cast<double>(k[i]) * k[i];
+        }
+        sq = wave_sum(sq);
+        sk = wave_sum(sk);
+        if (lane == 0) {
+            qinv[static_cast<size_t>(n) * key_heads + kh] = 1.0f / fmaxf(sqrtf(static_cast<float>(sq)), eps);
+            kinv[static_cast<size_t>(n) * key_heads + kh] = 1.0f / fmaxf(sqrtf(static_cast<float>(sk)), eps);
+        }
+    }
+    for (int h = tid; h < value_heads; h += 256) {
+        const size_t i = static_cast<size_t>(n) * value_heads + h;
+        beta_out[i] = sigmoid_ref(beta[i]);
+        decay_out[i] = exp_rounded(ssm_a[h] * softplus_ref(alpha[i] + ssm_dt[h]));
+    }
+}
+
+// The delta rule over time (fortai_q8_dot.c:356-398) for 16 state rows of one
+// value head of one sequence (blockIdx.y), the state in registers in the
+// decode kernel's layout: S[row][8 i + l] at
+// state[((h * HEAD + row) * 8 + l) * HEAD/8 + i].  Normalized q and k of
+// kStage tokens are staged in LDS at a time.
+constexpr int kGdnRows = 16;
+constexpr int kStage = 16;
+
+template <int HEAD>
+__global__ __launch_bounds__(kGdnRows * 8) void gdn_prefill_kernel(const float *__restrict__ qkv,
+    const float *__restrict__ qinv, const float *__restrict__ kinv, const float *__restrict__ beta,
+    const float *__restrict__ decay, float *__restrict__ state, float *__restrict__ out, int T, int C, int key_heads,
+    int value_heads, int state_size) {
+    constexpr int kCols = HEAD / 8;
+    __shared__ __align__(16) float qs[kStage][HEAD];
+    __shared__ __align__(16) float ks[kStage][HEAD];
+    __shared__ float vs[kStage][kGdnRows];
+    __shared__ float bs[kStage], ds[kStage];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int s = static_cast<int>(blockIdx.y);
+    const int bph = HEAD / kGdnRows;
+    const int h = static_cast<int>(blockIdx.x) / bph, r0 = (static_cast<int>(blockIdx.x) % bph) * kGdnRows;
+    const int kh = h / (value_heads / key_heads);
+    const int r8 = tid >> 3, l = tid & 7, row = r0 + r8;
+    const int inner = value_heads * HEAD;
+    float *sp = state + static_cast<size_t>(s) * value_heads * HEAD * HEAD + ((static_cast<size_t>(h) * HEAD + row) * 8 + l) * kCols;
+    float st[kCols];
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) st[i] = sp[i];
+    const float scale = 1.0f / sqrtf(static_cast<float>(HEAD));
+    for (int t0 = 0; t0 < T; t0 += kStage) {
+        const int steps = min(kStage, T - t0);
+        __syncthreads();  // the previous stage is consumed
+#pragma unroll
+        for (int e = tid; e < kStage * HEAD; e += kGdnRows * 8) {
+            const int j = e / HEAD, i = e % HEAD;
+            const size_t n = static_cast<size_t>(s) * T + t0 + min(j, steps - 1);
+            const float *rowp = qkv + n * C;
+            qs[j][i] = rowp[kh * HEAD + i] * qinv[n * key_heads + kh];
+            ks[j][i] = rowp[state_size * key_heads + kh * HEAD + i] * kinv[n * key_heads + kh];
+        }
+#pragma unroll
+        for (int e = tid; e < kStage * kGdnRows; e += kGdnRows * 8) {
+            const int j = e / kGdnRows, rr = e % kGdnRows;
+            const size_t n = static_cast<size_t>(s) * T + t0 + min(j, steps - 1);
+            vs[j][rr] = qkv[n * C + 2 * state_size * key_heads + h * HEAD + r0 + rr];
+        }
+        if (tid < kStage) {
+            const size_t n = static_cast<size_t>(s) * T + t0 + min(tid, steps - 1);
+            bs[tid] = beta[n * value_heads + h];
+            ds[tid] = decay[n * value_heads + h];
+        }
+        __syncthreads();
+        for (int j = 0; j < steps; ++j) {
+            const float dec = ds[j];
+            float kd = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kCols; ++i) {
+                const float d = st[i] * dec;
+                st[i] = d;
+                kd = __builtin_fmaf(d, ks[j][8 * i + l], kd);
+            }
+            kd = row_hsum8(kd);
+            const float delta = (vs[j][r8] - kd) * bs[j];
+            float qd = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kCols; ++i) {
+                const float u = __builtin_fmaf(delta, ks[j][8 * i + l], st[i]);
+                st[i] = u;
+                qd = __builtin_fmaf(u, qs[j][8 * i + l], qd);
+            }
+            qd = row_hsum8(qd);
+            if (l == 0) out[(static_cast<size_t>(s) * T + t0 + j) * inner + h * HEAD + row] = qd * scale;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) sp[i] = st[i];
+}
+
+// Per token: q and k per-head RMSNorm + RoPE at the token's position
+// (fortai_qwen35_cpu.f90:990-999, 1473-1497), q in place; k and v appended to
+// the fp16 caches [batch][max_context][kv_heads][head] with the reference's
+// float_to_half (:1594-1601); cache_flags [batch][kv_heads] set when an
+// exponent-31 half is stored.  One workgroup per token, one wave per head.
+__global__ __launch_bounds__(256) void qk_rope_append_kernel(float *__restrict__ q, const float *__restrict__ k,
+    const float *__restrict__ v, const float *__restrict__ q_norm, const float *__restrict__ k_norm,
+    const float2 *__restrict__ rope, uint16_t *__restrict__ kcache, uint16_t *__restrict__ vcache,
+    int *__restrict__ flags, int T, int heads, int kv_heads, int head, int value, int rope_dim, int max_context,
+    float eps) {
+    __shared__ __align__(16) float buf[4][256];
+    __shared__ __align__(16) float wq[256], wk[256];
+    const int n = static_cast<int>(blockIdx.x), tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int s = n / T, pos = n % T;
+    for (int i = tid; i < head; i += 256) {
+        wq[i] = q_norm[i];
+        wk[i] = k_norm[i];
+    }
+    __syncthreads();
+    const float2 *rp = rope + static_cast<size_t>(pos) * (rope_dim / 2);
+    // q heads then k heads, one wave each
+    for (int j = wave; j < heads + kv_heads; j += 4) {
+        float *b = buf[wave];
+        const bool isq = j < heads;
+        const float *src = isq ? q + (static_cast<size_t>(n) * heads + j) * 2 * head
+                               : k + (static_cast<size_t>(n) * kv_heads + (j - heads)) * head;
+        for (int i = lane; i < head; i += 64) b[i] = src[i];
+        __builtin_amdgcn_wave_barrier();
+        ea::norm_rope(b, head, isq ? wq : wk, eps, rp, rope_dim, lane);
+        if (isq) {
+            float *dst = q + (static_cast<size_t>(n) * heads + j) * 2 * head;
+            for (int i = lane; i < head; i += 64) dst[i] = b[i];
+        } else {
+            const int kvh = j - heads;
+            uint16_t *dst = kcache + ((static_cast<size_t>(s) * max_context + pos) * kv_heads + kvh) * head;
+            int over = 0;
+            for (int i = lane; i < head; i += 64) {
+                const uint16_t hb = float_to_half_kv(b[i]);
+                dst[i] = hb;
+                over |= (hb & 0x7c00u) == 0x7c00u;
+            }
+            if (__any(over) && lane == 0) flags[static_cast<size_t>(s) * kv_heads + kvh] = 1;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    for (int e = tid; e < kv_heads * value; e += 256) {
+        const int kvh = e / value, i = e % value;
+        const uint16_t hb = float_to_half_kv(v[(static_cast<size_t>(n) * kv_heads + kvh) * value + i]);
+        vcache[((static_cast<size_t>(s) * max_context + pos) * kv_heads + kvh) * value + i] = hb;
+        if ((hb & 0x7c00u) == 0x7c00u) flags[static_cast<size_t>(s) * kv_heads + kvh] = 1;
+    }
+}
+
+// Causal attention of every prompt token (fortai_qwen35_cpu.f90:1006-1033
+// with an online softmax): one workgroup per (query block of 64, head,
+// sequence); four threads per query, each with a quarter of the head dims;
+// keys and values staged through LDS 32 positions at a time.  out =
+// softmax(q k / sqrt(head)) v * sigmoid(gate).
+constexpr int kQBlock = 64;
+constexpr int kKTile = 32;
+
+template <int HEAD>
+__global__ __launch_bounds__(256) void attention_prefill_kernel(const float *__restrict__ q,
+    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, float *__restrict__ out, int T,
+    int heads, int kv_heads, int max_context) {
+    constexpr int kPart = HEAD / 4;
+    __shared__ __align__(16) float kt[kKTile][HEAD + 4];
+    __shared__ __align__(16) float vt[kKTile][HEAD + 4];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int qi = tid >> 2, part = tid & 3;
+    const int h = static_cast<int>(blockIdx.y), s = static_cast<int>(blockIdx.z);
+    const int q0 = static_cast<int>(blockIdx.x) * kQBlock;
+    const int t = min(q0 + qi, T - 1);
+    const int kvh = h / (heads / kv_heads);
+    const float *qrow = q + ((static_cast<size_t>(s) * T + t) * heads + h) * 2 * HEAD;
+    float qv[kPart], o[kPart];
+#pragma unroll
+    for (int d = 0; d < kPart; ++d) {
+        qv[d] = qrow[part * kPart + d];
+        o[d] = 0.0f;
+    }
+    const float scale = 1.0f / sqrtf(static_cast<float>(HEAD));
+    float m = -__builtin_inff(), z = 0.0f;
+    const int last = min(q0 + kQBlock, T) - 1;  // keys 0..last cover the block
+    for (int j0 = 0; j0 <= last; j0 += kKTile) {
+        __syncthreads();
+        for (int e = tid; e < kKTile * HEAD; e += 256) {
+            const int j = e / HEAD, d = e % HEAD;
+            const int p = min(j0 + j, last);
+            const size_t off = ((static_cast<size_t>(s) * max_context + p) * kv_heads + kvh) * HEAD + d;
+            kt[j][d] = gguf_half_to_real(kcache[off]);
+            vt[j][d] = gguf_half_to_real(vcache[off]);
+        }
+        __syncthreads();
+        const int jn = min(kKTile, t - j0 + 1);  // keys of this query in the tile
+        for (int j = 0; j < kKTile; ++j) {
+            float sc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < kPart; ++d) sc = __builtin_fmaf(qv[d], kt[j][part * kPart + d], sc);
+            sc += __shfl_xor(sc, 1);
+            sc += __shfl_xor(sc, 2);
+            if (j >= jn) continue;  // masked (uniform per query: the 4 threads agree)
+            sc *= scale;
+            const float mn = fmaxf(m, sc);
+            const float corr = exp_rounded(m - mn), p = exp_rounded(sc - mn);
+            z = z * corr + p;
+#pragma unroll
+            for (int d = 0; d < kPart; ++d) o[d] = __builtin_fmaf(p, vt[j][part * kPart + d], o[d] * corr);
+            m = mn;
+        }
+    }
+    if (q0 + qi >= T) return;
+    const float *gate = qrow + HEAD;
+    float *orow = out + ((static_cast<size_t>(s) * T + t) * heads + h) * HEAD;
+#pragma unroll
+    for (int d = 0; d < kPart; ++d) {
+        const int dd = part * kPart + d;
+        orow[dd] = (o[d] / z) * sigmoid_ref(gate[dd]);
+    }
+}
+
+// Rows [r0, r0 + count) of X8 -> the matvec's Q8L layout [count][q8l_bytes]
+// (the same quantized values: used by the exact prefill mode).
+__global__ __launch_bounds__(256) void x8_to_q8l_kernel(const int8_t *__restrict__ xq, const float *__restrict__ xs,
+    int ld, int chunks, int r0, uint32_t *__restrict__ q8l) {
+    const int rr = static_cast<int>(blockIdx.y), n = r0 + rr;
+    uint32_t *dst = q8l + static_cast<size_t>(rr) * chunks * 36;
+    for (int e = static_cast<int>(threadIdx.x); e < chunks * 36; e += 256) {
+        if (e < chunks * 32) {
+            const int c = e >> 5, l = (e >> 2) & 7, j = e & 3, b = 4 * c + j;
+            dst[e] = reinterpret_cast<const uint32_t *>(xq + (static_cast<size_t>(b) * ld + n) * 32)[l];
+        } else {
+            const int b = e - chunks * 32;
+            reinterpret_cast<float *>(dst)[e] = xs[static_cast<size_t>(b) * ld + n];
+        }
+    }
+}
+
+void x8_planes(void *x8, int tokens, int width, int8_t *&xq, float *&xs, int &ld, int &blocks_pad) {
+    ld = q8_tokens_ld(tokens);
+    blocks_pad = (width / kQ8Block + 3) / 4 * 4;
+    xq = static_cast<int8_t *>(x8);
+    xs = reinterpret_cast<float *>(xq + static_cast<size_t>(ld) * blocks_pad * 32);
+}
+
+}  // namespace
+
+hipError_t launch_x8_to_q8l(const void *x8, int tokens, int width, int r0, int count, void *q8l, hipStream_t stream) {
+    if (r0 < 0 || count < 1 || r0 + count > tokens || width % kQ8Block) return hipErrorInvalidValue;
+    int8_t *xq; float *xs; int ld, bp;
+    x8_planes(const_cast<void *>(x8), tokens, width, xq, xs, ld, bp);
+    hipLaunchKernelGGL(x8_to_q8l_kernel, dim3(1, count), dim3(256), 0, stream, xq, xs, ld, bp / 4, r0,
+        static_cast<uint32_t *>(q8l));
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_quantize_tokens(const float *x, int rows, int width, const float *norm, float eps, void *x8,
+    hipStream_t stream) {
+    if (rows <= 0 || width <= 0 || width % kQ8Block) return hipErrorInvalidValue;
+    int8_t *xq; float *xs; int ld, bp;
+    x8_planes(x8, rows, width, xq, xs, ld, bp);
+    hipLaunchKernelGGL(rms_quantize_tokens_kernel, dim3(rows), dim3(kRowThreads), 0, stream, x, width, width, norm, eps,
+        ld, bp, xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_gated_quantize_tokens(const float *o, const float *z, const float *norm, float eps, int rows,
+    int width, int head, void *x8, hipStream_t stream) {
+    const int hl = head / 4;
+    if (rows <= 0 || width % kQ8Block || head % 4 || hl > 64 || (hl & (hl - 1)) || width % head) return hipErrorInvalidValue;
+    int8_t *xq; float *xs; int ld, bp;
+    x8_planes(x8, rows, width, xq, xs, ld, bp);
+    hipLaunchKernelGGL(gated_quantize_tokens_kernel, dim3(rows), dim3(kRowThreads), 0, stream, o, z, norm, eps, width,
+        head, ld, bp, xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_product_quantize(const float *gate, const float *up, int rows, int width, void *x8,
+    hipStream_t stream) {
+    if (rows <= 0 || width % kQ8Block) return hipErrorInvalidValue;
+    int8_t *xq; float *xs; int ld, bp;
+    x8_planes(x8, rows, width, xq, xs, ld, bp);
+    hipLaunchKernelGGL(silu_product_quantize_kernel, dim3(rows), dim3(kRowThreads), 0, stream, gate, up, width, ld, bp,
+        xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv_silu_tokens(const float *x, const float *conv_w, float *conv_state, float *out, int batch, int T,
+    int C, int K, hipStream_t stream) {
+    if (batch < 1 || T < 1 || C < 1 || K < 2 || K > kConvMax) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(conv_silu_tokens_kernel, dim3((C + 255) / 256, batch), dim3(256), 0, stream, x, conv_w,
+        conv_state, out, T, C, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_prefill(const GdnParams &p, int batch, int T, float *qinv, float *kinv, float *beta_t,
+    float *decay_t, hipStream_t stream) {
+    if (batch < 1 || T < 1 || p.key_heads <= 0 || p.value_heads % p.key_heads || p.state_size != p.head)
+        return hipErrorInvalidValue;
+    const int C = 2 * p.state_size * p.key_heads + p.value_heads * p.head;
+    const int rows = batch * T;
+    hipLaunchKernelGGL(gdn_token_prep_kernel, dim3(rows), dim3(256), 0, stream, p.qkv, p.alpha, p.beta, p.ssm_a,
+        p.ssm_dt, C, p.key_heads, p.value_heads, p.head, p.state_size, p.eps, qinv, kinv, beta_t, decay_t);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid(p.value_heads * (p.head / kGdnRows), batch);
+    switch (p.head) {
+    case 64:
+        hipLaunchKernelGGL(gdn_prefill_kernel<64>, grid, dim3(kGdnRows * 8), 0, stream, p.qkv, qinv, kinv, beta_t,
+            decay_t, p.state, p.out, T, C, p.key_heads, p.value_heads, p.state_size);
+        break;
+    case 128:
+        hipLaunchKernelGGL(gdn_prefill_kernel<128>, grid, dim3(kGdnRows * 8), 0, stream, p.qkv, qinv, kinv, beta_t,
+            decay_t, p.state, p.out, T, C, p.key_heads, p.value_heads, p.state_size);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream) {
+    if (batch < 1 || T < 1 || T > p.max_context || p.heads % p.kv_heads || p.head != p.value ||
+        p.rope_dim > p.head || p.head > 256)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(qk_rope_append_kernel, dim3(batch * T), dim3(256), 0, stream, const_cast<float *>(p.q), p.k,
+        p.v, p.q_norm, p.k_norm, p.rope, p.kcache, p.vcache, p.cache_flags, T, p.heads, p.kv_heads, p.head, p.value,
+        p.rope_dim, p.max_context, p.eps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid((T + kQBlock - 1) / kQBlock, p.heads, batch);
+    switch (p.head) {
+    case 64:
+        hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache, out, T,
+            p.heads, p.kv_heads, p.max_context);
+        break;
+    case 128:
+        hipLaunchKernelGGL(attention_prefill_kernel<128>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache, out, T,
+            p.heads, p.kv_heads, p.max_context);
+        break;
+    case 256:
+        hipLaunchKernelGGL(attention_prefill_kernel<256>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache, out, T,
+            p.heads, p.kv_heads, p.max_context);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fortai_hip

@@ -348,6 +348,17 @@ int fortai_hip_qwen35_batch_generate(fortai_hip_qwen35_batch *batch_decoder, con
 /* enqueue `steps` further steps from the device tokens and positions (no
  * synchronisation; for timing loops) */
 int fortai_hip_qwen35_batch_replay(fortai_hip_qwen35_batch *batch_decoder, int steps);
+/* Prompt prefill of every sequence from position 0 (after create or reset):
+ * tokens [batch][T]; all batch x T tokens go through each layer at once (the
+ * projections as token-block products on the i8 matrix cores, conv1d / delta
+ * rule / causal attention looping over time), leaving every state, cache,
+ * token and position as T decode steps of those tokens would (within fp32
+ * rounding: the reference has no prefill and runs each prompt token through
+ * the decode step, fortai_qwen35_cpu.f90:591-711).  next_tokens [batch]
+ * (greedy token after the prompt), host_logits [batch][vocab] and kernel_ms
+ * (event-timed prefill) may be NULL. */
+int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *batch_decoder, const int64_t *tokens, int T,
+    int64_t *next_tokens, float *host_logits, float *kernel_ms);
 /* device pointer of the logits [batch][vocab] */
 int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batch_decoder, void **device_logits);
 
