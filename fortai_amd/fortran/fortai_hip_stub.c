@@ -598,3 +598,98 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *
     (void)device_logits;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
+
+FORTAI_HIP_WEAK int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_x, int batch, void *device_output, float *kernel_ms)
+{
+    (void)context; (void)weights; (void)device_x; (void)batch; (void)device_output; (void)kernel_ms;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK size_t fortai_hip_q8_tokens_bytes(int tokens, int width)
+{
+    (void)tokens; (void)width;
+    return 0;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_q8_quantize_tokens_device(fortai_hip_q8_context *context, const void *device_x,
+    int tokens, int width, void *device_tokens)
+{
+    (void)context; (void)device_x; (void)tokens; (void)width; (void)device_tokens;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_q8_mmq_device(fortai_hip_q8_context *context, const fortai_hip_q8_weights *weights,
+    const void *device_tokens, int tokens, void *device_output, const void *device_residual, float *kernel_ms)
+{
+    (void)context; (void)weights; (void)device_tokens; (void)tokens; (void)device_output; (void)device_residual;
+    (void)kernel_ms;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_q8_mmq_block_dots(fortai_hip_q8_context *context, const fortai_hip_q8_weights *weights,
+    const void *device_tokens, int tokens, void *device_dots)
+{
+    (void)context; (void)weights; (void)device_tokens; (void)tokens; (void)device_dots;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *context, int batch, int layer_count,
+    fortai_hip_qwen35_recurrent *const *recurrent, fortai_hip_qwen35_attention *const *attention,
+    const fortai_hip_q8_weights *const *ffn_gate, const fortai_hip_q8_weights *const *ffn_up,
+    const fortai_hip_q8_weights *const *ffn_down, const float *const *attn_norm, const float *const *post_norm,
+    const float *output_norm, int hidden_size, const fortai_hip_f16_weights *embedding_f16,
+    const fortai_hip_q8_weights *embedding_q8, const fortai_hip_f16_weights *output_f16,
+    const fortai_hip_q8_weights *output_q8, int max_context, float norm_epsilon, fortai_hip_qwen35_batch **batch_decoder)
+{
+    (void)context; (void)batch; (void)layer_count; (void)recurrent; (void)attention; (void)ffn_gate; (void)ffn_up;
+    (void)ffn_down; (void)attn_norm; (void)post_norm; (void)output_norm; (void)hidden_size; (void)embedding_f16;
+    (void)embedding_q8; (void)output_f16; (void)output_q8; (void)max_context; (void)norm_epsilon;
+    if (batch_decoder) *batch_decoder = NULL;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_destroy(fortai_hip_qwen35_batch *batch_decoder)
+{
+    (void)batch_decoder;
+    return FORTAI_HIP_OK;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_reset(fortai_hip_qwen35_batch *batch_decoder)
+{
+    (void)batch_decoder;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_forward(fortai_hip_qwen35_batch *batch_decoder, const int64_t *tokens,
+    const int *positions, float *host_logits, int64_t *next_tokens)
+{
+    (void)batch_decoder; (void)tokens; (void)positions; (void)host_logits; (void)next_tokens;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_generate(fortai_hip_qwen35_batch *batch_decoder, const int64_t *tokens,
+    const int *positions, int steps, int64_t *host_trace)
+{
+    (void)batch_decoder; (void)tokens; (void)positions; (void)steps; (void)host_trace;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_replay(fortai_hip_qwen35_batch *batch_decoder, int steps)
+{
+    (void)batch_decoder; (void)steps;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *batch_decoder, const int64_t *tokens,
+    int T, int64_t *next_tokens, float *host_logits, float *kernel_ms)
+{
+    (void)batch_decoder; (void)tokens; (void)T; (void)next_tokens; (void)host_logits; (void)kernel_ms;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batch_decoder, void **device_logits)
+{
+    (void)batch_decoder; (void)device_logits;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
