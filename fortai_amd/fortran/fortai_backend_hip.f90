@@ -89,6 +89,20 @@ module fortai_backend_hip
         procedure :: generate => decoder_generate
     end type hip_qwen35_decoder_t
 
+    ! Independent sequences (up to 8) over one set of layers and weights, with
+    ! a prompt prefill on the i8 matrix cores (fortai_hip_qwen35_batch_*).
+    type, public :: hip_qwen35_batch_t
+        type(c_ptr) :: handle = c_null_ptr
+        type(c_ptr) :: context = c_null_ptr
+        integer :: batch = 0
+    contains
+        procedure :: create => batch_create
+        procedure :: destroy => batch_destroy
+        procedure :: reset => batch_reset
+        procedure :: prefill => batch_prefill
+        procedure :: generate => batch_generate
+    end type hip_qwen35_batch_t
+
     public :: hip_q8_matvec_resident, hip_q8_matvec_device_f32, hip_qwen35_embedding_device
     public :: hip_qwen35_copy_device, hip_qwen35_add_device, hip_qwen35_rms_norm_device
     public :: hip_q8_matvec_host, hip_q8_matvec_host_pair, hip_q8_matvec_host_triplet
@@ -348,6 +362,38 @@ module fortai_backend_hip
             type(c_ptr), value :: decoder, trace
             integer(c_int64_t), value :: token
             integer(c_int), value :: position, steps
+        end function
+        integer(c_int) function fh_batch_create(context, batch, layer_count, recurrent, attention, ffn_gate, &
+                ffn_up, ffn_down, attn_norm, post_norm, output_norm, hidden, emb16, emb8, out16, out8, &
+                max_context, eps, decoder) bind(C, name='fortai_hip_qwen35_batch_create')
+            import :: c_float, c_int, c_ptr
+            type(c_ptr), value :: context
+            integer(c_int), value :: batch, layer_count, hidden, max_context
+            type(c_ptr), intent(in) :: recurrent(*), attention(*), ffn_gate(*), ffn_up(*), ffn_down(*)
+            type(c_ptr), intent(in) :: attn_norm(*), post_norm(*)
+            type(c_ptr), value :: output_norm, emb16, emb8, out16, out8
+            real(c_float), value :: eps
+            type(c_ptr), intent(out) :: decoder
+        end function
+        integer(c_int) function fh_batch_destroy(decoder) bind(C, name='fortai_hip_qwen35_batch_destroy')
+            import :: c_int, c_ptr
+            type(c_ptr), value :: decoder
+        end function
+        integer(c_int) function fh_batch_reset(decoder) bind(C, name='fortai_hip_qwen35_batch_reset')
+            import :: c_int, c_ptr
+            type(c_ptr), value :: decoder
+        end function
+        integer(c_int) function fh_batch_prefill(decoder, tokens, t, next_tokens, logits, kernel_ms) &
+                bind(C, name='fortai_hip_qwen35_batch_prefill')
+            import :: c_int, c_ptr
+            type(c_ptr), value :: decoder, tokens, next_tokens, logits, kernel_ms
+            integer(c_int), value :: t
+        end function
+        integer(c_int) function fh_batch_generate(decoder, tokens, positions, steps, trace) &
+                bind(C, name='fortai_hip_qwen35_batch_generate')
+            import :: c_int, c_ptr
+            type(c_ptr), value :: decoder, tokens, positions, trace
+            integer(c_int), value :: steps
         end function
         integer(c_int) function c_strlen(s) bind(C, name='strlen')
             import :: c_int, c_ptr
@@ -1211,5 +1257,125 @@ contains
         call settle(fh_decoder_generate(self%handle, token, int(position, c_int), int(size(trace), c_int), &
             c_loc(trace)), self%context, 'Qwen decoder generation', stat)
     end subroutine decoder_generate
+
+    ! ---- batched decoder (independent sequences, prompt prefill) ------------------
+
+    ! As decoder_create, for `batch` sequences (1..8) that share the weights;
+    ! the batch object holds every sequence's state and caches.
+    subroutine batch_create(self, context, batch, recurrent, attention, ffn_gate, ffn_up, ffn_down, &
+            attn_norm, post_norm, output_norm, embedding_f16, embedding_q8, output_f16, output_q8, &
+            max_context, norm_epsilon, stat)
+        class(hip_qwen35_batch_t), intent(inout) :: self
+        class(hip_q8_context_t), intent(in) :: context
+        integer, intent(in) :: batch
+        type(hip_qwen35_recurrent_t), intent(in) :: recurrent(:)
+        type(hip_qwen35_attention_t), intent(in) :: attention(:)
+        type(hip_q8_weights_t), intent(in) :: ffn_gate(:), ffn_up(:), ffn_down(:)
+        real(c_float), contiguous, target, intent(in) :: attn_norm(:, :), post_norm(:, :), output_norm(:)
+        type(hip_f16_weights_t), intent(in) :: embedding_f16, output_f16
+        type(hip_q8_weights_t), intent(in) :: embedding_q8, output_q8
+        integer, intent(in) :: max_context
+        real(c_float), intent(in) :: norm_epsilon
+        type(status_t), intent(out) :: stat
+        type(c_ptr), allocatable :: rec(:), att(:), gate(:), up(:), down(:), an(:), pn(:)
+        integer :: n, i
+        integer(c_int) :: code
+
+        call stat%clear()
+        n = size(ffn_gate)
+        if (.not. live(context%handle) .or. n <= 0 .or. size(recurrent) /= n .or. size(attention) /= n .or. &
+                size(ffn_up) /= n .or. size(ffn_down) /= n .or. size(attn_norm, 2) /= n .or. &
+                size(post_norm, 2) /= n .or. size(attn_norm, 1) /= size(output_norm) .or. &
+                size(post_norm, 1) /= size(output_norm) .or. max_context <= 0 .or. batch < 1 .or. batch > 8) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Qwen batch arguments')
+            return
+        end if
+        allocate (rec(n), att(n), gate(n), up(n), down(n), an(n), pn(n))
+        do i = 1, n
+            rec(i) = recurrent(i)%handle
+            att(i) = attention(i)%handle
+            gate(i) = ffn_gate(i)%handle
+            up(i) = ffn_up(i)%handle
+            down(i) = ffn_down(i)%handle
+            an(i) = c_loc(attn_norm(1, i))
+            pn(i) = c_loc(post_norm(1, i))
+        end do
+        if (live(self%handle)) call self%destroy(stat)
+        code = fh_batch_create(context%handle, int(batch, c_int), int(n, c_int), rec, att, gate, up, down, an, &
+            pn, c_loc(output_norm), int(size(output_norm), c_int), embedding_f16%handle, embedding_q8%handle, &
+            output_f16%handle, output_q8%handle, int(max_context, c_int), norm_epsilon, self%handle)
+        if (code /= FORTAI_HIP_OK) then
+            self%handle = c_null_ptr
+            self%context = c_null_ptr
+            self%batch = 0
+        else
+            self%context = context%handle
+            self%batch = batch
+        end if
+        call settle(code, context%handle, 'Qwen batch creation', stat)
+    end subroutine batch_create
+
+    subroutine batch_destroy(self, stat)
+        class(hip_qwen35_batch_t), intent(inout) :: self
+        type(status_t), intent(out) :: stat
+        integer(c_int) :: code
+
+        call stat%clear()
+        if (.not. live(self%handle)) return
+        code = fh_batch_destroy(self%handle)
+        self%handle = c_null_ptr
+        self%context = c_null_ptr
+        self%batch = 0
+        if (code /= FORTAI_HIP_OK) call stat%set(FORTAI_UNSUPPORTED, 'HIP Qwen batch destruction failed')
+    end subroutine batch_destroy
+
+    subroutine batch_reset(self, stat)
+        class(hip_qwen35_batch_t), intent(inout) :: self
+        type(status_t), intent(out) :: stat
+
+        call stat%clear()
+        if (.not. live(self%handle)) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Qwen batch')
+            return
+        end if
+        call settle(fh_batch_reset(self%handle), self%context, 'Qwen batch reset', stat)
+    end subroutine batch_reset
+
+    ! Prompt tokens(t, s) of every sequence from position 0 (after reset);
+    ! next_tokens(s) is the greedy token after the prompt.
+    subroutine batch_prefill(self, tokens, next_tokens, stat)
+        class(hip_qwen35_batch_t), intent(inout) :: self
+        integer(c_int64_t), contiguous, target, intent(in) :: tokens(:, :)
+        integer(c_int64_t), contiguous, target, intent(out) :: next_tokens(:)
+        type(status_t), intent(out) :: stat
+
+        call stat%clear()
+        if (.not. live(self%handle) .or. size(tokens, 2) /= self%batch .or. size(tokens, 1) <= 0 .or. &
+                size(next_tokens) /= self%batch) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Qwen batch prefill')
+            return
+        end if
+        call settle(fh_batch_prefill(self%handle, c_loc(tokens), int(size(tokens, 1), c_int), c_loc(next_tokens), &
+            c_null_ptr, c_null_ptr), self%context, 'Qwen batch prefill', stat)
+    end subroutine batch_prefill
+
+    ! Greedy decode of size(trace, 1) tokens per sequence from (tokens(s),
+    ! positions(s)); trace(k, s), device resident in between.
+    subroutine batch_generate(self, tokens, positions, trace, stat)
+        class(hip_qwen35_batch_t), intent(inout) :: self
+        integer(c_int64_t), contiguous, target, intent(in) :: tokens(:)
+        integer(c_int), contiguous, target, intent(in) :: positions(:)
+        integer(c_int64_t), contiguous, target, intent(out) :: trace(:, :)
+        type(status_t), intent(out) :: stat
+
+        call stat%clear()
+        if (.not. live(self%handle) .or. size(tokens) /= self%batch .or. size(positions) /= self%batch .or. &
+                size(trace, 2) /= self%batch .or. size(trace, 1) <= 0) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Qwen batch generation')
+            return
+        end if
+        call settle(fh_batch_generate(self%handle, c_loc(tokens), c_loc(positions), int(size(trace, 1), c_int), &
+            c_loc(trace)), self%context, 'Qwen batch generation', stat)
+    end subroutine batch_generate
 
 end module fortai_backend_hip
