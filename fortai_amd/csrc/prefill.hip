@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void conv_silu_tokens_kernel(const float *__re
     for (int t = 0; t < kConvMax; ++t) taps[t] = t < K ? conv_w[static_cast<size_t>(c) * K + t] : 0.0f;
     const float *xs = x + static_cast<size_t>(s) * T * C + c;
     float *os = out + static_cast<size_t>(s) * T * C + c;
-#pragma unroll 8
+#pragma unroll 32
     for (int t = 0; t < T; ++t) {
         const float v = xs[static_cast<size_t>(t) * C];
         os[static_cast<size_t>(t) * C] = conv_silu(win, taps, K, v);
@@ -326,8 +326,9 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float *__r
     const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, float *__restrict__ out, int T,
     int heads, int kv_heads, int max_context) {
     constexpr int kPart = HEAD / 4;
-    __shared__ __align__(16) float kt[kKTile][HEAD + 4];
-    __shared__ __align__(16) float vt[kKTile][HEAD + 4];
+    constexpr int kPartPitch = kPart + 4;  // the four quarters of a row on different banks
+    __shared__ __align__(16) float kt[kKTile][4 * kPartPitch];
+    __shared__ __align__(16) float vt[kKTile][4 * kPartPitch];
     const int tid = static_cast<int>(threadIdx.x);
     const int qi = tid >> 2, part = tid & 3;
     const int h = static_cast<int>(blockIdx.y), s = static_cast<int>(blockIdx.z);
@@ -350,25 +351,33 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float *__r
             const int j = e / HEAD, d = e % HEAD;
             const int p = min(j0 + j, last);
             const size_t off = ((static_cast<size_t>(s) * max_context + p) * kv_heads + kvh) * HEAD + d;
-            kt[j][d] = gguf_half_to_real(kcache[off]);
-            vt[j][d] = gguf_half_to_real(vcache[off]);
+            const int dd = (d / kPart) * kPartPitch + d % kPart;
+            kt[j][dd] = gguf_half_to_real(kcache[off]);
+            vt[j][dd] = gguf_half_to_real(vcache[off]);
         }
         __syncthreads();
         const int jn = min(kKTile, t - j0 + 1);  // keys of this query in the tile
         for (int j = 0; j < kKTile; ++j) {
             float sc = 0.0f;
 #pragma unroll
-            for (int d = 0; d < kPart; ++d) sc = __builtin_fmaf(qv[d], kt[j][part * kPart + d], sc);
+            for (int d = 0; d < kPart; ++d) sc = __builtin_fmaf(qv[d], kt[j][part * kPartPitch + d], sc);
             sc += __shfl_xor(sc, 1);
             sc += __shfl_xor(sc, 2);
             if (j >= jn) continue;  // masked (uniform per query: the 4 threads agree)
             sc *= scale;
-            const float mn = fmaxf(m, sc);
-            const float corr = exp_rounded(m - mn), p = exp_rounded(sc - mn);
-            z = z * corr + p;
+            // online softmax; the running sums are rescaled only when the
+            // maximum grows (within the fp32 tolerance of this path)
+            if (sc > m) {
+                const float corr = __expf(m - sc);
+                z *= corr;
 #pragma unroll
-            for (int d = 0; d < kPart; ++d) o[d] = __builtin_fmaf(p, vt[j][part * kPart + d], o[d] * corr);
-            m = mn;
+                for (int d = 0; d < kPart; ++d) o[d] *= corr;
+                m = sc;
+            }
+            const float p = __expf(sc - m);
+            z += p;
+#pragma unroll
+            for (int d = 0; d < kPart; ++d) o[d] = __builtin_fmaf(p, vt[j][part * kPartPitch + d], o[d]);
         }
     }
     if (q0 + qi >= T) return;
