@@ -74,6 +74,9 @@ _SIGNATURES = {
     "fortai_hip_q8_quantize_device": [_vp, _vp, _sz, _vp, _vp],
     "fortai_hip_q8_block_dots_device": [_vp, _vp, _vp, _vp],
     "fortai_hip_q8_batch_matvec_device": [_vp, _vp, _vp, _i, _vp, _fp],
+    "fortai_hip_q8_pack_bytes": [_i, _i],
+    "fortai_hip_q8_weights_pack": [_vp, _vp, _sz],
+    "fortai_hip_q8_weights_upload_packed": [_vp, _vp, _sz, _i, _i, _vpp],
     "fortai_hip_q8_tokens_bytes": [_i, _i],
     "fortai_hip_q8_quantize_tokens_device": [_vp, _vp, _i, _i, _vp],
     "fortai_hip_q8_mmq_device": [_vp, _vp, _vp, _i, _vp, _vp, _fp],
@@ -95,6 +98,8 @@ _SIGNATURES = {
     "fortai_hip_qwen35_decoder_status": [_vp],
     "fortai_hip_qwen35_decoder_persistent": [_vp],
     "fortai_hip_qwen35_decoder_phase_times": [_vp, _vp, C.c_size_t],
+    "fortai_hip_qwen35_decoder_plan": [_vp, _vp, _sz, C.POINTER(C.c_size_t)],
+    "fortai_hip_qwen35_batch_plan": [_vp, _i, _vp, _sz, C.POINTER(C.c_size_t)],
     "fortai_hip_qwen35_batch_create": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp,
                                        _vp, _i, _f, _vpp],
     "fortai_hip_qwen35_batch_destroy": [_vp],
@@ -105,7 +110,8 @@ _SIGNATURES = {
     "fortai_hip_qwen35_batch_logits": [_vp, _vpp],
     "fortai_hip_qwen35_batch_prefill": [_vp, _vp, _i, _vp, _vp, _fp],
 }
-_RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p, "fortai_hip_q8_tokens_bytes": C.c_size_t}
+_RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p, "fortai_hip_q8_tokens_bytes": C.c_size_t,
+            "fortai_hip_q8_pack_bytes": C.c_size_t}
 
 _lib: Optional[C.CDLL] = None
 
@@ -134,6 +140,19 @@ def load(path: str = LIB_PATH) -> C.CDLL:
 
 def exported_symbols() -> Sequence[str]:
     return list(_SIGNATURES)
+
+
+def _plan(ctx, name: str, *args):
+    """Read a recorded plan: [(operation, kernel, batch)] (PlanIR steps)."""
+    need = C.c_size_t()
+    ctx.call(name, *args, None, 0, C.byref(need))
+    buf = C.create_string_buffer(need.value)
+    ctx.call(name, *args, buf, need.value, C.byref(need))
+    steps = []
+    for line in buf.value.decode().splitlines():
+        op, kernel, batch = line.split("\t")
+        steps.append((op, kernel, int(batch)))
+    return steps
 
 
 def _ptr(a: np.ndarray) -> C.c_void_p:
@@ -232,12 +251,30 @@ class DeviceBuffer:
 class Q8Weights:
     """Resident Q8_0 matrix (GGUF bytes [rows][width/32][34])."""
 
-    def __init__(self, ctx: Context, gguf_bytes: np.ndarray, rows: int, width: int):
+    def __init__(self, ctx: Context, gguf_bytes: Optional[np.ndarray], rows: int, width: int,
+                 packed: Optional[np.ndarray] = None):
         self.ctx, self.rows, self.width = ctx, rows, width
-        data = np.ascontiguousarray(gguf_bytes).view(np.uint8)
         h = C.c_void_p()
-        ctx.call("fortai_hip_q8_weights_upload", ctx.h, _ptr(data), data.nbytes, rows, width, C.byref(h))
+        if packed is not None:
+            planes = np.ascontiguousarray(packed).view(np.uint8)
+            ctx.call("fortai_hip_q8_weights_upload_packed", ctx.h, _ptr(planes), planes.nbytes, rows, width,
+                     C.byref(h))
+        else:
+            data = np.ascontiguousarray(gguf_bytes).view(np.uint8)
+            ctx.call("fortai_hip_q8_weights_upload", ctx.h, _ptr(data), data.nbytes, rows, width, C.byref(h))
         self.h = h
+
+    @classmethod
+    def from_packed(cls, ctx: Context, planes: np.ndarray, rows: int, width: int) -> "Q8Weights":
+        """A resident matrix from planes written by pack() (no repack)."""
+        return cls(ctx, None, rows, width, packed=planes)
+
+    def pack(self) -> np.ndarray:
+        """The resident (repacked) planes, for a weight-pack cache."""
+        n = self.ctx.lib.fortai_hip_q8_pack_bytes(self.rows, self.width)
+        out = np.empty(n, dtype=np.uint8)
+        self.ctx.call("fortai_hip_q8_weights_pack", self.h, _ptr(out), n)
+        return out
 
     def free(self) -> None:
         if self.h:
@@ -394,6 +431,10 @@ class Decoder:
     def persistent(self) -> bool:
         return self.ctx.lib.fortai_hip_qwen35_decoder_persistent(self.h) == 1
 
+    def plan(self):
+        """The launches of one step: [(operation, kernel, batch)]."""
+        return _plan(self.ctx, "fortai_hip_qwen35_decoder_plan", self.h)
+
     def free(self) -> None:
         if self.h:
             self.ctx.lib.fortai_hip_qwen35_decoder_destroy(self.h)
@@ -455,6 +496,10 @@ class BatchDecoder:
 
     def replay(self, steps: int) -> None:
         self.ctx.call("fortai_hip_qwen35_batch_replay", self.h, steps)
+
+    def plan(self, prefill: bool = False):
+        """The launches of one batched step (or of the last prefill)."""
+        return _plan(self.ctx, "fortai_hip_qwen35_batch_plan", self.h, 1 if prefill else 0)
 
     def prefill(self, tokens, want_logits: bool = True):
         """Prompt tokens [batch][T] from position 0; returns (next tokens,

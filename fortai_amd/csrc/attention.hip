@@ -397,6 +397,8 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int ba
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads), lds, stream, p);
     e = hipGetLastError();
+    note_launch("attention_scores_kernel grid %dx%d + attention_output_kernel grid %dx%d", p.kv_heads * nblk_max, batch,
+        p.heads * (p.value / ea::kDims), batch);
     if (e != hipSuccess || p.max_context <= p.exact_max) return e;
     // long contexts: the split-K pair (each kernel picks its regime from the device position)
     hipLaunchKernelGGL(attention_split_kernel, dim3(p.kv_heads * attention_split_chunks(p.max_context), batch),
@@ -405,6 +407,8 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int ba
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attention_merge_kernel, dim3(p.heads * ((p.value + kMergeDims - 1) / kMergeDims), batch),
         dim3(ea::kThreads), 0, stream, p);
+    note_launch("attention_scores_kernel + attention_output_kernel (positions <= %d) + attention_split_kernel grid "
+        "%dx%d + attention_merge_kernel (beyond)", p.exact_max, p.kv_heads * attention_split_chunks(p.max_context), batch);
     return hipGetLastError();
 }
 

@@ -846,6 +846,7 @@ const char *persistent_unsupported(const PersistentPlan &P, int grid) {
 
 hipError_t launch_decode_persistent(const PersistentPlan *plan_device, uint32_t tag, int grid, hipStream_t stream) {
     hipLaunchKernelGGL(decode_persistent_kernel, dim3(grid), dim3(kT), kLdsBytes, stream, plan_device, tag);
+    note_launch("decode_persistent_kernel grid %d", grid);
     return hipGetLastError();
 }
 

@@ -24,6 +24,12 @@ using namespace fortai_hip;
 // (the fp16 LM head uses one per 128 rows: vocabularies up to 524,288)
 constexpr int kArgmaxParts = 4096;
 
+// one recorded launch: the reference's PlanIR step (src/fortai_plan_ir.f90:7-11)
+struct plan_step {
+    std::string operation, kernel;
+    int batch = 1;
+};
+
 struct fortai_hip_q8_context {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -118,6 +124,7 @@ struct fortai_hip_qwen35_decoder {
     uint32_t next_tag = 1;                   // tag of the next persistent launch
     int *status = nullptr;
     uint64_t *phase_times = nullptr;  // FORTAI_HIP_PHASE_TIMES=1: per-workgroup phase end clocks
+    std::vector<plan_step> plan;  // the launches of one step (PlanIR steps)
 };
 
 // Batched decoder: `batch` independent sequences over one set of layers and
@@ -161,6 +168,7 @@ struct fortai_hip_qwen35_batch {
     int64_t *ptokens = nullptr;
     void *pq8l = nullptr;                                  // exact mode: 8 tokens in the matvec layout
     bool use_graph = true;            // FORTAI_HIP_DECODER_GRAPH=0: enqueue the kernels every step
+    std::vector<plan_step> plan, prefill_plan;  // launches of one step / of the last prefill
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
@@ -173,6 +181,32 @@ int fail(fortai_hip_q8_context *ctx, int code, const char *op, hipError_t err = 
         else std::snprintf(ctx->error, sizeof(ctx->error), "%s: %s", op, hipGetErrorString(err));
     }
     return code;
+}
+
+// PlanIR recording (src/fortai_plan_ir.f90:7-21): while a plan is being
+// recorded, every successful launch appends (operation, kernel, batch).
+thread_local std::vector<plan_step> *g_plan = nullptr;
+thread_local int g_plan_batch = 1;
+
+hipError_t rec(hipError_t e, const char *operation) {
+    if (e == hipSuccess && g_plan) g_plan->push_back({operation, last_launch(), g_plan_batch});
+    return e;
+}
+
+// "operation\tkernel\tbatch\n" lines
+std::string plan_text(const std::vector<plan_step> &plan) {
+    std::string t;
+    for (const auto &s : plan) t += s.operation + "\t" + s.kernel + "\t" + std::to_string(s.batch) + "\n";
+    return t;
+}
+
+int copy_plan(const std::vector<plan_step> &plan, char *buffer, size_t bytes, size_t *needed) {
+    const std::string t = plan_text(plan);
+    if (needed) *needed = t.size() + 1;
+    if (!buffer) return FORTAI_HIP_OK;
+    if (bytes < t.size() + 1) return FORTAI_HIP_INVALID;
+    std::memcpy(buffer, t.c_str(), t.size() + 1);
+    return FORTAI_HIP_OK;
 }
 
 int done(fortai_hip_q8_context *ctx, hipError_t err, const char *op) {
@@ -283,8 +317,11 @@ hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &
     segs[0].conv_size = L->conv_size;
     segs[0].kernel = L->kernel;
     segs[1].silu = true;  // the gate is only used through SiLU
-    hipError_t e = launch_q8_matvec(segs, 4, in, pro, Epilogue::STORE, stream);
-    if (e == hipSuccess) e = launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw), stream);
+    hipError_t e = rec(launch_q8_matvec(segs, 4, in, pro, Epilogue::STORE, stream),
+        "GDN qkv/gate/alpha/beta projections, conv1d + SiLU");
+    if (e == hipSuccess)
+        e = rec(launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw), stream),
+            "GDN L2 norms, decay/beta, delta rule");
     if (e != hipSuccess) return e;
     MatvecInput gated;
     gated.x = L->o_raw;
@@ -294,7 +331,8 @@ hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &
     gated.head = L->head;
     gated.width = L->inner;
     const MatvecSegment oseg = segment(L->out, out, resid);
-    return launch_q8_matvec(&oseg, 1, gated, Prologue::GATED, resid ? Epilogue::ADD : Epilogue::STORE, stream);
+    return rec(launch_q8_matvec(&oseg, 1, gated, Prologue::GATED, resid ? Epilogue::ADD : Epilogue::STORE, stream),
+        "GDN gated RMSNorm, ssm_out projection + residual");
 }
 
 AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q, const float *k, const float *v,
@@ -311,26 +349,29 @@ AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q,
 hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &in, Prologue pro, float *out,
     const float *resid, hipStream_t stream) {
     const MatvecSegment segs[3] = {segment(A->q, A->q_out), segment(A->k, A->k_out), segment(A->v, A->v_out)};
-    hipError_t e = launch_q8_matvec(segs, 3, in, pro, Epilogue::STORE, stream);
+    hipError_t e = rec(launch_q8_matvec(segs, 3, in, pro, Epilogue::STORE, stream), "attention q/k/v projections");
     if (e != hipSuccess) return e;
-    e = launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream);
+    e = rec(launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream),
+        "q/k norm, RoPE, KV append, softmax.V, gate");
     if (e != hipSuccess) return e;
     const MatvecSegment oseg = segment(A->o, out, resid);
     MatvecInput oin;
     oin.x = A->attn_out;
     oin.width = A->heads * A->value;
-    return launch_q8_matvec(&oseg, 1, oin, Prologue::F32, resid ? Epilogue::ADD : Epilogue::STORE, stream);
+    return rec(launch_q8_matvec(&oseg, 1, oin, Prologue::F32, resid ? Epilogue::ADD : Epilogue::STORE, stream),
+        "attention o projection + residual");
 }
 
 hipError_t enqueue_ffn(const fortai_hip_q8_weights *gate, const fortai_hip_q8_weights *up,
     const fortai_hip_q8_weights *down, const MatvecInput &in, Prologue pro, void *h_q8l, float *out,
     const float *resid, hipStream_t stream) {
     const MatvecSegment pair = segment(gate, nullptr, nullptr, up, h_q8l);
-    hipError_t e = launch_q8_matvec(&pair, 1, in, pro, Epilogue::SILU_PAIR, stream);
+    hipError_t e = rec(launch_q8_matvec(&pair, 1, in, pro, Epilogue::SILU_PAIR, stream),
+        "FFN post-norm, gate/up projections, SiLU product");
     if (e != hipSuccess) return e;
     const MatvecSegment dseg = segment(down, out, resid);
-    return launch_q8_matvec(&dseg, 1, q8l_input(h_q8l, gate->m.rows), Prologue::Q8L,
-        resid ? Epilogue::ADD : Epilogue::STORE, stream);
+    return rec(launch_q8_matvec(&dseg, 1, q8l_input(h_q8l, gate->m.rows), Prologue::Q8L,
+        resid ? Epilogue::ADD : Epilogue::STORE, stream), "FFN down projection + residual");
 }
 
 bool ffn_shapes_ok(const fortai_hip_q8_weights *g, const fortai_hip_q8_weights *u, const fortai_hip_q8_weights *d) {
@@ -478,6 +519,66 @@ int fortai_hip_q8_weights_upload(fortai_hip_q8_context *c, const void *host_weig
         release(w->scales);
         delete w;
         return fail(c, FORTAI_HIP_RUNTIME_ERROR, "weight upload", e);
+    }
+    w->m.quants = w->quants;
+    w->m.scales = w->scales;
+    *weights = w;
+    return FORTAI_HIP_OK;
+}
+
+// ------------------------------------------------- repacked-weight cache
+// The resident planes (quants, then scales) of a rows x width Q8_0 matrix,
+// as a weight-pack cache stores them (the reference keys its pack files by
+// model / backend / variant / ABI version, src/fortai_cache.f90:6-31).
+size_t fortai_hip_q8_pack_bytes(int rows, int width) {
+    if (rows <= 0 || width <= 0 || width % kQ8Block) return 0;
+    const size_t groups = static_cast<size_t>((rows + kRowsPerWave - 1) / kRowsPerWave) * ((width / kQ8Block + 3) / 4);
+    return groups * (64 * sizeof(uint4) + 8 * sizeof(uint2));
+}
+
+int fortai_hip_q8_weights_pack(const fortai_hip_q8_weights *w, void *host, size_t bytes) {
+    if (!w || !host || bytes < fortai_hip_q8_pack_bytes(w->m.rows, w->width)) return FORTAI_HIP_INVALID;
+    auto *c = w->context;
+    (void)hipSetDevice(c->device);
+    const size_t groups = static_cast<size_t>(w->m.row_groups) * w->m.chunks;
+    uint8_t *h = static_cast<uint8_t *>(host);
+    hipError_t e = hipMemcpyAsync(h, w->quants, groups * 64 * sizeof(uint4), hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(h + groups * 64 * sizeof(uint4), w->scales, groups * 8 * sizeof(uint2), hipMemcpyDeviceToHost,
+            c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "weight pack");
+}
+
+int fortai_hip_q8_weights_upload_packed(fortai_hip_q8_context *c, const void *host, size_t bytes, int rows, int width,
+    fortai_hip_q8_weights **weights) {
+    if (!c || !host || !weights || rows <= 0 || width <= 0 || width % kQ8Block ||
+        bytes < fortai_hip_q8_pack_bytes(rows, width))
+        return FORTAI_HIP_INVALID;
+    *weights = nullptr;
+    auto *w = new (std::nothrow) fortai_hip_q8_weights;
+    if (!w) return FORTAI_HIP_RUNTIME_ERROR;
+    w->context = c;
+    w->width = width;
+    w->m.rows = rows;
+    w->m.blocks = width / kQ8Block;
+    w->m.chunks = (w->m.blocks + 3) / 4;
+    w->m.row_groups = (rows + kRowsPerWave - 1) / kRowsPerWave;
+    (void)hipSetDevice(c->device);
+    const size_t groups = static_cast<size_t>(w->m.row_groups) * w->m.chunks;
+    const uint8_t *h = static_cast<const uint8_t *>(host);
+    hipError_t e = alloc(&w->quants, groups * 64);
+    if (e == hipSuccess) e = alloc(&w->scales, groups * 8);
+    if (e == hipSuccess) e = hipMemcpyAsync(w->quants, h, groups * 64 * sizeof(uint4), hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(w->scales, h + groups * 64 * sizeof(uint4), groups * 8 * sizeof(uint2), hipMemcpyHostToDevice,
+            c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        release(w->quants);
+        release(w->scales);
+        delete w;
+        return fail(c, FORTAI_HIP_RUNTIME_ERROR, "packed weight upload", e);
     }
     w->m.quants = w->quants;
     w->m.scales = w->scales;
@@ -1228,8 +1329,8 @@ namespace {
 hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream);
 hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     auto *c = d->context;
-    hipError_t e = d->emb16 ? launch_f16_embedding(d->emb16->data, d->hidden, c->token, 0, d->x, stream)
-                            : launch_q8_embedding(d->emb8->m, c->token, 0, d->x, stream);
+    hipError_t e = rec(d->emb16 ? launch_f16_embedding(d->emb16->data, d->hidden, c->token, 0, d->x, stream)
+                                : launch_q8_embedding(d->emb8->m, c->token, 0, d->x, stream), "token embedding");
     for (size_t i = 0; i < d->layers.size() && e == hipSuccess; ++i) {
         const decoder_layer &L = d->layers[i];
         MatvecInput in;
@@ -1259,24 +1360,32 @@ hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     st.trace_capacity = d->max_context;
     st.position = c->position;
     if (d->out16)
-        return launch_f16_matvec(d->out16->data, d->vocab, d->hidden, d->out16->finite, d->x, d->output_norm, d->eps,
-            d->logits, &st, stream);
+        return rec(launch_f16_matvec(d->out16->data, d->vocab, d->hidden, d->out16->finite, d->x, d->output_norm, d->eps,
+            d->logits, &st, stream), "output RMSNorm, LM head, greedy argmax");
     MatvecInput in;
     in.x = d->x;
     in.norm = d->output_norm;
     in.eps = d->eps;
     in.width = d->hidden;
     const MatvecSegment s = segment(d->out8, d->logits);
-    e = launch_q8_matvec(&s, 1, in, Prologue::RMSNORM, Epilogue::STORE, stream);
-    if (e == hipSuccess) e = launch_argmax(d->logits, d->vocab, st, stream);
+    e = rec(launch_q8_matvec(&s, 1, in, Prologue::RMSNORM, Epilogue::STORE, stream), "output RMSNorm, LM head");
+    if (e == hipSuccess) e = rec(launch_argmax(d->logits, d->vocab, st, stream), "greedy argmax");
     return e;
 }
 hipError_t run_step(fortai_hip_qwen35_decoder *d) {
+    // the plan is recorded by the first step (at capture for the graph)
+    std::vector<plan_step> *saved = g_plan;
+    if (d->plan.empty() && !d->use_graph) g_plan = &d->plan;
+    hipError_t e;
     if (d->persistent) {
-        hipError_t e = launch_decode_persistent(d->plan_dev, d->next_tag++, d->grid, d->context->stream);
-        return e == hipSuccess ? enqueue_lm_head(d, d->context->stream) : e;
+        e = rec(launch_decode_persistent(d->plan_dev, d->next_tag++, d->grid, d->context->stream),
+            "every layer in one persistent kernel");
+        if (e == hipSuccess) e = enqueue_lm_head(d, d->context->stream);
+    } else {
+        e = d->use_graph ? hipGraphLaunch(d->exec, d->context->stream) : enqueue_decoder_step(d, d->context->stream);
     }
-    return d->use_graph ? hipGraphLaunch(d->exec, d->context->stream) : enqueue_decoder_step(d, d->context->stream);
+    g_plan = saved;
+    return e;
 }
 // after a synchronisation: a failed persistent step (a bounded wait expired)
 // is reported once and cleared
@@ -1527,7 +1636,10 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     d->use_graph = !d->persistent && !(graph_env && std::strcmp(graph_env, "0") == 0);
     if (e == hipSuccess && d->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess && d->use_graph) {
+        g_plan = &d->plan;
+        g_plan_batch = 1;
         const hipError_t ce = enqueue_decoder_step(d, c->stream);
+        g_plan = nullptr;
         e = hipStreamEndCapture(c->stream, &d->graph);
         if (ce != hipSuccess) e = ce;
     }
@@ -1659,6 +1771,11 @@ int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *d) {
     return d ? (d->persistent ? 1 : 0) : -1;
 }
 
+int fortai_hip_qwen35_decoder_plan(const fortai_hip_qwen35_decoder *d, char *buffer, size_t bytes, size_t *needed) {
+    if (!d) return FORTAI_HIP_INVALID;
+    return copy_plan(d->plan, buffer, bytes, needed);
+}
+
 int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits) {
     if (!d || !logits) return FORTAI_HIP_INVALID;
     *logits = d->logits;
@@ -1669,8 +1786,8 @@ int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits
 namespace {
 hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
     const int B = b->batch, H = b->hidden;
-    hipError_t e = b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->tokens, 0, b->x, stream, B)
-                            : launch_q8_embedding(b->emb8->m, b->tokens, 0, b->x, stream, B);
+    hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->tokens, 0, b->x, stream, B)
+                                : launch_q8_embedding(b->emb8->m, b->tokens, 0, b->x, stream, B), "token embeddings");
     for (size_t i = 0; i < b->layers.size() && e == hipSuccess; ++i) {
         batch_layer &L = b->layers[i];
         MatvecInput in;
@@ -1678,7 +1795,7 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
         in.norm = L.attn_norm;
         in.eps = b->eps;
         in.width = H;
-        e = launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream);
+        e = rec(launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream), "attention-norm and quantize");
         if (e != hipSuccess) break;
         if (L.rec) {
             auto *R = L.rec;
@@ -1689,10 +1806,11 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
             segs[0].conv_size = R->conv_size;
             segs[0].kernel = R->kernel;
             segs[1].silu = true;
-            e = launch_q8_batch_matvec(segs, 4, b->act, H, B, Epilogue::STORE, stream);
+            e = rec(launch_q8_batch_matvec(segs, 4, b->act, H, B, Epilogue::STORE, stream),
+                "GDN qkv/gate/alpha/beta projections, conv1d + SiLU");
             GdnParams gp = gdn_params(R, L.qkv, L.alpha, L.beta, L.o_raw);
             gp.state = L.state;
-            if (e == hipSuccess) e = launch_gdn_delta(gp, stream, B);
+            if (e == hipSuccess) e = rec(launch_gdn_delta(gp, stream, B), "GDN L2 norms, decay/beta, delta rule");
             MatvecInput gated;
             gated.x = L.o_raw;
             gated.z = L.z;
@@ -1700,31 +1818,40 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
             gated.eps = R->eps;
             gated.head = R->head;
             gated.width = R->inner;
-            if (e == hipSuccess) e = launch_q8l_prep(gated, Prologue::GATED, b->act, B, stream);
+            if (e == hipSuccess)
+                e = rec(launch_q8l_prep(gated, Prologue::GATED, b->act, B, stream), "GDN gated RMSNorm and quantize");
             const MatvecSegment oseg = segment(R->out, b->x, b->x);
-            if (e == hipSuccess) e = launch_q8_batch_matvec(&oseg, 1, b->act, R->inner, B, Epilogue::ADD, stream);
+            if (e == hipSuccess)
+                e = rec(launch_q8_batch_matvec(&oseg, 1, b->act, R->inner, B, Epilogue::ADD, stream),
+                    "GDN ssm_out projection + residual");
         } else {
             auto *A = L.att;
             const MatvecSegment segs[3] = {segment(A->q, L.q), segment(A->k, L.k), segment(A->v, L.v)};
-            e = launch_q8_batch_matvec(segs, 3, b->act, H, B, Epilogue::STORE, stream);
+            e = rec(launch_q8_batch_matvec(segs, 3, b->act, H, B, Epilogue::STORE, stream), "attention q/k/v projections");
             AttentionParams ap = attention_params(A, L.q, L.k, L.v, L.attn_out);
             ap.kcache = L.kcache; ap.vcache = L.vcache; ap.partial = L.partial; ap.cache_flags = L.flags;
             ap.split = L.split; ap.position = b->positions; ap.max_context = b->max_context;
-            if (e == hipSuccess) e = launch_attention(ap, stream, B);
+            if (e == hipSuccess) e = rec(launch_attention(ap, stream, B), "q/k norm, RoPE, KV append, softmax.V, gate");
             MatvecInput oin;
             oin.x = L.attn_out;
             oin.width = A->heads * A->value;
-            if (e == hipSuccess) e = launch_q8l_prep(oin, Prologue::F32, b->act, B, stream);
+            if (e == hipSuccess) e = rec(launch_q8l_prep(oin, Prologue::F32, b->act, B, stream), "quantize attention output");
             const MatvecSegment oseg = segment(A->o, b->x, b->x);
-            if (e == hipSuccess) e = launch_q8_batch_matvec(&oseg, 1, b->act, oin.width, B, Epilogue::ADD, stream);
+            if (e == hipSuccess)
+                e = rec(launch_q8_batch_matvec(&oseg, 1, b->act, oin.width, B, Epilogue::ADD, stream),
+                    "attention o projection + residual");
         }
         if (e != hipSuccess) break;
         in.norm = L.post_norm;
-        e = launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream);
+        e = rec(launch_q8l_prep(in, Prologue::RMSNORM, b->act, B, stream), "FFN post-norm and quantize");
         const MatvecSegment pair = segment(L.gate, nullptr, nullptr, L.up, b->h_q8l);
-        if (e == hipSuccess) e = launch_q8_batch_matvec(&pair, 1, b->act, H, B, Epilogue::SILU_PAIR, stream);
+        if (e == hipSuccess)
+            e = rec(launch_q8_batch_matvec(&pair, 1, b->act, H, B, Epilogue::SILU_PAIR, stream),
+                "FFN gate/up projections, SiLU product");
         const MatvecSegment dseg = segment(L.down, b->x, b->x);
-        if (e == hipSuccess) e = launch_q8_batch_matvec(&dseg, 1, b->h_q8l, L.gate->m.rows, B, Epilogue::ADD, stream);
+        if (e == hipSuccess)
+            e = rec(launch_q8_batch_matvec(&dseg, 1, b->h_q8l, L.gate->m.rows, B, Epilogue::ADD, stream),
+                "FFN down projection + residual");
     }
     if (e != hipSuccess) return e;
     ArgmaxState st;
@@ -1735,8 +1862,8 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
     st.trace_capacity = b->max_context;
     st.position = b->positions;
     if (b->out16)
-        return launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm, b->eps,
-            b->logits, st, stream);
+        return rec(launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm,
+            b->eps, b->logits, st, stream), "output RMSNorm, LM head, greedy argmax");
     // Q8_0 LM head: the batched matvec, then the argmax of each sequence
     MatvecInput in;
     in.x = b->x;
@@ -1759,7 +1886,16 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
 }
 
 hipError_t batch_step(fortai_hip_qwen35_batch *b) {
-    return b->use_graph ? hipGraphLaunch(b->exec, b->context->stream) : enqueue_batch_step(b, b->context->stream);
+    if (b->use_graph) return hipGraphLaunch(b->exec, b->context->stream);
+    std::vector<plan_step> *saved = g_plan;
+    if (b->plan.empty()) {
+        g_plan = &b->plan;
+        g_plan_batch = b->batch;
+    }
+    const hipError_t e = enqueue_batch_step(b, b->context->stream);
+    g_plan = saved;
+    g_plan_batch = 1;
+    return e;
 }
 
 hipError_t batch_zero_state(fortai_hip_qwen35_batch *b, hipStream_t stream) {
@@ -1897,7 +2033,11 @@ int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *c, int batch, int laye
     b->use_graph = !(graph_env && std::strcmp(graph_env, "0") == 0);
     if (e == hipSuccess && b->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess && b->use_graph) {
+        g_plan = &b->plan;
+        g_plan_batch = batch;
         const hipError_t ce = enqueue_batch_step(b, c->stream);
+        g_plan = nullptr;
+        g_plan_batch = 1;
         e = hipStreamEndCapture(c->stream, &b->graph);
         if (ce != hipSuccess) e = ce;
     }
@@ -2063,10 +2203,10 @@ hipError_t batch_prefill_buffers(fortai_hip_qwen35_batch *b, int rows) {
 // time (the reference's lane order; for validating the prefill kernels)
 hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, hipStream_t stream) {
     const int B = b->batch, H = b->hidden, N = B * T;
-    hipError_t e = b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->ptokens, 0, b->px, stream, N)
-                            : launch_q8_embedding(b->emb8->m, b->ptokens, 0, b->px, stream, N);
-    auto mmq = [&](const fortai_hip_q8_weights *w, float *out, const float *resid) {
-        if (!exact) return launch_q8_mmq(w->m, b->px8, N, out, w->m.rows, resid, nullptr, stream);
+    hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->ptokens, 0, b->px, stream, N)
+                                : launch_q8_embedding(b->emb8->m, b->ptokens, 0, b->px, stream, N), "token embeddings");
+    auto mmq = [&](const fortai_hip_q8_weights *w, float *out, const float *resid, const char *op) {
+        if (!exact) return rec(launch_q8_mmq(w->m, b->px8, N, out, w->m.rows, resid, nullptr, stream), op);
         hipError_t r = hipSuccess;
         for (int r0 = 0; r0 < N && r == hipSuccess; r0 += 8) {
             const int cnt = std::min(8, N - r0);
@@ -2081,37 +2221,47 @@ hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, 
     };
     for (size_t i = 0; i < b->layers.size() && e == hipSuccess; ++i) {
         batch_layer &L = b->layers[i];
-        e = launch_rms_quantize_tokens(b->px, N, H, L.attn_norm, b->eps, b->px8, stream);
+        e = rec(launch_rms_quantize_tokens(b->px, N, H, L.attn_norm, b->eps, b->px8, stream), "attention-norm and quantize");
         if (L.rec) {
             const auto *R = L.rec;
-            if (e == hipSuccess) e = mmq(R->qkv, b->pa, nullptr);
-            if (e == hipSuccess) e = mmq(R->gate, b->pb, nullptr);
-            if (e == hipSuccess) e = mmq(R->alpha, b->palpha, nullptr);
-            if (e == hipSuccess) e = mmq(R->beta, b->pbeta, nullptr);
+            if (e == hipSuccess) e = mmq(R->qkv, b->pa, nullptr, "GDN qkv projection");
+            if (e == hipSuccess) e = mmq(R->gate, b->pb, nullptr, "GDN gate projection");
+            if (e == hipSuccess) e = mmq(R->alpha, b->palpha, nullptr, "GDN alpha projection");
+            if (e == hipSuccess) e = mmq(R->beta, b->pbeta, nullptr, "GDN beta projection");
             if (e == hipSuccess)
-                e = launch_conv_silu_tokens(b->pa, R->conv_w, L.conv_state, b->pc, B, T, R->conv_size, R->kernel, stream);
+                e = rec(launch_conv_silu_tokens(b->pa, R->conv_w, L.conv_state, b->pc, B, T, R->conv_size, R->kernel, stream),
+                    "GDN conv1d + SiLU over time");
             GdnParams gp = gdn_params(const_cast<fortai_hip_qwen35_recurrent *>(R), b->pc, b->palpha, b->pbeta, b->pd);
             gp.state = L.state;
-            if (e == hipSuccess) e = launch_gdn_prefill(gp, B, T, b->pqinv, b->pkinv, b->pbt, b->pdt, stream);
             if (e == hipSuccess)
-                e = launch_gated_quantize_tokens(b->pd, b->pb, R->ssm_norm, R->eps, N, R->inner, R->head, b->px8, stream);
-            if (e == hipSuccess) e = mmq(R->out, b->px, b->px);
+                e = rec(launch_gdn_prefill(gp, B, T, b->pqinv, b->pkinv, b->pbt, b->pdt, stream),
+                    "GDN L2 norms, decay/beta, delta rule over time");
+            if (e == hipSuccess)
+                e = rec(launch_gated_quantize_tokens(b->pd, b->pb, R->ssm_norm, R->eps, N, R->inner, R->head, b->px8, stream),
+                    "GDN gated RMSNorm and quantize");
+            if (e == hipSuccess) e = mmq(R->out, b->px, b->px, "GDN ssm_out projection + residual");
         } else {
             const auto *A = L.att;
-            if (e == hipSuccess) e = mmq(A->q, b->pa, nullptr);
-            if (e == hipSuccess) e = mmq(A->k, b->pb, nullptr);
-            if (e == hipSuccess) e = mmq(A->v, b->pc, nullptr);
+            if (e == hipSuccess) e = mmq(A->q, b->pa, nullptr, "attention q projection");
+            if (e == hipSuccess) e = mmq(A->k, b->pb, nullptr, "attention k projection");
+            if (e == hipSuccess) e = mmq(A->v, b->pc, nullptr, "attention v projection");
             AttentionParams ap = attention_params(const_cast<fortai_hip_qwen35_attention *>(A), b->pa, b->pb, b->pc, b->pd);
             ap.kcache = L.kcache; ap.vcache = L.vcache; ap.cache_flags = L.flags; ap.max_context = b->max_context;
-            if (e == hipSuccess) e = launch_attention_prefill(ap, B, T, b->pd, stream);
-            if (e == hipSuccess) e = launch_rms_quantize_tokens(b->pd, N, A->heads * A->value, nullptr, 0.0f, b->px8, stream);
-            if (e == hipSuccess) e = mmq(A->o, b->px, b->px);
+            if (e == hipSuccess)
+                e = rec(launch_attention_prefill(ap, B, T, b->pd, stream), "q/k norm, RoPE, KV append, causal attention");
+            if (e == hipSuccess)
+                e = rec(launch_rms_quantize_tokens(b->pd, N, A->heads * A->value, nullptr, 0.0f, b->px8, stream),
+                    "quantize attention output");
+            if (e == hipSuccess) e = mmq(A->o, b->px, b->px, "attention o projection + residual");
         }
-        if (e == hipSuccess) e = launch_rms_quantize_tokens(b->px, N, H, L.post_norm, b->eps, b->px8, stream);
-        if (e == hipSuccess) e = mmq(L.gate, b->pa, nullptr);
-        if (e == hipSuccess) e = mmq(L.up, b->pb, nullptr);
-        if (e == hipSuccess) e = launch_silu_product_quantize(b->pa, b->pb, N, L.gate->m.rows, b->px8, stream);
-        if (e == hipSuccess) e = mmq(L.down, b->px, b->px);
+        if (e == hipSuccess)
+            e = rec(launch_rms_quantize_tokens(b->px, N, H, L.post_norm, b->eps, b->px8, stream), "FFN post-norm and quantize");
+        if (e == hipSuccess) e = mmq(L.gate, b->pa, nullptr, "FFN gate projection");
+        if (e == hipSuccess) e = mmq(L.up, b->pb, nullptr, "FFN up projection");
+        if (e == hipSuccess)
+            e = rec(launch_silu_product_quantize(b->pa, b->pb, N, L.gate->m.rows, b->px8, stream),
+                "FFN SiLU product and quantize");
+        if (e == hipSuccess) e = mmq(L.down, b->px, b->px, "FFN down projection + residual");
     }
     if (e != hipSuccess) return e;
     // each sequence's last token -> x [batch][hidden]; the LM head then
@@ -2127,8 +2277,8 @@ hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, 
     st.trace_capacity = b->max_context;
     st.position = b->positions;
     if (b->out16)
-        return launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm, b->eps,
-            b->logits, st, stream);
+        return rec(launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm,
+            b->eps, b->logits, st, stream), "output RMSNorm, LM head, greedy argmax (last prompt tokens)");
     MatvecInput in;
     in.x = b->x;
     in.norm = b->output_norm;
@@ -2170,7 +2320,12 @@ int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *b, const int64_t *t
     // order (slow; validates the rest of the prefill against decoding)
     const char *exact_env = std::getenv("FORTAI_HIP_PREFILL_EXACT");
     const bool exact = exact_env && std::strcmp(exact_env, "1") == 0;
+    b->prefill_plan.clear();
+    g_plan = &b->prefill_plan;
+    g_plan_batch = static_cast<int>(N);
     if (e == hipSuccess) e = enqueue_batch_prefill(b, T, exact, c->stream);
+    g_plan = nullptr;
+    g_plan_batch = 1;
     if (e == hipSuccess && kernel_ms) e = hipEventRecord(c->stop, c->stream);
     if (e == hipSuccess && logits)
         e = hipMemcpyAsync(logits, b->logits, static_cast<size_t>(b->batch) * b->vocab * sizeof(float),
@@ -2181,6 +2336,12 @@ int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *b, const int64_t *t
     if (e == hipSuccess && kernel_ms) e = hipEventElapsedTime(kernel_ms, c->start, c->stop);
     b->next_positions.assign(b->batch, T);
     return done(c, e, "batch prefill");
+}
+
+int fortai_hip_qwen35_batch_plan(const fortai_hip_qwen35_batch *b, int prefill, char *buffer, size_t bytes,
+    size_t *needed) {
+    if (!b) return FORTAI_HIP_INVALID;
+    return copy_plan(prefill ? b->prefill_plan : b->plan, buffer, bytes, needed);
 }
 
 int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *b, void **logits) {

@@ -80,6 +80,13 @@ struct MatvecInput {
     int width = 0;                // activation elements (multiple of 32)
 };
 
+// Plan recording: every launcher notes the kernel variant it launched
+// (printf-style); last_launch() returns the note of this thread's last launch.
+void note_launch(const char *fmt, ...);
+const char *last_launch();
+const char *prologue_name(Prologue p);
+const char *epilogue_name(Epilogue e);
+
 // Evaluate up to four matrices that share one activation in one launch.
 hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const MatvecInput &in,
     Prologue prologue, Epilogue epilogue, hipStream_t stream);

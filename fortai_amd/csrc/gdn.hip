@@ -150,6 +150,7 @@ hipError_t launch_conv_silu(const float *x, const float *conv_w, float *conv_sta
     if (channels <= 0 || K < 2 || K > kConvMax) return hipErrorInvalidValue;
     hipLaunchKernelGGL(conv_silu_kernel, dim3((channels + 255) / 256), dim3(256), 0, stream, x, conv_w, conv_state, out,
         channels, K);
+    note_launch("conv_silu_kernel grid %d", (channels + 255) / 256);
     return hipGetLastError();
 }
 
@@ -162,6 +163,7 @@ hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream, int batch) {
     case 256: hipLaunchKernelGGL(gdn_delta_kernel<256>, grid, dim3(kDeltaThreads), 0, stream, p); break;
     default: return hipErrorInvalidValue;
     }
+    note_launch("gdn_delta_kernel<%d> grid %dx%d", p.head, grid.x, batch);
     return hipGetLastError();
 }
 

@@ -374,8 +374,15 @@ hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite
     else FORTAI_LM(false, false, false);
 #undef FORTAI_LM
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !argmax) return e;
-    return launch_argmax_finish(grid, st, stream);
+    if (e != hipSuccess || !argmax) {
+        note_launch("f16_matvec_kernel<rms=%d,argmax=0,finite=%d,tile=%d> grid %d", norm != nullptr, finite, wide ? 128 : 64,
+            grid);
+        return e;
+    }
+    e = launch_argmax_finish(grid, st, stream);
+    note_launch("f16_matvec_kernel<rms=%d,argmax=1,finite=%d,tile=%d> grid %d + argmax_finish_kernel", norm != nullptr,
+        finite, wide ? 128 : 64, grid);
+    return e;
 }
 
 int f16_batch_lm_head_workgroups(int rows) { return (rows + kBatchRows - 1) / kBatchRows; }
@@ -393,7 +400,9 @@ hipError_t launch_f16_batch_lm_head(const uint16_t *w, int rows, int width, bool
             batch, x, norm, eps, out, argmax);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_argmax_finish(grid, argmax, stream, batch);
+    e = launch_argmax_finish(grid, argmax, stream, batch);
+    note_launch("f16_batch_lm_head_kernel<finite=%d> grid %d + argmax_finish_kernel grid 1x%d", finite, grid, batch);
+    return e;
 }
 
 hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, hipStream_t stream) {
@@ -402,7 +411,9 @@ hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, h
     hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, stream, values, n, state);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    return launch_argmax_finish(grid, state, stream);
+    e = launch_argmax_finish(grid, state, stream);
+    note_launch("argmax_kernel grid %d + argmax_finish_kernel", grid);
+    return e;
 }
 
 hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream, int batch) {

@@ -289,6 +289,7 @@ hipError_t launch_q8_mmq(const Q8Matrix &w, const void *x8, int tokens, float *o
     else
         hipLaunchKernelGGL((q8_mmq_kernel<0, false>), grid, dim3(kMmqThreads), lds, stream, w, xq, xs, tokens, ld, out,
             ld_out, resid, dots);
+    note_launch("q8_mmq_kernel<%s> grid %dx%d", resid ? "add" : "store", grid.x, grid.y);
     return hipGetLastError();
 }
 

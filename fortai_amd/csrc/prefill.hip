@@ -422,6 +422,7 @@ hipError_t launch_x8_to_q8l(const void *x8, int tokens, int width, int r0, int c
     x8_planes(const_cast<void *>(x8), tokens, width, xq, xs, ld, bp);
     hipLaunchKernelGGL(x8_to_q8l_kernel, dim3(1, count), dim3(256), 0, stream, xq, xs, ld, bp / 4, r0,
         static_cast<uint32_t *>(q8l));
+    note_launch("x8_to_q8l_kernel grid 1x%d", count);
     return hipGetLastError();
 }
 
@@ -432,6 +433,7 @@ hipError_t launch_rms_quantize_tokens(const float *x, int rows, int width, const
     x8_planes(x8, rows, width, xq, xs, ld, bp);
     hipLaunchKernelGGL(rms_quantize_tokens_kernel, dim3(rows), dim3(kRowThreads), 0, stream, x, width, width, norm, eps,
         ld, bp, xq, xs);
+    note_launch("rms_quantize_tokens_kernel<%s> grid %d", norm ? "rmsnorm" : "f32", rows);
     return hipGetLastError();
 }
 
@@ -443,6 +445,7 @@ hipError_t launch_gated_quantize_tokens(const float *o, const float *z, const fl
     x8_planes(x8, rows, width, xq, xs, ld, bp);
     hipLaunchKernelGGL(gated_quantize_tokens_kernel, dim3(rows), dim3(kRowThreads), 0, stream, o, z, norm, eps, width,
         head, ld, bp, xq, xs);
+    note_launch("gated_quantize_tokens_kernel grid %d", rows);
     return hipGetLastError();
 }
 
@@ -453,6 +456,7 @@ hipError_t launch_silu_product_quantize(const float *gate, const float *up, int 
     x8_planes(x8, rows, width, xq, xs, ld, bp);
     hipLaunchKernelGGL(silu_product_quantize_kernel, dim3(rows), dim3(kRowThreads), 0, stream, gate, up, width, ld, bp,
         xq, xs);
+    note_launch("silu_product_quantize_kernel grid %d", rows);
     return hipGetLastError();
 }
 
@@ -461,6 +465,7 @@ hipError_t launch_conv_silu_tokens(const float *x, const float *conv_w, float *c
     if (batch < 1 || T < 1 || C < 1 || K < 2 || K > kConvMax) return hipErrorInvalidValue;
     hipLaunchKernelGGL(conv_silu_tokens_kernel, dim3((C + 255) / 256, batch), dim3(256), 0, stream, x, conv_w,
         conv_state, out, T, C, K);
+    note_launch("conv_silu_tokens_kernel grid %dx%d", (C + 255) / 256, batch);
     return hipGetLastError();
 }
 
@@ -486,6 +491,7 @@ hipError_t launch_gdn_prefill(const GdnParams &p, int batch, int T, float *qinv,
         break;
     default: return hipErrorInvalidValue;
     }
+    note_launch("gdn_token_prep_kernel grid %d + gdn_prefill_kernel<%d> grid %dx%d", rows, p.head, grid.x, batch);
     return hipGetLastError();
 }
 
@@ -514,6 +520,8 @@ hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, 
         break;
     default: return hipErrorInvalidValue;
     }
+    note_launch("qk_rope_append_kernel grid %d + attention_prefill_kernel<%d> grid %dx%dx%d", batch * T, p.head, grid.x,
+        grid.y, grid.z);
     return hipGetLastError();
 }
 

@@ -367,6 +367,8 @@ template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>
 hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES;
     hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI>), dim3(grid), dim3(WAVES * 64), lds, stream, args);
+    note_launch("q8_matvec_kernel<waves=%d,regs=%d,%s,%s> grid %d", WAVES, NREG, prologue_name(PRO), epilogue_name(EPI),
+        grid);
     return hipGetLastError();
 }
 
@@ -780,6 +782,7 @@ hipError_t launch_batch_g(const BatchMatvecArgs &args, int grid, size_t lds, hip
     case 2: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 2>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
     default: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 1>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
     }
+    note_launch("q8_batch_matvec_kernel<%s,split=%d,group=%d> grid %d", epilogue_name(EPI), SPLIT, g, grid);
     return hipGetLastError();
 }
 
@@ -992,6 +995,7 @@ hipError_t launch_q8l_prep(const MatvecInput &in, Prologue prologue, void *q8l, 
     }
     default: return hipErrorInvalidValue;
     }
+    note_launch("q8l_prep_kernel<%s> grid %d", prologue_name(prologue), batch);
     return hipGetLastError();
 }
 
@@ -1067,6 +1071,7 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
         else { FORTAI_RING_E(Epilogue::ADD) }
 #undef FORTAI_RING_E
 #undef FORTAI_RING
+        note_launch("q8_batch_ring_kernel<%s,groups=%d> grid %d", epilogue_name(epilogue), ring_groups, ring_grid);
         return hipGetLastError();
     }
     if (epilogue == Epilogue::SILU_PAIR) return launch_batch_g<Epilogue::SILU_PAIR, 1>(args, grid, lds, stream);
@@ -1113,6 +1118,7 @@ hipError_t launch_q8_embedding(const Q8Matrix &w, const int64_t *token, int64_t 
     if (batch < 1 || (batch > 1 && !token)) return hipErrorInvalidValue;
     const int n = w.blocks * kQ8Block;
     hipLaunchKernelGGL(q8_embedding_kernel, dim3((n + 255) / 256, batch), dim3(256), 0, stream, w, token, token_value, out);
+    note_launch("q8_embedding_kernel grid %dx%d", (n + 255) / 256, batch);
     return hipGetLastError();
 }
 
@@ -1121,6 +1127,7 @@ hipError_t launch_f16_embedding(const uint16_t *table, int width, const int64_t 
     if (batch < 1 || (batch > 1 && !token)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(f16_embedding_kernel, dim3((width + 255) / 256, batch), dim3(256), 0, stream, table, width, token,
         token_value, out);
+    note_launch("f16_embedding_kernel grid %dx%d", (width + 255) / 256, batch);
     return hipGetLastError();
 }
 

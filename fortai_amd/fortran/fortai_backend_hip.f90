@@ -87,6 +87,7 @@ module fortai_backend_hip
         procedure :: reset => decoder_reset
         procedure :: forward => decoder_forward
         procedure :: generate => decoder_generate
+        procedure :: plan => decoder_plan
     end type hip_qwen35_decoder_t
 
     ! Independent sequences (up to 8) over one set of layers and weights, with
@@ -394,6 +395,13 @@ module fortai_backend_hip
             import :: c_int, c_ptr
             type(c_ptr), value :: decoder, tokens, positions, trace
             integer(c_int), value :: steps
+        end function
+        integer(c_int) function fh_decoder_plan(decoder, buffer, bytes, needed) &
+                bind(C, name='fortai_hip_qwen35_decoder_plan')
+            import :: c_int, c_ptr, c_size_t
+            type(c_ptr), value :: decoder, buffer
+            integer(c_size_t), value :: bytes
+            integer(c_size_t), intent(out) :: needed
         end function
         integer(c_int) function c_strlen(s) bind(C, name='strlen')
             import :: c_int, c_ptr
@@ -1257,6 +1265,38 @@ contains
         call settle(fh_decoder_generate(self%handle, token, int(position, c_int), int(size(trace), c_int), &
             c_loc(trace)), self%context, 'Qwen decoder generation', stat)
     end subroutine decoder_generate
+
+    ! The launches of one step as text lines "operation<TAB>kernel<TAB>batch"
+    ! (new_line separated): the fields of the reference's plan_step_t
+    ! (src/fortai_plan_ir.f90:7-11), for plan_ir_t%append.
+    subroutine decoder_plan(self, text, stat)
+        class(hip_qwen35_decoder_t), intent(in) :: self
+        character(len=:), allocatable, intent(out) :: text
+        type(status_t), intent(out) :: stat
+        character(kind=c_char), allocatable, target :: buf(:)
+        integer(c_size_t) :: need
+        integer :: i
+        integer(c_int) :: code
+
+        call stat%clear()
+        text = ''
+        if (.not. live(self%handle)) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Qwen decoder')
+            return
+        end if
+        code = fh_decoder_plan(self%handle, c_null_ptr, 0_c_size_t, need)
+        if (code /= FORTAI_HIP_OK .or. need < 1) then
+            call settle(code, self%context, 'Qwen decoder plan', stat)
+            return
+        end if
+        allocate (buf(need))
+        call settle(fh_decoder_plan(self%handle, c_loc(buf), need, need), self%context, 'Qwen decoder plan', stat)
+        if (.not. stat%is_ok()) return
+        allocate (character(len=int(need) - 1) :: text)
+        do i = 1, int(need) - 1
+            text(i:i) = buf(i)
+        end do
+    end subroutine decoder_plan
 
     ! ---- batched decoder (independent sequences, prompt prefill) ------------------
 

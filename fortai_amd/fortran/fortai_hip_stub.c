@@ -693,3 +693,39 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batc
     (void)batch_decoder; (void)device_logits;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_plan(const fortai_hip_qwen35_decoder *decoder, char *buffer, size_t bytes,
+    size_t *needed)
+{
+    (void)decoder; (void)buffer; (void)bytes;
+    if (needed) *needed = 0;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_plan(const fortai_hip_qwen35_batch *batch_decoder, int prefill,
+    char *buffer, size_t bytes, size_t *needed)
+{
+    (void)batch_decoder; (void)prefill; (void)buffer; (void)bytes;
+    if (needed) *needed = 0;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK size_t fortai_hip_q8_pack_bytes(int rows, int width)
+{
+    (void)rows; (void)width;
+    return 0;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_q8_weights_pack(const fortai_hip_q8_weights *weights, void *host, size_t bytes)
+{
+    (void)weights; (void)host; (void)bytes;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_q8_weights_upload_packed(fortai_hip_q8_context *context, const void *host, size_t bytes,
+    int rows, int width, fortai_hip_q8_weights **weights)
+{
+    (void)context; (void)host; (void)bytes; (void)rows; (void)width;
+    if (weights) *weights = NULL;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}

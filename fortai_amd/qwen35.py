@@ -81,15 +81,34 @@ def read_dims(f: gguf.GGUFFile) -> Qwen35Dims:
 
 
 class Qwen35Hip:
-    def __init__(self, path: str, max_context: int = 256, device: int = 0, fused: bool = True, batch: int = 0):
+    def __init__(self, path: str, max_context: int = 256, device: int = 0, fused: bool = True, batch: int = 0,
+                 pack_cache: Optional[str] = None):
+        """pack_cache: root of a repacked-weight cache (fortai_amd.pack_cache);
+        the Q8_0 matrices are uploaded from it when it holds this GGUF's pack,
+        and the pack is written after a repacking upload otherwise."""
         self.file = gguf.read(path)
         self.d = d = read_dims(self.file)
         self.max_context = max_context
         self.ctx = B.Context(device)
         self.q8: Dict[str, B.Q8Weights] = {}
+        packed = None
+        self.pack_path = None
+        self.loaded_from_pack = False
+        if pack_cache:
+            from . import pack_cache as pc
+            digest = pc.gguf_digest(path)
+            self.pack_path = pc.cache_path(pack_cache, pc.model_key(path))
+            packed = pc.read(self.pack_path, digest)
         for t in self.file.tensors:
             if t.ggml_type == gguf.GGML_TYPE_Q8_0 and len(t.shape) == 2:
-                self.q8[t.name] = B.Q8Weights(self.ctx, t.data, t.rows, t.width)
+                rec = packed.get(t.name) if packed else None
+                if rec is not None and rec[0] == t.rows and rec[1] == t.width:
+                    self.q8[t.name] = B.Q8Weights.from_packed(self.ctx, rec[2], t.rows, t.width)
+                else:
+                    self.q8[t.name] = B.Q8Weights(self.ctx, t.data, t.rows, t.width)
+        self.loaded_from_pack = bool(packed) and len(packed) == len(self.q8)
+        if pack_cache and not self.loaded_from_pack:
+            pc.write(self.pack_path, digest, {n: (w.rows, w.width, w.pack()) for n, w in self.q8.items()})
         emb = self.file.tensor("token_embd.weight")
         out = self.file.tensor("output.weight") or emb
         self.f16: Dict[str, B.F16Weights] = {}

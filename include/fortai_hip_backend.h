@@ -201,6 +201,18 @@ int fortai_hip_qwen35_embedding_f16_device(fortai_hip_q8_context *context,
 int fortai_hip_argmax_device(fortai_hip_q8_context *context,
     const void *device_values, size_t elements, void *device_token);
 
+/* Repacked-weight cache.  A Q8_0 matrix is repacked at upload into this
+ * backend's resident layout; these let a host cache those planes and skip
+ * the repack next time (the reference keys its pack files by model /
+ * backend / variant / ABI version, src/fortai_cache.f90:6-31).
+ * pack_bytes: size of the planes of a rows x width matrix (0 if invalid);
+ * weights_pack: copy a resident matrix's planes to host memory (synchronous);
+ * weights_upload_packed: create a resident matrix from such planes. */
+size_t fortai_hip_q8_pack_bytes(int rows, int width);
+int fortai_hip_q8_weights_pack(const fortai_hip_q8_weights *weights, void *host, size_t bytes);
+int fortai_hip_q8_weights_upload_packed(fortai_hip_q8_context *context, const void *host, size_t bytes, int rows,
+    int width, fortai_hip_q8_weights **weights);
+
 /* Parity probes: fortai_q8_quantize on device (GGUF block bytes + fp32
  * scales), and the exact int32 dot of every (row, block) [rows][width/32]. */
 int fortai_hip_q8_quantize_device(fortai_hip_q8_context *context,
@@ -311,6 +323,14 @@ int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *decode
  * slots = 6 * layers + 2 (embed, 6 per layer, one unused) */
 int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *decoder, uint64_t *host_times,
     size_t count);
+/* The kernels one decode step launches, as the reference's PlanIR steps
+ * (src/fortai_plan_ir.f90:7-21: operation, kernel, batch size), recorded when
+ * the step was captured (or by the first step): text lines
+ * "operation<TAB>kernel<TAB>batch<LF>", NUL-terminated.  *needed (may be NULL)
+ * receives the size including the NUL; buffer may be NULL to query it;
+ * INVALID when bytes is too small. */
+int fortai_hip_qwen35_decoder_plan(const fortai_hip_qwen35_decoder *decoder, char *buffer, size_t bytes,
+    size_t *needed);
 /* device pointer of the decoder's logits [vocab] */
 int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits);
 
@@ -359,6 +379,10 @@ int fortai_hip_qwen35_batch_replay(fortai_hip_qwen35_batch *batch_decoder, int s
  * (event-timed prefill) may be NULL. */
 int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *batch_decoder, const int64_t *tokens, int T,
     int64_t *next_tokens, float *host_logits, float *kernel_ms);
+/* As fortai_hip_qwen35_decoder_plan: the launches of one batched step
+ * (prefill == 0) or of the last prefill (prefill != 0). */
+int fortai_hip_qwen35_batch_plan(const fortai_hip_qwen35_batch *batch_decoder, int prefill, char *buffer,
+    size_t bytes, size_t *needed);
 /* device pointer of the logits [batch][vocab] */
 int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batch_decoder, void **device_logits);
 

@@ -168,3 +168,26 @@ def test_weak_stub_covers_the_header(tmp_path):
     assert lib.fortai_hip_q8_context_create(0, ctypes.byref(h)) == 2
     lib.fortai_hip_q8_last_error.restype = ctypes.c_char_p
     assert b"without the HIP backend" in lib.fortai_hip_q8_last_error(None)
+
+
+def test_pack_key_and_cache_path(tmp_path):
+    """pack_key_t / cache_path as src/fortai_cache.f90:6-43 defines them, and
+    the pack file round trip (records, digest check)."""
+    import numpy as np
+    from fortai_amd import pack_cache as pc
+    key = pc.PackKey(model="qwen35-0.8b", backend="hip-gfx950", variant="q8-lanes", abi_version=3)
+    assert key.is_valid()
+    assert pc.cache_path("/cache", key) == "/cache/qwen35-0.8b/hip-gfx950-q8-lanes-abi3.pack"
+    for bad in (pc.PackKey(), pc.PackKey("m", "b", " ", 1), pc.PackKey("m", "b", "v", 0)):
+        assert not bad.is_valid()
+        assert pc.cache_path("/cache", bad) == "/cache/invalid.pack"
+    recs = {"blk.0.ffn_up.weight": (3, 64, np.arange(200, dtype=np.uint8)),
+            "output.weight": (9, 32, np.zeros(7, dtype=np.uint8))}
+    path = str(tmp_path / "m" / "p.pack")
+    pc.write(path, b"d" * 32, recs)
+    got = pc.read(path, b"d" * 32)
+    assert set(got) == set(recs)
+    for n, (r, w, a) in recs.items():
+        assert got[n][0] == r and got[n][1] == w and np.array_equal(got[n][2], a)
+    assert pc.read(path, b"e" * 32) is None          # made from another GGUF
+    assert pc.read(str(tmp_path / "none.pack"), b"d" * 32) is None
