@@ -720,7 +720,7 @@ int fortai_hip_qwen35_embedding_f16_device(fortai_hip_q8_context *c, const forta
         output_elements < static_cast<size_t>(w->width))
         return FORTAI_HIP_INVALID;
     (void)hipSetDevice(c->device);
-    return done(c, launch_f16_embedding(w->data, w->width, nullptr, token_id, static_cast<float *>(device_output),
+    return done(c, launch_f16_embedding(w->data, w->rows, w->width, nullptr, token_id, static_cast<float *>(device_output),
         c->stream), "device F16 embedding");
 }
 
@@ -1329,7 +1329,7 @@ namespace {
 hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream);
 hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     auto *c = d->context;
-    hipError_t e = rec(d->emb16 ? launch_f16_embedding(d->emb16->data, d->hidden, c->token, 0, d->x, stream)
+    hipError_t e = rec(d->emb16 ? launch_f16_embedding(d->emb16->data, d->emb16->rows, d->hidden, c->token, 0, d->x, stream)
                                 : launch_q8_embedding(d->emb8->m, c->token, 0, d->x, stream), "token embedding");
     for (size_t i = 0; i < d->layers.size() && e == hipSuccess; ++i) {
         const decoder_layer &L = d->layers[i];
@@ -1786,7 +1786,7 @@ int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits
 namespace {
 hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
     const int B = b->batch, H = b->hidden;
-    hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->tokens, 0, b->x, stream, B)
+    hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, b->emb16->rows, H, b->tokens, 0, b->x, stream, B)
                                 : launch_q8_embedding(b->emb8->m, b->tokens, 0, b->x, stream, B), "token embeddings");
     for (size_t i = 0; i < b->layers.size() && e == hipSuccess; ++i) {
         batch_layer &L = b->layers[i];
@@ -1923,10 +1923,14 @@ hipError_t batch_zero_state(fortai_hip_qwen35_batch *b, hipStream_t stream) {
 
 int batch_set_inputs(fortai_hip_qwen35_batch *b, const int64_t *tokens, const int *positions, int steps) {
     const int rows = b->emb16 ? b->emb16->rows : b->emb8->m.rows;
-    for (int q = 0; q < b->batch; ++q)
-        if (tokens[q] < 0 || tokens[q] >= rows || positions[q] < 0 || positions[q] + steps > b->max_context)
-            return FORTAI_HIP_INVALID;
     auto *c = b->context;
+    for (int q = 0; q < b->batch; ++q)
+        if (tokens[q] < 0 || tokens[q] >= rows || positions[q] < 0 || positions[q] + steps > b->max_context) {
+            std::snprintf(c->error, sizeof(c->error), "batch inputs: sequence %d token %lld position %d steps %d "
+                "outside vocabulary %d / context %d", q, static_cast<long long>(tokens[q]), positions[q], steps,
+                rows, b->max_context);
+            return FORTAI_HIP_INVALID;
+        }
     hipError_t e = hipMemcpyAsync(b->tokens, tokens, b->batch * sizeof(int64_t), hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(b->positions, positions, b->batch * sizeof(int), hipMemcpyHostToDevice, c->stream);
     // the host arrays are borrowed for the call only
@@ -2203,7 +2207,7 @@ hipError_t batch_prefill_buffers(fortai_hip_qwen35_batch *b, int rows) {
 // time (the reference's lane order; for validating the prefill kernels)
 hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, hipStream_t stream) {
     const int B = b->batch, H = b->hidden, N = B * T;
-    hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, H, b->ptokens, 0, b->px, stream, N)
+    hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, b->emb16->rows, H, b->ptokens, 0, b->px, stream, N)
                                 : launch_q8_embedding(b->emb8->m, b->ptokens, 0, b->px, stream, N), "token embeddings");
     auto mmq = [&](const fortai_hip_q8_weights *w, float *out, const float *resid, const char *op) {
         if (!exact) return rec(launch_q8_mmq(w->m, b->px8, N, out, w->m.rows, resid, nullptr, stream), op);

@@ -242,7 +242,10 @@ __device__ __forceinline__ uint32_t quantize_group(float4 y, float &scale_out, u
 
 // One 16-byte Q8L chunk (4 blocks) of a row lane: the reference's per-block
 // acc = fma(f32(w_scale) * a_scale, (float)dot4(w, a), acc), block by block.
-// sum of the four int8 products of a and b
+// sum of the four int8 products of a and b.  Kept on the builtin: the
+// compiler then knows the result comes from a DOT instruction and pads the
+// DOT-write -> other-VALU-read hazard (three wait states on gfx950), which
+// it cannot do for an inline-asm dot.
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), 0, false);
 }

@@ -115,7 +115,7 @@ hipError_t launch_q8_block_dots(const Q8Matrix &w, const int8_t *xq34, int32_t *
 // batch > 1 (device tokens only): token[s] -> out + s * width
 hipError_t launch_q8_embedding(const Q8Matrix &w, const int64_t *token, int64_t token_value, float *out,
     hipStream_t stream, int batch = 1);
-hipError_t launch_f16_embedding(const uint16_t *table, int width, const int64_t *token,
+hipError_t launch_f16_embedding(const uint16_t *table, int rows, int width, const int64_t *token,
     int64_t token_value, float *out, hipStream_t stream, int batch = 1);
 hipError_t launch_add(const float *a, const float *b, float *out, int n, hipStream_t stream);
 hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, float eps,

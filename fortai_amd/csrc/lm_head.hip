@@ -65,7 +65,9 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(int partials, Argmax
         if (better(st.partial_value[w], st.partial_index[w], bv, bi)) { bv = st.partial_value[w]; bi = st.partial_index[w]; }
     block_argmax(bv, bi, sv, si);
     if (tid == 0) {
-        const int64_t token = bi;
+        // no candidate (every logit NaN): the first index, as maxloc over
+        // comparisons that all fail; never an id outside the vocabulary
+        const int64_t token = bi == 0x7fffffff ? 0 : bi;
         *st.token = token;
         if (st.position) {
             const int p = *st.position;

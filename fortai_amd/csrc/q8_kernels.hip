@@ -27,6 +27,8 @@
 #include "fortai_hip_internal.h"
 #include "fortai_hip_kernels.h"
 
+#include <algorithm>
+
 #ifndef FORTAI_MV_MARK
 #define FORTAI_MV_MARK(i)
 #endif
@@ -454,8 +456,10 @@ __device__ __forceinline__ void scales_f(uint2 sc, float (&ws)[4]) {
 // stream in groups of G chunks (G divides the chunk count), two groups in
 // flight while one is consumed.  Every load is unconditional (clamped), so
 // the compiler's in-order load counters never wait for a prefetch.
-template <Epilogue EPI, int SPLIT, int G>
-__global__ __launch_bounds__(kBatchThreads, 2) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
+// CH > 0: exactly CH chunks, the group loop fully unrolled (a rolled loop
+// makes the compiler wait for every prefetch at its head); CH == 0: any count.
+template <Epilogue EPI, int SPLIT, int G, int WAVES, int CH>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES / 2))) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
     constexpr int NS = kMaxBatch / SPLIT;
     extern __shared__ __align__(16) unsigned char lds[];
@@ -470,7 +474,7 @@ __global__ __launch_bounds__(kBatchThreads, 2) void q8_batch_matvec_kernel(const
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63, wave = tid >> 6;
     const int slot = wave / SPLIT, sub = wave % SPLIT;
-    const int rg = (wg - args.first_wg[sgi]) * (4 / SPLIT) + slot;
+    const int rg = (wg - args.first_wg[sgi]) * (WAVES / SPLIT) + slot;
     const bool active = rg < seg.w.row_groups;
     const int rgc = active ? rg : seg.w.row_groups - 1;
     const int r = lane >> 3, l = lane & 7;
@@ -505,7 +509,7 @@ __global__ __launch_bounds__(kBatchThreads, 2) void q8_batch_matvec_kernel(const
         const int pieces = args.batch * seq_bytes / 16;
         const int blocks = act_bytes / 1024;
         const u32x4_t *src = static_cast<const u32x4_t *>(args.act);
-        for (int b = wave; b < blocks; b += 4)
+        for (int b = wave; b < blocks; b += WAVES)
             __builtin_amdgcn_global_load_lds(src + min(b * 64 + lane, pieces - 1),
                 reinterpret_cast<u32x4_t *>(lds) + b * 64, 16, 0, 0);
     }
@@ -572,16 +576,34 @@ __global__ __launch_bounds__(kBatchThreads, 2) void q8_batch_matvec_kernel(const
             }
         }
     };
-    for (int c0 = 0;; c0 += 3 * G) {
-        fetch(c0 + 2 * G, qc, sc_, qc2, sc2_);
-        consume(c0, qa, sa, qa2, sa2);
-        if (c0 + G >= chunks) break;
-        fetch(c0 + 3 * G, qa, sa, qa2, sa2);
-        consume(c0 + G, qb, sb, qb2, sb2);
-        if (c0 + 2 * G >= chunks) break;
-        fetch(c0 + 4 * G, qb, sb, qb2, sb2);
-        consume(c0 + 2 * G, qc, sc_, qc2, sc2_);
-        if (c0 + 3 * G >= chunks) break;
+    if constexpr (CH > 0) {
+        constexpr int NG = CH / G;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+            // folded after unrolling: group gi in buffer gi % 3, group gi + 2 fetched
+            if (gi % 3 == 0) {
+                if (gi + 2 < NG) fetch((gi + 2) * G, qc, sc_, qc2, sc2_);
+                consume(gi * G, qa, sa, qa2, sa2);
+            } else if (gi % 3 == 1) {
+                if (gi + 2 < NG) fetch((gi + 2) * G, qa, sa, qa2, sa2);
+                consume(gi * G, qb, sb, qb2, sb2);
+            } else {
+                if (gi + 2 < NG) fetch((gi + 2) * G, qb, sb, qb2, sb2);
+                consume(gi * G, qc, sc_, qc2, sc2_);
+            }
+        }
+    } else {
+        for (int c0 = 0;; c0 += 3 * G) {
+            fetch(c0 + 2 * G, qc, sc_, qc2, sc2_);
+            consume(c0, qa, sa, qa2, sa2);
+            if (c0 + G >= chunks) break;
+            fetch(c0 + 3 * G, qa, sa, qa2, sa2);
+            consume(c0 + G, qb, sb, qb2, sb2);
+            if (c0 + 2 * G >= chunks) break;
+            fetch(c0 + 4 * G, qb, sb, qb2, sb2);
+            consume(c0 + 2 * G, qc, sc_, qc2, sc2_);
+            if (c0 + 3 * G >= chunks) break;
+        }
     }
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
@@ -609,13 +631,13 @@ __global__ __launch_bounds__(kBatchThreads, 2) void q8_batch_matvec_kernel(const
             const float h = row < args.pair_vector_rows ? silu_poly(acc[k]) * acc2[k]
                                                         : acc[k] / (1.0f + exp_rounded(-acc[k])) * acc2[k];
             if (writer && mine && out) out[row] = h;
-            if (seg.out_q8l && l == 0 && mine) epi[sq[k] * 32 + wave * 8 + r] = h;
+            if (seg.out_q8l && l == 0 && mine) epi[sq[k] * 32 + slot * 8 + r] = h;
         }
     }
     if constexpr (kPair) {
         if (seg.out_q8l) {
-            // SPLIT == 1: the workgroup's 32 rows form one quantization block of
-            // every sequence's h
+            // WAVES / SPLIT == 4: the workgroup's 32 rows form one quantization
+            // block of every sequence's h
             __syncthreads();
             const int t = tid & 7, q = tid >> 3;
             if (q < args.batch) {
@@ -648,14 +670,16 @@ constexpr int kRingG = 4;  // chunks per ring group
 // in flight per wave; just before a group is consumed the four waves put it
 // into one of two LDS slots and, after one barrier, all read it from there.
 // Per (row, sequence) the chain is the single-sequence kernel's.
-template <Epilogue EPI, int GROUPS>
+template <Epilogue EPI, int GROUPS, int NS>
 __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const BatchMatvecArgs args) {
-    constexpr int NS = 2;
     constexpr int R = GROUPS < 8 ? GROUPS : 8;  // groups in flight per wave
     constexpr int kSlot = kRingG * 1024 + kRingG * 64;  // quants then scales of one group
     extern __shared__ __align__(16) unsigned char lds[];
     const int seq_bytes = args.chunks * 144;
-    const int act_bytes = (args.batch * seq_bytes + 1023) / 1024 * 1024;
+    // this workgroup's block of 4 NS sequences (blockIdx.y)
+    const int base = static_cast<int>(blockIdx.y) * 4 * NS;
+    const int nseq = min(4 * NS, args.batch - base);
+    const int act_bytes = (nseq * seq_bytes + 1023) / 1024 * 1024;
     unsigned char *slots = lds + act_bytes;  // [2][kSlot]
 
     const int wg = static_cast<int>(blockIdx.x);
@@ -669,9 +693,9 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
     constexpr int chunks = GROUPS * kRingG, groups = GROUPS;
     const u32x4_t *qsrc = reinterpret_cast<const u32x4_t *>(seg.w.quants) + static_cast<size_t>(rg) * chunks * 64;
     const uint32_t *ssrc = reinterpret_cast<const uint32_t *>(seg.w.scales) + static_cast<size_t>(rg) * chunks * 16;
-    int sq[NS];
+    int sq[NS];  // sequences of this wave (clamped to the batch)
 #pragma unroll
-    for (int k = 0; k < NS; ++k) sq[k] = min(wave + 4 * k, args.batch - 1);
+    for (int k = 0; k < NS; ++k) sq[k] = min(base + wave + 4 * k, args.batch - 1);
 
     u32x4_t rq[R];
     uint32_t rs[R];
@@ -684,9 +708,9 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
 #pragma unroll
     for (int g = 0; g < R; ++g) fetch(g, rq[g], rs[g]);
     {
-        const int pieces = args.batch * seq_bytes / 16;
+        const int pieces = nseq * seq_bytes / 16;
         const int blocks = act_bytes / 1024;
-        const u32x4_t *src = static_cast<const u32x4_t *>(args.act);
+        const u32x4_t *src = static_cast<const u32x4_t *>(args.act) + static_cast<size_t>(base) * seq_bytes / 16;
         for (int b = wave; b < blocks; b += 4)
             __builtin_amdgcn_global_load_lds(src + min(b * 64 + lane, pieces - 1),
                 reinterpret_cast<u32x4_t *>(lds) + b * 64, 16, 0, 0);
@@ -733,7 +757,7 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
             scales_f(sc, ws);
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
-                const unsigned char *sbase = lds + static_cast<size_t>(sq[k]) * seq_bytes;
+                const unsigned char *sbase = lds + static_cast<size_t>(sq[k] - base) * seq_bytes;
                 const uint4 a = reinterpret_cast<const uint4 *>(sbase)[c * 8 + l];
                 const float4 as = reinterpret_cast<const float4 *>(sbase + static_cast<size_t>(args.chunks) * 128)[c];
                 acc[k] = dot_chunk_f(qq, ws, a, as, acc[k]);
@@ -751,7 +775,7 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
     for (int k = 0; k < NS; ++k) acc[k] = row_hsum8(acc[k]);
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-        const bool mine = wave + 4 * k < args.batch;
+        const bool mine = base + wave + 4 * k < args.batch;
         if (!(writer && mine)) continue;
         float *out = seg.out + static_cast<size_t>(sq[k]) * seg.w.rows;
         if constexpr (EPI == Epilogue::STORE) {
@@ -771,18 +795,35 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
     }
 }
 
-template <Epilogue EPI, int SPLIT>
+template <Epilogue EPI, int SPLIT, int WAVES = 4>
 hipError_t launch_batch_g(const BatchMatvecArgs &args, int grid, size_t lds, hipStream_t stream) {
     // groups of at most 4 chunks (with three groups in registers, larger
     // groups exceed the register budget of two workgroups per CU)
     const int c = args.chunks;
-    const int g = c % 4 == 0 ? 4 : (c % 2 == 0 ? 2 : 1);
-    switch (g) {
-    case 4: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 4>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
-    case 2: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 2>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
-    default: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 1>), dim3(grid), dim3(kBatchThreads), lds, stream, args); break;
+    // eight-wave workgroups run two per CU with single-chunk groups (larger
+    // groups exceed that register budget)
+    const int g = WAVES == 8 ? 1 : (c % 4 == 0 ? 4 : (c % 2 == 0 ? 2 : 1));
+    if constexpr (WAVES == 8) {
+        // the widths of the supported shapes unrolled exactly
+#define FORTAI_PAIR(CHN) hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 1, WAVES, CHN>), dim3(grid), \
+        dim3(WAVES * 64), lds, stream, args)
+        switch (c) {
+        case 2: FORTAI_PAIR(2); break;
+        case 8: FORTAI_PAIR(8); break;
+        case 20: FORTAI_PAIR(20); break;
+        case 32: FORTAI_PAIR(32); break;
+        default: FORTAI_PAIR(0); break;
+        }
+#undef FORTAI_PAIR
+    } else {
+        switch (g) {
+        case 4: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 4, WAVES, 0>), dim3(grid), dim3(WAVES * 64), lds, stream, args); break;
+        case 2: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 2, WAVES, 0>), dim3(grid), dim3(WAVES * 64), lds, stream, args); break;
+        default: hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 1, WAVES, 0>), dim3(grid), dim3(WAVES * 64), lds, stream, args); break;
+        }
     }
-    note_launch("q8_batch_matvec_kernel<%s,split=%d,group=%d> grid %d", epilogue_name(EPI), SPLIT, g, grid);
+    note_launch("q8_batch_matvec_kernel<%s,split=%d,group=%d,waves=%d> grid %d", epilogue_name(EPI), SPLIT, g, WAVES,
+        grid);
     return hipGetLastError();
 }
 
@@ -853,10 +894,10 @@ __global__ void q8_block_dots_kernel(Q8Matrix w, const int8_t *xq, int32_t *out,
     for (int c = 0; c < w.chunks; ++c) {
         const uint4 q = qp[static_cast<size_t>(c) * 64];
         const uint4 a = act4[c * 8 + l];
-        int d[4] = {__builtin_amdgcn_sdot4(static_cast<int>(q.x), static_cast<int>(a.x), 0, false),
-            __builtin_amdgcn_sdot4(static_cast<int>(q.y), static_cast<int>(a.y), 0, false),
-            __builtin_amdgcn_sdot4(static_cast<int>(q.z), static_cast<int>(a.z), 0, false),
-            __builtin_amdgcn_sdot4(static_cast<int>(q.w), static_cast<int>(a.w), 0, false)};
+        int d[4] = {sdot4(q.x, a.x),
+            sdot4(q.y, a.y),
+            sdot4(q.z, a.z),
+            sdot4(q.w, a.w)};
         for (int j = 0; j < 4; ++j) {
             int v = d[j];
             v += __shfl_xor(v, 4);
@@ -873,7 +914,8 @@ __global__ void q8_embedding_kernel(Q8Matrix w, const int64_t *token, int64_t to
     if (i >= w.blocks * kQ8Block) return;
     const int seq = static_cast<int>(blockIdx.y);  // batch: token[seq] -> row seq of out
     out += static_cast<size_t>(seq) * w.blocks * kQ8Block;
-    const int64_t t = token ? token[seq] : token_value;
+    int64_t t = token ? token[seq] : token_value;
+    if (t < 0 || t >= w.rows) t = 0;  // a device-fed id is never trusted as an address
     const int g = static_cast<int>(t >> 3), r = static_cast<int>(t & 7);
     const int b = i / kQ8Block, within = i % kQ8Block, l = within >> 2, byte = within & 3;
     const int c = b >> 2, j = b & 3;
@@ -885,13 +927,14 @@ __global__ void q8_embedding_kernel(Q8Matrix w, const int64_t *token, int64_t to
     out[i] = half_bits_to_float(sb) * static_cast<float>(q);
 }
 
-__global__ void f16_embedding_kernel(const uint16_t *table, int width, const int64_t *token,
+__global__ void f16_embedding_kernel(const uint16_t *table, int rows, int width, const int64_t *token,
     int64_t token_value, float *out) {
     const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= width) return;
     const int seq = static_cast<int>(blockIdx.y);  // batch: token[seq] -> row seq of out
     out += static_cast<size_t>(seq) * width;
-    const int64_t t = token ? token[seq] : token_value;
+    int64_t t = token ? token[seq] : token_value;
+    if (t < 0 || t >= rows) t = 0;  // a device-fed id is never trusted as an address
     out[i] = gguf_half_to_real(table[t * width + i]);
 }
 
@@ -1019,7 +1062,9 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
     int split = total_groups >= 1024 ? 1 : (total_groups >= 512 ? 2 : 4);
     if (epilogue == Epilogue::SILU_PAIR) {
         if (count != 1 || (segments[0].out_q8l && segments[0].w.rows % kQ8Block)) return hipErrorInvalidValue;
-        split = 1;  // one workgroup = 32 rows of every sequence (one quantization block of h)
+        // one workgroup = 32 rows of every sequence (one quantization block of
+        // h): eight waves, two per row group with four sequences each
+        split = 2;
     }
     BatchMatvecArgs args{};
     args.count = count;
@@ -1028,7 +1073,7 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
     args.split = split;
     args.act = q8l;
     int grid = 0;
-    const int per_wg = 4 / split;
+    const int per_wg = epilogue == Epilogue::SILU_PAIR ? 4 : 4 / split;
     for (int s = 0; s < count; ++s) {
         args.seg[s] = segments[s];
         args.first_wg[s] = grid;
@@ -1053,10 +1098,22 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
         }
         args.first_wg[count] = ring_grid;
         constexpr size_t kSlot = kRingG * 1024 + kRingG * 64;
-        const size_t ring_lds = act + 2 * kSlot;
+        // two sequences per wave, or one when eight sequences' activations
+        // would keep the workgroup at one per CU
+        const int ns = static_cast<size_t>(std::min(batch, 8)) * chunks * 144 > 48 * 1024 ? 1 : 2;
+        const int per_block = 4 * ns, seq_blocks = (batch + per_block - 1) / per_block;
+        const size_t ring_lds =
+            (static_cast<size_t>(std::min(batch, per_block)) * chunks * 144 + 1023) / 1024 * 1024 + 2 * kSlot;
         if (ring_lds > 160 * 1024) return hipErrorInvalidValue;
-#define FORTAI_RING(E, G) hipLaunchKernelGGL((q8_batch_ring_kernel<E, G>), dim3(ring_grid), dim3(kBatchThreads), \
-        ring_lds, stream, args)
+#define FORTAI_RING(E, G)                                                                                          \
+    do {                                                                                                          \
+        if (ns == 1)                                                                                              \
+            hipLaunchKernelGGL((q8_batch_ring_kernel<E, G, 1>), dim3(ring_grid, seq_blocks), dim3(kBatchThreads), \
+                ring_lds, stream, args);                                                                          \
+        else                                                                                                      \
+            hipLaunchKernelGGL((q8_batch_ring_kernel<E, G, 2>), dim3(ring_grid, seq_blocks), dim3(kBatchThreads), \
+                ring_lds, stream, args);                                                                          \
+    } while (0)
 #define FORTAI_RING_E(E)                                 \
         switch (ring_groups) {                           \
         case 2: FORTAI_RING(E, 2); break;                \
@@ -1071,10 +1128,11 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
         else { FORTAI_RING_E(Epilogue::ADD) }
 #undef FORTAI_RING_E
 #undef FORTAI_RING
-        note_launch("q8_batch_ring_kernel<%s,groups=%d> grid %d", epilogue_name(epilogue), ring_groups, ring_grid);
+        note_launch("q8_batch_ring_kernel<%s,groups=%d,seqs/wave=%d> grid %dx%d", epilogue_name(epilogue), ring_groups,
+            ns, ring_grid, seq_blocks);
         return hipGetLastError();
     }
-    if (epilogue == Epilogue::SILU_PAIR) return launch_batch_g<Epilogue::SILU_PAIR, 1>(args, grid, lds, stream);
+    if (epilogue == Epilogue::SILU_PAIR) return launch_batch_g<Epilogue::SILU_PAIR, 2, 8>(args, grid, lds, stream);
     if (epilogue == Epilogue::STORE) {
         if (split == 1) return launch_batch_g<Epilogue::STORE, 1>(args, grid, lds, stream);
         if (split == 2) return launch_batch_g<Epilogue::STORE, 2>(args, grid, lds, stream);
@@ -1122,11 +1180,11 @@ hipError_t launch_q8_embedding(const Q8Matrix &w, const int64_t *token, int64_t 
     return hipGetLastError();
 }
 
-hipError_t launch_f16_embedding(const uint16_t *table, int width, const int64_t *token, int64_t token_value,
-    float *out, hipStream_t stream, int batch) {
+hipError_t launch_f16_embedding(const uint16_t *table, int rows, int width, const int64_t *token,
+    int64_t token_value, float *out, hipStream_t stream, int batch) {
     if (batch < 1 || (batch > 1 && !token)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(f16_embedding_kernel, dim3((width + 255) / 256, batch), dim3(256), 0, stream, table, width, token,
-        token_value, out);
+    hipLaunchKernelGGL(f16_embedding_kernel, dim3((width + 255) / 256, batch), dim3(256), 0, stream, table, rows, width,
+        token, token_value, out);
     note_launch("f16_embedding_kernel grid %dx%d", (width + 255) / 256, batch);
     return hipGetLastError();
 }

@@ -286,4 +286,9 @@ def test_f16_lm_head_and_argmax(ctx, oracle):
     dv = ctx.upload_array(vals)
     ctx.call("fortai_hip_argmax_device", ctx.h, dv.ptr, vals.size, dt.ptr)
     assert int(dt.download(np.int64)[0]) == 777
+    # every value NaN: no comparison succeeds and the first index is returned
+    # (the oracle's maxloc); the id is always inside the vector
+    dn = ctx.upload_array(np.full(100000, np.nan, np.float32))
+    ctx.call("fortai_hip_argmax_device", ctx.h, dn.ptr, 100000, dt.ptr)
+    assert int(dt.download(np.int64)[0]) == 0
     W.free()
