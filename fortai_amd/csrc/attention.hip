@@ -168,6 +168,112 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
 
 size_t output_lds_bytes() { return ea::work_floats() * sizeof(float); }
 
+// ------------------------------------------------------- exact, batches
+// The same arithmetic as attention_output_kernel (the reference's two-pass
+// softmax and P.V with its summation orders, fortai_qwen35_cpu.f90:1016-1031)
+// with one workgroup per (head, sequence) instead of one per (head, 8 value
+// dims): e_p = expf(s_p - m) is computed once into LDS, one lane sums Z left
+// to right, w_p = e_p / Z replaces e_p, and lane d of wave d / 64 runs the
+// P.V chain of value dim d over the positions in order.  A batch has many
+// (head, sequence) pairs, so this fills the chip with 8 / 64 as many
+// workgroups, each with all 64 lanes of its chaining waves busy; a single
+// sequence keeps the per-slice kernel, whose chains are shorter per
+// workgroup.  LDS: the scores of up to wide_positions(max) positions.
+constexpr int kWideUnroll = 16;  // positions per P.V step (value loads in flight)
+
+template <bool FINITE>
+__device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int n, float *w, float *red) {
+    const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+    const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
+    const int kvh = h / group;
+    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
+    // max (any order gives the same value)
+    constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
+    float m = kLowest;
+    for (int i = tid; i < n; i += ea::kThreads) {
+        const float v = sc[i];
+        w[i] = v;
+        m = fmaxf(m, v);
+    }
+    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int i = tid; i < n; i += ea::kThreads) w[i] = expf_libm(w[i] - m);
+    __syncthreads();
+    // Z = e_0 + e_1 + ... left to right, by one lane
+    if (tid == 0) {
+        float z = 0.0f;
+        int i = 0;
+        for (; i + 4 <= n; i += 4) {
+            const float4 e4 = *reinterpret_cast<const float4 *>(w + i);
+            z = z + e4.x;
+            z = z + e4.y;
+            z = z + e4.z;
+            z = z + e4.w;
+        }
+        for (; i < n; ++i) z = z + w[i];
+        red[4] = z;
+    }
+    __syncthreads();
+    const float z = red[4];
+    for (int i = tid; i < n; i += ea::kThreads) w[i] = w[i] / z;
+    __syncthreads();
+    // P.V: out_d = fl(w_0 v_0,d) + fl(w_1 v_1,d) + ... left to right
+    const int d = wave * 64 + lane;
+    if (wave * 64 >= VD) return;
+    const int dd = min(d, VD - 1);  // lanes past VD repeat the last dim and write nothing
+    const uint16_t *vb = p.vcache + static_cast<size_t>(kvh) * VD + dd;
+    const size_t vs = static_cast<size_t>(NKV) * VD;
+    float acc = 0.0f;
+    const int full = n / kWideUnroll * kWideUnroll;
+    uint16_t va[kWideUnroll], vn[kWideUnroll];
+    if (full > 0) {
+#pragma unroll
+        for (int j = 0; j < kWideUnroll; ++j) va[j] = vb[static_cast<size_t>(j) * vs];
+    }
+    for (int p0 = 0; p0 < full; p0 += kWideUnroll) {
+        const int pn = min(p0 + kWideUnroll, full - kWideUnroll);  // the next step (clamped: in bounds)
+#pragma unroll
+        for (int j = 0; j < kWideUnroll; ++j) vn[j] = vb[static_cast<size_t>(pn + j) * vs];
+#pragma unroll
+        for (int j = 0; j < kWideUnroll; j += 4) {
+            const float4 w4 = *reinterpret_cast<const float4 *>(w + p0 + j);
+            acc = acc + w4.x * ea::kv<FINITE>(va[j]);
+            acc = acc + w4.y * ea::kv<FINITE>(va[j + 1]);
+            acc = acc + w4.z * ea::kv<FINITE>(va[j + 2]);
+            acc = acc + w4.w * ea::kv<FINITE>(va[j + 3]);
+        }
+#pragma unroll
+        for (int j = 0; j < kWideUnroll; ++j) va[j] = vn[j];
+    }
+    for (int q = full; q < n; ++q) acc = acc + w[q] * ea::kv<FINITE>(vb[static_cast<size_t>(q) * vs]);
+    if (d < VD) {
+        const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d];
+        p.out[static_cast<size_t>(h) * VD + d] = acc * sigmoid_ref(gate);
+    }
+}
+
+__global__ __launch_bounds__(ea::kThreads) void attention_output_wide_kernel(const AttentionParams p_batch) {
+    const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
+    extern __shared__ __align__(16) float wide_lds[];
+    __shared__ float red[8];
+    const int pos = *p.position;
+    if (pos < 0 || pos >= p.max_context) return;
+    const int n = pos + 1;
+    if (n > p.exact_max) return;  // the split-K kernels cover this position
+    const int h = static_cast<int>(blockIdx.x);
+    const int kvh = h / (p.heads / p.kv_heads);
+    if (p.cache_flags[kvh] == 0)
+        attend_wide<true>(p, h, n, wide_lds, red);
+    else
+        attend_wide<false>(p, h, n, wide_lds, red);
+}
+
+// positions whose scores the wide kernel holds in LDS
+int wide_positions(const AttentionParams &p) { return std::min(p.max_context, p.exact_max); }
+constexpr int kWideMaxPositions = 8192;
+
 // ---------------------------------------------------------------- split-K
 // Beyond exact_max positions: each workgroup takes one kv head and a chunk of
 // kChunk positions for the whole GQA group: the chunk's max m_c, Z_c =
@@ -395,10 +501,20 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int ba
     hipLaunchKernelGGL(attention_scores_kernel, dim3(p.kv_heads * nblk_max, batch), dim3(ea::kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads), lds, stream, p);
-    e = hipGetLastError();
-    note_launch("attention_scores_kernel grid %dx%d + attention_output_kernel grid %dx%d", p.kv_heads * nblk_max, batch,
-        p.heads * (p.value / ea::kDims), batch);
+    const bool wide = batch > 1 && wide_positions(p) <= kWideMaxPositions && p.value <= ea::kThreads;
+    if (wide) {
+        const size_t wlds = static_cast<size_t>((wide_positions(p) + 3) / 4 * 4) * sizeof(float);
+        hipLaunchKernelGGL(attention_output_wide_kernel, dim3(p.heads, batch), dim3(ea::kThreads), wlds, stream, p);
+        e = hipGetLastError();
+        note_launch("attention_scores_kernel grid %dx%d + attention_output_wide_kernel grid %dx%d", p.kv_heads * nblk_max,
+            batch, p.heads, batch);
+    } else {
+        hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads), lds,
+            stream, p);
+        e = hipGetLastError();
+        note_launch("attention_scores_kernel grid %dx%d + attention_output_kernel grid %dx%d", p.kv_heads * nblk_max,
+            batch, p.heads * (p.value / ea::kDims), batch);
+    }
     if (e != hipSuccess || p.max_context <= p.exact_max) return e;
     // long contexts: the split-K pair (each kernel picks its regime from the device position)
     hipLaunchKernelGGL(attention_split_kernel, dim3(p.kv_heads * attention_split_chunks(p.max_context), batch),

@@ -152,6 +152,7 @@ struct fortai_hip_qwen35_batch {
     const fortai_hip_f16_weights *emb16 = nullptr, *out16 = nullptr;
     const fortai_hip_q8_weights *emb8 = nullptr, *out8 = nullptr;
     float *output_norm = nullptr, *x = nullptr, *logits = nullptr;
+    float *xnorm = nullptr;  // output-RMSNormed x [hidden][8 slots], the fp16 LM head input
     void *act = nullptr;     // quantized activations [batch][q8l_bytes(act_width)]
     void *h_q8l = nullptr;   // quantized FFN hidden [batch][q8l_bytes(ffn)]
     float *argmax_value = nullptr;
@@ -1863,7 +1864,7 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
     st.position = b->positions;
     if (b->out16)
         return rec(launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm,
-            b->eps, b->logits, st, stream), "output RMSNorm, LM head, greedy argmax");
+            b->eps, b->xnorm, b->logits, st, stream), "output RMSNorm, LM head, greedy argmax");
     // Q8_0 LM head: the batched matvec, then the argmax of each sequence
     MatvecInput in;
     in.x = b->x;
@@ -2017,6 +2018,7 @@ int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *c, int batch, int laye
     }
     if (e == hipSuccess) e = upload_f32(&b->output_norm, output_norm, hidden, c->stream);
     if (e == hipSuccess) e = alloc(&b->x, B * hidden);
+    if (e == hipSuccess) e = alloc(&b->xnorm, static_cast<size_t>(8) * hidden);
     if (e == hipSuccess) e = hipMalloc(&b->act, B * q8l_bytes(width));
     if (e == hipSuccess) e = hipMemsetAsync(b->act, 0, B * q8l_bytes(width), c->stream);
     if (e == hipSuccess) e = hipMalloc(&b->h_q8l, B * q8l_bytes(ffn));
@@ -2073,7 +2075,7 @@ int fortai_hip_qwen35_batch_destroy(fortai_hip_qwen35_batch *b) {
         release(L.kcache); release(L.vcache); release(L.q); release(L.k); release(L.v); release(L.partial);
         release(L.attn_out); release(L.split); release(L.flags);
     }
-    release(b->output_norm); release(b->x); release(b->logits); release(b->argmax_value); release(b->argmax_index);
+    release(b->output_norm); release(b->x); release(b->xnorm); release(b->logits); release(b->argmax_value); release(b->argmax_index);
     release(b->tokens); release(b->positions); release(b->trace);
     if (b->act) (void)hipFree(b->act);
     if (b->h_q8l) (void)hipFree(b->h_q8l);
@@ -2282,7 +2284,7 @@ hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, 
     st.position = b->positions;
     if (b->out16)
         return rec(launch_f16_batch_lm_head(b->out16->data, b->vocab, H, b->out16->finite, B, b->x, b->output_norm,
-            b->eps, b->logits, st, stream), "output RMSNorm, LM head, greedy argmax (last prompt tokens)");
+            b->eps, b->xnorm, b->logits, st, stream), "output RMSNorm, LM head, greedy argmax (last prompt tokens)");
     MatvecInput in;
     in.x = b->x;
     in.norm = b->output_norm;

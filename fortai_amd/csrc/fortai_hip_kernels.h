@@ -136,10 +136,11 @@ hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite
     const float *norm, float eps, float *out, const ArgmaxState *argmax, hipStream_t stream);
 int f16_matvec_workgroups(int rows);
 // The fp16 LM head for `batch` (<= 8) sequences at once: final RMSNorm
-// (norm required), x [batch][width] -> out [batch][rows], argmax partials
-// [batch][f16_batch_lm_head_workgroups(rows)], then the per-sequence finish.
+// (norm required) of x [batch][width] into xnorm [width][8] (interleaved), then
+// out [batch][rows], argmax partials [batch][f16_batch_lm_head_workgroups(rows)]
+// and the per-sequence finish.
 hipError_t launch_f16_batch_lm_head(const uint16_t *w, int rows, int width, bool finite, int batch, const float *x,
-    const float *norm, float eps, float *out, const ArgmaxState &argmax, hipStream_t stream);
+    const float *norm, float eps, float *xnorm, float *out, const ArgmaxState &argmax, hipStream_t stream);
 int f16_batch_lm_head_workgroups(int rows);
 hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, hipStream_t stream);
 // reduce `partials` argmax partials and publish token / trace / position

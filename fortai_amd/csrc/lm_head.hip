@@ -186,20 +186,48 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
 // RMSNorm of each sequence uses that kernel's reduction layout (128 strided
 // partial sums, then the two wave sums in order), so each sequence's logits
 // equal the single-sequence kernel's bit for bit.  256 rows x 64 columns per
-// tile; x of every sequence in LDS; per-sequence argmax partials.
+// tile; x of every sequence through scalar loads; per-sequence argmax partials.
 constexpr int kBatchRows = 256;
 constexpr int kBatchTile = 64;
 constexpr int kMaxBatch = 8;
 
+// Final RMSNorm of each sequence (fortai_qwen35_cpu.f90:707), one workgroup
+// of 128 threads per sequence with the single-sequence LM head's partition of
+// the sum (128 strided partial sums in double, the two wave sums in order), so
+// xnorm equals the x that kernel multiplies, bit for bit.  xnorm is
+// interleaved, [width][kMaxBatch]: workgroup s writes slot s with sequence
+// min(s, batch - 1), so the slots past the batch repeat the last sequence.
+__global__ __launch_bounds__(128) void batch_output_norm_kernel(const float *__restrict__ x,
+    const float *__restrict__ norm, float eps, int width, int batch, float *__restrict__ xnorm) {
+    __shared__ double red[2];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int slot = static_cast<int>(blockIdx.x);
+    const size_t base = static_cast<size_t>(min(slot, batch - 1)) * width;
+    double ss = 0.0;
+#pragma unroll 8
+    for (int i = tid; i < width; i += 128) ss += static_cast<double>(x[base + i]) * static_cast<double>(x[base + i]);
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    double total = 0.0;
+    total += red[0];
+    total += red[1];
+    const float inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+#pragma unroll 8
+    for (int i = tid; i < width; i += 128) xnorm[static_cast<size_t>(i) * kMaxBatch + slot] = (x[base + i] * inv) * norm[i];
+}
+
+// xn: the normalized x of every sequence slot, interleaved [width][kMaxBatch].
+// Its addresses are uniform across the workgroup, so the 32 values of four
+// columns arrive by scalar loads into SGPRs and feed the VALU as operands: no
+// LDS traffic and no VGPRs for x (which would otherwise hold 64 floats per
+// column group and cap the occupancy at one wave per SIMD).
 template <bool FINITE>
 __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uint16_t *__restrict__ w, int rows,
-    int width, int batch, const float *__restrict__ x, const float *__restrict__ norm, float eps,
-    float *__restrict__ out, ArgmaxState st) {
+    int width, int batch, const float *__restrict__ xn, float *__restrict__ out, ArgmaxState st) {
     constexpr int kPitch = kBatchTile + 8;
     extern __shared__ __align__(16) unsigned char lds[];
     uint16_t *tile = reinterpret_cast<uint16_t *>(lds);
-    float *xs = reinterpret_cast<float *>(lds + kBatchRows * kPitch * 2);  // [batch][width]
-    __shared__ double red[kMaxBatch][2];
     __shared__ float sv[kBatchRows / 64];
     __shared__ int si[kBatchRows / 64];
     const int tid = static_cast<int>(threadIdx.x);
@@ -229,66 +257,49 @@ __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uin
     fetch(0, ra);
     if (tiles > 1) fetch(kBatchTile, rb);
 
-    // RMSNorm of every sequence (fortai_qwen35_cpu.f90:707): threads 0-127
-    // take the even sequences, 128-255 the odd ones, each with the
-    // single-sequence kernel's partition of the sum
-    const int half = tid >> 7, ht = tid & 127;
-    for (int s0 = 0; s0 < batch; s0 += 2) {
-        const int s = s0 + half;
-        if (s < batch) {
-            const float *xq = x + static_cast<size_t>(s) * width;
-            double ss = 0.0;
-            for (int i = ht; i < width; i += 128) ss += static_cast<double>(xq[i]) * static_cast<double>(xq[i]);
-            ss = wave_sum(ss);
-            if ((ht & 63) == 0) red[s][ht >> 6] = ss;
-        }
-    }
-    __syncthreads();
-    for (int s = 0; s < batch; ++s) {
-        double total = 0.0;
-        total += red[s][0];
-        total += red[s][1];
-        const float inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
-        const float *xq = x + static_cast<size_t>(s) * width;
-        for (int i = tid; i < width; i += kBatchRows) xs[s * width + i] = (xq[i] * inv) * norm[i];
-    }
-
     // every sequence slot is computed (slots past the batch repeat the last
     // sequence and are not written): no per-sequence branch in the inner loop
-    int xo[kMaxBatch];
-#pragma unroll
-    for (int s = 0; s < kMaxBatch; ++s) xo[s] = min(s, batch - 1) * width;
     float acc[kMaxBatch];
 #pragma unroll
     for (int s = 0; s < kMaxBatch; ++s) acc[s] = 0.0f;
+    // four columns per step (32 SGPRs of x; the other waves of the SIMD
+    // cover the scalar-load latency)
+    auto xload = [&](int k, float (&xv)[4][kMaxBatch]) {
+        const float4 *src = reinterpret_cast<const float4 *>(xn + static_cast<size_t>(k) * kMaxBatch);
+#pragma unroll
+        for (int i = 0; i < 4 * kMaxBatch / 4; ++i) {
+            const float4 v = src[i];
+            xv[i / 2][(i % 2) * 4 + 0] = v.x;
+            xv[i / 2][(i % 2) * 4 + 1] = v.y;
+            xv[i / 2][(i % 2) * 4 + 2] = v.z;
+            xv[i / 2][(i % 2) * 4 + 3] = v.w;
+        }
+    };
+    auto step = [&](const uint16_t *mine, int c, const float (&xv)[4][kMaxBatch]) {
+        const uint2 h4 = *reinterpret_cast<const uint2 *>(mine + c * 4);
+        float a[4];
+        a[0] = FINITE ? half_bits_to_float(static_cast<uint16_t>(h4.x & 0xffffu))
+                      : gguf_half_to_real(static_cast<uint16_t>(h4.x & 0xffffu));
+        a[1] = FINITE ? half_bits_to_float(static_cast<uint16_t>(h4.x >> 16))
+                      : gguf_half_to_real(static_cast<uint16_t>(h4.x >> 16));
+        a[2] = FINITE ? half_bits_to_float(static_cast<uint16_t>(h4.y & 0xffffu))
+                      : gguf_half_to_real(static_cast<uint16_t>(h4.y & 0xffffu));
+        a[3] = FINITE ? half_bits_to_float(static_cast<uint16_t>(h4.y >> 16))
+                      : gguf_half_to_real(static_cast<uint16_t>(h4.y >> 16));
+#pragma unroll
+        for (int s = 0; s < kMaxBatch; ++s) {
+            float v = acc[s];
+            v = v + a[0] * xv[0][s]; v = v + a[1] * xv[1][s]; v = v + a[2] * xv[2][s]; v = v + a[3] * xv[3][s];
+            acc[s] = v;
+        }
+    };
     auto consume = [&](int k0) {
         const uint16_t *mine = tile + tid * kPitch;
-#pragma unroll 2
-        for (int sg = 0; sg < kBatchTile / 8; ++sg) {
-            const uint4 h8 = *reinterpret_cast<const uint4 *>(mine + sg * 8);
-            const uint32_t hw[4] = {h8.x, h8.y, h8.z, h8.w};
-            const int k = k0 + sg * 8;
-            float4 x0[kMaxBatch], x1[kMaxBatch];
-#pragma unroll
-            for (int s = 0; s < kMaxBatch; ++s) {
-                x0[s] = *reinterpret_cast<const float4 *>(xs + xo[s] + k);
-                x1[s] = *reinterpret_cast<const float4 *>(xs + xo[s] + k + 4);
-            }
-            float a[8];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                a[2 * q] = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[q] & 0xffffu))
-                                  : gguf_half_to_real(static_cast<uint16_t>(hw[q] & 0xffffu));
-                a[2 * q + 1] = FINITE ? half_bits_to_float(static_cast<uint16_t>(hw[q] >> 16))
-                                      : gguf_half_to_real(static_cast<uint16_t>(hw[q] >> 16));
-            }
-#pragma unroll
-            for (int s = 0; s < kMaxBatch; ++s) {
-                float v = acc[s];
-                v = v + a[0] * x0[s].x; v = v + a[1] * x0[s].y; v = v + a[2] * x0[s].z; v = v + a[3] * x0[s].w;
-                v = v + a[4] * x1[s].x; v = v + a[5] * x1[s].y; v = v + a[6] * x1[s].z; v = v + a[7] * x1[s].w;
-                acc[s] = v;
-            }
+#pragma unroll 1
+        for (int c = 0; c < kBatchTile / 4; ++c) {
+            float xv[4][kMaxBatch];
+            xload(k0 + c * 4, xv);
+            step(mine, c, xv);
         }
     };
     for (int t = 0; t < tiles; t += 2) {
@@ -390,20 +401,26 @@ hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite
 int f16_batch_lm_head_workgroups(int rows) { return (rows + kBatchRows - 1) / kBatchRows; }
 
 hipError_t launch_f16_batch_lm_head(const uint16_t *w, int rows, int width, bool finite, int batch, const float *x,
-    const float *norm, float eps, float *out, const ArgmaxState &argmax, hipStream_t stream) {
-    if (rows <= 0 || width <= 0 || width % kBatchTile || batch < 1 || batch > kMaxBatch || !norm) return hipErrorInvalidValue;
+    const float *norm, float eps, float *xnorm, float *out, const ArgmaxState &argmax, hipStream_t stream) {
+    if (rows <= 0 || width <= 0 || width % kBatchTile || batch < 1 || batch > kMaxBatch || !norm || !xnorm)
+        return hipErrorInvalidValue;
     const int grid = f16_batch_lm_head_workgroups(rows);
-    const size_t lds = static_cast<size_t>(kBatchRows) * (kBatchTile + 8) * 2 + static_cast<size_t>(batch) * width * 4;
-    if (finite)
-        hipLaunchKernelGGL(f16_batch_lm_head_kernel<true>, dim3(grid), dim3(kBatchRows), lds, stream, w, rows, width,
-            batch, x, norm, eps, out, argmax);
-    else
-        hipLaunchKernelGGL(f16_batch_lm_head_kernel<false>, dim3(grid), dim3(kBatchRows), lds, stream, w, rows, width,
-            batch, x, norm, eps, out, argmax);
+    hipLaunchKernelGGL(batch_output_norm_kernel, dim3(kMaxBatch), dim3(128), 0, stream, x, norm, eps, width, batch,
+        xnorm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const size_t lds = static_cast<size_t>(kBatchRows) * (kBatchTile + 8) * 2;
+    if (finite)
+        hipLaunchKernelGGL(f16_batch_lm_head_kernel<true>, dim3(grid), dim3(kBatchRows), lds, stream, w, rows, width,
+            batch, xnorm, out, argmax);
+    else
+        hipLaunchKernelGGL(f16_batch_lm_head_kernel<false>, dim3(grid), dim3(kBatchRows), lds, stream, w, rows, width,
+            batch, xnorm, out, argmax);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
     e = launch_argmax_finish(grid, argmax, stream, batch);
-    note_launch("f16_batch_lm_head_kernel<finite=%d> grid %d + argmax_finish_kernel grid 1x%d", finite, grid, batch);
+    note_launch("batch_output_norm_kernel grid %d + f16_batch_lm_head_kernel<finite=%d> grid %d + argmax_finish_kernel "
+        "grid 1x%d", kMaxBatch, finite, grid, batch);
     return e;
 }
 
