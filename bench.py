@@ -465,6 +465,8 @@ def main() -> int:
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 2 (GDN) and config 3 (attention) figures")
     ap.add_argument("--no-config5", action="store_true", help="skip the config 5 figures (4B shape, batch 8, prefill)")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="print only the config 5 figures (for kernel tracing of the batch-8 decode)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the kernels the --pmc traffic passes measure (see traffic_probe)")
     ap.add_argument("--no-graph", action="store_true",
@@ -485,6 +487,9 @@ def main() -> int:
         return 2
     if args.traffic_probe:
         traffic_probe()
+        return 0
+    if args.config5_only:
+        print(json.dumps({"config5": bench_config5()}), flush=True)
         return 0
     path = model_path(args)
     model, wall_ms, ev_ms = bench_decode(args, path)

@@ -250,15 +250,35 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), 0, false);
 }
 
+// (float)sdot4 of four word pairs.  The three-operand dot with an inline
+// zero addend saves the v_mov of a zero accumulator that the builtin's
+// two-operand form needs (a fifth of the VALU work of the lane-exact
+// matvecs).  A DOT result read by another VALU needs three wait states on
+// gfx950, which the compiler inserts only for dots it emits itself: here the
+// four dots come first, so three instructions separate each dot from its
+// convert, and the early-clobber outputs keep every result register apart
+// from the inputs of the later dots.
+__device__ __forceinline__ float4 sdot4x4_f(uint4 q, uint4 a) {
+    float4 r;
+    asm("v_dot4_i32_i8 %0, %4, %8, 0\n\t"
+        "v_dot4_i32_i8 %1, %5, %9, 0\n\t"
+        "v_dot4_i32_i8 %2, %6, %10, 0\n\t"
+        "v_dot4_i32_i8 %3, %7, %11, 0\n\t"
+        "v_cvt_f32_i32 %0, %0\n\t"
+        "v_cvt_f32_i32 %1, %1\n\t"
+        "v_cvt_f32_i32 %2, %2\n\t"
+        "v_cvt_f32_i32 %3, %3"
+        : "=&v"(r.x), "=&v"(r.y), "=&v"(r.z), "=&v"(r.w)
+        : "v"(q.x), "v"(q.y), "v"(q.z), "v"(q.w), "v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w));
+    return r;
+}
+
 __device__ __forceinline__ float dot_chunk(uint4 q, uint2 sc, uint4 a, float4 as, float acc) {
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x,
-        static_cast<float>(sdot4(q.x, a.x)), acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y,
-        static_cast<float>(sdot4(q.y, a.y)), acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z,
-        static_cast<float>(sdot4(q.z, a.z)), acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w,
-        static_cast<float>(sdot4(q.w, a.w)), acc);
+    const float4 d = sdot4x4_f(q, a);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x, d.x, acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y, d.y, acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z, d.z, acc);
+    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w, d.w, acc);
     return acc;
 }
 

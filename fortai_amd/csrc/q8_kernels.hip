@@ -435,10 +435,11 @@ struct BatchMatvecArgs {
 };
 
 __device__ __forceinline__ float dot_chunk_f(uint4 q, const float (&ws)[4], uint4 a, float4 as, float acc) {
-    acc = __builtin_fmaf(ws[0] * as.x, static_cast<float>(sdot4(q.x, a.x)), acc);
-    acc = __builtin_fmaf(ws[1] * as.y, static_cast<float>(sdot4(q.y, a.y)), acc);
-    acc = __builtin_fmaf(ws[2] * as.z, static_cast<float>(sdot4(q.z, a.z)), acc);
-    acc = __builtin_fmaf(ws[3] * as.w, static_cast<float>(sdot4(q.w, a.w)), acc);
+    const float4 d = sdot4x4_f(q, a);
+    acc = __builtin_fmaf(ws[0] * as.x, d.x, acc);
+    acc = __builtin_fmaf(ws[1] * as.y, d.y, acc);
+    acc = __builtin_fmaf(ws[2] * as.z, d.z, acc);
+    acc = __builtin_fmaf(ws[3] * as.w, d.w, acc);
     return acc;
 }
 
@@ -811,7 +812,6 @@ hipError_t launch_batch_g(const BatchMatvecArgs &args, int grid, size_t lds, hip
         case 2: FORTAI_PAIR(2); break;
         case 8: FORTAI_PAIR(8); break;
         case 20: FORTAI_PAIR(20); break;
-        case 32: FORTAI_PAIR(32); break;
         default: FORTAI_PAIR(0); break;
         }
 #undef FORTAI_PAIR
