@@ -171,29 +171,74 @@ size_t output_lds_bytes() { return ea::work_floats() * sizeof(float); }
 // ------------------------------------------------------- exact, batches
 // The same arithmetic as attention_output_kernel (the reference's two-pass
 // softmax and P.V with its summation orders, fortai_qwen35_cpu.f90:1016-1031)
-// with one workgroup per (head, sequence) instead of one per (head, 8 value
-// dims): e_p = expf(s_p - m) is computed once into LDS, one lane sums Z left
-// to right, w_p = e_p / Z replaces e_p, and lane d of wave d / 64 runs the
-// P.V chain of value dim d over the positions in order.  A batch has many
-// (head, sequence) pairs, so this fills the chip with 8 / 64 as many
-// workgroups, each with all 64 lanes of its chaining waves busy; a single
-// sequence keeps the per-slice kernel, whose chains are shorter per
-// workgroup.  LDS: the scores of up to wide_positions(max) positions.
-constexpr int kWideUnroll = 16;  // positions per P.V step (value loads in flight)
+// with one workgroup per (head, 64 value dims, sequence) instead of one per
+// (head, 8 value dims): e_p = expf(s_p - m) is computed once into LDS, one
+// lane sums Z left to right, w_p = e_p / Z replaces e_p, and lane d of wave 0
+// runs the P.V chain of value dim d0 + d over the positions in order.  The
+// value columns reach LDS in tiles of kWideTile positions, loaded by all
+// four waves two tiles ahead of the chains (the first two while the softmax
+// is computed).  A batch has many (head, sequence) pairs, so this fills the
+// chip with 1/8 as many workgroups, each chain step using all 64 lanes; a
+// single sequence keeps the per-slice kernel, whose chains are shorter per
+// workgroup.
+constexpr int kWideTile = 256;                                        // positions per value tile
+constexpr int kWideDims = 64;                                         // value dims per workgroup
+constexpr int kWidePitch = kWideDims + 8;                             // halves per LDS tile row
+constexpr int kWideLoads = kWideTile * kWideDims / 8 / ea::kThreads;  // 16-byte pieces per thread and tile
+constexpr int kWideMaxPositions = 8192;
+
+// positions whose scores the wide kernel holds in LDS, and their floats
+// (a multiple of 4: the value tile after them stays 16-byte aligned)
+__host__ __device__ inline int wide_positions(const AttentionParams &p) {
+    return p.max_context < p.exact_max ? p.max_context : p.exact_max;
+}
+__host__ __device__ inline int wide_score_floats(const AttentionParams &p) { return (wide_positions(p) + 3) / 4 * 4; }
 
 template <bool FINITE>
-__device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int n, float *w, float *red) {
+__device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int d0, int n, float *w, uint16_t *vt,
+    float *red) {
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
     const int kvh = h / group;
     const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
+    const uint16_t *vb = p.vcache + static_cast<size_t>(kvh) * VD + d0;
+    const size_t vs = static_cast<size_t>(NKV) * VD;
+    const int pieces = min(kWideDims, VD - d0) / 8;  // 16-byte pieces of a row slice
+    const int tiles = (n + kWideTile - 1) / kWideTile;
+    uint4 ra[kWideLoads], rb[kWideLoads];
+    auto fetch = [&](int t, uint4 (&regs)[kWideLoads]) {
+#pragma unroll
+        for (int j = 0; j < kWideLoads; ++j) {
+            const int li = tid + ea::kThreads * j;  // piece index within the tile
+            const int pp = min(t * kWideTile + li / pieces, n - 1), pc = li % pieces;
+            regs[j] = li < kWideTile * pieces ? *reinterpret_cast<const uint4 *>(vb + pp * vs + pc * 8)
+                                              : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto stash = [&](const uint4 (&regs)[kWideLoads]) {
+#pragma unroll
+        for (int j = 0; j < kWideLoads; ++j) {
+            const int li = tid + ea::kThreads * j;
+            if (li < kWideTile * pieces)
+                *reinterpret_cast<uint4 *>(vt + (li / pieces) * kWidePitch + (li % pieces) * 8) = regs[j];
+        }
+    };
+    fetch(0, ra);
+    if (tiles > 1) fetch(1, rb);
+
     // max (any order gives the same value)
     constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
     float m = kLowest;
-    for (int i = tid; i < n; i += ea::kThreads) {
-        const float v = sc[i];
-        w[i] = v;
-        m = fmaxf(m, v);
+    constexpr int kU = 8;  // score loads in flight per thread
+    for (int i0 = tid; i0 < n; i0 += ea::kThreads * kU) {
+        float x[kU];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) x[k] = sc[min(i0 + k * ea::kThreads, n - 1)];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            if (i0 + k * ea::kThreads < n) w[i0 + k * ea::kThreads] = x[k];
+            m = fmaxf(m, x[k]);  // clamped duplicates change nothing
+        }
     }
     for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
     if (lane == 0) red[wave] = m;
@@ -201,59 +246,105 @@ __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (int i = tid; i < n; i += ea::kThreads) w[i] = expf_libm(w[i] - m);
     __syncthreads();
-    // Z = e_0 + e_1 + ... left to right, by one lane
+    // Z = e_0 + e_1 + ... left to right, by one lane; the LDS reads of the
+    // next 16 values are in flight while the current 16 are added
     if (tid == 0) {
         float z = 0.0f;
+        const int full = n / 16 * 16;
+        float4 ea4[4], eb4[4];
+        auto rd = [&](int i, float4 (&r)[4]) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) r[k] = *reinterpret_cast<const float4 *>(w + i + 4 * k);
+        };
+        auto add = [&](const float4 (&r)[4]) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                z = z + r[k].x;
+                z = z + r[k].y;
+                z = z + r[k].z;
+                z = z + r[k].w;
+            }
+        };
+        if (full > 0) rd(0, ea4);
         int i = 0;
-        for (; i + 4 <= n; i += 4) {
-            const float4 e4 = *reinterpret_cast<const float4 *>(w + i);
-            z = z + e4.x;
-            z = z + e4.y;
-            z = z + e4.z;
-            z = z + e4.w;
+        for (; i + 32 <= full; i += 32) {
+            rd(i + 16, eb4);
+            add(ea4);
+            if (i + 32 < full) rd(i + 32, ea4);
+            add(eb4);
         }
-        for (; i < n; ++i) z = z + w[i];
+        if (i < full) add(ea4);
+        for (i = full; i < n; ++i) z = z + w[i];
         red[4] = z;
     }
     __syncthreads();
     const float z = red[4];
     for (int i = tid; i < n; i += ea::kThreads) w[i] = w[i] / z;
-    __syncthreads();
+    // (the first stash's barrier below orders these writes before the chains)
+
     // P.V: out_d = fl(w_0 v_0,d) + fl(w_1 v_1,d) + ... left to right
-    const int d = wave * 64 + lane;
-    if (wave * 64 >= VD) return;
-    const int dd = min(d, VD - 1);  // lanes past VD repeat the last dim and write nothing
-    const uint16_t *vb = p.vcache + static_cast<size_t>(kvh) * VD + dd;
-    const size_t vs = static_cast<size_t>(NKV) * VD;
-    float acc = 0.0f;
-    const int full = n / kWideUnroll * kWideUnroll;
-    uint16_t va[kWideUnroll], vn[kWideUnroll];
-    if (full > 0) {
+    const int d = d0 + lane;
+    const int col = min(d, VD - 1) - d0;  // lanes past VD repeat the last dim and write nothing
+    // groups of 16 positions: the LDS reads of the next group are in flight
+    // while the current one is multiplied and added
+    constexpr int kG = 16;
+    struct Group {
+        float4 w4[kG / 4];
+        uint16_t v[kG];
+    };
+    auto gread = [&](int p0, int j, Group &g) {
 #pragma unroll
-        for (int j = 0; j < kWideUnroll; ++j) va[j] = vb[static_cast<size_t>(j) * vs];
-    }
-    for (int p0 = 0; p0 < full; p0 += kWideUnroll) {
-        const int pn = min(p0 + kWideUnroll, full - kWideUnroll);  // the next step (clamped: in bounds)
+        for (int k = 0; k < kG / 4; ++k) g.w4[k] = *reinterpret_cast<const float4 *>(w + p0 + j + 4 * k);
 #pragma unroll
-        for (int j = 0; j < kWideUnroll; ++j) vn[j] = vb[static_cast<size_t>(pn + j) * vs];
+        for (int k = 0; k < kG; ++k) g.v[k] = vt[(j + k) * kWidePitch + col];
+    };
+    auto gadd = [&](const Group &g, float acc) {
 #pragma unroll
-        for (int j = 0; j < kWideUnroll; j += 4) {
-            const float4 w4 = *reinterpret_cast<const float4 *>(w + p0 + j);
-            acc = acc + w4.x * ea::kv<FINITE>(va[j]);
-            acc = acc + w4.y * ea::kv<FINITE>(va[j + 1]);
-            acc = acc + w4.z * ea::kv<FINITE>(va[j + 2]);
-            acc = acc + w4.w * ea::kv<FINITE>(va[j + 3]);
+        for (int k = 0; k < kG / 4; ++k) {
+            acc = acc + g.w4[k].x * ea::kv<FINITE>(g.v[4 * k + 0]);
+            acc = acc + g.w4[k].y * ea::kv<FINITE>(g.v[4 * k + 1]);
+            acc = acc + g.w4[k].z * ea::kv<FINITE>(g.v[4 * k + 2]);
+            acc = acc + g.w4[k].w * ea::kv<FINITE>(g.v[4 * k + 3]);
         }
-#pragma unroll
-        for (int j = 0; j < kWideUnroll; ++j) va[j] = vn[j];
+        return acc;
+    };
+    auto chain = [&](int t, float acc) {
+        const int p0 = t * kWideTile, cnt = min(kWideTile, n - p0);
+        const int full = cnt / kG * kG;
+        Group ga, gb;
+        if (full > 0) gread(p0, 0, ga);
+        int j = 0;
+        for (; j + 2 * kG <= full; j += 2 * kG) {
+            gread(p0, j + kG, gb);
+            acc = gadd(ga, acc);
+            if (j + 2 * kG < full) gread(p0, j + 2 * kG, ga);
+            acc = gadd(gb, acc);
+        }
+        if (j < full) acc = gadd(ga, acc);
+        for (j = full; j < cnt; ++j) acc = acc + w[p0 + j] * ea::kv<FINITE>(vt[j * kWidePitch + col]);
+        return acc;
+    };
+    float acc = 0.0f;
+    for (int t = 0; t < tiles; t += 2) {
+        stash(ra);
+        __syncthreads();
+        if (t + 2 < tiles) fetch(t + 2, ra);
+        if (wave == 0) acc = chain(t, acc);
+        __syncthreads();
+        if (t + 1 >= tiles) break;
+        stash(rb);
+        __syncthreads();
+        if (t + 3 < tiles) fetch(t + 3, rb);
+        if (wave == 0) acc = chain(t + 1, acc);
+        __syncthreads();
     }
-    for (int q = full; q < n; ++q) acc = acc + w[q] * ea::kv<FINITE>(vb[static_cast<size_t>(q) * vs]);
-    if (d < VD) {
+    if (wave == 0 && d < VD) {
         const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d];
         p.out[static_cast<size_t>(h) * VD + d] = acc * sigmoid_ref(gate);
     }
 }
 
+// grid: (heads x ceil(value / 64), batch)
 __global__ __launch_bounds__(ea::kThreads) void attention_output_wide_kernel(const AttentionParams p_batch) {
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     extern __shared__ __align__(16) float wide_lds[];
@@ -262,17 +353,16 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_wide_kernel(con
     if (pos < 0 || pos >= p.max_context) return;
     const int n = pos + 1;
     if (n > p.exact_max) return;  // the split-K kernels cover this position
-    const int h = static_cast<int>(blockIdx.x);
+    const int slices = (p.value + kWideDims - 1) / kWideDims;
+    const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * kWideDims;
     const int kvh = h / (p.heads / p.kv_heads);
+    uint16_t *vt = reinterpret_cast<uint16_t *>(wide_lds + wide_score_floats(p));
     if (p.cache_flags[kvh] == 0)
-        attend_wide<true>(p, h, n, wide_lds, red);
+        attend_wide<true>(p, h, d0, n, wide_lds, vt, red);
     else
-        attend_wide<false>(p, h, n, wide_lds, red);
+        attend_wide<false>(p, h, d0, n, wide_lds, vt, red);
 }
 
-// positions whose scores the wide kernel holds in LDS
-int wide_positions(const AttentionParams &p) { return std::min(p.max_context, p.exact_max); }
-constexpr int kWideMaxPositions = 8192;
 
 // ---------------------------------------------------------------- split-K
 // Beyond exact_max positions: each workgroup takes one kv head and a chunk of
@@ -503,11 +593,13 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int ba
     if (e != hipSuccess) return e;
     const bool wide = batch > 1 && wide_positions(p) <= kWideMaxPositions && p.value <= ea::kThreads;
     if (wide) {
-        const size_t wlds = static_cast<size_t>((wide_positions(p) + 3) / 4 * 4) * sizeof(float);
-        hipLaunchKernelGGL(attention_output_wide_kernel, dim3(p.heads, batch), dim3(ea::kThreads), wlds, stream, p);
+        const size_t wlds = static_cast<size_t>(wide_score_floats(p)) * sizeof(float) +
+            static_cast<size_t>(kWideTile) * kWidePitch * sizeof(uint16_t);
+        const int wgrid = p.heads * ((p.value + kWideDims - 1) / kWideDims);
+        hipLaunchKernelGGL(attention_output_wide_kernel, dim3(wgrid, batch), dim3(ea::kThreads), wlds, stream, p);
         e = hipGetLastError();
         note_launch("attention_scores_kernel grid %dx%d + attention_output_wide_kernel grid %dx%d", p.kv_heads * nblk_max,
-            batch, p.heads, batch);
+            batch, wgrid, batch);
     } else {
         hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads), lds,
             stream, p);
