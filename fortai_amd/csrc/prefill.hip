@@ -117,36 +117,69 @@ __global__ __launch_bounds__(kRowThreads) void silu_product_quantize_kernel(cons
     }
 }
 
-// Causal conv1d + SiLU over time: one thread per (sequence, channel), the
-// window in registers, continuing from and returning conv_state
-// [batch][K-1][C] (oldest first).  x: raw projections [batch*T][C].
+// Causal conv1d + SiLU over the prompt (fortai_qwen35_cpu.f90:856-879).  The
+// conv has no recurrence: output t reads the inputs t-K+1..t, those before
+// the prompt from conv_state [batch][K-1][C] (oldest first).  One thread per
+// (sequence, channel, kConvTokens consecutive tokens) computes each output
+// with the decode's conv_silu (same window, same order), reading the old
+// state only; conv_state_advance_kernel then stores the last K-1 inputs.
+// x: raw projections [batch*T][C].
+constexpr int kConvTokens = 8;
+
 __global__ __launch_bounds__(256) void conv_silu_tokens_kernel(const float *__restrict__ x,
-    const float *__restrict__ conv_w, float *__restrict__ conv_state, float *__restrict__ out, int T, int C, int K) {
+    const float *__restrict__ conv_w, const float *__restrict__ conv_state, float *__restrict__ out, int T, int C,
+    int K) {
+    const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    const int t0 = static_cast<int>(blockIdx.y) * kConvTokens;
+    const int s = static_cast<int>(blockIdx.z);
+    if (c >= C) return;
+    float taps[kConvMax];
+#pragma unroll
+    for (int i = 0; i < kConvMax; ++i) taps[i] = i < K ? conv_w[static_cast<size_t>(c) * K + i] : 0.0f;
+    const float *cs = conv_state + static_cast<size_t>(s) * (K - 1) * C + c;
+    const float *xs = x + static_cast<size_t>(s) * T * C + c;
+    float *os = out + static_cast<size_t>(s) * T * C + c;
+    // inputs t0-K+1 .. t0+kConvTokens-1 (kConvMax-1 window slots, then the tokens)
+    float in[kConvMax - 1 + kConvTokens];
+#pragma unroll
+    for (int i = 0; i < kConvMax - 1 + kConvTokens; ++i) {
+        const int u = t0 - (kConvMax - 1) + i;  // input index; < 0: from the state
+        float v = 0.0f;
+        if (u >= 0 && u < T) v = xs[static_cast<size_t>(u) * C];
+        else if (u < 0 && u >= -(K - 1)) v = cs[static_cast<size_t>(K - 1 + u) * C];
+        in[i] = v;
+    }
+#pragma unroll
+    for (int j = 0; j < kConvTokens; ++j) {
+        const int t = t0 + j;
+        if (t >= T) break;
+        float win[kConvMax - 1];
+#pragma unroll
+        for (int i = 0; i < kConvMax - 1; ++i) win[i] = i < K - 1 ? in[j + (kConvMax - K) + i] : 0.0f;
+        os[static_cast<size_t>(t) * C] = conv_silu(win, taps, K, in[j + kConvMax - 1]);
+    }
+}
+
+// conv_state <- the last K-1 inputs of the prompt (older state entries when
+// the prompt is shorter than K-1); each thread reads its channel's old state
+// before writing it.
+__global__ __launch_bounds__(256) void conv_state_advance_kernel(const float *__restrict__ x, float *conv_state, int T,
+    int C, int K) {
     const int c = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
     const int s = static_cast<int>(blockIdx.y);
     if (c >= C) return;
-    float win[kConvMax - 1], taps[kConvMax];
-    float *cs = conv_state + static_cast<size_t>(s) * (K - 1) * C;
-#pragma unroll
-    for (int t = 0; t < kConvMax - 1; ++t) win[t] = t < K - 1 ? cs[static_cast<size_t>(t) * C + c] : 0.0f;
-#pragma unroll
-    for (int t = 0; t < kConvMax; ++t) taps[t] = t < K ? conv_w[static_cast<size_t>(c) * K + t] : 0.0f;
+    float *cs = conv_state + static_cast<size_t>(s) * (K - 1) * C + c;
     const float *xs = x + static_cast<size_t>(s) * T * C + c;
-    float *os = out + static_cast<size_t>(s) * T * C + c;
-#pragma unroll 32
-    for (int t = 0; t < T; ++t) {
-        const float v = xs[static_cast<size_t>(t) * C];
-        os[static_cast<size_t>(t) * C] = conv_silu(win, taps, K, v);
+    float nw[kConvMax - 1];
 #pragma unroll
-        for (int i = 0; i + 1 < kConvMax - 1; ++i)
-            if (i + 1 < K - 1) win[i] = win[i + 1];
-#pragma unroll
-        for (int i = 0; i < kConvMax - 1; ++i)
-            if (i == K - 2) win[i] = v;
+    for (int i = 0; i < kConvMax - 1; ++i) {
+        if (i >= K - 1) break;
+        const int u = T - (K - 1) + i;
+        nw[i] = u >= 0 ? xs[static_cast<size_t>(u) * C] : cs[static_cast<size_t>(i + T) * C];
     }
 #pragma unroll
-    for (int t = 0; t < kConvMax - 1; ++t)
-        if (t < K - 1) cs[static_cast<size_t>(t) * C + c] = win[t];
+    for (int i = 0; i < kConvMax - 1; ++i)
+        if (i < K - 1) cs[static_cast<size_t>(i) * C] = nw[i];
 }
 
 // Per token: the L2 norms of every key head's q and k (1 / max(|x|, eps),
@@ -463,9 +496,13 @@ hipError_t launch_silu_product_quantize(const float *gate, const float *up, int 
 hipError_t launch_conv_silu_tokens(const float *x, const float *conv_w, float *conv_state, float *out, int batch, int T,
     int C, int K, hipStream_t stream) {
     if (batch < 1 || T < 1 || C < 1 || K < 2 || K > kConvMax) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(conv_silu_tokens_kernel, dim3((C + 255) / 256, batch), dim3(256), 0, stream, x, conv_w,
-        conv_state, out, T, C, K);
-    note_launch("conv_silu_tokens_kernel grid %dx%d", (C + 255) / 256, batch);
+    const int cb = (C + 255) / 256, tb = (T + kConvTokens - 1) / kConvTokens;
+    hipLaunchKernelGGL(conv_silu_tokens_kernel, dim3(cb, tb, batch), dim3(256), 0, stream, x, conv_w, conv_state, out,
+        T, C, K);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(conv_state_advance_kernel, dim3(cb, batch), dim3(256), 0, stream, x, conv_state, T, C, K);
+    note_launch("conv_silu_tokens_kernel grid %dx%dx%d + conv_state_advance_kernel grid %dx%d", cb, tb, batch, cb, batch);
     return hipGetLastError();
 }
 
