@@ -2254,7 +2254,7 @@ hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, 
             AttentionParams ap = attention_params(const_cast<fortai_hip_qwen35_attention *>(A), b->pa, b->pb, b->pc, b->pd);
             ap.kcache = L.kcache; ap.vcache = L.vcache; ap.cache_flags = L.flags; ap.max_context = b->max_context;
             if (e == hipSuccess)
-                e = rec(launch_attention_prefill(ap, B, T, b->pd, stream), "q/k norm, RoPE, KV append, causal attention");
+                e = rec(launch_attention_prefill(ap, B, T, b->pd, stream, !exact), "q/k norm, RoPE, KV append, causal attention");
             if (e == hipSuccess)
                 e = rec(launch_rms_quantize_tokens(b->pd, N, A->heads * A->value, nullptr, 0.0f, b->px8, stream),
                     "quantize attention output");

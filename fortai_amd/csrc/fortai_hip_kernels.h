@@ -234,7 +234,10 @@ hipError_t launch_gdn_prefill(const GdnParams &p, int batch, int T, float *qinv,
 // q/k norm + RoPE, fp16 K/V append at positions 0..T-1 and causal attention:
 // p.q [rows][heads][2 head] (normalized in place), p.k/p.v [rows][kv_heads][head],
 // caches and flags [batch][...]; out [rows][heads][head]
-hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream);
+// matrix_cores: fp16 MFMA scores and P.V (the default prefill mode); false:
+// the fp32 kernel throughout (the exact mode)
+hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream,
+    bool matrix_cores);
 
 // ---- persistent decoder ------------------------------------------------------
 // One launch per token (decode_persistent.hip).  Activations cross

@@ -356,8 +356,8 @@ constexpr int kKTile = 32;
 
 template <int HEAD>
 __global__ __launch_bounds__(256) void attention_prefill_kernel(const float *__restrict__ q,
-    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, float *__restrict__ out, int T,
-    int heads, int kv_heads, int max_context) {
+    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, const int *__restrict__ flags,
+    int only_flagged, float *__restrict__ out, int T, int heads, int kv_heads, int max_context) {
     constexpr int kPart = HEAD / 4;
     constexpr int kPartPitch = kPart + 4;  // the four quarters of a row on different banks
     __shared__ __align__(16) float kt[kKTile][4 * kPartPitch];
@@ -368,6 +368,9 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float *__r
     const int q0 = static_cast<int>(blockIdx.x) * kQBlock;
     const int t = min(q0 + qi, T - 1);
     const int kvh = h / (heads / kv_heads);
+    // after the matrix-core kernel: only the (sequence, kv head) pairs whose
+    // cache holds exponent-31 halves, which that kernel leaves to this one
+    if (only_flagged && flags[static_cast<size_t>(s) * kv_heads + kvh] == 0) return;
     const float *qrow = q + ((static_cast<size_t>(s) * T + t) * heads + h) * 2 * HEAD;
     float qv[kPart], o[kPart];
 #pragma unroll
@@ -420,6 +423,192 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float *__r
     for (int d = 0; d < kPart; ++d) {
         const int dd = part * kPart + d;
         orow[dd] = (o[d] / z) * sigmoid_ref(gate[dd]);
+    }
+}
+
+// The same causal attention on the fp16 matrix cores (the default prefill
+// mode, within its tolerance): one workgroup per (32-query block, kv head,
+// sequence), wave w taking q head kvh * group + w.  Per 32-key tile,
+//   S^T = K Q^T  (v_mfma_f32_32x32x16_f16, keys x queries, q pre-scaled by
+//                 1/sqrt(head) and rounded to fp16; K is the fp16 cache),
+// an online softmax in fp32 (__expf, the running sums rescaled when a
+// query's maximum grows), and
+//   O^T += V^T P^T (the same instruction, dims x queries, P rounded to fp16).
+// The accumulator of a 32x32 MFMA holds, in element i of lane l, row
+// 8*(i/4) + 4*(l/32) + i%4 and column l%32: with keys and dims as rows and
+// queries as columns, every value of a query stays in lanes l%32 == query,
+// so the softmax rescale is a per-lane scalar, and the 16 probabilities of a
+// lane are the B operand of the two P.V instructions of the tile as they are
+// (A and B present the same keys in the same slots; which k the instruction
+// assigns to a slot does not change the sum).  K reaches LDS key-major (the
+// A operand of S^T: 16 bytes of one key per lane), V dim-major (the A operand
+// of O^T: two 8-byte runs of keys per lane).  A (sequence, kv head) whose
+// cache holds exponent-31 halves is left to attention_prefill_kernel.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+constexpr int kMfmaQ = 32;  // queries per workgroup (one MFMA column block)
+constexpr int kMfmaK = 32;  // keys per tile
+
+template <int HEAD>
+__global__ __launch_bounds__(256) void attention_prefill_mfma_kernel(const float *__restrict__ q,
+    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, const int *__restrict__ flags,
+    float *__restrict__ out, int T, int heads, int kv_heads, int max_context) {
+    static_assert(HEAD % 64 == 0, "whole 16-byte pieces per thread and tile");
+    constexpr int kKPitch = HEAD + 8;             // halves per K row (key-major)
+    constexpr int kVPitch = kMfmaK + 8;           // halves per V^T row (dim-major)
+    constexpr int kSteps = HEAD / 16;             // k-steps of S^T
+    constexpr int kDT = HEAD / 32;                // 32-dim tiles of O^T
+    constexpr int kPieces = HEAD / 8;             // 16-byte pieces of a key row
+    constexpr int kLoads = kMfmaK * kPieces / 256;  // pieces per thread and tile (K and V each)
+    extern __shared__ __align__(16) _Float16 mfma_lds[];
+    _Float16 *kt = mfma_lds;                                   // [kMfmaK][kKPitch]
+    _Float16 *vt = kt + kMfmaK * kKPitch;                      // [HEAD][kVPitch]
+    _Float16 *qs = vt + HEAD * kVPitch;                        // [4 waves][kMfmaQ][kKPitch]
+    const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+    const int col = lane & 31, g = lane >> 5;
+    const int kvh = static_cast<int>(blockIdx.y), s = static_cast<int>(blockIdx.z);
+    const int q0 = static_cast<int>(blockIdx.x) * kMfmaQ;
+    if (flags[static_cast<size_t>(s) * kv_heads + kvh] != 0) return;
+    const int group = heads / kv_heads;
+    const bool active = wave < group;
+    const int h = kvh * group + (active ? wave : 0);
+    const int qq = q0 + col;                       // this lane's query
+    const int qt = min(qq, T - 1);
+    const float *qrow = q + ((static_cast<size_t>(s) * T + qt) * heads + h) * 2 * HEAD;
+    // the wave's 32 query rows, scaled by 1/sqrt(head), in fp16 (the B
+    // operand of S^T, read from LDS each tile): lane l writes dims
+    // 4 * (l % kPieces4) .. of rows l / kPieces4, l / kPieces4 + 64 / kPieces4, ...
+    _Float16 *qw = qs + wave * kMfmaQ * kKPitch;
+    {
+        const float scale = 1.0f / sqrtf(static_cast<float>(HEAD));
+        constexpr int kPieces4 = HEAD / 4;  // float4 pieces of a q row
+        for (int e = lane; e < kMfmaQ * kPieces4; e += 64) {
+            const int r = e / kPieces4, c4 = e % kPieces4;
+            const int t = min(q0 + r, T - 1);
+            const float4 a = *reinterpret_cast<const float4 *>(
+                q + ((static_cast<size_t>(s) * T + t) * heads + h) * 2 * HEAD + c4 * 4);
+            const half4_t v = {static_cast<_Float16>(a.x * scale), static_cast<_Float16>(a.y * scale),
+                static_cast<_Float16>(a.z * scale), static_cast<_Float16>(a.w * scale)};
+            *reinterpret_cast<half4_t *>(qw + r * kKPitch + c4 * 4) = v;
+        }
+    }
+    const int last = min(q0 + kMfmaQ, T) - 1;      // keys 0..last cover the block
+    const int ntiles = last / kMfmaK + 1;
+    u32x4_t kr[kLoads], vr[kLoads];
+    // K pieces key-major (consecutive lanes: consecutive 16 bytes of a key
+    // row); V pieces key-minor (consecutive lanes: consecutive keys), so that
+    // each transposed 2-byte LDS store of a wave covers 32 consecutive keys
+    // of one dim row (no bank conflicts)
+    auto fetch = [&](int j0) {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int li = tid + 256 * j;
+            const int kkey = li / kPieces, kpc = li % kPieces;
+            const int vkey = li % kMfmaK, vpc = li / kMfmaK;
+            const size_t base = (static_cast<size_t>(s) * max_context) * kv_heads + kvh;
+            kr[j] = *reinterpret_cast<const u32x4_t *>(
+                kcache + (base + static_cast<size_t>(min(j0 + kkey, last)) * kv_heads) * HEAD + kpc * 8);
+            vr[j] = *reinterpret_cast<const u32x4_t *>(
+                vcache + (base + static_cast<size_t>(min(j0 + vkey, last)) * kv_heads) * HEAD + vpc * 8);
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) {
+            const int li = tid + 256 * j;
+            const int kkey = li / kPieces, kpc = li % kPieces;
+            const int vkey = li % kMfmaK, vpc = li / kMfmaK;
+            *reinterpret_cast<u32x4_t *>(kt + kkey * kKPitch + kpc * 8) = kr[j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt[(vpc * 8 + 2 * e) * kVPitch + vkey] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(vr[j][e] & 0xffffu));
+                vt[(vpc * 8 + 2 * e + 1) * kVPitch + vkey] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(vr[j][e] >> 16));
+            }
+        }
+    };
+    float16_t o[kDT];
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt) o[dt] = float16_t{};
+    float m = -__builtin_inff(), zl = 0.0f;
+    fetch(0);
+    for (int t = 0; t < ntiles; ++t) {
+        const int j0 = t * kMfmaK;
+        __syncthreads();  // every wave is done with the previous tile
+        stash();
+        __syncthreads();
+        if (t + 1 < ntiles) fetch(j0 + kMfmaK);
+        if (!active) continue;
+        float16_t sc = float16_t{};
+#pragma unroll
+        for (int kk = 0; kk < kSteps; ++kk) {
+            const half8_t a = *reinterpret_cast<const half8_t *>(kt + col * kKPitch + kk * 16 + g * 8);
+            const half8_t b = *reinterpret_cast<const half8_t *>(qw + col * kKPitch + kk * 16 + g * 8);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, sc, 0, 0, 0);
+        }
+        // element i: key j0 + 8 * (i / 4) + 4 * g + i % 4 of query qq
+        float tmax = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int key = j0 + 8 * (i / 4) + 4 * g + (i % 4);
+            if (key > qq || key >= T) sc[i] = -__builtin_inff();
+            tmax = fmaxf(tmax, sc[i]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mnew = fmaxf(m, tmax);
+        const float corr = __expf(m - mnew);  // 0 on the first tile (m = -inf)
+        m = mnew;
+        float pl[16];
+        float zt = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pl[i] = sc[i] == -__builtin_inff() ? 0.0f : __expf(sc[i] - mnew);
+            zt += pl[i];
+        }
+        zl = zl * corr + zt;
+        const half8_t pb0 = {static_cast<_Float16>(pl[0]), static_cast<_Float16>(pl[1]), static_cast<_Float16>(pl[2]),
+            static_cast<_Float16>(pl[3]), static_cast<_Float16>(pl[4]), static_cast<_Float16>(pl[5]),
+            static_cast<_Float16>(pl[6]), static_cast<_Float16>(pl[7])};
+        const half8_t pb1 = {static_cast<_Float16>(pl[8]), static_cast<_Float16>(pl[9]), static_cast<_Float16>(pl[10]),
+            static_cast<_Float16>(pl[11]), static_cast<_Float16>(pl[12]), static_cast<_Float16>(pl[13]),
+            static_cast<_Float16>(pl[14]), static_cast<_Float16>(pl[15])};
+        // rescale only when a maximum of the wave's queries grew
+        if (__builtin_amdgcn_read_exec() && __any(corr != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][i] *= corr;
+        }
+#pragma unroll
+        for (int dt = 0; dt < kDT; ++dt) {
+            const _Float16 *vrow = vt + (dt * 32 + col) * kVPitch + 4 * g;
+            const half4_t v0 = *reinterpret_cast<const half4_t *>(vrow);
+            const half4_t v1 = *reinterpret_cast<const half4_t *>(vrow + 8);
+            const half4_t v2 = *reinterpret_cast<const half4_t *>(vrow + 16);
+            const half4_t v3 = *reinterpret_cast<const half4_t *>(vrow + 24);
+            const half8_t va0 = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            const half8_t va1 = {v2[0], v2[1], v2[2], v2[3], v3[0], v3[1], v3[2], v3[3]};
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va0, pb0, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va1, pb1, o[dt], 0, 0, 0);
+        }
+    }
+    if (!active || qq >= T) return;
+    const float z = zl + __shfl_xor(zl, 32);
+    const float *gate = qrow + HEAD;
+    float *orow = out + ((static_cast<size_t>(s) * T + qq) * heads + h) * HEAD;
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d = dt * 32 + 8 * r + 4 * g;
+            const float4 gt = *reinterpret_cast<const float4 *>(gate + d);
+            float4 v;
+            v.x = (o[dt][4 * r + 0] / z) * sigmoid_ref(gt.x);
+            v.y = (o[dt][4 * r + 1] / z) * sigmoid_ref(gt.y);
+            v.z = (o[dt][4 * r + 2] / z) * sigmoid_ref(gt.z);
+            v.w = (o[dt][4 * r + 3] / z) * sigmoid_ref(gt.w);
+            *reinterpret_cast<float4 *>(orow + d) = v;
+        }
     }
 }
 
@@ -532,7 +721,8 @@ hipError_t launch_gdn_prefill(const GdnParams &p, int batch, int T, float *qinv,
     return hipGetLastError();
 }
 
-hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream) {
+hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream,
+    bool matrix_cores) {
     if (batch < 1 || T < 1 || T > p.max_context || p.heads % p.kv_heads || p.head != p.value ||
         p.rope_dim > p.head || p.head > 256)
         return hipErrorInvalidValue;
@@ -541,24 +731,56 @@ hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, 
         p.rope_dim, p.max_context, p.eps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // the matrix-core kernel: head 64..256 in whole 64s, a GQA group of <= 4
+    // (one wave per q head); it leaves the flagged (sequence, kv head) pairs
+    // to the fp32 kernel below
+    const bool mfma = matrix_cores && p.head % 64 == 0 && p.heads / p.kv_heads <= 4;
+    if (mfma) {
+        const dim3 mgrid((T + kMfmaQ - 1) / kMfmaQ, p.kv_heads, batch);
+        // K tile, V^T tile and four waves' q rows, fp16
+        const size_t mlds = static_cast<size_t>(kMfmaK * (p.head + 8) + p.head * (kMfmaK + 8) + 4 * kMfmaQ * (p.head + 8)) *
+            sizeof(_Float16);
+        switch (p.head) {
+        case 64:
+            hipLaunchKernelGGL(attention_prefill_mfma_kernel<64>, mgrid, dim3(256), mlds, stream, p.q, p.kcache, p.vcache,
+                p.cache_flags, out, T, p.heads, p.kv_heads, p.max_context);
+            break;
+        case 128:
+            hipLaunchKernelGGL(attention_prefill_mfma_kernel<128>, mgrid, dim3(256), mlds, stream, p.q, p.kcache,
+                p.vcache, p.cache_flags, out, T, p.heads, p.kv_heads, p.max_context);
+            break;
+        default:
+            hipLaunchKernelGGL(attention_prefill_mfma_kernel<256>, mgrid, dim3(256), mlds, stream, p.q, p.kcache,
+                p.vcache, p.cache_flags, out, T, p.heads, p.kv_heads, p.max_context);
+            break;
+        }
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const int only_flagged = mfma ? 1 : 0;
     const dim3 grid((T + kQBlock - 1) / kQBlock, p.heads, batch);
     switch (p.head) {
     case 64:
-        hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache, out, T,
-            p.heads, p.kv_heads, p.max_context);
+        hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache,
+            p.cache_flags, only_flagged, out, T, p.heads, p.kv_heads, p.max_context);
         break;
     case 128:
-        hipLaunchKernelGGL(attention_prefill_kernel<128>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache, out, T,
-            p.heads, p.kv_heads, p.max_context);
+        hipLaunchKernelGGL(attention_prefill_kernel<128>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache,
+            p.cache_flags, only_flagged, out, T, p.heads, p.kv_heads, p.max_context);
         break;
     case 256:
-        hipLaunchKernelGGL(attention_prefill_kernel<256>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache, out, T,
-            p.heads, p.kv_heads, p.max_context);
+        hipLaunchKernelGGL(attention_prefill_kernel<256>, grid, dim3(256), 0, stream, p.q, p.kcache, p.vcache,
+            p.cache_flags, only_flagged, out, T, p.heads, p.kv_heads, p.max_context);
         break;
     default: return hipErrorInvalidValue;
     }
-    note_launch("qk_rope_append_kernel grid %d + attention_prefill_kernel<%d> grid %dx%dx%d", batch * T, p.head, grid.x,
-        grid.y, grid.z);
+    if (mfma)
+        note_launch("qk_rope_append_kernel grid %d + attention_prefill_mfma_kernel<%d> grid %dx%dx%d + "
+            "attention_prefill_kernel<%d> (exponent-31 caches only) grid %dx%dx%d", batch * T, p.head,
+            (T + kMfmaQ - 1) / kMfmaQ, p.kv_heads, batch, p.head, grid.x, grid.y, grid.z);
+    else
+        note_launch("qk_rope_append_kernel grid %d + attention_prefill_kernel<%d> grid %dx%dx%d", batch * T, p.head,
+            grid.x, grid.y, grid.z);
     return hipGetLastError();
 }
 
