@@ -431,8 +431,9 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(const float *__r
 // sequence), wave w taking q head kvh * group + w.  Per 32-key tile,
 //   S^T = K Q^T  (v_mfma_f32_32x32x16_f16, keys x queries, q pre-scaled by
 //                 1/sqrt(head) and rounded to fp16; K is the fp16 cache),
-// an online softmax in fp32 (__expf, the running sums rescaled when a
-// query's maximum grows), and
+// an online softmax in fp32 (__expf; the running sums rescaled when a
+// query's reference maximum moves, which it does only by jumps of more than
+// 8), and
 //   O^T += V^T P^T (the same instruction, dims x queries, P rounded to fp16).
 // The accumulator of a 32x32 MFMA holds, in element i of lane l, row
 // 8*(i/4) + 4*(l/32) + i%4 and column l%32: with keys and dims as rows and
@@ -555,30 +556,34 @@ __global__ __launch_bounds__(256) void attention_prefill_mfma_kernel(const float
             tmax = fmaxf(tmax, sc[i]);
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mnew = fmaxf(m, tmax);
-        const float corr = __expf(m - mnew);  // 0 on the first tile (m = -inf)
-        m = mnew;
+        // the reference maximum m of a query moves only when a score exceeds
+        // it by more than 8 (probabilities stay <= e^8, well inside fp16), so
+        // the sums are rescaled on few tiles: the first, and big jumps
+        const bool grow = tmax > m + 8.0f;
+        if (__any(grow)) {
+            const float mnew = grow ? tmax : m;
+            const float corr = __expf(m - mnew);  // 0 on the first tile (m = -inf), 1 where m stays
+            m = mnew;
+            zl *= corr;
+#pragma unroll
+            for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][i] *= corr;
+        }
         float pl[16];
         float zt = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            pl[i] = sc[i] == -__builtin_inff() ? 0.0f : __expf(sc[i] - mnew);
+            pl[i] = sc[i] == -__builtin_inff() ? 0.0f : __expf(sc[i] - m);
             zt += pl[i];
         }
-        zl = zl * corr + zt;
+        zl += zt;
         const half8_t pb0 = {static_cast<_Float16>(pl[0]), static_cast<_Float16>(pl[1]), static_cast<_Float16>(pl[2]),
             static_cast<_Float16>(pl[3]), static_cast<_Float16>(pl[4]), static_cast<_Float16>(pl[5]),
             static_cast<_Float16>(pl[6]), static_cast<_Float16>(pl[7])};
         const half8_t pb1 = {static_cast<_Float16>(pl[8]), static_cast<_Float16>(pl[9]), static_cast<_Float16>(pl[10]),
             static_cast<_Float16>(pl[11]), static_cast<_Float16>(pl[12]), static_cast<_Float16>(pl[13]),
             static_cast<_Float16>(pl[14]), static_cast<_Float16>(pl[15])};
-        // rescale only when a maximum of the wave's queries grew
-        if (__builtin_amdgcn_read_exec() && __any(corr != 1.0f)) {
-#pragma unroll
-            for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[dt][i] *= corr;
-        }
 #pragma unroll
         for (int dt = 0; dt < kDT; ++dt) {
             const _Float16 *vrow = vt + (dt * 32 + col) * kVPitch + 4 * g;
@@ -593,9 +598,13 @@ __global__ __launch_bounds__(256) void attention_prefill_mfma_kernel(const float
         }
     }
     if (!active || qq >= T) return;
-    const float z = zl + __shfl_xor(zl, 32);
+    // the gate: 1 / (1 + e^-g) with the hardware exp and reciprocal (this
+    // mode's tolerance; the exact mode's kernel uses the reference sigmoid),
+    // and one reciprocal of Z per query
+    const float zi = __builtin_amdgcn_rcpf(zl + __shfl_xor(zl, 32));
     const float *gate = qrow + HEAD;
     float *orow = out + ((static_cast<size_t>(s) * T + qq) * heads + h) * HEAD;
+    auto sig = [](float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); };
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt) {
 #pragma unroll
@@ -603,10 +612,10 @@ __global__ __launch_bounds__(256) void attention_prefill_mfma_kernel(const float
             const int d = dt * 32 + 8 * r + 4 * g;
             const float4 gt = *reinterpret_cast<const float4 *>(gate + d);
             float4 v;
-            v.x = (o[dt][4 * r + 0] / z) * sigmoid_ref(gt.x);
-            v.y = (o[dt][4 * r + 1] / z) * sigmoid_ref(gt.y);
-            v.z = (o[dt][4 * r + 2] / z) * sigmoid_ref(gt.z);
-            v.w = (o[dt][4 * r + 3] / z) * sigmoid_ref(gt.w);
+            v.x = (o[dt][4 * r + 0] * zi) * sig(gt.x);
+            v.y = (o[dt][4 * r + 1] * zi) * sig(gt.y);
+            v.z = (o[dt][4 * r + 2] * zi) * sig(gt.z);
+            v.w = (o[dt][4 * r + 3] * zi) * sig(gt.w);
             *reinterpret_cast<float4 *>(orow + d) = v;
         }
     }
