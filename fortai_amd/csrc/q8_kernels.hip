@@ -670,11 +670,20 @@ constexpr int kRingG = 4;  // chunks per ring group
 // the group's row scales into a register ring R groups deep, so R groups are
 // in flight per wave; just before a group is consumed the four waves put it
 // into one of two LDS slots and, after one barrier, all read it from there.
-// Per (row, sequence) the chain is the single-sequence kernel's.
+// With two sequences per wave (NS = 2) the scale products
+// fl(f32(w_scale) * a_scale) of the group (4 blocks per chunk, row and
+// sequence of the workgroup) are then formed once into an LDS table (one
+// float4 per thread) instead of by each of the 8 lanes of a row, and after a
+// second barrier every lane reads its four products with one 16-byte load
+// (with NS = 1 half the threads would fill the table and the extra barrier
+// costs more than the products: measured 18.4 -> 19.9 us).  Per (row, sequence) the chain is the
+// single-sequence kernel's, rounding for rounding.
 template <Epilogue EPI, int GROUPS, int NS>
 __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const BatchMatvecArgs args) {
     constexpr int R = GROUPS < 8 ? GROUPS : 8;  // groups in flight per wave
     constexpr int kSlot = kRingG * 1024 + kRingG * 64;  // quants then scales of one group
+    constexpr bool kTable = NS == 2;
+    constexpr int kTab = kRingG * 4 * NS * 8;            // float4 products of one group [chunk][seq][row]
     extern __shared__ __align__(16) unsigned char lds[];
     const int seq_bytes = args.chunks * 144;
     // this workgroup's block of 4 NS sequences (blockIdx.y)
@@ -682,6 +691,7 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
     const int nseq = min(4 * NS, args.batch - base);
     const int act_bytes = (nseq * seq_bytes + 1023) / 1024 * 1024;
     unsigned char *slots = lds + act_bytes;  // [2][kSlot]
+    float4 *tabs = reinterpret_cast<float4 *>(slots + 2 * kSlot);  // [2][kTab]
 
     const int wg = static_cast<int>(blockIdx.x);
     int sgi = 0;
@@ -745,23 +755,44 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
     // group g + R, then the dots from LDS
     auto step = [&](int g, u32x4_t &q, uint32_t &sw) {
         unsigned char *slot = slots + (g & 1) * kSlot;
+        float4 *tab = tabs + (g & 1) * kTab;
         reinterpret_cast<u32x4_t *>(slot + wave * 1024)[lane] = q;
         if (wave == 0) reinterpret_cast<uint32_t *>(slot + kRingG * 1024)[lane] = sw;
         __syncthreads();  // the group is in LDS (and, the first time, the activations: see below)
         if (g + R < GROUPS) fetch(g + R, q, sw);
+        if (kTable && tid < kTab) {
+            // entry (chunk i, workgroup sequence kk, row rr): the four blocks' products
+            const int rr = tid & 7, kk = (tid >> 3) % (4 * NS), i = tid / (8 * 4 * NS);
+            const int sk = min(base + kk, args.batch - 1) - base;
+            const uint2 sc = reinterpret_cast<const uint2 *>(slot + kRingG * 1024 + i * 64)[rr];
+            float ws[4];
+            scales_f(sc, ws);
+            const float4 as = reinterpret_cast<const float4 *>(
+                lds + static_cast<size_t>(sk) * seq_bytes + static_cast<size_t>(args.chunks) * 128)[g * kRingG + i];
+            tab[tid] = make_float4(ws[0] * as.x, ws[1] * as.y, ws[2] * as.z, ws[3] * as.w);
+        }
+        if constexpr (kTable) __syncthreads();  // the products are in LDS
 #pragma unroll
         for (int i = 0; i < kRingG; ++i) {
             const int c = g * kRingG + i;
             const uint4 qq = reinterpret_cast<const uint4 *>(slot + i * 1024)[lane];
-            const uint2 sc = reinterpret_cast<const uint2 *>(slot + kRingG * 1024 + i * 64)[r];
             float ws[4];
-            scales_f(sc, ws);
+            if constexpr (!kTable) scales_f(reinterpret_cast<const uint2 *>(slot + kRingG * 1024 + i * 64)[r], ws);
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
                 const unsigned char *sbase = lds + static_cast<size_t>(sq[k] - base) * seq_bytes;
                 const uint4 a = reinterpret_cast<const uint4 *>(sbase)[c * 8 + l];
-                const float4 as = reinterpret_cast<const float4 *>(sbase + static_cast<size_t>(args.chunks) * 128)[c];
-                acc[k] = dot_chunk_f(qq, ws, a, as, acc[k]);
+                if constexpr (kTable) {
+                    const float4 pr = tab[(i * 4 * NS + wave + 4 * k) * 8 + r];
+                    const float4 d = sdot4x4_f(qq, a);
+                    acc[k] = __builtin_fmaf(pr.x, d.x, acc[k]);
+                    acc[k] = __builtin_fmaf(pr.y, d.y, acc[k]);
+                    acc[k] = __builtin_fmaf(pr.z, d.z, acc[k]);
+                    acc[k] = __builtin_fmaf(pr.w, d.w, acc[k]);
+                } else {
+                    const float4 as = reinterpret_cast<const float4 *>(sbase + static_cast<size_t>(args.chunks) * 128)[c];
+                    acc[k] = dot_chunk_f(qq, ws, a, as, acc[k]);
+                }
             }
         }
     };
@@ -1102,8 +1133,8 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
         // would keep the workgroup at one per CU
         const int ns = static_cast<size_t>(std::min(batch, 8)) * chunks * 144 > 48 * 1024 ? 1 : 2;
         const int per_block = 4 * ns, seq_blocks = (batch + per_block - 1) / per_block;
-        const size_t ring_lds =
-            (static_cast<size_t>(std::min(batch, per_block)) * chunks * 144 + 1023) / 1024 * 1024 + 2 * kSlot;
+        const size_t ring_lds = (static_cast<size_t>(std::min(batch, per_block)) * chunks * 144 + 1023) / 1024 * 1024 +
+            2 * kSlot + (ns == 2 ? 2 * static_cast<size_t>(kRingG) * per_block * 8 * 16 : 0);
         if (ring_lds > 160 * 1024) return hipErrorInvalidValue;
 #define FORTAI_RING(E, G)                                                                                          \
     do {                                                                                                          \
