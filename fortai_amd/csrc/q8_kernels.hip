@@ -467,6 +467,13 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
     const int seq_bytes = args.chunks * 144;
     const int act_bytes = (args.batch * seq_bytes + 1023) / 1024 * 1024;  // whole 1 KiB load blocks
     float *epi = reinterpret_cast<float *>(lds + act_bytes);  // [8][32]
+    // the gate/up pair with one chunk per group: each wave forms the chunk's
+    // scale products fl(f32(w_scale) * a_scale) once per (matrix, row,
+    // sequence, block) -- four per lane -- into its own LDS table, instead of
+    // every lane of a row forming all of them; LDS operations of one wave
+    // complete in order, so the wave reads them back without a barrier
+    constexpr bool kTable = kPair && G == 1 && NS == 4;
+    float *ptab = epi + kMaxBatch * 32 + (static_cast<int>(threadIdx.x) >> 6) * 2 * 8 * NS * 4;  // [2][8][NS][4]
 
     const int wg = static_cast<int>(blockIdx.x);
     int sgi = 0;
@@ -547,6 +554,42 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
     // sequence's chain still runs chunk by chunk in order)
     auto consume = [&](int c0, const uint4 (&q)[G], const uint2 (&sc)[G], const uint4 (&q2)[kPair ? G : 1],
                        const uint2 (&sc2)[kPair ? G : 1]) {
+        if constexpr (kTable) {
+            // lane (r, l): sequence l / 2, blocks 2 (l % 2) and 2 (l % 2) + 1, both matrices
+            {
+                const int ks = l >> 1, j0 = (l & 1) * 2;
+                const unsigned char *sb = lds + static_cast<size_t>(sq[ks]) * seq_bytes;
+                const float4 a4 = reinterpret_cast<const float4 *>(sb + static_cast<size_t>(args.chunks) * 128)[c0];
+                float ws[4], ws2[4];
+                scales_f(sc[0], ws);
+                scales_f(sc2[0], ws2);
+                const float a0 = j0 == 0 ? a4.x : a4.z, a1 = j0 == 0 ? a4.y : a4.w;
+                const float w0 = j0 == 0 ? ws[0] : ws[2], w1 = j0 == 0 ? ws[1] : ws[3];
+                const float v0 = j0 == 0 ? ws2[0] : ws2[2], v1 = j0 == 0 ? ws2[1] : ws2[3];
+                *reinterpret_cast<float2 *>(ptab + ((0 * 8 + r) * NS + ks) * 4 + j0) = make_float2(w0 * a0, w1 * a1);
+                *reinterpret_cast<float2 *>(ptab + ((1 * 8 + r) * NS + ks) * 4 + j0) = make_float2(v0 * a0, v1 * a1);
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                const unsigned char *sbase = lds + static_cast<size_t>(sq[k]) * seq_bytes;
+                const uint4 a = reinterpret_cast<const uint4 *>(sbase)[c0 * 8 + l];
+                const float4 p1 = *reinterpret_cast<const float4 *>(ptab + ((0 * 8 + r) * NS + k) * 4);
+                const float4 p2 = *reinterpret_cast<const float4 *>(ptab + ((1 * 8 + r) * NS + k) * 4);
+                const float4 d = sdot4x4_f(q[0], a);
+                const float4 d2 = sdot4x4_f(q2[0], a);
+                acc[k] = __builtin_fmaf(p1.x, d.x, acc[k]);
+                acc[k] = __builtin_fmaf(p1.y, d.y, acc[k]);
+                acc[k] = __builtin_fmaf(p1.z, d.z, acc[k]);
+                acc[k] = __builtin_fmaf(p1.w, d.w, acc[k]);
+                acc2[k] = __builtin_fmaf(p2.x, d2.x, acc2[k]);
+                acc2[k] = __builtin_fmaf(p2.y, d2.y, acc2[k]);
+                acc2[k] = __builtin_fmaf(p2.z, d2.z, acc2[k]);
+                acc2[k] = __builtin_fmaf(p2.w, d2.w, acc2[k]);
+            }
+            __builtin_amdgcn_wave_barrier();
+            return;
+        }
         float ws[G][4], ws2[kPair ? G : 1][4];
 #pragma unroll
         for (int i = 0; i < G; ++i) {
@@ -1163,7 +1206,9 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
             ns, ring_grid, seq_blocks);
         return hipGetLastError();
     }
-    if (epilogue == Epilogue::SILU_PAIR) return launch_batch_g<Epilogue::SILU_PAIR, 2, 8>(args, grid, lds, stream);
+    // the pair's per-wave scale-product tables: 8 waves x [2][8][4][4] floats
+    if (epilogue == Epilogue::SILU_PAIR)
+        return launch_batch_g<Epilogue::SILU_PAIR, 2, 8>(args, grid, lds + 8 * 2 * 8 * 4 * 4 * sizeof(float), stream);
     if (epilogue == Epilogue::STORE) {
         if (split == 1) return launch_batch_g<Epilogue::STORE, 1>(args, grid, lds, stream);
         if (split == 2) return launch_batch_g<Epilogue::STORE, 2>(args, grid, lds, stream);
