@@ -89,6 +89,29 @@ def test_batch_generate_trace_matches_oracle(model_paths, oracle):
         m.close()
 
 
+@pytest.mark.parametrize("name,batch,steps", [("qwen35-tiny", 3, 700), ("qwen35-4b-short", 2, 300)])
+def test_batch_long_trace_matches_single_sequence(model_paths, name, batch, steps):
+    """Long traces from filled caches: past 256 positions the batch's exact
+    attention stages the values in several tiles (the last one partial) while
+    the single-sequence decoder chains 256-position segments; both keep the
+    reference's summation orders, so the traces and the next step's logits
+    must be identical."""
+    m = Qwen35Hip(model_paths[name], max_context=1024, batch=batch)
+    try:
+        starts = [9, 100, 4000][:batch]
+        m.batch.reset()
+        got = m.batch.generate(starts, [0] * batch, steps)
+        nxt = m.batch.forward(got[:, -1], [steps] * batch)
+        for s, t in enumerate(starts):
+            m.decoder.reset()
+            want = m.decoder.generate(t, 0, steps)
+            assert got[s].tolist() == want.tolist(), f"sequence {s}"
+            assert m.decoder.forward(int(want[-1]), steps) == int(nxt[s])
+            assert np.array_equal(m.batch.logits[s].view(np.uint32), m.decoder.logits.view(np.uint32)), f"sequence {s}"
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("rows,width,batch", [(3584, 1024, 8), (13, 96, 3), (2560, 9216, 8), (12352, 2560, 5),
                                               (1024, 3584, 1)])
 def test_batch_matvec_bit_identical(ctx, oracle, rows, width, batch):

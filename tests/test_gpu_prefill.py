@@ -59,9 +59,12 @@ def decode_prompt(m, prompt):
 
 @pytest.mark.parametrize("name,batch,lengths", [("qwen35-tiny", 4, (17, 24, 33, 48, 64, 70)),
                                                 ("qwen35-tiny-q8emb", 4, (33, 65)),
-                                                ("qwen35-4b-short", 8, (64,))])
+                                                ("qwen35-4b-short", 8, (64,)),
+                                                # many 32-key tiles of the matrix-core attention
+                                                ("qwen35-tiny", 2, (511,)),
+                                                ("qwen35-4b-short", 2, (300,))])
 def test_prefill_close_to_token_by_token_decode(paths, name, batch, lengths):
-    m = Qwen35Hip(paths[name], max_context=128, batch=batch)
+    m = Qwen35Hip(paths[name], max_context=max(128, max(lengths) + 8), batch=batch)
     errs, agree, total = [], 0, 0
     try:
         for T in lengths:
