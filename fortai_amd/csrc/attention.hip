@@ -57,7 +57,9 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     const int pos = *p.position;
     if (pos < 0 || pos >= p.max_context) return;  // never index past the cache
     const int positions = pos + 1, nblk_max = (p.max_context + ea::kPosBlock - 1) / ea::kPosBlock;
-    const int kvh = static_cast<int>(blockIdx.x) / nblk_max, b = static_cast<int>(blockIdx.x) % nblk_max;
+    // block-major: the blocks that hold positions are dispatched first, the
+    // ones past the current position (which only read it and exit) last
+    const int kvh = static_cast<int>(blockIdx.x) % p.kv_heads, b = static_cast<int>(blockIdx.x) / p.kv_heads;
     const int p0 = b * ea::kPosBlock;
     if (p0 >= positions) return;
     const int n = min(ea::kPosBlock, positions - p0);
