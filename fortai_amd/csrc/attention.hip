@@ -511,7 +511,8 @@ __global__ __launch_bounds__(ea::kThreads) void attention_split_kernel(const Att
     const int positions = pos + 1;
     if (positions <= p.exact_max) return;  // the exact kernel covers this position
     const int nmax = (p.max_context + kChunk - 1) / kChunk;
-    const int kvh = static_cast<int>(blockIdx.x) / nmax, c = static_cast<int>(blockIdx.x) % nmax;
+    // chunk-major, like the scores kernel: chunks holding positions dispatch first
+    const int kvh = static_cast<int>(blockIdx.x) % p.kv_heads, c = static_cast<int>(blockIdx.x) / p.kv_heads;
     const int p0 = c * kChunk;
     if (p0 >= positions) return;
     const int n = min(kChunk, positions - p0);
