@@ -137,21 +137,30 @@ def traffic_from_profile(name: str):
         return json.load(f).get("traffic_bytes_per_launch")
 
 
-def traffic_probe(reps: int = 5) -> None:
+def traffic_probe(reps: int = 5, decode_model: str = None) -> None:
     """Launches for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes that
-    price the LM head's HBM traffic (no model file, no timing):
+    price each kernel's HBM traffic (direct launches, no graphs, no timing):
     * calibration: fortai_hip_qwen35_add_device over 2^26 floats, algorithmic
       traffic 512 MiB read + 256 MiB written per launch;
-    * the fp16 LM head with fused argmax over a random 248320 x 1024 table,
-      the dominant kernel's real shape."""
+    * the fp16 LM head with fused argmax over a random 248320 x 1024 table;
+    * the 3584 x 1024 Q8_0 matvec (quantize fused) over 275
+      distinct weight copies (1.07 GB, beyond the 256 MB Infinity Cache);
+    * BASELINE config 3 at L = 4096: append + scores + exact output kernels;
+    * BASELINE config 2: the GDN conv1d + delta-rule step;
+    * with decode_model: 8 decode steps of that GGUF with direct launches
+      (every matvec, GDN, attention, LM head kernel of the step)."""
+    import ctypes as C
     import numpy as np
     from fortai_amd import backend as B
+    from fortai_amd import synth
     ctx = B.Context(0)
     n = 1 << 26
     a, b, o = ctx.alloc(4 * n), ctx.alloc(4 * n), ctx.alloc(4 * n)
     for _ in range(reps):
         ctx.call("fortai_hip_qwen35_add_device", ctx.h, a.ptr, b.ptr, o.ptr, n)
     ctx.synchronize()
+    for buf in (a, b, o):
+        buf.free()
     rows, width = 248320, 1024
     rng = np.random.default_rng(7)
     w = (rng.standard_normal(rows * width, dtype=np.float32) * np.float32(0.02)).astype(np.float16)
@@ -162,7 +171,119 @@ def traffic_probe(reps: int = 5) -> None:
     for _ in range(reps):
         ctx.call("fortai_hip_f16_matvec_device", ctx.h, lm.h, x.ptr, width, logits.ptr, rows, tok.ptr)
     ctx.synchronize()
-    log("traffic probe: 5 add launches (2^26 floats) and 5 LM head launches done")
+    for buf in (x, logits, tok):
+        buf.free()
+    lm.free()
+    log("traffic probe: add (2^26 floats) and LM head launches done")
+    # config 1 over rotating copies
+    wq, xv = synth.matvec_inputs()
+    mats = [B.Q8Weights(ctx, wq, 3584, 1024) for _ in range(275)]
+    dx, dout = ctx.upload_array(xv), ctx.alloc(3584 * 4)
+    for m in mats:
+        ctx.call("fortai_hip_q8_matvec_device_f32", ctx.h, m.h, dx.ptr, 1024, dout.ptr, 3584)
+    ctx.synchronize()
+    for m in mats:
+        m.free()
+    dx.free()
+    dout.free()
+    log("traffic probe: 275 config-1 matvecs done")
+    # config 3 at L = 4096
+    heads, kvh, head, H, L = 8, 2, 256, 1024, 4096
+    ws = [_q8(ctx, rng, heads * 2 * head, H), _q8(ctx, rng, kvh * head, H), _q8(ctx, rng, kvh * head, H),
+          _q8(ctx, rng, H, heads * head)]
+    A = B.Attention(ctx, *ws, (1 + 0.05 * rng.standard_normal(head)).astype(np.float32),
+                    (1 + 0.05 * rng.standard_normal(head)).astype(np.float32), heads, kvh, head, head, L, 64,
+                    1.0e7, 1e-6)
+    nkv = L * kvh * head
+    A.set_cache(rng.standard_normal(nkv).astype(np.float16).view(np.uint16),
+                rng.standard_normal(nkv).astype(np.float16).view(np.uint16), L)
+    dq = ctx.upload_array(rng.standard_normal(heads * 2 * head).astype(np.float32))
+    dk = ctx.upload_array(rng.standard_normal(kvh * head).astype(np.float32))
+    dv = ctx.upload_array(rng.standard_normal(kvh * head).astype(np.float32))
+    do = ctx.alloc(heads * head * 4)
+    ctx.set_position(L - 1)
+    for _ in range(reps):
+        ctx.call("fortai_hip_qwen35_attention_core_device", A.h, dq.ptr, dk.ptr, dv.ptr, do.ptr)
+    ctx.synchronize()
+    for buf in (dq, dk, dv, do):
+        buf.free()
+    A.free()
+    for w_ in ws:
+        w_.free()
+    log("traffic probe: attention at L = 4096 done")
+    # config 2
+    heads, head, kernel = 16, 128, 4
+    inner = heads * head
+    conv = 2 * head * heads + inner
+    ws = [_q8(ctx, rng, conv, H), _q8(ctx, rng, inner, H), _q8(ctx, rng, heads, H), _q8(ctx, rng, heads, H),
+          _q8(ctx, rng, H, inner)]
+    layer = B.Recurrent(ctx, *ws, (rng.standard_normal(conv * kernel) * 0.1).astype(np.float32), conv, kernel,
+                        -np.exp(rng.standard_normal(heads) * 0.5).astype(np.float32),
+                        rng.standard_normal(heads).astype(np.float32), np.ones(head, np.float32), head, heads, heads,
+                        head, inner, 1e-6)
+    layer.set_state((rng.standard_normal(heads * head * head) * 0.02).astype(np.float32),
+                    np.zeros((kernel - 1) * conv, np.float32))
+    qkv = ctx.upload_array(rng.standard_normal(conv).astype(np.float32))
+    ab = ctx.upload_array(rng.standard_normal(2 * heads).astype(np.float32))
+    out = ctx.alloc(inner * 4)
+    for _ in range(reps):
+        ctx.call("fortai_hip_qwen35_recurrent_core_device", layer.h, qkv.ptr, ab.ptr,
+                 C.c_void_p(ab.ptr.value + heads * 4), out.ptr)
+    ctx.synchronize()
+    for buf in (qkv, ab, out):
+        buf.free()
+    layer.free()
+    for w_ in ws:
+        w_.free()
+    ctx.close()
+    log("traffic probe: GDN step done")
+    if decode_model:
+        os.environ["FORTAI_HIP_DECODER_GRAPH"] = "0"
+        from fortai_amd.qwen35 import Qwen35Hip
+        model = Qwen35Hip(decode_model, max_context=256)
+        model.reset()
+        model.generate(START_TOKEN, 8, 0)
+        model.ctx.synchronize()
+        model.close()
+        log("traffic probe: 8 direct-launch decode steps done")
+
+
+def pmc_summary(fetch_dir: str, write_dir: str) -> None:
+    """Per-kernel HBM traffic from the two rocprofv3 --pmc passes of
+    --traffic-probe (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each
+    scaled by what the same counter reads for the calibration add kernel
+    (512 MiB read, 256 MiB written).  Prints a JSON document."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    def read(directory, counter):
+        paths = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+        if not paths:
+            raise SystemExit(f"no counter_collection.csv under {directory}")
+        per = defaultdict(list)
+        with open(paths[0]) as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name", counter) != counter:
+                    continue
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("fortai_hip::", "")
+                name = name.replace("void ", "").replace("(Prologue)", "P").replace("(Epilogue)", "E").split("(")[0]
+                per[name].append(float(r["Counter_Value"]))
+        return per
+
+    fetch, write = read(fetch_dir, "FETCH_SIZE"), read(write_dir, "WRITE_SIZE")
+    cal = [k for k in fetch if k.startswith("add_kernel")][0]
+    fscale = 536870912 / (sum(fetch[cal]) / len(fetch[cal]) * 1024)
+    wscale = 268435456 / (sum(write[cal]) / len(write[cal]) * 1024)
+    kernels = {}
+    for k in sorted(fetch):
+        f_ = fetch[k]
+        w_ = write.get(k, [0.0])
+        kernels[k] = {"dispatches": len(f_), "fetch_kib_avg": round(sum(f_) / len(f_), 3),
+                      "write_kib_avg": round(sum(w_) / len(w_), 3),
+                      "traffic_bytes_avg": int(sum(f_) / len(f_) * 1024 * fscale + sum(w_) / len(w_) * 1024 * wscale)}
+    print(json.dumps({"calibration": {"kernel": cal, "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4)},
+                      "kernels": kernels}, indent=1))
 
 
 def bench_matvec(model, copies: int = 275, reps: int = 4):
@@ -469,6 +590,10 @@ def main() -> int:
                     help="print only the config 5 figures (for kernel tracing of the batch-8 decode)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the kernels the --pmc traffic passes measure (see traffic_probe)")
+    ap.add_argument("--probe-decode", action="store_true",
+                    help="with --traffic-probe: also run 8 direct-launch decode steps of the 0.8B model")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print per-kernel HBM traffic from the FETCH_SIZE and WRITE_SIZE passes, then exit")
     ap.add_argument("--no-graph", action="store_true",
                     help="enqueue each decode step's kernels directly instead of replaying the HIP graph "
                          "(for kernel tracing)")
@@ -486,7 +611,10 @@ def main() -> int:
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     if args.traffic_probe:
-        traffic_probe()
+        traffic_probe(decode_model=model_path(args) if args.probe_decode else None)
+        return 0
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
         return 0
     if args.config5_only:
         print(json.dumps({"config5": bench_config5()}), flush=True)

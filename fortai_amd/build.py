@@ -22,16 +22,34 @@ HIP_FLAGS = [
 ]
 
 
-def build_library(verbose: bool = False) -> str:
+def build_library(verbose: bool = False, jobs: int = 0) -> str:
+    """Each source is compiled to its own object in parallel (no relocatable
+    device code: no kernel or device symbol crosses a source file), then
+    linked into the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
     os.makedirs(os.path.dirname(LIB), exist_ok=True)
+    objdir = os.path.join(os.path.dirname(LIB), "obj")
+    os.makedirs(objdir, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+
+    def compile_one(src):
+        obj = os.path.join(objdir, os.path.basename(src).replace(".hip", ".o"))
+        res = subprocess.run([HIPCC, *compile_flags, "-c", src, "-o", obj], capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {os.path.basename(src)}:\n" + res.stderr)
+        if verbose and res.stderr:
+            print(res.stderr)
+        return obj
+
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 1)), 8)
+    with ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(compile_one, sources))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, *sources, "-o", tmp]
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    res = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp],
+                         capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + res.stderr)
-    if verbose and res.stderr:
-        print(res.stderr)
+        raise RuntimeError("hipcc link failed:\n" + res.stderr)
     os.replace(tmp, LIB)
     return LIB
 

@@ -732,18 +732,20 @@ hipError_t launch_gdn_prefill(const GdnParams &p, int batch, int T, float *qinv,
 
 hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream,
     bool matrix_cores) {
+    // every head width a kernel below is instantiated for; checked before
+    // anything is enqueued, so an unsupported layer launches nothing
     if (batch < 1 || T < 1 || T > p.max_context || p.heads % p.kv_heads || p.head != p.value ||
-        p.rope_dim > p.head || p.head > 256)
+        p.rope_dim > p.head || (p.head != 64 && p.head != 128 && p.head != 256))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(qk_rope_append_kernel, dim3(batch * T), dim3(256), 0, stream, const_cast<float *>(p.q), p.k,
         p.v, p.q_norm, p.k_norm, p.rope, p.kcache, p.vcache, p.cache_flags, T, p.heads, p.kv_heads, p.head, p.value,
         p.rope_dim, p.max_context, p.eps);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // the matrix-core kernel: head 64..256 in whole 64s, a GQA group of <= 4
+    // the matrix-core kernel: head 64, 128 or 256, a GQA group of <= 4
     // (one wave per q head); it leaves the flagged (sequence, kv head) pairs
     // to the fp32 kernel below
-    const bool mfma = matrix_cores && p.head % 64 == 0 && p.heads / p.kv_heads <= 4;
+    const bool mfma = matrix_cores && p.heads / p.kv_heads <= 4;
     if (mfma) {
         const dim3 mgrid((T + kMfmaQ - 1) / kMfmaQ, p.kv_heads, batch);
         // K tile, V^T tile and four waves' q rows, fp16
@@ -758,7 +760,7 @@ hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, 
             hipLaunchKernelGGL(attention_prefill_mfma_kernel<128>, mgrid, dim3(256), mlds, stream, p.q, p.kcache,
                 p.vcache, p.cache_flags, out, T, p.heads, p.kv_heads, p.max_context);
             break;
-        default:
+        case 256:
             hipLaunchKernelGGL(attention_prefill_mfma_kernel<256>, mgrid, dim3(256), mlds, stream, p.q, p.kcache,
                 p.vcache, p.cache_flags, out, T, p.heads, p.kv_heads, p.max_context);
             break;

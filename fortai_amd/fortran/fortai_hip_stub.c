@@ -1,8 +1,12 @@
 /* fortai_hip_stub.c -- weak stand-ins for every entry point of
  * include/fortai_hip_backend.h, for FortAI builds that link the HIP binding
  * module without libfortai_hip.so (as src/backend/cpu/fortai_cuda_stub.c does
- * for the CUDA binding).  Every call fails with FORTAI_HIP_RUNTIME_ERROR and
- * last_error says why; linking the real library overrides all of them. */
+ * for the CUDA binding).  As the reference's stub
+ * (src/backend/cpu/fortai_cuda_stub.c:13-23) does: a create or upload sets
+ * its out-handle to NULL and fails with FORTAI_HIP_RUNTIME_ERROR, every
+ * destroy (NULL included) succeeds, every other call fails with
+ * FORTAI_HIP_RUNTIME_ERROR and last_error says why.  Linking the real library
+ * overrides all of them. */
 #include "fortai_hip_backend.h"
 
 #define FORTAI_HIP_WEAK __attribute__((weak))
@@ -12,14 +16,14 @@ static const char *const fortai_hip_stub_message = "FortAI was built without the
 FORTAI_HIP_WEAK int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context)
 {
     (void)device;
-    (void)context;
+    if (context) *context = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_q8_context_destroy(fortai_hip_q8_context *context)
 {
     (void)context;
-    return FORTAI_HIP_RUNTIME_ERROR;
+    return FORTAI_HIP_OK;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_q8_context_set_position(fortai_hip_q8_context *context, int position)
@@ -73,21 +77,21 @@ FORTAI_HIP_WEAK int fortai_hip_q8_weights_upload(fortai_hip_q8_context *context,
     (void)weight_bytes;
     (void)rows;
     (void)width;
-    (void)weights;
+    if (weights) *weights = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_q8_weights_destroy(fortai_hip_q8_weights *weights)
 {
     (void)weights;
-    return FORTAI_HIP_RUNTIME_ERROR;
+    return FORTAI_HIP_OK;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_q8_device_buffer_create(fortai_hip_q8_context *context, size_t bytes, void **device_buffer)
 {
     (void)context;
     (void)bytes;
-    (void)device_buffer;
+    if (device_buffer) *device_buffer = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
@@ -95,7 +99,7 @@ FORTAI_HIP_WEAK int fortai_hip_q8_device_buffer_destroy(fortai_hip_q8_context *c
 {
     (void)context;
     (void)device_buffer;
-    return FORTAI_HIP_RUNTIME_ERROR;
+    return FORTAI_HIP_OK;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_q8_device_buffer_upload(fortai_hip_q8_context *context, void *device_buffer, const void *host_data, size_t bytes)
@@ -296,14 +300,14 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_recurrent_create(fortai_hip_q8_context *co
     (void)head_size;
     (void)inner_size;
     (void)norm_epsilon;
-    (void)layer;
+    if (layer) *layer = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_qwen35_recurrent_destroy(fortai_hip_qwen35_recurrent *layer)
 {
     (void)layer;
-    return FORTAI_HIP_RUNTIME_ERROR;
+    return FORTAI_HIP_OK;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_qwen35_recurrent_reset(fortai_hip_qwen35_recurrent *layer)
@@ -352,14 +356,14 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *co
     (void)rope_dimension;
     (void)rope_base;
     (void)norm_epsilon;
-    (void)layer;
+    if (layer) *layer = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_qwen35_attention_destroy(fortai_hip_qwen35_attention *layer)
 {
     (void)layer;
-    return FORTAI_HIP_RUNTIME_ERROR;
+    return FORTAI_HIP_OK;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_qwen35_attention_reset(fortai_hip_qwen35_attention *layer)
@@ -392,14 +396,14 @@ FORTAI_HIP_WEAK int fortai_hip_f16_weights_upload(fortai_hip_q8_context *context
     (void)weight_bytes;
     (void)rows;
     (void)width;
-    (void)weights;
+    if (weights) *weights = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_f16_weights_destroy(fortai_hip_f16_weights *weights)
 {
     (void)weights;
-    return FORTAI_HIP_RUNTIME_ERROR;
+    return FORTAI_HIP_OK;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_f16_matvec_device(fortai_hip_q8_context *context, const fortai_hip_f16_weights *weights, const void *device_activation, size_t activation_elements, void *device_output, size_t output_elements, void *device_token)
@@ -529,14 +533,14 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *cont
     (void)output_q8;
     (void)max_context;
     (void)norm_epsilon;
-    (void)decoder;
+    if (decoder) *decoder = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *decoder)
 {
     (void)decoder;
-    return FORTAI_HIP_RUNTIME_ERROR;
+    return FORTAI_HIP_OK;
 }
 
 FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_reset(fortai_hip_qwen35_decoder *decoder)
@@ -595,7 +599,7 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_deco
 FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits)
 {
     (void)decoder;
-    (void)device_logits;
+    if (device_logits) *device_logits = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
@@ -691,6 +695,7 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *bat
 FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batch_decoder, void **device_logits)
 {
     (void)batch_decoder; (void)device_logits;
+    if (device_logits) *device_logits = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 

@@ -168,6 +168,24 @@ def test_weak_stub_covers_the_header(tmp_path):
     assert lib.fortai_hip_q8_context_create(0, ctypes.byref(h)) == 2
     lib.fortai_hip_q8_last_error.restype = ctypes.c_char_p
     assert b"without the HIP backend" in lib.fortai_hip_q8_last_error(None)
+    # as src/backend/cpu/fortai_cuda_stub.c:13-23: a failed create leaves its
+    # out-handle NULL (a caller's later destroy is then a no-op) ...
+    for name, nargs in (("fortai_hip_q8_context_create", 1), ("fortai_hip_q8_weights_upload", 5),
+                        ("fortai_hip_f16_weights_upload", 5), ("fortai_hip_q8_device_buffer_create", 2),
+                        ("fortai_hip_q8_weights_upload_packed", 5)):
+        h = ctypes.c_void_p(0x1234)
+        fn = getattr(lib, name)
+        fn.argtypes = [ctypes.c_void_p] * nargs + [ctypes.POINTER(ctypes.c_void_p)]
+        assert fn(*([None] * nargs), ctypes.byref(h)) == 2, name
+        assert h.value is None, name
+    # ... and every destroy succeeds, NULL included
+    destroys = [s for s in header_symbols() if s.endswith("_destroy")]
+    assert len(destroys) >= 8
+    for name in destroys:
+        fn = getattr(lib, name)
+        nargs = 2 if name == "fortai_hip_q8_device_buffer_destroy" else 1
+        fn.argtypes = [ctypes.c_void_p] * nargs
+        assert fn(*([None] * nargs)) == 0, name
 
 
 def test_pack_key_and_cache_path(tmp_path):
