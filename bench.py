@@ -629,7 +629,7 @@ def main() -> int:
         kernels = {"gdn_step": bench_gdn(), "attention": bench_attention()}
     d = model.d
     model_cfg5 = None
-    decoder = "persistent (one launch per token)" if model.decoder.persistent else "HIP graph of per-op kernels"
+    decoder = "HIP graph of per-op kernels, replayed once per token"
     step_bytes = bytes_per_token(d, args.ctx - args.steps // 2)
     decode_gbps = step_bytes * tok_s / 1e9
     model.close()

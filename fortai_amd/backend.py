@@ -96,8 +96,6 @@ _SIGNATURES = {
     "fortai_hip_qwen35_decoder_replay": [_vp, _i],
     "fortai_hip_qwen35_decoder_logits": [_vp, _vpp],
     "fortai_hip_qwen35_decoder_status": [_vp],
-    "fortai_hip_qwen35_decoder_persistent": [_vp],
-    "fortai_hip_qwen35_decoder_phase_times": [_vp, _vp, C.c_size_t],
     "fortai_hip_qwen35_decoder_plan": [_vp, _vp, _sz, C.POINTER(C.c_size_t)],
     "fortai_hip_qwen35_batch_plan": [_vp, _i, _vp, _sz, C.POINTER(C.c_size_t)],
     "fortai_hip_qwen35_batch_create": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp,
@@ -424,12 +422,8 @@ class Decoder:
         self.ctx.call("fortai_hip_qwen35_decoder_replay", self.h, steps)
 
     def check(self) -> None:
-        """Wait for the queued steps; raise if a persistent step failed."""
+        """Wait for the queued steps; raise if one failed."""
         self.ctx.call("fortai_hip_qwen35_decoder_status", self.h)
-
-    @property
-    def persistent(self) -> bool:
-        return self.ctx.lib.fortai_hip_qwen35_decoder_persistent(self.h) == 1
 
     def plan(self):
         """The launches of one step: [(operation, kernel, batch)]."""

@@ -25,6 +25,20 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 256;  // positions per split-K chunk (long contexts)
 
+// The per-sequence workspace behind AttentionParams::partial, in floats:
+//   scores [heads][max_context] | e values [heads][max_context] |
+//   Z tables [heads][z_segments(max_context)][kZStride]
+__host__ __device__ inline size_t workspace_floats(int heads, int max_context) {
+    return static_cast<size_t>(heads) * max_context * 2 +
+        static_cast<size_t>(heads) * ea::z_segments(max_context) * ea::kZStride;
+}
+__device__ __forceinline__ float *evals_of(const AttentionParams &p) {
+    return p.partial + static_cast<size_t>(p.heads) * p.max_context;
+}
+__device__ __forceinline__ float *ztab_of(const AttentionParams &p) {
+    return p.partial + static_cast<size_t>(p.heads) * p.max_context * 2;
+}
+
 // Sequence s of a batch (blockIdx.y): every per-sequence buffer is laid out
 // [batch][...] with the single-sequence size, and position[s] is its own.
 __device__ __forceinline__ AttentionParams attention_seq(AttentionParams p, int s) {
@@ -34,7 +48,7 @@ __device__ __forceinline__ AttentionParams attention_seq(AttentionParams p, int 
     p.v += static_cast<size_t>(s) * p.kv_heads * p.value;
     p.kcache += static_cast<size_t>(s) * p.max_context * p.kv_heads * p.head;
     p.vcache += static_cast<size_t>(s) * p.max_context * p.kv_heads * p.value;
-    p.partial += static_cast<size_t>(s) * p.heads * p.max_context;
+    p.partial += static_cast<size_t>(s) * workspace_floats(p.heads, p.max_context);
     p.cache_flags += static_cast<size_t>(s) * p.kv_heads;
     p.out += static_cast<size_t>(s) * p.heads * p.value;
     p.position += s;
@@ -140,35 +154,211 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     FORTAI_ATT_MARK(11);
 }
 
+// e_p = expf(s_p - m) of one kSeg-position segment of one head, stored for
+// the output kernels, and the segment's Z candidate table (attention_exact.h,
+// resolve_z): thread c runs the segment's left-to-right chain from candidate
+// starting sum c.  grid (heads x z_segments(max_context), batch), segments
+// holding positions dispatched first.
+__global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const AttentionParams p_batch) {
+    const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
+    __shared__ __align__(16) float e_seg[ea::kSeg];
+    __shared__ double dred[2 * ea::kWaves];
+    __shared__ float fred[ea::kWaves];
+    static_assert(ea::kZCand == ea::kThreads && ea::kSeg == ea::kThreads, "one candidate and one position per thread");
+    const int pos = *p.position;
+    const int h = static_cast<int>(blockIdx.x) % p.heads, k = static_cast<int>(blockIdx.x) / p.heads;
+    const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
+    // up to kHeld * 256 positions the scores are loaded in the position's
+    // round trip (clamped to the cache; those past the position are masked)
+    constexpr int kHeld = 32;
+    const int cap = p.max_context < p.exact_max ? p.max_context : p.exact_max;
+    const bool held = cap <= kHeld * ea::kThreads;
+    float x[kHeld];
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < kHeld; ++i)
+            if (i * ea::kThreads < cap) x[i] = sc[min(tid + i * ea::kThreads, cap - 1)];
+    }
+    if (pos < 0 || pos >= p.max_context) return;
+    const int n = pos + 1;
+    if (n > p.exact_max) return;  // the split-K kernels cover this position
+    const int p0 = k * ea::kSeg;
+    if (p0 >= n) return;
+    const int cnt = min(ea::kSeg, n - p0);
+    // m = max over every score (any order gives the same value)
+    constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
+    float m = kLowest;
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < kHeld; ++i)
+            if (tid + i * ea::kThreads < n) m = fmaxf(m, x[i]);
+    } else {
+        for (int i = tid; i < n; i += ea::kThreads) m = fmaxf(m, sc[i]);
+    }
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) fred[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    // the segment's own e values, exactly as the reference computes them
+    const float e = tid < cnt ? expf_libm(sc[p0 + tid] - m) : -0.0f;  // -0 leaves a sum unchanged
+    e_seg[tid] = e;
+    if (tid < cnt) evals_of(p)[static_cast<size_t>(h) * p.max_context + p0 + tid] = e;
+    // the estimates of the running sums entering this segment and the next
+    // (a fast exp; the next segment's workgroup forms the same sum the same way)
+    double est = 0.0, est_next = 0.0;
+    if (held) {
+#pragma unroll
+        for (int i = 0; i < kHeld; ++i) {
+            const int q = tid + i * ea::kThreads;
+            if (q < p0 + ea::kSeg) {
+                const double t = static_cast<double>(__expf(x[i] - m));
+                if (q < p0) est += t;
+                est_next += t;
+            }
+        }
+    } else {
+        for (int q = tid; q < p0 + ea::kSeg; q += ea::kThreads) {
+            const double t = static_cast<double>(__expf(sc[q] - m));
+            if (q < p0) est += t;
+            est_next += t;
+        }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        est += __shfl_xor(est, o);
+        est_next += __shfl_xor(est_next, o);
+    }
+    if (lane == 0) {
+        dred[wave] = est;
+        dred[ea::kWaves + wave] = est_next;
+    }
+    __syncthreads();
+    est = (dred[0] + dred[1]) + (dred[2] + dred[3]);
+    est_next = (dred[4] + dred[5]) + (dred[6] + dred[7]);
+    const uint32_t skew = static_cast<uint32_t>(p.z_skew);
+    const uint32_t centre = k == 0 ? 0u : __float_as_uint(static_cast<float>(est)) + skew;
+    const uint32_t centre_next = __float_as_uint(static_cast<float>(est_next)) + skew;
+    float acc = k == 0 ? 0.0f : __uint_as_float(centre + static_cast<uint32_t>(tid) - ea::kZCand / 2);
+#pragma unroll 16
+    for (int j = 0; j < ea::kSeg; j += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(e_seg + j);
+        acc = acc + v.x;
+        acc = acc + v.y;
+        acc = acc + v.z;
+        acc = acc + v.w;
+    }
+    const bool last = p0 + ea::kSeg >= n;
+    float *tab = ztab_of(p) + (static_cast<size_t>(h) * ea::z_segments(p.max_context) + k) * ea::kZStride;
+    tab[tid] = acc;
+    tab[ea::kZNext + tid] = last ? acc : __int_as_float(ea::z_index(acc, centre_next));
+    if (tid == 0) tab[ea::kZCentre] = __uint_as_float(centre);
+}
+
+// Z of head h: the walk words of the candidate tables into LDS (up to
+// kZLdsSegments segments; longer contexts walk in global memory), then
+// resolve_z by one thread.  walk_lds: min(z_segments(n), kZLdsSegments) *
+// kZCand words.  Returns Z in every thread.
+constexpr int kZLdsSegments = 32;
+__host__ __device__ inline int z_lds_segments(int positions) {
+    return ea::z_segments(positions) < kZLdsSegments ? ea::z_segments(positions) : kZLdsSegments;
+}
+__device__ __forceinline__ const float *head_tab(const AttentionParams &p, int h) {
+    return ztab_of(p) + static_cast<size_t>(h) * ea::z_segments(p.max_context) * ea::kZStride;
+}
+__device__ __forceinline__ float head_z(const AttentionParams &p, int h, int n, int32_t *walk_lds, float *slot) {
+    const int tid = static_cast<int>(threadIdx.x);
+    const int nseg = (n + ea::kSeg - 1) / ea::kSeg;
+    const float *tab = head_tab(p, h);
+    if (nseg <= kZLdsSegments) {
+        for (int i = tid; i < nseg * ea::kZCand; i += ea::kThreads)
+            walk_lds[i] = __float_as_int(tab[static_cast<size_t>(i / ea::kZCand) * ea::kZStride + ea::kZNext + i % ea::kZCand]);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float *ev = evals_of(p) + static_cast<size_t>(h) * p.max_context;
+        *slot = nseg <= kZLdsSegments
+            ? ea::resolve_z(walk_lds, ea::kZCand, tab, ev, n)
+            : ea::resolve_z(reinterpret_cast<const int32_t *>(tab + ea::kZNext), ea::kZStride, tab, ev, n);
+    }
+    __syncthreads();
+    return *slot;
+}
+
+// The output of one head x kDims value dims.  Workgroups are numbered so
+// that the ones reading the same 128-byte value lines (the 64 dims of a kv
+// head that 8 slices x the GQA group share) are consecutive on one XCD
+// (workgroup b runs on XCD b % 8).  Every load that does not depend on the
+// position (the first value pieces, e values and the Z tables, all clamped to
+// the cache) is issued together with the position's, in one round trip.
+constexpr int kTabRegs = kZLdsSegments * ea::kZCand / ea::kThreads;  // walk words per thread
 __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const AttentionParams p_batch) {
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     extern __shared__ __align__(16) float lds[];
     const int tid = static_cast<int>(threadIdx.x);
     FORTAI_ATT_MARK(0);
     const int pos = *p.position;
+    const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
+    const int slices = VD / ea::kDims, nwg = p.heads * slices;
+    const int b = static_cast<int>(blockIdx.x);
+    int h, d0;
+    if (nwg % 8 == 0 && VD % 64 == 0) {
+        const int i = (b % 8) * (nwg / 8) + b / 8;  // logical index, consecutive on one XCD
+        const int sl = i % 8, g = (i / 8) % group, t = i / 8 / group, lg = t % (VD / 64), kvh = t / (VD / 64);
+        h = kvh * group + g;
+        d0 = (lg * 8 + sl) * ea::kDims;
+    } else {
+        h = b / slices;
+        d0 = (b % slices) * ea::kDims;
+    }
+    const int kvh = h / group;
+    const int cap = p.max_context < p.exact_max ? p.max_context : p.exact_max;  // positions this kernel serves
+    const uint16_t *vbase = p.vcache + static_cast<size_t>(kvh) * VD + d0;
+    const size_t vstride = static_cast<size_t>(NKV) * VD;
+    const float *ev = evals_of(p) + static_cast<size_t>(h) * p.max_context;
+    const float *tab = head_tab(p, h);
+    const int rows = z_lds_segments(cap);
+    ea::ValuePieces v;
+    float e4[ea::kPieces];
+    int32_t tr[kTabRegs];  // walk word tid of segment r
+    ea::value_prefetch(vbase, vstride, p.max_context, v);
+    ea::e_prefetch(ev, p.max_context, e4);
+    static_assert(ea::kZCand == ea::kThreads, "one walk word per thread and segment");
+#pragma unroll
+    for (int r = 0; r < kTabRegs; ++r)
+        if (r < rows) tr[r] = __float_as_int(tab[static_cast<size_t>(r) * ea::kZStride + ea::kZNext + tid]);
+    const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
+    const int flag = p.cache_flags[kvh];
+    FORTAI_ATT_MARK(3);
     if (pos < 0 || pos >= p.max_context) return;
     const int positions = pos + 1;
     if (positions > p.exact_max) return;  // the split-K kernels cover this position
-    const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
-    const int slices = VD / ea::kDims;
-    const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * ea::kDims;
-    const int kvh = h / group;
     float *work = lds;
-    const uint16_t *vbase = p.vcache + static_cast<size_t>(kvh) * VD + d0;
-    const size_t vstride = static_cast<size_t>(NKV) * VD;
-    ea::ValuePieces v;
-    ea::value_prefetch(vbase, vstride, positions, v);
-    const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
-    const int flag = p.cache_flags[kvh];
-    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;  // read in place
-    FORTAI_ATT_MARK(3);
-    const float acc = flag == 0 ? ea::attend<true>(sc, positions, vbase, vstride, work, v)
-                                : ea::attend<false>(sc, positions, vbase, vstride, work, v);
+    int32_t *walk_lds = reinterpret_cast<int32_t *>(lds + ea::work_floats());
+    const int nseg = ea::z_segments(positions);
+    if (nseg <= kZLdsSegments) {
+#pragma unroll
+        for (int r = 0; r < kTabRegs; ++r)
+            if (r < nseg) walk_lds[r * ea::kZCand + tid] = tr[r];
+    }
+    __syncthreads();
+    FORTAI_ATT_MARK(1);
+    if (tid == 0)
+        work[0] = nseg <= kZLdsSegments
+            ? ea::resolve_z(walk_lds, ea::kZCand, tab, ev, positions)
+            : ea::resolve_z(reinterpret_cast<const int32_t *>(tab + ea::kZNext), ea::kZStride, tab, ev, positions);
+    FORTAI_ATT_MARK(2);
+    __syncthreads();
+    const float z = work[0];
+    FORTAI_ATT_MARK(5);
+    const float acc = flag == 0 ? ea::attend_given_z<true>(ev, z, positions, vbase, vstride, work, v, e4)
+                                : ea::attend_given_z<false>(ev, z, positions, vbase, vstride, work, v, e4);
     if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * sigmoid_ref(gate);
     FORTAI_ATT_MARK(4);
 }
 
-size_t output_lds_bytes() { return ea::work_floats() * sizeof(float); }
+size_t output_lds_bytes(int positions) {
+    return (ea::work_floats() + static_cast<size_t>(z_lds_segments(positions)) * ea::kZCand) * sizeof(float);
+}
 
 // ------------------------------------------------------- exact, batches
 // The same arithmetic as attention_output_kernel (the reference's two-pass
@@ -198,11 +388,10 @@ __host__ __device__ inline int wide_score_floats(const AttentionParams &p) { ret
 
 template <bool FINITE>
 __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int d0, int n, float *w, uint16_t *vt,
-    float *red) {
+    float *tab_lds, float *red) {
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
     const int kvh = h / group;
-    const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
     const uint16_t *vb = p.vcache + static_cast<size_t>(kvh) * VD + d0;
     const size_t vs = static_cast<size_t>(NKV) * VD;
     const int pieces = min(kWideDims, VD - d0) / 8;  // 16-byte pieces of a row slice
@@ -228,59 +417,10 @@ __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int
     fetch(0, ra);
     if (tiles > 1) fetch(1, rb);
 
-    // max (any order gives the same value)
-    constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
-    float m = kLowest;
-    constexpr int kU = 8;  // score loads in flight per thread
-    for (int i0 = tid; i0 < n; i0 += ea::kThreads * kU) {
-        float x[kU];
-#pragma unroll
-        for (int k = 0; k < kU; ++k) x[k] = sc[min(i0 + k * ea::kThreads, n - 1)];
-#pragma unroll
-        for (int k = 0; k < kU; ++k) {
-            if (i0 + k * ea::kThreads < n) w[i0 + k * ea::kThreads] = x[k];
-            m = fmaxf(m, x[k]);  // clamped duplicates change nothing
-        }
-    }
-    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int i = tid; i < n; i += ea::kThreads) w[i] = expf_libm(w[i] - m);
-    __syncthreads();
-    // Z = e_0 + e_1 + ... left to right, by one lane; the LDS reads of the
-    // next 16 values are in flight while the current 16 are added
-    if (tid == 0) {
-        float z = 0.0f;
-        const int full = n / 16 * 16;
-        float4 ea4[4], eb4[4];
-        auto rd = [&](int i, float4 (&r)[4]) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) r[k] = *reinterpret_cast<const float4 *>(w + i + 4 * k);
-        };
-        auto add = [&](const float4 (&r)[4]) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                z = z + r[k].x;
-                z = z + r[k].y;
-                z = z + r[k].z;
-                z = z + r[k].w;
-            }
-        };
-        if (full > 0) rd(0, ea4);
-        int i = 0;
-        for (; i + 32 <= full; i += 32) {
-            rd(i + 16, eb4);
-            add(ea4);
-            if (i + 32 < full) rd(i + 32, ea4);
-            add(eb4);
-        }
-        if (i < full) add(ea4);
-        for (i = full; i < n; ++i) z = z + w[i];
-        red[4] = z;
-    }
-    __syncthreads();
-    const float z = red[4];
+    // e_p (attention_softmax_kernel) into LDS, and Z from the candidate tables
+    const float *ev = evals_of(p) + static_cast<size_t>(h) * p.max_context;
+    for (int i = tid; i < n; i += ea::kThreads) w[i] = ev[i];
+    const float z = head_z(p, h, n, reinterpret_cast<int32_t *>(tab_lds), red + 4);
     for (int i = tid; i < n; i += ea::kThreads) w[i] = w[i] / z;
     // (the first stash's barrier below orders these writes before the chains)
 
@@ -359,10 +499,11 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_wide_kernel(con
     const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * kWideDims;
     const int kvh = h / (p.heads / p.kv_heads);
     uint16_t *vt = reinterpret_cast<uint16_t *>(wide_lds + wide_score_floats(p));
+    float *tab_lds = wide_lds + wide_score_floats(p) + kWideTile * kWidePitch / 2;
     if (p.cache_flags[kvh] == 0)
-        attend_wide<true>(p, h, d0, n, wide_lds, vt, red);
+        attend_wide<true>(p, h, d0, n, wide_lds, vt, tab_lds, red);
     else
-        attend_wide<false>(p, h, d0, n, wide_lds, vt, red);
+        attend_wide<false>(p, h, d0, n, wide_lds, vt, tab_lds, red);
 }
 
 
@@ -577,7 +718,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_merge_kernel(const Att
 
 }  // namespace
 
-size_t attention_scores_floats(int heads, int max_context) { return static_cast<size_t>(heads) * max_context; }
+size_t attention_scores_floats(int heads, int max_context) { return workspace_floats(heads, max_context); }
 
 int attention_split_chunks(int max_context) { return (max_context + kChunk - 1) / kChunk; }
 
@@ -589,26 +730,35 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int ba
     if (group < 1 || group > kMaxGroup || p.heads % p.kv_heads || p.head > kMaxHead || p.head % 8 ||
         p.value % ea::kDims || p.value > p.head || p.rope_dim > p.head || p.rope_dim % 2 || !p.out || !p.partial)
         return hipErrorInvalidValue;
-    const size_t lds = output_lds_bytes();  // independent of the context length
+    const int exact_positions = p.max_context < p.exact_max ? p.max_context : p.exact_max;
     const int nblk_max = (p.max_context + ea::kPosBlock - 1) / ea::kPosBlock;
     hipLaunchKernelGGL(attention_scores_kernel, dim3(p.kv_heads * nblk_max, batch), dim3(ea::kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (exact_positions > 0) {
+        hipLaunchKernelGGL(attention_softmax_kernel, dim3(p.heads * ea::z_segments(exact_positions), batch),
+            dim3(ea::kThreads), 0, stream, p);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const size_t tab_bytes = static_cast<size_t>(z_lds_segments(exact_positions)) * ea::kZCand * sizeof(float);
     const bool wide = batch > 1 && wide_positions(p) <= kWideMaxPositions && p.value <= ea::kThreads;
     if (wide) {
         const size_t wlds = static_cast<size_t>(wide_score_floats(p)) * sizeof(float) +
-            static_cast<size_t>(kWideTile) * kWidePitch * sizeof(uint16_t);
+            static_cast<size_t>(kWideTile) * kWidePitch * sizeof(uint16_t) + tab_bytes;
         const int wgrid = p.heads * ((p.value + kWideDims - 1) / kWideDims);
         hipLaunchKernelGGL(attention_output_wide_kernel, dim3(wgrid, batch), dim3(ea::kThreads), wlds, stream, p);
         e = hipGetLastError();
-        note_launch("attention_scores_kernel grid %dx%d + attention_output_wide_kernel grid %dx%d", p.kv_heads * nblk_max,
-            batch, wgrid, batch);
+        note_launch("attention_scores_kernel grid %dx%d + attention_softmax_kernel grid %dx%d + "
+            "attention_output_wide_kernel grid %dx%d", p.kv_heads * nblk_max, batch,
+            p.heads * ea::z_segments(exact_positions), batch, wgrid, batch);
     } else {
-        hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads), lds,
-            stream, p);
+        hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads),
+            output_lds_bytes(exact_positions), stream, p);
         e = hipGetLastError();
-        note_launch("attention_scores_kernel grid %dx%d + attention_output_kernel grid %dx%d", p.kv_heads * nblk_max,
-            batch, p.heads * (p.value / ea::kDims), batch);
+        note_launch("attention_scores_kernel grid %dx%d + attention_softmax_kernel grid %dx%d + "
+            "attention_output_kernel grid %dx%d", p.kv_heads * nblk_max, batch,
+            p.heads * ea::z_segments(exact_positions), batch, p.heads * (p.value / ea::kDims), batch);
     }
     if (e != hipSuccess || p.max_context <= p.exact_max) return e;
     // long contexts: the split-K pair (each kernel picks its regime from the device position)
@@ -618,7 +768,8 @@ hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int ba
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attention_merge_kernel, dim3(p.heads * ((p.value + kMergeDims - 1) / kMergeDims), batch),
         dim3(ea::kThreads), 0, stream, p);
-    note_launch("attention_scores_kernel + attention_output_kernel (positions <= %d) + attention_split_kernel grid "
+    note_launch("attention_scores_kernel + attention_softmax_kernel + attention_output_kernel (positions <= %d) + "
+        "attention_split_kernel grid "
         "%dx%d + attention_merge_kernel (beyond)", p.exact_max, p.kv_heads * attention_split_chunks(p.max_context), batch);
     return hipGetLastError();
 }

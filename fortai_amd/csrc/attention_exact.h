@@ -155,6 +155,68 @@ __device__ __forceinline__ void pass_turn(uint64_t *word, int k_next, float acc)
         __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// ------------------------------------------------- Z from candidate tables
+// Z = e_0 + e_1 + ... left to right is one chain of n dependent adds.  The
+// softmax kernel cuts it into kSeg-position segments and runs every segment
+// in parallel from kZCand candidate starting sums: the consecutive floats
+// around (float) of an estimate of the sum entering the segment (the
+// double sum of a fast exp over the earlier positions; the true running sum
+// differs from it by the chain's accumulated rounding, a few tens of ulps).
+// Candidate c's chain over the segment's e values gives the entry T[c]; the
+// workgroup also knows the next segment's window (its estimate is the same
+// double sum, one segment longer) and stores, for every c, the index of T[c]
+// among the next segment's candidates.  resolve_z() then walks the segments
+// from candidate kZCand/2 of segment 0 (every candidate of segment 0 starts
+// at exactly 0), one index per segment, and reads T of the last one: the
+// chain's exact value.  When a running sum lies outside the next window that
+// segment's chain is run from it over the stored e values, so the result is
+// the left-to-right sum in every case.
+constexpr int kZCand = 256;                // candidate starting sums per segment (one per thread)
+constexpr int kZNext = kZCand;             // row offset of the next-segment indices
+constexpr int kZCentre = 2 * kZCand;       // row offset of the centre's bits
+constexpr int kZStride = 2 * kZCand + 2;   // row: T[kZCand] | next[kZCand] | centre | pad
+__host__ __device__ constexpr int z_segments(int max_context) { return (max_context + kSeg - 1) / kSeg; }
+
+// the index of s among the candidates around centre, or -1
+__device__ __forceinline__ int z_index(float s, uint32_t centre) {
+    const long long c = static_cast<long long>(__float_as_uint(s)) - static_cast<long long>(centre) + kZCand / 2;
+    return c >= 0 && c < kZCand ? static_cast<int>(c) : -1;
+}
+
+// walk: the next indices of segment k (the last segment: its T bits) at
+// walk + k * walk_stride, in LDS (compact, stride kZCand) or in the rows
+// themselves (tab + kZNext, stride kZStride); tab: the full rows (global
+// memory); ev: the n e values.
+__device__ __forceinline__ float resolve_z(const int32_t *walk, int walk_stride, const float *tab, const float *ev,
+    int n) {
+    const int nseg = (n + kSeg - 1) / kSeg;
+    int idx = kZCand / 2;
+    bool have = true;  // the running sum is candidate idx of segment k
+    float s = 0.0f;
+    for (int k = 0; k < nseg; ++k) {
+        if (!have) {
+            const int c = z_index(s, __float_as_uint(tab[static_cast<size_t>(k) * kZStride + kZCentre]));
+            if (c < 0) {
+                const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
+                for (int j = 0; j < cnt; ++j) s = s + ev[p0 + j];
+                continue;
+            }
+            idx = c;
+            have = true;
+        }
+        const int w = walk[static_cast<size_t>(k) * walk_stride + idx];
+        if (k == nseg - 1) {
+            s = __int_as_float(w);
+        } else if (w >= 0) {
+            idx = w;
+        } else {
+            s = tab[static_cast<size_t>(k) * kZStride + idx];
+            have = false;
+        }
+    }
+    return s;
+}
+
 // LDS of the output step, in floats: 8 reduction slots, kDims handoff words
 // and one stage of kDims x kSeg values per wave (work_floats); a caller that
 // keeps the scores in LDS adds sw_floats(max_context) in front.
@@ -185,6 +247,13 @@ __device__ __forceinline__ void value_fetch(const uint16_t *vbase, size_t vstrid
 
 __device__ __forceinline__ void value_prefetch(const uint16_t *vbase, size_t vstride, int n, ValuePieces &v) {
     value_fetch(vbase, vstride, n, static_cast<int>(threadIdx.x) >> 6, v);
+}
+
+// The e values of the wave's first segment (clamped to the first n).
+__device__ __forceinline__ void e_prefetch(const float *ev, int n, float (&e4)[kPieces]) {
+    const int lane = static_cast<int>(threadIdx.x) & 63, wave = static_cast<int>(threadIdx.x) >> 6;
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) e4[i] = ev[min(wave * kSeg + lane + 64 * i, n - 1)];
 }
 
 // Softmax weights and P.V of kDims value dims over n positions
@@ -292,6 +361,67 @@ __device__ __forceinline__ float attend(const float *scores, int n, const uint16
         }
     }
     __syncthreads();
+    if (tid < kDims) acc = __uint_as_float(static_cast<uint32_t>(hand[tid]));
+    __syncthreads();  // hand and stage are free again when this returns
+    return acc;
+}
+
+// P.V of kDims value dims with Z given (attention_softmax_kernel's e values
+// and resolve_z): out_j = fl(e_0/Z v_0,j) + fl(e_1/Z v_1,j) + ... left to
+// right, the second half of attend().  ev: the n e values (global memory);
+// v and e4: the value pieces and e values of the wave's first segment
+// (value_prefetch, e_prefetch).  All threads call it; the result is valid in
+// threads 0..kDims-1.
+template <bool FINITE>
+__device__ __forceinline__ float attend_given_z(const float *ev, float z, int n, const uint16_t *vbase,
+    size_t vstride, float *work, ValuePieces &v, float (&e4)[kPieces]) {
+    static_assert(kDims == 8, "one 16-byte value piece per position");
+    const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+    uint64_t *hand = reinterpret_cast<uint64_t *>(work + 8);
+    float *stage = work + 8 + 2 * kDims + wave * kDims * kStagePitch;
+    const int nseg = (n + kSeg - 1) / kSeg;
+    if (tid < kDims) hand[tid] = 0;
+    auto load_e = [&](int k) {
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) e4[i] = ev[min(k * kSeg + lane + 64 * i, n - 1)];
+    };
+    __syncthreads();
+    FORTAI_ATT_MARK(6);
+    f4 r[kSegVec];
+    float acc = 0.0f;
+    for (int k = wave; k < nseg; k += kWaves) {
+        const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+            const int j = lane + 64 * i, p = p0 + j;
+            if (p < n) {
+                const float wp = e4[i] / z;
+                const uint32_t hw[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    stage[(2 * q) * kStagePitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] & 0xffffu));
+                    stage[(2 * q + 1) * kStagePitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] >> 16));
+                }
+            } else {
+#pragma unroll
+                for (int d = 0; d < kDims; ++d) stage[d * kStagePitch + j] = -0.0f;
+            }
+        }
+        if (k + kWaves < nseg) {
+            load_e(k + kWaves);
+            value_fetch(vbase, vstride, n, k + kWaves, v);
+        }
+        if (lane < kDims) {
+            seg_read(r, stage + lane * kStagePitch);
+            seg_held<0>(r);
+            float a = take_turn(hand + lane, k);
+            a = seg_chain(r, cnt, a);
+            pass_turn(hand + lane, k + 1, a);
+        }
+        if (k == 0) FORTAI_ATT_MARK(9);
+    }
+    __syncthreads();
+    FORTAI_ATT_MARK(7);
     if (tid < kDims) acc = __uint_as_float(static_cast<uint32_t>(hand[tid]));
     __syncthreads();  // hand and stage are free again when this returns
     return acc;

@@ -15,8 +15,10 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <initializer_list>
 #include <string>
 #include <vector>
+#include <initializer_list>
 
 using namespace fortai_hip;
 
@@ -73,8 +75,14 @@ struct fortai_hip_qwen35_recurrent {
     float eps = 0.0f;
     float *conv_w = nullptr, *ssm_a = nullptr, *ssm_dt = nullptr, *ssm_norm = nullptr;
     float *conv_state = nullptr, *state = nullptr;
-    float *qkv_out = nullptr, *z_out = nullptr, *alpha_out = nullptr, *beta_out = nullptr;
+    float *proj = nullptr;  // projection outputs, one buffer: qkv | z | alpha | beta
+    float *qkv_out = nullptr, *z_out = nullptr, *alpha_out = nullptr, *beta_out = nullptr;  // views of proj
     float *o_raw = nullptr;  // GDN output before the gated norm (ssm_out input)
+    // qkv | gate | alpha | beta as one matrix (when each is whole 8-row
+    // groups): the four projections then run as one single-segment launch
+    Q8Matrix in_m;
+    uint4 *in_quants = nullptr;
+    uint2 *in_scales = nullptr;
 };
 
 struct fortai_hip_qwen35_attention {
@@ -85,10 +93,16 @@ struct fortai_hip_qwen35_attention {
     float *q_norm = nullptr, *k_norm = nullptr;
     float2 *rope = nullptr;
     uint16_t *kcache = nullptr, *vcache = nullptr;
-    float *q_out = nullptr, *k_out = nullptr, *v_out = nullptr, *partial = nullptr;
+    float *proj = nullptr;  // projection outputs, one buffer: q | k | v
+    float *q_out = nullptr, *k_out = nullptr, *v_out = nullptr;  // views of proj
+    float *partial = nullptr;
+    Q8Matrix in_m;  // q | k | v as one matrix (whole 8-row groups each)
+    uint4 *in_quants = nullptr;
+    uint2 *in_scales = nullptr;
     int *cache_flags = nullptr;  // per kv head: the cache holds an exponent-31 half
     float *attn_out = nullptr;   // gated attention output (o_proj input)
     int exact_max = 0;           // positions with the bit-exact two-pass softmax; split-K beyond
+    int z_skew = 0;              // test hook: offset of the Z candidate windows (FORTAI_HIP_ZTABLE_SKEW)
     float *split = nullptr;      // split-K partials (allocated when max_context > exact_max)
 };
 
@@ -115,15 +129,6 @@ struct fortai_hip_qwen35_decoder {
     bool use_graph = true;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
-    // persistent one-launch-per-token path (decode_persistent.hip)
-    bool persistent = false;
-    int grid = 0;
-    uint64_t *arena = nullptr;               // tagged-word buffers of every phase
-    PersistentLayer *layers_dev = nullptr;
-    PersistentPlan *plan_dev = nullptr;
-    uint32_t next_tag = 1;                   // tag of the next persistent launch
-    int *status = nullptr;
-    uint64_t *phase_times = nullptr;  // FORTAI_HIP_PHASE_TIMES=1: per-workgroup phase end clocks
     std::vector<plan_step> plan;  // the launches of one step (PlanIR steps)
 };
 
@@ -227,6 +232,41 @@ void release(T *&ptr) {
     ptr = nullptr;
 }
 
+// The planes of several Q8_0 matrices of one width, one after the other, as
+// one matrix (the planes are row-group major, so this is a concatenation).
+// Only when every matrix is whole 8-row groups; returns hipSuccess with
+// *quants left null otherwise.
+hipError_t fuse_q8(std::initializer_list<const fortai_hip_q8_weights *> parts, Q8Matrix *m, uint4 **quants,
+    uint2 **scales, hipStream_t stream) {
+    *quants = nullptr;
+    *scales = nullptr;
+    int rows = 0;
+    const fortai_hip_q8_weights *first = *parts.begin();
+    for (const auto *w : parts) {
+        if (w->m.rows % kRowsPerWave || w->m.chunks != first->m.chunks) return hipSuccess;
+        rows += w->m.rows;
+    }
+    Q8Matrix f = first->m;
+    f.rows = rows;
+    f.row_groups = rows / kRowsPerWave;
+    const size_t per_group = static_cast<size_t>(f.chunks);
+    hipError_t e = alloc(quants, static_cast<size_t>(f.row_groups) * per_group * 64);
+    if (e == hipSuccess) e = alloc(scales, static_cast<size_t>(f.row_groups) * per_group * 8);
+    size_t at = 0;
+    for (const auto *w : parts) {
+        const size_t groups = static_cast<size_t>(w->m.row_groups) * per_group;
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(*quants + at * 64, w->m.quants, groups * 64 * sizeof(uint4), hipMemcpyDeviceToDevice, stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(*scales + at * 8, w->m.scales, groups * 8 * sizeof(uint2), hipMemcpyDeviceToDevice, stream);
+        at += groups;
+    }
+    f.quants = *quants;
+    f.scales = *scales;
+    *m = f;
+    return e;
+}
+
 hipError_t upload_f32(float **dst, const void *src, size_t count, hipStream_t stream) {
     hipError_t e = alloc(dst, count);
     if (e == hipSuccess) e = hipMemcpyAsync(*dst, src, count * sizeof(float), hipMemcpyHostToDevice, stream);
@@ -318,7 +358,18 @@ hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &
     segs[0].conv_size = L->conv_size;
     segs[0].kernel = L->kernel;
     segs[1].silu = true;  // the gate is only used through SiLU
-    hipError_t e = rec(launch_q8_matvec(segs, 4, in, pro, Epilogue::STORE, stream),
+    int count = 4;
+    if (L->in_quants) {
+        // the fused matrix: rows [0, conv_size) qkv through the conv, the gate
+        // rows through SiLU, then alpha and beta, into proj (laid out alike)
+        segs[0].w = L->in_m;
+        segs[0].out = L->proj;
+        segs[0].conv_rows = L->conv_size;
+        segs[0].silu_begin = L->conv_size;
+        segs[0].silu_end = L->conv_size + L->inner;
+        count = 1;
+    }
+    hipError_t e = rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream),
         "GDN qkv/gate/alpha/beta projections, conv1d + SiLU");
     if (e == hipSuccess)
         e = rec(launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw), stream),
@@ -343,14 +394,20 @@ AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q,
     p.kcache = A->kcache; p.vcache = A->vcache; p.partial = A->partial; p.cache_flags = A->cache_flags; p.out = out;
     p.position = A->context->position; p.heads = A->heads; p.kv_heads = A->kv_heads; p.head = A->head;
     p.value = A->value; p.max_context = A->max_context; p.rope_dim = A->rope_dim;
-    p.eps = A->eps; p.exact_max = A->exact_max; p.split = A->split;
+    p.eps = A->eps; p.exact_max = A->exact_max; p.split = A->split; p.z_skew = A->z_skew;
     return p;
 }
 
 hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &in, Prologue pro, float *out,
     const float *resid, hipStream_t stream) {
-    const MatvecSegment segs[3] = {segment(A->q, A->q_out), segment(A->k, A->k_out), segment(A->v, A->v_out)};
-    hipError_t e = rec(launch_q8_matvec(segs, 3, in, pro, Epilogue::STORE, stream), "attention q/k/v projections");
+    MatvecSegment segs[3] = {segment(A->q, A->q_out), segment(A->k, A->k_out), segment(A->v, A->v_out)};
+    int count = 3;
+    if (A->in_quants) {
+        segs[0].w = A->in_m;  // q | k | v into proj (laid out alike)
+        segs[0].out = A->proj;
+        count = 1;
+    }
+    hipError_t e = rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream), "attention q/k/v projections");
     if (e != hipSuccess) return e;
     e = rec(launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream),
         "q/k norm, RoPE, KV append, softmax.V, gate");
@@ -1030,10 +1087,14 @@ int fortai_hip_qwen35_recurrent_create(fortai_hip_q8_context *c, const fortai_hi
     if (e == hipSuccess) e = upload_f32(&L->ssm_norm, ssm_norm, head_size, c->stream);
     if (e == hipSuccess) e = alloc(&L->conv_state, static_cast<size_t>(conv_kernel - 1) * conv_size);
     if (e == hipSuccess) e = alloc(&L->state, state_n);
-    if (e == hipSuccess) e = alloc(&L->qkv_out, conv_size);
-    if (e == hipSuccess) e = alloc(&L->z_out, inner_size);
-    if (e == hipSuccess) e = alloc(&L->alpha_out, value_heads);
-    if (e == hipSuccess) e = alloc(&L->beta_out, value_heads);
+    if (e == hipSuccess) e = alloc(&L->proj, static_cast<size_t>(conv_size) + inner_size + 2 * value_heads);
+    if (e == hipSuccess) {
+        L->qkv_out = L->proj;
+        L->z_out = L->qkv_out + conv_size;
+        L->alpha_out = L->z_out + inner_size;
+        L->beta_out = L->alpha_out + value_heads;
+    }
+    if (e == hipSuccess) e = fuse_q8({qkv, gate, alpha, beta}, &L->in_m, &L->in_quants, &L->in_scales, c->stream);
     if (e == hipSuccess) e = alloc(&L->o_raw, inner_size);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
@@ -1056,7 +1117,7 @@ int fortai_hip_qwen35_recurrent_destroy(fortai_hip_qwen35_recurrent *L) {
         (void)hipStreamSynchronize(L->context->stream);
     }
     release(L->conv_w); release(L->ssm_a); release(L->ssm_dt); release(L->ssm_norm); release(L->conv_state);
-    release(L->state); release(L->qkv_out); release(L->z_out); release(L->alpha_out); release(L->beta_out);
+    release(L->state); release(L->proj); release(L->in_quants); release(L->in_scales);
     release(L->o_raw);
     delete L;
     return FORTAI_HIP_OK;
@@ -1211,9 +1272,14 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
         e = hipMemcpyAsync(A->rope, table.data(), table.size() * sizeof(float2), hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = alloc(&A->kcache, kv_n * head_size);
     if (e == hipSuccess) e = alloc(&A->vcache, kv_n * value_size);
-    if (e == hipSuccess) e = alloc(&A->q_out, static_cast<size_t>(heads) * 2 * head_size);
-    if (e == hipSuccess) e = alloc(&A->k_out, static_cast<size_t>(kv_heads) * head_size);
-    if (e == hipSuccess) e = alloc(&A->v_out, static_cast<size_t>(kv_heads) * value_size);
+    if (e == hipSuccess)
+        e = alloc(&A->proj, static_cast<size_t>(heads) * 2 * head_size + static_cast<size_t>(kv_heads) * (head_size + value_size));
+    if (e == hipSuccess) {
+        A->q_out = A->proj;
+        A->k_out = A->q_out + static_cast<size_t>(heads) * 2 * head_size;
+        A->v_out = A->k_out + static_cast<size_t>(kv_heads) * head_size;
+    }
+    if (e == hipSuccess) e = fuse_q8({q, k, v}, &A->in_m, &A->in_quants, &A->in_scales, c->stream);
     if (e == hipSuccess) e = alloc(&A->attn_out, static_cast<size_t>(heads) * value_size);
     if (e == hipSuccess) e = alloc(&A->partial, attention_scores_floats(heads, max_context));
     // FORTAI_HIP_EXACT_ATTENTION_MAX: the positions up to which the attention
@@ -1221,6 +1287,9 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
     // them the split-K path (within 1e-3 relative) takes over
     A->exact_max = 8192;
     if (const char *env = std::getenv("FORTAI_HIP_EXACT_ATTENTION_MAX")) A->exact_max = std::max(0, std::atoi(env));
+    // test hook: shift every Z candidate window by this many floats, so that
+    // the running sums fall outside them and resolve_z's own chain runs
+    if (const char *env = std::getenv("FORTAI_HIP_ZTABLE_SKEW")) A->z_skew = std::atoi(env);
     if (e == hipSuccess && max_context > A->exact_max)
         e = alloc(&A->split, static_cast<size_t>(heads) * attention_split_chunks(max_context) * (value_size + 2));
     if (e == hipSuccess) e = alloc(&A->cache_flags, kv_heads);
@@ -1245,7 +1314,7 @@ int fortai_hip_qwen35_attention_destroy(fortai_hip_qwen35_attention *A) {
         (void)hipStreamSynchronize(A->context->stream);
     }
     release(A->q_norm); release(A->k_norm); release(A->rope); release(A->kcache); release(A->vcache);
-    release(A->q_out); release(A->k_out); release(A->v_out); release(A->partial); release(A->cache_flags);
+    release(A->proj); release(A->in_quants); release(A->in_scales); release(A->partial); release(A->cache_flags);
     release(A->attn_out); release(A->split);
     delete A;
     return FORTAI_HIP_OK;
@@ -1377,191 +1446,12 @@ hipError_t run_step(fortai_hip_qwen35_decoder *d) {
     // the plan is recorded by the first step (at capture for the graph)
     std::vector<plan_step> *saved = g_plan;
     if (d->plan.empty() && !d->use_graph) g_plan = &d->plan;
-    hipError_t e;
-    if (d->persistent) {
-        e = rec(launch_decode_persistent(d->plan_dev, d->next_tag++, d->grid, d->context->stream),
-            "every layer in one persistent kernel");
-        if (e == hipSuccess) e = enqueue_lm_head(d, d->context->stream);
-    } else {
-        e = d->use_graph ? hipGraphLaunch(d->exec, d->context->stream) : enqueue_decoder_step(d, d->context->stream);
-    }
+    const hipError_t e = d->use_graph ? hipGraphLaunch(d->exec, d->context->stream)
+                                      : enqueue_decoder_step(d, d->context->stream);
     g_plan = saved;
     return e;
 }
-// after a synchronisation: a failed persistent step (a bounded wait expired)
-// is reported once and cleared
-int persistent_status(fortai_hip_qwen35_decoder *d) {
-    if (!d->persistent) return FORTAI_HIP_OK;
-    int st[8 + 2 * 256] = {};
-    if (hipMemcpy(st, d->status, sizeof(st), hipMemcpyDeviceToHost) != hipSuccess)
-        return fail(d->context, FORTAI_HIP_RUNTIME_ERROR, "persistent decode status read");
-    if (st[0] == 0) return FORTAI_HIP_OK;
-    (void)hipMemset(d->status, 0, sizeof(st));
-    if (st[0] & 2) return fail(d->context, FORTAI_HIP_RUNTIME_ERROR, "persistent decode: token or position out of range");
-    int lag = -1;  // the workgroup that failed in the earliest phase
-    for (int b = 0; b < d->grid; ++b)
-        if (st[8 + b] > 0 && (lag < 0 || st[8 + b] < st[8 + lag])) lag = b;
-    char msg[240];
-    std::snprintf(msg, sizeof(msg),
-        "persistent decode: wait timed out in phase %d (workgroup %d, word %d, tag %d, expected %d); earliest "
-        "failing phase %d (workgroup %d, word %d)",
-        st[1] - 1, st[2], st[3], st[4], st[5], lag >= 0 ? st[8 + lag] - 1 : -1, lag, lag >= 0 ? st[8 + 256 + lag] : -1);
-    return fail(d->context, FORTAI_HIP_RUNTIME_ERROR, msg);
-}
 }  // namespace
-
-extern "C++" {
-namespace {
-PersistentMatvec persistent_matvec(std::initializer_list<std::pair<const fortai_hip_q8_weights *, uint64_t *>> segs) {
-    PersistentMatvec m{};
-    m.count = 0;
-    m.plain = nullptr;
-    m.first_rg[0] = 0;
-    for (const auto &sgm : segs) {
-        m.w[m.count] = sgm.first->m;
-        m.out[m.count] = sgm.second;
-        m.first_rg[m.count + 1] = m.first_rg[m.count] + sgm.first->m.row_groups;
-        ++m.count;
-    }
-    return m;
-}
-
-// Build the persistent plan; returns "" on success, else why the shapes are
-// not supported (the decoder then keeps the per-op graph path).
-std::string setup_persistent(fortai_hip_qwen35_decoder *d) {
-    auto *c = d->context;
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device) != hipSuccess || cus <= 0)
-        return "device query";
-    const int grid = cus < 256 ? cus : 256;
-    if (persistent_blocks_per_cu() < 1) return "occupancy";
-    PersistentPlan P{};
-    P.layers = static_cast<int>(d->layers.size());
-    P.hidden = d->hidden; P.ffn = d->ffn; P.vocab = d->vocab; P.max_context = d->max_context; P.eps = d->eps;
-    const fortai_hip_qwen35_recurrent *R0 = nullptr;
-    const fortai_hip_qwen35_attention *A0 = nullptr;
-    for (auto &L : d->layers) {
-        if (L.recurrent && !R0) R0 = L.recurrent;
-        if (L.attention && !A0) A0 = L.attention;
-        if (L.gate->m.rows != d->ffn) return "FFN widths differ between layers";
-        if (L.recurrent && R0 && (L.recurrent->conv_size != R0->conv_size || L.recurrent->kernel != R0->kernel ||
-                                  L.recurrent->key_heads != R0->key_heads || L.recurrent->value_heads != R0->value_heads ||
-                                  L.recurrent->head != R0->head || L.recurrent->inner != R0->inner))
-            return "GDN shapes differ between layers";
-        if (L.attention && A0 && (L.attention->heads != A0->heads || L.attention->kv_heads != A0->kv_heads ||
-                                  L.attention->head != A0->head || L.attention->value != A0->value ||
-                                  L.attention->rope_dim != A0->rope_dim))
-            return "attention shapes differ between layers";
-    }
-    if (R0) {
-        if (R0->state_size != R0->head) return "GDN state size";
-        P.conv_size = R0->conv_size; P.kernel = R0->kernel; P.key_heads = R0->key_heads;
-        P.value_heads = R0->value_heads; P.head = R0->head; P.inner = R0->inner;
-    }
-    if (A0) {
-        P.heads = A0->heads; P.kv_heads = A0->kv_heads; P.head_dim = A0->head; P.value_dim = A0->value;
-        P.rope_dim = A0->rope_dim;
-    }
-    P.emb16 = d->emb16 ? d->emb16->data : nullptr;
-    if (d->emb8) P.emb8 = d->emb8->m;
-    const char *why = persistent_unsupported(P, grid);
-    if (*why) return why;
-    for (auto &L : d->layers) {  // projections: at most two row groups per wave
-        const int rg = L.recurrent ? L.recurrent->qkv->m.row_groups + L.recurrent->gate->m.row_groups +
-                                         L.recurrent->alpha->m.row_groups + L.recurrent->beta->m.row_groups
-                                   : L.attention->q->m.row_groups + L.attention->k->m.row_groups +
-                                         L.attention->v->m.row_groups;
-        if (rg > 2 * grid * 4) return "projection rows exceed two row groups per wave";
-    }
-    if (d->out16 && d->hidden % 64) return "LM head width";
-
-    // tagged-word arena: x0, then per layer proj | mid | ao | x1 | h | x2
-    size_t words = static_cast<size_t>(d->hidden);
-    std::vector<size_t> offs;
-    for (auto &L : d->layers) {
-        size_t proj, mid, ao = 0;
-        if (L.recurrent) {
-            proj = static_cast<size_t>(P.conv_size) + P.inner + 2 * P.value_heads;
-            mid = P.inner;
-        } else {
-            proj = 2 * static_cast<size_t>(P.heads) * P.head_dim + static_cast<size_t>(P.kv_heads) * (P.head_dim + P.value_dim);
-            mid = static_cast<size_t>(P.heads) * d->max_context;  // scores [head][position]
-            ao = static_cast<size_t>(P.heads) * P.value_dim;
-        }
-        offs.push_back(words);
-        words += proj + mid + ao + 2 * static_cast<size_t>(d->hidden) + d->ffn;
-    }
-    hipError_t e = alloc(&d->arena, words);
-    if (e == hipSuccess) e = hipMemsetAsync(d->arena, 0, words * sizeof(uint64_t), c->stream);
-    if (e == hipSuccess) e = alloc(&d->status, 8 + 2 * 256);
-    if (e == hipSuccess) e = hipMemsetAsync(d->status, 0, (8 + 2 * 256) * sizeof(int), c->stream);
-    if (e != hipSuccess) return "allocation";
-    std::vector<PersistentLayer> host(d->layers.size());
-    for (size_t i = 0; i < d->layers.size(); ++i) {
-        const decoder_layer &L = d->layers[i];
-        PersistentLayer &H = host[i];
-        uint64_t *b = d->arena + offs[i];
-        H.recurrent = L.recurrent ? 1 : 0;
-        H.attn_norm = L.attn_norm;
-        H.post_norm = L.post_norm;
-        H.ll_proj = b;
-        if (L.recurrent) {
-            const auto *R = L.recurrent;
-            H.ll_mid = b + P.conv_size + P.inner + 2 * P.value_heads;
-            H.ll_ao = nullptr;
-            H.ll_x1 = H.ll_mid + P.inner;
-            H.proj = persistent_matvec({{R->qkv, b}, {R->gate, b + P.conv_size}, {R->alpha, b + P.conv_size + P.inner},
-                                        {R->beta, b + P.conv_size + P.inner + P.value_heads}});
-            H.outp = persistent_matvec({{R->out, H.ll_x1}});
-            H.conv_w = R->conv_w; H.ssm_a = R->ssm_a; H.ssm_dt = R->ssm_dt; H.ssm_norm = R->ssm_norm;
-            H.conv_state = R->conv_state; H.state = R->state;
-        } else {
-            const auto *A = L.attention;
-            const size_t qw = 2 * static_cast<size_t>(P.heads) * P.head_dim;
-            const size_t kw = static_cast<size_t>(P.kv_heads) * P.head_dim;
-            const size_t vw = static_cast<size_t>(P.kv_heads) * P.value_dim;
-            H.ll_mid = b + qw + kw + vw;
-            H.ll_ao = H.ll_mid + static_cast<size_t>(P.heads) * d->max_context;
-            H.ll_x1 = H.ll_ao + static_cast<size_t>(P.heads) * P.value_dim;
-            H.proj = persistent_matvec({{A->q, b}, {A->k, b + qw}, {A->v, b + qw + kw}});
-            H.outp = persistent_matvec({{A->o, H.ll_x1}});
-            H.q_norm = A->q_norm; H.k_norm = A->k_norm; H.rope = A->rope;
-            H.kcache = A->kcache; H.vcache = A->vcache; H.cache_flags = A->cache_flags;
-        }
-        H.ll_h = H.ll_x1 + d->hidden;
-        H.ll_x2 = H.ll_h + d->ffn;
-        H.ffn1 = persistent_matvec({{L.gate, H.ll_h}, {L.up, nullptr}});
-        H.ffn2 = persistent_matvec({{L.down, H.ll_x2}});
-        if (i + 1 == d->layers.size()) H.ffn2.plain = d->x;  // the LM head's input
-    }
-    P.ll_x0 = d->arena;
-    P.token = c->token;
-    P.position = c->position;
-    P.status = d->status;
-    const char *times_env = std::getenv("FORTAI_HIP_PHASE_TIMES");
-    if (times_env && (std::strcmp(times_env, "1") == 0 || std::strcmp(times_env, "2") == 0)) {
-        const size_t n = static_cast<size_t>(grid) * (P.layers * 6 + 2);
-        const size_t n_all = times_env[0] == '2' ? 5 * n : n;  // times, then 4 marks per phase
-        if (alloc(&d->phase_times, n_all) != hipSuccess) return "allocation";
-        (void)hipMemsetAsync(d->phase_times, 0, n_all * sizeof(uint64_t), c->stream);
-        P.phase_times = d->phase_times;
-        if (times_env[0] == '2') P.phase_marks = d->phase_times + n;
-    }
-    e = hipMalloc(reinterpret_cast<void **>(&d->layers_dev), host.size() * sizeof(PersistentLayer));
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(d->layers_dev, host.data(), host.size() * sizeof(PersistentLayer), hipMemcpyHostToDevice,
-            c->stream);
-    P.layer = d->layers_dev;
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&d->plan_dev), sizeof(PersistentPlan));
-    if (e == hipSuccess) e = hipMemcpyAsync(d->plan_dev, &P, sizeof(PersistentPlan), hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return "plan upload";
-    d->grid = grid;
-    d->persistent = true;
-    return "";
-}
-}  // namespace
-}  // extern "C++"
 
 int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     fortai_hip_qwen35_recurrent *const *recurrent, fortai_hip_qwen35_attention *const *attention,
@@ -1620,21 +1510,10 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     if (e == hipSuccess) e = alloc(&d->trace, max_context + 1);
     if (e == hipSuccess) e = hipMemsetAsync(d->trace, 0, (max_context + 1) * sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    // FORTAI_HIP_DECODER=persistent: the one-launch step (all layers in one
-    // kernel, phases handed over through tagged words).  The default is the
-    // captured graph of per-op kernels, which measures faster on MI355X.
-    const char *path_env = std::getenv("FORTAI_HIP_DECODER");
-    if (e == hipSuccess && path_env && std::strcmp(path_env, "persistent") == 0) {
-        const std::string why = setup_persistent(d);
-        if (!why.empty()) {
-            fortai_hip_qwen35_decoder_destroy(d);
-            return fail(c, FORTAI_HIP_INVALID, ("persistent decoder unsupported: " + why).c_str());
-        }
-    }
     // the per-op decode step captured as a graph (FORTAI_HIP_DECODER_GRAPH=0
     // enqueues the kernels directly every step instead, e.g. for kernel tracing)
     const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
-    d->use_graph = !d->persistent && !(graph_env && std::strcmp(graph_env, "0") == 0);
+    d->use_graph = !(graph_env && std::strcmp(graph_env, "0") == 0);
     if (e == hipSuccess && d->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess && d->use_graph) {
         g_plan = &d->plan;
@@ -1666,8 +1545,6 @@ int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *d) {
     }
     release(d->output_norm); release(d->x); release(d->logits); release(d->argmax_value);
     release(d->argmax_index); release(d->trace);
-    release(d->arena); release(d->layers_dev); release(d->plan_dev); release(d->status);
-    release(d->phase_times);
     if (d->h_q8l) (void)hipFree(d->h_q8l);
     delete d;
     return FORTAI_HIP_OK;
@@ -1706,10 +1583,6 @@ int fortai_hip_qwen35_decoder_forward(fortai_hip_qwen35_decoder *d, int64_t toke
     if (e == hipSuccess && next_token)
         e = hipMemcpyAsync(next_token, c->token, sizeof(int64_t), hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess && (logits || next_token)) e = hipStreamSynchronize(c->stream);
-    if (e == hipSuccess && (logits || next_token)) {
-        const int rc = persistent_status(d);
-        if (rc != FORTAI_HIP_OK) return rc;
-    }
     return done(c, e, "decoder forward");
 }
 
@@ -1729,10 +1602,6 @@ int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *d, int64_t tok
         e = hipMemcpyAsync(trace, d->trace + position, static_cast<size_t>(steps) * sizeof(int64_t),
             hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e == hipSuccess) {
-        const int rc = persistent_status(d);
-        if (rc != FORTAI_HIP_OK) return rc;
-    }
     return done(c, e, "decoder generate");
 }
 
@@ -1750,26 +1619,7 @@ int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *d) {
     if (!d) return FORTAI_HIP_INVALID;
     auto *c = d->context;
     (void)hipSetDevice(c->device);
-    const hipError_t e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return done(c, e, "decoder status");
-    return persistent_status(d);
-}
-
-int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *d, uint64_t *host_times, size_t count) {
-    if (!d || !host_times || !d->phase_times) return FORTAI_HIP_INVALID;
-    size_t n = static_cast<size_t>(d->grid) * (d->layers.size() * 6 + 2);
-    const char *times_env = std::getenv("FORTAI_HIP_PHASE_TIMES");
-    if (times_env && times_env[0] == '2' && count >= 5 * n) n *= 5;  // marks follow the times
-    if (count < n) return FORTAI_HIP_INVALID;
-    auto *c = d->context;
-    (void)hipSetDevice(c->device);
-    hipError_t e = hipStreamSynchronize(c->stream);
-    if (e == hipSuccess) e = hipMemcpy(host_times, d->phase_times, n * sizeof(uint64_t), hipMemcpyDeviceToHost);
-    return done(c, e, "decoder phase times");
-}
-
-int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *d) {
-    return d ? (d->persistent ? 1 : 0) : -1;
+    return done(c, hipStreamSynchronize(c->stream), "decoder status");
 }
 
 int fortai_hip_qwen35_decoder_plan(const fortai_hip_qwen35_decoder *d, char *buffer, size_t bytes, size_t *needed) {

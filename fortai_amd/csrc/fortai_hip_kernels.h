@@ -66,7 +66,9 @@ struct MatvecSegment {
     const float *conv_w = nullptr;  // [rows][kernel]
     float *conv_state = nullptr;
     int conv_size = 0, kernel = 0;
+    int conv_rows = 0;              // > 0: only rows below it have the conv (rows past it: STORE)
     bool silu = false;              // STORE without conv: out[row] = silu(dot)
+    int silu_begin = 0, silu_end = 0;  // STORE: rows in [silu_begin, silu_end) also through SiLU
 };
 
 struct MatvecInput {
@@ -191,7 +193,7 @@ struct AttentionParams {
     const float2 *rope = nullptr;   // [max_context][rope_dim/2] (cos, sin)
     uint16_t *kcache = nullptr;     // [max_context][kv_heads][head] fp16 bits
     uint16_t *vcache = nullptr;     // [max_context][kv_heads][value] fp16 bits
-    float *partial = nullptr;       // scores [heads][max_context] (attention_scores_floats)
+    float *partial = nullptr;       // workspace (attention_scores_floats): scores, e values, Z tables
     int *cache_flags = nullptr;     // [kv_heads]: 1 once the cache holds an exponent-31 half
     float *out = nullptr;           // [heads][value] gated output
     const int *position = nullptr;  // device position (the new token's index)
@@ -203,6 +205,7 @@ struct AttentionParams {
     // split-K kernels are launched only when max_context > exact_max.
     int exact_max = 1 << 30;
     float *split = nullptr;         // [heads][attention_split_chunks][value + 2]
+    int z_skew = 0;                 // test hook: offset of the Z candidate windows (0 in use)
 };
 int attention_split_chunks(int max_context);
 // batch > 1: sequences along blockIdx.y, every buffer [batch][single size],
@@ -238,60 +241,5 @@ hipError_t launch_gdn_prefill(const GdnParams &p, int batch, int T, float *qinv,
 // the fp32 kernel throughout (the exact mode)
 hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, float *out, hipStream_t stream,
     bool matrix_cores);
-
-// ---- persistent decoder ------------------------------------------------------
-// One launch per token (decode_persistent.hip).  Activations cross
-// workgroups as 64-bit tagged words (tag << 32 | payload) in per-phase buffers;
-// the tag is the token sequence number + 1.
-struct PersistentMatvec {
-    Q8Matrix w[4];              // segments sharing the activation
-    uint64_t *out[4];           // tagged output words, one per row
-    int first_rg[5];            // cumulative row-group offsets of the segments
-    int count;
-    float *plain;               // optional plain fp32 copy of the outputs (read after the launch)
-};
-struct PersistentLayer {
-    int recurrent;              // 1 Gated DeltaNet, 0 full attention
-    const float *attn_norm, *post_norm;
-    PersistentMatvec proj;      // GDN: qkv | z | alpha | beta;  attention: q (q|gate per head) | k | v
-    PersistentMatvec outp;      // ssm_out / o_proj -> ll_x1 (+ residual)
-    PersistentMatvec ffn1;      // gate, up (SiLU pair) -> ll_h
-    PersistentMatvec ffn2;      // down -> ll_x2 (+ residual)
-    const float *conv_w, *ssm_a, *ssm_dt, *ssm_norm;
-    float *conv_state, *state;
-    const float *q_norm, *k_norm;
-    const float2 *rope;
-    uint16_t *kcache, *vcache;
-    int *cache_flags;
-    uint64_t *ll_proj;          // projection outputs (segments are views)
-    uint64_t *ll_mid;           // GDN raw output [inner] | attention chunk partials
-    uint64_t *ll_ao;            // attention merged, gated output [heads * value]
-    uint64_t *ll_x1, *ll_h, *ll_x2;  // residual after the mixer, FFN hidden, residual after the FFN
-};
-struct PersistentPlan {
-    int layers, hidden, ffn, vocab, max_context;
-    float eps;
-    int conv_size, kernel, key_heads, value_heads, head, inner;     // GDN
-    int heads, kv_heads, head_dim, value_dim, rope_dim;            // attention
-    const uint16_t *emb16;
-    Q8Matrix emb8;
-    uint64_t *ll_x0;            // embedding row [hidden]
-    const int64_t *token;
-    const int *position;
-    int *status;                // non-zero: a wait timed out (every workgroup has exited)
-    uint64_t *phase_times;      // optional [grid][phases]: realtime clock at the end of each phase
-    uint64_t *phase_marks;      // optional [grid][phases][4]: matvec phases' internal marks
-    const PersistentLayer *layer;  // device array [layers]
-};
-// Launch the layers of one decode step on `grid` workgroups (one per CU; all
-// must be co-resident); the plan lives in device memory.  The last layer's
-// residual is left in plain fp32 (ffn2.plain of the last layer) for the LM
-// head, which runs as its own kernels.  persistent_lds_bytes() is the
-// dynamic LDS of a workgroup.
-hipError_t launch_decode_persistent(const PersistentPlan *plan_device, uint32_t tag, int grid, hipStream_t stream);
-size_t persistent_lds_bytes();
-int persistent_blocks_per_cu();
-// Shape limits of the persistent path ("" when supported, else the reason).
-const char *persistent_unsupported(const PersistentPlan &plan, int grid);
 
 }  // namespace fortai_hip

@@ -217,7 +217,11 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
 // One wave per 8-row group, eight lanes per row.
 // NREG > 0: the matrix has exactly NREG chunks per row, all held in
 // registers; NREG = 0: any width, weights streamed in batches of 8 chunks.
-template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>
+// MULTI: several segments share the activation (a workgroup finds its
+// segment in first_wg); otherwise segment 0 only, so that every kernel
+// argument the waves read has a fixed offset and all of them arrive in one
+// scalar round trip.
+template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI>
 __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs args) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
     constexpr int kRegs = NREG > 0 ? NREG : 1;
@@ -227,9 +231,11 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     double *red = reinterpret_cast<double *>(lds + static_cast<size_t>(args.chunks) * 144);
     float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 144 + 8 * WAVES);
 
+    FORTAI_MV_MARK(5);
     const int wg = static_cast<int>(blockIdx.x);
     int s = 0;
-    while (s + 1 < args.count && wg >= args.first_wg[s + 1]) ++s;
+    if constexpr (MULTI)
+        while (s + 1 < args.count && wg >= args.first_wg[s + 1]) ++s;
     const MatvecSegment &seg = args.seg[s];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
@@ -268,7 +274,8 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
         if (writer) resid = seg.resid[row];
     // STORE with a conv: the row's window and taps, loaded now
     float win[kConvMax - 1], taps[kConvMax];
-    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr;
+    // (row groups are whole 8-row groups, so conv and SiLU are uniform per wave)
+    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr && (seg.conv_rows == 0 || row < seg.conv_rows);
     const int ck = conv ? seg.kernel : 0;
     if (conv && writer) {
 #pragma unroll
@@ -332,7 +339,8 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
                 if (t + 1 < ck - 1) seg.conv_state[static_cast<size_t>(t) * seg.conv_size + row] = win[t + 1];
             seg.conv_state[static_cast<size_t>(ck - 2) * seg.conv_size + row] = acc;
         } else if (writer) {
-            seg.out[row] = seg.silu ? silu_poly(acc) : acc;
+            const bool silu = seg.silu || (row >= seg.silu_begin && row < seg.silu_end);
+            seg.out[row] = silu ? silu_poly(acc) : acc;
         }
     } else if constexpr (EPI == Epilogue::ADD) {
         if (writer) seg.out[row] = acc + resid;
@@ -365,18 +373,22 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
 
 constexpr int kMatvecWaves = 4;  // large launches; small ones use one wave per workgroup
 
-template <int WAVES, int NREG, Prologue PRO, Epilogue EPI>
+template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI = false>
 hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES;
-    hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI>), dim3(grid), dim3(WAVES * 64), lds, stream, args);
-    note_launch("q8_matvec_kernel<waves=%d,regs=%d,%s,%s> grid %d", WAVES, NREG, prologue_name(PRO), epilogue_name(EPI),
-        grid);
+    hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI, MULTI>), dim3(grid), dim3(WAVES * 64), lds, stream,
+        args);
+    note_launch("q8_matvec_kernel<waves=%d,regs=%d,%s,%s%s> grid %d", WAVES, NREG, prologue_name(PRO),
+        epilogue_name(EPI), MULTI ? ",segments" : "", grid);
     return hipGetLastError();
 }
 
 template <int WAVES, Prologue PRO, Epilogue EPI>
 hipError_t launch_matvec_regs(const MatvecArgs &args, int grid, int chunks, hipStream_t stream) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
+    // several segments (the host-side pair/triplet products): the streamed form
+    if constexpr (EPI == Epilogue::STORE)
+        if (args.count > 1) return launch_matvec_t<WAVES, 0, PRO, EPI, true>(args, grid, stream);
     if (chunks == 8) return launch_matvec_t<WAVES, 8, PRO, EPI>(args, grid, stream);
     if (chunks == 16) return launch_matvec_t<WAVES, 16, PRO, EPI>(args, grid, stream);
     if (!kPair && chunks == 28) return launch_matvec_t<WAVES, kPair ? 0 : 28, PRO, EPI>(args, grid, stream);
@@ -526,7 +538,8 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
     const bool writer = active && l == 0 && row < seg.w.rows;
     // per-sequence residuals and conv windows, loaded now (clamped, unconditional)
     float resid[NS], win[NS][kConvMax - 1], taps[kConvMax];
-    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr;
+    // (row groups are whole 8-row groups, so conv and SiLU are uniform per wave)
+    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr && (seg.conv_rows == 0 || row < seg.conv_rows);
     const int ck = conv ? seg.kernel : 0;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
@@ -773,7 +786,8 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
     const int rowc = min(row, seg.w.rows - 1);
     const bool writer = l == 0 && row < seg.w.rows;
     float resid[NS], win[NS][kConvMax - 1], taps[kConvMax];
-    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr;
+    // (row groups are whole 8-row groups, so conv and SiLU are uniform per wave)
+    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr && (seg.conv_rows == 0 || row < seg.conv_rows);
     const int ck = conv ? seg.kernel : 0;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
@@ -1048,10 +1062,17 @@ hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const Matv
         if (in.head <= 0 || in.head % 4 || hl > 64 || (hl & (hl - 1)) || in.width % in.head || !in.z || !in.norm)
             return hipErrorInvalidValue;
     }
-    for (int s = 0; s < count; ++s)
-        if (segments[s].conv_w && (epilogue != Epilogue::STORE || segments[s].kernel < 2 ||
-                                     segments[s].kernel > kConvMax || segments[s].conv_size < segments[s].w.rows))
+    for (int s = 0; s < count; ++s) {
+        const MatvecSegment &g = segments[s];
+        const int conv_rows = g.conv_rows > 0 ? g.conv_rows : g.w.rows;
+        if (g.conv_w && (epilogue != Epilogue::STORE || g.kernel < 2 || g.kernel > kConvMax || g.conv_size < conv_rows ||
+                            conv_rows > g.w.rows || (g.conv_rows > 0 && conv_rows % kRowsPerWave)))
             return hipErrorInvalidValue;
+        if (g.silu_end > g.silu_begin && (epilogue != Epilogue::STORE || g.silu_begin % kRowsPerWave ||
+                                             (g.silu_end % kRowsPerWave && g.silu_end != g.w.rows)))
+            return hipErrorInvalidValue;
+    }
+    if (count > 1 && epilogue != Epilogue::STORE) return hipErrorInvalidValue;
     if (f32_in && in.width / 4 > kPre * kMatvecWaves * 64) return hipErrorInvalidValue;
     // small matrices: one wave per workgroup keeps their row groups spread
     // over many CUs (each CU's memory pipeline serves one wave's loads); large

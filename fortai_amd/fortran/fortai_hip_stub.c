@@ -582,20 +582,6 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
-FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *decoder)
-{
-    (void)decoder;
-    return -1;
-}
-
-FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *decoder, uint64_t *host_times, size_t count)
-{
-    (void)decoder;
-    (void)host_times;
-    (void)count;
-    return FORTAI_HIP_RUNTIME_ERROR;
-}
-
 FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits)
 {
     (void)decoder;

@@ -312,17 +312,9 @@ int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *decoder, int64
 /* enqueue `steps` further graph replays continuing from the device token and
  * position (no host synchronisation; for timing loops) */
 int fortai_hip_qwen35_decoder_replay(fortai_hip_qwen35_decoder *decoder, int steps);
-/* wait for the queued steps and report whether every persistent step
- * completed (RUNTIME_ERROR with the reason in last_error otherwise) */
+/* wait for the queued steps (RUNTIME_ERROR with the reason in last_error
+ * when a step failed) */
 int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *decoder);
-/* 1 when the decoder runs the persistent one-launch-per-token kernel, 0 for
- * the captured per-op graph (FORTAI_HIP_DECODER=graph|persistent selects) */
-int fortai_hip_qwen35_decoder_persistent(const fortai_hip_qwen35_decoder *decoder);
-/* with FORTAI_HIP_PHASE_TIMES=1 at create: the device realtime clock (100 MHz)
- * at the end of every phase of the last persistent step, [workgroup][slot],
- * slots = 6 * layers + 2 (embed, 6 per layer, one unused) */
-int fortai_hip_qwen35_decoder_phase_times(fortai_hip_qwen35_decoder *decoder, uint64_t *host_times,
-    size_t count);
 /* The kernels one decode step launches, as the reference's PlanIR steps
  * (src/fortai_plan_ir.f90:7-21: operation, kernel, batch size), recorded when
  * the step was captured (or by the first step): text lines

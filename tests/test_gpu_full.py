@@ -29,14 +29,13 @@ def full_model_path():
     return path
 
 
-@pytest.mark.parametrize("mode", ["persistent", "graph"])
-def test_full_model_128_step_trace(full_model_path, mode):
+def test_full_model_128_step_trace(full_model_path):
     from test_gpu_model import open_decoder
     with np.load(os.path.join(GOLDEN, "qwen35_0.8b_trace.npz")) as z:
         tokens, top_i, top_v = z["tokens"], z["top_index"], z["top_value"]
     with open(os.path.join(GOLDEN, "qwen35_0.8b_trace.json")) as f:
         meta = json.load(f)
-    m = open_decoder(full_model_path, meta["context"], mode)
+    m = open_decoder(full_model_path, meta["context"])
     try:
         logits = m.forward(meta["token"], 0).copy()
         scale = float(abs(top_v[0, 0]))

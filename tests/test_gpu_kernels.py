@@ -207,13 +207,17 @@ def test_gdn_core_128_steps(ctx, oracle):
         w.free()
 
 
-@pytest.mark.parametrize("L,exact_max", [(1, None), (70, None), (1024, None), (4096, None), (32768, None),
-                                         (32768, 1 << 20), (70, 0), (1024, 0), (4095, 0)])
-def test_attention_core(ctx, oracle, L, exact_max):
+@pytest.mark.parametrize("L,exact_max,skew", [(1, None, 0), (70, None, 0), (1024, None, 0), (4096, None, 0),
+                                              (32768, None, 0), (32768, 1 << 20, 0), (70, 0, 0), (1024, 0, 0),
+                                              (4095, 0, 0), (4096, None, 60), (4096, None, 1 << 20),
+                                              (8192, None, -90)])
+def test_attention_core(ctx, oracle, L, exact_max, skew):
     """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7, append + attend at position L-1.
     Up to FORTAI_HIP_EXACT_ATTENTION_MAX positions (default 8192) the output keeps the reference's two-pass
     summation orders and is bit-exact; beyond it, split-K with an online-softmax merge, within the north
-    star's 1e-3 relative.  exact_max None: the default; 1 << 20: exact at 32768; 0: split-K at every L."""
+    star's 1e-3 relative.  exact_max None: the default; 1 << 20: exact at 32768; 0: split-K at every L.
+    skew: FORTAI_HIP_ZTABLE_SKEW, which moves the Z candidate windows so that some (60, -90) or all
+    (1 << 20) running sums fall outside them and the resolution's own chain runs."""
     rng = np.random.default_rng(L)
     heads, kvh, head, H = 8, 2, 256, 1024
     mk = lambda rows, width: B.Q8Weights(ctx, synth.q8_blocks(rng, rows, width), rows, width)
@@ -221,16 +225,18 @@ def test_attention_core(ctx, oracle, L, exact_max):
     qn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     kn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     maxc = max(L, 64)
-    saved = os.environ.get("FORTAI_HIP_EXACT_ATTENTION_MAX")
+    saved = {k: os.environ.get(k) for k in ("FORTAI_HIP_EXACT_ATTENTION_MAX", "FORTAI_HIP_ZTABLE_SKEW")}
     if exact_max is not None:
         os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = str(exact_max)  # read when the layer is created
+    os.environ["FORTAI_HIP_ZTABLE_SKEW"] = str(skew)
     try:
         A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
     finally:
-        if saved is None:
-            os.environ.pop("FORTAI_HIP_EXACT_ATTENTION_MAX", None)
-        else:
-            os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = saved
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     kc = np.zeros(maxc * kvh * head, np.uint16)
     vc = np.zeros(maxc * kvh * head, np.uint16)
     n = (L - 1) * kvh * head
