@@ -80,6 +80,7 @@ _SIGNATURES = {
     "fortai_hip_q8_tokens_bytes": [_i, _i],
     "fortai_hip_q8_quantize_tokens_device": [_vp, _vp, _i, _i, _vp],
     "fortai_hip_q8_mmq_device": [_vp, _vp, _vp, _i, _vp, _vp, _fp],
+    "fortai_hip_q8_mmq_exact_device": [_vp, _vp, _vp, _i, _vp, _vp, _fp],
     "fortai_hip_q8_mmq_block_dots": [_vp, _vp, _vp, _i, _vp],
     "fortai_hip_qwen35_recurrent_core_device": [_vp, _vp, _vp, _vp, _vp],
     "fortai_hip_qwen35_recurrent_state_download": [_vp, _vp, _sz, _vp, _sz],

@@ -907,6 +907,23 @@ int fortai_hip_q8_mmq_device(fortai_hip_q8_context *c, const fortai_hip_q8_weigh
     return done(c, e, "token-block matmul");
 }
 
+int fortai_hip_q8_mmq_exact_device(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x8, int tokens,
+    void *out, const void *resid, float *kernel_ms) {
+    if (!c || !owned(c, w) || !x8 || !out || tokens <= 0) return FORTAI_HIP_INVALID;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipSuccess;
+    if (kernel_ms) e = hipEventRecord(c->start, c->stream);
+    if (e == hipSuccess)
+        e = launch_q8_mmq_exact(w->m, x8, tokens, static_cast<float *>(out), w->m.rows,
+            static_cast<const float *>(resid), c->stream);
+    if (kernel_ms) {
+        if (e == hipSuccess) e = hipEventRecord(c->stop, c->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(c->stop);
+        if (e == hipSuccess) e = hipEventElapsedTime(kernel_ms, c->start, c->stop);
+    }
+    return done(c, e, "token-block matmul (lane order)");
+}
+
 int fortai_hip_q8_mmq_block_dots(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x8,
     int tokens, void *dots) {
     if (!c || !owned(c, w) || !x8 || !dots || tokens <= 0) return FORTAI_HIP_INVALID;
@@ -2055,14 +2072,24 @@ hipError_t batch_prefill_buffers(fortai_hip_qwen35_batch *b, int rows) {
 // Every layer over batch * T prompt tokens (positions 0..T-1), then the LM
 // head on each sequence's last token, which leaves tokens / positions / trace
 // as after T decode steps.
-// exact: every projection through the bit-exact batched matvec, 8 tokens at a
-// time (the reference's lane order; for validating the prefill kernels)
-hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, hipStream_t stream) {
+// The modes (FORTAI_HIP_PREFILL):
+//  exact (default): the projections in the reference's lane order on the
+//    matrix cores (q8_mmq_exact_kernel) and the fp32 causal attention: every
+//    logit and state bit-identical to token-by-token decoding;
+//  fast: the projections as whole-block int32 dots (q8_mmq_kernel) and the
+//    fp16 matrix-core attention (outputs within fp32 rounding of the
+//    reference, not bit for bit);
+//  matvec: the projections through the batched decode matvec, 8 tokens at a
+//    time (a cross-check of the exact mode).
+enum class PrefillMode { EXACT, FAST, MATVEC };
+hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, PrefillMode mode, hipStream_t stream) {
     const int B = b->batch, H = b->hidden, N = B * T;
     hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, b->emb16->rows, H, b->ptokens, 0, b->px, stream, N)
                                 : launch_q8_embedding(b->emb8->m, b->ptokens, 0, b->px, stream, N), "token embeddings");
     auto mmq = [&](const fortai_hip_q8_weights *w, float *out, const float *resid, const char *op) {
-        if (!exact) return rec(launch_q8_mmq(w->m, b->px8, N, out, w->m.rows, resid, nullptr, stream), op);
+        if (mode == PrefillMode::EXACT)
+            return rec(launch_q8_mmq_exact(w->m, b->px8, N, out, w->m.rows, resid, stream), op);
+        if (mode == PrefillMode::FAST) return rec(launch_q8_mmq(w->m, b->px8, N, out, w->m.rows, resid, nullptr, stream), op);
         hipError_t r = hipSuccess;
         for (int r0 = 0; r0 < N && r == hipSuccess; r0 += 8) {
             const int cnt = std::min(8, N - r0);
@@ -2104,7 +2131,7 @@ hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, bool exact, 
             AttentionParams ap = attention_params(const_cast<fortai_hip_qwen35_attention *>(A), b->pa, b->pb, b->pc, b->pd);
             ap.kcache = L.kcache; ap.vcache = L.vcache; ap.cache_flags = L.flags; ap.max_context = b->max_context;
             if (e == hipSuccess)
-                e = rec(launch_attention_prefill(ap, B, T, b->pd, stream, !exact), "q/k norm, RoPE, KV append, causal attention");
+                e = rec(launch_attention_prefill(ap, B, T, b->pd, stream, mode == PrefillMode::FAST), "q/k norm, RoPE, KV append, causal attention");
             if (e == hipSuccess)
                 e = rec(launch_rms_quantize_tokens(b->pd, N, A->heads * A->value, nullptr, 0.0f, b->px8, stream),
                     "quantize attention output");
@@ -2172,14 +2199,16 @@ int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *b, const int64_t *t
     if (e == hipSuccess) e = hipMemcpyAsync(b->positions, last.data(), b->batch * sizeof(int), hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);  // the host arrays are borrowed for the call
     if (e == hipSuccess && kernel_ms) e = hipEventRecord(c->start, c->stream);
-    // FORTAI_HIP_PREFILL_EXACT=1: the projections in the reference's lane
-    // order (slow; validates the rest of the prefill against decoding)
-    const char *exact_env = std::getenv("FORTAI_HIP_PREFILL_EXACT");
-    const bool exact = exact_env && std::strcmp(exact_env, "1") == 0;
+    PrefillMode mode = PrefillMode::EXACT;
+    if (const char *env = std::getenv("FORTAI_HIP_PREFILL")) {
+        if (std::strcmp(env, "fast") == 0) mode = PrefillMode::FAST;
+        else if (std::strcmp(env, "matvec") == 0) mode = PrefillMode::MATVEC;
+        else if (std::strcmp(env, "exact") != 0) return fail(c, FORTAI_HIP_INVALID, "FORTAI_HIP_PREFILL: exact, fast or matvec");
+    }
     b->prefill_plan.clear();
     g_plan = &b->prefill_plan;
     g_plan_batch = static_cast<int>(N);
-    if (e == hipSuccess) e = enqueue_batch_prefill(b, T, exact, c->stream);
+    if (e == hipSuccess) e = enqueue_batch_prefill(b, T, mode, c->stream);
     g_plan = nullptr;
     g_plan_batch = 1;
     if (e == hipSuccess && kernel_ms) e = hipEventRecord(c->stop, c->stream);

@@ -192,6 +192,42 @@ __device__ __forceinline__ uint2 load_stream(const uint2 *p) {
     return make_uint2(v.x, v.y);
 }
 
+// ------------------------------------------------------ kernel arguments ----
+
+// Fetch every 64-byte line of the first BYTES of the kernel-argument segment
+// into the scalar cache with one round trip.  A kernel's argument reads are
+// scalar loads, and the compiler issues them where their values are first
+// needed, so a prologue that reads a pointer, waits, loads through it and
+// then reads the next argument pays one memory round trip per step; after
+// this every later argument read hits the scalar cache.
+// (One asm statement: the loads land in its own early-clobber register
+// before the statement ends, so no later instruction can be handed that
+// register while a load into it is still in flight.)
+#define FORTAI_KW1 "s_load_dword %0, %1, 0x0\n"
+#define FORTAI_KW2 FORTAI_KW1 "s_load_dword %0, %1, 0x40\n"
+#define FORTAI_KW3 FORTAI_KW2 "s_load_dword %0, %1, 0x80\n"
+#define FORTAI_KW4 FORTAI_KW3 "s_load_dword %0, %1, 0xc0\n"
+#define FORTAI_KW5 FORTAI_KW4 "s_load_dword %0, %1, 0x100\n"
+#define FORTAI_KW6 FORTAI_KW5 "s_load_dword %0, %1, 0x140\n"
+#define FORTAI_KW7 FORTAI_KW6 "s_load_dword %0, %1, 0x180\n"
+#define FORTAI_KW8 FORTAI_KW7 "s_load_dword %0, %1, 0x1c0\n"
+#define FORTAI_KW9 FORTAI_KW8 "s_load_dword %0, %1, 0x200\n"
+#define FORTAI_KW10 FORTAI_KW9 "s_load_dword %0, %1, 0x240\n"
+#define FORTAI_KW11 FORTAI_KW10 "s_load_dword %0, %1, 0x280\n"
+#define FORTAI_KW12 FORTAI_KW11 "s_load_dword %0, %1, 0x2c0\n"
+template <int BYTES>
+__device__ __forceinline__ void kernarg_warm() {
+    constexpr int kLines = (BYTES + 63) / 64;
+    static_assert(kLines >= 1 && kLines <= 12, "at most 12 lines");
+    const auto k = __builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t t;
+#define FORTAI_KW_CASE(n) \
+    if constexpr (kLines == n) asm volatile(FORTAI_KW##n "s_waitcnt lgkmcnt(0)" : "=&s"(t) : "s"(k) : "memory");
+    FORTAI_KW_CASE(1) FORTAI_KW_CASE(2) FORTAI_KW_CASE(3) FORTAI_KW_CASE(4) FORTAI_KW_CASE(5) FORTAI_KW_CASE(6)
+    FORTAI_KW_CASE(7) FORTAI_KW_CASE(8) FORTAI_KW_CASE(9) FORTAI_KW_CASE(10) FORTAI_KW_CASE(11) FORTAI_KW_CASE(12)
+#undef FORTAI_KW_CASE
+}
+
 // --------------------------------------------------------- reductions ----
 
 template <typename T>

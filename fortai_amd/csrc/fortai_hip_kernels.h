@@ -162,6 +162,10 @@ hipError_t launch_q8_quantize_tokens(const float *x, int tokens, int width, int 
 // int32 block dots [tokens][rows][blocks]
 hipError_t launch_q8_mmq(const Q8Matrix &w, const void *x8, int tokens, float *out, int ld_out, const float *resid,
     int32_t *dots, hipStream_t stream);
+// The same product with the reference's eight-lane fp32 order kept: every
+// output is bit-identical to the decode matvec of its token.
+hipError_t launch_q8_mmq_exact(const Q8Matrix &w, const void *x8, int tokens, float *out, int ld_out,
+    const float *resid, hipStream_t stream);
 
 // ---- Gated DeltaNet ------------------------------------------------------
 struct GdnParams {

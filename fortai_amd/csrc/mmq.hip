@@ -233,6 +233,190 @@ __global__ __launch_bounds__(kMmqThreads, 2) void q8_mmq_kernel(Q8Matrix w, cons
     }
 }
 
+// ------------------------------------------------------------- lane order
+// The same product with the reference's AVX2 accumulation kept exactly
+// (fortai_q8_dot.c:287-331): per (token, row) eight fp32 lane chains, lane L
+// adding fma(f32(w_scale) * x_scale, f32(dot of bytes 4L..4L+3), acc_L) block
+// by block, then the horizontal sum ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)).  So
+// every output is bit-identical to the decode matvec of that token.
+//
+// The 4-byte lane dots come from v_mfma_f32_32x32x4_2b_f16: two independent
+// 32x32x4 products per instruction (lanes 0..31 feed the first, 32..63 the
+// second), so four instructions give the eight lane dots of a 32 x 32 tile
+// and block.  int8 values are exact in fp16, and the products and their
+// 4-term sums (|sum| <= 4 * 128 * 127) are exact in the fp32 accumulator, so
+// the dots arrive as exact floats and need no conversion.  The int8 operands
+// are widened to fp16 once, when a chunk (four blocks) is staged in LDS: the
+// biased byte b + 128 under the fp16 exponent of 1024 is 1024 + b + 128
+// exactly, and one packed fp16 subtraction of 1152 leaves b.
+//
+// Staging: per block and token (or row) the eight 4-value lane parts in the
+// order 0 2 4 6 1 3 5 7, so that a lane reads its four parts (the first or
+// the second of each pair) as 32 contiguous bytes.
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+constexpr int kXTile = 64;    // tokens and rows per workgroup (4 waves of 32 x 32)
+constexpr int kXPitch = 36;   // halves per staged (block, token or row): 32 + 4 pad
+constexpr int kXThreads = 256;
+
+struct MmqExactStage {
+    _Float16 a[4][kXTile][kXPitch];
+    _Float16 b[4][kXTile][kXPitch];
+    float as[4][kXTile];
+    float bs[4][kXTile];
+};
+
+// the staged position of lane part L (order 0 2 4 6 1 3 5 7), in halves
+__device__ __forceinline__ int part_slot(int L) { return ((L & 1) * 4 + (L >> 1)) * 4; }
+
+// four signed bytes -> four fp16 values (exact)
+__device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;  // b + 128
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+    const h2 a = __builtin_bit_cast(h2, lo) - bias;
+    const h2 b = __builtin_bit_cast(h2, hi) - bias;
+    return h4{a.x, a.y, b.x, b.y};
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kXThreads, 2) void q8_mmq_exact_kernel(Q8Matrix w, const int8_t *__restrict__ xq,
+    const float *__restrict__ xs, int tokens, int ld, float *__restrict__ out, int ld_out,
+    const float *__restrict__ resid) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    MmqExactStage *stage = reinterpret_cast<MmqExactStage *>(lds_raw);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 31, h = lane >> 5;
+    const int t0 = static_cast<int>(blockIdx.y) * kXTile;
+    const int r0 = static_cast<int>(blockIdx.x) * kXTile;
+    const int twl = (wave & 1) * 32;   // wave's first token within the tile
+    const int rwl = (wave >> 1) * 32;  // wave's first row within the tile
+    const int chunks = w.chunks;
+    const size_t bstride = static_cast<size_t>(ld) * 32;  // bytes per block of X8
+    const int g_last = w.row_groups - 1;
+
+    // this thread's share of a chunk:
+    //   tokens: 4 blocks x 64 tokens x 2 halves = 512 pieces of 16 bytes, 2 per thread
+    //   rows:   8 row groups x 64 lanes         = 512 pieces of 16 bytes, 2 per thread
+    //   token scales: 256 floats, 1 per thread; row scales: 64 x uint2, threads < 64
+    u32x4_t ra[2], rb[2];
+    float rs = 0.0f;
+    uint2 rws = make_uint2(0u, 0u);
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = tid + k * kXThreads;  // 0..511
+            const int j = p >> 7, t = (p >> 1) & 63, hh = p & 1;
+            ra[k] = *reinterpret_cast<const u32x4_t *>(xq + static_cast<size_t>(4 * c + j) * bstride +
+                static_cast<size_t>(t0 + t) * 32 + hh * 16);
+            const int g = min((r0 >> 3) + (p >> 6), g_last);  // clamped; rows past the end are not stored
+            rb[k] = reinterpret_cast<const u32x4_t *>(w.quants)[(static_cast<size_t>(g) * chunks + c) * 64 + (p & 63)];
+        }
+        rs = xs[static_cast<size_t>(4 * c + (tid >> 6)) * ld + t0 + (tid & 63)];
+        if (tid < kXTile) {
+            const int g = min((r0 >> 3) + (tid >> 3), g_last);
+            rws = w.scales[(static_cast<size_t>(g) * chunks + c) * 8 + (tid & 7)];
+        }
+    };
+    auto stash = [&](MmqExactStage &st) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int p = tid + k * kXThreads;
+            const int j = p >> 7, t = (p >> 1) & 63, hh = p & 1;
+            const uint32_t wd[4] = {ra[k].x, ra[k].y, ra[k].z, ra[k].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                *reinterpret_cast<h4 *>(&st.a[j][t][part_slot(4 * hh + m)]) = i8x4_to_h4(wd[m]);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            // row piece: row (p >> 6) * 8 + r, lane part l of the four blocks
+            const int p = tid + k * kXThreads;
+            const int q = p & 63, r = q >> 3, l = q & 7;
+            const int row = (p >> 6) * 8 + r;
+            const uint32_t wd[4] = {rb[k].x, rb[k].y, rb[k].z, rb[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<h4 *>(&st.b[j][row][part_slot(l)]) = i8x4_to_h4(wd[j]);
+        }
+        st.as[tid >> 6][tid & 63] = rs;
+        if (tid < kXTile) {
+            st.bs[0][tid] = half_bits_to_float(static_cast<uint16_t>(rws.x & 0xffffu));
+            st.bs[1][tid] = half_bits_to_float(static_cast<uint16_t>(rws.x >> 16));
+            st.bs[2][tid] = half_bits_to_float(static_cast<uint16_t>(rws.y & 0xffffu));
+            st.bs[3][tid] = half_bits_to_float(static_cast<uint16_t>(rws.y >> 16));
+        }
+    };
+
+    float acc[8][16];
+#pragma unroll
+    for (int L = 0; L < 8; ++L)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[L][v] = 0.0f;
+
+    fetch(0);
+    stash(stage[0]);
+    __syncthreads();
+    for (int c = 0; c < chunks; ++c) {
+        const MmqExactStage &st = stage[c & 1];
+        if (c + 1 < chunks) fetch(c + 1);
+#pragma unroll 1
+        for (int j = 0; j < 4; ++j) {
+            // this lane's parts h, 2 + h, 4 + h, 6 + h of token twl + i and row rwl + i
+            const h4 *ap = reinterpret_cast<const h4 *>(&st.a[j][twl + i][16 * h]);
+            const h4 *bp = reinterpret_cast<const h4 *>(&st.b[j][rwl + i][16 * h]);
+            h4 av[4], bv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                av[k] = ap[k];
+                bv[k] = bp[k];
+            }
+            // scale products of this lane's 16 tokens twl + 8 (v / 4) + 4 h + v % 4 and row rwl + i
+            const float wsc = st.bs[j][rwl + i];
+            float sc[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 s4 = *reinterpret_cast<const float4 *>(&st.as[j][twl + 8 * q + 4 * h]);
+                sc[4 * q] = wsc * s4.x;
+                sc[4 * q + 1] = wsc * s4.y;
+                sc[4 * q + 2] = wsc * s4.z;
+                sc[4 * q + 3] = wsc * s4.w;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const f32x32 zero = {};
+                const f32x32 d = __builtin_amdgcn_mfma_f32_32x32x4f16(av[k], bv[k], zero, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    acc[2 * k][v] = __builtin_fmaf(sc[v], d[v], acc[2 * k][v]);
+                    acc[2 * k + 1][v] = __builtin_fmaf(sc[v], d[16 + v], acc[2 * k + 1][v]);
+                }
+                // one MFMA result live at a time (the other wave of the SIMD
+                // covers the MFMA latency)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (c + 1 < chunks) stash(stage[(c + 1) & 1]);
+        __syncthreads();
+    }
+    const int row = r0 + rwl + i;
+    if (row >= w.rows) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int t = t0 + twl + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (t >= tokens) continue;
+        // the horizontal sum of fortai_q8_dot.c:323-330
+        const float sum = ((acc[0][v] + acc[4][v]) + (acc[2][v] + acc[6][v])) +
+            ((acc[1][v] + acc[5][v]) + (acc[3][v] + acc[7][v]));
+        const size_t o = static_cast<size_t>(t) * ld_out + row;
+        if constexpr (EPI == 1) out[o] = sum + resid[o];
+        else out[o] = sum;
+    }
+}
+
 // fortai_q8_quantize (fortai_q8_dot.c:153-198) of every token into X8: one
 // thread per 4 values, 8 consecutive threads per block.
 __global__ __launch_bounds__(256) void q8_quantize_tokens_kernel(const float *__restrict__ x, int tokens, int width,
@@ -269,6 +453,24 @@ hipError_t launch_q8_quantize_tokens(const float *x, int tokens, int width, int 
     const size_t threads = static_cast<size_t>(ld) * blocks_pad * 8;
     hipLaunchKernelGGL(q8_quantize_tokens_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
         stream, x, tokens, width, ld_x, ld, blocks_pad, xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_mmq_exact(const Q8Matrix &w, const void *x8, int tokens, float *out, int ld_out,
+    const float *resid, hipStream_t stream) {
+    if (tokens <= 0 || ld_out < w.rows || w.rows <= 0) return hipErrorInvalidValue;
+    const int ld = q8_tokens_ld(tokens);  // a multiple of the 64-token tile
+    const int8_t *xq = static_cast<const int8_t *>(x8);
+    const float *xs = reinterpret_cast<const float *>(xq + static_cast<size_t>(ld) * w.chunks * 4 * 32);
+    const dim3 grid((w.rows + kXTile - 1) / kXTile, (tokens + kXTile - 1) / kXTile);
+    const size_t lds = 2 * sizeof(MmqExactStage);
+    if (resid)
+        hipLaunchKernelGGL((q8_mmq_exact_kernel<1>), grid, dim3(kXThreads), lds, stream, w, xq, xs, tokens, ld, out,
+            ld_out, resid);
+    else
+        hipLaunchKernelGGL((q8_mmq_exact_kernel<0>), grid, dim3(kXThreads), lds, stream, w, xq, xs, tokens, ld, out,
+            ld_out, resid);
+    note_launch("q8_mmq_exact_kernel<%s> grid %dx%d", resid ? "add" : "store", grid.x, grid.y);
     return hipGetLastError();
 }
 

@@ -346,6 +346,173 @@ __global__ __launch_bounds__(256) void qk_rope_append_kernel(float *__restrict__
     }
 }
 
+// Causal attention of every prompt token with the reference's arithmetic
+// and summation orders (fortai_qwen35_cpu.f90:1006-1031), so every output is
+// bit-identical to the decode step's exact attention at that position:
+//   s_j = (q . k_j, left to right, separately rounded) / sqrt(head)
+//   m = max s_j;  e_j = expf(s_j - m);  Z = e_0 + e_1 + ... (left to right)
+//   out_d = fl(e_0/Z v_0,d) + fl(e_1/Z v_1,d) + ... (left to right) * sigmoid(gate_d)
+// One workgroup per (block of qb queries, head, sequence).  The scores of
+// the block's keys stay in LDS (qb is chosen so that they fit); keys and
+// values pass through LDS 64 positions at a time.  A query's masked keys
+// (past its position) get e = +0 and weight +0: adding +0 or -0 to a running
+// sum leaves it unchanged, so every chain can run to the block's last key.
+constexpr int kXKeys = 64;  // keys per staged tile
+
+template <int HEAD>
+__global__ __launch_bounds__(256) void attention_prefill_exact_kernel(const float *__restrict__ q,
+    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, float *__restrict__ out, int T,
+    int heads, int kv_heads, int max_context, int qb, int kcap) {
+    static_assert(HEAD % 64 == 0 && HEAD <= 256, "head 64, 128 or 256");
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    float *qs = reinterpret_cast<float *>(lds_raw);                  // [qb][HEAD] normalized q
+    uint16_t *kv = reinterpret_cast<uint16_t *>(qs + qb * HEAD);    // K: [HEAD/8][kXKeys][8]; V: [kXKeys][HEAD]
+    float *sc = reinterpret_cast<float *>(kv + kXKeys * HEAD);       // [qb][kcap] scores, then e, then weights
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const int h = static_cast<int>(blockIdx.y), s = static_cast<int>(blockIdx.z);
+    const int q0 = static_cast<int>(blockIdx.x) * qb;
+    const int nq = min(qb, T - q0);
+    const int keys = q0 + nq;  // keys 0..keys-1 cover the block
+    const int kvh = h / (heads / kv_heads);
+    const float sqrt_head = sqrtf(static_cast<float>(HEAD));
+    for (int e = tid; e < qb * HEAD; e += 256) {
+        const int qi = e / HEAD, d = e % HEAD;
+        qs[e] = qi < nq ? q[((static_cast<size_t>(s) * T + q0 + qi) * heads + h) * 2 * HEAD + d] : 0.0f;
+    }
+    // ---- scores: thread (key j = lane, query group = wave), queries wave + 4 r
+    for (int j0 = 0; j0 < keys; j0 += kXKeys) {
+        __syncthreads();
+        for (int e = tid; e < kXKeys * (HEAD / 8); e += 256) {
+            const int j = e / (HEAD / 8), piece = e % (HEAD / 8);
+            const int p = min(j0 + j, keys - 1);
+            const uint4 v8 = *reinterpret_cast<const uint4 *>(
+                kcache + ((static_cast<size_t>(s) * max_context + p) * kv_heads + kvh) * HEAD + piece * 8);
+            *reinterpret_cast<uint4 *>(kv + (piece * kXKeys + j) * 8) = v8;
+        }
+        __syncthreads();
+        const int j = j0 + lane;
+        for (int r0 = 0; r0 < qb; r0 += 16) {  // up to 4 queries of this wave at a time
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int d = 0; d < HEAD; d += 8) {
+                const uint4 k8 = *reinterpret_cast<const uint4 *>(kv + ((d / 8) * kXKeys + lane) * 8);
+                const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+                float kf[8];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    kf[2 * u] = gguf_half_to_real(static_cast<uint16_t>(kw[u] & 0xffffu));
+                    kf[2 * u + 1] = gguf_half_to_real(static_cast<uint16_t>(kw[u] >> 16));
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int qi = r0 + wave + 4 * r;
+                    if (qi >= qb) break;
+                    const float4 qa = *reinterpret_cast<const float4 *>(qs + qi * HEAD + d);
+                    const float4 qc = *reinterpret_cast<const float4 *>(qs + qi * HEAD + d + 4);
+                    float a = acc[r];
+                    a = a + qa.x * kf[0];
+                    a = a + qa.y * kf[1];
+                    a = a + qa.z * kf[2];
+                    a = a + qa.w * kf[3];
+                    a = a + qc.x * kf[4];
+                    a = a + qc.y * kf[5];
+                    a = a + qc.z * kf[6];
+                    a = a + qc.w * kf[7];
+                    acc[r] = a;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int qi = r0 + wave + 4 * r;
+                if (qi < qb && j < keys) sc[qi * kcap + j] = acc[r] / sqrt_head;
+            }
+        }
+    }
+    __syncthreads();
+    // ---- softmax weights: queries wave, wave + 4, ...; lanes over keys
+    constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
+    for (int qi = wave; qi < nq; qi += 4) {
+        const int n = q0 + qi + 1;  // this query's keys
+        float *row = sc + qi * kcap;
+        float m = kLowest;
+        for (int j = lane; j < n; j += 64) m = fmaxf(m, row[j]);
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        for (int j = lane; j < keys; j += 64) row[j] = j < n ? expf_libm(row[j] - m) : 0.0f;
+    }
+    __syncthreads();
+    // Z of each query by one lane, left to right (masked keys add +0)
+    if (lane < 4) {
+        const int qi = wave + 4 * lane;
+        float z = 0.0f;
+        if (qi < nq) {
+            const float *row = sc + qi * kcap;
+            int j = 0;
+            for (; j + 4 <= keys; j += 4) {
+                const float4 e4 = *reinterpret_cast<const float4 *>(row + j);
+                z = z + e4.x;
+                z = z + e4.y;
+                z = z + e4.z;
+                z = z + e4.w;
+            }
+            for (; j < keys; ++j) z = z + row[j];
+        }
+        // the weights e_j / Z (lanes of this wave finish the row below)
+        if (qi < nq) qs[qi * HEAD] = z;  // q is no longer needed: slot 0 of the row holds Z
+    }
+    __syncthreads();
+    for (int qi = wave; qi < nq; qi += 4) {
+        const float z = qs[qi * HEAD];
+        float *row = sc + qi * kcap;
+        for (int j = lane; j < keys; j += 64) row[j] = row[j] / z;
+    }
+    // ---- P.V: thread = (dim d, queries qd, qd + QS, ...)
+    constexpr int kQS = 256 / HEAD;  // query phases per dim
+    const int d = tid % HEAD, qd = tid / HEAD;
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int j0 = 0; j0 < keys; j0 += kXKeys) {
+        __syncthreads();
+        for (int e = tid; e < kXKeys * (HEAD / 8); e += 256) {
+            const int j = e / (HEAD / 8), piece = e % (HEAD / 8);
+            const int p = min(j0 + j, keys - 1);
+            *reinterpret_cast<uint4 *>(kv + j * HEAD + piece * 8) = *reinterpret_cast<const uint4 *>(
+                vcache + ((static_cast<size_t>(s) * max_context + p) * kv_heads + kvh) * HEAD + piece * 8);
+        }
+        __syncthreads();
+        const int jn = min(kXKeys, keys - j0);
+        for (int jj = 0; jj < jn; jj += 4) {
+            float vf[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) vf[u] = gguf_half_to_real(kv[min(jj + u, jn - 1) * HEAD + d]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int qi = qd + kQS * r;
+                if (qi >= nq) break;
+                const float *w = sc + qi * kcap + j0 + jj;
+                if (jj + 4 <= jn) {
+                    const float4 w4 = *reinterpret_cast<const float4 *>(w);
+                    float a = acc[r];
+                    a = a + w4.x * vf[0];
+                    a = a + w4.y * vf[1];
+                    a = a + w4.z * vf[2];
+                    a = a + w4.w * vf[3];
+                    acc[r] = a;
+                } else {
+                    for (int u = 0; u < jn - jj; ++u) acc[r] = acc[r] + w[u] * vf[u];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int qi = qd + kQS * r;
+        if (qi >= nq) break;
+        const size_t row = (static_cast<size_t>(s) * T + q0 + qi) * heads + h;
+        const float gate = q[row * 2 * HEAD + HEAD + d];
+        out[row * HEAD + d] = acc[r] * sigmoid_ref(gate);
+    }
+}
+
 // Causal attention of every prompt token (fortai_qwen35_cpu.f90:1006-1033
 // with an online softmax): one workgroup per (query block of 64, head,
 // sequence); four threads per query, each with a quarter of the head dims;
@@ -570,12 +737,14 @@ __global__ __launch_bounds__(256) void attention_prefill_mfma_kernel(const float
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[dt][i] *= corr;
         }
+        // the denominator sums the same fp16-rounded probabilities the P.V
+        // products use, so numerator and denominator round alike
         float pl[16];
         float zt = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             pl[i] = sc[i] == -__builtin_inff() ? 0.0f : __expf(sc[i] - m);
-            zt += pl[i];
+            zt += static_cast<float>(static_cast<_Float16>(pl[i]));
         }
         zl += zt;
         const half8_t pb0 = {static_cast<_Float16>(pl[0]), static_cast<_Float16>(pl[1]), static_cast<_Float16>(pl[2]),
@@ -767,6 +936,36 @@ hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, 
         }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
+    }
+    if (!matrix_cores) {
+        // the exact kernel: queries per workgroup so that the block's scores fit in LDS
+        const int kcap = (T + 3) / 4 * 4;
+        int qb = 16;
+        auto lds_of = [&](int b) {
+            return static_cast<size_t>(b) * p.head * 4 + static_cast<size_t>(kXKeys) * p.head * 2 +
+                static_cast<size_t>(b) * kcap * 4;
+        };
+        while (qb > 1 && lds_of(qb) > 150 * 1024) qb /= 2;
+        if (lds_of(qb) > 150 * 1024) return hipErrorInvalidValue;
+        const dim3 xgrid((T + qb - 1) / qb, p.heads, batch);
+        switch (p.head) {
+        case 64:
+            hipLaunchKernelGGL(attention_prefill_exact_kernel<64>, xgrid, dim3(256), lds_of(qb), stream, p.q, p.kcache,
+                p.vcache, out, T, p.heads, p.kv_heads, p.max_context, qb, kcap);
+            break;
+        case 128:
+            hipLaunchKernelGGL(attention_prefill_exact_kernel<128>, xgrid, dim3(256), lds_of(qb), stream, p.q, p.kcache,
+                p.vcache, out, T, p.heads, p.kv_heads, p.max_context, qb, kcap);
+            break;
+        case 256:
+            hipLaunchKernelGGL(attention_prefill_exact_kernel<256>, xgrid, dim3(256), lds_of(qb), stream, p.q, p.kcache,
+                p.vcache, out, T, p.heads, p.kv_heads, p.max_context, qb, kcap);
+            break;
+        default: return hipErrorInvalidValue;
+        }
+        note_launch("qk_rope_append_kernel grid %d + attention_prefill_exact_kernel<%d> grid %dx%dx%d", batch * T, p.head,
+            xgrid.x, xgrid.y, xgrid.z);
+        return hipGetLastError();
     }
     const int only_flagged = mfma ? 1 : 0;
     const dim3 grid((T + kQBlock - 1) / kQBlock, p.heads, batch);

@@ -232,6 +232,7 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 144 + 8 * WAVES);
 
     FORTAI_MV_MARK(5);
+    kernarg_warm<sizeof(MatvecArgs)>();
     const int wg = static_cast<int>(blockIdx.x);
     int s = 0;
     if constexpr (MULTI)

@@ -617,6 +617,14 @@ FORTAI_HIP_WEAK int fortai_hip_q8_mmq_device(fortai_hip_q8_context *context, con
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
+FORTAI_HIP_WEAK int fortai_hip_q8_mmq_exact_device(fortai_hip_q8_context *context, const fortai_hip_q8_weights *weights,
+    const void *device_tokens, int tokens, void *device_output, const void *device_residual, float *kernel_ms)
+{
+    (void)context; (void)weights; (void)device_tokens; (void)tokens; (void)device_output; (void)device_residual;
+    (void)kernel_ms;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
 FORTAI_HIP_WEAK int fortai_hip_q8_mmq_block_dots(fortai_hip_q8_context *context, const fortai_hip_q8_weights *weights,
     const void *device_tokens, int tokens, void *device_dots)
 {

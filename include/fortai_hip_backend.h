@@ -242,12 +242,19 @@ int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *context,
  * result += scale * dot per block (fortai_q8_dot.c:262-284), so results
  * agree with the AVX2 path to fp32 rounding.  kernel_ms (may be NULL):
  * event-timed kernel duration, synchronising.
+ * mmq_exact: the same product with the reference's AVX2 accumulation kept
+ * (eight fp32 lane chains per output and its horizontal sum,
+ * fortai_q8_dot.c:287-331): every output is bit-identical to the decode
+ * matvec of its token.  The prompt prefill's default projections.
  * mmq_block_dots: the exact int32 dot of every (token, row, block), device
  * int32 [tokens][rows][width/32] (parity probe). */
 size_t fortai_hip_q8_tokens_bytes(int tokens, int width);
 int fortai_hip_q8_quantize_tokens_device(fortai_hip_q8_context *context,
     const void *device_x, int tokens, int width, void *device_tokens);
 int fortai_hip_q8_mmq_device(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_tokens, int tokens,
+    void *device_output, const void *device_residual, float *kernel_ms);
+int fortai_hip_q8_mmq_exact_device(fortai_hip_q8_context *context,
     const fortai_hip_q8_weights *weights, const void *device_tokens, int tokens,
     void *device_output, const void *device_residual, float *kernel_ms);
 int fortai_hip_q8_mmq_block_dots(fortai_hip_q8_context *context,

@@ -1,10 +1,11 @@
-"""Token-block Q8_0 x Q8_0 product on the i8 matrix cores, through the C ABI.
+"""Token-block Q8_0 x Q8_0 products on the matrix cores, through the C ABI.
 
 The reference runs every token through the Q8 matvec
 (fortai_gguf_runtime.f90:424-465).  Bars: the per-token quantization and
-the int32 block dots bit-exact against the oracle; the fp32 outputs within
-1e-3 relative of the oracle's AVX2 matvec of each token (north_star), which
-the scalar per-block accumulation meets with a large margin.
+the int32 block dots bit-exact against the oracle; the lane-order product
+(mmq_exact, the prefill's default) bit-identical to the oracle's AVX2 matvec
+of every token; the whole-block product (mmq, the fast variant) within 1e-5
+relative of it (the north star allows 1e-3).
 """
 
 import ctypes
@@ -99,4 +100,34 @@ def test_mmq_prefill_shape(ctx, oracle):
     got = out.download(np.float32).reshape(tokens, rows)
     for t in (0, 1, 63, 64, 255, 511):
         assert rel_err(got[t], oracle.matvec(w, rows, width, x[t])) <= 1e-5, f"token {t}"
+    W.free()
+
+
+@pytest.mark.parametrize("rows,width,tokens", [(13, 96, 5), (200, 1024, 37), (3584, 1024, 64), (1024, 3584, 70),
+                                               (9216, 2560, 130)])
+def test_mmq_lane_order_bit_identical(ctx, oracle, rows, width, tokens):
+    """q8_mmq_exact_kernel: every output equals the reference matvec of its
+    token bit for bit (ragged rows, partial token tiles, a 4B FFN shape); the
+    residual epilogue adds in place."""
+    rng = np.random.default_rng(rows + 7 * width + tokens)
+    w = synth.q8_blocks(rng, rows, width)
+    x = rng.standard_normal((tokens, width)).astype(np.float32)
+    x[0, :32] = 0.0
+    x[1 % tokens, 32:64] = 1e4
+    W = B.Q8Weights(ctx, w, rows, width)
+    dx = ctx.upload_array(x)
+    dq = ctx.alloc(B.load().fortai_hip_q8_tokens_bytes(tokens, width))
+    ctx.call("fortai_hip_q8_quantize_tokens_device", ctx.h, dx.ptr, tokens, width, dq.ptr)
+    out = ctx.alloc(tokens * rows * 4)
+    ctx.call("fortai_hip_q8_mmq_exact_device", ctx.h, W.h, dq.ptr, tokens, out.ptr, None, None)
+    got = out.download(np.float32).reshape(tokens, rows)
+    sample = range(tokens) if tokens <= 70 else (0, 1, 63, 64, 65, 127, 128, 129)
+    for t in sample:
+        want = oracle.matvec(w, rows, width, x[t])
+        assert np.array_equal(got[t].view(np.uint32), want.view(np.uint32)), \
+            f"token {t}: max rel {rel_err(got[t], want):.2e}"
+    resid = rng.standard_normal((tokens, rows)).astype(np.float32)
+    dr = ctx.upload_array(resid)
+    ctx.call("fortai_hip_q8_mmq_exact_device", ctx.h, W.h, dq.ptr, tokens, dr.ptr, dr.ptr, None)
+    assert np.array_equal(dr.download(np.float32).reshape(tokens, rows), (got + resid).astype(np.float32))
     W.free()

@@ -1,27 +1,23 @@
-"""Prompt prefill of a batch (512-token prefill per
-sequence on the Q8_0 x Q8_0 token-block path) through the C ABI.
+"""Prompt prefill of a batch (a prefill per sequence on
+the Q8_0 x Q8_0 token-block path) through the C ABI.
 
 The reference has no prefill: it decodes the prompt one token at a time
 (fortai_qwen35_cpu.f90:591-711), with the AVX2 eight-lane accumulation of
-every Q8_0 dot.  The prefill computes each block dot exactly (int32, on the
-matrix cores) but accumulates the scaled block dots in a different fp32 order,
-so each projection agrees with the reference to ~1e-6 relative
-(tests/test_gpu_mmq.py).  End to end, every layer re-quantizes its
-activations to int8: a ~1e-7 difference now and then moves a value across an
-int8 rounding boundary, and that one-step change propagates through the
-recurrent state, the caches and the later layers (the 4B widths re-quantize
-~18K values per token and layer, so at that shape most sequences see one).
-Two bars follow:
-- with FORTAI_HIP_PREFILL_EXACT=1 the projections run in the reference's
-  lane order and everything else is the prefill's own code: the logits are
-  then bit-identical to token-by-token decoding (one-token prompts by
-  construction; longer prompts as measured) -- this validates the conv1d, the
-  delta rule, RoPE and the KV append, the causal attention, the gating and
-  the quantizers of the prefill;
-- in the default (matrix-core) mode the logits stay within 1e-1 relative of
-  token-by-token decoding and the greedy next token agrees for nearly every
-  sequence.
-The prefilled state continues decoding deterministically.
+every Q8_0 dot.  The bars:
+- default mode (exact): the projections keep that eight-lane order on the
+  matrix cores (q8_mmq_exact_kernel) and the causal attention keeps the
+  reference's summation orders (attention_prefill_kernel), so the logits of
+  the last prompt token are bit-identical to token-by-token decoding, which
+  is itself bit-identical to the reference (tests/test_gpu_model.py,
+  tests/test_gpu_full.py) -- and to the oracle directly;
+- FORTAI_HIP_PREFILL=matvec (projections through the batched decode matvec)
+  gives the same bits, a cross-check of the matrix-core lane order;
+- FORTAI_HIP_PREFILL=fast (whole-block int32 dots with one fp32 chain per
+  output and the fp16 matrix-core attention) is a performance variant: every
+  layer re-quantizes its activations to int8, so a ~1e-7 difference now and
+  then moves a value across an int8 rounding boundary and propagates; its
+  logits are held to the measured bound below and its greedy next tokens to
+  token-by-token decoding for all but one sequence in ten.
 """
 
 import numpy as np
@@ -32,11 +28,20 @@ from fortai_amd.qwen35 import Qwen35Hip
 
 pytestmark = pytest.mark.gpu
 
+# FORTAI_HIP_PREFILL=fast: bound on the relative logit error against
+# token-by-token decoding at these shapes (largest measured: 4.1e-2, 4B
+# layer shapes at T = 64)
+FAST_REL = 5e-2
+
 
 def rel_err(got, want):
     want = np.asarray(want, dtype=np.float64)
     scale = np.maximum(np.abs(want), np.sqrt(np.mean(want ** 2)) + 1e-30)
     return float(np.max(np.abs(np.asarray(got, np.float64) - want) / scale))
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
 @pytest.fixture(scope="module")
@@ -52,18 +57,57 @@ def paths(tmp_path_factory):
 def decode_prompt(m, prompt):
     """The single-sequence decoder fed the prompt token by token."""
     m.decoder.reset()
-    for pos, tok in enumerate(prompt):
-        nxt = m.decoder.forward(int(tok), pos)
+    for pos, tok in enumerate(prompt[:-1]):
+        m.decoder.forward(int(tok), pos, want_logits=False)
+    nxt = m.decoder.forward(int(prompt[-1]), len(prompt) - 1)
     return m.decoder.logits.copy(), nxt
 
 
-@pytest.mark.parametrize("name,batch,lengths", [("qwen35-tiny", 4, (17, 24, 33, 48, 64, 70)),
+@pytest.mark.parametrize("name,batch,lengths", [("qwen35-tiny", 4, (1, 2, 17, 24, 33, 48, 64, 70)),
                                                 ("qwen35-tiny-q8emb", 4, (33, 65)),
-                                                ("qwen35-4b-short", 8, (64,)),
-                                                # many 32-key tiles of the matrix-core attention
+                                                ("qwen35-4b-short", 8, (1, 64)),
                                                 ("qwen35-tiny", 2, (511,)),
                                                 ("qwen35-4b-short", 2, (300,))])
-def test_prefill_close_to_token_by_token_decode(paths, name, batch, lengths):
+def test_prefill_bit_identical_to_token_by_token_decode(paths, name, batch, lengths):
+    m = Qwen35Hip(paths[name], max_context=max(128, max(lengths) + 8), batch=batch)
+    try:
+        for T in lengths:
+            rng = np.random.default_rng(T * 13 + batch)
+            prompts = rng.integers(0, m.d.vocab, size=(batch, T))
+            m.batch.reset()
+            nxt, _ = m.batch.prefill(prompts)
+            logits = m.batch.logits.copy()
+            for s in range(batch):
+                want_logits, want_next = decode_prompt(m, prompts[s])
+                print(f"{name} T {T} sequence {s}: rel {rel_err(logits[s], want_logits):.2e} "
+                      f"next {int(nxt[s])} / {want_next}", flush=True)
+                assert same_bits(logits[s], want_logits), f"T {T} sequence {s}"
+                assert int(nxt[s]) == want_next
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("name,batch,T", [("qwen35-tiny", 4, 24), ("qwen35-4b-short", 8, 17)])
+def test_matvec_mode_gives_the_same_bits(paths, name, batch, T, monkeypatch):
+    rng = np.random.default_rng(T)
+    m = Qwen35Hip(paths[name], max_context=64, batch=batch)
+    try:
+        prompts = rng.integers(0, m.d.vocab, size=(batch, T))
+        m.batch.reset()
+        m.batch.prefill(prompts)
+        exact = m.batch.logits.copy()
+        monkeypatch.setenv("FORTAI_HIP_PREFILL", "matvec")
+        m.batch.reset()
+        m.batch.prefill(prompts)
+        assert same_bits(m.batch.logits, exact)
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("name,batch,lengths", [("qwen35-tiny", 4, (17, 64)), ("qwen35-tiny", 2, (511,)),
+                                                ("qwen35-4b-short", 8, (64,)), ("qwen35-4b-short", 2, (300,))])
+def test_fast_mode_prefill_close_to_decode(paths, name, batch, lengths, monkeypatch):
+    monkeypatch.setenv("FORTAI_HIP_PREFILL", "fast")
     m = Qwen35Hip(paths[name], max_context=max(128, max(lengths) + 8), batch=batch)
     errs, agree, total = [], 0, 0
     try:
@@ -78,34 +122,36 @@ def test_prefill_close_to_token_by_token_decode(paths, name, batch, lengths):
                 errs.append(rel_err(logits[s], want_logits))
                 agree += int(nxt[s]) == want_next
                 total += 1
-                print(f"{name} T {T} sequence {s}: rel {errs[-1]:.2e} next {int(nxt[s])} / {want_next}", flush=True)
+                print(f"fast {name} T {T} sequence {s}: rel {errs[-1]:.2e} next {int(nxt[s])} / {want_next}",
+                      flush=True)
     finally:
         m.close()
-    assert max(errs) <= 1e-1
+    assert max(errs) <= FAST_REL
     assert agree >= total - max(1, total // 10)
 
 
 @pytest.mark.parametrize("name,batch,T", [("qwen35-tiny", 3, 40), ("qwen35-4b-short", 8, 32)])
 def test_prefilled_state_continues_exactly(paths, name, batch, T):
-    """Prefill T-1 tokens then decode the last prompt token and 6 more: the
-    same steps replayed after a second identical prefill give the same
-    tokens (the prefill leaves a complete, deterministic decode state), and
-    the decode steps after a prefill are the batch decoder's own."""
+    """Prefill T-1 tokens then decode the last prompt token: the logits equal
+    those of a prefill of all T tokens bit for bit, and the decode steps that
+    follow equal the single-sequence decoder's."""
     m = Qwen35Hip(paths[name], max_context=128, batch=batch)
     try:
         rng = np.random.default_rng(T + batch)
         prompts = rng.integers(0, m.d.vocab, size=(batch, T))
-        runs = []
-        for _ in range(2):
-            m.batch.reset()
-            m.batch.prefill(prompts[:, :-1])
-            runs.append(m.batch.generate(prompts[:, -1], np.full(batch, T - 1, dtype=np.int32), 7))
-        assert np.array_equal(runs[0], runs[1])
-        # prefill of all T tokens vs prefill of T-1 + one decode step: same next token
+        m.batch.reset()
+        m.batch.prefill(prompts[:, :-1])
+        step = m.batch.forward(prompts[:, -1], np.full(batch, T - 1, dtype=np.int32))
+        step_logits = m.batch.logits.copy()
         m.batch.reset()
         nxt, _ = m.batch.prefill(prompts)
-        agree = int(np.sum(nxt == runs[0][:, 0]))
-        assert agree >= batch - 1
+        assert same_bits(m.batch.logits, step_logits)
+        assert np.array_equal(nxt, step)
+        trace = m.batch.generate(nxt, np.full(batch, T, dtype=np.int32), 6)
+        for s in range(batch):
+            _, want_next = decode_prompt(m, prompts[s])
+            assert want_next == int(nxt[s])
+            assert m.decoder.generate(want_next, T, 6).tolist() == trace[s].tolist(), f"sequence {s}"
     finally:
         m.close()
 
@@ -123,42 +169,7 @@ def test_prefill_matches_oracle(paths, oracle):
             ref.reset()
             for pos, tok in enumerate(prompts[s]):
                 want = ref.forward(int(tok), pos)
-            err = rel_err(m.batch.logits[s], want)
-            print(f"oracle sequence {s}: rel {err:.2e}", flush=True)
-            assert err <= 1e-1
+            assert same_bits(m.batch.logits[s], want), f"sequence {s}: rel {rel_err(m.batch.logits[s], want):.2e}"
             assert int(nxt[s]) == int(np.argmax(want))
-    finally:
-        m.close()
-
-
-@pytest.mark.parametrize("name,batch", [("qwen35-tiny", 8), ("qwen35-4b-short", 8)])
-def test_exact_mode_prefill_matches_decode(paths, name, batch, monkeypatch):
-    """FORTAI_HIP_PREFILL_EXACT=1 runs the projections in the reference's
-    lane order; everything else is the prefill's own code.  A one-token prompt
-    then has no order difference left anywhere (the single-key softmax is
-    exact), so its logits must equal the decoder's bit for bit; with longer
-    prompts only the attention's online softmax differs from the decoder's
-    two-pass sums."""
-    monkeypatch.setenv("FORTAI_HIP_PREFILL_EXACT", "1")
-    m = Qwen35Hip(paths[name], max_context=64, batch=batch)
-    try:
-        rng = np.random.default_rng(7)
-        prompts = rng.integers(0, m.d.vocab, size=(batch, 1))
-        m.batch.reset()
-        nxt, _ = m.batch.prefill(prompts)
-        for s in range(batch):
-            want_logits, want_next = decode_prompt(m, prompts[s])
-            assert np.array_equal(m.batch.logits[s].view(np.uint32), want_logits.view(np.uint32)), f"sequence {s}"
-            assert int(nxt[s]) == want_next
-        errs = []
-        for T in (2, 5, 24):
-            prompts = rng.integers(0, m.d.vocab, size=(batch, T))
-            m.batch.reset()
-            nxt, _ = m.batch.prefill(prompts)
-            for s in range(batch):
-                want_logits, want_next = decode_prompt(m, prompts[s])
-                errs.append(rel_err(m.batch.logits[s], want_logits))
-                print(f"exact {name} T {T} sequence {s}: rel {errs[-1]:.2e}", flush=True)
-        assert np.median(errs) <= 1e-5
     finally:
         m.close()
