@@ -13,9 +13,14 @@ over ~4096 positions.  Each step is one replay of the decoder's HIP graph;
 the greedy token and the position advance on the device, so the timed region
 holds no host round trip.  All weights are resident in HBM before timing.
 
+The greedy ids of all 4096 positions (cache fill, warm-up, timed steps) are
+compared with the compiled reference's 4096-step trace (`trace`).
+
 Also reported:
-  roofline      -- the dominant kernel (fp16 LM head + fused argmax, 508.6 MB
-                   per launch) timed live with HIP events on the context stream;
+  roofline      -- the dominant kernel family, every Q8_0 matvec launch of a
+                   decode step, timed live with HIP events on the context
+                   stream (a graph of exactly those launches);
+  roofline_lm_head -- the fp16 LM head + fused argmax (508.6 MB per launch);
   matvec        -- BASELINE config 1 (3584 x 1024 Q8_0, quantize + GEMV) over
                    275 distinct weight copies (1.07 GB, beyond the 256 MB
                    Infinity Cache), as a captured graph of back-to-back launches;
@@ -97,7 +102,30 @@ def bench_decode(args, path):
     ev_ms = ctx.timer_stop()
     t1 = time.perf_counter()
     wall_ms = (t1 - t0) * 1e3
-    return model, wall_ms, ev_ms
+    return model, wall_ms, ev_ms, trace_check(dec, ctx_len)
+
+
+GOLDEN_TRACE = os.path.join(ROOT, "tests", "golden", "qwen35_0.8b_trace_4096.npz")
+
+
+def trace_check(dec, n: int):
+    """The greedy ids of positions 0..n-1 (cache fill, warm-up and timed
+    steps) against the compiled reference's trace from token 9419
+    (tests/golden/qwen35_0.8b_trace_4096.npz, written by
+    tests/golden/make_golden.py --trace4096)."""
+    got = dec.trace(0, n)
+    out = {"positions": f"0..{n - 1}", "golden": os.path.relpath(GOLDEN_TRACE, ROOT)}
+    if not os.path.exists(GOLDEN_TRACE):
+        out["trace_matches_reference"] = None
+        return out
+    import numpy as np
+    with np.load(GOLDEN_TRACE) as z:
+        want = z["tokens"][:n]
+    diff = np.nonzero(got[:len(want)] != want)[0]
+    out["compared"] = int(len(want))
+    out["trace_matches_reference"] = bool(len(want) == n and diff.size == 0)
+    out["first_mismatch"] = int(diff[0]) if diff.size else None
+    return out
 
 
 def lm_head_roofline(model, reps: int = 20):
@@ -127,6 +155,58 @@ def lm_head_roofline(model, reps: int = 20):
             "algorithmic_bytes": algo, "avg_launch_us": round(ms * 1e3, 2)}
 
 
+def matvec_family_bytes(d) -> int:
+    """Algorithmic bytes of every Q8_0 matvec of one decode step: each
+    weight once (34 B per 32 values) plus the activation and output vectors."""
+    q8 = lambda rows, width: rows * (width // 32) * 34
+    total = 0
+    for i in range(d.layers):
+        if (i + 1) % d.interval != 0:
+            mats = [(d.conv_size + d.inner + 2 * d.value_heads, d.hidden), (d.hidden, d.inner)]
+        else:
+            mats = [(2 * d.heads * d.head_size + 2 * d.kv_heads * d.head_size, d.hidden),
+                    (d.hidden, d.heads * d.value_size)]
+        mats += [(2 * d.ffn, d.hidden), (d.hidden, d.ffn)]
+        total += sum(q8(r, w) + 4 * (r + w) for r, w in mats)
+    return total
+
+
+def matvec_family_roofline(model, warmup: int = 4, reps: int = 32):
+    """The dominant kernel family of the decode step: every Q8_0 matvec launch
+    of one step (q8_matvec_kernel, 114 launches at the 0.8B shape), timed live
+    with HIP events on the context stream by replaying a graph of exactly those
+    launches (a decoder created with FORTAI_HIP_DECODER_MATVEC_ONLY=1: same
+    kernels, weights and arguments, the other kernels of the step left out)."""
+    from fortai_amd import backend as B
+    d = model.d
+    os.environ["FORTAI_HIP_DECODER_MATVEC_ONLY"] = "1"
+    try:
+        dec = B.Decoder(model.ctx, model.recurrent, model.attention,
+                        [model.q8[f"blk.{i}.ffn_gate.weight"] for i in range(d.layers)],
+                        [model.q8[f"blk.{i}.ffn_up.weight"] for i in range(d.layers)],
+                        [model.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
+                        [n["attn"] for n in model.norms], [n["post"] for n in model.norms], model.output_norm,
+                        d.hidden, model.embedding, model.output, 64, d.eps, d.vocab)
+    finally:
+        os.environ.pop("FORTAI_HIP_DECODER_MATVEC_ONLY", None)
+    try:
+        ctx = model.ctx
+        launches = sum(1 for step in dec.plan() if "q8_matvec" in step[1])
+        dec.replay(warmup)
+        ctx.synchronize()
+        ctx.timer_start()
+        dec.replay(reps)
+        us = ctx.timer_stop() * 1e3 / reps
+    finally:
+        dec.free()
+    algo = matvec_family_bytes(d)
+    achieved = algo / (us * 1e-6) / 1e9
+    return {"kernel": f"q8_matvec_kernel family: every Q8_0 projection of one decode step ({launches} launches)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_from_profile("decode_matvec"),
+            "algorithmic_bytes": algo, "us_per_step": round(us, 2), "avg_launch_us": round(us / max(launches, 1), 3)}
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     (profiles/<name>_pmc.json, written from a committed profiling run)."""
@@ -137,7 +217,7 @@ def traffic_from_profile(name: str):
         return json.load(f).get("traffic_bytes_per_launch")
 
 
-def traffic_probe(reps: int = 5, decode_model: str = None) -> None:
+def traffic_probe(reps: int = 5, decode_model: str = None, decode_only: bool = False) -> None:
     """Launches for the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes that
     price each kernel's HBM traffic (direct launches, no graphs, no timing):
     * calibration: fortai_hip_qwen35_add_device over 2^26 floats, algorithmic
@@ -161,6 +241,9 @@ def traffic_probe(reps: int = 5, decode_model: str = None) -> None:
     ctx.synchronize()
     for buf in (a, b, o):
         buf.free()
+    if decode_only:
+        ctx.close()
+        return decode_probe(decode_model)
     rows, width = 248320, 1024
     rng = np.random.default_rng(7)
     w = (rng.standard_normal(rows * width, dtype=np.float32) * np.float32(0.02)).astype(np.float16)
@@ -238,17 +321,25 @@ def traffic_probe(reps: int = 5, decode_model: str = None) -> None:
     ctx.close()
     log("traffic probe: GDN step done")
     if decode_model:
-        os.environ["FORTAI_HIP_DECODER_GRAPH"] = "0"
-        from fortai_amd.qwen35 import Qwen35Hip
-        model = Qwen35Hip(decode_model, max_context=256)
-        model.reset()
-        model.generate(START_TOKEN, 8, 0)
-        model.ctx.synchronize()
-        model.close()
-        log("traffic probe: 8 direct-launch decode steps done")
+        decode_probe(decode_model)
 
 
-def pmc_summary(fetch_dir: str, write_dir: str) -> None:
+PROBE_STEPS = 8
+
+
+def decode_probe(path: str) -> None:
+    """PROBE_STEPS decode steps of the 0.8B model with direct launches."""
+    os.environ["FORTAI_HIP_DECODER_GRAPH"] = "0"
+    from fortai_amd.qwen35 import Qwen35Hip
+    model = Qwen35Hip(path, max_context=256)
+    model.reset()
+    model.generate(START_TOKEN, PROBE_STEPS, 0)
+    model.ctx.synchronize()
+    model.close()
+    log(f"traffic probe: {PROBE_STEPS} direct-launch decode steps done")
+
+
+def pmc_summary(fetch_dir: str, write_dir: str, family_steps: int = 0) -> None:
     """Per-kernel HBM traffic from the two rocprofv3 --pmc passes of
     --traffic-probe (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each
     scaled by what the same counter reads for the calibration add kernel
@@ -282,8 +373,17 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> None:
         kernels[k] = {"dispatches": len(f_), "fetch_kib_avg": round(sum(f_) / len(f_), 3),
                       "write_kib_avg": round(sum(w_) / len(w_), 3),
                       "traffic_bytes_avg": int(sum(f_) / len(f_) * 1024 * fscale + sum(w_) / len(w_) * 1024 * wscale)}
-    print(json.dumps({"calibration": {"kernel": cal, "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4)},
-                      "kernels": kernels}, indent=1))
+    doc = {"calibration": {"kernel": cal, "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4)},
+           "kernels": kernels}
+    if family_steps:
+        # a decode-only probe: the matvec family's traffic per step
+        fam = [k for k in kernels if k.startswith("q8_matvec_kernel")]
+        per_step = sum(kernels[k]["traffic_bytes_avg"] * kernels[k]["dispatches"] for k in fam) / family_steps
+        doc["matvec_family"] = {"kernels": fam, "steps": family_steps,
+                                "launches_per_step": sum(kernels[k]["dispatches"] for k in fam) / family_steps,
+                                "traffic_bytes_per_step": int(per_step)}
+        doc["traffic_bytes_per_launch"] = int(per_step)  # the family's launches of one step
+    print(json.dumps(doc, indent=1))
 
 
 def bench_matvec(model, copies: int = 275, reps: int = 4):
@@ -435,41 +535,81 @@ def bench_attention(cases=((1024, None), (4096, None), (32768, None), (32768, 1 
             "lengths": results}
 
 
-def cpu_baseline(path, ctx_len: int, steps: int):
-    """The reference CPU decode (oracle/_ref/fortai_cpu_run) on this host."""
-    exe = os.path.join(ROOT, "oracle", "_ref", "fortai_cpu_run")
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="spread", OMP_PLACES="cores")
-    if os.path.exists(exe):
-        log(f"timing the reference CPU path: {steps} decode steps, {threads} threads")
-        out = subprocess.run([exe, path, str(START_TOKEN), str(steps), str(ctx_len)], capture_output=True,
+def host_cpu() -> dict:
+    """lscpu model name, physical cores and the CPUs this process may use."""
+    info = {"model": None, "physical_cores": None, "cpus_available": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                info["model"] = line.split(":", 1)[1].strip()
+        cores = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, timeout=20).stdout
+        info["physical_cores"] = len({ln for ln in cores.splitlines() if ln and not ln.startswith("#")})
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
+def cpu_baseline(path, ctx_len: int, steps: int, repeats: int = 5):
+    """The reference CPU decode on this host (benchmark/README.md:120-135,
+    benchmark/tune_qwen35_cpu.sh:18): oracle/_ref/fast/ref_time (the
+    reference's sources with its native optimisation flags) runs `steps`
+    greedy steps of the same GGUF at the positions the GPU line is timed at
+    (ctx-steps .. ctx-1; the cache below them holds zeros, the same work per
+    step); first a thread sweep (one run each), then `repeats` runs at the
+    fastest thread count, whose median is the value."""
+    import statistics
+    exe = os.path.join(ROOT, "oracle", "_ref", "fast", "ref_time")
+    if not os.path.exists(exe):
+        exe = os.path.join(ROOT, "oracle", "_ref", "ref_time")
+    if not os.path.exists(exe):
+        log("oracle/_ref is not built: no CPU baseline")
+        return None
+    host = host_cpu()
+    limit = min(16, int(os.environ.get("OMP_NUM_THREADS", host["cpus_available"])), host["cpus_available"])
+    start = ctx_len - steps
+
+    def run(threads, nsteps, first):
+        env = dict(os.environ, OMP_NUM_THREADS=str(threads), OMP_PROC_BIND="spread", OMP_PLACES="cores")
+        out = subprocess.run([exe, path, str(START_TOKEN), str(nsteps), str(ctx_len), str(first)], capture_output=True,
                              text=True, env=env, timeout=600)
         m = re.search(r"forward_seconds=\s*([0-9.Ee+-]+)", out.stdout)
         if out.returncode != 0 or not m:
-            log("reference CPU run failed: " + out.stdout[-500:] + out.stderr[-500:])
-            return None
-        secs = float(m.group(1))
-        return {"value": round(steps / secs, 4), "unit": "tokens/s", "cores": threads, "kind": "reference",
-                "sample": f"{steps} greedy decode steps of the same 0.8B GGUF from token {START_TOKEN} at positions "
-                          f"0..{steps - 1} (forward only, load excluded); reference Fortran+C CPU path built by "
-                          f"oracle/Makefile (-O2, AVX2 dispatch), OMP_NUM_THREADS={threads}"}
-    # the restated CPU path (same algorithm) when the reference build is absent
-    import numpy as np
-    from oracle.oracle import Oracle, OracleModel
-    log(f"oracle/_ref missing; timing the restated CPU path ({steps} steps)")
-    m = OracleModel(Oracle(), path, ctx_len)
-    t = time.perf_counter()
-    m.greedy(START_TOKEN, steps)
-    secs = time.perf_counter() - t
-    return {"value": round(steps / secs, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} greedy decode steps at positions 0..{steps - 1} with oracle/liboracle.so"}
+            raise RuntimeError("reference CPU run failed: " + out.stdout[-300:] + out.stderr[-300:])
+        return nsteps / float(m.group(1))
+
+    sweep = {}
+    t = 1
+    while t <= limit:
+        log(f"CPU baseline: thread sweep, {t} threads")
+        sweep[t] = round(run(t, 1, ctx_len - 1), 4)
+        t *= 2
+    if limit not in sweep:
+        sweep[limit] = round(run(limit, 1, ctx_len - 1), 4)
+    best = max(sweep, key=sweep.get)
+    log(f"CPU baseline: {repeats} runs of {steps} steps at {best} threads")
+    vals = [run(best, steps, start) for _ in range(repeats)]
+    return {"value": round(statistics.median(vals), 4), "unit": "tokens/s", "cores": best, "kind": "reference",
+            "sample": f"{steps} greedy decode steps of the same 0.8B GGUF from token {START_TOKEN} at positions "
+                      f"{start}..{ctx_len - 1} of a {ctx_len} context (forward + maxloc, load excluded); median of "
+                      f"{repeats} runs; the reference's Fortran+C sources built with its native flags "
+                      f"(oracle/Makefile ref-fast: -O3 -march=x86-64-v3 -funroll-loops -ffast-math, OpenMP, the "
+                      f"AVX2 paths it dispatches)",
+            "repeats": [round(v, 4) for v in vals], "min": round(min(vals), 4), "max": round(max(vals), 4),
+            "stdev": round(statistics.stdev(vals), 4) if len(vals) > 1 else 0.0,
+            "thread_sweep_tokens_per_s": sweep, "host": host}
 
 
-def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: int = 8, ctx: int = 8192):
+def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: int = 8, ctx: int = 8192,
+                  check: int = 2):
     """Qwen3.5-4B shape (hidden 2560, 32 layers, FFN 9216,
     16 q / 4 kv heads, vocab 248320), batch 8 independent sequences, context
-    8192: a 512-token prefill of every sequence (token-block products on the
-    i8 matrix cores), then batch-8 greedy decode from the prefilled state."""
+    8192: a 512-token prefill of every sequence, then batch-8 greedy decode
+    from the prefilled state.  The default prefill is bit-exact (projections
+    in the reference's lane order on the matrix cores, the exact causal
+    attention); FORTAI_HIP_PREFILL=fast (whole-block dots, fp16 matrix-core
+    attention) is timed as a separate variant.  `check` sequences are decoded
+    token by token with the single-sequence decoder and compared bit for bit."""
     import ctypes
     import numpy as np
     from fortai_amd import backend as B, synth
@@ -482,21 +622,46 @@ def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: in
         synth.write_model(path + ".part", synth.CONFIGS["qwen35-4b"])
         os.replace(path + ".part", path)
         log(f"  done in {time.time() - t:.1f}s")
-    m = Qwen35Hip(path, max_context=ctx, fused=False, batch=batch)
+    m = Qwen35Hip(path, max_context=ctx, batch=batch)
     d, ctxh = m.d, m.ctx
     rng = np.random.default_rng(0x51E5)
     prompts = rng.integers(0, d.vocab, size=(batch, prompt))
+
+    def prefill(mode):
+        os.environ["FORTAI_HIP_PREFILL"] = mode
+        try:
+            m.batch.reset()
+            m.batch.prefill(prompts)  # the first call allocates the prefill buffers
+            m.batch.reset()
+            return m.batch.prefill(prompts)
+        finally:
+            os.environ.pop("FORTAI_HIP_PREFILL", None)
+
+    _, fast_ms = prefill("fast")
+    nxt, prefill_ms = prefill("exact")
+    logits = m.batch.logits.copy()
+    log(f"config 5 prefill: {batch} x {prompt} tokens in {prefill_ms:.1f} ms (fast variant {fast_ms:.1f} ms)")
+    trace = m.batch.generate(nxt, np.full(batch, prompt, dtype=np.int32), 4)
+    # decode timing from the prefilled state
     m.batch.reset()
-    m.batch.prefill(prompts)  # allocates the prefill buffers
-    m.batch.reset()
-    nxt, prefill_ms = m.batch.prefill(prompts)
-    log(f"config 5 prefill: {batch} x {prompt} tokens in {prefill_ms:.1f} ms")
+    prefill("exact")
     m.batch.replay(warmup)
     ctxh.synchronize()
     ctxh.timer_start()
     m.batch.replay(steps)
     dec_ms = ctxh.timer_stop()
     step_ms = dec_ms / steps
+    # exactness: sequences decoded token by token with the single-sequence decoder
+    checked = []
+    for s_ in range(check):
+        dec = m.decoder
+        dec.reset()
+        for pos in range(prompt - 1):
+            dec.forward(int(prompts[s_, pos]), pos, want_logits=False)
+        want_next = dec.forward(int(prompts[s_, -1]), prompt - 1)
+        same_logits = bool(np.array_equal(logits[s_].view(np.uint32), dec.logits.view(np.uint32)))
+        same_steps = dec.generate(want_next, prompt, 4).tolist() == trace[s_].tolist()
+        checked.append(same_logits and int(nxt[s_]) == want_next and same_steps)
     L = prompt + warmup + steps // 2
     q8 = lambda rows, width: rows * (width // 32) * 34
     n_attn = sum(1 for i in range(d.layers) if (i + 1) % d.interval == 0)
@@ -516,29 +681,44 @@ def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: in
     out = ctxh.alloc(tokens * d.ffn * 4)
     ctxh.call("fortai_hip_q8_quantize_tokens_device", ctxh.h, dx.ptr, tokens, d.hidden, dq.ptr)
     ms = ctypes.c_float()
-    best = 1e9
-    for _ in range(5):
-        ctxh.call("fortai_hip_q8_mmq_device", ctxh.h, w.h, dq.ptr, tokens, out.ptr, None, ctypes.byref(ms))
-        best = min(best, ms.value)
-    ops = 2.0 * d.ffn * d.hidden * tokens
-    tops = ops / (best * 1e-3) / 1e12
+
+    def best_of(entry):
+        best = 1e9
+        for _ in range(5):
+            ctxh.call(entry, ctxh.h, w.h, dq.ptr, tokens, out.ptr, None, ctypes.byref(ms))
+            best = min(best, ms.value)
+        return best
+    exact_best, fast_best = best_of("fortai_hip_q8_mmq_exact_device"), best_of("fortai_hip_q8_mmq_device")
+    macs = float(d.ffn) * d.hidden * tokens
     for b_ in (dx, dq, out):
         b_.free()
     m.close()
+    tops = 2 * macs / (exact_best * 1e-3) / 1e12
+    # vector work of the lane order: per (token, row, block) eight fp32 FMAs and one scale product
+    valu_tflops = macs / 32 * 17 / (exact_best * 1e-3) / 1e12
     return {
         "workload": f"Qwen3.5-4B-shaped Q8_0, batch {batch} independent sequences, context {ctx}",
         "prefill": {"tokens": tokens, "prompt_per_sequence": prompt, "ms": round(prefill_ms, 2),
                     "tokens_per_s": round(tokens / (prefill_ms * 1e-3), 1),
-                    "path": "token-block Q8_0 x Q8_0 products on v_mfma_i32_32x32x32_i8; conv1d, delta rule and "
-                            "causal attention looping over time"},
+                    "path": "projections in the reference's eight-lane fp32 order on v_mfma_f32_32x32x4_2b_f16 "
+                            "(q8_mmq_exact_kernel); conv1d, delta rule and exact causal attention over time",
+                    "fast_variant": {"ms": round(fast_ms, 2), "tokens_per_s": round(tokens / (fast_ms * 1e-3), 1),
+                                     "path": "FORTAI_HIP_PREFILL=fast: whole-block int32 dots on "
+                                             "v_mfma_i32_32x32x32_i8, fp16 matrix-core attention (not bit-exact)"}},
         "decode": {"batch": batch, "positions": f"{prompt + warmup}..{prompt + warmup + steps - 1}",
                    "ms_per_step": round(step_ms, 4), "tokens_per_s": round(batch * steps / (dec_ms * 1e-3), 1),
                    "algorithmic_bytes_per_step": int(step_bytes),
-                   "gbps": round(step_bytes / (step_ms * 1e-3) / 1e9, 1),
-                   "exactness": "every sequence bit-identical to the single-sequence decoder"},
-        "mmq": {"kernel": f"q8_mmq_kernel ({d.ffn} x {d.hidden} FFN gate over {tokens} tokens)",
-                "bound": "mfma", "achieved": round(tops, 1), "peak": 5000.0, "unit": "TOP/s (int8)",
-                "frac": round(tops * 1e12 / 5.0e15, 4), "avg_launch_us": round(best * 1e3, 1)},
+                   "gbps": round(step_bytes / (step_ms * 1e-3) / 1e9, 1)},
+        "exactness": {"sequences_checked": check, "bit_identical_to_token_by_token_decode": all(checked),
+                      "per_sequence": checked,
+                      "what": "last prompt token's logits (bits), greedy next token and the next 4 batched decode "
+                              "steps against the single-sequence decoder fed the prompt token by token"},
+        "mmq": {"kernel": f"q8_mmq_exact_kernel ({d.ffn} x {d.hidden} FFN gate over {tokens} tokens)",
+                "bound": "mfma", "achieved": round(tops, 1), "peak": 2500.0, "unit": "TFLOP/s (fp16 dense)",
+                "frac": round(tops / 2500.0, 4), "avg_launch_us": round(exact_best * 1e3, 1),
+                "valu": {"achieved": round(valu_tflops, 1), "peak": 157.3, "unit": "TFLOP/s (fp32)",
+                         "frac": round(valu_tflops / 157.3, 4)},
+                "fast_variant_us": round(fast_best * 1e3, 1)},
     }
 
 
@@ -582,6 +762,7 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--model", default=None)
     ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--cpu-repeats", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 2 (GDN) and config 3 (attention) figures")
@@ -592,6 +773,9 @@ def main() -> int:
                     help="only launch the kernels the --pmc traffic passes measure (see traffic_probe)")
     ap.add_argument("--probe-decode", action="store_true",
                     help="with --traffic-probe: also run 8 direct-launch decode steps of the 0.8B model")
+    ap.add_argument("--probe-decode-only", action="store_true",
+                    help="with --traffic-probe: only the calibration and the decode steps; with --pmc-summary: "
+                         "also report the matvec family's traffic per decode step")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print per-kernel HBM traffic from the FETCH_SIZE and WRITE_SIZE passes, then exit")
     ap.add_argument("--no-graph", action="store_true",
@@ -611,18 +795,20 @@ def main() -> int:
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     if args.traffic_probe:
-        traffic_probe(decode_model=model_path(args) if args.probe_decode else None)
+        traffic_probe(decode_model=model_path(args) if (args.probe_decode or args.probe_decode_only) else None,
+                      decode_only=args.probe_decode_only)
         return 0
     if args.pmc_summary:
-        pmc_summary(*args.pmc_summary)
+        pmc_summary(*args.pmc_summary, family_steps=PROBE_STEPS if args.probe_decode_only else 0)
         return 0
     if args.config5_only:
         print(json.dumps({"config5": bench_config5()}), flush=True)
         return 0
     path = model_path(args)
-    model, wall_ms, ev_ms = bench_decode(args, path)
+    model, wall_ms, ev_ms, trace = bench_decode(args, path)
     tok_s = args.steps / (wall_ms * 1e-3)
-    roof = lm_head_roofline(model)
+    roof = matvec_family_roofline(model)
+    roof_lm = lm_head_roofline(model)
     mv = None if args.no_matvec else bench_matvec(model)
     kernels = None
     if not args.no_kernels:
@@ -635,7 +821,7 @@ def main() -> int:
     model.close()
     if not args.no_config5:
         model_cfg5 = bench_config5()
-    cpu = None if args.no_cpu_baseline else cpu_baseline(path, args.ctx, args.cpu_steps)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(path, args.ctx, args.cpu_steps, args.cpu_repeats)
     line = {
         "metric": "decode tokens/sec (bs=1, ctx 4096) + Q8_0 matvec HBM GB/s, Qwen3.5-0.8B shape",
         "value": round(tok_s, 2),
@@ -657,7 +843,9 @@ def main() -> int:
                    "context": args.ctx, "batch": 1, "decoder": decoder},
         "decode_hbm": {"algorithmic_bytes_per_token": int(step_bytes), "gbps": round(decode_gbps, 1),
                        "frac_of_8TBps": round(decode_gbps / HBM_PEAK_GBPS, 4)},
+        "trace": trace,
         "roofline": roof,
+        "roofline_lm_head": roof_lm,
         "matvec": mv,
         "kernels": kernels,
         "config5": model_cfg5,

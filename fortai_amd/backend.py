@@ -96,6 +96,7 @@ _SIGNATURES = {
     "fortai_hip_qwen35_decoder_generate": [_vp, _i64, _i, _i, _vp],
     "fortai_hip_qwen35_decoder_replay": [_vp, _i],
     "fortai_hip_qwen35_decoder_logits": [_vp, _vpp],
+    "fortai_hip_qwen35_decoder_trace": [_vp, _i, _i, _vp],
     "fortai_hip_qwen35_decoder_status": [_vp],
     "fortai_hip_qwen35_decoder_plan": [_vp, _vp, _sz, C.POINTER(C.c_size_t)],
     "fortai_hip_qwen35_batch_plan": [_vp, _i, _vp, _sz, C.POINTER(C.c_size_t)],
@@ -421,6 +422,12 @@ class Decoder:
 
     def replay(self, steps: int) -> None:
         self.ctx.call("fortai_hip_qwen35_decoder_replay", self.h, steps)
+
+    def trace(self, first: int, count: int) -> np.ndarray:
+        """The greedy ids chosen at positions first .. first+count-1."""
+        out = np.zeros(count, dtype=np.int64)
+        self.ctx.call("fortai_hip_qwen35_decoder_trace", self.h, first, count, _ptr(out))
+        return out
 
     def check(self) -> None:
         """Wait for the queued steps; raise if one failed."""

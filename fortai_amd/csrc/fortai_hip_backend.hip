@@ -129,6 +129,11 @@ struct fortai_hip_qwen35_decoder {
     bool use_graph = true;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // FORTAI_HIP_DECODER_MATVEC_ONLY=1 at create: a step enqueues only its
+    // Q8_0 matvec launches (same kernels, weights and arguments; the other
+    // kernels are left out, so the values are meaningless) -- for timing
+    // the matvec family of a decode step
+    bool matvec_only = false;
     std::vector<plan_step> plan;  // the launches of one step (PlanIR steps)
 };
 
@@ -189,6 +194,7 @@ int fail(fortai_hip_q8_context *ctx, int code, const char *op, hipError_t err = 
     return code;
 }
 
+thread_local bool g_matvec_only = false;  // enqueue only the Q8_0 matvecs (decoder matvec_only)
 // PlanIR recording (src/fortai_plan_ir.f90:7-21): while a plan is being
 // recorded, every successful launch appends (operation, kernel, batch).
 thread_local std::vector<plan_step> *g_plan = nullptr;
@@ -371,7 +377,7 @@ hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &
     }
     hipError_t e = rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream),
         "GDN qkv/gate/alpha/beta projections, conv1d + SiLU");
-    if (e == hipSuccess)
+    if (e == hipSuccess && !g_matvec_only)
         e = rec(launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw), stream),
             "GDN L2 norms, decay/beta, delta rule");
     if (e != hipSuccess) return e;
@@ -409,8 +415,9 @@ hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &
     }
     hipError_t e = rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream), "attention q/k/v projections");
     if (e != hipSuccess) return e;
-    e = rec(launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream),
-        "q/k norm, RoPE, KV append, softmax.V, gate");
+    if (!g_matvec_only)
+        e = rec(launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream),
+            "q/k norm, RoPE, KV append, softmax.V, gate");
     if (e != hipSuccess) return e;
     const MatvecSegment oseg = segment(A->o, out, resid);
     MatvecInput oin;
@@ -1416,8 +1423,11 @@ namespace {
 hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream);
 hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     auto *c = d->context;
-    hipError_t e = rec(d->emb16 ? launch_f16_embedding(d->emb16->data, d->emb16->rows, d->hidden, c->token, 0, d->x, stream)
-                                : launch_q8_embedding(d->emb8->m, c->token, 0, d->x, stream), "token embedding");
+    g_matvec_only = d->matvec_only;
+    hipError_t e = hipSuccess;
+    if (!g_matvec_only)
+        e = rec(d->emb16 ? launch_f16_embedding(d->emb16->data, d->emb16->rows, d->hidden, c->token, 0, d->x, stream)
+                         : launch_q8_embedding(d->emb8->m, c->token, 0, d->x, stream), "token embedding");
     for (size_t i = 0; i < d->layers.size() && e == hipSuccess; ++i) {
         const decoder_layer &L = d->layers[i];
         MatvecInput in;
@@ -1431,7 +1441,9 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
         in.norm = L.post_norm;
         e = enqueue_ffn(L.gate, L.up, L.down, in, Prologue::RMSNORM, d->h_q8l, d->x, d->x, stream);
     }
-    if (e != hipSuccess) return e;
+    const bool only = g_matvec_only;
+    g_matvec_only = false;
+    if (e != hipSuccess || only) return e;
     return enqueue_lm_head(d, stream);
 }
 // final RMSNorm + LM head + greedy argmax from d->x; advances token, trace
@@ -1527,6 +1539,7 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     if (e == hipSuccess) e = alloc(&d->trace, max_context + 1);
     if (e == hipSuccess) e = hipMemsetAsync(d->trace, 0, (max_context + 1) * sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (const char *env = std::getenv("FORTAI_HIP_DECODER_MATVEC_ONLY")) d->matvec_only = std::strcmp(env, "1") == 0;
     // the per-op decode step captured as a graph (FORTAI_HIP_DECODER_GRAPH=0
     // enqueues the kernels directly every step instead, e.g. for kernel tracing)
     const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
@@ -1648,6 +1661,16 @@ int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits
     if (!d || !logits) return FORTAI_HIP_INVALID;
     *logits = d->logits;
     return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_decoder_trace(fortai_hip_qwen35_decoder *d, int first, int count, int64_t *host_trace) {
+    if (!d || !host_trace || first < 0 || count <= 0 || first + count > d->max_context) return FORTAI_HIP_INVALID;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipMemcpyAsync(host_trace, d->trace + first, static_cast<size_t>(count) * sizeof(int64_t),
+        hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    return done(c, e, "decoder trace");
 }
 
 // ------------------------------------------------------------ batched decoder

@@ -582,6 +582,13 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_status(fortai_hip_qwen35_decoder *
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
+FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_trace(fortai_hip_qwen35_decoder *decoder, int first, int count,
+    int64_t *host_trace)
+{
+    (void)decoder; (void)first; (void)count; (void)host_trace;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
 FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits)
 {
     (void)decoder;

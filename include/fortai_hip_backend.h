@@ -332,6 +332,9 @@ int fortai_hip_qwen35_decoder_plan(const fortai_hip_qwen35_decoder *decoder, cha
     size_t *needed);
 /* device pointer of the decoder's logits [vocab] */
 int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *decoder, void **device_logits);
+/* the greedy ids the decoder wrote at positions first .. first+count-1
+ * (the token each step chose; synchronises) */
+int fortai_hip_qwen35_decoder_trace(fortai_hip_qwen35_decoder *decoder, int first, int count, int64_t *host_trace);
 
 /* [extension] Batched decoder: `batch` (1..8) independent sequences over the
  * same layers and weights as fortai_hip_qwen35_decoder_create (same
