@@ -256,13 +256,17 @@ class Reference:
         return os.path.exists(self.exe(name))
 
     def dump(self, model: str, token: int, steps: int, context: int, out_dir: str,
-             state: bool = False, threads: Optional[int] = None) -> dict:
+             state: bool = False, threads: Optional[int] = None, keep_logits: bool = False) -> dict:
+        """keep_logits: leave the logits on disk (out_dir/logits.f32) instead
+        of loading them (a long trace's logits are gigabytes)."""
         os.makedirs(out_dir, exist_ok=True)
         env = dict(os.environ)
         if threads:
             env["OMP_NUM_THREADS"] = str(threads)
         subprocess.run([self.exe("ref_dump"), model, str(token), str(steps), str(context), out_dir,
                         "1" if state else "0"], check=True, env=env, stdout=subprocess.DEVNULL)
+        if keep_logits:
+            return {"tokens": np.fromfile(os.path.join(out_dir, "tokens.i64"), dtype=np.int64)}
         logits = np.fromfile(os.path.join(out_dir, "logits.f32"), dtype=np.float32).reshape(steps, -1)
         tokens = np.fromfile(os.path.join(out_dir, "tokens.i64"), dtype=np.int64)
         return {"logits": logits, "tokens": tokens}

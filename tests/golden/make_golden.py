@@ -4,6 +4,9 @@ Run in a container that has /root/reference (after ``make -C oracle ref``):
 
     python tests/golden/make_golden.py          # kernels + tiny models (seconds)
     python tests/golden/make_golden.py --full   # + the 0.8B 128-step trace (minutes)
+    python tests/golden/make_golden.py --trace4096 [DUMP_DIR]
+        # the 0.8B greedy trace over the whole 4096 context (hours on the CPU;
+        # DUMP_DIR: an existing ref_dump output of that run to summarize)
 
 Every expected value here comes from the reference's own CPU code compiled
 from its sources by oracle/Makefile into oracle/_ref (the AVX2 kernels of
@@ -26,6 +29,7 @@ import json
 import os
 import sys
 import tempfile
+from typing import Optional
 
 import numpy as np
 
@@ -149,10 +153,56 @@ def summarize_full(tokens, logits):
     return arrays, meta
 
 
+TRACE_STEPS = 4096
+LAST_TOP = 64  # steps whose top-8 logits are kept
+
+
+def trace4096(ref: Reference, dump_dir: Optional[str] = None, threads: int = 7) -> tuple[dict, dict]:
+    """The 0.8B-shaped model's greedy trace from token 9419 over the whole
+    4096-position context (the headline config), run by the compiled
+    reference; per step the top-1/top-2 logit margin, and the top-8 logits of
+    the last LAST_TOP steps.  The logits (4 GB) are read row by row."""
+    with tempfile.TemporaryDirectory() as tmp:
+        if dump_dir is None:
+            path = os.path.join(tmp, "m.gguf")
+            synth.write_model(path, synth.CONFIGS["qwen35-0.8b"])
+            dump_dir = os.path.join(tmp, "out")
+            ref.dump(path, FULL_TOKEN, TRACE_STEPS, FULL_CONTEXT, dump_dir, threads=threads, keep_logits=True)
+        tokens = np.fromfile(os.path.join(dump_dir, "tokens.i64"), dtype=np.int64)
+        logits = np.memmap(os.path.join(dump_dir, "logits.f32"), dtype=np.float32, mode="r").reshape(TRACE_STEPS, -1)
+        margins = np.zeros(TRACE_STEPS, dtype=np.float32)
+        top_i = np.zeros((LAST_TOP, TOPK), dtype=np.int32)
+        top_v = np.zeros((LAST_TOP, TOPK), dtype=np.float32)
+        for t in range(TRACE_STEPS):
+            row = np.asarray(logits[t])
+            idx = np.argsort(-row, kind="stable")[:TOPK]
+            if int(idx[0]) != int(np.argmax(row)) or int(tokens[t]) != int(np.argmax(row)):
+                raise SystemExit(f"step {t}: trace and logits disagree")
+            margins[t] = row[idx[0]] - row[idx[1]]
+            if t >= TRACE_STEPS - LAST_TOP:
+                top_i[t - (TRACE_STEPS - LAST_TOP)] = idx
+                top_v[t - (TRACE_STEPS - LAST_TOP)] = row[idx]
+    arrays = {"tokens": tokens.astype(np.int64), "margin": margins, "last_top_index": top_i, "last_top_value": top_v}
+    meta = {"model": "qwen35-0.8b", "seed": "fortai_amd.synth default", "token": FULL_TOKEN, "steps": TRACE_STEPS,
+            "context": FULL_CONTEXT, "positions": f"0..{TRACE_STEPS - 1}",
+            "min_top2_margin": float(margins.min()), "argmin_top2_margin": int(np.argmin(margins)),
+            "last_top_steps": f"{TRACE_STEPS - LAST_TOP}..{TRACE_STEPS - 1}",
+            "reference": "oracle/_ref/ref_dump (the reference's Fortran+C CPU path, -O2 -ffp-contract=off)"}
+    return arrays, meta
+
+
 def main() -> None:
     ref = Reference()
     if not ref.available or not ref.has("ref_dump"):
         sys.exit("oracle/_ref is not built (make -C oracle ref)")
+    if "--trace4096" in sys.argv:
+        rest = sys.argv[sys.argv.index("--trace4096") + 1:]
+        arrays, meta = trace4096(ref, rest[0] if rest else None)
+        np.savez_compressed(os.path.join(HERE, "qwen35_0.8b_trace_4096.npz"), **arrays)
+        with open(os.path.join(HERE, "qwen35_0.8b_trace_4096.json"), "w") as f:
+            json.dump(meta, f, indent=1, sort_keys=True)
+        print("wrote the 4096-step trace")
+        return
     rng = np.random.default_rng(0x60D)
     np.savez_compressed(os.path.join(HERE, "kernels.npz"), **kernels(ref, rng))
     for config, stem in (("qwen35-tiny", "tiny_model"), ("qwen35-tiny-q8emb", "tiny_q8emb_model")):

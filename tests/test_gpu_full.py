@@ -1,8 +1,10 @@
 """BASELINE config 4 at full size on the GPU: the 0.8B-shaped synthetic model,
-greedy decode of 128 steps from token 9419.  The trace must equal the
-compiled reference CPU path's (tests/golden/qwen35_0.8b_trace.*, written by
-tests/golden/make_golden.py --full) and the first step's top-8 logits must
-agree within 1e-3 of the top logit."""
+greedy decode from token 9419.  The traces must equal the compiled reference
+CPU path's: 128 steps (tests/golden/qwen35_0.8b_trace.*, written by
+tests/golden/make_golden.py --full; the first step's top-8 logits bit for
+bit) and the whole 4096-position context of the headline config
+(tests/golden/qwen35_0.8b_trace_4096.*, make_golden.py --trace4096; the last
+64 steps' top-8 logits bit for bit)."""
 from __future__ import annotations
 
 import json
@@ -38,12 +40,40 @@ def test_full_model_128_step_trace(full_model_path):
     m = open_decoder(full_model_path, meta["context"])
     try:
         logits = m.forward(meta["token"], 0).copy()
-        scale = float(abs(top_v[0, 0]))
-        assert np.max(np.abs(logits[top_i[0]] - top_v[0])) <= 1e-3 * scale
+        assert np.array_equal(logits[top_i[0]].view(np.uint32), top_v[0].view(np.uint32))
         assert int(np.argmax(logits)) == int(tokens[0])
         m.reset()
         trace = m.generate(meta["token"], meta["steps"])
         first_diff = next((i for i in range(len(tokens)) if trace[i] != tokens[i]), None)
+        assert first_diff is None, f"trace differs from step {first_diff}: {trace[first_diff]} vs {tokens[first_diff]}"
+    finally:
+        m.close()
+
+
+GOLDEN_4096 = os.path.join(GOLDEN, "qwen35_0.8b_trace_4096.npz")
+
+
+@pytest.mark.skipif(not os.path.exists(GOLDEN_4096), reason="the 4096-step golden is not generated")
+def test_full_model_4096_step_trace(full_model_path):
+    """The headline config: the decoder's greedy trace over every position of
+    the 4096-token context equals the compiled reference's, and the logits of
+    the last 64 steps agree at their top 8 entries bit for bit."""
+    from test_gpu_model import open_decoder
+    with np.load(GOLDEN_4096) as z:
+        tokens, top_i, top_v = z["tokens"], z["last_top_index"], z["last_top_value"]
+    with open(GOLDEN_4096.replace(".npz", ".json")) as f:
+        meta = json.load(f)
+    n, last = meta["steps"], len(top_i)
+    m = open_decoder(full_model_path, meta["context"])
+    try:
+        trace = m.generate(meta["token"], n - last)
+        for k in range(last):
+            pos = n - last + k
+            nxt = m.decoder.forward(int(trace[-1]), pos)
+            lg = m.decoder.logits
+            assert np.array_equal(lg[top_i[k]].view(np.uint32), top_v[k].view(np.uint32)), f"logits at step {pos}"
+            trace = np.append(trace, nxt)
+        first_diff = next((i for i in range(n) if trace[i] != tokens[i]), None)
         assert first_diff is None, f"trace differs from step {first_diff}: {trace[first_diff]} vs {tokens[first_diff]}"
     finally:
         m.close()
