@@ -73,6 +73,7 @@ _SIGNATURES = {
     "fortai_hip_argmax_device": [_vp, _vp, _sz, _vp],
     "fortai_hip_q8_quantize_device": [_vp, _vp, _sz, _vp, _vp],
     "fortai_hip_q8_block_dots_device": [_vp, _vp, _vp, _vp],
+    "fortai_hip_q8_batch_matvec_noalloc": [_vp, _vp, _vp, _i, _vp],
     "fortai_hip_q8_batch_matvec_device": [_vp, _vp, _vp, _i, _vp, _fp],
     "fortai_hip_q8_pack_bytes": [_i, _i],
     "fortai_hip_q8_weights_pack": [_vp, _vp, _sz],

@@ -48,6 +48,7 @@ struct fortai_hip_q8_context {
     int32_t *argmax_index = nullptr;
     void *scratch_q8l = nullptr;  // quantized FFN hidden of the ABI FFN paths
     size_t scratch_q8l_bytes = 0;
+    void *noalloc_scratch = nullptr;  // device address of this GPU's `scratch` array (set at create)
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     char error[256] = {};
@@ -448,6 +449,14 @@ bool ffn_shapes_ok(const fortai_hip_q8_weights *g, const fortai_hip_q8_weights *
 
 extern "C" {
 
+// ------------------------------------------------------ allocation-free path
+// `scratch`: the quantized activations (Q8L, batch x q8l_bytes(width)) of
+// fortai_hip_q8_batch_matvec_noalloc.  Every GPU the library runs on holds one
+// copy until the process ends; its device address is looked up once per
+// context (with the context's device current) and kept in the context.
+constexpr size_t kNoAllocScratchBytes = 8 * 18432;  // batch 8 x q8l_bytes(16384)
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 // ------------------------------------------------------------------ context
 // fortai_cuda_backend.cu:805-833
 int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context) {
@@ -467,6 +476,13 @@ int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context) {
     if (e == hipSuccess) e = hipMemsetAsync(c->position, 0, sizeof(int), c->stream);
     if (e == hipSuccess) e = hipMemsetAsync(c->token, 0, sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) {
+        // the allocation-free entry point's array on this device (on failure
+        // that entry point reports it; nothing else depends on it)
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess) c->noalloc_scratch = ptr;
+        else (void)hipGetLastError();
+    }
     if (e != hipSuccess) {
         fortai_hip_q8_context_destroy(c);
         return FORTAI_HIP_RUNTIME_ERROR;
@@ -865,6 +881,26 @@ int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *c, const fortai_hip_q
 }
 
 // ------------------------------------------------------ batched matvec
+int fortai_hip_q8_batch_matvec_noalloc(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x,
+    int batch, void *out) {
+    if (!c || !owned(c, w) || !x || !out || batch < 1 || batch > 8) return FORTAI_HIP_INVALID;
+    const size_t q8l = static_cast<size_t>(batch) * q8l_bytes(w->width);
+    if (q8l > kNoAllocScratchBytes || w->width > 16384) {
+        char msg[160];
+        std::snprintf(msg, sizeof(msg), "batch_matvec_noalloc: batch %d x width %d needs %zu scratch bytes (limit %zu)",
+            batch, w->width, q8l, kNoAllocScratchBytes);
+        return fail(c, FORTAI_HIP_INVALID, msg);
+    }
+    if (!c->noalloc_scratch) return fail(c, FORTAI_HIP_RUNTIME_ERROR, "batch_matvec_noalloc: scratch address unavailable");
+    (void)hipSetDevice(c->device);
+    // the prologue writes every byte the matvec reads (padding blocks as zeros)
+    MatvecInput in = f32_input(static_cast<const float *>(x), w->width);
+    hipError_t e = launch_q8l_prep(in, Prologue::F32, c->noalloc_scratch, batch, c->stream);
+    const MatvecSegment seg = segment(w, static_cast<float *>(out));
+    if (e == hipSuccess) e = launch_q8_batch_matvec(&seg, 1, c->noalloc_scratch, w->width, batch, Epilogue::STORE, c->stream);
+    return done(c, e, "batched matvec (no allocation)");
+}
+
 int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x,
     int batch, void *out, float *kernel_ms) {
     if (!c || !owned(c, w) || !x || !out || batch < 1 || batch > 8) return FORTAI_HIP_INVALID;

@@ -596,6 +596,13 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
+FORTAI_HIP_WEAK int fortai_hip_q8_batch_matvec_noalloc(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_x, int batch, void *device_output)
+{
+    (void)context; (void)weights; (void)device_x; (void)batch; (void)device_output;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
 FORTAI_HIP_WEAK int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *context,
     const fortai_hip_q8_weights *weights, const void *device_x, int batch, void *device_output, float *kernel_ms)
 {

@@ -229,6 +229,16 @@ int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *context,
 int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *context,
     const fortai_hip_q8_weights *weights, const void *device_x, int batch,
     void *device_output, float *kernel_ms);
+/* [extension, no reference counterpart] fortai_hip_q8_batch_matvec_device
+ * without any allocation, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops): the quantized
+ * activations go to a fixed per-GPU array inside the library instead of a
+ * buffer it allocates on demand.  Limit: batch * ceil(width / 128) * 144 <=
+ * 147456 bytes (batch 8 at width 16384); larger requests return INVALID.  The
+ * array is shared by every call on a GPU: calls that overlap on one GPU race.
+ * Outputs are bit-identical to fortai_hip_q8_batch_matvec_device. */
+int fortai_hip_q8_batch_matvec_noalloc(fortai_hip_q8_context *context,
+    const fortai_hip_q8_weights *weights, const void *device_x, int batch, void *device_output);
 
 /* Token blocks (prefill, batches) on the i8 matrix cores.  The reference runs
  * every token through the matvec of fortai_gguf_runtime.f90:424-465; these
