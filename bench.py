@@ -462,16 +462,38 @@ def bench_gdn(steps: int = 128, reps: int = 8):
     us = ctx.timer_stop() * 1e3 / (reps * steps)
     # state r+w + conv state r+w + conv weights + qkv in + o out + alpha/beta (survey section 8(d), config 2)
     algo = 2 * heads * head * head * 4 + 2 * (kernel - 1) * conv * 4 + conv * kernel * 4 + conv * 4 + inner * 4 + 2 * heads * 4
-    for b in (qkv, ab, out):
+    # state-resident: the same 128 steps in one launch (the state stays in registers)
+    alpha_s = ctx.upload_array(rng.standard_normal(steps * heads).astype(np.float32))
+    beta_s = ctx.upload_array(rng.standard_normal(steps * heads).astype(np.float32))
+    outs = ctx.alloc(steps * inner * 4)
+    run = lambda: ctx.call("fortai_hip_qwen35_recurrent_core_steps_device", layer.h, qkv.ptr, alpha_s.ptr, beta_s.ptr,
+                           steps, outs.ptr)
+    run()
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        run()
+    us_res = ctx.timer_stop() * 1e3 / (reps * steps)
+    # per step: q, k, v inputs, alpha/beta, output; state and windows touch memory once per launch
+    algo_res = conv * 4 + inner * 4 + 2 * heads * 4 + (2 * heads * head * head * 4 + 2 * (kernel - 1) * conv * 4 +
+                                                       conv * kernel * 4) / steps
+    for b in (qkv, ab, out, alpha_s, beta_s, outs):
         b.free()
     layer.free()
     for w in ws:
         w.free()
     ctx.close()
     gbps = algo / (us * 1e-6) / 1e9
-    return {"config": f"GDN layer 16x128, conv 4x6144, {steps} autoregressive steps (conv1d+SiLU + delta rule kernels), "
-                      "graph replay", "us_per_step": round(us, 3), "algorithmic_bytes": algo, "gbps": round(gbps, 1),
-            "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+    return {"config": f"GDN layer 16x128, conv 4x6144, {steps} autoregressive steps",
+            "state_streamed": {"path": "per step: conv1d+SiLU kernel + delta-rule kernel (state read and written "
+                                       "every step), graph replay",
+                               "us_per_step": round(us, 3), "algorithmic_bytes": algo, "gbps": round(gbps, 1),
+                               "frac": round(gbps / HBM_PEAK_GBPS, 4)},
+            "state_resident": {"path": "gdn_recurrence_kernel: all steps in one launch, state in registers",
+                               "us_per_step": round(us_res, 3), "algorithmic_bytes_per_step": int(algo_res),
+                               "gbps": round(algo_res / (us_res * 1e-6) / 1e9, 1),
+                               "frac": round(algo_res / (us_res * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                               "note": "latency-bound: a serial chain of 128 dependent steps in 128 workgroups"}}
 
 
 def bench_attention(cases=((1024, None), (4096, None), (32768, None), (32768, 1 << 20)), calls: int = 16,

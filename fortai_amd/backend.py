@@ -83,6 +83,7 @@ _SIGNATURES = {
     "fortai_hip_q8_mmq_device": [_vp, _vp, _vp, _i, _vp, _vp, _fp],
     "fortai_hip_q8_mmq_exact_device": [_vp, _vp, _vp, _i, _vp, _vp, _fp],
     "fortai_hip_q8_mmq_block_dots": [_vp, _vp, _vp, _i, _vp],
+    "fortai_hip_qwen35_recurrent_core_steps_device": [_vp, _vp, _vp, _vp, _i, _vp],
     "fortai_hip_qwen35_recurrent_core_device": [_vp, _vp, _vp, _vp, _vp],
     "fortai_hip_qwen35_recurrent_state_download": [_vp, _vp, _sz, _vp, _sz],
     "fortai_hip_qwen35_recurrent_state_upload": [_vp, _vp, _sz, _vp, _sz],

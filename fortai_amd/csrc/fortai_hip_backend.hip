@@ -79,6 +79,7 @@ struct fortai_hip_qwen35_recurrent {
     float *proj = nullptr;  // projection outputs, one buffer: qkv | z | alpha | beta
     float *qkv_out = nullptr, *z_out = nullptr, *alpha_out = nullptr, *beta_out = nullptr;  // views of proj
     float *o_raw = nullptr;  // GDN output before the gated norm (ssm_out input)
+    float *conv_snap = nullptr;  // recurrent_core_steps: the conv windows before a launch
     // qkv | gate | alpha | beta as one matrix (when each is whole 8-row
     // groups): the four projections then run as one single-segment launch
     Q8Matrix in_m;
@@ -1177,7 +1178,7 @@ int fortai_hip_qwen35_recurrent_destroy(fortai_hip_qwen35_recurrent *L) {
         (void)hipStreamSynchronize(L->context->stream);
     }
     release(L->conv_w); release(L->ssm_a); release(L->ssm_dt); release(L->ssm_norm); release(L->conv_state);
-    release(L->state); release(L->proj); release(L->in_quants); release(L->in_scales);
+    release(L->state); release(L->proj); release(L->in_quants); release(L->in_scales); release(L->conv_snap);
     release(L->o_raw);
     delete L;
     return FORTAI_HIP_OK;
@@ -1243,6 +1244,23 @@ int fortai_hip_qwen35_recurrent_core_device(fortai_hip_qwen35_recurrent *L, cons
         e = launch_gdn_delta(gdn_params(L, L->qkv_out, static_cast<const float *>(alpha),
             static_cast<const float *>(beta), static_cast<float *>(out)), c->stream);
     return done(c, e, "Qwen recurrent core");
+}
+
+int fortai_hip_qwen35_recurrent_core_steps_device(fortai_hip_qwen35_recurrent *L, const void *qkv, const void *alpha,
+    const void *beta, int steps, void *out) {
+    if (!L || !L->context || !qkv || !alpha || !beta || !out || steps < 1) return FORTAI_HIP_INVALID;
+    auto *c = L->context;
+    (void)hipSetDevice(c->device);
+    const size_t window = static_cast<size_t>(L->kernel - 1) * L->conv_size;
+    hipError_t e = L->conv_snap ? hipSuccess : alloc(&L->conv_snap, window);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(L->conv_snap, L->conv_state, window * sizeof(float), hipMemcpyDeviceToDevice, c->stream);
+    GdnParams p = gdn_params(L, static_cast<const float *>(qkv), static_cast<const float *>(alpha),
+        static_cast<const float *>(beta), static_cast<float *>(out));
+    if (e == hipSuccess)
+        e = launch_gdn_recurrence(p, L->conv_w, L->conv_snap, L->conv_state, L->conv_size, L->kernel, steps, c->stream);
+    if (e == hipErrorInvalidValue) return fail(c, FORTAI_HIP_INVALID, "recurrent core steps: head 128 layers only");
+    return done(c, e, "Qwen recurrent core steps");
 }
 
 int fortai_hip_qwen35_recurrent_state_download(fortai_hip_qwen35_recurrent *L, float *gdn, size_t gdn_bytes,

@@ -159,9 +159,44 @@ __device__ __forceinline__ float expf_libm(float x) {
     return static_cast<float>(y * s);
 }
 __device__ __forceinline__ float exp_rounded(float v) { return expf_libm(v); }
-// logf: evaluated in double and rounded once (glibc's logf differs from this
-// in about 7 of 10^4 arguments near 1; only softplus uses it).
-__device__ __forceinline__ float log_rounded(float v) { return static_cast<float>(log(static_cast<double>(v))); }
+
+// logf of the same C library (the Fortran real32 log intrinsic calls it):
+// glibc's algorithm from ARM optimized-routines (sysdeps/ieee754/flt-32/
+// e_logf.c).  x = 2^k z with z in [0x1.66p-1, 0x1.66p0); the top 4 mantissa
+// bits of z pick a table centre c, log(x) = k ln2 + log(c) + log1p(r) with
+// r = z/c - 1 = z * invc - 1 exact in double, log1p(r) by a cubic; all in
+// double, rounded once to float.  Like expf it is not correctly rounded
+// (170327 of the 241653829 floats in [1, 1 + expf(20)], the softplus
+// domain, differ from the rounded exact value), so only this sequence
+// reproduces it; on every positive normal float it equals glibc 2.35's logf
+// bit for bit.  Entry i: {invc, log(c)} with c near the centre of the i-th
+// subinterval, chosen in the library so that 1/invc and log(c) are exact
+// enough for the error bound; the values are the library's.
+static __constant__ const double kLogfTable[16][2] = {
+    {0x1.661ec79f8f3bep+0, -0x1.57bf7808caadep-2}, {0x1.571ed4aaf883dp+0, -0x1.2bef0a7c06ddbp-2},
+    {0x1.49539f0f010bp+0, -0x1.01eae7f513a67p-2},  {0x1.3c995b0b80385p+0, -0x1.b31d8a68224e9p-3},
+    {0x1.30d190c8864a5p+0, -0x1.6574f0ac07758p-3}, {0x1.25e227b0b8eap+0, -0x1.1aa2bc79c81p-3},
+    {0x1.1bb4a4a1a343fp+0, -0x1.a4e76ce8c0e5ep-4}, {0x1.12358f08ae5bap+0, -0x1.1973c5a611cccp-4},
+    {0x1.0953f419900a7p+0, -0x1.252f438e10c1ep-5}, {0x1p+0, 0x0p+0},
+    {0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5},  {0x1.ca4b31f026aap-1, 0x1.c5e53aa362eb4p-4},
+    {0x1.b2036576afce6p-1, 0x1.526e57720db08p-3}, {0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3},
+    {0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2}, {0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}};
+// positive normal finite x only (softplus passes 1 + expf(v) > 1)
+__device__ __forceinline__ float logf_libm(float x) {
+    const uint32_t ix = __float_as_uint(x);
+    if (ix == 0x3f800000u) return 0.0f;
+    const uint32_t tmp = ix - 0x3f330000u;  // offset so that z lands in [0x1.66p-1, 0x1.66p0)
+    const uint32_t i = (tmp >> 19) & 15u;
+    const int k = static_cast<int32_t>(tmp) >> 23;
+    const double z = static_cast<double>(__uint_as_float(ix - (tmp & 0xff800000u)));
+    const double r = __builtin_fma(z, kLogfTable[i][0], -1.0);
+    const double y0 = kLogfTable[i][1] + static_cast<double>(k) * 0x1.62e42fefa39efp-1;
+    const double r2 = r * r;
+    double y = __builtin_fma(0x1.5575b0be00b6ap-2, r, -0x1.ffffef20a4123p-2);
+    y = __builtin_fma(-0x1.00ea348b88334p-2, r2, y);
+    y = __builtin_fma(y, r2, y0 + r);
+    return static_cast<float>(y);
+}
 
 // fortai_qwen35_cpu.f90:1506-1514
 __device__ __forceinline__ float sigmoid_ref(float v) {
@@ -174,7 +209,7 @@ __device__ __forceinline__ float sigmoid_ref(float v) {
 __device__ __forceinline__ float softplus_ref(float v) {
     if (v > 20.0f) return v;
     if (v < -20.0f) return exp_rounded(v);
-    return log_rounded(1.0f + exp_rounded(v));
+    return logf_libm(1.0f + exp_rounded(v));
 }
 
 // ------------------------------------------------------ streaming loads ----

@@ -181,6 +181,13 @@ struct GdnParams {
 };
 // The delta rule, 16 state rows per workgroup: writes the raw output o.
 // batch > 1: sequences along blockIdx.y, every buffer [batch][single size]
+// `steps` autoregressive core steps (conv1d + SiLU + delta rule) in one launch
+// with the state held in registers: qkv [steps][conv_size] projection outputs,
+// alpha / beta [steps][value_heads], out [steps][value_heads * head]; p.qkv,
+// p.alpha, p.beta, p.out point at those arrays; conv_in: a copy of
+// conv_state taken before the launch.  head 128 only.
+hipError_t launch_gdn_recurrence(const GdnParams &p, const float *conv_w, const float *conv_in, float *conv_state,
+    int conv_size, int K, int steps, hipStream_t stream);
 hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream, int batch = 1);
 // Causal conv1d + SiLU of every channel of x, shifting the windows
 // conv_state[K-1][channels] (oldest first).

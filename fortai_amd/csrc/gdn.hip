@@ -143,6 +143,144 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
     if (l == 0) p.out[h * HEAD + row] = qd * (1.0f / sqrtf(static_cast<float>(HEAD)));
 }
 
+// ------------------------------------------------------- state-resident
+// `steps` autoregressive steps of the recurrent core in one launch: each
+// workgroup keeps its 16 state rows in registers across every step, and the
+// conv1d window of each channel it reads in registers too.  Per step it
+// runs the conv1d + SiLU of the channels it needs (the key head's q and k,
+// its own v rows; the q / k channels are computed by every workgroup of the
+// key head, redundantly and identically), then the same delta-rule code as
+// gdn_delta_kernel.  Bit-identical to `steps` calls of conv_silu_kernel +
+// gdn_delta_kernel.  At the end the state rows go back, and each conv
+// window is written by the one workgroup that owns the channel: v channels
+// by their row's workgroup, q / k channels by row block 0 of the first value
+// head of the key head.  The windows are read from conv_in, a copy taken
+// before the launch, so no workgroup can read a window another has already
+// advanced.
+// qkv [steps][conv_size] (projection outputs), alpha / beta [steps][value_heads],
+// out [steps][value_heads * head].
+template <int HEAD>
+__global__ __launch_bounds__(kDeltaThreads) void gdn_recurrence_kernel(const GdnParams p, const float *__restrict__ conv_w,
+    const float *__restrict__ conv_in, float *__restrict__ conv_state, int conv_size, int K, int steps) {
+    static_assert(HEAD == kDeltaThreads, "one q and one k channel per thread");
+    constexpr int kCols = HEAD / 8;
+    __shared__ __align__(16) float qs[HEAD];
+    __shared__ __align__(16) float ks[HEAD];
+    __shared__ float vs[kDeltaRows];
+    __shared__ double red[2];
+    __shared__ float hs[2];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int blocks_per_head = HEAD / kDeltaRows;
+    const int h = static_cast<int>(blockIdx.x) / blocks_per_head;
+    const int rb = static_cast<int>(blockIdx.x) % blocks_per_head, r0 = rb * kDeltaRows;
+    const int group = p.value_heads / p.key_heads, kh = h / group;
+    const int r8 = tid >> 3, l = tid & 7, row = r0 + r8;
+    const int inner = p.value_heads * HEAD;
+    // this thread's channels: q and k of the key head, v of row r0 + tid (tid < 16)
+    const int cq = kh * HEAD + tid, ck = p.state_size * p.key_heads + kh * HEAD + tid;
+    const int cv = 2 * p.state_size * p.key_heads + h * HEAD + r0 + min(tid, kDeltaRows - 1);
+    const int chans[3] = {cq, ck, cv};
+    float win[3][kConvMax - 1], taps[3][kConvMax];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+#pragma unroll
+        for (int t = 0; t < kConvMax; ++t) {
+            if (t < K - 1) win[c][t] = conv_in[static_cast<size_t>(t) * conv_size + chans[c]];
+            if (t < K) taps[c][t] = conv_w[static_cast<size_t>(chans[c]) * K + t];
+        }
+    }
+    float s[kCols];
+    float4 *srow = reinterpret_cast<float4 *>(p.state + ((static_cast<size_t>(h) * HEAD + row) * 8 + l) * kCols);
+#pragma unroll
+    for (int i = 0; i < kCols / 4; ++i) {
+        const float4 f = srow[i];
+        s[4 * i] = f.x; s[4 * i + 1] = f.y; s[4 * i + 2] = f.z; s[4 * i + 3] = f.w;
+    }
+    const float inv_sqrt = 1.0f / sqrtf(static_cast<float>(HEAD));
+    // the next step's inputs are loaded while the current one runs
+    float xn[3], an = 0.0f, bn = 0.0f;
+    auto fetch = [&](int t) {
+        const float *x = p.qkv + static_cast<size_t>(t) * conv_size;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) xn[c] = x[chans[c]];
+        if (tid == 0) {
+            an = p.alpha[static_cast<size_t>(t) * p.value_heads + h];
+            bn = p.beta[static_cast<size_t>(t) * p.value_heads + h];
+        }
+    };
+    fetch(0);
+    for (int t = 0; t < steps; ++t) {
+        float x[3] = {xn[0], xn[1], xn[2]};
+        const float a = an, b = bn;
+        if (t + 1 < steps) fetch(t + 1);
+        // conv1d + SiLU of the three channels, then the windows move by one
+        float y[3];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            y[c] = conv_silu(win[c], taps[c], K, x[c]);
+#pragma unroll
+            for (int u = 0; u + 1 < kConvMax - 1; ++u)
+                if (u + 1 < K - 1) win[c][u] = win[c][u + 1];
+#pragma unroll
+            for (int u = 0; u < kConvMax - 1; ++u)
+                if (u == K - 2) win[c][u] = x[c];
+        }
+        qs[tid] = y[0];
+        ks[tid] = y[1];
+        if (tid < kDeltaRows) vs[tid] = y[2];
+        if (tid == 0) {
+            // fortai_qwen35_cpu.f90:890-894
+            hs[0] = sigmoid_ref(b);
+            hs[1] = exp_rounded(p.ssm_a[h] * softplus_ref(a + p.ssm_dt[h]));
+        }
+        __syncthreads();
+        // L2 norms of q (wave 0) and k (wave 1), fortai_qwen35_cpu.f90:1455-1471
+        {
+            const float *v = (tid < 64) ? qs : ks;
+            double ss = 0.0;
+            for (int i = tid & 63; i < HEAD; i += 64) ss += static_cast<double>(v[i]) * static_cast<double>(v[i]);
+            ss = wave_sum(ss);
+            if ((tid & 63) == 0) red[tid >> 6] = ss;
+        }
+        __syncthreads();
+        const float qinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[0])), p.eps);
+        const float kinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[1])), p.eps);
+        const float beta = hs[0], decay = hs[1];
+        const float vrow = vs[r8];
+        // delta rule (fortai_q8_dot.c:363-396)
+        float kd = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCols; ++i) {
+            const float d = s[i] * decay;
+            s[i] = d;
+            kd = __builtin_fmaf(d, ks[8 * i + l] * kinv, kd);
+        }
+        kd = row_hsum8(kd);
+        const float delta = (vrow - kd) * beta;
+        float qd = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCols; ++i) {
+            const float u = __builtin_fmaf(delta, ks[8 * i + l] * kinv, s[i]);
+            s[i] = u;
+            qd = __builtin_fmaf(u, qs[8 * i + l] * qinv, qd);
+        }
+        qd = row_hsum8(qd);
+        if (l == 0) p.out[static_cast<size_t>(t) * inner + h * HEAD + row] = qd * inv_sqrt;
+        __syncthreads();  // qs / ks / vs / hs / red are rewritten by the next step
+    }
+#pragma unroll
+    for (int i = 0; i < kCols / 4; ++i) srow[i] = make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
+    const bool qk_owner = rb == 0 && h % group == 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const bool owner = c < 2 ? qk_owner : tid < kDeltaRows;
+        if (!owner) continue;
+#pragma unroll
+        for (int u = 0; u < kConvMax - 1; ++u)
+            if (u < K - 1) conv_state[static_cast<size_t>(u) * conv_size + chans[c]] = win[c][u];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_conv_silu(const float *x, const float *conv_w, float *conv_state, float *out, int channels, int K,
@@ -167,4 +305,19 @@ hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream, int batch) {
     return hipGetLastError();
 }
 
+}  // namespace fortai_hip
+
+namespace fortai_hip {
+hipError_t launch_gdn_recurrence(const GdnParams &p, const float *conv_w, const float *conv_in, float *conv_state,
+    int conv_size, int K, int steps, hipStream_t stream) {
+    if (steps < 1 || p.key_heads <= 0 || p.value_heads % p.key_heads || p.state_size != p.head || !p.out ||
+        K < 2 || K > kConvMax || p.head != kDeltaThreads ||
+        conv_size != 2 * p.state_size * p.key_heads + p.value_heads * p.head)
+        return hipErrorInvalidValue;
+    const dim3 grid(p.value_heads * (p.head / kDeltaRows));
+    hipLaunchKernelGGL(gdn_recurrence_kernel<kDeltaThreads>, grid, dim3(kDeltaThreads), 0, stream, p, conv_w, conv_in,
+        conv_state, conv_size, K, steps);
+    note_launch("gdn_recurrence_kernel<%d> grid %d, %d steps", p.head, grid.x, steps);
+    return hipGetLastError();
+}
 }  // namespace fortai_hip

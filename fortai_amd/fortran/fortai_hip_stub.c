@@ -456,6 +456,13 @@ FORTAI_HIP_WEAK int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *conte
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
+FORTAI_HIP_WEAK int fortai_hip_qwen35_recurrent_core_steps_device(fortai_hip_qwen35_recurrent *layer,
+    const void *device_qkv, const void *device_alpha, const void *device_beta, int steps, void *device_output)
+{
+    (void)layer; (void)device_qkv; (void)device_alpha; (void)device_beta; (void)steps; (void)device_output;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
 FORTAI_HIP_WEAK int fortai_hip_qwen35_recurrent_core_device(fortai_hip_qwen35_recurrent *layer, const void *device_qkv, const void *device_alpha, const void *device_beta, void *device_output)
 {
     (void)layer;

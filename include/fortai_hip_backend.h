@@ -279,6 +279,13 @@ int fortai_hip_q8_mmq_block_dots(fortai_hip_q8_context *context,
 int fortai_hip_qwen35_recurrent_core_device(fortai_hip_qwen35_recurrent *layer,
     const void *device_qkv, const void *device_alpha, const void *device_beta,
     void *device_output);
+/* [extension] `steps` autoregressive core steps in one launch with the state
+ * held in registers (state-resident): device qkv
+ * [steps][conv_size], alpha and beta [steps][value_heads], out
+ * [steps][inner_size]; state, conv windows and outputs bit-identical to
+ * `steps` calls of fortai_hip_qwen35_recurrent_core_device.  Head 128. */
+int fortai_hip_qwen35_recurrent_core_steps_device(fortai_hip_qwen35_recurrent *layer,
+    const void *device_qkv, const void *device_alpha, const void *device_beta, int steps, void *device_output);
 int fortai_hip_qwen35_recurrent_state_download(fortai_hip_qwen35_recurrent *layer,
     float *host_gdn_state, size_t gdn_bytes, float *host_conv_state, size_t conv_bytes);
 int fortai_hip_qwen35_recurrent_state_upload(fortai_hip_qwen35_recurrent *layer,

@@ -175,33 +175,49 @@ def gdn_layer_for_core(ctx, rng, H=1024, heads=16, head=128, kernel=4):
 
 
 def test_gdn_core_128_steps(ctx, oracle):
-    """16 heads x 128, state ~ N(0, 0.02), 128 autoregressive steps."""
+    """16 heads x 128, state ~ N(0, 0.02), 128 autoregressive
+    steps, through both the per-step entry point (conv1d + SiLU kernel, then the
+    delta-rule kernel) and the state-resident one (all 128 steps in one
+    launch): every output, the GDN state and the conv windows bit-identical to
+    the oracle's."""
     rng = np.random.default_rng(0x35A08B)
-    heads, head, kernel = 16, 128, 4
+    heads, head, kernel, steps = 16, 128, 4, 128
     layer, ws, conv_w, ssm_a, ssm_dt, conv = gdn_layer_for_core(ctx, rng)
     state = (rng.standard_normal(heads * head * head) * 0.02).astype(np.float32)
-    cstate = np.zeros((kernel - 1) * conv, np.float32)
-    layer.set_state(state, cstate)
+    cstate = (rng.standard_normal((kernel - 1) * conv) * 0.5).astype(np.float32)
+    qkv = rng.standard_normal((steps, conv)).astype(np.float32)
+    alpha = rng.standard_normal((steps, heads)).astype(np.float32)
+    beta = rng.standard_normal((steps, heads)).astype(np.float32)
     ref_state, ref_conv = state.copy(), cstate.copy()
-    dq, da, db, do = ctx.alloc(conv * 4), ctx.alloc(heads * 4), ctx.alloc(heads * 4), ctx.alloc(heads * head * 4)
     work = np.zeros(conv, np.float32)
-    want = np.zeros(heads * head, np.float32)
-    worst = 0.0
-    for step in range(128):
-        qkv = rng.standard_normal(conv).astype(np.float32)
-        alpha = rng.standard_normal(heads).astype(np.float32)
-        beta = rng.standard_normal(heads).astype(np.float32)
-        dq.upload(qkv); da.upload(alpha); db.upload(beta)
+    want = np.zeros((steps, heads * head), np.float32)
+    for t in range(steps):
+        oracle.gdn_core_step(qkv[t], alpha[t], beta[t], ssm_a, ssm_dt, conv_w, ref_conv, ref_state, conv, kernel, head,
+                             heads, heads, head, np.float32(1e-6), work, want[t])
+    bits = lambda a: np.asarray(a, np.float32).view(np.uint32)
+    # per step
+    layer.set_state(state, cstate)
+    dq, da, db, do = ctx.alloc(conv * 4), ctx.alloc(heads * 4), ctx.alloc(heads * 4), ctx.alloc(heads * head * 4)
+    for t in range(steps):
+        dq.upload(qkv[t]); da.upload(alpha[t]); db.upload(beta[t])
         ctx.call("fortai_hip_qwen35_recurrent_core_device", layer.h, dq.ptr, da.ptr, db.ptr, do.ptr)
-        oracle.gdn_core_step(qkv, alpha, beta, ssm_a, ssm_dt, conv_w, ref_conv, ref_state, conv, kernel, head,
-                             heads, heads, head, np.float32(1e-6), work, want)
-        got = do.download(np.float32)
-        worst = max(worst, rel_err(got, want))
+        assert np.array_equal(bits(do.download(np.float32)), bits(want[t])), f"per-step output {t}"
     gdn, cst = layer.state()
-    assert np.array_equal(cst, ref_conv)
-    # reference tolerance of the GDN AR bench: 2e-5 + 3e-4 |x| (fortai_cuda_gdn_ar_bench.cu:24-25)
-    assert np.all(np.abs(gdn - ref_state) <= 2e-5 + 3e-4 * np.abs(ref_state))
-    assert worst <= REL
+    assert np.array_equal(bits(cst), bits(ref_conv))
+    assert np.array_equal(bits(gdn), bits(ref_state))
+    # state-resident: the 128 steps in one launch
+    layer.set_state(state, cstate)
+    dQ, dA, dB = ctx.upload_array(qkv), ctx.upload_array(alpha), ctx.upload_array(beta)
+    dO = ctx.alloc(steps * heads * head * 4)
+    ctx.call("fortai_hip_qwen35_recurrent_core_steps_device", layer.h, dQ.ptr, dA.ptr, dB.ptr, steps, dO.ptr)
+    got = dO.download(np.float32).reshape(steps, heads * head)
+    first = next((t for t in range(steps) if not np.array_equal(bits(got[t]), bits(want[t]))), None)
+    assert first is None, f"state-resident output differs from step {first}"
+    gdn, cst = layer.state()
+    assert np.array_equal(bits(cst), bits(ref_conv))
+    assert np.array_equal(bits(gdn), bits(ref_state))
+    for b in (dq, da, db, do, dQ, dA, dB, dO):
+        b.free()
     layer.free()
     for w in ws:
         w.free()
