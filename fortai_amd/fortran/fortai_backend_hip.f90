@@ -48,6 +48,8 @@ module fortai_backend_hip
     contains
         procedure :: upload => q8_weights_upload
         procedure :: destroy => q8_weights_destroy
+        procedure :: pack => q8_weights_pack
+        procedure :: upload_packed => q8_weights_upload_packed
     end type hip_q8_weights_t
 
     type, public :: hip_f16_weights_t
@@ -104,6 +106,7 @@ module fortai_backend_hip
         procedure :: generate => batch_generate
     end type hip_qwen35_batch_t
 
+    public :: hip_q8_pack_bytes
     public :: hip_q8_matvec_resident, hip_q8_matvec_device_f32, hip_qwen35_embedding_device
     public :: hip_qwen35_copy_device, hip_qwen35_add_device, hip_qwen35_rms_norm_device
     public :: hip_q8_matvec_host, hip_q8_matvec_host_pair, hip_q8_matvec_host_triplet
@@ -158,6 +161,23 @@ module fortai_backend_hip
         integer(c_int) function fh_weights_destroy(weights) bind(C, name='fortai_hip_q8_weights_destroy')
             import :: c_int, c_ptr
             type(c_ptr), value :: weights
+        end function
+        integer(c_size_t) function fh_pack_bytes(rows, width) bind(C, name='fortai_hip_q8_pack_bytes')
+            import :: c_int, c_size_t
+            integer(c_int), value :: rows, width
+        end function
+        integer(c_int) function fh_weights_pack(weights, host, bytes) bind(C, name='fortai_hip_q8_weights_pack')
+            import :: c_int, c_ptr, c_size_t
+            type(c_ptr), value :: weights, host
+            integer(c_size_t), value :: bytes
+        end function
+        integer(c_int) function fh_weights_upload_packed(context, host, bytes, rows, width, weights) &
+                bind(C, name='fortai_hip_q8_weights_upload_packed')
+            import :: c_int, c_ptr, c_size_t
+            type(c_ptr), value :: context, host
+            integer(c_size_t), value :: bytes
+            integer(c_int), value :: rows, width
+            type(c_ptr), intent(out) :: weights
         end function
         integer(c_int) function fh_f16_upload(context, host, bytes, rows, width, weights) &
                 bind(C, name='fortai_hip_f16_weights_upload')
@@ -691,6 +711,58 @@ contains
         self%handle = c_null_ptr
         if (code /= FORTAI_HIP_OK) call stat%set(FORTAI_UNSUPPORTED, 'HIP Q8 weight destruction failed')
     end subroutine q8_weights_destroy
+
+    ! Bytes of the resident planes of a rows x width Q8_0 matrix (0 if the
+    ! shape is invalid): the size of a pack record.
+    function hip_q8_pack_bytes(rows, width) result(bytes)
+        integer, intent(in) :: rows, width
+        integer(c_size_t) :: bytes
+
+        bytes = 0_c_size_t
+        if (rows <= 0 .or. width <= 0) return
+        bytes = fh_pack_bytes(int(rows, c_int), int(width, c_int))
+    end function hip_q8_pack_bytes
+
+    ! Copy the resident planes to host memory (synchronous); host_planes must
+    ! hold hip_q8_pack_bytes(rows, width) bytes.
+    subroutine q8_weights_pack(self, host_planes, stat)
+        class(hip_q8_weights_t), intent(in) :: self
+        integer(c_int8_t), contiguous, target, intent(inout) :: host_planes(:)
+        type(status_t), intent(out) :: stat
+        integer(c_int) :: code
+
+        call stat%clear()
+        if (.not. live(self%handle) .or. size(host_planes) <= 0) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Q8 weight pack')
+            return
+        end if
+        code = fh_weights_pack(self%handle, c_loc(host_planes), int(size(host_planes), c_size_t))
+        if (code /= FORTAI_HIP_OK) call stat%set(FORTAI_UNSUPPORTED, &
+            'HIP Q8 weight pack failed (buffer smaller than the planes, or a device error)')
+    end subroutine q8_weights_pack
+
+    ! Create the resident matrix from planes written by pack (no repack).
+    subroutine q8_weights_upload_packed(self, context, host_planes, rows, width, stat)
+        class(hip_q8_weights_t), intent(inout) :: self
+        class(hip_q8_context_t), intent(in) :: context
+        integer(c_int8_t), contiguous, target, intent(in) :: host_planes(:)
+        integer, intent(in) :: rows, width
+        type(status_t), intent(out) :: stat
+        integer(c_int) :: code
+
+        call stat%clear()
+        if (.not. live(context%handle) .or. rows <= 0 .or. width <= 0 .or. &
+                int(size(host_planes), c_size_t) < hip_q8_pack_bytes(rows, width) .or. &
+                hip_q8_pack_bytes(rows, width) == 0_c_size_t) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Q8 packed weight upload')
+            return
+        end if
+        if (live(self%handle)) call self%destroy(stat)
+        code = fh_weights_upload_packed(context%handle, c_loc(host_planes), int(size(host_planes), c_size_t), &
+            int(rows, c_int), int(width, c_int), self%handle)
+        if (code /= FORTAI_HIP_OK) self%handle = c_null_ptr
+        call settle(code, context%handle, 'Q8 packed weight upload', stat)
+    end subroutine q8_weights_upload_packed
 
     subroutine f16_weights_upload(self, context, host_weights, weight_bytes, rows, width, stat)
         class(hip_f16_weights_t), intent(inout) :: self

@@ -9,6 +9,12 @@
   (fortai_qwen35_cpu.f90:287-384, 600-800) on this library; its greedy trace
   must equal the compiled reference CPU path's and its logits agree within
   1e-3 of the logit range.
+* oracle/_ref/hip_pack_smoke: the Fortran pack cache
+  (fortai_amd/fortran/fortai_hip_pack_cache.f90) keyed by the reference's
+  pack_key_t / cache_path (src/fortai_cache.f90:6-31).  Matrices uploaded
+  from a pack give the same matvec bits as the repacking upload; a pack
+  written from Fortran reads in Python (fortai_amd/pack_cache.py) and one
+  written from Python reads in Fortran.
 """
 from __future__ import annotations
 
@@ -22,6 +28,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SMOKE = os.path.join(ROOT, "fortai_amd", "lib", "hip_abi_smoke")
 REF_HIP = os.path.join(ROOT, "oracle", "_ref", "ref_dump_hip")
+PACK_SMOKE = os.path.join(ROOT, "oracle", "_ref", "hip_pack_smoke")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 pytestmark = pytest.mark.gpu
@@ -66,3 +73,30 @@ def test_reference_model_on_hip_backend(tmp_path, stem, graph):
     for got, want in ((logits[0], arrays["logits_first"]), (logits[-1], arrays["logits_last"])):
         scale = float(np.max(np.abs(want)))
         assert float(np.max(np.abs(got - want))) <= 1e-3 * scale
+
+
+def test_fortran_pack_cache(tmp_path):
+    if not os.path.exists(PACK_SMOKE):
+        pytest.skip("oracle/_ref/hip_pack_smoke not built (needs /root/reference at build time)")
+    from fortai_amd import pack_cache, synth
+    gguf = str(tmp_path / "m.gguf")
+    synth.write_model(gguf, synth.CONFIGS["qwen35-tiny"])
+
+    def run(root, mode):
+        r = subprocess.run([PACK_SMOKE, gguf, str(root), mode], capture_output=True, text=True, timeout=120)
+        print(r.stdout, r.stderr, flush=True)
+        assert r.returncode == 0
+        assert "fortran pack cache ok" in r.stdout
+        return r.stdout.split("pack ", 1)[1].split("\n", 1)[0].strip()
+
+    written = run(tmp_path / "fortran", "write")
+    assert written == str(tmp_path / "fortran") + "/packsmoke/hip-gfx950-q8-lanes-abi1.pack"
+    records = pack_cache.read(written, pack_cache.gguf_digest(gguf))
+    assert records is not None, "the Fortran pack does not read in Python (format or digest differ)"
+    assert {k: v[:2] for k, v in records.items()} == {"blk.0.a": (13, 96), "blk.0.bb": (200, 1024),
+                                                      "output": (64, 256)}
+    # the same records written from Python, read back by the Fortran program
+    again = pack_cache.cache_path(str(tmp_path / "python"), pack_cache.PackKey("packsmoke", "hip-gfx950", "q8-lanes", 1))
+    pack_cache.write(again, pack_cache.gguf_digest(gguf), records)
+    assert open(again, "rb").read() == open(written, "rb").read()
+    assert run(tmp_path / "python", "read") == again
