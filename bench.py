@@ -226,7 +226,8 @@ def traffic_probe(reps: int = 5, decode_model: str = None, decode_only: bool = F
     * the 3584 x 1024 Q8_0 matvec (quantize fused) over 275
       distinct weight copies (1.07 GB, beyond the 256 MB Infinity Cache);
     * BASELINE config 3 at L = 4096: append + scores + exact output kernels;
-    * BASELINE config 2: the GDN conv1d + delta-rule step;
+    * the GDN conv1d + delta-rule step, and the
+      state-resident recurrence (128 steps per launch);
     * with decode_model: 8 decode steps of that GGUF with direct launches
       (every matvec, GDN, attention, LM head kernel of the step)."""
     import ctypes as C
@@ -313,13 +314,23 @@ def traffic_probe(reps: int = 5, decode_model: str = None, decode_only: bool = F
         ctx.call("fortai_hip_qwen35_recurrent_core_device", layer.h, qkv.ptr, ab.ptr,
                  C.c_void_p(ab.ptr.value + heads * 4), out.ptr)
     ctx.synchronize()
-    for buf in (qkv, ab, out):
+    # the state-resident form: 128 steps in one launch
+    steps = 128
+    qkv_s = ctx.upload_array(rng.standard_normal(steps * conv).astype(np.float32))
+    alpha_s = ctx.upload_array(rng.standard_normal(steps * heads).astype(np.float32))
+    beta_s = ctx.upload_array(rng.standard_normal(steps * heads).astype(np.float32))
+    outs = ctx.alloc(steps * inner * 4)
+    for _ in range(reps):
+        ctx.call("fortai_hip_qwen35_recurrent_core_steps_device", layer.h, qkv_s.ptr, alpha_s.ptr, beta_s.ptr, steps,
+                 outs.ptr)
+    ctx.synchronize()
+    for buf in (qkv, ab, out, qkv_s, alpha_s, beta_s, outs):
         buf.free()
     layer.free()
     for w_ in ws:
         w_.free()
     ctx.close()
-    log("traffic probe: GDN step done")
+    log("traffic probe: GDN step and 128-step recurrence done")
     if decode_model:
         decode_probe(decode_model)
 

@@ -62,6 +62,11 @@ __device__ __forceinline__ GdnParams gdn_seq(GdnParams p, int s) {
     return p;
 }
 
+// Workgroup b runs on XCD b % 8.  The logical (head, row block) index of b
+// is chosen so that a head's row blocks are consecutive on one XCD, whose L2
+// then serves the head's q and k to all of them.
+__device__ __forceinline__ int xcd_grouped(int b, int n) { return n % 8 == 0 ? (b % 8) * (n / 8) + b / 8 : b; }
+
 template <int HEAD>
 __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParams p_batch) {
     const GdnParams p = gdn_seq(p_batch, static_cast<int>(blockIdx.y));
@@ -72,8 +77,9 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
     __shared__ float hs[2];
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks_per_head = HEAD / kDeltaRows;
-    const int h = static_cast<int>(blockIdx.x) / blocks_per_head;
-    const int r0 = (static_cast<int>(blockIdx.x) % blocks_per_head) * kDeltaRows;
+    const int wg = xcd_grouped(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+    const int h = wg / blocks_per_head;
+    const int r0 = (wg % blocks_per_head) * kDeltaRows;
     const int kh = h / (p.value_heads / p.key_heads);
     const int r8 = tid >> 3, l = tid & 7, row = r0 + r8;
     // every load first: the state row, q and k of the key head, v, the scalars
@@ -171,8 +177,9 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_recurrence_kernel(const Gdn
     __shared__ float hs[2];
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks_per_head = HEAD / kDeltaRows;
-    const int h = static_cast<int>(blockIdx.x) / blocks_per_head;
-    const int rb = static_cast<int>(blockIdx.x) % blocks_per_head, r0 = rb * kDeltaRows;
+    const int wg = xcd_grouped(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+    const int h = wg / blocks_per_head;
+    const int rb = wg % blocks_per_head, r0 = rb * kDeltaRows;
     const int group = p.value_heads / p.key_heads, kh = h / group;
     const int r8 = tid >> 3, l = tid & 7, row = r0 + r8;
     const int inner = p.value_heads * HEAD;
