@@ -73,19 +73,21 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     const int positions = pos + 1, nblk_max = (p.max_context + ea::kPosBlock - 1) / ea::kPosBlock;
     // block-major: the blocks that hold positions are dispatched first, the
     // ones past the current position (which only read it and exit) last
-    const int kvh = static_cast<int>(blockIdx.x) % p.kv_heads, b = static_cast<int>(blockIdx.x) / p.kv_heads;
+    const int b = div(static_cast<int>(blockIdx.x), p.div_kv_heads);
+    const int kvh = static_cast<int>(blockIdx.x) - b * p.kv_heads;
     const int p0 = b * ea::kPosBlock;
     if (p0 >= positions) return;
     const int n = min(ea::kPosBlock, positions - p0);
     const bool owns_new = pos >= p0 && pos < p0 + n;
-    const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
-    const int half = p.rope_dim / 2, segs = HD / 8;
+    const int group = static_cast<int>(p.div_group.d), HD = p.head, VD = p.value, NKV = p.kv_heads;
+    const int half = p.rope_dim / 2;
 
     v4u kr[kLoads];  // key rows first: the only HBM stream of this kernel
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int li = tid + i * ea::kThreads;
-        const int j = min(li / segs, n - 1), sg = li % segs;  // rows past n re-read row n-1 (in bounds)
+        const int jj = div(li, p.div_segs), sg = li - jj * static_cast<int>(p.div_segs.d);
+        const int j = min(jj, n - 1);  // rows past n re-read row n-1 (in bounds)
         kr[i] = reinterpret_cast<const v4u *>(p.kcache + (static_cast<size_t>(p0 + j) * NKV + kvh) * HD)[sg];
     }
     // every other input in the same round trip (indices clamped in bounds),
@@ -94,7 +96,8 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
 #pragma unroll
     for (int i = 0; i < kQLoads; ++i) {
         const int e = min(tid + i * ea::kThreads, group * HD - 1);
-        qv[i] = p.q[static_cast<size_t>(kvh * group + e / HD) * 2 * HD + e % HD];
+        const int eh = div(e, p.div_head);
+        qv[i] = p.q[static_cast<size_t>(kvh * group + eh) * 2 * HD + (e - eh * HD)];
     }
     const int th = min(tid, HD - 1), tv = min(tid, VD - 1);
     const float qwv = p.q_norm[th], kwv = p.k_norm[th];
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int li = tid + i * ea::kThreads;
-        const int j = li / segs, sg = li % segs;
+        const int j = div(li, p.div_segs), sg = li - j * static_cast<int>(p.div_segs.d);
         if (j < n) *reinterpret_cast<v4u *>(&ktile[j][sg * 8]) = kr[i];
     }
     __syncthreads();
@@ -166,7 +169,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     __shared__ float fred[ea::kWaves];
     static_assert(ea::kZCand == ea::kThreads && ea::kSeg == ea::kThreads, "one candidate and one position per thread");
     const int pos = *p.position;
-    const int h = static_cast<int>(blockIdx.x) % p.heads, k = static_cast<int>(blockIdx.x) / p.heads;
+    const int k = div(static_cast<int>(blockIdx.x), p.div_heads), h = static_cast<int>(blockIdx.x) - k * p.heads;
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
     // up to kHeld * 256 positions the scores are loaded in the position's
@@ -297,20 +300,22 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     const int tid = static_cast<int>(threadIdx.x);
     FORTAI_ATT_MARK(0);
     const int pos = *p.position;
-    const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
-    const int slices = VD / ea::kDims, nwg = p.heads * slices;
+    const int group = static_cast<int>(p.div_group.d), HD = p.head, VD = p.value, NKV = p.kv_heads;
+    const int slices = static_cast<int>(p.div_slices.d), nwg = p.heads * slices;
     const int b = static_cast<int>(blockIdx.x);
     int h, d0;
     if (nwg % 8 == 0 && VD % 64 == 0) {
         const int i = (b % 8) * (nwg / 8) + b / 8;  // logical index, consecutive on one XCD
-        const int sl = i % 8, g = (i / 8) % group, t = i / 8 / group, lg = t % (VD / 64), kvh = t / (VD / 64);
+        const int i8 = i / 8, sl = i % 8;
+        const int t = div(i8, p.div_group), g = i8 - t * group;
+        const int kvh = div(t, p.div_vd64), lg = t - kvh * static_cast<int>(p.div_vd64.d);
         h = kvh * group + g;
         d0 = (lg * 8 + sl) * ea::kDims;
     } else {
-        h = b / slices;
-        d0 = (b % slices) * ea::kDims;
+        h = div(b, p.div_slices);
+        d0 = (b - h * slices) * ea::kDims;
     }
-    const int kvh = h / group;
+    const int kvh = div(h, p.div_group);
     const int cap = p.max_context < p.exact_max ? p.max_context : p.exact_max;  // positions this kernel serves
     const uint16_t *vbase = p.vcache + static_cast<size_t>(kvh) * VD + d0;
     const size_t vstride = static_cast<size_t>(NKV) * VD;
@@ -323,9 +328,12 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     ea::value_prefetch(vbase, vstride, p.max_context, v);
     ea::e_prefetch(ev, p.max_context, e4);
     static_assert(ea::kZCand == ea::kThreads, "one walk word per thread and segment");
+    // unconditional loads (a branch around each would make the compiler wait
+    // for it): rows past the cached ones re-read the last (row 0 always exists)
+    const int last_row = max(rows, 1) - 1;
 #pragma unroll
     for (int r = 0; r < kTabRegs; ++r)
-        if (r < rows) tr[r] = __float_as_int(tab[static_cast<size_t>(r) * ea::kZStride + ea::kZNext + tid]);
+        tr[r] = __float_as_int(tab[static_cast<size_t>(min(r, last_row)) * ea::kZStride + ea::kZNext + tid]);
     const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
     const int flag = p.cache_flags[kvh];
     FORTAI_ATT_MARK(3);
@@ -722,9 +730,17 @@ size_t attention_scores_floats(int heads, int max_context) { return workspace_fl
 
 int attention_split_chunks(int max_context) { return (max_context + kChunk - 1) / kChunk; }
 
-hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int batch) {
+hipError_t launch_attention(const AttentionParams &params, hipStream_t stream, int batch) {
     if (batch < 1) return hipErrorInvalidValue;
-    const int group = p.kv_heads > 0 ? p.heads / p.kv_heads : 0;
+    const int group = params.kv_heads > 0 ? params.heads / params.kv_heads : 0;
+    AttentionParams p = params;
+    p.div_heads = fast_div(static_cast<uint32_t>(p.heads));
+    p.div_kv_heads = fast_div(static_cast<uint32_t>(p.kv_heads));
+    p.div_group = fast_div(static_cast<uint32_t>(group));
+    p.div_head = fast_div(static_cast<uint32_t>(p.head));
+    p.div_segs = fast_div(static_cast<uint32_t>(p.head / 8));
+    p.div_slices = fast_div(static_cast<uint32_t>(p.value / ea::kDims));
+    p.div_vd64 = fast_div(static_cast<uint32_t>(p.value / 64));
     if (p.max_context > p.exact_max && (!p.split || attention_split_chunks(p.max_context) > kMaxSplitChunks))
         return hipErrorInvalidValue;
     if (group < 1 || group > kMaxGroup || p.heads % p.kv_heads || p.head > kMaxHead || p.head % 8 ||

@@ -172,6 +172,7 @@ __device__ __forceinline__ void pass_turn(uint64_t *word, int k_next, float acc)
 // segment's chain is run from it over the stored e values, so the result is
 // the left-to-right sum in every case.
 constexpr int kZCand = 256;                // candidate starting sums per segment (one per thread)
+static_assert((kZCand & (kZCand - 1)) == 0, "candidate indices are masked to a row");
 constexpr int kZNext = kZCand;             // row offset of the next-segment indices
 constexpr int kZCentre = 2 * kZCand;       // row offset of the centre's bits
 constexpr int kZStride = 2 * kZCand + 2;   // row: T[kZCand] | next[kZCand] | centre | pad
@@ -190,6 +191,19 @@ __device__ __forceinline__ int z_index(float s, uint32_t centre) {
 __device__ __forceinline__ float resolve_z(const int32_t *walk, int walk_stride, const float *tab, const float *ev,
     int n) {
     const int nseg = (n + kSeg - 1) / kSeg;
+    // every running sum a candidate of its segment (the usual case): one
+    // dependent LDS read per segment, an index outside a window (w < 0) only
+    // noted, and the general walk below taken if one occurred
+    {
+        int idx = kZCand / 2, miss = 0;
+#pragma unroll 4
+        for (int k = 0; k + 1 < nseg; ++k) {
+            const int w = walk[static_cast<size_t>(k) * walk_stride + idx];
+            miss |= w;
+            idx = w & (kZCand - 1);  // stays in the row when w < 0
+        }
+        if (miss >= 0) return __int_as_float(walk[static_cast<size_t>(nseg - 1) * walk_stride + idx]);
+    }
     int idx = kZCand / 2;
     bool have = true;  // the running sum is candidate idx of segment k
     float s = 0.0f;
@@ -235,13 +249,16 @@ __host__ __device__ constexpr size_t output_lds_floats(int max_context) {
 constexpr int kPieces = kSeg / 64;
 typedef uint4 ValuePieces[kPieces];
 
+// Every load is unconditional, its position clamped to the first n (n >= 1):
+// a per-lane condition around a load makes the compiler branch and wait for
+// it on the spot.  The pieces of positions p >= n are never used (their
+// products are staged as -0 by the callers).
 __device__ __forceinline__ void value_fetch(const uint16_t *vbase, size_t vstride, int n, int k, ValuePieces &v) {
     const int lane = static_cast<int>(threadIdx.x) & 63;
 #pragma unroll
     for (int i = 0; i < kPieces; ++i) {
-        const int p = k * kSeg + lane + 64 * i;
-        v[i] = p < n ? *reinterpret_cast<const uint4 *>(vbase + static_cast<size_t>(p) * vstride)
-                     : make_uint4(0u, 0u, 0u, 0u);
+        const int p = min(k * kSeg + lane + 64 * i, n - 1);
+        v[i] = *reinterpret_cast<const uint4 *>(vbase + static_cast<size_t>(p) * vstride);
     }
 }
 

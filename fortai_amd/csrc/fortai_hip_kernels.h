@@ -8,6 +8,7 @@
 // finished by a small follow-up kernel instead.
 #pragma once
 
+#include "fastdiv.h"
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -217,6 +218,9 @@ struct AttentionParams {
     int exact_max = 1 << 30;
     float *split = nullptr;         // [heads][attention_split_chunks][value + 2]
     int z_skew = 0;                 // test hook: offset of the Z candidate windows (0 in use)
+    // the kernels' divisors, set by launch_attention from the fields above:
+    // heads, kv_heads, heads / kv_heads, head, head / 8, value / 8, value / 64
+    FastDiv div_heads, div_kv_heads, div_group, div_head, div_segs, div_slices, div_vd64;
 };
 int attention_split_chunks(int max_context);
 // batch > 1: sequences along blockIdx.y, every buffer [batch][single size],

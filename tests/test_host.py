@@ -209,3 +209,49 @@ def test_pack_key_and_cache_path(tmp_path):
         assert got[n][0] == r and got[n][1] == w and np.array_equal(got[n][2], a)
     assert pc.read(path, b"e" * 32) is None          # made from another GGUF
     assert pc.read(str(tmp_path / "none.pack"), b"d" * 32) is None
+
+
+def test_fast_division_matches_integer_division(tmp_path):
+    """fortai_amd/csrc/fastdiv.h (the device kernels' division by launch-fixed
+    divisors) against C's / and %: every divisor 1..1024 with every dividend
+    below 2^16, and 2^22 pseudo-random dividends below 2^31 per divisor up to
+    2^20 in powers of two and their neighbours."""
+    import shutil
+    import subprocess
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    src = tmp_path / "fd.cpp"
+    src.write_text(r'''
+#define __host__
+#define __device__
+#include "fastdiv.h"
+#include <cstdio>
+using namespace fortai_hip;
+static int check(uint32_t d, uint32_t n) {
+    const FastDiv f = fast_div(d);
+    return div((int)n, f) != (int)(n / d) || mod((int)n, f) != (int)(n % d);
+}
+int main() {
+    long bad = 0;
+    for (uint32_t d = 1; d <= 1024; ++d)
+        for (uint32_t n = 0; n < 65536; ++n) bad += check(d, n);
+    uint32_t s = 0x6f727461u;
+    for (uint32_t e = 0; e <= 20; ++e)
+        for (int k = -1; k <= 1; ++k) {
+            const uint32_t d = (1u << e) + k;
+            if (d == 0) continue;
+            for (int i = 0; i < (1 << 18); ++i) {
+                s ^= s << 13; s ^= s >> 17; s ^= s << 5;
+                bad += check(d, s & 0x7fffffffu);
+            }
+            bad += check(d, 0x7fffffffu) + check(d, 0x7ffffffeu);
+        }
+    printf("%ld\n", bad);
+    return bad != 0;
+}
+''')
+    exe = tmp_path / "fd"
+    subprocess.run([gxx, "-O2", "-I", os.path.join(ROOT, "fortai_amd", "csrc"), str(src), "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout
