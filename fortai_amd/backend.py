@@ -88,6 +88,7 @@ _SIGNATURES = {
     "fortai_hip_qwen35_recurrent_state_download": [_vp, _vp, _sz, _vp, _sz],
     "fortai_hip_qwen35_recurrent_state_upload": [_vp, _vp, _sz, _vp, _sz],
     "fortai_hip_qwen35_attention_core_device": [_vp, _vp, _vp, _vp, _vp],
+    "fortai_hip_qwen35_attention_prefill_core_device": [_vp, _vp, _vp, _vp, _i, _i, _vp],
     "fortai_hip_qwen35_attention_cache_download": [_vp, _vp, _vp, _i],
     "fortai_hip_qwen35_attention_cache_upload": [_vp, _vp, _vp, _i],
     "fortai_hip_qwen35_decoder_create": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,

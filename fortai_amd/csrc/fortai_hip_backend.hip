@@ -1433,6 +1433,18 @@ int fortai_hip_qwen35_attention_core_device(fortai_hip_qwen35_attention *A, cons
         static_cast<const float *>(v), static_cast<float *>(out)), c->stream), "Qwen attention core");
 }
 
+int fortai_hip_qwen35_attention_prefill_core_device(fortai_hip_qwen35_attention *A, void *q, const void *k,
+    const void *v, int T, int matrix_cores, void *out) {
+    if (!A || !A->context || !q || !k || !v || !out || T < 1 || T > A->max_context) return FORTAI_HIP_INVALID;
+    auto *c = A->context;
+    (void)hipSetDevice(c->device);
+    AttentionParams ap = attention_params(A, static_cast<const float *>(q), static_cast<const float *>(k),
+        static_cast<const float *>(v), static_cast<float *>(out));
+    const hipError_t e = launch_attention_prefill(ap, 1, T, static_cast<float *>(out), c->stream, matrix_cores != 0);
+    if (e == hipErrorInvalidValue) return fail(c, FORTAI_HIP_INVALID, "prefill attention: unsupported layer shape", e);
+    return done(c, e, "Qwen prefill attention core");
+}
+
 int fortai_hip_qwen35_attention_cache_download(fortai_hip_qwen35_attention *A, uint16_t *keys, uint16_t *values,
     int positions) {
     if (!A || !A->context || positions <= 0 || positions > A->max_context) return FORTAI_HIP_INVALID;

@@ -493,6 +493,18 @@ FORTAI_HIP_WEAK int fortai_hip_qwen35_recurrent_state_upload(fortai_hip_qwen35_r
     return FORTAI_HIP_RUNTIME_ERROR;
 }
 
+FORTAI_HIP_WEAK int fortai_hip_qwen35_attention_prefill_core_device(fortai_hip_qwen35_attention *layer, void *device_query, const void *device_key, const void *device_value, int T, int matrix_cores, void *device_output)
+{
+    (void)layer;
+    (void)device_query;
+    (void)device_key;
+    (void)device_value;
+    (void)T;
+    (void)matrix_cores;
+    (void)device_output;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
 FORTAI_HIP_WEAK int fortai_hip_qwen35_attention_core_device(fortai_hip_qwen35_attention *layer, const void *device_query, const void *device_key, const void *device_value, void *device_output)
 {
     (void)layer;

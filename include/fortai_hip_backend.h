@@ -299,6 +299,17 @@ int fortai_hip_qwen35_recurrent_state_upload(fortai_hip_qwen35_recurrent *layer,
 int fortai_hip_qwen35_attention_core_device(fortai_hip_qwen35_attention *layer,
     const void *device_query, const void *device_key, const void *device_value,
     void *device_output);
+/* The prompt prefill's attention for one sequence of T tokens from position
+ * 0 [extension; the reference has no prefill, it runs
+ * fortai_qwen35_cpu.f90:990-1031 once per token]: q [T][heads][q | gate],
+ * k [T][kv_heads][head], v [T][kv_heads][value] (device fp32) -> gated
+ * outputs [T][heads][value]; q is normalised and rotated in place and K/V are
+ * appended at positions 0..T-1.  matrix_cores = 0: the exact kernel (the
+ * reference's summation orders, the default prefill), 1: the fp16
+ * matrix-core kernel of FORTAI_HIP_PREFILL=fast.  Heads of 64, 128 or 256. */
+int fortai_hip_qwen35_attention_prefill_core_device(fortai_hip_qwen35_attention *layer,
+    void *device_query, const void *device_key, const void *device_value, int T,
+    int matrix_cores, void *device_output);
 int fortai_hip_qwen35_attention_cache_download(fortai_hip_qwen35_attention *layer,
     uint16_t *host_keys, uint16_t *host_values, int positions);
 int fortai_hip_qwen35_attention_cache_upload(fortai_hip_qwen35_attention *layer,
