@@ -344,12 +344,26 @@ __device__ __forceinline__ float4 sdot4x4_f(uint4 q, uint4 a) {
     return r;
 }
 
+// fl(f32(h) * a) for the low (HI = false) or high half h of a packed pair of
+// fp16 bits: v_fma_mix_f32 widens the fp16 operand exactly, multiplies and
+// adds -0 (which leaves every product, zero or not, as it is) with one
+// rounding -- the value of the convert-then-multiply, in one instruction.
+template <bool HI>
+__device__ __forceinline__ float half_times(uint32_t h2, float a) {
+    float r;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(a), "v"(-0.0f));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(a), "v"(-0.0f));
+    return r;
+}
+
 __device__ __forceinline__ float dot_chunk(uint4 q, uint2 sc, uint4 a, float4 as, float acc) {
     const float4 d = sdot4x4_f(q, a);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x)) * as.x, d.x, acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.x >> 16)) * as.y, d.y, acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y)) * as.z, d.z, acc);
-    acc = __builtin_fmaf(half_bits_to_float(static_cast<uint16_t>(sc.y >> 16)) * as.w, d.w, acc);
+    acc = __builtin_fmaf(half_times<false>(sc.x, as.x), d.x, acc);
+    acc = __builtin_fmaf(half_times<true>(sc.x, as.y), d.y, acc);
+    acc = __builtin_fmaf(half_times<false>(sc.y, as.z), d.z, acc);
+    acc = __builtin_fmaf(half_times<true>(sc.y, as.w), d.w, acc);
     return acc;
 }
 

@@ -80,6 +80,38 @@ def test_block_dots_and_matvec_bit_exact(ctx, oracle, rows, width):
     W.free()
 
 
+def test_matvec_denormal_and_zero_scales(ctx, oracle):
+    """Weight scales that are fp16 subnormals (both signs) or zeros, and
+    activation blocks so small that their Q8_0 scales are fp16 subnormals or
+    zero: the scale products fl(f32(w_scale) * a_scale) widen the halves
+    exactly whatever their class (F16C, fortai_q8_dot.c:305-318), so every
+    matvec output is still bit-identical to the reference."""
+    rng = np.random.default_rng(0xDE40)
+    rows, width = 512, 2048
+    w = synth.q8_blocks(rng, rows, width)
+    nb = width // 32
+    pick = rng.random((rows, nb))
+    sub = (rng.integers(1, 0x400, size=(rows, nb)) | (rng.integers(0, 2, size=(rows, nb)) << 15)).astype(np.uint16)
+    zero = np.where(rng.integers(0, 2, size=(rows, nb)) == 0, 0x0000, 0x8000).astype(np.uint16)
+    bits = w[:, :, 0:2].copy().view(np.uint16)[..., 0]
+    bits = np.where(pick < 0.3, sub, np.where(pick < 0.35, zero, bits)).astype(np.uint16)
+    w[:, :, 0:2] = bits[..., None].view(np.uint8).reshape(rows, nb, 2)
+    x = rng.standard_normal(width).astype(np.float32)
+    tiny = rng.choice(nb, size=nb // 3, replace=False)
+    for b in tiny:  # amax / 127 below the smallest normal half (6.1e-5), some below half the smallest subnormal
+        x[32 * b:32 * b + 32] *= np.float32(rng.choice([1e-3, 1e-4, 1e-5, 1e-7]))
+    q, s_ = oracle.quantize(x)
+    assert np.any((s_ != 0) & (np.abs(s_) < 6.1e-5)) and np.any(s_ == 0), "the activation has subnormal and zero scales"
+    want = oracle.matvec(w, rows, width, x)
+    W = B.Q8Weights(ctx, w, rows, width)
+    dx = ctx.upload_array(x)
+    out = ctx.alloc(rows * 4)
+    ctx.call("fortai_hip_q8_matvec_device_f32", ctx.h, W.h, dx.ptr, width, out.ptr, rows)
+    got = out.download(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"max diff {np.max(np.abs(got - want))}"
+    W.free()
+
+
 def smoke_tensor(rows_scale):
     """The reference smoke test's Q8 tensors (test_fortai_smoke.f90:221-265)."""
     b = np.zeros((len(rows_scale), 34), dtype=np.uint8)
