@@ -60,9 +60,6 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     __shared__ __align__(16) float qh[kMaxGroup * kMaxHead];
     __shared__ __align__(16) float kn[kMaxHead];
-    __shared__ __align__(16) float vn[kMaxHead];
-    __shared__ __align__(16) float qw[kMaxHead];
-    __shared__ __align__(16) float kw[kMaxHead];
     __shared__ __align__(16) float2 rs[kMaxHead / 2];
     __shared__ __align__(16) uint16_t ktile[ea::kPosBlock][kMaxHead + 8];
     __shared__ int overflow;
@@ -100,20 +97,22 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
         qv[i] = p.q[static_cast<size_t>(kvh * group + eh) * 2 * HD + (e - eh * HD)];
     }
     const int th = min(tid, HD - 1), tv = min(tid, VD - 1);
-    const float qwv = p.q_norm[th], kwv = p.k_norm[th];
     const float knv = p.k[static_cast<size_t>(kvh) * HD + th];
+    // the q and k norm weights a lane applies (elements lane + 64 j of a head)
+    constexpr int kNW = kMaxHead / 64;
+    float qwr[kNW], kwr[kNW];
+#pragma unroll
+    for (int j = 0; j < kNW; ++j) {
+        qwr[j] = p.q_norm[min(lane + 64 * j, HD - 1)];
+        kwr[j] = p.k_norm[min(lane + 64 * j, HD - 1)];
+    }
     const float vnv = p.v[static_cast<size_t>(kvh) * VD + tv];
     const float2 rsv = half > 0 ? p.rope[static_cast<size_t>(pos) * half + min(tid, half - 1)] : make_float2(0.0f, 0.0f);
     const int flag = p.cache_flags[kvh];
 #pragma unroll
     for (int i = 0; i < kQLoads; ++i)
         if (tid + i * ea::kThreads < group * HD) qh[tid + i * ea::kThreads] = qv[i];
-    if (tid < HD) {
-        qw[tid] = qwv;
-        kw[tid] = kwv;
-        kn[tid] = knv;
-    }
-    if (tid < VD) vn[tid] = vnv;
+    if (tid < HD) kn[tid] = knv;
     if (tid < half) rs[tid] = rsv;
     if (tid == 0) overflow = 0;
     FORTAI_ATT_MARK(9);
@@ -125,8 +124,8 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     }
     __syncthreads();
     for (int sl = wave; sl < group + (owns_new ? 1 : 0); sl += ea::kThreads / 64) {
-        if (sl < group) ea::norm_rope(qh + sl * HD, HD, qw, p.eps, rs, p.rope_dim, lane);
-        else ea::norm_rope(kn, HD, kw, p.eps, rs, p.rope_dim, lane);
+        if (sl < group) ea::norm_rope_regs(qh + sl * HD, HD, qwr, p.eps, rs, p.rope_dim, lane);
+        else ea::norm_rope_regs(kn, HD, kwr, p.eps, rs, p.rope_dim, lane);
     }
     __syncthreads();
     FORTAI_ATT_MARK(10);
@@ -139,7 +138,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
             if ((kb & 0x7c00u) == 0x7c00u) overflow = 1;
         }
         if (tid < VD) {
-            const uint16_t vb = float_to_half_kv(vn[tid]);
+            const uint16_t vb = float_to_half_kv(vnv);
             p.vcache[(static_cast<size_t>(pos) * NKV + kvh) * VD + tid] = vb;
             if ((vb & 0x7c00u) == 0x7c00u) overflow = 1;
         }

@@ -47,11 +47,51 @@ __device__ __forceinline__ void norm_rope(float *v, int head, const float *w, fl
     __builtin_amdgcn_wave_barrier();
 }
 
+// The same with the weights in registers: wr[j] = w[lane + 64 j] (loaded by
+// the caller ahead of time), head <= 64 * NW.
+template <int NW>
+__device__ __forceinline__ void norm_rope_regs(float *v, int head, const float (&wr)[NW], float eps,
+    const float2 *rope, int rope_dim, int lane) {
+    double ss = 0.0;
+    for (int i = lane; i < head; i += 64) ss += static_cast<double>(v[i]) * static_cast<double>(v[i]);
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(head)) + eps);
+#pragma unroll
+    for (int j = 0; j < NW; ++j)
+        if (lane + 64 * j < head) v[lane + 64 * j] = (v[lane + 64 * j] * inv) * wr[j];
+    __builtin_amdgcn_wave_barrier();
+    const int half = rope_dim / 2;
+    for (int i = lane; i < half; i += 64) {
+        const float2 cs = rope[i];
+        const float a = v[i], b = v[i + half];
+        v[i] = a * cs.x - b * cs.y;
+        v[i + half] = a * cs.y + b * cs.x;
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 // One position's score: the sequential dot of fortai_qwen35_cpu.f90:1009-1014.
 // q in LDS (broadcast reads), the key row in LDS, 8 halves per read.
 template <bool FINITE>
 __device__ __forceinline__ float score(const float *q, const uint16_t *krow, int head, float sqrt_head) {
     float acc = 0.0f;
+    if constexpr (FINITE) {
+        // fl(q_i * f32(k_i)) straight from the fp16 half: one v_fma_mix_f32 each
+        for (int i = 0; i < head; i += 8) {
+            const uint4 h8 = *reinterpret_cast<const uint4 *>(krow + i);
+            const float4 qa = *reinterpret_cast<const float4 *>(q + i);
+            const float4 qb = *reinterpret_cast<const float4 *>(q + i + 4);
+            acc = acc + half_times<false>(h8.x, qa.x);
+            acc = acc + half_times<true>(h8.x, qa.y);
+            acc = acc + half_times<false>(h8.y, qa.z);
+            acc = acc + half_times<true>(h8.y, qa.w);
+            acc = acc + half_times<false>(h8.z, qb.x);
+            acc = acc + half_times<true>(h8.z, qb.y);
+            acc = acc + half_times<false>(h8.w, qb.z);
+            acc = acc + half_times<true>(h8.w, qb.w);
+        }
+        return acc / sqrt_head;
+    }
     for (int i = 0; i < head; i += 8) {
         const uint4 h8 = *reinterpret_cast<const uint4 *>(krow + i);
         const float4 qa = *reinterpret_cast<const float4 *>(q + i);
