@@ -513,6 +513,170 @@ __global__ __launch_bounds__(256) void attention_prefill_exact_kernel(const floa
     }
 }
 
+// The same arithmetic and orders with fixed trip counts: 16 queries per
+// workgroup (rows past the prompt are zero and never stored), keys clamped
+// into the cache and masked through zero weights, K / V tiles loaded one
+// ahead into registers, and (FINITE, no exponent-31 half in this cache) each
+// product fl(a * f32(h)) taken straight from the fp16 half by v_fma_mix_f32.
+// A workgroup whose cache is flagged returns unless !FINITE, and the !FINITE
+// instance serves only flagged caches, so the two launches split the work.
+constexpr int kXQ = 16;  // queries per workgroup
+
+template <bool FINITE>
+__device__ __forceinline__ float times_half(uint32_t h2, bool hi, float a) {
+    if constexpr (FINITE) return hi ? half_times<true>(h2, a) : half_times<false>(h2, a);
+    return a * gguf_half_to_real(static_cast<uint16_t>(hi ? h2 >> 16 : h2 & 0xffffu));
+}
+
+template <int HEAD, bool FINITE>
+__global__ __launch_bounds__(256, 2) void attention_prefill_exact16_kernel(const float *__restrict__ q,
+    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, const int *__restrict__ flags,
+    float *__restrict__ out, int T, int heads, int kv_heads, int max_context, int kcap) {
+    static_assert(HEAD % 64 == 0 && HEAD <= 256, "head 64, 128 or 256");
+    constexpr int kPieces = kXKeys * HEAD / 8 / 256;  // 16-byte tile pieces per thread
+    constexpr int kQS = 256 / HEAD;                   // P.V: query phases per dim
+    constexpr int kQPT = kXQ / kQS;                   // P.V: queries per thread
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    float *qs = reinterpret_cast<float *>(lds_raw);                   // [16][HEAD] normalized q
+    uint16_t *kv = reinterpret_cast<uint16_t *>(qs + kXQ * HEAD);      // K: [HEAD/8][kXKeys][8]; V: [kXKeys][HEAD]
+    float *sc = reinterpret_cast<float *>(kv + kXKeys * HEAD);          // [16][kcap] scores, then e, then weights
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const int h = static_cast<int>(blockIdx.y), s = static_cast<int>(blockIdx.z);
+    const int kvh = h / (heads / kv_heads);
+    if ((flags[static_cast<size_t>(s) * kv_heads + kvh] != 0) == FINITE) return;
+    const int q0 = static_cast<int>(blockIdx.x) * kXQ;
+    const int nq = min(kXQ, T - q0);
+    const int keys = q0 + nq;                                       // keys 0..keys-1 cover the block
+    const int tiles = (keys + kXKeys - 1) / kXKeys, kpad = tiles * kXKeys;
+    const float sqrt_head = sqrtf(static_cast<float>(HEAD));
+    const uint16_t *kbase = kcache + (static_cast<size_t>(s) * max_context * kv_heads + kvh) * HEAD;
+    const uint16_t *vbase = vcache + (static_cast<size_t>(s) * max_context * kv_heads + kvh) * HEAD;
+    const size_t kvstride = static_cast<size_t>(kv_heads) * HEAD;
+    u32x4_t tile[kPieces];  // plain vectors (an array of the uint4 class would live in scratch)
+    // K tile piece e: key e / (HEAD/8), 8 dims (e % (HEAD/8)) of it; V tile piece e: the same key and dims
+    auto fetch = [&](const uint16_t *base, int j0) {
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+            const int e = tid + 256 * i, j = e / (HEAD / 8), piece = e % (HEAD / 8);
+            tile[i] = *reinterpret_cast<const u32x4_t *>(base + static_cast<size_t>(min(j0 + j, keys - 1)) * kvstride +
+                piece * 8);
+        }
+    };
+    fetch(kbase, 0);
+    for (int e = tid; e < kXQ * HEAD; e += 256) {
+        const int qi = e / HEAD, d = e % HEAD;
+        qs[e] = qi < nq ? q[((static_cast<size_t>(s) * T + q0 + qi) * heads + h) * 2 * HEAD + d] : 0.0f;
+    }
+
+    // ---- scores: lane = key, wave = queries wave + 4 r
+    for (int t = 0; t < tiles; ++t) {
+        __syncthreads();  // the previous tile is consumed (and q is in place)
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+            const int e = tid + 256 * i, j = e / (HEAD / 8), piece = e % (HEAD / 8);
+            *reinterpret_cast<u32x4_t *>(kv + (piece * kXKeys + j) * 8) = tile[i];
+        }
+        __syncthreads();
+        if (t + 1 < tiles) fetch(kbase, (t + 1) * kXKeys);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int d = 0; d < HEAD; d += 8) {
+            const uint4 k8 = *reinterpret_cast<const uint4 *>(kv + ((d / 8) * kXKeys + lane) * 8);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float4 qa = *reinterpret_cast<const float4 *>(qs + (wave + 4 * r) * HEAD + d);
+                const float4 qc = *reinterpret_cast<const float4 *>(qs + (wave + 4 * r) * HEAD + d + 4);
+                float a = acc[r];
+                a = a + times_half<FINITE>(k8.x, false, qa.x);
+                a = a + times_half<FINITE>(k8.x, true, qa.y);
+                a = a + times_half<FINITE>(k8.y, false, qa.z);
+                a = a + times_half<FINITE>(k8.y, true, qa.w);
+                a = a + times_half<FINITE>(k8.z, false, qc.x);
+                a = a + times_half<FINITE>(k8.z, true, qc.y);
+                a = a + times_half<FINITE>(k8.w, false, qc.z);
+                a = a + times_half<FINITE>(k8.w, true, qc.w);
+                acc[r] = a;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[(wave + 4 * r) * kcap + t * kXKeys + lane] = acc[r] / sqrt_head;
+    }
+    fetch(vbase, 0);  // the first value tile, while the weights are formed
+    __syncthreads();
+    // ---- softmax weights: query wave + 4 r, lanes over keys; e = +0 past the query's keys
+    constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int qi = wave + 4 * r, n = min(q0 + qi + 1, keys);
+        float *row = sc + qi * kcap;
+        float m = kLowest;
+        for (int j = lane; j < n; j += 64) m = fmaxf(m, row[j]);
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        for (int j = lane; j < kpad; j += 64) row[j] = j < n ? expf_libm(row[j] - m) : 0.0f;
+    }
+    __syncthreads();
+    // Z of each query by one lane, left to right (the masked keys add +0)
+    if (lane < 4) {
+        const int qi = wave + 4 * lane;
+        const float *row = sc + qi * kcap;
+        float z = 0.0f;
+        for (int j = 0; j < kpad; j += 4) {
+            const float4 e4 = *reinterpret_cast<const float4 *>(row + j);
+            z = z + e4.x;
+            z = z + e4.y;
+            z = z + e4.z;
+            z = z + e4.w;
+        }
+        qs[qi * HEAD] = z;  // q is no longer needed: slot 0 of the row holds Z
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int qi = wave + 4 * r;
+        const float z = qs[qi * HEAD];
+        float *row = sc + qi * kcap;
+        for (int j = lane; j < kpad; j += 64) row[j] = row[j] / z;
+    }
+
+    // ---- P.V: thread = (dim d, queries qd + kQS r), keys left to right
+    const int d = tid % HEAD, qd = tid / HEAD;
+    float acc[kQPT];
+#pragma unroll
+    for (int r = 0; r < kQPT; ++r) acc[r] = 0.0f;
+    for (int t = 0; t < tiles; ++t) {
+        __syncthreads();  // the weights are complete / the previous tile is consumed
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+            const int e = tid + 256 * i, j = e / (HEAD / 8), piece = e % (HEAD / 8);
+            *reinterpret_cast<u32x4_t *>(kv + j * HEAD + piece * 8) = tile[i];
+        }
+        __syncthreads();
+        if (t + 1 < tiles) fetch(vbase, (t + 1) * kXKeys);
+        for (int jj = 0; jj < kXKeys; jj += 4) {
+            uint32_t vh[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) vh[u] = kv[(jj + u) * HEAD + d];
+#pragma unroll
+            for (int r = 0; r < kQPT; ++r) {
+                const float4 w4 = *reinterpret_cast<const float4 *>(sc + (qd + kQS * r) * kcap + t * kXKeys + jj);
+                float a = acc[r];
+                a = a + times_half<FINITE>(vh[0], false, w4.x);
+                a = a + times_half<FINITE>(vh[1], false, w4.y);
+                a = a + times_half<FINITE>(vh[2], false, w4.z);
+                a = a + times_half<FINITE>(vh[3], false, w4.w);
+                acc[r] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kQPT; ++r) {
+        const int qi = qd + kQS * r;
+        if (qi >= nq) continue;
+        const size_t row = (static_cast<size_t>(s) * T + q0 + qi) * heads + h;
+        const float gate = q[row * 2 * HEAD + HEAD + d];
+        out[row * HEAD + d] = acc[r] * sigmoid_ref(gate);
+    }
+}
+
 // Causal attention of every prompt token (fortai_qwen35_cpu.f90:1006-1033
 // with an online softmax): one workgroup per (query block of 64, head,
 // sequence); four threads per query, each with a quarter of the head dims;
@@ -938,7 +1102,32 @@ hipError_t launch_attention_prefill(const AttentionParams &p, int batch, int T, 
         if (e != hipSuccess) return e;
     }
     if (!matrix_cores) {
-        // the exact kernel: queries per workgroup so that the block's scores fit in LDS
+        // 16 queries per workgroup when the block's scores fit in LDS (two
+        // launches: caches without and with exponent-31 halves)
+        const int kpad = (T + kXKeys - 1) / kXKeys * kXKeys;
+        const size_t lds16 = static_cast<size_t>(kXQ) * p.head * 4 + static_cast<size_t>(kXKeys) * p.head * 2 +
+            static_cast<size_t>(kXQ) * kpad * 4;
+        if (lds16 <= 80 * 1024) {
+            const dim3 xgrid((T + kXQ - 1) / kXQ, p.heads, batch);
+#define FORTAI_PREX(H)                                                                                              \
+    do {                                                                                                            \
+        hipLaunchKernelGGL((attention_prefill_exact16_kernel<H, true>), xgrid, dim3(256), lds16, stream, p.q,       \
+            p.kcache, p.vcache, p.cache_flags, out, T, p.heads, p.kv_heads, p.max_context, kpad);                   \
+        hipLaunchKernelGGL((attention_prefill_exact16_kernel<H, false>), xgrid, dim3(256), lds16, stream, p.q,      \
+            p.kcache, p.vcache, p.cache_flags, out, T, p.heads, p.kv_heads, p.max_context, kpad);                   \
+    } while (0)
+            switch (p.head) {
+            case 64: FORTAI_PREX(64); break;
+            case 128: FORTAI_PREX(128); break;
+            case 256: FORTAI_PREX(256); break;
+            default: return hipErrorInvalidValue;
+            }
+#undef FORTAI_PREX
+            note_launch("qk_rope_append_kernel grid %d + attention_prefill_exact16_kernel<%d> grid %dx%dx%d (x2)",
+                batch * T, p.head, xgrid.x, xgrid.y, xgrid.z);
+            return hipGetLastError();
+        }
+        // longer prompts: queries per workgroup so that the block's scores fit in LDS
         const int kcap = (T + 3) / 4 * 4;
         int qb = 16;
         auto lds_of = [&](int b) {
