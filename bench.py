@@ -742,7 +742,7 @@ def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: in
                    "ms_per_step": round(step_ms, 4), "tokens_per_s": round(batch * steps / (dec_ms * 1e-3), 1),
                    "algorithmic_bytes_per_step": int(step_bytes),
                    "gbps": round(step_bytes / (step_ms * 1e-3) / 1e9, 1)},
-        "exactness": {"sequences_checked": check, "bit_identical_to_token_by_token_decode": all(checked),
+        "exactness": {"sequences_checked": check, "bit_identical_to_token_by_token_decode": (all(checked) if checked else None),
                       "per_sequence": checked,
                       "what": "last prompt token's logits (bits), greedy next token and the next 4 batched decode "
                               "steps against the single-sequence decoder fed the prompt token by token"},
@@ -802,6 +802,9 @@ def main() -> int:
     ap.add_argument("--no-config5", action="store_true", help="skip the config 5 figures (4B shape, batch 8, prefill)")
     ap.add_argument("--config5-only", action="store_true",
                     help="print only the config 5 figures (for kernel tracing of the batch-8 decode)")
+    ap.add_argument("--config5-check", type=int, default=2, metavar="N",
+                    help="config 5: sequences re-decoded token by token for the exactness check (0 for a kernel "
+                         "trace whose last steps are the batched ones)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the kernels the --pmc traffic passes measure (see traffic_probe)")
     ap.add_argument("--probe-decode", action="store_true",
@@ -835,7 +838,7 @@ def main() -> int:
         pmc_summary(*args.pmc_summary, family_steps=PROBE_STEPS if args.probe_decode_only else 0)
         return 0
     if args.config5_only:
-        print(json.dumps({"config5": bench_config5()}), flush=True)
+        print(json.dumps({"config5": bench_config5(check=args.config5_check)}), flush=True)
         return 0
     path = model_path(args)
     model, wall_ms, ev_ms, trace = bench_decode(args, path)
@@ -853,7 +856,7 @@ def main() -> int:
     decode_gbps = step_bytes * tok_s / 1e9
     model.close()
     if not args.no_config5:
-        model_cfg5 = bench_config5()
+        model_cfg5 = bench_config5(check=args.config5_check)
     cpu = None if args.no_cpu_baseline else cpu_baseline(path, args.ctx, args.cpu_steps, args.cpu_repeats)
     line = {
         "metric": "decode tokens/sec (bs=1, ctx 4096) + Q8_0 matvec HBM GB/s, Qwen3.5-0.8B shape",

@@ -127,6 +127,7 @@ struct fortai_hip_qwen35_decoder {
     float *argmax_value = nullptr;
     int32_t *argmax_index = nullptr;
     int64_t *trace = nullptr;
+    int64_t *embed = nullptr;  // the next step's token, or -1: the argmax of the LM head's partials
     int next_position = 0;  // host mirror of the device position after the queued steps
     bool use_graph = true;
     hipGraph_t graph = nullptr;
@@ -1487,13 +1488,32 @@ const char *fortai_hip_q8_last_error(const fortai_hip_q8_context *c) {
 // ------------------------------------------------------------------ decoder
 namespace {
 hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream);
-hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
+// the greedy argmax state of the decoder: partials of the LM head (or of the
+// argmax over the Q8_0 head's logits), token, trace, position, next token
+ArgmaxState decoder_argmax(fortai_hip_qwen35_decoder *d, int *partials) {
     auto *c = d->context;
+    ArgmaxState st;
+    st.partial_value = d->argmax_value;
+    st.partial_index = d->argmax_index;
+    st.token = c->token;
+    st.trace = d->trace;
+    st.trace_capacity = d->max_context;
+    st.position = c->position;
+    st.embed = d->embed;
+    if (partials) *partials = d->out16 ? f16_matvec_workgroups(d->vocab) : std::min((d->vocab + 255) / 256, 1024);
+    return st;
+}
+hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     g_matvec_only = d->matvec_only;
     hipError_t e = hipSuccess;
-    if (!g_matvec_only)
-        e = rec(d->emb16 ? launch_f16_embedding(d->emb16->data, d->emb16->rows, d->hidden, c->token, 0, d->x, stream)
-                         : launch_q8_embedding(d->emb8->m, c->token, 0, d->x, stream), "token embedding");
+    if (!g_matvec_only) {
+        // the embedding finishes the previous step's argmax (token, trace, position)
+        int parts = 0;
+        const ArgmaxState st = decoder_argmax(d, &parts);
+        e = rec(launch_step_embedding(d->emb16 ? d->emb16->data : nullptr, d->emb8 ? &d->emb8->m : nullptr,
+                    d->emb16 ? d->emb16->rows : d->emb8->m.rows, d->hidden, st, parts, d->x, stream),
+            "token embedding");
+    }
     for (size_t i = 0; i < d->layers.size() && e == hipSuccess; ++i) {
         const decoder_layer &L = d->layers[i];
         MatvecInput in;
@@ -1512,18 +1532,11 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
     if (e != hipSuccess || only) return e;
     return enqueue_lm_head(d, stream);
 }
-// final RMSNorm + LM head + greedy argmax from d->x; advances token, trace
-// and position for the next step
+// final RMSNorm + LM head + greedy argmax partials from d->x; the next step's
+// embedding (or finish_decoder_steps) turns them into token, trace and position
 hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
-    auto *c = d->context;
     hipError_t e = hipSuccess;
-    ArgmaxState st;
-    st.partial_value = d->argmax_value;
-    st.partial_index = d->argmax_index;
-    st.token = c->token;
-    st.trace = d->trace;
-    st.trace_capacity = d->max_context;
-    st.position = c->position;
+    const ArgmaxState st = decoder_argmax(d, nullptr);
     if (d->out16)
         return rec(launch_f16_matvec(d->out16->data, d->vocab, d->hidden, d->out16->finite, d->x, d->output_norm, d->eps,
             d->logits, &st, stream), "output RMSNorm, LM head, greedy argmax");
@@ -1545,6 +1558,22 @@ hipError_t run_step(fortai_hip_qwen35_decoder *d) {
                                       : enqueue_decoder_step(d, d->context->stream);
     g_plan = saved;
     return e;
+}
+// after a call's last step: the pending argmax finish, so token, trace and
+// position are current for the host (nothing when already finished)
+hipError_t finish_decoder_steps(fortai_hip_qwen35_decoder *d) {
+    if (d->matvec_only) return hipSuccess;
+    int parts = 0;
+    const ArgmaxState st = decoder_argmax(d, &parts);
+    return launch_argmax_finish(parts, st, d->context->stream);
+}
+// the token the next step embeds, as given by the host
+hipError_t set_decoder_token(fortai_hip_qwen35_decoder *d, int64_t token, int position) {
+    auto *c = d->context;
+    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, c->token, token);
+    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, d->embed, token);
+    hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
+    return hipGetLastError();
 }
 }  // namespace
 
@@ -1604,6 +1633,8 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     if (e == hipSuccess) e = alloc(&d->argmax_index, parts);
     if (e == hipSuccess) e = alloc(&d->trace, max_context + 1);
     if (e == hipSuccess) e = hipMemsetAsync(d->trace, 0, (max_context + 1) * sizeof(int64_t), c->stream);
+    if (e == hipSuccess) e = alloc(&d->embed, 1);
+    if (e == hipSuccess) e = hipMemsetAsync(d->embed, 0, sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (const char *env = std::getenv("FORTAI_HIP_DECODER_MATVEC_ONLY")) d->matvec_only = std::strcmp(env, "1") == 0;
     // the per-op decode step captured as a graph (FORTAI_HIP_DECODER_GRAPH=0
@@ -1640,7 +1671,7 @@ int fortai_hip_qwen35_decoder_destroy(fortai_hip_qwen35_decoder *d) {
         release(L.post_norm);
     }
     release(d->output_norm); release(d->x); release(d->logits); release(d->argmax_value);
-    release(d->argmax_index); release(d->trace);
+    release(d->argmax_index); release(d->trace); release(d->embed);
     if (d->h_q8l) (void)hipFree(d->h_q8l);
     delete d;
     return FORTAI_HIP_OK;
@@ -1669,10 +1700,9 @@ int fortai_hip_qwen35_decoder_forward(fortai_hip_qwen35_decoder *d, int64_t toke
         return FORTAI_HIP_INVALID;
     auto *c = d->context;
     (void)hipSetDevice(c->device);
-    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, c->token, token);
-    hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
-    hipError_t e = hipGetLastError();
+    hipError_t e = set_decoder_token(d, token, position);
     if (e == hipSuccess) e = run_step(d);
+    if (e == hipSuccess) e = finish_decoder_steps(d);
     d->next_position = position + 1;
     if (e == hipSuccess && logits)
         e = hipMemcpyAsync(logits, d->logits, static_cast<size_t>(d->vocab) * 4, hipMemcpyDeviceToHost, c->stream);
@@ -1689,10 +1719,9 @@ int fortai_hip_qwen35_decoder_generate(fortai_hip_qwen35_decoder *d, int64_t tok
         return FORTAI_HIP_INVALID;
     auto *c = d->context;
     (void)hipSetDevice(c->device);
-    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, c->stream, c->token, token);
-    hipLaunchKernelGGL(set_position_kernel, dim3(1), dim3(1), 0, c->stream, c->position, position);
-    hipError_t e = hipGetLastError();
+    hipError_t e = set_decoder_token(d, token, position);
     for (int s = 0; s < steps && e == hipSuccess; ++s) e = run_step(d);
+    if (e == hipSuccess) e = finish_decoder_steps(d);
     d->next_position = position + steps;
     if (e == hipSuccess)
         e = hipMemcpyAsync(trace, d->trace + position, static_cast<size_t>(steps) * sizeof(int64_t),
@@ -1707,6 +1736,7 @@ int fortai_hip_qwen35_decoder_replay(fortai_hip_qwen35_decoder *d, int steps) {
     (void)hipSetDevice(c->device);
     hipError_t e = hipSuccess;
     for (int s = 0; s < steps && e == hipSuccess; ++s) e = run_step(d);
+    if (e == hipSuccess) e = finish_decoder_steps(d);
     d->next_position += steps;
     return done(c, e, "decoder replay");
 }

@@ -134,6 +134,11 @@ struct ArgmaxState {
     int64_t *trace = nullptr;         // optional: trace[*position] = token
     int *position = nullptr;          // optional: advanced by one after the trace write
     int trace_capacity = 0;           // entries of trace
+    // optional, single sequence: the token the next decode step embeds when
+    // >= 0; -1 when it is still the argmax of the partials.  The producer of
+    // the partials writes -1 and leaves the finish to launch_step_embedding
+    // (or to launch_argmax_finish, which writes the resolved token here)
+    int64_t *embed = nullptr;
 };
 hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite_halves, const float *x,
     const float *norm, float eps, float *out, const ArgmaxState *argmax, hipStream_t stream);
@@ -149,7 +154,16 @@ hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, h
 // reduce `partials` argmax partials and publish token / trace / position
 // batch > 1: sequence s reduces partials [s * partials, (s + 1) * partials)
 // into token[s], trace[s * trace_capacity + position[s]], position[s]
+// With state.embed: nothing when *embed >= 0 already, else the finish above and
+// *embed = token.
 hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream, int batch = 1);
+// A decode step's first kernel, the token embedding (fp16 table16 or Q8_0
+// table8) with the previous step's argmax finish folded in: *state.embed >= 0
+// is embedded as is; otherwise every workgroup reduces the `partials` partials
+// (the first maximum, as launch_argmax_finish) and workgroup 0 publishes token,
+// trace and position.  One launch fewer per token than finish + embedding.
+hipError_t launch_step_embedding(const uint16_t *table16, const Q8Matrix *table8, int rows, int width,
+    const ArgmaxState &state, int partials, float *out, hipStream_t stream);
 // scan an fp16 table for exponent-31 patterns (inf/NaN), counted into *count
 hipError_t launch_count_nonfinite_halves(const uint16_t *w, size_t n, unsigned int *count, hipStream_t stream);
 

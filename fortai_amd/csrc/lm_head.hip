@@ -59,6 +59,7 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(int partials, Argmax
     st.token += seq;
     if (st.trace) st.trace += static_cast<size_t>(seq) * st.trace_capacity;
     if (st.position) st.position += seq;
+    if (st.embed && *st.embed >= 0) return;  // already finished (uniform)
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
     for (int w = tid; w < partials; w += 256)
@@ -74,7 +75,61 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(int partials, Argmax
             if (st.trace && p >= 0 && p < st.trace_capacity) st.trace[p] = token;
             *st.position = p + 1;
         }
+        if (st.embed) *st.embed = token;
     }
+}
+
+// The decode step's token embedding with the previous step's argmax finish
+// folded in (launch_step_embedding).  Every workgroup that finds *embed < 0
+// reduces all partials itself (the same first-maximum rule and all-NaN
+// fallback as argmax_finish_kernel), so no workgroup depends on another's
+// writes; only workgroup 0 writes token, trace[position] and position + 1,
+// which no other workgroup of this launch reads.  *embed is left as it is:
+// the next LM head writes -1 again, a finish writes the token.
+__global__ __launch_bounds__(256) void step_embedding_kernel(const uint16_t *table16, Q8Matrix table8, int rows,
+    int width, ArgmaxState st, int partials, float *out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    __shared__ int64_t chosen;
+    const int tid = static_cast<int>(threadIdx.x);
+    int64_t t = *st.embed;  // uniform
+    if (t < 0) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+        for (int w = tid; w < partials; w += 256)
+            if (better(st.partial_value[w], st.partial_index[w], bv, bi)) { bv = st.partial_value[w]; bi = st.partial_index[w]; }
+        block_argmax(bv, bi, sv, si);
+        if (tid == 0) {
+            const int64_t token = bi == 0x7fffffff ? 0 : bi;
+            chosen = token;
+            if (blockIdx.x == 0) {
+                *st.token = token;
+                const int p = *st.position;
+                if (st.trace && p >= 0 && p < st.trace_capacity) st.trace[p] = token;
+                *st.position = p + 1;
+            }
+        }
+        __syncthreads();
+        t = chosen;
+    }
+    if (t < 0 || t >= rows) t = 0;  // a device-fed id is never trusted as an address
+    const int i = static_cast<int>(blockIdx.x) * 256 + tid;
+    if (i >= width) return;
+    if (table16) {
+        out[i] = gguf_half_to_real(table16[t * width + i]);
+        return;
+    }
+    // Q8_0 row t in the repacked layout: value i is byte i % 4 of lane part
+    // (i % 32) / 4 of block i / 32
+    const int g = static_cast<int>(t >> 3), r = static_cast<int>(t & 7);
+    const int b = i / kQ8Block, within = i % kQ8Block, l = within >> 2, byte = within & 3;
+    const int c = b >> 2, j = b & 3;
+    const uint32_t *q32 = reinterpret_cast<const uint32_t *>(table8.quants);
+    const uint32_t word = q32[((static_cast<size_t>(g) * table8.chunks + c) * 64 + r * 8 + l) * 4 + j];
+    const int8_t q = static_cast<int8_t>((word >> (8 * byte)) & 0xffu);
+    const uint16_t *s16 = reinterpret_cast<const uint16_t *>(table8.scales);
+    const uint16_t sb = s16[((static_cast<size_t>(g) * table8.chunks + c) * 8 + r) * 4 + j];
+    out[i] = half_bits_to_float(sb) * static_cast<float>(q);
 }
 
 // TILE fp16 columns per LDS tile (row pitch TILE + 8 halves: eight 16-byte
@@ -176,6 +231,7 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
         if (tid == 0) {
             st.partial_value[blockIdx.x] = v;
             st.partial_index[blockIdx.x] = i;
+            if (st.embed && blockIdx.x == 0) *st.embed = -1;  // the next step's embedding finishes the argmax
         }
     }
 }
@@ -345,6 +401,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *values, int n,
     if (threadIdx.x == 0) {
         st.partial_value[blockIdx.x] = v;
         st.partial_index[blockIdx.x] = i;
+        if (st.embed && blockIdx.x == 0) *st.embed = -1;
     }
 }
 
@@ -387,7 +444,7 @@ hipError_t launch_f16_matvec(const uint16_t *w, int rows, int width, bool finite
     else FORTAI_LM(false, false, false);
 #undef FORTAI_LM
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !argmax) {
+    if (e != hipSuccess || !argmax || st.embed) {  // with embed the next step's embedding finishes
         note_launch("f16_matvec_kernel<rms=%d,argmax=0,finite=%d,tile=%d> grid %d", norm != nullptr, finite, wide ? 128 : 64,
             grid);
         return e;
@@ -438,6 +495,19 @@ hipError_t launch_argmax(const float *values, int n, const ArgmaxState &state, h
 hipError_t launch_argmax_finish(int partials, const ArgmaxState &state, hipStream_t stream, int batch) {
     if (batch < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL(argmax_finish_kernel, dim3(1, batch), dim3(256), 0, stream, partials, state);
+    return hipGetLastError();
+}
+
+hipError_t launch_step_embedding(const uint16_t *table16, const Q8Matrix *table8, int rows, int width,
+    const ArgmaxState &state, int partials, float *out, hipStream_t stream) {
+    if (!table16 == !table8 || rows <= 0 || width <= 0 || partials <= 0 || !state.embed || !state.token ||
+        !state.position || !state.partial_value || !state.partial_index || (table8 && table8->blocks * kQ8Block != width))
+        return hipErrorInvalidValue;
+    const Q8Matrix t8 = table8 ? *table8 : Q8Matrix{};
+    hipLaunchKernelGGL(step_embedding_kernel, dim3((width + 255) / 256), dim3(256), 0, stream, table16, t8, rows,
+        width, state, partials, out);
+    note_launch("step_embedding_kernel<%s> grid %d (argmax finish of %d partials folded in)", table16 ? "f16" : "q8",
+        (width + 255) / 256, partials);
     return hipGetLastError();
 }
 

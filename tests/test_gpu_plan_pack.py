@@ -33,7 +33,7 @@ def test_decoder_plans(tiny_model_path):
         m.batch.prefill(np.array([[1, 2, 3]] * 3))
         pplan = m.batch.plan(prefill=True)
         assert any(k.startswith("q8_mmq_exact_kernel") for _, k, _ in pplan)
-        assert any("attention_prefill_exact_kernel" in k for _, k, _ in pplan)
+        assert any("attention_prefill_exact" in k for _, k, _ in pplan)
         assert all(b == 9 for _, _, b in pplan)
     finally:
         m.close()
