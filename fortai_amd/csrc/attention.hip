@@ -371,123 +371,165 @@ size_t output_lds_bytes(int positions) {
 // The same arithmetic as attention_output_kernel (the reference's two-pass
 // softmax and P.V with its summation orders, fortai_qwen35_cpu.f90:1016-1031)
 // with one workgroup per (head, 64 value dims, sequence) instead of one per
-// (head, 8 value dims): e_p = expf(s_p - m) is computed once into LDS, one
-// lane sums Z left to right, w_p = e_p / Z replaces e_p, and lane d of wave 0
-// runs the P.V chain of value dim d0 + d over the positions in order.  The
-// value columns reach LDS in tiles of kWideTile positions, loaded by all
-// four waves two tiles ahead of the chains (the first two while the softmax
-// is computed).  A batch has many (head, sequence) pairs, so this fills the
-// chip with 1/8 as many workgroups, each chain step using all 64 lanes; a
-// single sequence keeps the per-slice kernel, whose chains are shorter per
-// workgroup.
-constexpr int kWideTile = 256;                                        // positions per value tile
-constexpr int kWideDims = 64;                                         // value dims per workgroup
-constexpr int kWidePitch = kWideDims + 8;                             // halves per LDS tile row
-constexpr int kWideLoads = kWideTile * kWideDims / 8 / ea::kThreads;  // 16-byte pieces per thread and tile
+// (head, 8 value dims): Z from the candidate tables (head_z), then lane d of
+// one wave runs the P.V chain of value dim d0 + d over the positions in order,
+// out_d = fl(w_0 v_0,d) + fl(w_1 v_1,d) + ... with w_p = e_p / Z.  A batch has
+// many (head, sequence) pairs, so this fills the chip with 1/8 as many
+// workgroups, each chain step using all 64 lanes; a single sequence keeps the
+// per-slice kernel, whose chains are shorter per workgroup.
+//
+// Values reach LDS in tiles of kWideTile positions, loaded by all four waves
+// two tiles ahead of the chain: each thread loads 8 positions x 8 dims (eight
+// 16-byte pieces), transposes them in registers and stores one 16-byte row
+// of 8 positions per dim, so the tile is [dim][position] and a chain lane
+// reads 8 positions of its dim with one 16-byte LDS read (and w_p of the tile,
+// divided when the tile is stored, with two).  The Z walk words use the tile's
+// LDS before the first tile is stored; nothing is sized by the context, so
+// four workgroups fit a CU.
+constexpr int kWideTile = 256;                   // positions per value tile
+constexpr int kWideDims = 64;                    // value dims per workgroup
+constexpr int kWidePitchT = kWideTile + 8;       // halves per LDS row of one dim (16-byte rows, no bank conflicts)
 constexpr int kWideMaxPositions = 8192;
+static_assert(kWideTile / 8 * (kWideDims / 8) == ea::kThreads, "one 8 x 8 block of (position, dim) per thread");
+static_assert(kWideDims * kWidePitchT * 2 >= kZLdsSegments * ea::kZCand * 4, "the Z walk words fit the tile's LDS");
 
-// positions whose scores the wide kernel holds in LDS, and their floats
-// (a multiple of 4: the value tile after them stays 16-byte aligned)
-__host__ __device__ inline int wide_positions(const AttentionParams &p) {
-    return p.max_context < p.exact_max ? p.max_context : p.exact_max;
+// dynamic LDS of attention_output_wide_kernel: the transposed tile, then w of the tile
+constexpr size_t kWideLdsBytes = static_cast<size_t>(kWideDims) * kWidePitchT * 2 + kWideTile * 4;
+
+// halves k of dwords a (low half of the result) and b (high half)
+__device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b, int hi) {
+    return hi ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
 }
-__host__ __device__ inline int wide_score_floats(const AttentionParams &p) { return (wide_positions(p) + 3) / 4 * 4; }
 
 template <bool FINITE>
-__device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int d0, int n, float *w, uint16_t *vt,
-    float *tab_lds, float *red) {
+__device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int d0, int n, uint16_t *vt, float *wt,
+    float *red) {
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     const int group = p.heads / p.kv_heads, HD = p.head, VD = p.value, NKV = p.kv_heads;
     const int kvh = h / group;
     const uint16_t *vb = p.vcache + static_cast<size_t>(kvh) * VD + d0;
     const size_t vs = static_cast<size_t>(NKV) * VD;
-    const int pieces = min(kWideDims, VD - d0) / 8;  // 16-byte pieces of a row slice
     const int tiles = (n + kWideTile - 1) / kWideTile;
-    uint4 ra[kWideLoads], rb[kWideLoads];
-    auto fetch = [&](int t, uint4 (&regs)[kWideLoads]) {
-#pragma unroll
-        for (int j = 0; j < kWideLoads; ++j) {
-            const int li = tid + ea::kThreads * j;  // piece index within the tile
-            const int pp = min(t * kWideTile + li / pieces, n - 1), pc = li % pieces;
-            regs[j] = li < kWideTile * pieces ? *reinterpret_cast<const uint4 *>(vb + pp * vs + pc * 8)
-                                              : make_uint4(0u, 0u, 0u, 0u);
-        }
-    };
-    auto stash = [&](const uint4 (&regs)[kWideLoads]) {
-#pragma unroll
-        for (int j = 0; j < kWideLoads; ++j) {
-            const int li = tid + ea::kThreads * j;
-            if (li < kWideTile * pieces)
-                *reinterpret_cast<uint4 *>(vt + (li / pieces) * kWidePitch + (li % pieces) * 8) = regs[j];
-        }
-    };
-    fetch(0, ra);
-    if (tiles > 1) fetch(1, rb);
-
-    // e_p (attention_softmax_kernel) into LDS, and Z from the candidate tables
+    // the wave that runs the chain: a hash of the workgroup, so that the
+    // chains of the workgroups sharing a CU spread over its four SIMDs (wave
+    // w of every workgroup lands on the same SIMD)
+    const uint32_t hw = (blockIdx.x * 2654435761u) ^ (blockIdx.y * 40503u);
+    const int cw = static_cast<int>((hw >> 13) & 3u);
     const float *ev = evals_of(p) + static_cast<size_t>(h) * p.max_context;
-    for (int i = tid; i < n; i += ea::kThreads) w[i] = ev[i];
-    const float z = head_z(p, h, n, reinterpret_cast<int32_t *>(tab_lds), red + 4);
-    for (int i = tid; i < n; i += ea::kThreads) w[i] = w[i] / z;
-    // (the first stash's barrier below orders these writes before the chains)
-
-    // P.V: out_d = fl(w_0 v_0,d) + fl(w_1 v_1,d) + ... left to right
+    // this thread's block: positions pg * 8 .. + 7 of a tile, dims pc * 8 .. + 7
+    const int pc = tid & 7, pg = tid >> 3;
+    const int pcl = min(pc, (min(kWideDims, VD - d0) >> 3) - 1);  // dims past VD re-read the last piece
+    FORTAI_ATTW_MARK(0);
+    // tile t: eight 16-byte pieces and e of position t * kWideTile + tid (all clamped to the last position)
+    auto fetch = [&](int t, uint4 (&regs)[8], float &e) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int pp = min(t * kWideTile + pg * 8 + i, n - 1);
+            regs[i] = *reinterpret_cast<const uint4 *>(vb + static_cast<size_t>(pp) * vs + pcl * 8);
+        }
+        e = ev[min(t * kWideTile + tid, n - 1)];
+    };
+    // Z first: its table loads would otherwise return after the whole value
+    // fetch (loads complete in order)
+    const float z = head_z(p, h, n, reinterpret_cast<int32_t *>(vt), red + 4);  // ends with a barrier
+    FORTAI_ATTW_MARK(3);
+    uint4 ra[8], rb[8];
+    float ea_ = 0.0f, eb_ = 0.0f;
+    fetch(0, ra, ea_);
+    if (tiles > 1) fetch(1, rb, eb_);
+    FORTAI_ATTW_MARK(1);
+    // the block transposed: row of dim pc * 8 + k holds positions pg * 8 .. + 7
+    auto stash = [&](const uint4 (&r)[8], float e) {
+        const uint32_t *w32 = reinterpret_cast<const uint32_t *>(r);  // w32[4 i + m]: dims 2m, 2m + 1 of position i
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int m = k >> 1, hi = k & 1;
+            uint4 row;
+            row.x = pick_halves(w32[0 * 4 + m], w32[1 * 4 + m], hi);
+            row.y = pick_halves(w32[2 * 4 + m], w32[3 * 4 + m], hi);
+            row.z = pick_halves(w32[4 * 4 + m], w32[5 * 4 + m], hi);
+            row.w = pick_halves(w32[6 * 4 + m], w32[7 * 4 + m], hi);
+            *reinterpret_cast<uint4 *>(vt + (pc * 8 + k) * kWidePitchT + pg * 8) = row;
+        }
+        wt[tid] = e / z;
+    };
     const int d = d0 + lane;
-    const int col = min(d, VD - 1) - d0;  // lanes past VD repeat the last dim and write nothing
-    // groups of 16 positions: the LDS reads of the next group are in flight
-    // while the current one is multiplied and added
-    constexpr int kG = 16;
-    struct Group {
-        float4 w4[kG / 4];
-        uint16_t v[kG];
+    const uint16_t *myrow = vt + lane * kWidePitchT;  // lanes past VD read a row of the tile they do not write
+    // the chain of one tile: groups of 8 positions from a ring of three
+    // register sets, each group's LDS reads issued two groups before its adds
+    struct Grp {
+        uint4 v;
+        float4 w0, w1;
     };
-    auto gread = [&](int p0, int j, Group &g) {
-#pragma unroll
-        for (int k = 0; k < kG / 4; ++k) g.w4[k] = *reinterpret_cast<const float4 *>(w + p0 + j + 4 * k);
-#pragma unroll
-        for (int k = 0; k < kG; ++k) g.v[k] = vt[(j + k) * kWidePitch + col];
+    // group g of the tile (a compile-time index: immediate LDS offsets)
+    auto ld = [&](int g, Grp &r) {
+        r.v = *reinterpret_cast<const uint4 *>(myrow + g * 8);
+        r.w0 = *reinterpret_cast<const float4 *>(wt + g * 8);
+        r.w1 = *reinterpret_cast<const float4 *>(wt + g * 8 + 4);
     };
-    auto gadd = [&](const Group &g, float acc) {
+    auto add8 = [&](const Grp &r, float acc) {
+        if constexpr (FINITE) {
+            // fl(w * f32(v)) in one instruction (exact widening, one rounding)
+            acc = acc + half_times<false>(r.v.x, r.w0.x);
+            acc = acc + half_times<true>(r.v.x, r.w0.y);
+            acc = acc + half_times<false>(r.v.y, r.w0.z);
+            acc = acc + half_times<true>(r.v.y, r.w0.w);
+            acc = acc + half_times<false>(r.v.z, r.w1.x);
+            acc = acc + half_times<true>(r.v.z, r.w1.y);
+            acc = acc + half_times<false>(r.v.w, r.w1.z);
+            acc = acc + half_times<true>(r.v.w, r.w1.w);
+        } else {
+            const uint32_t q[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
+            const float wv[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
 #pragma unroll
-        for (int k = 0; k < kG / 4; ++k) {
-            acc = acc + g.w4[k].x * ea::kv<FINITE>(g.v[4 * k + 0]);
-            acc = acc + g.w4[k].y * ea::kv<FINITE>(g.v[4 * k + 1]);
-            acc = acc + g.w4[k].z * ea::kv<FINITE>(g.v[4 * k + 2]);
-            acc = acc + g.w4[k].w * ea::kv<FINITE>(g.v[4 * k + 3]);
+            for (int k = 0; k < 8; ++k)
+                acc = acc + wv[k] * ea::kv<false>(static_cast<uint16_t>(q[k >> 1] >> (16 * (k & 1))));
         }
         return acc;
     };
     auto chain = [&](int t, float acc) {
-        const int p0 = t * kWideTile, cnt = min(kWideTile, n - p0);
-        const int full = cnt / kG * kG;
-        Group ga, gb;
-        if (full > 0) gread(p0, 0, ga);
-        int j = 0;
-        for (; j + 2 * kG <= full; j += 2 * kG) {
-            gread(p0, j + kG, gb);
-            acc = gadd(ga, acc);
-            if (j + 2 * kG < full) gread(p0, j + 2 * kG, ga);
-            acc = gadd(gb, acc);
+        const int cnt = min(kWideTile, n - t * kWideTile);
+        const int full = cnt >> 3;
+        constexpr int kGroups = kWideTile / 8;
+        Grp ring[3];
+        ld(0, ring[0]);
+        ld(1, ring[1]);
+        // fully unrolled: every LDS offset is an immediate, and the scheduling
+        // barriers keep each group's reads two groups ahead of its adds
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            if (g < full) {  // uniform
+                if (g + 2 < kGroups) ld(g + 2, ring[(g + 2) % 3]);
+                __builtin_amdgcn_sched_barrier(0);
+                acc = add8(ring[g % 3], acc);
+            }
         }
-        if (j < full) acc = gadd(ga, acc);
-        for (j = full; j < cnt; ++j) acc = acc + w[p0 + j] * ea::kv<FINITE>(vt[j * kWidePitch + col]);
+        // the last cnt % 8 positions
+        for (int k = 0; k < (cnt & 7); ++k) {
+            const int pp = full * 8 + k;
+            acc = acc + wt[pp] * ea::kv<FINITE>(myrow[pp]);
+        }
         return acc;
     };
     float acc = 0.0f;
     for (int t = 0; t < tiles; t += 2) {
-        stash(ra);
+        stash(ra, ea_);
         __syncthreads();
-        if (t + 2 < tiles) fetch(t + 2, ra);
-        if (wave == 0) acc = chain(t, acc);
+        if (t == 0) FORTAI_ATTW_MARK(6);
+        if (t + 2 < tiles) fetch(t + 2, ra, ea_);
+        if (t == 0) FORTAI_ATTW_MARK(7);
+        if (wave == cw) acc = chain(t, acc);
         __syncthreads();
+        if (t == 0) FORTAI_ATTW_MARK(4);
         if (t + 1 >= tiles) break;
-        stash(rb);
+        stash(rb, eb_);
         __syncthreads();
-        if (t + 3 < tiles) fetch(t + 3, rb);
-        if (wave == 0) acc = chain(t + 1, acc);
+        if (t + 3 < tiles) fetch(t + 3, rb, eb_);
+        if (wave == cw) acc = chain(t + 1, acc);
         __syncthreads();
     }
-    if (wave == 0 && d < VD) {
+    FORTAI_ATTW_MARK(5);
+    if (wave == cw && d < VD) {
         const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d];
         p.out[static_cast<size_t>(h) * VD + d] = acc * sigmoid_ref(gate);
     }
@@ -505,12 +547,12 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_wide_kernel(con
     const int slices = (p.value + kWideDims - 1) / kWideDims;
     const int h = static_cast<int>(blockIdx.x) / slices, d0 = (static_cast<int>(blockIdx.x) % slices) * kWideDims;
     const int kvh = h / (p.heads / p.kv_heads);
-    uint16_t *vt = reinterpret_cast<uint16_t *>(wide_lds + wide_score_floats(p));
-    float *tab_lds = wide_lds + wide_score_floats(p) + kWideTile * kWidePitch / 2;
+    uint16_t *vt = reinterpret_cast<uint16_t *>(wide_lds);
+    float *wt = wide_lds + kWideDims * kWidePitchT / 2;
     if (p.cache_flags[kvh] == 0)
-        attend_wide<true>(p, h, d0, n, wide_lds, vt, tab_lds, red);
+        attend_wide<true>(p, h, d0, n, vt, wt, red);
     else
-        attend_wide<false>(p, h, d0, n, wide_lds, vt, tab_lds, red);
+        attend_wide<false>(p, h, d0, n, vt, wt, red);
 }
 
 
@@ -756,11 +798,9 @@ hipError_t launch_attention(const AttentionParams &params, hipStream_t stream, i
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    const size_t tab_bytes = static_cast<size_t>(z_lds_segments(exact_positions)) * ea::kZCand * sizeof(float);
-    const bool wide = batch > 1 && wide_positions(p) <= kWideMaxPositions && p.value <= ea::kThreads;
+    const bool wide = (batch > 1 || p.force_wide) && exact_positions <= kWideMaxPositions && p.value <= ea::kThreads;
     if (wide) {
-        const size_t wlds = static_cast<size_t>(wide_score_floats(p)) * sizeof(float) +
-            static_cast<size_t>(kWideTile) * kWidePitch * sizeof(uint16_t) + tab_bytes;
+        const size_t wlds = kWideLdsBytes;
         const int wgrid = p.heads * ((p.value + kWideDims - 1) / kWideDims);
         hipLaunchKernelGGL(attention_output_wide_kernel, dim3(wgrid, batch), dim3(ea::kThreads), wlds, stream, p);
         e = hipGetLastError();

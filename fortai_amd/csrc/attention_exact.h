@@ -16,6 +16,9 @@
 #ifndef FORTAI_ATT_MARK
 #define FORTAI_ATT_MARK(i)
 #endif
+#ifndef FORTAI_ATTW_MARK
+#define FORTAI_ATTW_MARK(i)
+#endif
 
 namespace fortai_hip {
 namespace exact_attention {

@@ -105,6 +105,7 @@ struct fortai_hip_qwen35_attention {
     float *attn_out = nullptr;   // gated attention output (o_proj input)
     int exact_max = 0;           // positions with the bit-exact two-pass softmax; split-K beyond
     int z_skew = 0;              // test hook: offset of the Z candidate windows (FORTAI_HIP_ZTABLE_SKEW)
+    int force_wide = 0;          // test hook: the wide output kernel for one sequence (FORTAI_HIP_ATTENTION_WIDE)
     float *split = nullptr;      // split-K partials (allocated when max_context > exact_max)
 };
 
@@ -404,6 +405,7 @@ AttentionParams attention_params(fortai_hip_qwen35_attention *A, const float *q,
     p.position = A->context->position; p.heads = A->heads; p.kv_heads = A->kv_heads; p.head = A->head;
     p.value = A->value; p.max_context = A->max_context; p.rope_dim = A->rope_dim;
     p.eps = A->eps; p.exact_max = A->exact_max; p.split = A->split; p.z_skew = A->z_skew;
+    p.force_wide = A->force_wide;
     return p;
 }
 
@@ -1369,6 +1371,8 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
     // test hook: shift every Z candidate window by this many floats, so that
     // the running sums fall outside them and resolve_z's own chain runs
     if (const char *env = std::getenv("FORTAI_HIP_ZTABLE_SKEW")) A->z_skew = std::atoi(env);
+    // test hook: the batches' wide output kernel for a single sequence too
+    if (const char *env = std::getenv("FORTAI_HIP_ATTENTION_WIDE")) A->force_wide = std::atoi(env) != 0;
     if (e == hipSuccess && max_context > A->exact_max)
         e = alloc(&A->split, static_cast<size_t>(heads) * attention_split_chunks(max_context) * (value_size + 2));
     if (e == hipSuccess) e = alloc(&A->cache_flags, kv_heads);

@@ -232,6 +232,7 @@ struct AttentionParams {
     int exact_max = 1 << 30;
     float *split = nullptr;         // [heads][attention_split_chunks][value + 2]
     int z_skew = 0;                 // test hook: offset of the Z candidate windows (0 in use)
+    int force_wide = 0;             // test hook: the batches' wide output kernel for one sequence too
     // the kernels' divisors, set by launch_attention from the fields above:
     // heads, kv_heads, heads / kv_heads, head, head / 8, value / 8, value / 64
     FastDiv div_heads, div_kv_heads, div_group, div_head, div_segs, div_slices, div_vd64;

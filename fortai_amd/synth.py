@@ -48,6 +48,9 @@ class Qwen35Config:
     eps: float = 1.0e-6
     rope_base: float = 1.0e7
     embedding_q8: bool = False  # tied token_embd as Q8_0 (as llama.cpp Q8_0 exports) instead of F16
+    # factor on the attn_v block scales: large enough and the value projection
+    # leaves the fp16 range, so the KV cache holds exponent-31 halves
+    value_gain: float = 1.0
 
     @property
     def conv_size(self) -> int:
@@ -82,6 +85,13 @@ CONFIGS: Dict[str, Qwen35Config] = {
                                       kv_heads=2, head_size=64, value_size=64, rope_dim=16,
                                       gdn_key_heads=2, gdn_value_heads=4, gdn_state=64,
                                       gdn_inner=256, conv_kernel=4, vocab=4096, embedding_q8=True),
+    # The tiny model with value projections of |v| up to ~2e5: fp16 KV appends
+    # of exponent-31 halves (read back as +-huge by gguf_fp16_to_real), the
+    # attention kernels' flagged path.
+    "qwen35-tiny-hugev": Qwen35Config("qwen35-tiny-hugev", hidden=256, layers=4, ffn=512, heads=4,
+                                      kv_heads=2, head_size=64, value_size=64, rope_dim=16,
+                                      gdn_key_heads=2, gdn_value_heads=4, gdn_state=64,
+                                      gdn_inner=256, conv_kernel=4, vocab=4096, value_gain=1000.0),
     # Mid-size: every 0.8B layer shape except the vocabulary and depth.
     "qwen35-0.8b-short": Qwen35Config("qwen35-0.8b-short", hidden=1024, layers=4, ffn=3584,
                                       heads=8, kv_heads=2, head_size=256, value_size=256,
@@ -169,7 +179,11 @@ def tensor_payload(cfg: Qwen35Config, seed: int, name: str, shape, ggml_type) ->
     rng = _rng(seed, name)
     n = int(np.prod(shape))
     if ggml_type == gguf.GGML_TYPE_Q8_0:
-        return q8_blocks(rng, int(np.prod(shape[1:])), shape[0])
+        blocks = q8_blocks(rng, int(np.prod(shape[1:])), shape[0])
+        if cfg.value_gain != 1.0 and name.endswith("attn_v.weight"):
+            sc = blocks[..., 0:2].copy().view(np.float16).astype(np.float32) * np.float32(cfg.value_gain)
+            blocks[..., 0:2] = np.clip(sc, -60000.0, 60000.0).astype(np.float16).view(np.uint8)
+        return blocks
     if ggml_type == gguf.GGML_TYPE_F16:
         return _normal(rng, n, 0.02, np.float16)
     base = name.split(".", 2)[-1]

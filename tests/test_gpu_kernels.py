@@ -318,6 +318,75 @@ def test_attention_core(ctx, oracle, L, exact_max, skew):
         w.free()
 
 
+def same_values(a, b):
+    """Bit-identical, NaNs only at the same places (their payloads are not part
+    of the reference's arithmetic)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+@pytest.mark.parametrize("L,wide,big", [(70, 0, True), (1024, 0, True), (70, 1, False), (600, 1, False),
+                                        (4096, 1, False), (600, 1, True), (4096, 1, True)])
+def test_attention_output_kernels(ctx, oracle, L, wide, big):
+    """The exact attention output of one sequence through the per-slice kernel
+    (wide 0, the decode's) or the batches' wide kernel (wide 1, selected for one
+    sequence by FORTAI_HIP_ATTENTION_WIDE), against the reference step.
+    big: exponent-31 halves in value dims 0..19 of kv head 0 at every 7th
+    position, which the reference reads as +-huge (gguf_fp16_to_real,
+    fortai_gguf_runtime.f90:770-788): those dims of that kv head's heads sum
+    terms of ~1e36 (or overflow), and every output, huge or not, must be
+    bit-identical through the kernels' flagged instances."""
+    rng = np.random.default_rng(L + 7 * wide + big)
+    heads, kvh, head, H = 8, 2, 256, 1024
+    mk = lambda rows, width: B.Q8Weights(ctx, synth.q8_blocks(rng, rows, width), rows, width)
+    ws = [mk(heads * 2 * head, H), mk(kvh * head, H), mk(kvh * head, H), mk(H, heads * head)]
+    qn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
+    kn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
+    maxc = max(L, 64)
+    saved = os.environ.get("FORTAI_HIP_ATTENTION_WIDE")
+    os.environ["FORTAI_HIP_ATTENTION_WIDE"] = str(wide)  # read when the layer is created
+    try:
+        A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
+    finally:
+        if saved is None:
+            os.environ.pop("FORTAI_HIP_ATTENTION_WIDE", None)
+        else:
+            os.environ["FORTAI_HIP_ATTENTION_WIDE"] = saved
+    kc = np.zeros(maxc * kvh * head, np.uint16)
+    vc = np.zeros(maxc * kvh * head, np.uint16)
+    n = (L - 1) * kvh * head
+    kc[:n] = rng.standard_normal(n).astype(np.float16).view(np.uint16)
+    vc[:n] = rng.standard_normal(n).astype(np.float16).view(np.uint16)
+    if big:
+        rows = np.arange(0, L - 1, 7)
+        idx = (rows[:, None] * kvh * head + np.arange(20)[None, :]).ravel()
+        vc[idx] = (vc[idx] & 0x83ff) | 0x7c00  # exponent 31, the sign and fraction kept
+    A.set_cache(kc, vc, maxc)
+    q = rng.standard_normal(heads * 2 * head).astype(np.float32)
+    k = rng.standard_normal(kvh * head).astype(np.float32)
+    v = rng.standard_normal(kvh * head).astype(np.float32)
+    ctx.set_position(L - 1)
+    dq, dk, dv, do = ctx.upload_array(q), ctx.upload_array(k), ctx.upload_array(v), ctx.alloc(heads * head * 4)
+    try:
+        ctx.call("fortai_hip_qwen35_attention_core_device", A.h, dq.ptr, dk.ptr, dv.ptr, do.ptr)
+        got = do.download(np.float32)
+        want = np.zeros(heads * head, np.float32)
+        scores = np.zeros(maxc, np.float32)
+        oracle.attention_core_step(q.copy(), k.copy(), v, qn, kn, kc, vc, heads, kvh, head, head, L - 1, 64,
+                                   np.float32(1e7), np.float32(1e-6), scores, want)
+        if big:  # those dims carry the huge terms (|out| ~ 1e36, or beyond: inf / NaN)
+            huge = ~np.isfinite(want) | (np.abs(want) > 1e30)
+            assert 0 < huge.sum() < heads * head // 2
+        assert same_values(got, want), f"{int(np.sum(got.view(np.uint32) != want.view(np.uint32)))} outputs differ"
+    finally:
+        for b_ in (dq, dk, dv, do):
+            b_.free()
+        A.free()
+        for w in ws:
+            w.free()
+
+
 def test_f16_lm_head_and_argmax(ctx, oracle):
     rng = np.random.default_rng(3)
     rows, width = 248320, 1024

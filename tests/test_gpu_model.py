@@ -110,6 +110,54 @@ def test_q8_embedding_model_trace(oracle, tiny_q8emb_path):
         m.close()
 
 
+def same_values(got, want):
+    """Bit-identical, NaNs only at the same places (their payloads are not
+    part of the reference's arithmetic)."""
+    a, b = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+def test_exponent31_value_cache_matches_oracle(oracle, tmp_path):
+    """attn_v scaled so that about one value in ten leaves the fp16 range: the
+    KV append (ties-away fp16 with overflow) must store the reference's
+    exponent-31 halves bit for bit.  The reference reads them back as +-huge()
+    (gguf_fp16_to_real, fortai_gguf_runtime.f90:770-788), which the o
+    projection turns into inf and NaN, so from the first attention layer on
+    every logit is NaN in both: this checks the caches, that the NaNs are the
+    reference's (no finite value where it has NaN) and the greedy trace of
+    first indices.  The flagged attention arithmetic itself is compared
+    bit for bit in test_gpu_kernels.py::test_attention_output_kernels."""
+    from fortai_amd import synth
+    from oracle.oracle import OracleModel
+    path = str(tmp_path / "hugev.gguf")
+    synth.write_model(path, synth.CONFIGS["qwen35-tiny-hugev"])
+    ref = OracleModel(oracle, path, 64)
+    m = open_decoder(path, 64)
+    try:
+        token = 5
+        for pos in range(20):
+            got = m.forward(token, pos).copy()
+            want = ref.forward(token, pos)
+            assert same_values(got, want), f"step {pos}: logits differ"
+            token = int(np.argmax(want))
+            assert int(np.argmax(got)) == token, f"greedy token differs at step {pos}"
+        flagged = 0
+        for i, layer in enumerate(m.attention):
+            if layer is None:
+                continue
+            k, v = layer.cache(20)
+            assert np.array_equal(v, ref.vcache(i)[:v.size]), f"V cache of layer {i}"
+            flagged += int(np.count_nonzero((v & 0x7c00) == 0x7c00))
+        assert flagged > 0, "the V caches hold exponent-31 halves"
+        print(f"exponent-31 halves in the V caches: {flagged}", flush=True)
+        m.reset()
+        ref.reset()
+        assert m.generate(5, 48).tolist() == ref.greedy(5, 48)
+    finally:
+        m.close()
+
+
 @pytest.fixture(scope="module")
 def short_path(tmp_path_factory):
     """Every 0.8B layer shape (hidden 1024, FFN 3584, GDN 16x128, attention
