@@ -787,6 +787,38 @@ def trace_summary(directory: str, steps: int = 64) -> None:
     print(f"\nkernel busy time per step: {busy:.1f} us over {len(sel) / steps:.0f} dispatches")
 
 
+def prefill_summary(directory: str) -> None:
+    """Per-kernel time per prompt prefill of a rocprofv3 --kernel-trace CSV of
+    one or more batch prefills (each starts with one embedding kernel); the
+    upload-time kernels (weight repack, fp16 table scan, runtime copies and
+    fills) are left out."""
+    import csv
+    import glob
+    from collections import defaultdict
+    paths = glob.glob(os.path.join(directory, "**", "*kernel_trace.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no kernel_trace.csv under {directory}")
+    agg = defaultdict(lambda: [0, 0])
+    with open(paths[0]) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if any(s in name for s in ("q8_repack_kernel", "count_nonfinite_halves_kernel", "__amd_rocclr")):
+                continue
+            key = name.replace("(anonymous namespace)::", "").replace("fortai_hip::", "").replace("void ", "")
+            key = key.replace("(Prologue)", "P").replace("(Epilogue)", "E").split("(")[0]
+            agg[key][0] += 1
+            agg[key][1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    n = sum(c for k, (c, _) in agg.items() if "embedding" in k)
+    if n == 0:
+        raise SystemExit("no prefill (embedding kernel) in the trace")
+    busy = sum(v[1] for v in agg.values()) / n / 1e3
+    print(f"| kernel | calls/prefill | avg us | us/prefill | % |")
+    print(f"|---|---:|---:|---:|---:|")
+    for k, (c, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        print(f"| `{k}` | {c / n:.0f} | {t / c / 1e3:.1f} | {t / n / 1e3:.0f} | {100 * t / n / 1e3 / busy:.1f} |")
+    print(f"\nkernel busy time per prefill: {busy / 1e3:.1f} ms over {n} prefills")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -820,7 +852,13 @@ def main() -> int:
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="print the per-kernel table of the last --steps decode steps of a rocprofv3 "
                          "--kernel-trace CSV under DIR, then exit")
+    ap.add_argument("--prefill-summary", metavar="DIR",
+                    help="print the per-kernel table per prompt prefill of a rocprofv3 --kernel-trace CSV under DIR, "
+                         "then exit")
     args = ap.parse_args()
+    if args.prefill_summary:
+        prefill_summary(args.prefill_summary)
+        return 0
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps)
         return 0
