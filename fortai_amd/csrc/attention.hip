@@ -156,11 +156,14 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     FORTAI_ATT_MARK(11);
 }
 
-// e_p = expf(s_p - m) of one kSeg-position segment of one head, stored for
-// the output kernels, and the segment's Z candidate table (attention_exact.h,
+// e_p = expf(s_p - m) of kSeg-position segments of one head, stored for the
+// output kernels, and each segment's Z candidate table (attention_exact.h,
 // resolve_z): thread c runs the segment's left-to-right chain from candidate
-// starting sum c.  grid (heads x z_segments(max_context), batch), segments
-// holding positions dispatched first.
+// starting sum c.  grid (heads x G, batch): workgroup (k0, h) takes segments
+// k0, k0 + G, ... of head h (G = z_segments(max_context) for one sequence, so
+// one segment each; at most 8 for a batch, so that at a short position in a
+// long cache few workgroups load the scores and exit idle), segments holding
+// positions dispatched first.
 __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const AttentionParams p_batch) {
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     __shared__ __align__(16) float e_seg[ea::kSeg];
@@ -168,7 +171,8 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     __shared__ float fred[ea::kWaves];
     static_assert(ea::kZCand == ea::kThreads && ea::kSeg == ea::kThreads, "one candidate and one position per thread");
     const int pos = *p.position;
-    const int k = div(static_cast<int>(blockIdx.x), p.div_heads), h = static_cast<int>(blockIdx.x) - k * p.heads;
+    const int k0 = div(static_cast<int>(blockIdx.x), p.div_heads), h = static_cast<int>(blockIdx.x) - k0 * p.heads;
+    const int G = div(static_cast<int>(gridDim.x), p.div_heads);
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
     // up to kHeld * 256 positions the scores are loaded in the position's
@@ -185,9 +189,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     if (pos < 0 || pos >= p.max_context) return;
     const int n = pos + 1;
     if (n > p.exact_max) return;  // the split-K kernels cover this position
-    const int p0 = k * ea::kSeg;
-    if (p0 >= n) return;
-    const int cnt = min(ea::kSeg, n - p0);
+    if (k0 * ea::kSeg >= n) return;
     // m = max over every score (any order gives the same value)
     constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
     float m = kLowest;
@@ -202,6 +204,10 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     if (lane == 0) fred[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    for (int k = k0; k * ea::kSeg < n; k += G) {
+    if (k != k0) __syncthreads();  // the previous segment's chains have read e_seg and dred
+    const int p0 = k * ea::kSeg;
+    const int cnt = min(ea::kSeg, n - p0);
     // the segment's own e values, exactly as the reference computes them
     const float e = tid < cnt ? expf_libm(sc[p0 + tid] - m) : -0.0f;  // -0 leaves a sum unchanged
     e_seg[tid] = e;
@@ -254,6 +260,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     tab[tid] = acc;
     tab[ea::kZNext + tid] = last ? acc : __int_as_float(ea::z_index(acc, centre_next));
     if (tid == 0) tab[ea::kZCentre] = __uint_as_float(centre);
+    }
 }
 
 // Z of head h: the walk words of the candidate tables into LDS (up to
@@ -771,6 +778,13 @@ size_t attention_scores_floats(int heads, int max_context) { return workspace_fl
 
 int attention_split_chunks(int max_context) { return (max_context + kChunk - 1) / kChunk; }
 
+// workgroups per head of attention_softmax_kernel: one per segment for a
+// single sequence, at most 8 (each looping over segments) for a batch
+int softmax_groups(int positions, int batch) {
+    const int segs = ea::z_segments(positions);
+    return batch > 1 && segs > 8 ? 8 : segs;
+}
+
 hipError_t launch_attention(const AttentionParams &params, hipStream_t stream, int batch) {
     if (batch < 1) return hipErrorInvalidValue;
     const int group = params.kv_heads > 0 ? params.heads / params.kv_heads : 0;
@@ -793,7 +807,7 @@ hipError_t launch_attention(const AttentionParams &params, hipStream_t stream, i
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (exact_positions > 0) {
-        hipLaunchKernelGGL(attention_softmax_kernel, dim3(p.heads * ea::z_segments(exact_positions), batch),
+        hipLaunchKernelGGL(attention_softmax_kernel, dim3(p.heads * softmax_groups(exact_positions, batch), batch),
             dim3(ea::kThreads), 0, stream, p);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -806,14 +820,14 @@ hipError_t launch_attention(const AttentionParams &params, hipStream_t stream, i
         e = hipGetLastError();
         note_launch("attention_scores_kernel grid %dx%d + attention_softmax_kernel grid %dx%d + "
             "attention_output_wide_kernel grid %dx%d", p.kv_heads * nblk_max, batch,
-            p.heads * ea::z_segments(exact_positions), batch, wgrid, batch);
+            p.heads * softmax_groups(exact_positions, batch), batch, wgrid, batch);
     } else {
         hipLaunchKernelGGL(attention_output_kernel, dim3(p.heads * (p.value / ea::kDims), batch), dim3(ea::kThreads),
             output_lds_bytes(exact_positions), stream, p);
         e = hipGetLastError();
         note_launch("attention_scores_kernel grid %dx%d + attention_softmax_kernel grid %dx%d + "
             "attention_output_kernel grid %dx%d", p.kv_heads * nblk_max, batch,
-            p.heads * ea::z_segments(exact_positions), batch, p.heads * (p.value / ea::kDims), batch);
+            p.heads * softmax_groups(exact_positions, batch), batch, p.heads * (p.value / ea::kDims), batch);
     }
     if (e != hipSuccess || p.max_context <= p.exact_max) return e;
     // long contexts: the split-K pair (each kernel picks its regime from the device position)
