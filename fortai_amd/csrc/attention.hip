@@ -379,7 +379,7 @@ size_t output_lds_bytes(int positions) {
 // softmax and P.V with its summation orders, fortai_qwen35_cpu.f90:1016-1031)
 // with one workgroup per (head, 64 value dims, sequence) instead of one per
 // (head, 8 value dims): Z from the candidate tables (head_z), then lane d of
-// one wave runs the P.V chain of value dim d0 + d over the positions in order,
+// wave 0 runs the P.V chain of value dim d0 + d over the positions in order,
 // out_d = fl(w_0 v_0,d) + fl(w_1 v_1,d) + ... with w_p = e_p / Z.  A batch has
 // many (head, sequence) pairs, so this fills the chip with 1/8 as many
 // workgroups, each chain step using all 64 lanes; a single sequence keeps the
@@ -417,11 +417,6 @@ __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int
     const uint16_t *vb = p.vcache + static_cast<size_t>(kvh) * VD + d0;
     const size_t vs = static_cast<size_t>(NKV) * VD;
     const int tiles = (n + kWideTile - 1) / kWideTile;
-    // the wave that runs the chain: a hash of the workgroup, so that the
-    // chains of the workgroups sharing a CU spread over its four SIMDs (wave
-    // w of every workgroup lands on the same SIMD)
-    const uint32_t hw = (blockIdx.x * 2654435761u) ^ (blockIdx.y * 40503u);
-    const int cw = static_cast<int>((hw >> 13) & 3u);
     const float *ev = evals_of(p) + static_cast<size_t>(h) * p.max_context;
     // this thread's block: positions pg * 8 .. + 7 of a tile, dims pc * 8 .. + 7
     const int pc = tid & 7, pg = tid >> 3;
@@ -522,21 +517,18 @@ __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int
     for (int t = 0; t < tiles; t += 2) {
         stash(ra, ea_);
         __syncthreads();
-        if (t == 0) FORTAI_ATTW_MARK(6);
         if (t + 2 < tiles) fetch(t + 2, ra, ea_);
-        if (t == 0) FORTAI_ATTW_MARK(7);
-        if (wave == cw) acc = chain(t, acc);
+        if (wave == 0) acc = chain(t, acc);
         __syncthreads();
-        if (t == 0) FORTAI_ATTW_MARK(4);
         if (t + 1 >= tiles) break;
         stash(rb, eb_);
         __syncthreads();
         if (t + 3 < tiles) fetch(t + 3, rb, eb_);
-        if (wave == cw) acc = chain(t + 1, acc);
+        if (wave == 0) acc = chain(t + 1, acc);
         __syncthreads();
     }
     FORTAI_ATTW_MARK(5);
-    if (wave == cw && d < VD) {
+    if (wave == 0 && d < VD) {
         const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d];
         p.out[static_cast<size_t>(h) * VD + d] = acc * sigmoid_ref(gate);
     }
