@@ -77,3 +77,53 @@ def test_full_model_4096_step_trace(full_model_path):
         assert first_diff is None, f"trace differs from step {first_diff}: {trace[first_diff]} vs {tokens[first_diff]}"
     finally:
         m.close()
+
+
+def _golden_4096():
+    with np.load(GOLDEN_4096) as z:
+        tokens = z["tokens"].astype(np.int64)
+    with open(GOLDEN_4096.replace(".npz", ".json")) as f:
+        meta = json.load(f)
+    return tokens, meta
+
+
+@pytest.mark.skipif(not os.path.exists(GOLDEN_4096), reason="the 4096-step golden is not generated")
+def test_batch_decoder_4096_step_trace(full_model_path):
+    """The batched decoder (batch matvecs, the wide attention kernel) over the
+    whole 4096-token context: two sequences from the reference's start token
+    each reproduce the compiled reference's trace."""
+    from fortai_amd.qwen35 import Qwen35Hip
+    tokens, meta = _golden_4096()
+    m = Qwen35Hip(full_model_path, max_context=meta["context"], batch=2)
+    try:
+        m.batch.reset()
+        trace = m.batch.generate([meta["token"]] * 2, [0, 0], meta["steps"])
+        for s in range(2):
+            first_diff = next((i for i in range(len(tokens)) if trace[s][i] != tokens[i]), None)
+            assert first_diff is None, f"sequence {s} differs from step {first_diff}"
+    finally:
+        m.close()
+
+
+@pytest.mark.skipif(not os.path.exists(GOLDEN_4096), reason="the 4096-step golden is not generated")
+def test_prefill_then_batch_decode_4096_step_trace(full_model_path):
+    """The exact prompt prefill at the 0.8B shape: the first 512 tokens of the
+    reference's trace as the prompt (the start token, then its greedy
+    choices), whose next token must be the reference's 512th choice, then
+    batched decoding to the end of the 4096-token context, token for token."""
+    from fortai_amd.qwen35 import Qwen35Hip
+    tokens, meta = _golden_4096()
+    T = 512
+    prompt = np.concatenate([[meta["token"]], tokens[:T - 1]]).astype(np.int64)
+    m = Qwen35Hip(full_model_path, max_context=meta["context"], batch=2)
+    try:
+        m.batch.reset()
+        nxt, _ = m.batch.prefill(np.stack([prompt, prompt]))
+        assert nxt.tolist() == [int(tokens[T - 1])] * 2, "the prefill's next token"
+        trace = m.batch.generate(nxt, [T, T], meta["steps"] - T)
+        for s in range(2):
+            want = tokens[T:]
+            first_diff = next((i for i in range(len(want)) if trace[s][i] != want[i]), None)
+            assert first_diff is None, f"sequence {s} differs from step {T + first_diff}"
+    finally:
+        m.close()
