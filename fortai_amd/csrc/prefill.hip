@@ -581,21 +581,21 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_exact16_kernel(const
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int d = 0; d < HEAD; d += 8) {
             const uint4 k8 = *reinterpret_cast<const uint4 *>(kv + ((d / 8) * kXKeys + lane) * 8);
+            const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+            float qv[4][8];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float4 qa = *reinterpret_cast<const float4 *>(qs + (wave + 4 * r) * HEAD + d);
                 const float4 qc = *reinterpret_cast<const float4 *>(qs + (wave + 4 * r) * HEAD + d + 4);
-                float a = acc[r];
-                a = a + times_half<FINITE>(k8.x, false, qa.x);
-                a = a + times_half<FINITE>(k8.x, true, qa.y);
-                a = a + times_half<FINITE>(k8.y, false, qa.z);
-                a = a + times_half<FINITE>(k8.y, true, qa.w);
-                a = a + times_half<FINITE>(k8.z, false, qc.x);
-                a = a + times_half<FINITE>(k8.z, true, qc.y);
-                a = a + times_half<FINITE>(k8.w, false, qc.z);
-                a = a + times_half<FINITE>(k8.w, true, qc.w);
-                acc[r] = a;
+                qv[r][0] = qa.x; qv[r][1] = qa.y; qv[r][2] = qa.z; qv[r][3] = qa.w;
+                qv[r][4] = qc.x; qv[r][5] = qc.y; qv[r][6] = qc.z; qv[r][7] = qc.w;
             }
+            // the four queries' chains interleaved (each chain's order unchanged),
+            // so consecutive adds do not wait on each other
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] = acc[r] + times_half<FINITE>(kw[k >> 1], (k & 1) != 0, qv[r][k]);
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) sc[(wave + 4 * r) * kcap + t * kXKeys + lane] = acc[r] / sqrt_head;
@@ -655,16 +655,19 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_exact16_kernel(const
             uint32_t vh[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) vh[u] = kv[(jj + u) * HEAD + d];
+            float4 w4[kQPT];
 #pragma unroll
-            for (int r = 0; r < kQPT; ++r) {
-                const float4 w4 = *reinterpret_cast<const float4 *>(sc + (qd + kQS * r) * kcap + t * kXKeys + jj);
-                float a = acc[r];
-                a = a + times_half<FINITE>(vh[0], false, w4.x);
-                a = a + times_half<FINITE>(vh[1], false, w4.y);
-                a = a + times_half<FINITE>(vh[2], false, w4.z);
-                a = a + times_half<FINITE>(vh[3], false, w4.w);
-                acc[r] = a;
-            }
+            for (int r = 0; r < kQPT; ++r)
+                w4[r] = *reinterpret_cast<const float4 *>(sc + (qd + kQS * r) * kcap + t * kXKeys + jj);
+            // the queries' chains interleaved key by key (each chain's order unchanged)
+#pragma unroll
+            for (int r = 0; r < kQPT; ++r) acc[r] = acc[r] + times_half<FINITE>(vh[0], false, w4[r].x);
+#pragma unroll
+            for (int r = 0; r < kQPT; ++r) acc[r] = acc[r] + times_half<FINITE>(vh[1], false, w4[r].y);
+#pragma unroll
+            for (int r = 0; r < kQPT; ++r) acc[r] = acc[r] + times_half<FINITE>(vh[2], false, w4[r].z);
+#pragma unroll
+            for (int r = 0; r < kQPT; ++r) acc[r] = acc[r] + times_half<FINITE>(vh[3], false, w4[r].w);
         }
     }
 #pragma unroll
