@@ -390,3 +390,29 @@ def test_expf_restatement_matches_host_expf(oracle):
     restatement without the fused r = x * 32/ln2 - k gets wrong."""
     assert oracle.lib.orc_expf_restated_mismatches(0x80000000, 0xC2CF0001) == 0
     assert oracle.lib.orc_expf_restated_mismatches(0x00000000, 0x42B00001) == 0
+
+
+def test_full_trace_goldens_agree():
+    """The two compiled-reference goldens of the 0.8B model from token 9419,
+    written by separate runs (128 steps and the whole 4096-token context),
+    agree on their common steps; the 4096-step file is self-consistent (its
+    last 64 steps' top-8 lists start at the traced token, in descending order,
+    and the recorded top-2 margins are non-negative)."""
+    import json
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    with np.load(os.path.join(golden, "qwen35_0.8b_trace.npz")) as z:
+        short = z["tokens"].astype(np.int64)
+    with np.load(os.path.join(golden, "qwen35_0.8b_trace_4096.npz")) as z:
+        tokens, margin = z["tokens"].astype(np.int64), z["margin"]
+        top_i, top_v = z["last_top_index"], z["last_top_value"]
+    with open(os.path.join(golden, "qwen35_0.8b_trace_4096.json")) as f:
+        meta = json.load(f)
+    with open(os.path.join(golden, "qwen35_0.8b_trace.json")) as f:
+        meta_short = json.load(f)
+    assert meta["token"] == meta_short["token"] and meta["model"] == "qwen35-0.8b"
+    assert tokens.shape == (meta["steps"],) and meta["steps"] == meta["context"] == 4096
+    assert np.array_equal(tokens[:len(short)], short)
+    assert np.all(tokens >= 0) and np.all(tokens < 248320)
+    assert np.all(margin >= 0) and float(margin.min()) == meta["min_top2_margin"]
+    assert np.array_equal(top_i[:, 0], tokens[-len(top_i):])
+    assert np.all(np.diff(top_v, axis=1) <= 0)
