@@ -344,18 +344,25 @@ __device__ __forceinline__ float4 sdot4x4_f(uint4 q, uint4 a) {
     return r;
 }
 
+// -0.0f that the compiler cannot see as a constant (so that an fma with it is
+// not folded into a multiply); no inputs and no side effects, so it is
+// computed once and hoisted
+__device__ __forceinline__ float opaque_negzero() {
+    float z;
+    asm("v_mov_b32 %0, 0x80000000" : "=v"(z));
+    return z;
+}
+
 // fl(f32(h) * a) for the low (HI = false) or high half h of a packed pair of
-// fp16 bits: v_fma_mix_f32 widens the fp16 operand exactly, multiplies and
-// adds -0 (which leaves every product, zero or not, as it is) with one
-// rounding -- the value of the convert-then-multiply, in one instruction.
+// fp16 bits: fma(f32(h), a, -0) widens exactly, multiplies and adds -0 (which
+// leaves every product, zero or not, as it is) with one rounding -- the value
+// of the convert-then-multiply.  The compiler selects v_fma_mix_f32 for it
+// (one instruction) and, unlike for inline asm, knows its latencies.
 template <bool HI>
 __device__ __forceinline__ float half_times(uint32_t h2, float a) {
-    float r;
-    if constexpr (HI)
-        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(a), "v"(-0.0f));
-    else
-        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(a), "v"(-0.0f));
-    return r;
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    const half2_t v = __builtin_bit_cast(half2_t, h2);
+    return __builtin_fmaf(static_cast<float>(HI ? v.y : v.x), a, opaque_negzero());
 }
 
 __device__ __forceinline__ float dot_chunk(uint4 q, uint2 sc, uint4 a, float4 as, float acc) {
