@@ -41,7 +41,11 @@ def run_single(m, token, position, steps):
     return np.stack(logits), toks
 
 
+# batch 1, 5 and 7: the kernels' sequence slots past the batch (clamped,
+# never written) and the ring kernels' partial sequence blocks
 @pytest.mark.parametrize("name,batch,steps", [("qwen35-tiny", 3, 12), ("qwen35-tiny-q8emb", 8, 8),
+                                              ("qwen35-tiny", 1, 6), ("qwen35-0.8b-short", 5, 5),
+                                              ("qwen35-4b-short", 7, 4),
                                               ("qwen35-0.8b-short", 8, 6), ("qwen35-4b-short", 8, 4)])
 def test_batch_matches_single_sequence(model_paths, name, batch, steps):
     m = Qwen35Hip(model_paths[name], max_context=64, batch=batch)
