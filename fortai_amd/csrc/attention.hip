@@ -390,14 +390,19 @@ size_t output_lds_bytes(int positions) {
 // 16-byte pieces), transposes them in registers and stores one 16-byte row
 // of 8 positions per dim, so the tile is [dim][position] and a chain lane
 // reads 8 positions of its dim with one 16-byte LDS read (and w_p of the tile,
-// divided when the tile is stored, with two).  The Z walk words use the tile's
-// LDS before the first tile is stored; nothing is sized by the context, so
-// four workgroups fit a CU.
+// divided when the tile is stored, with two).  Row R (dim R) keeps its group g
+// of 8 positions at column g + 2 (R / 16): with a row pitch of 49 16-byte bank
+// groups (1 mod 16), the 16 lanes of a store pass (8 rows 8 apart, two column
+// groups) and of a read pass (16 consecutive rows, one group) all fall on
+// different banks.  The Z walk words use the tile's LDS before the first tile
+// is stored; nothing is sized by the context.
 constexpr int kWideTile = 256;                   // positions per value tile
 constexpr int kWideDims = 64;                    // value dims per workgroup
-constexpr int kWidePitchT = kWideTile + 8;       // halves per LDS row of one dim (16-byte rows, no bank conflicts)
+constexpr int kWidePitchT = 392;                 // halves per LDS row: 32 + 6 column groups, 49 x 16 bytes
 constexpr int kWideMaxPositions = 8192;
 static_assert(kWideTile / 8 * (kWideDims / 8) == ea::kThreads, "one 8 x 8 block of (position, dim) per thread");
+static_assert(kWidePitchT >= (kWideTile / 8 + 2 * (kWideDims / 16 - 1)) * 8 && kWidePitchT % 8 == 0 &&
+    (kWidePitchT / 8) % 16 == 1, "every shifted column in the row; 16-byte rows one bank group apart");
 static_assert(kWideDims * kWidePitchT * 2 >= kZLdsSegments * ea::kZCand * 4, "the Z walk words fit the tile's LDS");
 
 // dynamic LDS of attention_output_wide_kernel: the transposed tile, then w of the tile
@@ -451,12 +456,13 @@ __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int
             row.y = pick_halves(w32[2 * 4 + m], w32[3 * 4 + m], hi);
             row.z = pick_halves(w32[4 * 4 + m], w32[5 * 4 + m], hi);
             row.w = pick_halves(w32[6 * 4 + m], w32[7 * 4 + m], hi);
-            *reinterpret_cast<uint4 *>(vt + (pc * 8 + k) * kWidePitchT + pg * 8) = row;
+            *reinterpret_cast<uint4 *>(vt + (pc * 8 + k) * kWidePitchT + (pg + 2 * (pc >> 1)) * 8) = row;
         }
         wt[tid] = e / z;
     };
     const int d = d0 + lane;
-    const uint16_t *myrow = vt + lane * kWidePitchT;  // lanes past VD read a row of the tile they do not write
+    // this lane's row from its shifted column 0 (lanes past VD read a row they do not write)
+    const uint16_t *myrow = vt + lane * kWidePitchT + 2 * (lane >> 4) * 8;
     // the chain of one tile: groups of 8 positions from a ring of three
     // register sets, each group's LDS reads issued two groups before its adds
     struct Grp {
