@@ -310,7 +310,9 @@ __global__ __launch_bounds__(kXThreads, 2) void q8_mmq_exact_kernel(Q8Matrix w, 
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int p = tid + k * kXThreads;  // 0..511
-            const int j = p >> 7, t = (p >> 1) & 63, hh = p & 1;
+            // a wave takes one (block, half) and 64 tokens, lane = token, so
+            // that its LDS stores (rows 18 dwords apart) meet no bank twice
+            const int j = p >> 7, hh = (p >> 6) & 1, t = p & 63;
             ra[k] = *reinterpret_cast<const u32x4_t *>(xq + static_cast<size_t>(4 * c + j) * bstride +
                 static_cast<size_t>(t0 + t) * 32 + hh * 16);
             const int g = min((r0 >> 3) + (p >> 6), g_last);  // clamped; rows past the end are not stored
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(kXThreads, 2) void q8_mmq_exact_kernel(Q8Matrix w, 
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int p = tid + k * kXThreads;
-            const int j = p >> 7, t = (p >> 1) & 63, hh = p & 1;
+            const int j = p >> 7, hh = (p >> 6) & 1, t = p & 63;
             const uint32_t wd[4] = {ra[k].x, ra[k].y, ra[k].z, ra[k].w};
 #pragma unroll
             for (int m = 0; m < 4; ++m)
