@@ -64,7 +64,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     __shared__ __align__(16) uint16_t ktile[ea::kPosBlock][kMaxHead + 8];
     __shared__ int overflow;
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
-    FORTAI_ATT_MARK(8);
+    FORTAI_ATT_MARK(16);
     const int pos = *p.position;
     if (pos < 0 || pos >= p.max_context) return;  // never index past the cache
     const int positions = pos + 1, nblk_max = (p.max_context + ea::kPosBlock - 1) / ea::kPosBlock;
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     if (tid < HD) kn[tid] = knv;
     if (tid < half) rs[tid] = rsv;
     if (tid == 0) overflow = 0;
-    FORTAI_ATT_MARK(9);
+    FORTAI_ATT_MARK(17);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int li = tid + i * ea::kThreads;
@@ -123,12 +123,13 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
         if (j < n) *reinterpret_cast<v4u *>(&ktile[j][sg * 8]) = kr[i];
     }
     __syncthreads();
+    FORTAI_ATT_MARK(18);
     for (int sl = wave; sl < group + (owns_new ? 1 : 0); sl += ea::kThreads / 64) {
         if (sl < group) ea::norm_rope_regs(qh + sl * HD, HD, qwr, p.eps, rs, p.rope_dim, lane);
         else ea::norm_rope_regs(kn, HD, kwr, p.eps, rs, p.rope_dim, lane);
     }
     __syncthreads();
-    FORTAI_ATT_MARK(10);
+    FORTAI_ATT_MARK(19);
     if (owns_new) {
         // append at pos (fortai_qwen35_cpu.f90:1594-1601)
         if (tid < HD) {
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
                                 : ea::score<false>(qh + gi * HD, &ktile[j][0], HD, sqrt_head);
         p.partial[static_cast<size_t>(kvh * group + gi) * p.max_context + p0 + j] = sc;
     }
-    FORTAI_ATT_MARK(11);
+    FORTAI_ATT_MARK(20);
 }
 
 // e_p = expf(s_p - m) of kSeg-position segments of one head, stored for the
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     } else {
         for (int i = tid; i < n; i += ea::kThreads) m = fmaxf(m, sc[i]);
     }
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = wave_max(m);
     if (lane == 0) fred[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
@@ -232,10 +233,8 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
             est_next += t;
         }
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-        est += __shfl_xor(est, o);
-        est_next += __shfl_xor(est_next, o);
-    }
+    est = wave_sum(est);
+    est_next = wave_sum(est_next);
     if (lane == 0) {
         dred[wave] = est;
         dred[ea::kWaves + wave] = est_next;
@@ -570,7 +569,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_wide_kernel(con
 // scores are the scores kernel's (the reference's per-position dots).
 
 __device__ __forceinline__ float block_max256(float v, float *red) {
-    for (int k = 32; k >= 1; k >>= 1) v = fmaxf(v, __shfl_xor(v, k));
+    v = wave_max(v);
     const int tid = static_cast<int>(threadIdx.x);
     __syncthreads();
     if ((tid & 63) == 0) red[tid >> 6] = v;
@@ -579,7 +578,7 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
 }
 
 __device__ __forceinline__ float block_sum256(float v, float *red) {
-    for (int k = 32; k >= 1; k >>= 1) v += __shfl_xor(v, k);
+    v = wave_sum(v);
     const int tid = static_cast<int>(threadIdx.x);
     __syncthreads();
     if ((tid & 63) == 0) red[tid >> 6] = v;
@@ -628,7 +627,7 @@ __device__ __forceinline__ void split_chunk(const AttentionParams &p, int kvh, i
 #pragma unroll
     for (int g = 0; g < kMaxGroup; ++g) {
         m[g] = tid < n ? sc[g] : -__builtin_inff();
-        for (int k = 32; k >= 1; k >>= 1) m[g] = fmaxf(m[g], __shfl_xor(m[g], k));
+        m[g] = wave_max(m[g]);
     }
     if ((tid & 63) == 0)
 #pragma unroll
@@ -640,7 +639,7 @@ __device__ __forceinline__ void split_chunk(const AttentionParams &p, int kvh, i
         const float ev = (g < group && tid < n) ? expf_libm(sc[g] - m[g]) : 0.0f;
         if (tid < kChunk) L.e[g][tid] = ev;
         z[g] = ev;
-        for (int k = 32; k >= 1; k >>= 1) z[g] += __shfl_xor(z[g], k);
+        z[g] = wave_sum(z[g]);
     }
     __syncthreads();  // every wave has read red4
     if ((tid & 63) == 0)

@@ -74,31 +74,22 @@ __device__ __forceinline__ void norm_rope_regs(float *v, int head, const float (
 }
 
 // One position's score: the sequential dot of fortai_qwen35_cpu.f90:1009-1014.
-// q in LDS (broadcast reads), the key row in LDS, 8 halves per read.
+// q in LDS (broadcast reads), the key row in LDS, 8 halves per read.  The
+// reads run two groups of 8 ahead of the chain, so that their LDS latency
+// overlaps the adds instead of stalling the chain every 8 elements.
 template <bool FINITE>
-__device__ __forceinline__ float score(const float *q, const uint16_t *krow, int head, float sqrt_head) {
-    float acc = 0.0f;
+__device__ __forceinline__ void score_group(float &acc, uint4 h8, float4 qa, float4 qb) {
     if constexpr (FINITE) {
         // fl(q_i * f32(k_i)) straight from the fp16 half: one v_fma_mix_f32 each
-        for (int i = 0; i < head; i += 8) {
-            const uint4 h8 = *reinterpret_cast<const uint4 *>(krow + i);
-            const float4 qa = *reinterpret_cast<const float4 *>(q + i);
-            const float4 qb = *reinterpret_cast<const float4 *>(q + i + 4);
-            acc = acc + half_times<false>(h8.x, qa.x);
-            acc = acc + half_times<true>(h8.x, qa.y);
-            acc = acc + half_times<false>(h8.y, qa.z);
-            acc = acc + half_times<true>(h8.y, qa.w);
-            acc = acc + half_times<false>(h8.z, qb.x);
-            acc = acc + half_times<true>(h8.z, qb.y);
-            acc = acc + half_times<false>(h8.w, qb.z);
-            acc = acc + half_times<true>(h8.w, qb.w);
-        }
-        return acc / sqrt_head;
-    }
-    for (int i = 0; i < head; i += 8) {
-        const uint4 h8 = *reinterpret_cast<const uint4 *>(krow + i);
-        const float4 qa = *reinterpret_cast<const float4 *>(q + i);
-        const float4 qb = *reinterpret_cast<const float4 *>(q + i + 4);
+        acc = acc + half_times<false>(h8.x, qa.x);
+        acc = acc + half_times<true>(h8.x, qa.y);
+        acc = acc + half_times<false>(h8.y, qa.z);
+        acc = acc + half_times<true>(h8.y, qa.w);
+        acc = acc + half_times<false>(h8.z, qb.x);
+        acc = acc + half_times<true>(h8.z, qb.y);
+        acc = acc + half_times<false>(h8.w, qb.z);
+        acc = acc + half_times<true>(h8.w, qb.w);
+    } else {
         acc = acc + qa.x * kv<FINITE>(static_cast<uint16_t>(h8.x));
         acc = acc + qa.y * kv<FINITE>(static_cast<uint16_t>(h8.x >> 16));
         acc = acc + qa.z * kv<FINITE>(static_cast<uint16_t>(h8.y));
@@ -107,6 +98,27 @@ __device__ __forceinline__ float score(const float *q, const uint16_t *krow, int
         acc = acc + qb.y * kv<FINITE>(static_cast<uint16_t>(h8.z >> 16));
         acc = acc + qb.z * kv<FINITE>(static_cast<uint16_t>(h8.w));
         acc = acc + qb.w * kv<FINITE>(static_cast<uint16_t>(h8.w >> 16));
+    }
+}
+
+template <bool FINITE>
+__device__ __forceinline__ float score(const float *q, const uint16_t *krow, int head, float sqrt_head) {
+    const uint4 *k8 = reinterpret_cast<const uint4 *>(krow);
+    const float4 *q4 = reinterpret_cast<const float4 *>(q);
+    const int groups = head / 8, last = groups - 1;  // head % 8 == 0
+    uint4 h0 = k8[0], h1 = k8[min(1, last)];
+    float4 a0 = q4[0], b0 = q4[1];
+    float4 a1 = q4[2 * min(1, last)], b1 = q4[2 * min(1, last) + 1];
+    float acc = 0.0f;
+    for (int g = 0; g < groups; g += 2) {
+        // groups g + 2 and g + 3 (clamped; the clamped copies are not used)
+        const int g2 = min(g + 2, last), g3 = min(g + 3, last);
+        const uint4 h2 = k8[g2], h3 = k8[g3];
+        const float4 a2 = q4[2 * g2], b2 = q4[2 * g2 + 1], a3 = q4[2 * g3], b3 = q4[2 * g3 + 1];
+        score_group<FINITE>(acc, h0, a0, b0);
+        if (g + 1 < groups) score_group<FINITE>(acc, h1, a1, b1);
+        h0 = h2; a0 = a2; b0 = b2;
+        h1 = h3; a1 = a3; b1 = b3;
     }
     return acc / sqrt_head;
 }
@@ -355,7 +367,7 @@ __device__ __forceinline__ float attend(const float *scores, int n, const uint16
 #pragma unroll
         for (int k = 0; k < kUnroll; ++k) m = fmaxf(m, x[k]);  // clamped duplicates change nothing
     }
-    for (int k = 32; k >= 1; k >>= 1) m = fmaxf(m, __shfl_xor(m, k));
+    m = wave_max(m);
     if (lane == 0) red[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

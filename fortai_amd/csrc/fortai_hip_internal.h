@@ -265,9 +265,81 @@ __device__ __forceinline__ void kernarg_warm() {
 
 // --------------------------------------------------------- reductions ----
 
+// The value lane (lane ^ M) holds, M a power of two up to 32, in VALU
+// operations only (a ds_bpermute costs an LDS round trip per exchange):
+// DPP within 16-lane rows -- quad permutes for 1 and 2, the quad reversal
+// then the half-row mirror for 4 ((l ^ 3) ^ 7 = l ^ 4), the row rotation by 8
+// for 8 -- and the gfx950 permlane swaps across rows (16) and wave halves
+// (32).  A swap of v with itself leaves {v.row0, v.row0, v.row2, v.row2} in
+// its first result and {v.row1, v.row1, v.row3, v.row3} in its second (rows
+// of 16 or 32 lanes), so a lane picks the one that is not its own row.
+// Every lane of the wave must be active.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "M: a power of two <= 32");
+    const int x = static_cast<int>(v);
+    if constexpr (M == 1) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+    } else if constexpr (M == 2) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+    } else if constexpr (M == 4) {
+        const int t = __builtin_amdgcn_update_dpp(0, x, 0x1B, 0xF, 0xF, false);          // quad [3,2,1,0]
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, t, 0x141, 0xF, 0xF, false));  // half-row mirror
+    } else if constexpr (M == 8) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));  // row rotate 8
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (__lane_id() & 16) ? r[0] : r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (__lane_id() & 32) ? r[0] : r[1];
+    }
+}
+
+template <int M, typename T>
+__device__ __forceinline__ T xor_lane(T v) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, xor_lane_u32<M>(__builtin_bit_cast(uint32_t, v)));
+    } else {
+        static_assert(sizeof(T) == 8, "4- or 8-byte values");
+        const uint2 u = __builtin_bit_cast(uint2, v);
+        return __builtin_bit_cast(T, make_uint2(xor_lane_u32<M>(u.x), xor_lane_u32<M>(u.y)));
+    }
+}
+
+// Butterfly over the wave: v + v[lane ^ m] for m = 32, 16, ..., 1; every
+// lane ends with the same value.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    v += xor_lane<32>(v);
+    v += xor_lane<16>(v);
+    v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<1>(v);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, xor_lane<32>(v));
+    v = fmaxf(v, xor_lane<16>(v));
+    v = fmaxf(v, xor_lane<8>(v));
+    v = fmaxf(v, xor_lane<4>(v));
+    v = fmaxf(v, xor_lane<2>(v));
+    v = fmaxf(v, xor_lane<1>(v));
+    return v;
+}
+
+// The butterfly sum over aligned groups of n lanes (n a power of two <= 64,
+// uniform): m = 1, 2, ..., n / 2.
+template <typename T>
+__device__ __forceinline__ T group_sum_up(T v, int n) {
+    if (n > 1) v += xor_lane<1>(v);
+    if (n > 2) v += xor_lane<2>(v);
+    if (n > 4) v += xor_lane<4>(v);
+    if (n > 8) v += xor_lane<8>(v);
+    if (n > 16) v += xor_lane<16>(v);
+    if (n > 32) v += xor_lane<32>(v);
     return v;
 }
 
@@ -276,9 +348,9 @@ __device__ __forceinline__ T wave_sum(T v) {
 // fp32 addition is commutative, so every lane of the group ends with the
 // bit pattern lane 0 of the reference produces.
 __device__ __forceinline__ float row_hsum8(float v) {
-    v = v + __shfl_xor(v, 4);
-    v = v + __shfl_xor(v, 2);
-    v = v + __shfl_xor(v, 1);
+    v = v + xor_lane<4>(v);
+    v = v + xor_lane<2>(v);
+    v = v + xor_lane<1>(v);
     return v;
 }
 
@@ -297,9 +369,9 @@ __device__ __forceinline__ int8_t sat8_rne(float v) {
 // the block's fp32 scale (f32 of the fp16 RNE scale).
 __device__ __forceinline__ uint32_t quantize_group(float4 y, float &scale_out, uint16_t &scale_bits) {
     float amax = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    amax = fmaxf(amax, xor_lane<1>(amax));
+    amax = fmaxf(amax, xor_lane<2>(amax));
+    amax = fmaxf(amax, xor_lane<4>(amax));
     const float scale = amax / 127.0f;
     const float inverse = amax != 0.0f ? 127.0f / amax : 0.0f;
     scale_bits = float_to_half_rne(scale);

@@ -28,14 +28,22 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i < bi);
 }
 
+template <int M>
+__device__ __forceinline__ void argmax_step(float &v, int &i) {
+    const float ov = xor_lane<M>(v);
+    const int oi = xor_lane<M>(i);
+    if (better(ov, oi, v, i)) { v = ov; i = oi; }
+}
+
 // (value, index) first-maximum reduction over the workgroup; result valid in
 // thread 0.
 __device__ __forceinline__ void block_argmax(float &v, int &i, float *sv, int *si) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = __shfl_xor(v, m);
-        const int oi = __shfl_xor(i, m);
-        if (better(ov, oi, v, i)) { v = ov; i = oi; }
-    }
+    argmax_step<32>(v, i);
+    argmax_step<16>(v, i);
+    argmax_step<8>(v, i);
+    argmax_step<4>(v, i);
+    argmax_step<2>(v, i);
+    argmax_step<1>(v, i);
     const int tid = static_cast<int>(threadIdx.x);
     const int waves = static_cast<int>(blockDim.x) >> 6;
     if ((tid & 63) == 0) { sv[tid >> 6] = v; si[tid >> 6] = i; }

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kRowThreads) void gated_quantize_tokens_kernel(cons
         float4 y = in ? reinterpret_cast<const float4 *>(orow)[g] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         double ss = static_cast<double>(y.x) * y.x + static_cast<double>(y.y) * y.y +
             static_cast<double>(y.z) * y.z + static_cast<double>(y.w) * y.w;
-        for (int m = 1; m < hl; m <<= 1) ss += __shfl_xor(ss, m);
+        ss = group_sum_up(ss, hl);
         if (in) {
             const float nf = sqrtf(static_cast<float>(ss / static_cast<double>(head)) + eps);
             const float4 w4 = reinterpret_cast<const float4 *>(norm)[g % hl];
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(256) void attention_prefill_exact_kernel(const floa
         float *row = sc + qi * kcap;
         float m = kLowest;
         for (int j = lane; j < n; j += 64) m = fmaxf(m, row[j]);
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = wave_max(m);
         for (int j = lane; j < keys; j += 64) row[j] = j < n ? expf_libm(row[j] - m) : 0.0f;
     }
     __syncthreads();
@@ -610,7 +610,7 @@ __global__ __launch_bounds__(256, 2) void attention_prefill_exact16_kernel(const
         float *row = sc + qi * kcap;
         float m = kLowest;
         for (int j = lane; j < n; j += 64) m = fmaxf(m, row[j]);
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = wave_max(m);
         for (int j = lane; j < kpad; j += 64) row[j] = j < n ? expf_libm(row[j] - m) : 0.0f;
     }
     __syncthreads();

@@ -181,7 +181,7 @@ __device__ __forceinline__ void act_store(const MatvecInput &in, int chunks, con
                     ss += static_cast<double>(y.y) * static_cast<double>(y.y);
                     ss += static_cast<double>(y.z) * static_cast<double>(y.z);
                     ss += static_cast<double>(y.w) * static_cast<double>(y.w);
-                    for (int m = 1; m < in.head / 4; m <<= 1) ss += __shfl_xor(ss, m);
+                    ss = group_sum_up(ss, in.head / 4);
                     const float nf = sqrtf(static_cast<float>(ss / static_cast<double>(in.head)) + in.eps);
                     y.x = ((y.x / nf) * wr[k].x) * zr[k].x;
                     y.y = ((y.y / nf) * wr[k].y) * zr[k].y;
@@ -989,9 +989,9 @@ __global__ void q8_block_dots_kernel(Q8Matrix w, const int8_t *xq, int32_t *out,
             sdot4(q.w, a.w)};
         for (int j = 0; j < 4; ++j) {
             int v = d[j];
-            v += __shfl_xor(v, 4);
-            v += __shfl_xor(v, 2);
-            v += __shfl_xor(v, 1);
+            v += xor_lane<4>(v);
+            v += xor_lane<2>(v);
+            v += xor_lane<1>(v);
             const int b = 4 * c + j;
             if (l == 0 && row < w.rows && b < blocks) out[static_cast<size_t>(row) * blocks + b] = v;
         }
