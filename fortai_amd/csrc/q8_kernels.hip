@@ -221,15 +221,25 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
 // segment in first_wg); otherwise segment 0 only, so that every kernel
 // argument the waves read has a fixed offset and all of them arrive in one
 // scalar round trip.
-template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI>
+// SPLIT: the four waves share one 8-row group, wave w loading chunks
+// [w NREG/4, (w+1) NREG/4); waves 1..3 hand wave 0, through LDS, each of
+// their blocks' scale product fl(f32(w_scale) * a_scale) and lane dot, and
+// wave 0 runs every lane's fma chain over all blocks in order (the same
+// operations as the unsplit chain).  A workgroup then moves a quarter of
+// the bytes and a wave issues a quarter of the dot work.
+template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI, bool SPLIT>
 __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs args) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
-    constexpr int kRegs = NREG > 0 ? NREG : 1;
+    static_assert(!SPLIT || (WAVES == 4 && NREG > 0 && NREG % 4 == 0 && !MULTI && !kPair), "split form");
+    constexpr int kPer = SPLIT ? NREG / 4 : NREG;  // chunks this wave loads
+    constexpr int kRegs = kPer > 0 ? kPer : 1;
     extern __shared__ __align__(16) unsigned char lds[];
     uint32_t *act32 = reinterpret_cast<uint32_t *>(lds);
     float *act_s = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 8 * 16);
     double *red = reinterpret_cast<double *>(lds + static_cast<size_t>(args.chunks) * 144);
     float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 144 + 8 * WAVES);
+    // SPLIT: [wave - 1][chunk][scales, dots][lane]
+    float4 *handoff = reinterpret_cast<float4 *>(lds + static_cast<size_t>(args.chunks) * 144 + 40 * WAVES);
 
     FORTAI_MV_MARK(5);
     kernarg_warm<sizeof(MatvecArgs)>();
@@ -240,13 +250,14 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     const MatvecSegment &seg = args.seg[s];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
-    const int rg = (wg - args.first_wg[s]) * WAVES + wave;
+    const int rg = SPLIT ? wg - args.first_wg[s] : (wg - args.first_wg[s]) * WAVES + wave;
     const bool active = rg < seg.w.row_groups;
     const int rgc = active ? rg : seg.w.row_groups - 1;  // excess waves re-read the last group, write nothing
     const int r = lane >> 3, l = lane & 7;
     const int chunks = seg.w.chunks;
-    const uint4 *qp = seg.w.quants + static_cast<size_t>(rgc) * chunks * 64 + lane;
-    const uint2 *sp = seg.w.scales + static_cast<size_t>(rgc) * chunks * 8 + r;
+    const int c_first = SPLIT ? wave * kPer : 0;
+    const uint4 *qp = seg.w.quants + (static_cast<size_t>(rgc) * chunks + c_first) * 64 + lane;
+    const uint2 *sp = seg.w.scales + (static_cast<size_t>(rgc) * chunks + c_first) * 8 + r;
     const uint4 *qp2 = kPair ? seg.w2.quants + static_cast<size_t>(rgc) * chunks * 64 + lane : nullptr;
     const uint2 *sp2 = kPair ? seg.w2.scales + static_cast<size_t>(rgc) * chunks * 8 + r : nullptr;
 
@@ -259,7 +270,7 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     uint2 sc[kRegs], sc2[kPair ? kRegs : 1];
     if constexpr (NREG > 0) {
 #pragma unroll
-        for (int c = 0; c < NREG; ++c) {
+        for (int c = 0; c < kPer; ++c) {
             q[c] = load_stream(qp + static_cast<size_t>(c) * 64);
             sc[c] = load_stream(sp + static_cast<size_t>(c) * 8);
             if constexpr (kPair) {
@@ -269,7 +280,7 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
         }
     }
     const int row = rg * kRowsPerWave + r;
-    const bool writer = active && l == 0 && row < seg.w.rows;
+    const bool writer = active && l == 0 && row < seg.w.rows && (!SPLIT || wave == 0);
     float resid = 0.0f;  // loaded now, used after the dot
     if constexpr (EPI == Epilogue::ADD)
         if (writer) resid = seg.resid[row];
@@ -292,7 +303,39 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     const uint4 *act4 = reinterpret_cast<const uint4 *>(act32);
     const float4 *as4 = reinterpret_cast<const float4 *>(act_s);
     float acc = 0.0f, acc2 = 0.0f;
-    if (active) {
+    if constexpr (SPLIT) {
+        if (active) {
+            if (wave > 0) {
+#pragma unroll
+                for (int c = 0; c < kPer; ++c) {
+                    const uint4 a = act4[(c_first + c) * 8 + l];
+                    const float4 as = as4[c_first + c];
+                    const float4 d = sdot4x4_f(q[c], a);
+                    const float4 sv = make_float4(half_times<false>(sc[c].x, as.x), half_times<true>(sc[c].x, as.y),
+                        half_times<false>(sc[c].y, as.z), half_times<true>(sc[c].y, as.w));
+                    float4 *h = handoff + ((wave - 1) * kPer + c) * 128 + lane;
+                    h[0] = sv;
+                    h[64] = d;
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < kPer; ++c) acc = dot_chunk(q[c], sc[c], act4[c * 8 + l], as4[c], acc);
+            }
+        }
+        __syncthreads();
+        if (wave > 0) return;
+        if (active) {
+#pragma unroll
+            for (int c = 0; c < 3 * kPer; ++c) {
+                const float4 sv = handoff[c * 128 + lane];
+                const float4 d = handoff[c * 128 + 64 + lane];
+                acc = __builtin_fmaf(sv.x, d.x, acc);
+                acc = __builtin_fmaf(sv.y, d.y, acc);
+                acc = __builtin_fmaf(sv.z, d.z, acc);
+                acc = __builtin_fmaf(sv.w, d.w, acc);
+            }
+        }
+    } else if (active) {
         if constexpr (NREG > 0) {
 #pragma unroll
             for (int c = 0; c < NREG; ++c) {
@@ -374,14 +417,25 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
 
 constexpr int kMatvecWaves = 4;  // large launches; small ones use one wave per workgroup
 
-template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI = false>
+template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI = false, bool SPLIT = false>
 hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES;
-    hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI, MULTI>), dim3(grid), dim3(WAVES * 64), lds, stream,
-        args);
-    note_launch("q8_matvec_kernel<waves=%d,regs=%d,%s,%s%s> grid %d", WAVES, NREG, prologue_name(PRO),
-        epilogue_name(EPI), MULTI ? ",segments" : "", grid);
+    const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES +
+        (SPLIT ? static_cast<size_t>(3 * (NREG / 4)) * 128 * 16 : 0);
+    hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI, MULTI, SPLIT>), dim3(grid), dim3(WAVES * 64), lds,
+        stream, args);
+    note_launch("q8_matvec_kernel<waves=%d,regs=%d,%s,%s%s%s> grid %d", WAVES, NREG, prologue_name(PRO),
+        epilogue_name(EPI), MULTI ? ",segments" : "", SPLIT ? ",split" : "", grid);
     return hipGetLastError();
+}
+
+// one 8-row group per workgroup, its chunks split over four waves
+template <Prologue PRO, Epilogue EPI>
+hipError_t launch_matvec_split(const MatvecArgs &args, int grid, int chunks, hipStream_t stream) {
+    if (chunks == 8) return launch_matvec_t<4, 8, PRO, EPI, false, true>(args, grid, stream);
+    if (chunks == 16) return launch_matvec_t<4, 16, PRO, EPI, false, true>(args, grid, stream);
+    if (chunks == 28) return launch_matvec_t<4, 28, PRO, EPI, false, true>(args, grid, stream);
+    if (chunks == 32) return launch_matvec_t<4, 32, PRO, EPI, false, true>(args, grid, stream);
+    return hipErrorInvalidValue;
 }
 
 template <int WAVES, Prologue PRO, Epilogue EPI>
@@ -399,7 +453,12 @@ hipError_t launch_matvec_regs(const MatvecArgs &args, int grid, int chunks, hipS
 
 template <Prologue PRO>
 hipError_t launch_matvec_pro(const MatvecArgs &args, int waves, int grid, int chunks, Epilogue epi,
-    hipStream_t stream) {
+    hipStream_t stream, bool split) {
+    if (split) {
+        if (epi == Epilogue::STORE) return launch_matvec_split<PRO, Epilogue::STORE>(args, grid, chunks, stream);
+        if (epi == Epilogue::ADD) return launch_matvec_split<PRO, Epilogue::ADD>(args, grid, chunks, stream);
+        return hipErrorInvalidValue;
+    }
     if (epi == Epilogue::SILU_PAIR) return launch_matvec_regs<4, PRO, Epilogue::SILU_PAIR>(args, grid, chunks, stream);
     if (epi == Epilogue::STORE) {
         if (waves == 4) return launch_matvec_regs<4, PRO, Epilogue::STORE>(args, grid, chunks, stream);
@@ -1050,6 +1109,22 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const flo
 
 }  // namespace
 
+// Which launches take the split form: single matrices of whole register
+// chunks that would otherwise run one-wave workgroups (their dot work then
+// spreads over four SIMDs) or the gated prologue (32 four-wave workgroups
+// would each move 70 KB for ssm_out).  FORTAI_HIP_MATVEC_SPLIT=0 turns it
+// off, 2 extends it to every eligible launch (measured slower for the large
+// four-wave projections).
+bool matvec_split(int count, int chunks, Prologue prologue, Epilogue epilogue, int waves) {
+    static const int mode = [] {
+        const char *e = getenv("FORTAI_HIP_MATVEC_SPLIT");
+        return e ? atoi(e) : 1;
+    }();
+    if (mode <= 0 || count != 1 || epilogue == Epilogue::SILU_PAIR) return false;
+    if (chunks != 8 && chunks != 16 && chunks != 28 && chunks != 32) return false;
+    return mode >= 2 || waves == 1 || prologue == Prologue::GATED;
+}
+
 hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const MatvecInput &in,
     Prologue prologue, Epilogue epilogue, hipStream_t stream) {
     if (count < 1 || count > 4 || in.width <= 0 || in.width % kQ8Block) return hipErrorInvalidValue;
@@ -1091,24 +1166,25 @@ hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const Matv
     args.count = count;
     args.in = in;
     args.chunks = (in.width / kQ8Block + 3) / 4;
+    const bool split = matvec_split(count, args.chunks, prologue, epilogue, waves);
     int grid = 0;
     for (int s = 0; s < count; ++s) {
         args.seg[s] = segments[s];
         args.first_wg[s] = grid;
         if (segments[s].w.chunks != args.chunks) return hipErrorInvalidValue;
-        grid += (segments[s].w.row_groups + waves - 1) / waves;
+        grid += split ? segments[s].w.row_groups : (segments[s].w.row_groups + waves - 1) / waves;
     }
     args.first_wg[count] = grid;
     const int rows = segments[0].w.rows;
     args.pair_vector_rows = rows >= 8 ? (rows / 8) * 8 : 0;
     if (grid == 0) return hipSuccess;
     switch (prologue) {
-    case Prologue::Q8: return launch_matvec_pro<Prologue::Q8>(args, waves, grid, args.chunks, epilogue, stream);
-    case Prologue::F32: return launch_matvec_pro<Prologue::F32>(args, waves, grid, args.chunks, epilogue, stream);
+    case Prologue::Q8: return launch_matvec_pro<Prologue::Q8>(args, waves, grid, args.chunks, epilogue, stream, split);
+    case Prologue::F32: return launch_matvec_pro<Prologue::F32>(args, waves, grid, args.chunks, epilogue, stream, split);
     case Prologue::RMSNORM:
-        return launch_matvec_pro<Prologue::RMSNORM>(args, waves, grid, args.chunks, epilogue, stream);
-    case Prologue::Q8L: return launch_matvec_pro<Prologue::Q8L>(args, waves, grid, args.chunks, epilogue, stream);
-    case Prologue::GATED: return launch_matvec_pro<Prologue::GATED>(args, waves, grid, args.chunks, epilogue, stream);
+        return launch_matvec_pro<Prologue::RMSNORM>(args, waves, grid, args.chunks, epilogue, stream, split);
+    case Prologue::Q8L: return launch_matvec_pro<Prologue::Q8L>(args, waves, grid, args.chunks, epilogue, stream, split);
+    case Prologue::GATED: return launch_matvec_pro<Prologue::GATED>(args, waves, grid, args.chunks, epilogue, stream, split);
     }
     return hipErrorInvalidValue;
 }
