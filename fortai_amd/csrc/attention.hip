@@ -150,8 +150,11 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     const float sqrt_head = sqrtf(static_cast<float>(HD));
     const int gi = tid >> 6, j = tid & 63;
     if (gi < group && j < n) {
-        const float sc = finite ? ea::score<true>(qh + gi * HD, &ktile[j][0], HD, sqrt_head)
-                                : ea::score<false>(qh + gi * HD, &ktile[j][0], HD, sqrt_head);
+        const float *qg = qh + gi * HD;
+        const uint16_t *kr = &ktile[j][0];
+        float sc;
+        if (finite) sc = HD == 256 ? ea::score_n<true, 256>(qg, kr, sqrt_head) : ea::score<true>(qg, kr, HD, sqrt_head);
+        else sc = ea::score<false>(qg, kr, HD, sqrt_head);
         p.partial[static_cast<size_t>(kvh * group + gi) * p.max_context + p0 + j] = sc;
     }
     FORTAI_ATT_MARK(20);

@@ -75,29 +75,30 @@ __device__ __forceinline__ void norm_rope_regs(float *v, int head, const float (
 
 // One position's score: the sequential dot of fortai_qwen35_cpu.f90:1009-1014.
 // q in LDS (broadcast reads), the key row in LDS, 8 halves per read.  The
-// reads run two groups of 8 ahead of the chain, so that their LDS latency
-// overlaps the adds instead of stalling the chain every 8 elements.
+// products of a group of 8 are formed one group ahead of their adds, so the
+// chain never waits on a product just issued, and the reads run two groups
+// ahead of the products.
 template <bool FINITE>
-__device__ __forceinline__ void score_group(float &acc, uint4 h8, float4 qa, float4 qb) {
+__device__ __forceinline__ void score_products(float (&p)[8], uint4 h8, float4 qa, float4 qb) {
     if constexpr (FINITE) {
         // fl(q_i * f32(k_i)) straight from the fp16 half: one v_fma_mix_f32 each
-        acc = acc + half_times<false>(h8.x, qa.x);
-        acc = acc + half_times<true>(h8.x, qa.y);
-        acc = acc + half_times<false>(h8.y, qa.z);
-        acc = acc + half_times<true>(h8.y, qa.w);
-        acc = acc + half_times<false>(h8.z, qb.x);
-        acc = acc + half_times<true>(h8.z, qb.y);
-        acc = acc + half_times<false>(h8.w, qb.z);
-        acc = acc + half_times<true>(h8.w, qb.w);
+        p[0] = half_times<false>(h8.x, qa.x);
+        p[1] = half_times<true>(h8.x, qa.y);
+        p[2] = half_times<false>(h8.y, qa.z);
+        p[3] = half_times<true>(h8.y, qa.w);
+        p[4] = half_times<false>(h8.z, qb.x);
+        p[5] = half_times<true>(h8.z, qb.y);
+        p[6] = half_times<false>(h8.w, qb.z);
+        p[7] = half_times<true>(h8.w, qb.w);
     } else {
-        acc = acc + qa.x * kv<FINITE>(static_cast<uint16_t>(h8.x));
-        acc = acc + qa.y * kv<FINITE>(static_cast<uint16_t>(h8.x >> 16));
-        acc = acc + qa.z * kv<FINITE>(static_cast<uint16_t>(h8.y));
-        acc = acc + qa.w * kv<FINITE>(static_cast<uint16_t>(h8.y >> 16));
-        acc = acc + qb.x * kv<FINITE>(static_cast<uint16_t>(h8.z));
-        acc = acc + qb.y * kv<FINITE>(static_cast<uint16_t>(h8.z >> 16));
-        acc = acc + qb.z * kv<FINITE>(static_cast<uint16_t>(h8.w));
-        acc = acc + qb.w * kv<FINITE>(static_cast<uint16_t>(h8.w >> 16));
+        p[0] = qa.x * kv<FINITE>(static_cast<uint16_t>(h8.x));
+        p[1] = qa.y * kv<FINITE>(static_cast<uint16_t>(h8.x >> 16));
+        p[2] = qa.z * kv<FINITE>(static_cast<uint16_t>(h8.y));
+        p[3] = qa.w * kv<FINITE>(static_cast<uint16_t>(h8.y >> 16));
+        p[4] = qb.x * kv<FINITE>(static_cast<uint16_t>(h8.z));
+        p[5] = qb.y * kv<FINITE>(static_cast<uint16_t>(h8.z >> 16));
+        p[6] = qb.z * kv<FINITE>(static_cast<uint16_t>(h8.w));
+        p[7] = qb.w * kv<FINITE>(static_cast<uint16_t>(h8.w >> 16));
     }
 }
 
@@ -106,19 +107,46 @@ __device__ __forceinline__ float score(const float *q, const uint16_t *krow, int
     const uint4 *k8 = reinterpret_cast<const uint4 *>(krow);
     const float4 *q4 = reinterpret_cast<const float4 *>(q);
     const int groups = head / 8, last = groups - 1;  // head % 8 == 0
-    uint4 h0 = k8[0], h1 = k8[min(1, last)];
-    float4 a0 = q4[0], b0 = q4[1];
-    float4 a1 = q4[2 * min(1, last)], b1 = q4[2 * min(1, last) + 1];
+    float p[8];
+    score_products<FINITE>(p, k8[0], q4[0], q4[1]);
+    const int g1 = min(1, last), g2 = min(2, last);
+    uint4 h1 = k8[g1], h2 = k8[g2];
+    float4 a1 = q4[2 * g1], b1 = q4[2 * g1 + 1], a2 = q4[2 * g2], b2 = q4[2 * g2 + 1];
     float acc = 0.0f;
-    for (int g = 0; g < groups; g += 2) {
-        // groups g + 2 and g + 3 (clamped; the clamped copies are not used)
-        const int g2 = min(g + 2, last), g3 = min(g + 3, last);
-        const uint4 h2 = k8[g2], h3 = k8[g3];
-        const float4 a2 = q4[2 * g2], b2 = q4[2 * g2 + 1], a3 = q4[2 * g3], b3 = q4[2 * g3 + 1];
-        score_group<FINITE>(acc, h0, a0, b0);
-        if (g + 1 < groups) score_group<FINITE>(acc, h1, a1, b1);
-        h0 = h2; a0 = a2; b0 = b2;
-        h1 = h3; a1 = a3; b1 = b3;
+    for (int g = 0; g < groups; ++g) {
+        // group g + 3's reads (clamped; the clamped copies are not used)
+        const int g3 = min(g + 3, last);
+        const uint4 h3 = k8[g3];
+        const float4 a3 = q4[2 * g3], b3 = q4[2 * g3 + 1];
+        float pn[8];
+        score_products<FINITE>(pn, h1, a1, b1);  // group g + 1 (unused past the end)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = acc + p[i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = pn[i];
+        h1 = h2; a1 = a2; b1 = b2;
+        h2 = h3; a2 = a3; b2 = b3;
+    }
+    return acc / sqrt_head;
+}
+
+// The same for a head width known at compile time, fully unrolled (the
+// reads become immediate offsets and the scheduler can run them ahead).
+template <bool FINITE, int HEAD>
+__device__ __forceinline__ float score_n(const float *q, const uint16_t *krow, float sqrt_head) {
+    const uint4 *k8 = reinterpret_cast<const uint4 *>(krow);
+    const float4 *q4 = reinterpret_cast<const float4 *>(q);
+    float acc = 0.0f;
+    float p[8];
+    score_products<FINITE>(p, k8[0], q4[0], q4[1]);
+#pragma unroll
+    for (int g = 0; g < HEAD / 8; ++g) {
+        float pn[8];
+        if (g + 1 < HEAD / 8) score_products<FINITE>(pn, k8[g + 1], q4[2 * g + 2], q4[2 * g + 3]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = acc + p[i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = pn[i];
     }
     return acc / sqrt_head;
 }
