@@ -233,12 +233,18 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     static_assert(!SPLIT || (WAVES == 4 && NREG > 0 && NREG % 4 == 0 && !MULTI && !kPair), "split form");
     constexpr int kPer = SPLIT ? NREG / 4 : NREG;  // chunks this wave loads
     constexpr int kRegs = kPer > 0 ? kPer : 1;
+    // unsplit, whole groups of 8 chunks: the weight scales come in one load
+    // per 8 chunks (lane (r, l) takes chunk l of row r, 512 contiguous bytes)
+    // instead of one 64-byte load per chunk, and go through the wave's own
+    // LDS slice, from which the 8 lanes of a row read each chunk's scales
+    constexpr bool kScLds = !SPLIT && NREG > 0 && NREG % 8 == 0;
+    constexpr int kScLoads = kScLds ? NREG / 8 : 1;
     extern __shared__ __align__(16) unsigned char lds[];
     uint32_t *act32 = reinterpret_cast<uint32_t *>(lds);
     float *act_s = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 8 * 16);
     double *red = reinterpret_cast<double *>(lds + static_cast<size_t>(args.chunks) * 144);
     float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 144 + 8 * WAVES);
-    // SPLIT: [wave - 1][chunk][scales, dots][lane]
+    // SPLIT: [wave - 1][chunk][scales, dots][lane]; kScLds: [wave][w, w2][chunk / 8][lane] scales
     float4 *handoff = reinterpret_cast<float4 *>(lds + static_cast<size_t>(args.chunks) * 144 + 40 * WAVES);
 
     FORTAI_MV_MARK(5);
@@ -267,15 +273,24 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     float4 act_x[AS::kX], act_w[AS::kW], act_z[AS::kZ];
     act_fetch<WAVES * 64, PRO>(args.in, args.chunks, act_q, act_x, act_w, act_z);
     uint4 q[kRegs], q2[kPair ? kRegs : 1];
-    uint2 sc[kRegs], sc2[kPair ? kRegs : 1];
+    uint2 sc[kScLds ? 1 : kRegs], sc2[kPair && !kScLds ? kRegs : 1];
+    uint2 scw[kScLoads], scw2[kPair ? kScLoads : 1];
+    if constexpr (kScLds) {
+        const size_t sb = static_cast<size_t>(rgc) * chunks * 8 + l * 8 + r;
+#pragma unroll
+        for (int k = 0; k < kScLoads; ++k) {
+            scw[k] = load_stream(seg.w.scales + sb + k * 64);
+            if constexpr (kPair) scw2[k] = load_stream(seg.w2.scales + sb + k * 64);
+        }
+    }
     if constexpr (NREG > 0) {
 #pragma unroll
         for (int c = 0; c < kPer; ++c) {
             q[c] = load_stream(qp + static_cast<size_t>(c) * 64);
-            sc[c] = load_stream(sp + static_cast<size_t>(c) * 8);
+            if constexpr (!kScLds) sc[c] = load_stream(sp + static_cast<size_t>(c) * 8);
             if constexpr (kPair) {
                 q2[c] = load_stream(qp2 + static_cast<size_t>(c) * 64);
-                sc2[c] = load_stream(sp2 + static_cast<size_t>(c) * 8);
+                if constexpr (!kScLds) sc2[c] = load_stream(sp2 + static_cast<size_t>(c) * 8);
             }
         }
     }
@@ -336,7 +351,22 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
             }
         }
     } else if (active) {
-        if constexpr (NREG > 0) {
+        if constexpr (kScLds) {
+            uint2 *ws = reinterpret_cast<uint2 *>(handoff) + static_cast<size_t>(wave) * (kPair ? 2 : 1) * kScLoads * 64;
+#pragma unroll
+            for (int k = 0; k < kScLoads; ++k) {
+                ws[k * 64 + lane] = scw[k];
+                if constexpr (kPair) ws[(kScLoads + k) * 64 + lane] = scw2[k];
+            }
+#pragma unroll
+            for (int c = 0; c < NREG; ++c) {
+                const uint4 a = act4[c * 8 + l];
+                const float4 as = as4[c];
+                const int si = (c >> 3) * 64 + r * 8 + (c & 7);
+                acc = dot_chunk(q[c], ws[si], a, as, acc);
+                if constexpr (kPair) acc2 = dot_chunk(q2[c], ws[kScLoads * 64 + si], a, as, acc2);
+            }
+        } else if constexpr (NREG > 0) {
 #pragma unroll
             for (int c = 0; c < NREG; ++c) {
                 const uint4 a = act4[c * 8 + l];
@@ -419,8 +449,10 @@ constexpr int kMatvecWaves = 4;  // large launches; small ones use one wave per 
 
 template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI = false, bool SPLIT = false>
 hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream) {
+    constexpr bool kScLds = !SPLIT && NREG > 0 && NREG % 8 == 0;
     const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES +
-        (SPLIT ? static_cast<size_t>(3 * (NREG / 4)) * 128 * 16 : 0);
+        (SPLIT ? static_cast<size_t>(3 * (NREG / 4)) * 128 * 16 : 0) +
+        (kScLds ? static_cast<size_t>(WAVES) * (EPI == Epilogue::SILU_PAIR ? 2 : 1) * (NREG / 8) * 64 * 8 : 0);
     hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI, MULTI, SPLIT>), dim3(grid), dim3(WAVES * 64), lds,
         stream, args);
     note_launch("q8_matvec_kernel<waves=%d,regs=%d,%s,%s%s%s> grid %d", WAVES, NREG, prologue_name(PRO),
