@@ -237,14 +237,16 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     // per 8 chunks (lane (r, l) takes chunk l of row r, 512 contiguous bytes)
     // instead of one 64-byte load per chunk, and go through the wave's own
     // LDS slice, from which the 8 lanes of a row read each chunk's scales
-    constexpr bool kScLds = !SPLIT && NREG > 0 && NREG % 8 == 0;
-    constexpr int kScLoads = kScLds ? NREG / 8 : 1;
+    // (split: the wave's kPer <= 8 chunks in one load, lanes past kPer clamped)
+    constexpr bool kScLds = NREG > 0 && (SPLIT ? kPer <= 8 : NREG % 8 == 0);
+    constexpr int kScLoads = kScLds ? (SPLIT ? 1 : NREG / 8) : 1;
     extern __shared__ __align__(16) unsigned char lds[];
     uint32_t *act32 = reinterpret_cast<uint32_t *>(lds);
     float *act_s = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 8 * 16);
     double *red = reinterpret_cast<double *>(lds + static_cast<size_t>(args.chunks) * 144);
     float *epi = reinterpret_cast<float *>(lds + static_cast<size_t>(args.chunks) * 144 + 8 * WAVES);
-    // SPLIT: [wave - 1][chunk][scales, dots][lane]; kScLds: [wave][w, w2][chunk / 8][lane] scales
+    // SPLIT: [wave - 1][chunk][scales, dots][lane], then (kScLds) each wave's
+    // 512 scale bytes; unsplit kScLds: [wave][w, w2][chunk / 8][lane] scales
     float4 *handoff = reinterpret_cast<float4 *>(lds + static_cast<size_t>(args.chunks) * 144 + 40 * WAVES);
 
     FORTAI_MV_MARK(5);
@@ -276,7 +278,8 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     uint2 sc[kScLds ? 1 : kRegs], sc2[kPair && !kScLds ? kRegs : 1];
     uint2 scw[kScLoads], scw2[kPair ? kScLoads : 1];
     if constexpr (kScLds) {
-        const size_t sb = static_cast<size_t>(rgc) * chunks * 8 + l * 8 + r;
+        const int lc = SPLIT ? c_first + min(l, kPer - 1) : l;
+        const size_t sb = (static_cast<size_t>(rgc) * chunks + lc) * 8 + r;
 #pragma unroll
         for (int k = 0; k < kScLoads; ++k) {
             scw[k] = load_stream(seg.w.scales + sb + k * 64);
@@ -319,22 +322,29 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     const float4 *as4 = reinterpret_cast<const float4 *>(act_s);
     float acc = 0.0f, acc2 = 0.0f;
     if constexpr (SPLIT) {
+        uint2 *ws = reinterpret_cast<uint2 *>(handoff + 3 * kPer * 128) + wave * 64;
+        auto wscale = [&](int c) {
+            if constexpr (kScLds) return ws[r * 8 + c];
+            else return sc[c];
+        };
         if (active) {
+            if constexpr (kScLds) ws[lane] = scw[0];
             if (wave > 0) {
 #pragma unroll
                 for (int c = 0; c < kPer; ++c) {
                     const uint4 a = act4[(c_first + c) * 8 + l];
                     const float4 as = as4[c_first + c];
                     const float4 d = sdot4x4_f(q[c], a);
-                    const float4 sv = make_float4(half_times<false>(sc[c].x, as.x), half_times<true>(sc[c].x, as.y),
-                        half_times<false>(sc[c].y, as.z), half_times<true>(sc[c].y, as.w));
+                    const uint2 sw = wscale(c);
+                    const float4 sv = make_float4(half_times<false>(sw.x, as.x), half_times<true>(sw.x, as.y),
+                        half_times<false>(sw.y, as.z), half_times<true>(sw.y, as.w));
                     float4 *h = handoff + ((wave - 1) * kPer + c) * 128 + lane;
                     h[0] = sv;
                     h[64] = d;
                 }
             } else {
 #pragma unroll
-                for (int c = 0; c < kPer; ++c) acc = dot_chunk(q[c], sc[c], act4[c * 8 + l], as4[c], acc);
+                for (int c = 0; c < kPer; ++c) acc = dot_chunk(q[c], wscale(c), act4[c * 8 + l], as4[c], acc);
             }
         }
         __syncthreads();
@@ -449,10 +459,11 @@ constexpr int kMatvecWaves = 4;  // large launches; small ones use one wave per 
 
 template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI = false, bool SPLIT = false>
 hipError_t launch_matvec_t(const MatvecArgs &args, int grid, hipStream_t stream) {
-    constexpr bool kScLds = !SPLIT && NREG > 0 && NREG % 8 == 0;
+    constexpr bool kScLds = NREG > 0 && (SPLIT ? NREG / 4 <= 8 : NREG % 8 == 0);
+    constexpr int kScLoads = SPLIT ? 1 : NREG / 8;
     const size_t lds = static_cast<size_t>(args.chunks) * 144 + 8 * WAVES + 4 * 8 * WAVES +
         (SPLIT ? static_cast<size_t>(3 * (NREG / 4)) * 128 * 16 : 0) +
-        (kScLds ? static_cast<size_t>(WAVES) * (EPI == Epilogue::SILU_PAIR ? 2 : 1) * (NREG / 8) * 64 * 8 : 0);
+        (kScLds ? static_cast<size_t>(WAVES) * (EPI == Epilogue::SILU_PAIR ? 2 : 1) * kScLoads * 64 * 8 : 0);
     hipLaunchKernelGGL((q8_matvec_kernel<WAVES, NREG, PRO, EPI, MULTI, SPLIT>), dim3(grid), dim3(WAVES * 64), lds,
         stream, args);
     note_launch("q8_matvec_kernel<waves=%d,regs=%d,%s,%s%s%s> grid %d", WAVES, NREG, prologue_name(PRO),
