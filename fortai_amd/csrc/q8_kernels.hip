@@ -270,6 +270,27 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
     const uint2 *sp2 = kPair ? seg.w2.scales + static_cast<size_t>(rgc) * chunks * 8 + r : nullptr;
 
     FORTAI_MV_MARK(0);
+    // The epilogue's own inputs first: the compiler's in-order load counter
+    // cannot count loads under a condition, so one issued after the weights
+    // would make the prologue's wait for the activation also wait for most
+    // of the weights.  The residual is loaded by every lane (row clamped),
+    // the conv window and taps by every lane of a conv wave.
+    const int row = rg * kRowsPerWave + r;
+    const int rowc = min(row, seg.w.rows - 1);
+    const bool writer = active && l == 0 && row < seg.w.rows && (!SPLIT || wave == 0);
+    float resid = 0.0f;  // used after the dot
+    if constexpr (EPI == Epilogue::ADD) resid = seg.resid[rowc];
+    float win[kConvMax - 1], taps[kConvMax];
+    // (row groups are whole 8-row groups, so conv and SiLU are uniform per wave)
+    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr && (seg.conv_rows == 0 || row < seg.conv_rows);
+    const int ck = conv ? seg.kernel : 0;
+    if (conv) {
+#pragma unroll
+        for (int t = 0; t < kConvMax; ++t) {
+            if (t < ck - 1) win[t] = seg.conv_state[static_cast<size_t>(t) * seg.conv_size + rowc];
+            if (t < ck) taps[t] = seg.conv_w[static_cast<size_t>(rowc) * ck + t];
+        }
+    }
     using AS = ActShape<WAVES * 64, PRO>;
     u32x4_t act_q[AS::kQ];
     float4 act_x[AS::kX], act_w[AS::kW], act_z[AS::kZ];
@@ -295,23 +316,6 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
                 q2[c] = load_stream(qp2 + static_cast<size_t>(c) * 64);
                 if constexpr (!kScLds) sc2[c] = load_stream(sp2 + static_cast<size_t>(c) * 8);
             }
-        }
-    }
-    const int row = rg * kRowsPerWave + r;
-    const bool writer = active && l == 0 && row < seg.w.rows && (!SPLIT || wave == 0);
-    float resid = 0.0f;  // loaded now, used after the dot
-    if constexpr (EPI == Epilogue::ADD)
-        if (writer) resid = seg.resid[row];
-    // STORE with a conv: the row's window and taps, loaded now
-    float win[kConvMax - 1], taps[kConvMax];
-    // (row groups are whole 8-row groups, so conv and SiLU are uniform per wave)
-    const bool conv = EPI == Epilogue::STORE && seg.conv_w != nullptr && (seg.conv_rows == 0 || row < seg.conv_rows);
-    const int ck = conv ? seg.kernel : 0;
-    if (conv && writer) {
-#pragma unroll
-        for (int t = 0; t < kConvMax; ++t) {
-            if (t < ck - 1) win[t] = seg.conv_state[static_cast<size_t>(t) * seg.conv_size + row];
-            if (t < ck) taps[t] = seg.conv_w[static_cast<size_t>(row) * ck + t];
         }
     }
     FORTAI_MV_MARK(1);
