@@ -212,8 +212,19 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     if (k != k0) __syncthreads();  // the previous segment's chains have read e_seg and dred
     const int p0 = k * ea::kSeg;
     const int cnt = min(ea::kSeg, n - p0);
-    // the segment's own e values, exactly as the reference computes them
-    const float e = tid < cnt ? expf_libm(sc[p0 + tid] - m) : -0.0f;  // -0 leaves a sum unchanged
+    // the segment's own e values, exactly as the reference computes them; the
+    // score is the held one (x[k] holds position k * kSeg + tid), selected
+    // without a dynamic register index or a second round trip to memory
+    float sv;
+    if (held) {
+        sv = x[0];
+#pragma unroll
+        for (int i = 1; i < kHeld; ++i)
+            if (i == k && i * ea::kThreads < cap) sv = x[i];
+    } else {
+        sv = sc[min(p0 + tid, n - 1)];
+    }
+    const float e = tid < cnt ? expf_libm(sv - m) : -0.0f;  // -0 leaves a sum unchanged
     e_seg[tid] = e;
     if (tid < cnt) evals_of(p)[static_cast<size_t>(h) * p.max_context + p0 + tid] = e;
     // the estimates of the running sums entering this segment and the next
