@@ -180,14 +180,29 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
         }
     };
     const int tiles = width / TILE;
+    // x and the norm weights of the first kXRegs * kRows columns first, into
+    // registers (clamped, unconditional), then the first two tiles: the
+    // RMSNorm then waits for x only, not for the tiles behind it
+    constexpr int kXRegs = 8;
+    float xr[kXRegs], nr[kXRegs];
+#pragma unroll
+    for (int k = 0; k < kXRegs; ++k) {
+        const int i = min(tid + k * kRows, width - 1);
+        xr[k] = x[i];
+        nr[k] = RMS ? norm[i] : 0.0f;
+    }
     fetch(0, ra);
-    if (tiles > 1) fetch(TILE, rb);
+    fetch(min(TILE, width - TILE), rb);  // (one tile: a harmless second copy)
 
-    // x (optionally RMS-normalised, fortai_qwen35_cpu.f90:707) into LDS
+    // x (optionally RMS-normalised, fortai_qwen35_cpu.f90:707) into LDS; each
+    // thread sums its columns tid, tid + kRows, ... in order
     float inv = 1.0f;
     if constexpr (RMS) {
         double ss = 0.0;
-        for (int i = tid; i < width; i += kRows) ss += static_cast<double>(x[i]) * static_cast<double>(x[i]);
+#pragma unroll
+        for (int k = 0; k < kXRegs; ++k)
+            if (tid + k * kRows < width) ss += static_cast<double>(xr[k]) * static_cast<double>(xr[k]);
+        for (int i = tid + kXRegs * kRows; i < width; i += kRows) ss += static_cast<double>(x[i]) * static_cast<double>(x[i]);
         ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
@@ -195,7 +210,12 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
         for (int i = 0; i < kRows / 64; ++i) total += red[i];
         inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
     }
-    for (int i = tid; i < width; i += kRows) xs[i] = RMS ? (x[i] * inv) * norm[i] : x[i];
+#pragma unroll
+    for (int k = 0; k < kXRegs; ++k) {
+        const int i = tid + k * kRows;
+        if (i < width) xs[i] = RMS ? (xr[k] * inv) * nr[k] : xr[k];
+    }
+    for (int i = tid + kXRegs * kRows; i < width; i += kRows) xs[i] = RMS ? (x[i] * inv) * norm[i] : x[i];
 
     // each thread's row: the reference's sequential chain value(i) * x(i)
     float acc = 0.0f;
