@@ -104,7 +104,21 @@ __global__ __launch_bounds__(256) void step_embedding_kernel(const uint16_t *tab
     if (t < 0) {
         float bv = -__builtin_inff();
         int bi = 0x7fffffff;
-        for (int w = tid; w < partials; w += 256)
+        // the first 8 * 256 partials in one round trip (clamped; duplicates
+        // of the last partial change no first maximum), in the loop's order
+        constexpr int kHeldParts = 8;
+        float pv[kHeldParts];
+        int pi[kHeldParts];
+#pragma unroll
+        for (int k = 0; k < kHeldParts; ++k) {
+            const int w = min(tid + k * 256, partials - 1);
+            pv[k] = st.partial_value[w];
+            pi[k] = st.partial_index[w];
+        }
+#pragma unroll
+        for (int k = 0; k < kHeldParts; ++k)
+            if (better(pv[k], pi[k], bv, bi)) { bv = pv[k]; bi = pi[k]; }
+        for (int w = tid + kHeldParts * 256; w < partials; w += 256)
             if (better(st.partial_value[w], st.partial_index[w], bv, bi)) { bv = st.partial_value[w]; bi = st.partial_index[w]; }
         block_argmax(bv, bi, sv, si);
         if (tid == 0) {
