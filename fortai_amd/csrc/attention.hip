@@ -173,12 +173,15 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     __shared__ __align__(16) float e_seg[ea::kSeg];
     __shared__ double dred[2 * ea::kWaves];
     __shared__ float fred[ea::kWaves];
+    __shared__ MathTables mt;
+    mt.load();
     static_assert(ea::kZCand == ea::kThreads && ea::kSeg == ea::kThreads, "one candidate and one position per thread");
     const int pos = *p.position;
     const int k0 = div(static_cast<int>(blockIdx.x), p.div_heads), h = static_cast<int>(blockIdx.x) - k0 * p.heads;
     const int G = div(static_cast<int>(gridDim.x), p.div_heads);
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
+    FORTAI_ATT_MARK(21);
     // up to kHeld * 256 positions the scores are loaded in the position's
     // round trip (clamped to the cache; those past the position are masked)
     constexpr int kHeld = 32;
@@ -208,6 +211,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     if (lane == 0) fred[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    FORTAI_ATT_MARK(22);
     for (int k = k0; k * ea::kSeg < n; k += G) {
     if (k != k0) __syncthreads();  // the previous segment's chains have read e_seg and dred
     const int p0 = k * ea::kSeg;
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     } else {
         sv = sc[min(p0 + tid, n - 1)];
     }
-    const float e = tid < cnt ? expf_libm(sv - m) : -0.0f;  // -0 leaves a sum unchanged
+    const float e = tid < cnt ? mt.expf(sv - m) : -0.0f;  // -0 leaves a sum unchanged
     e_seg[tid] = e;
     if (tid < cnt) evals_of(p)[static_cast<size_t>(h) * p.max_context + p0 + tid] = e;
     // the estimates of the running sums entering this segment and the next
@@ -256,6 +260,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     __syncthreads();
     est = (dred[0] + dred[1]) + (dred[2] + dred[3]);
     est_next = (dred[4] + dred[5]) + (dred[6] + dred[7]);
+    if (k == k0) FORTAI_ATT_MARK(23);
     const uint32_t skew = static_cast<uint32_t>(p.z_skew);
     const uint32_t centre = k == 0 ? 0u : __float_as_uint(static_cast<float>(est)) + skew;
     const uint32_t centre_next = __float_as_uint(static_cast<float>(est_next)) + skew;
@@ -268,12 +273,14 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
         acc = acc + v.z;
         acc = acc + v.w;
     }
+    if (k == k0) FORTAI_ATT_MARK(24);
     const bool last = p0 + ea::kSeg >= n;
     float *tab = ztab_of(p) + (static_cast<size_t>(h) * ea::z_segments(p.max_context) + k) * ea::kZStride;
     tab[tid] = acc;
     tab[ea::kZNext + tid] = last ? acc : __int_as_float(ea::z_index(acc, centre_next));
     if (tid == 0) tab[ea::kZCentre] = __uint_as_float(centre);
     }
+    FORTAI_ATT_MARK(25);
 }
 
 // Z of head h: the walk words of the candidate tables into LDS (up to
@@ -316,6 +323,8 @@ constexpr int kTabRegs = kZLdsSegments * ea::kZCand / ea::kThreads;  // walk wor
 __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const AttentionParams p_batch) {
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     extern __shared__ __align__(16) float lds[];
+    __shared__ MathTables mt;
+    mt.load();
     const int tid = static_cast<int>(threadIdx.x);
     FORTAI_ATT_MARK(0);
     const int pos = *p.position;
@@ -379,7 +388,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     FORTAI_ATT_MARK(5);
     const float acc = flag == 0 ? ea::attend_given_z<true>(ev, z, positions, vbase, vstride, work, v, e4)
                                 : ea::attend_given_z<false>(ev, z, positions, vbase, vstride, work, v, e4);
-    if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * sigmoid_ref(gate);
+    if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * mt.sigmoid(gate);
     FORTAI_ATT_MARK(4);
 }
 

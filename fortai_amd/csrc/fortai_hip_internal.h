@@ -137,7 +137,10 @@ static __constant__ const uint64_t kExpf2Table[32] = {
     0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
-__device__ __forceinline__ float expf_libm(float x) {
+// tab: kExpf2Table, or a copy of it in LDS (a lookup in the constant table
+// is a memory round trip that depends on x; see MathTables)
+template <typename TAB>
+__device__ __forceinline__ float expf_libm_t(float x, const TAB *tab) {
     if (x != x) return x + x;
     if (x > 0x1.62e42ep6f) return __builtin_inff();
     if (x < -0x1.9fe368p6f) return 0.0f;
@@ -150,7 +153,7 @@ __device__ __forceinline__ float expf_libm(float x) {
     const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    const uint64_t t = kExpf2Table[ki % 32] + (ki << 47);
+    const uint64_t t = static_cast<uint64_t>(tab[ki % 32]) + (ki << 47);
     const double s = __builtin_bit_cast(double, t);
     const double zz = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
@@ -158,6 +161,7 @@ __device__ __forceinline__ float expf_libm(float x) {
     y = __builtin_fma(zz, r2, y);
     return static_cast<float>(y * s);
 }
+__device__ __forceinline__ float expf_libm(float x) { return expf_libm_t(x, kExpf2Table); }
 __device__ __forceinline__ float exp_rounded(float v) { return expf_libm(v); }
 
 // logf of the same C library (the Fortran real32 log intrinsic calls it):
@@ -181,22 +185,25 @@ static __constant__ const double kLogfTable[16][2] = {
     {0x1.e608cfd9a47acp-1, 0x1.aa5aa5df25984p-5},  {0x1.ca4b31f026aap-1, 0x1.c5e53aa362eb4p-4},
     {0x1.b2036576afce6p-1, 0x1.526e57720db08p-3}, {0x1.9c2d163a1aa2dp-1, 0x1.bc2860d22477p-3},
     {0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2}, {0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2}};
-// positive normal finite x only (softplus passes 1 + expf(v) > 1)
-__device__ __forceinline__ float logf_libm(float x) {
+// positive normal finite x only (softplus passes 1 + expf(v) > 1); tab:
+// kLogfTable or a copy of it in LDS
+template <typename TAB>
+__device__ __forceinline__ float logf_libm_t(float x, const TAB (*tab)[2]) {
     const uint32_t ix = __float_as_uint(x);
     if (ix == 0x3f800000u) return 0.0f;
     const uint32_t tmp = ix - 0x3f330000u;  // offset so that z lands in [0x1.66p-1, 0x1.66p0)
     const uint32_t i = (tmp >> 19) & 15u;
     const int k = static_cast<int32_t>(tmp) >> 23;
     const double z = static_cast<double>(__uint_as_float(ix - (tmp & 0xff800000u)));
-    const double r = __builtin_fma(z, kLogfTable[i][0], -1.0);
-    const double y0 = kLogfTable[i][1] + static_cast<double>(k) * 0x1.62e42fefa39efp-1;
+    const double r = __builtin_fma(z, static_cast<double>(tab[i][0]), -1.0);
+    const double y0 = static_cast<double>(tab[i][1]) + static_cast<double>(k) * 0x1.62e42fefa39efp-1;
     const double r2 = r * r;
     double y = __builtin_fma(0x1.5575b0be00b6ap-2, r, -0x1.ffffef20a4123p-2);
     y = __builtin_fma(-0x1.00ea348b88334p-2, r2, y);
     y = __builtin_fma(y, r2, y0 + r);
     return static_cast<float>(y);
 }
+__device__ __forceinline__ float logf_libm(float x) { return logf_libm_t(x, kLogfTable); }
 
 // fortai_qwen35_cpu.f90:1506-1514
 __device__ __forceinline__ float sigmoid_ref(float v) {
@@ -211,6 +218,34 @@ __device__ __forceinline__ float softplus_ref(float v) {
     if (v < -20.0f) return exp_rounded(v);
     return logf_libm(1.0f + exp_rounded(v));
 }
+
+// The expf and logf tables in LDS: a kernel whose critical path runs through
+// those functions copies them at entry (load() by every thread, no wait: the
+// copy completes before the kernel's next barrier), so that each lookup is an
+// LDS read instead of a data-dependent memory round trip.  Same values, so
+// the same results.
+struct MathTables {
+    uint64_t exp2[32];
+    double logc[16][2];
+    __device__ __forceinline__ void load() {
+        const int t = static_cast<int>(threadIdx.x);
+        if (t < 32) exp2[t] = kExpf2Table[t];
+        else if (t < 64) logc[(t - 32) >> 1][t & 1] = kLogfTable[(t - 32) >> 1][t & 1];
+    }
+    __device__ __forceinline__ float expf(float x) const { return expf_libm_t(x, exp2); }
+    __device__ __forceinline__ float logf(float x) const { return logf_libm_t(x, logc); }
+    // sigmoid_ref and softplus_ref with these tables
+    __device__ __forceinline__ float sigmoid(float v) const {
+        if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+        const float e = expf(v);
+        return e / (1.0f + e);
+    }
+    __device__ __forceinline__ float softplus(float v) const {
+        if (v > 20.0f) return v;
+        if (v < -20.0f) return expf(v);
+        return logf(1.0f + expf(v));
+    }
+};
 
 // ------------------------------------------------------ streaming loads ----
 

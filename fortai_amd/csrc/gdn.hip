@@ -75,6 +75,8 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
     __shared__ __align__(16) float ks[HEAD];
     __shared__ double red[2];
     __shared__ float hs[2];
+    __shared__ MathTables mt;
+    mt.load();
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks_per_head = HEAD / kDeltaRows;
     const int wg = xcd_grouped(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
@@ -98,14 +100,7 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
         qk[k] = p.qkv[i < HEAD ? kh * HEAD + i : p.state_size * p.key_heads + kh * HEAD + (i - HEAD)];
     }
     const float vrow = p.qkv[2 * p.state_size * p.key_heads + h * HEAD + row];
-    float beta = 0.0f, decay = 0.0f;
-    if (tid == 0) {
-        // fortai_qwen35_cpu.f90:890-894
-        beta = sigmoid_ref(p.beta[h]);
-        decay = exp_rounded(p.ssm_a[h] * softplus_ref(p.alpha[h] + p.ssm_dt[h]));
-        hs[0] = beta;
-        hs[1] = decay;
-    }
+    const float beta_in = p.beta[h], alpha_in = p.alpha[h], ssm_a = p.ssm_a[h], ssm_dt = p.ssm_dt[h];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = tid + k * kDeltaThreads;
@@ -113,6 +108,11 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
         else if (i < 2 * HEAD) ks[i - HEAD] = qk[k];
     }
     __syncthreads();
+    if (tid == 0) {
+        // fortai_qwen35_cpu.f90:890-894 (the tables in LDS since the barrier)
+        hs[0] = mt.sigmoid(beta_in);
+        hs[1] = mt.expf(ssm_a * mt.softplus(alpha_in + ssm_dt));
+    }
     // L2 norms of q (wave 0) and k (wave 1), fortai_qwen35_cpu.f90:1455-1471
     {
         const float *v = (tid < 64) ? qs : ks;
@@ -124,8 +124,8 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
     __syncthreads();
     const float qinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[0])), p.eps);
     const float kinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[1])), p.eps);
-    beta = hs[0];
-    decay = hs[1];
+    const float beta = hs[0];
+    const float decay = hs[1];
     // delta rule (fortai_q8_dot.c:363-396), the normalized q and k read from LDS
     float kd = 0.0f;
 #pragma unroll
