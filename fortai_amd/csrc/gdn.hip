@@ -175,6 +175,8 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_recurrence_kernel(const Gdn
     __shared__ float vs[kDeltaRows];
     __shared__ double red[2];
     __shared__ float hs[2];
+    __shared__ MathTables mt;  // written and read by wave 0 (thread 0 uses it), in order
+    mt.load();
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks_per_head = HEAD / kDeltaRows;
     const int wg = xcd_grouped(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
@@ -237,8 +239,8 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_recurrence_kernel(const Gdn
         if (tid < kDeltaRows) vs[tid] = y[2];
         if (tid == 0) {
             // fortai_qwen35_cpu.f90:890-894
-            hs[0] = sigmoid_ref(b);
-            hs[1] = exp_rounded(p.ssm_a[h] * softplus_ref(a + p.ssm_dt[h]));
+            hs[0] = mt.sigmoid(b);
+            hs[1] = mt.expf(p.ssm_a[h] * mt.softplus(a + p.ssm_dt[h]));
         }
         __syncthreads();
         // L2 norms of q (wave 0) and k (wave 1), fortai_qwen35_cpu.f90:1455-1471
