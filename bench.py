@@ -84,7 +84,7 @@ def bench_decode(args, path):
     ctx_len = args.ctx
     log(f"loading {path} onto the GPU (max_context {ctx_len})")
     t = time.time()
-    model = Qwen35Hip(path, max_context=ctx_len)
+    model = Qwen35Hip(path, max_context=ctx_len, direct=DIRECT)
     log(f"  resident in {time.time() - t:.1f}s")
     fill = ctx_len - args.warmup - args.steps
     if fill < 1:
@@ -175,20 +175,17 @@ def matvec_family_roofline(model, warmup: int = 4, reps: int = 32):
     """The dominant kernel family of the decode step: every Q8_0 matvec launch
     of one step (q8_matvec_kernel, 114 launches at the 0.8B shape), timed live
     with HIP events on the context stream by replaying a graph of exactly those
-    launches (a decoder created with FORTAI_HIP_DECODER_MATVEC_ONLY=1: same
+    launches (a decoder in the FORTAI_HIP_DECODER_MATVEC_ONLY mode: same
     kernels, weights and arguments, the other kernels of the step left out)."""
     from fortai_amd import backend as B
     d = model.d
-    os.environ["FORTAI_HIP_DECODER_MATVEC_ONLY"] = "1"
-    try:
-        dec = B.Decoder(model.ctx, model.recurrent, model.attention,
-                        [model.q8[f"blk.{i}.ffn_gate.weight"] for i in range(d.layers)],
-                        [model.q8[f"blk.{i}.ffn_up.weight"] for i in range(d.layers)],
-                        [model.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
-                        [n["attn"] for n in model.norms], [n["post"] for n in model.norms], model.output_norm,
-                        d.hidden, model.embedding, model.output, 64, d.eps, d.vocab)
-    finally:
-        os.environ.pop("FORTAI_HIP_DECODER_MATVEC_ONLY", None)
+    dec = B.Decoder(model.ctx, model.recurrent, model.attention,
+                    [model.q8[f"blk.{i}.ffn_gate.weight"] for i in range(d.layers)],
+                    [model.q8[f"blk.{i}.ffn_up.weight"] for i in range(d.layers)],
+                    [model.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
+                    [n["attn"] for n in model.norms], [n["post"] for n in model.norms], model.output_norm,
+                    d.hidden, model.embedding, model.output, 64, d.eps, d.vocab)
+    dec.set_mode(matvec_only=True)
     try:
         ctx = model.ctx
         launches = sum(1 for step in dec.plan() if "q8_matvec" in step[1])
@@ -336,13 +333,13 @@ def traffic_probe(reps: int = 5, decode_model: str = None, decode_only: bool = F
 
 
 PROBE_STEPS = 8
+DIRECT = False  # --no-graph: the decoders enqueue their kernels every step (kernel tracing)
 
 
 def decode_probe(path: str) -> None:
     """PROBE_STEPS decode steps of the 0.8B model with direct launches."""
-    os.environ["FORTAI_HIP_DECODER_GRAPH"] = "0"
     from fortai_amd.qwen35 import Qwen35Hip
-    model = Qwen35Hip(path, max_context=256)
+    model = Qwen35Hip(path, max_context=256, direct=True)
     model.reset()
     model.generate(START_TOKEN, PROBE_STEPS, 0)
     model.ctx.synchronize()
@@ -512,7 +509,7 @@ def bench_attention(cases=((1024, None), (4096, None), (32768, None), (32768, 1 
     """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7; one K/V
     append at position L-1, then attention over 0..L-1, through
     fortai_hip_qwen35_attention_core_device (scores kernel + exact two-pass
-    output kernel up to FORTAI_HIP_EXACT_ATTENTION_MAX positions, split-K
+    output kernel up to the layer's exact_max positions, split-K
     beyond), replayed from a captured graph (one context per case).  A case
     is (L, exact_max); exact_max None is the default (8192)."""
     import numpy as np
@@ -524,16 +521,11 @@ def bench_attention(cases=((1024, None), (4096, None), (32768, None), (32768, 1 
         rng = np.random.default_rng(L)
         ws = [_q8(ctx, rng, heads * 2 * head, H), _q8(ctx, rng, kvh * head, H), _q8(ctx, rng, kvh * head, H),
               _q8(ctx, rng, H, heads * head)]
-        saved = os.environ.get("FORTAI_HIP_EXACT_ATTENTION_MAX")
-        if exact_max is not None:
-            os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = str(exact_max)
         A = B.Attention(ctx, *ws, (1 + 0.05 * rng.standard_normal(head)).astype(np.float32),
                         (1 + 0.05 * rng.standard_normal(head)).astype(np.float32), heads, kvh, head, head, L, 64,
                         1.0e7, 1e-6)
-        if saved is None:
-            os.environ.pop("FORTAI_HIP_EXACT_ATTENTION_MAX", None)
-        else:
-            os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = saved
+        if exact_max is not None:
+            A.set_exact_max(exact_max)
         path = "exact two-pass" if L <= (8192 if exact_max is None else exact_max) else "split-K (1e-3)"
         n = L * kvh * head
         A.set_cache(rng.standard_normal(n).astype(np.float16).view(np.uint16),
@@ -640,7 +632,7 @@ def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: in
     8192: a 512-token prefill of every sequence, then batch-8 greedy decode
     from the prefilled state.  The default prefill is bit-exact (projections
     in the reference's lane order on the matrix cores, the exact causal
-    attention); FORTAI_HIP_PREFILL=fast (whole-block dots, fp16 matrix-core
+    attention); the 'fast' prefill mode (whole-block dots, fp16 matrix-core
     attention) is timed as a separate variant.  `check` sequences are decoded
     token by token with the single-sequence decoder and compared bit for bit."""
     import ctypes
@@ -655,20 +647,20 @@ def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: in
         synth.write_model(path + ".part", synth.CONFIGS["qwen35-4b"])
         os.replace(path + ".part", path)
         log(f"  done in {time.time() - t:.1f}s")
-    m = Qwen35Hip(path, max_context=ctx, batch=batch)
+    m = Qwen35Hip(path, max_context=ctx, batch=batch, direct=DIRECT)
     d, ctxh = m.d, m.ctx
     rng = np.random.default_rng(0x51E5)
     prompts = rng.integers(0, d.vocab, size=(batch, prompt))
 
     def prefill(mode):
-        os.environ["FORTAI_HIP_PREFILL"] = mode
+        m.batch.set_prefill_mode(mode)
         try:
             m.batch.reset()
             m.batch.prefill(prompts)  # the first call allocates the prefill buffers
             m.batch.reset()
             return m.batch.prefill(prompts)
         finally:
-            os.environ.pop("FORTAI_HIP_PREFILL", None)
+            m.batch.set_prefill_mode("exact")
 
     _, fast_ms = prefill("fast")
     nxt, prefill_ms = prefill("exact")
@@ -736,7 +728,7 @@ def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: in
                     "path": "projections in the reference's eight-lane fp32 order on v_mfma_f32_32x32x4_2b_f16 "
                             "(q8_mmq_exact_kernel); conv1d, delta rule and exact causal attention over time",
                     "fast_variant": {"ms": round(fast_ms, 2), "tokens_per_s": round(tokens / (fast_ms * 1e-3), 1),
-                                     "path": "FORTAI_HIP_PREFILL=fast: whole-block int32 dots on "
+                                     "path": "prefill mode fast: whole-block int32 dots on "
                                              "v_mfma_i32_32x32x32_i8, fp16 matrix-core attention (not bit-exact)"}},
         "decode": {"batch": batch, "positions": f"{prompt + warmup}..{prompt + warmup + steps - 1}",
                    "ms_per_step": round(step_ms, 4), "tokens_per_s": round(batch * steps / (dec_ms * 1e-3), 1),
@@ -862,8 +854,8 @@ def main() -> int:
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps)
         return 0
-    if args.no_graph:
-        os.environ["FORTAI_HIP_DECODER_GRAPH"] = "0"
+    global DIRECT
+    DIRECT = bool(args.no_graph)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the decode step is a batch-1 single-GPU path); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)

@@ -33,6 +33,7 @@ _SIGNATURES = {
     "fortai_hip_q8_context_capture_end": [_vp],
     "fortai_hip_q8_context_graph_launch": [_vp],
     "fortai_hip_q8_context_synchronize": [_vp],
+    "fortai_hip_q8_context_scratch_bytes": [_vp, C.POINTER(C.c_size_t)],
     "fortai_hip_q8_context_timer_start": [_vp],
     "fortai_hip_q8_context_timer_stop": [_vp, _fp],
     "fortai_hip_q8_weights_upload": [_vp, _vp, _sz, _i, _i, _vpp],
@@ -112,11 +113,22 @@ _SIGNATURES = {
     "fortai_hip_qwen35_batch_replay": [_vp, _i],
     "fortai_hip_qwen35_batch_logits": [_vp, _vpp],
     "fortai_hip_qwen35_batch_prefill": [_vp, _vp, _i, _vp, _vp, _fp],
+    "fortai_hip_qwen35_attention_set_exact_max": [_vp, _i],
+    "fortai_hip_qwen35_attention_set_test_options": [_vp, _i, _i],
+    "fortai_hip_qwen35_decoder_set_mode": [_vp, _i],
+    "fortai_hip_qwen35_batch_set_mode": [_vp, _i],
+    "fortai_hip_qwen35_batch_set_prefill_mode": [_vp, _i],
 }
 _RESTYPE = {"fortai_hip_q8_last_error": C.c_char_p, "fortai_hip_q8_tokens_bytes": C.c_size_t,
             "fortai_hip_q8_pack_bytes": C.c_size_t}
 
 _lib: Optional[C.CDLL] = None
+
+
+# option values of include/fortai_hip_backend.h
+DECODER_DIRECT = 1
+DECODER_MATVEC_ONLY = 2
+PREFILL_MODES = {"exact": 0, "matvec": 1, "fast": 2}
 
 
 class BackendError(RuntimeError):
@@ -188,6 +200,12 @@ class Context:
 
     def set_position(self, position: int) -> None:
         self.call("fortai_hip_q8_context_set_position", self.h, position)
+
+    def scratch_bytes(self) -> int:
+        """Bytes of the scratch buffers this context has allocated on demand."""
+        n = C.c_size_t()
+        self.call("fortai_hip_q8_context_scratch_bytes", self.h, C.byref(n))
+        return n.value
 
     def synchronize(self) -> None:
         self.call("fortai_hip_q8_context_synchronize", self.h)
@@ -362,6 +380,15 @@ class Attention:
     def reset(self) -> None:
         self.ctx.call("fortai_hip_qwen35_attention_reset", self.h)
 
+    def set_exact_max(self, exact_max: int) -> None:
+        """Positions up to which the output keeps the reference's summation
+        orders (default 8192); split-K beyond.  Before a decoder is created."""
+        self.ctx.call("fortai_hip_qwen35_attention_set_exact_max", self.h, exact_max)
+
+    def set_test_options(self, z_skew: int = 0, force_wide: bool = False) -> None:
+        """Test only: shift the Z candidate windows; the wide output kernel for one sequence."""
+        self.ctx.call("fortai_hip_qwen35_attention_set_test_options", self.h, z_skew, 1 if force_wide else 0)
+
     def cache(self, positions: int):
         d = self.dims
         k = np.empty(positions * d["kv_heads"] * d["head_size"], dtype=np.uint16)
@@ -411,6 +438,12 @@ class Decoder:
 
     def reset(self) -> None:
         self.ctx.call("fortai_hip_qwen35_decoder_reset", self.h)
+
+    def set_mode(self, direct: bool = False, matvec_only: bool = False) -> None:
+        """direct: enqueue the kernels every step instead of a graph replay
+        (kernel tracing); matvec_only: a timing probe of the Q8_0 projections."""
+        self.ctx.call("fortai_hip_qwen35_decoder_set_mode", self.h,
+                      (DECODER_DIRECT if direct else 0) | (DECODER_MATVEC_ONLY if matvec_only else 0))
 
     def forward(self, token: int, position: int, want_logits: bool = True) -> int:
         nxt = np.zeros(1, dtype=np.int64)
@@ -485,6 +518,13 @@ class BatchDecoder:
 
     def reset(self) -> None:
         self.ctx.call("fortai_hip_qwen35_batch_reset", self.h)
+
+    def set_mode(self, direct: bool = False) -> None:
+        self.ctx.call("fortai_hip_qwen35_batch_set_mode", self.h, DECODER_DIRECT if direct else 0)
+
+    def set_prefill_mode(self, mode: str) -> None:
+        """'exact' (default), 'matvec' (same bits) or 'fast' (not bit-exact)."""
+        self.ctx.call("fortai_hip_qwen35_batch_set_prefill_mode", self.h, PREFILL_MODES[mode])
 
     def forward(self, tokens, positions, want_logits: bool = True) -> np.ndarray:
         t, p = self._inputs(tokens, positions)

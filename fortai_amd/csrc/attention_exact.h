@@ -39,7 +39,7 @@ __device__ __forceinline__ void norm_rope(float *v, int head, const float *w, fl
     ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(head)) + eps);
     for (int i = lane; i < head; i += 64) v[i] = (v[i] * inv) * w[i];
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_fence();
     const int half = rope_dim / 2;
     for (int i = lane; i < half; i += 64) {
         const float2 cs = rope[i];
@@ -47,7 +47,7 @@ __device__ __forceinline__ void norm_rope(float *v, int head, const float *w, fl
         v[i] = a * cs.x - b * cs.y;
         v[i + half] = a * cs.y + b * cs.x;
     }
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_fence();
 }
 
 // The same with the weights in registers: wr[j] = w[lane + 64 j] (loaded by
@@ -62,7 +62,7 @@ __device__ __forceinline__ void norm_rope_regs(float *v, int head, const float (
 #pragma unroll
     for (int j = 0; j < NW; ++j)
         if (lane + 64 * j < head) v[lane + 64 * j] = (v[lane + 64 * j] * inv) * wr[j];
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_fence();
     const int half = rope_dim / 2;
     for (int i = lane; i < half; i += 64) {
         const float2 cs = rope[i];
@@ -70,7 +70,7 @@ __device__ __forceinline__ void norm_rope_regs(float *v, int head, const float (
         v[i] = a * cs.x - b * cs.y;
         v[i + half] = a * cs.y + b * cs.x;
     }
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_fence();
 }
 
 // One position's score: the sequential dot of fortai_qwen35_cpu.f90:1009-1014.

@@ -16,6 +16,7 @@
 #include <cstring>
 #include <new>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 #include <vector>
 #include <initializer_list>
@@ -49,6 +50,7 @@ struct fortai_hip_q8_context {
     void *scratch_q8l = nullptr;  // quantized FFN hidden of the ABI FFN paths
     size_t scratch_q8l_bytes = 0;
     void *noalloc_scratch = nullptr;  // device address of this GPU's `scratch` array (set at create)
+    hipEvent_t noalloc_done = nullptr;  // recorded after this context's last use of that array
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     char error[256] = {};
@@ -104,10 +106,15 @@ struct fortai_hip_qwen35_attention {
     int *cache_flags = nullptr;  // per kv head: the cache holds an exponent-31 half
     float *attn_out = nullptr;   // gated attention output (o_proj input)
     int exact_max = 0;           // positions with the bit-exact two-pass softmax; split-K beyond
-    int z_skew = 0;              // test hook: offset of the Z candidate windows (FORTAI_HIP_ZTABLE_SKEW)
-    int force_wide = 0;          // test hook: the wide output kernel for one sequence (FORTAI_HIP_ATTENTION_WIDE)
+    int z_skew = 0;              // test option: offset of the Z candidate windows
+    int force_wide = 0;          // test option: the wide output kernel for one sequence
     float *split = nullptr;      // split-K partials (allocated when max_context > exact_max)
 };
+
+constexpr int kDefaultExactMax = 8192;
+// prompt prefill projections: the exact token-block product (default), the
+// batched decode matvec (same bits), or whole-block int32 dots (not exact)
+enum class PrefillMode { EXACT = 0, MATVEC = 1, FAST = 2 };
 
 struct decoder_layer {
     fortai_hip_qwen35_recurrent *recurrent = nullptr;
@@ -133,10 +140,10 @@ struct fortai_hip_qwen35_decoder {
     bool use_graph = true;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
-    // FORTAI_HIP_DECODER_MATVEC_ONLY=1 at create: a step enqueues only its
-    // Q8_0 matvec launches (same kernels, weights and arguments; the other
-    // kernels are left out, so the values are meaningless) -- for timing
-    // the matvec family of a decode step
+    // FORTAI_HIP_DECODER_MATVEC_ONLY mode: a step enqueues only its Q8_0
+    // matvec launches (same kernels, weights and arguments; the other kernels
+    // are left out, so the values are meaningless) -- for timing the matvec
+    // family of a decode step
     bool matvec_only = false;
     std::vector<plan_step> plan;  // the launches of one step (PlanIR steps)
 };
@@ -182,7 +189,8 @@ struct fortai_hip_qwen35_batch {
     float *palpha = nullptr, *pbeta = nullptr, *pqinv = nullptr, *pkinv = nullptr, *pbt = nullptr, *pdt = nullptr;
     int64_t *ptokens = nullptr;
     void *pq8l = nullptr;                                  // exact mode: 8 tokens in the matvec layout
-    bool use_graph = true;            // FORTAI_HIP_DECODER_GRAPH=0: enqueue the kernels every step
+    bool use_graph = true;            // FORTAI_HIP_DECODER_DIRECT mode: enqueue the kernels every step
+    PrefillMode prefill_mode = PrefillMode::EXACT;
     std::vector<plan_step> plan, prefill_plan;  // launches of one step / of the last prefill
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -461,6 +469,19 @@ extern "C" {
 constexpr size_t kNoAllocScratchBytes = 8 * 18432;  // batch 8 x q8l_bytes(16384)
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
+// The last user of each GPU's array: its context (stream) and the event
+// recorded after its launches.  A call from another context makes its own
+// stream wait for that event first, so calls from different contexts on one
+// GPU run one after the other instead of overwriting each other's
+// activations; calls on one stream are in order anyway.
+constexpr int kNoAllocDevices = 64;
+struct NoAllocUser {
+    fortai_hip_q8_context *context = nullptr;
+    hipEvent_t done = nullptr;
+};
+std::mutex g_noalloc_mutex;
+NoAllocUser g_noalloc_user[kNoAllocDevices];
+
 // ------------------------------------------------------------------ context
 // fortai_cuda_backend.cu:805-833
 int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context) {
@@ -473,6 +494,7 @@ int fortai_hip_q8_context_create(int device, fortai_hip_q8_context **context) {
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&c->start);
     if (e == hipSuccess) e = hipEventCreate(&c->stop);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->noalloc_done, hipEventDisableTiming);
     if (e == hipSuccess) e = alloc(&c->position, 1);
     if (e == hipSuccess) e = alloc(&c->token, 1);
     if (e == hipSuccess) e = alloc(&c->argmax_value, kArgmaxParts);
@@ -500,6 +522,11 @@ int fortai_hip_q8_context_destroy(fortai_hip_q8_context *c) {
     if (!c) return FORTAI_HIP_OK;
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->device < kNoAllocDevices) {
+        std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+        if (g_noalloc_user[c->device].context == c) g_noalloc_user[c->device] = NoAllocUser{};
+    }
+    if (c->noalloc_done) (void)hipEventDestroy(c->noalloc_done);
     if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
     release(c->position); release(c->token); release(c->scratch_act); release(c->scratch_out);
@@ -784,8 +811,18 @@ int fortai_hip_q8_matvec_device_f32(fortai_hip_q8_context *c, const fortai_hip_q
         return FORTAI_HIP_INVALID;
     (void)hipSetDevice(c->device);
     const MatvecSegment s = segment(w, static_cast<float *>(device_output));
-    return done(c, launch_q8_matvec(&s, 1, f32_input(static_cast<const float *>(device_activation), w->width),
-        Prologue::F32, Epilogue::STORE, c->stream), "device F32 matvec");
+    const MatvecInput in = f32_input(static_cast<const float *>(device_activation), w->width);
+    if (w->width <= kMatvecF32MaxWidth)
+        return done(c, launch_q8_matvec(&s, 1, in, Prologue::F32, Epilogue::STORE, c->stream), "device F32 matvec");
+    // wider than the in-kernel quantizer holds (e.g. the 4B FFN down, 9216):
+    // quantize once into the Q8L layout (the same quantizer, so the same
+    // bits), then the matvec reads it as a producer-quantized activation
+    if (w->width > kQ8lPrepMaxWidth) return FORTAI_HIP_INVALID;
+    hipError_t e = ensure_scratch(c, 0, 0, q8l_bytes(w->width));
+    if (e == hipSuccess) e = launch_q8l_prep(in, Prologue::F32, c->scratch_q8l, 1, c->stream);
+    if (e == hipSuccess)
+        e = launch_q8_matvec(&s, 1, q8l_input(c->scratch_q8l, w->width), Prologue::Q8L, Epilogue::STORE, c->stream);
+    return done(c, e, "device F32 matvec (wide)");
 }
 
 // fortai_cuda_backend.cu:1041-1055
@@ -885,6 +922,12 @@ int fortai_hip_q8_block_dots_device(fortai_hip_q8_context *c, const fortai_hip_q
 }
 
 // ------------------------------------------------------ batched matvec
+int fortai_hip_q8_context_scratch_bytes(const fortai_hip_q8_context *c, size_t *bytes) {
+    if (!c || !bytes) return FORTAI_HIP_INVALID;
+    *bytes = c->scratch_act_bytes + c->scratch_out_bytes + c->scratch_aux_bytes + c->scratch_q8l_bytes;
+    return FORTAI_HIP_OK;
+}
+
 int fortai_hip_q8_batch_matvec_noalloc(fortai_hip_q8_context *c, const fortai_hip_q8_weights *w, const void *x,
     int batch, void *out) {
     if (!c || !owned(c, w) || !x || !out || batch < 1 || batch > 8) return FORTAI_HIP_INVALID;
@@ -896,12 +939,20 @@ int fortai_hip_q8_batch_matvec_noalloc(fortai_hip_q8_context *c, const fortai_hi
         return fail(c, FORTAI_HIP_INVALID, msg);
     }
     if (!c->noalloc_scratch) return fail(c, FORTAI_HIP_RUNTIME_ERROR, "batch_matvec_noalloc: scratch address unavailable");
+    if (c->device >= kNoAllocDevices) return fail(c, FORTAI_HIP_INVALID, "batch_matvec_noalloc: device index");
     (void)hipSetDevice(c->device);
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    NoAllocUser &user = g_noalloc_user[c->device];
+    hipError_t e = hipSuccess;
+    // another context's calls on this GPU: wait for them (no overlap on the array)
+    if (user.context && user.context != c) e = hipStreamWaitEvent(c->stream, user.done, 0);
     // the prologue writes every byte the matvec reads (padding blocks as zeros)
     MatvecInput in = f32_input(static_cast<const float *>(x), w->width);
-    hipError_t e = launch_q8l_prep(in, Prologue::F32, c->noalloc_scratch, batch, c->stream);
+    if (e == hipSuccess) e = launch_q8l_prep(in, Prologue::F32, c->noalloc_scratch, batch, c->stream);
     const MatvecSegment seg = segment(w, static_cast<float *>(out));
     if (e == hipSuccess) e = launch_q8_batch_matvec(&seg, 1, c->noalloc_scratch, w->width, batch, Epilogue::STORE, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(c->noalloc_done, c->stream);
+    if (e == hipSuccess) user = NoAllocUser{c, c->noalloc_done};
     return done(c, e, "batched matvec (no allocation)");
 }
 
@@ -1363,16 +1414,11 @@ int fortai_hip_qwen35_attention_create(fortai_hip_q8_context *c, const fortai_hi
     if (e == hipSuccess) e = fuse_q8({q, k, v}, &A->in_m, &A->in_quants, &A->in_scales, c->stream);
     if (e == hipSuccess) e = alloc(&A->attn_out, static_cast<size_t>(heads) * value_size);
     if (e == hipSuccess) e = alloc(&A->partial, attention_scores_floats(heads, max_context));
-    // FORTAI_HIP_EXACT_ATTENTION_MAX: the positions up to which the attention
-    // output keeps the reference's summation orders (default 8192); beyond
-    // them the split-K path (within 1e-3 relative) takes over
-    A->exact_max = 8192;
-    if (const char *env = std::getenv("FORTAI_HIP_EXACT_ATTENTION_MAX")) A->exact_max = std::max(0, std::atoi(env));
-    // test hook: shift every Z candidate window by this many floats, so that
-    // the running sums fall outside them and resolve_z's own chain runs
-    if (const char *env = std::getenv("FORTAI_HIP_ZTABLE_SKEW")) A->z_skew = std::atoi(env);
-    // test hook: the batches' wide output kernel for a single sequence too
-    if (const char *env = std::getenv("FORTAI_HIP_ATTENTION_WIDE")) A->force_wide = std::atoi(env) != 0;
+    // the positions up to which the attention output keeps the reference's
+    // summation orders (default 8192); beyond them the split-K path (within
+    // 1e-3 relative) takes over.  fortai_hip_qwen35_attention_set_exact_max
+    // changes it.
+    A->exact_max = kDefaultExactMax;
     if (e == hipSuccess && max_context > A->exact_max)
         e = alloc(&A->split, static_cast<size_t>(heads) * attention_split_chunks(max_context) * (value_size + 2));
     if (e == hipSuccess) e = alloc(&A->cache_flags, kv_heads);
@@ -1554,6 +1600,27 @@ hipError_t enqueue_lm_head(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
     if (e == hipSuccess) e = rec(launch_argmax(d->logits, d->vocab, st, stream), "greedy argmax");
     return e;
 }
+// The decode step as one captured graph (unless the decoder is in direct
+// mode); the plan is recorded at capture (direct mode: by the first step).
+hipError_t capture_decoder(fortai_hip_qwen35_decoder *d) {
+    auto *c = d->context;
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    d->exec = nullptr;
+    d->graph = nullptr;
+    d->plan.clear();
+    if (!d->use_graph) return hipSuccess;
+    hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return e;
+    g_plan = &d->plan;
+    g_plan_batch = 1;
+    const hipError_t ce = enqueue_decoder_step(d, c->stream);
+    g_plan = nullptr;
+    e = hipStreamEndCapture(c->stream, &d->graph);
+    if (ce != hipSuccess) e = ce;
+    if (e == hipSuccess) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
+    return e;
+}
 hipError_t run_step(fortai_hip_qwen35_decoder *d) {
     // the plan is recorded by the first step (at capture for the graph)
     std::vector<plan_step> *saved = g_plan;
@@ -1640,21 +1707,7 @@ int fortai_hip_qwen35_decoder_create(fortai_hip_q8_context *c, int layer_count,
     if (e == hipSuccess) e = alloc(&d->embed, 1);
     if (e == hipSuccess) e = hipMemsetAsync(d->embed, 0, sizeof(int64_t), c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (const char *env = std::getenv("FORTAI_HIP_DECODER_MATVEC_ONLY")) d->matvec_only = std::strcmp(env, "1") == 0;
-    // the per-op decode step captured as a graph (FORTAI_HIP_DECODER_GRAPH=0
-    // enqueues the kernels directly every step instead, e.g. for kernel tracing)
-    const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
-    d->use_graph = !(graph_env && std::strcmp(graph_env, "0") == 0);
-    if (e == hipSuccess && d->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
-    if (e == hipSuccess && d->use_graph) {
-        g_plan = &d->plan;
-        g_plan_batch = 1;
-        const hipError_t ce = enqueue_decoder_step(d, c->stream);
-        g_plan = nullptr;
-        e = hipStreamEndCapture(c->stream, &d->graph);
-        if (ce != hipSuccess) e = ce;
-    }
-    if (e == hipSuccess && d->use_graph) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
+    if (e == hipSuccess) e = capture_decoder(d);
     if (e != hipSuccess) {
         fortai_hip_qwen35_decoder_destroy(d);
         return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen decoder create", e);
@@ -1764,7 +1817,7 @@ int fortai_hip_qwen35_decoder_logits(fortai_hip_qwen35_decoder *d, void **logits
 }
 
 int fortai_hip_qwen35_decoder_trace(fortai_hip_qwen35_decoder *d, int first, int count, int64_t *host_trace) {
-    if (!d || !host_trace || first < 0 || count <= 0 || first + count > d->max_context) return FORTAI_HIP_INVALID;
+    if (!d || !host_trace || first < 0 || count <= 0 || count > d->max_context - first) return FORTAI_HIP_INVALID;
     auto *c = d->context;
     (void)hipSetDevice(c->device);
     hipError_t e = hipMemcpyAsync(host_trace, d->trace + first, static_cast<size_t>(count) * sizeof(int64_t),
@@ -1931,6 +1984,28 @@ int batch_set_inputs(fortai_hip_qwen35_batch *b, const int64_t *tokens, const in
 }
 }  // namespace
 
+// One batched step as a captured graph (unless in direct mode).
+hipError_t capture_batch(fortai_hip_qwen35_batch *b) {
+    auto *c = b->context;
+    if (b->exec) (void)hipGraphExecDestroy(b->exec);
+    if (b->graph) (void)hipGraphDestroy(b->graph);
+    b->exec = nullptr;
+    b->graph = nullptr;
+    b->plan.clear();
+    if (!b->use_graph) return hipSuccess;
+    hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return e;
+    g_plan = &b->plan;
+    g_plan_batch = b->batch;
+    const hipError_t ce = enqueue_batch_step(b, c->stream);
+    g_plan = nullptr;
+    g_plan_batch = 1;
+    e = hipStreamEndCapture(c->stream, &b->graph);
+    if (ce != hipSuccess) e = ce;
+    if (e == hipSuccess) e = hipGraphInstantiate(&b->exec, b->graph, nullptr, nullptr, 0);
+    return e;
+}
+
 int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *c, int batch, int layer_count,
     fortai_hip_qwen35_recurrent *const *recurrent, fortai_hip_qwen35_attention *const *attention,
     const fortai_hip_q8_weights *const *ffn_gate, const fortai_hip_q8_weights *const *ffn_up,
@@ -2023,21 +2098,8 @@ int fortai_hip_qwen35_batch_create(fortai_hip_q8_context *c, int batch, int laye
     if (e == hipSuccess) e = hipMemsetAsync(b->positions, 0, B * sizeof(int), c->stream);
     if (e == hipSuccess) e = batch_zero_state(b, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    // one step captured as a graph (state, tokens and positions are device-side);
-    // FORTAI_HIP_DECODER_GRAPH=0 enqueues the kernels directly (kernel tracing)
-    const char *graph_env = std::getenv("FORTAI_HIP_DECODER_GRAPH");
-    b->use_graph = !(graph_env && std::strcmp(graph_env, "0") == 0);
-    if (e == hipSuccess && b->use_graph) e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
-    if (e == hipSuccess && b->use_graph) {
-        g_plan = &b->plan;
-        g_plan_batch = batch;
-        const hipError_t ce = enqueue_batch_step(b, c->stream);
-        g_plan = nullptr;
-        g_plan_batch = 1;
-        e = hipStreamEndCapture(c->stream, &b->graph);
-        if (ce != hipSuccess) e = ce;
-    }
-    if (e == hipSuccess && b->use_graph) e = hipGraphInstantiate(&b->exec, b->graph, nullptr, nullptr, 0);
+    // one step captured as a graph (state, tokens and positions are device-side)
+    if (e == hipSuccess) e = capture_batch(b);
     if (e != hipSuccess) {
         fortai_hip_qwen35_batch_destroy(b);
         return fail(c, FORTAI_HIP_RUNTIME_ERROR, "Qwen batch create", e);
@@ -2204,7 +2266,6 @@ hipError_t batch_prefill_buffers(fortai_hip_qwen35_batch *b, int rows) {
 //    reference, not bit for bit);
 //  matvec: the projections through the batched decode matvec, 8 tokens at a
 //    time (a cross-check of the exact mode).
-enum class PrefillMode { EXACT, FAST, MATVEC };
 hipError_t enqueue_batch_prefill(fortai_hip_qwen35_batch *b, int T, PrefillMode mode, hipStream_t stream) {
     const int B = b->batch, H = b->hidden, N = B * T;
     hipError_t e = rec(b->emb16 ? launch_f16_embedding(b->emb16->data, b->emb16->rows, H, b->ptokens, 0, b->px, stream, N)
@@ -2322,12 +2383,7 @@ int fortai_hip_qwen35_batch_prefill(fortai_hip_qwen35_batch *b, const int64_t *t
     if (e == hipSuccess) e = hipMemcpyAsync(b->positions, last.data(), b->batch * sizeof(int), hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);  // the host arrays are borrowed for the call
     if (e == hipSuccess && kernel_ms) e = hipEventRecord(c->start, c->stream);
-    PrefillMode mode = PrefillMode::EXACT;
-    if (const char *env = std::getenv("FORTAI_HIP_PREFILL")) {
-        if (std::strcmp(env, "fast") == 0) mode = PrefillMode::FAST;
-        else if (std::strcmp(env, "matvec") == 0) mode = PrefillMode::MATVEC;
-        else if (std::strcmp(env, "exact") != 0) return fail(c, FORTAI_HIP_INVALID, "FORTAI_HIP_PREFILL: exact, fast or matvec");
-    }
+    const PrefillMode mode = b->prefill_mode;
     b->prefill_plan.clear();
     g_plan = &b->prefill_plan;
     g_plan_batch = static_cast<int>(N);
@@ -2358,5 +2414,53 @@ int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *b, void **logits) {
     return FORTAI_HIP_OK;
 }
 
+// ---- options (explicit calls; nothing is read from the environment) ----
+
+int fortai_hip_qwen35_attention_set_exact_max(fortai_hip_qwen35_attention *A, int exact_max) {
+    if (!A || !A->context || exact_max < 0) return FORTAI_HIP_INVALID;
+    auto *c = A->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipSuccess;
+    if (A->max_context > exact_max && !A->split)
+        e = alloc(&A->split, static_cast<size_t>(A->heads) * attention_split_chunks(A->max_context) * (A->value + 2));
+    if (e == hipSuccess) A->exact_max = exact_max;
+    return done(c, e, "Qwen attention exact_max");
+}
+
+int fortai_hip_qwen35_attention_set_test_options(fortai_hip_qwen35_attention *A, int z_skew, int force_wide) {
+    if (!A || !A->context) return FORTAI_HIP_INVALID;
+    A->z_skew = z_skew;
+    A->force_wide = force_wide != 0;
+    return FORTAI_HIP_OK;
+}
+
+int fortai_hip_qwen35_decoder_set_mode(fortai_hip_qwen35_decoder *d, int flags) {
+    if (!d || (flags & ~(FORTAI_HIP_DECODER_DIRECT | FORTAI_HIP_DECODER_MATVEC_ONLY))) return FORTAI_HIP_INVALID;
+    auto *c = d->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    d->use_graph = !(flags & FORTAI_HIP_DECODER_DIRECT);
+    d->matvec_only = (flags & FORTAI_HIP_DECODER_MATVEC_ONLY) != 0;
+    if (e == hipSuccess) e = capture_decoder(d);
+    return done(c, e, "Qwen decoder mode");
+}
+
+int fortai_hip_qwen35_batch_set_mode(fortai_hip_qwen35_batch *b, int flags) {
+    if (!b || (flags & ~FORTAI_HIP_DECODER_DIRECT)) return FORTAI_HIP_INVALID;
+    auto *c = b->context;
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    b->use_graph = !(flags & FORTAI_HIP_DECODER_DIRECT);
+    if (e == hipSuccess) e = capture_batch(b);
+    return done(c, e, "Qwen batch mode");
+}
+
+int fortai_hip_qwen35_batch_set_prefill_mode(fortai_hip_qwen35_batch *b, int mode) {
+    if (!b || mode < FORTAI_HIP_PREFILL_EXACT || mode > FORTAI_HIP_PREFILL_FAST) return FORTAI_HIP_INVALID;
+    b->prefill_mode = static_cast<PrefillMode>(mode);
+    return FORTAI_HIP_OK;
+}
+
 }  // extern "C"
+
 

@@ -224,6 +224,13 @@ __device__ __forceinline__ float softplus_ref(float v) {
 // copy completes before the kernel's next barrier), so that each lookup is an
 // LDS read instead of a data-dependent memory round trip.  Same values, so
 // the same results.
+// Cross-lane exchange through LDS within one wave: the writes of every lane
+// are ordered before the reads that follow (no workgroup barrier needed).
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 struct MathTables {
     uint64_t exp2[32];
     double logc[16][2];
@@ -231,6 +238,13 @@ struct MathTables {
         const int t = static_cast<int>(threadIdx.x);
         if (t < 32) exp2[t] = kExpf2Table[t];
         else if (t < 64) logc[(t - 32) >> 1][t & 1] = kLogfTable[(t - 32) >> 1][t & 1];
+    }
+    // load() for kernels whose tables are read only by wave 0 (threads 0..63
+    // write them all) before any workgroup barrier: a wavefront-scope fence
+    // orders the lanes' LDS writes before the reads that follow
+    __device__ __forceinline__ void load_wave0() {
+        load();
+        wave_lds_fence();
     }
     __device__ __forceinline__ float expf(float x) const { return expf_libm_t(x, exp2); }
     __device__ __forceinline__ float logf(float x) const { return logf_libm_t(x, logc); }

@@ -90,6 +90,12 @@ const char *last_launch();
 const char *prologue_name(Prologue p);
 const char *epilogue_name(Epilogue e);
 
+// Activation widths: the fp32-input prologues quantize up to
+// kMatvecF32MaxWidth values in-kernel; the Q8L layout (producer-quantized, or
+// launch_q8l_prep) serves up to kQ8lPrepMaxWidth.
+constexpr int kMatvecF32MaxWidth = 8192;
+constexpr int kQ8lPrepMaxWidth = 12288;
+
 // Evaluate up to four matrices that share one activation in one launch.
 hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const MatvecInput &in,
     Prologue prologue, Epilogue epilogue, hipStream_t stream);

@@ -175,8 +175,8 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_recurrence_kernel(const Gdn
     __shared__ float vs[kDeltaRows];
     __shared__ double red[2];
     __shared__ float hs[2];
-    __shared__ MathTables mt;  // written and read by wave 0 (thread 0 uses it), in order
-    mt.load();
+    __shared__ MathTables mt;  // written and read by wave 0 (thread 0 uses it)
+    mt.load_wave0();
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks_per_head = HEAD / kDeltaRows;
     const int wg = xcd_grouped(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));

@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void qk_rope_append_kernel(float *__restrict__
         const float *src = isq ? q + (static_cast<size_t>(n) * heads + j) * 2 * head
                                : k + (static_cast<size_t>(n) * kv_heads + (j - heads)) * head;
         for (int i = lane; i < head; i += 64) b[i] = src[i];
-        __builtin_amdgcn_wave_barrier();
+        wave_lds_fence();
         ea::norm_rope(b, head, isq ? wq : wk, eps, rp, rope_dim, lane);
         if (isq) {
             float *dst = q + (static_cast<size_t>(n) * heads + j) * 2 * head;
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256) void qk_rope_append_kernel(float *__restrict__
             }
             if (__any(over) && lane == 0) flags[static_cast<size_t>(s) * kv_heads + kvh] = 1;
         }
-        __builtin_amdgcn_wave_barrier();
+        wave_lds_fence();
     }
     for (int e = tid; e < kv_heads * value; e += 256) {
         const int kvh = e / value, i = e % value;

@@ -332,7 +332,10 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
             else return sc[c];
         };
         if (active) {
-            if constexpr (kScLds) ws[lane] = scw[0];
+            if constexpr (kScLds) {
+                ws[lane] = scw[0];
+                wave_lds_fence();  // the row's lanes read each other's scales
+            }
             if (wave > 0) {
 #pragma unroll
                 for (int c = 0; c < kPer; ++c) {
@@ -372,6 +375,7 @@ __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs 
                 ws[k * 64 + lane] = scw[k];
                 if constexpr (kPair) ws[(kScLoads + k) * 64 + lane] = scw2[k];
             }
+            wave_lds_fence();  // the row's lanes read each other's scales
 #pragma unroll
             for (int c = 0; c < NREG; ++c) {
                 const uint4 a = act4[c * 8 + l];
@@ -590,7 +594,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
     // scale products fl(f32(w_scale) * a_scale) once per (matrix, row,
     // sequence, block) -- four per lane -- into its own LDS table, instead of
     // every lane of a row forming all of them; LDS operations of one wave
-    // complete in order, so the wave reads them back without a barrier
+    // read back after a wavefront-scope fence, without a workgroup barrier
     constexpr bool kTable = kPair && G == 1 && NS == 4;
     float *ptab = epi + kMaxBatch * 32 + (static_cast<int>(threadIdx.x) >> 6) * 2 * 8 * NS * 4;  // [2][8][NS][4]
 
@@ -689,7 +693,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
                 *reinterpret_cast<float2 *>(ptab + ((0 * 8 + r) * NS + ks) * 4 + j0) = make_float2(w0 * a0, w1 * a1);
                 *reinterpret_cast<float2 *>(ptab + ((1 * 8 + r) * NS + ks) * 4 + j0) = make_float2(v0 * a0, v1 * a1);
             }
-            __builtin_amdgcn_wave_barrier();
+            wave_lds_fence();
 #pragma unroll
             for (int k = 0; k < NS; ++k) {
                 const unsigned char *sbase = lds + static_cast<size_t>(sq[k]) * seq_bytes;
@@ -707,7 +711,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
                 acc2[k] = __builtin_fmaf(p2.z, d2.z, acc2[k]);
                 acc2[k] = __builtin_fmaf(p2.w, d2.w, acc2[k]);
             }
-            __builtin_amdgcn_wave_barrier();
+            wave_lds_fence();
             return;
         }
         float ws[G][4], ws2[kPair ? G : 1][4];
@@ -1159,17 +1163,12 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const flo
 // Which launches take the split form: single matrices of whole register
 // chunks that would otherwise run one-wave workgroups (their dot work then
 // spreads over four SIMDs) or the gated prologue (32 four-wave workgroups
-// would each move 70 KB for ssm_out).  FORTAI_HIP_MATVEC_SPLIT=0 turns it
-// off, 2 extends it to every eligible launch (measured slower for the large
-// four-wave projections).
+// would each move 70 KB for ssm_out).  The large four-wave projections keep
+// the unsplit form (measured faster).  Both forms give the same bits.
 bool matvec_split(int count, int chunks, Prologue prologue, Epilogue epilogue, int waves) {
-    static const int mode = [] {
-        const char *e = getenv("FORTAI_HIP_MATVEC_SPLIT");
-        return e ? atoi(e) : 1;
-    }();
-    if (mode <= 0 || count != 1 || epilogue == Epilogue::SILU_PAIR) return false;
+    if (count != 1 || epilogue == Epilogue::SILU_PAIR) return false;
     if (chunks != 8 && chunks != 16 && chunks != 28 && chunks != 32) return false;
-    return mode >= 2 || waves == 1 || prologue == Prologue::GATED;
+    return waves == 1 || prologue == Prologue::GATED;
 }
 
 hipError_t launch_q8_matvec(const MatvecSegment *segments, int count, const MatvecInput &in,

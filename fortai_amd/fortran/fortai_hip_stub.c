@@ -761,3 +761,41 @@ FORTAI_HIP_WEAK int fortai_hip_q8_weights_upload_packed(fortai_hip_q8_context *c
     if (weights) *weights = NULL;
     return FORTAI_HIP_RUNTIME_ERROR;
 }
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_attention_set_exact_max(fortai_hip_qwen35_attention *layer, int exact_max)
+{
+    (void)layer; (void)exact_max;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_attention_set_test_options(fortai_hip_qwen35_attention *layer, int z_skew,
+    int force_wide)
+{
+    (void)layer; (void)z_skew; (void)force_wide;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_decoder_set_mode(fortai_hip_qwen35_decoder *decoder, int flags)
+{
+    (void)decoder; (void)flags;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_set_mode(fortai_hip_qwen35_batch *batch_decoder, int flags)
+{
+    (void)batch_decoder; (void)flags;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_qwen35_batch_set_prefill_mode(fortai_hip_qwen35_batch *batch_decoder, int mode)
+{
+    (void)batch_decoder; (void)mode;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}
+
+FORTAI_HIP_WEAK int fortai_hip_q8_context_scratch_bytes(const fortai_hip_q8_context *context, size_t *bytes)
+{
+    (void)context;
+    if (bytes) *bytes = 0;
+    return FORTAI_HIP_RUNTIME_ERROR;
+}

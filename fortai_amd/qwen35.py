@@ -82,10 +82,13 @@ def read_dims(f: gguf.GGUFFile) -> Qwen35Dims:
 
 class Qwen35Hip:
     def __init__(self, path: str, max_context: int = 256, device: int = 0, fused: bool = True, batch: int = 0,
-                 pack_cache: Optional[str] = None):
+                 pack_cache: Optional[str] = None, direct: bool = False, exact_max: Optional[int] = None):
         """pack_cache: root of a repacked-weight cache (fortai_amd.pack_cache);
         the Q8_0 matrices are uploaded from it when it holds this GGUF's pack,
-        and the pack is written after a repacking upload otherwise."""
+        and the pack is written after a repacking upload otherwise.
+        direct: the decoders enqueue their kernels every step instead of
+        replaying a captured graph (same results; for kernel tracing).
+        exact_max: the attention layers' exact-softmax limit (default 8192)."""
         self.file = gguf.read(path)
         self.d = d = read_dims(self.file)
         self.max_context = max_context
@@ -140,6 +143,10 @@ class Qwen35Hip:
                     self.ctx, Q("attn_q.weight"), Q("attn_k.weight"), Q("attn_v.weight"), Q("attn_output.weight"),
                     T("attn_q_norm.weight").as_f32(), T("attn_k_norm.weight").as_f32(), d.heads, d.kv_heads,
                     d.head_size, d.value_size, max_context, d.rope_dim, d.rope_base, d.eps))
+        if exact_max is not None:
+            for a in self.attention:
+                if a is not None:
+                    a.set_exact_max(exact_max)
         self.output_norm = self.file.tensor("output_norm.weight").as_f32()
         self.decoder: Optional[B.Decoder] = None
         if fused:
@@ -150,6 +157,8 @@ class Qwen35Hip:
                 [self.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
                 [n["attn"] for n in self.norms], [n["post"] for n in self.norms], self.output_norm, d.hidden,
                 self.embedding, self.output, max_context, d.eps, d.vocab)
+            if direct:
+                self.decoder.set_mode(direct=True)
         self.batch: Optional[B.BatchDecoder] = None
         if batch:
             self.batch = B.BatchDecoder(
@@ -159,6 +168,8 @@ class Qwen35Hip:
                 [self.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
                 [n["attn"] for n in self.norms], [n["post"] for n in self.norms], self.output_norm, d.hidden,
                 self.embedding, self.output, max_context, d.eps, d.vocab)
+            if direct:
+                self.batch.set_mode(direct=True)
         self._ops = None
 
     # ---------------------------------------------------------------- fused

@@ -51,6 +51,9 @@ int fortai_hip_q8_context_set_position(fortai_hip_q8_context *context, int posit
 int fortai_hip_q8_context_capture_begin(fortai_hip_q8_context *context);
 int fortai_hip_q8_context_capture_end(fortai_hip_q8_context *context);
 int fortai_hip_q8_context_graph_launch(fortai_hip_q8_context *context);
+/* [extension] bytes of the scratch buffers the context has allocated on
+ * demand (quantized activations, FFN hidden, outputs of the host paths) */
+int fortai_hip_q8_context_scratch_bytes(const fortai_hip_q8_context *context, size_t *bytes);
 /* [extension] wait for all work queued on the context's stream */
 int fortai_hip_q8_context_synchronize(fortai_hip_q8_context *context);
 /* [extension] HIP events on the context's stream: timer_start records the
@@ -235,7 +238,9 @@ int fortai_hip_q8_batch_matvec_device(fortai_hip_q8_context *context,
  * activations go to a fixed per-GPU array inside the library instead of a
  * buffer it allocates on demand.  Limit: batch * ceil(width / 128) * 144 <=
  * 147456 bytes (batch 8 at width 16384); larger requests return INVALID.  The
- * array is shared by every call on a GPU: calls that overlap on one GPU race.
+ * array is shared by every call on a GPU and keeps the last call's contents.
+ * Calls from different contexts on one GPU are serialised: a call makes its
+ * context's stream wait for the previous other context's call to finish.
  * Outputs are bit-identical to fortai_hip_q8_batch_matvec_device. */
 int fortai_hip_q8_batch_matvec_noalloc(fortai_hip_q8_context *context,
     const fortai_hip_q8_weights *weights, const void *device_x, int batch, void *device_output);
@@ -306,7 +311,7 @@ int fortai_hip_qwen35_attention_core_device(fortai_hip_qwen35_attention *layer,
  * outputs [T][heads][value]; q is normalised and rotated in place and K/V are
  * appended at positions 0..T-1.  matrix_cores = 0: the exact kernel (the
  * reference's summation orders, the default prefill), 1: the fp16
- * matrix-core kernel of FORTAI_HIP_PREFILL=fast.  Heads of 64, 128 or 256. */
+ * matrix-core kernel of the FORTAI_HIP_PREFILL_FAST prefill mode.  Heads of 64, 128 or 256. */
 int fortai_hip_qwen35_attention_prefill_core_device(fortai_hip_qwen35_attention *layer,
     void *device_query, const void *device_key, const void *device_value, int T,
     int matrix_cores, void *device_output);
@@ -415,6 +420,37 @@ int fortai_hip_qwen35_batch_plan(const fortai_hip_qwen35_batch *batch_decoder, i
     size_t bytes, size_t *needed);
 /* device pointer of the logits [batch][vocab] */
 int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batch_decoder, void **device_logits);
+
+/* [extension] Options, set by explicit calls (the library reads nothing from
+ * the environment).
+ * attention_set_exact_max: the positions up to which the attention output
+ * keeps the reference's two-pass summation orders, bit-exact
+ * (fortai_qwen35_cpu.f90:1006-1031; default 8192); beyond them split-K with an
+ * online-softmax merge, within 1e-3 relative.  Set it before a decoder or
+ * batch is created over the layer.
+ * attention_set_test_options [test only; results stay bit-identical]:
+ * z_skew moves every Z candidate window by that many floats, so that the
+ * running sums fall outside them and the walk's own chain runs; force_wide
+ * runs the batches' wide output kernel for a single sequence too.
+ * decoder_set_mode / batch_set_mode: FORTAI_HIP_DECODER_DIRECT enqueues the
+ * kernels every step instead of replaying a captured graph (same kernels,
+ * same results; for kernel tracing); FORTAI_HIP_DECODER_MATVEC_ONLY [timing
+ * probe, decoder only] enqueues only the step's Q8_0 projections, so its
+ * values are meaningless.  The step is re-captured.
+ * batch_set_prefill_mode: FORTAI_HIP_PREFILL_EXACT (default; bit-identical to
+ * token-by-token decoding), _MATVEC (the batched decode matvec, 8 tokens at a
+ * time; the same bits), _FAST (whole-block int32 dots on the i8 matrix cores
+ * and the fp16 matrix-core attention; within 5e-2, not bit-exact). */
+#define FORTAI_HIP_DECODER_DIRECT 1
+#define FORTAI_HIP_DECODER_MATVEC_ONLY 2
+#define FORTAI_HIP_PREFILL_EXACT 0
+#define FORTAI_HIP_PREFILL_MATVEC 1
+#define FORTAI_HIP_PREFILL_FAST 2
+int fortai_hip_qwen35_attention_set_exact_max(fortai_hip_qwen35_attention *layer, int exact_max);
+int fortai_hip_qwen35_attention_set_test_options(fortai_hip_qwen35_attention *layer, int z_skew, int force_wide);
+int fortai_hip_qwen35_decoder_set_mode(fortai_hip_qwen35_decoder *decoder, int flags);
+int fortai_hip_qwen35_batch_set_mode(fortai_hip_qwen35_batch *batch_decoder, int flags);
+int fortai_hip_qwen35_batch_set_prefill_mode(fortai_hip_qwen35_batch *batch_decoder, int mode);
 
 #ifdef __cplusplus
 }

@@ -51,7 +51,8 @@ def test_quantize_bit_exact(ctx, oracle, n):
     assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,width", [(3584, 1024), (13, 96), (1024, 3584), (16, 1024)])
+@pytest.mark.parametrize("rows,width", [(3584, 1024), (13, 96), (1024, 3584), (16, 1024), (9216, 2560),
+                                        (2560, 9216), (8192, 2560), (2560, 4096)])
 def test_block_dots_and_matvec_bit_exact(ctx, oracle, rows, width):
     rng = np.random.default_rng(rows * 7 + width)
     w = synth.q8_blocks(rng, rows, width)
@@ -261,10 +262,10 @@ def test_gdn_core_128_steps(ctx, oracle):
                                               (8192, None, -90)])
 def test_attention_core(ctx, oracle, L, exact_max, skew):
     """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7, append + attend at position L-1.
-    Up to FORTAI_HIP_EXACT_ATTENTION_MAX positions (default 8192) the output keeps the reference's two-pass
+    Up to the layer's exact_max positions (default 8192; fortai_hip_qwen35_attention_set_exact_max) the output keeps the reference's two-pass
     summation orders and is bit-exact; beyond it, split-K with an online-softmax merge, within the north
     star's 1e-3 relative.  exact_max None: the default; 1 << 20: exact at 32768; 0: split-K at every L.
-    skew: FORTAI_HIP_ZTABLE_SKEW, which moves the Z candidate windows so that some (60, -90) or all
+    skew: the test option z_skew, which moves the Z candidate windows so that some (60, -90) or all
     (1 << 20) running sums fall outside them and the resolution's own chain runs."""
     rng = np.random.default_rng(L)
     heads, kvh, head, H = 8, 2, 256, 1024
@@ -273,18 +274,10 @@ def test_attention_core(ctx, oracle, L, exact_max, skew):
     qn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     kn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     maxc = max(L, 64)
-    saved = {k: os.environ.get(k) for k in ("FORTAI_HIP_EXACT_ATTENTION_MAX", "FORTAI_HIP_ZTABLE_SKEW")}
+    A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
     if exact_max is not None:
-        os.environ["FORTAI_HIP_EXACT_ATTENTION_MAX"] = str(exact_max)  # read when the layer is created
-    os.environ["FORTAI_HIP_ZTABLE_SKEW"] = str(skew)
-    try:
-        A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
-    finally:
-        for k, v in saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
+        A.set_exact_max(exact_max)
+    A.set_test_options(z_skew=skew)
     kc = np.zeros(maxc * kvh * head, np.uint16)
     vc = np.zeros(maxc * kvh * head, np.uint16)
     n = (L - 1) * kvh * head
@@ -331,7 +324,7 @@ def same_values(a, b):
 def test_attention_output_kernels(ctx, oracle, L, wide, big):
     """The exact attention output of one sequence through the per-slice kernel
     (wide 0, the decode's) or the batches' wide kernel (wide 1, selected for one
-    sequence by FORTAI_HIP_ATTENTION_WIDE), against the reference step.
+    sequence by the test option force_wide), against the reference step.
     big: exponent-31 halves in value dims 0..19 of kv head 0 at every 7th
     position, which the reference reads as +-huge (gguf_fp16_to_real,
     fortai_gguf_runtime.f90:770-788): those dims of that kv head's heads sum
@@ -344,15 +337,8 @@ def test_attention_output_kernels(ctx, oracle, L, wide, big):
     qn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     kn = (1 + 0.05 * rng.standard_normal(head)).astype(np.float32)
     maxc = max(L, 64)
-    saved = os.environ.get("FORTAI_HIP_ATTENTION_WIDE")
-    os.environ["FORTAI_HIP_ATTENTION_WIDE"] = str(wide)  # read when the layer is created
-    try:
-        A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
-    finally:
-        if saved is None:
-            os.environ.pop("FORTAI_HIP_ATTENTION_WIDE", None)
-        else:
-            os.environ["FORTAI_HIP_ATTENTION_WIDE"] = saved
+    A = B.Attention(ctx, *ws, qn, kn, heads, kvh, head, head, maxc, 64, 1.0e7, 1e-6)
+    A.set_test_options(force_wide=bool(wide))
     kc = np.zeros(maxc * kvh * head, np.uint16)
     vc = np.zeros(maxc * kvh * head, np.uint16)
     n = (L - 1) * kvh * head

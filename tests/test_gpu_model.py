@@ -201,3 +201,50 @@ def test_full_layer_shapes_long_context(oracle, short_path):
             assert same_bits(conv, ref.conv_state(i)), f"conv state of layer {i}"
     finally:
         m.close()
+
+
+@pytest.fixture(scope="module")
+def short4b_path(tmp_path_factory):
+    """Every 4B layer shape (hidden 2560, FFN 9216, GDN 16 key / 32 value
+    heads of 128, attention 16/4 heads x 256) with 4 layers and a
+    16384-token vocabulary -- BASELINE config 5's layers."""
+    from fortai_amd import synth
+    path = str(tmp_path_factory.mktemp("models") / "short4b.gguf")
+    synth.write_model(path, synth.CONFIGS["qwen35-4b-short"])
+    return path
+
+
+def test_4b_layer_shapes_match_oracle(oracle, short4b_path):
+    """The single-sequence decoder at the 4B layer shapes against the oracle
+    (fortai_qwen35_cpu.f90:231-235 grouped GDN heads, :801-918, :978-1035):
+    logits of every step, then the K/V caches, GDN and conv states, bit for
+    bit.  The batched decoder and the prefill are pinned to this decoder
+    (test_gpu_batch.py, test_gpu_config5.py), so this closes their chain to
+    the reference at config 5's own shapes."""
+    from oracle.oracle import OracleModel
+    ctx = 64
+    steps = 16
+    ref = OracleModel(oracle, short4b_path, ctx)
+    m = open_decoder(short4b_path, ctx)
+    try:
+        token = 9419 % 16384
+        for pos in range(steps):
+            got = m.forward(token, pos).copy()
+            want = ref.forward(token, pos)
+            assert same_bits(got, want), f"step {pos}: logits differ (max rel {rel_err(got, want):.3e})"
+            token = int(np.argmax(want))
+            assert int(np.argmax(got)) == token, f"step {pos}"
+        for i, layer in enumerate(m.attention):
+            if layer is None:
+                continue
+            k, v = layer.cache(steps)
+            assert np.array_equal(k, ref.kcache(i)[:k.size]), f"K cache of layer {i}"
+            assert np.array_equal(v, ref.vcache(i)[:v.size]), f"V cache of layer {i}"
+        for i, layer in enumerate(m.recurrent):
+            if layer is None:
+                continue
+            gdn, conv = layer.state()
+            assert same_bits(gdn, ref.gdn_state(i)), f"GDN state of layer {i}"
+            assert same_bits(conv, ref.conv_state(i)), f"conv state of layer {i}"
+    finally:
+        m.close()

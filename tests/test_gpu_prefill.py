@@ -10,9 +10,9 @@ every Q8_0 dot.  The bars:
   the last prompt token are bit-identical to token-by-token decoding, which
   is itself bit-identical to the reference (tests/test_gpu_model.py,
   tests/test_gpu_full.py) -- and to the oracle directly;
-- FORTAI_HIP_PREFILL=matvec (projections through the batched decode matvec)
+- prefill mode 'matvec' (projections through the batched decode matvec)
   gives the same bits, a cross-check of the matrix-core lane order;
-- FORTAI_HIP_PREFILL=fast (whole-block int32 dots with one fp32 chain per
+- prefill mode 'fast' (whole-block int32 dots with one fp32 chain per
   output and the fp16 matrix-core attention) is a performance variant: every
   layer re-quantizes its activations to int8, so a ~1e-7 difference now and
   then moves a value across an int8 rounding boundary and propagates; its
@@ -28,7 +28,7 @@ from fortai_amd.qwen35 import Qwen35Hip
 
 pytestmark = pytest.mark.gpu
 
-# FORTAI_HIP_PREFILL=fast: bound on the relative logit error against
+# prefill mode fast: bound on the relative logit error against
 # token-by-token decoding at these shapes (largest measured: 4.1e-2, 4B
 # layer shapes at T = 64)
 FAST_REL = 5e-2
@@ -88,7 +88,7 @@ def test_prefill_bit_identical_to_token_by_token_decode(paths, name, batch, leng
 
 
 @pytest.mark.parametrize("name,batch,T", [("qwen35-tiny", 4, 24), ("qwen35-4b-short", 8, 17)])
-def test_matvec_mode_gives_the_same_bits(paths, name, batch, T, monkeypatch):
+def test_matvec_mode_gives_the_same_bits(paths, name, batch, T):
     rng = np.random.default_rng(T)
     m = Qwen35Hip(paths[name], max_context=64, batch=batch)
     try:
@@ -96,7 +96,7 @@ def test_matvec_mode_gives_the_same_bits(paths, name, batch, T, monkeypatch):
         m.batch.reset()
         m.batch.prefill(prompts)
         exact = m.batch.logits.copy()
-        monkeypatch.setenv("FORTAI_HIP_PREFILL", "matvec")
+        m.batch.set_prefill_mode("matvec")
         m.batch.reset()
         m.batch.prefill(prompts)
         assert same_bits(m.batch.logits, exact)
@@ -106,9 +106,9 @@ def test_matvec_mode_gives_the_same_bits(paths, name, batch, T, monkeypatch):
 
 @pytest.mark.parametrize("name,batch,lengths", [("qwen35-tiny", 4, (17, 64)), ("qwen35-tiny", 2, (511,)),
                                                 ("qwen35-4b-short", 8, (64,)), ("qwen35-4b-short", 2, (300,))])
-def test_fast_mode_prefill_close_to_decode(paths, name, batch, lengths, monkeypatch):
-    monkeypatch.setenv("FORTAI_HIP_PREFILL", "fast")
+def test_fast_mode_prefill_close_to_decode(paths, name, batch, lengths):
     m = Qwen35Hip(paths[name], max_context=max(128, max(lengths) + 8), batch=batch)
+    m.batch.set_prefill_mode("fast")
     errs, agree, total = [], 0, 0
     try:
         for T in lengths:

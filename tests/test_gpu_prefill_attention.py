@@ -7,7 +7,7 @@ token.  The oracle's attention_core_step restates that step; run for
 t = 0..T-1 it gives every prefill row.
 - the exact kernel (the default prefill) must equal it bit for bit, outputs
   and the appended K/V cache;
-- the fp16 matrix-core kernel (FORTAI_HIP_PREFILL=fast) rounds q, k, v and
+- the fp16 matrix-core kernel (the 'fast' prefill mode) rounds q, k, v and
   the probabilities to fp16 (11-bit significands, relative 2^-11 = 4.9e-4
   each) and uses the hardware exp and reciprocal; its outputs are held to
   FAST_ATT_REL, relative to the output scale (rel_err below), and its K/V
@@ -22,7 +22,7 @@ from fortai_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-# FORTAI_HIP_PREFILL=fast attention against the reference's step.  fp16 q
+# The fast prefill mode's attention against the reference's step.  fp16 q
 # and k move a score by up to ~2^-11 x sum|q_i k_i| / sqrt(head), about 1e-3
 # for these normalised heads, and a probability by as much relative to
 # itself; P's own fp16 rounding adds 2^-11.  Measured here: 1.8e-3 (head
