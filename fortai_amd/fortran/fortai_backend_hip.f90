@@ -104,6 +104,7 @@ module fortai_backend_hip
         procedure :: reset => batch_reset
         procedure :: prefill => batch_prefill
         procedure :: generate => batch_generate
+        procedure :: plan => batch_plan
     end type hip_qwen35_batch_t
 
     public :: hip_q8_pack_bytes
@@ -420,6 +421,15 @@ module fortai_backend_hip
                 bind(C, name='fortai_hip_qwen35_decoder_plan')
             import :: c_int, c_ptr, c_size_t
             type(c_ptr), value :: decoder, buffer
+            integer(c_size_t), value :: bytes
+            integer(c_size_t), intent(out) :: needed
+        end function
+        integer(c_int) function fh_batch_plan(decoder, prefill, buffer, bytes, needed) &
+                bind(C, name='fortai_hip_qwen35_batch_plan')
+            import :: c_int, c_ptr, c_size_t
+            type(c_ptr), value :: decoder
+            integer(c_int), value :: prefill
+            type(c_ptr), value :: buffer
             integer(c_size_t), value :: bytes
             integer(c_size_t), intent(out) :: needed
         end function
@@ -1489,5 +1499,41 @@ contains
         call settle(fh_batch_generate(self%handle, c_loc(tokens), c_loc(positions), int(size(trace, 1), c_int), &
             c_loc(trace)), self%context, 'Qwen batch generation', stat)
     end subroutine batch_generate
+
+    ! As decoder_plan, for one batched step (prefill false) or the last
+    ! prompt prefill (prefill true).
+    subroutine batch_plan(self, prefill, text, stat)
+        class(hip_qwen35_batch_t), intent(in) :: self
+        logical, intent(in) :: prefill
+        character(len=:), allocatable, intent(out) :: text
+        type(status_t), intent(out) :: stat
+        character(kind=c_char), allocatable, target :: buf(:)
+        integer(c_size_t) :: need
+        integer(c_int) :: which
+        integer :: i
+
+        call stat%clear()
+        text = ''
+        if (.not. live(self%handle)) then
+            call stat%set(FORTAI_INVALID, 'invalid HIP Qwen batch decoder')
+            return
+        end if
+        which = 0_c_int
+        if (prefill) which = 1_c_int
+        call settle(fh_batch_plan(self%handle, which, c_null_ptr, 0_c_size_t, need), self%context, &
+            'Qwen batch plan', stat)
+        if (.not. stat%is_ok()) return
+        if (need < 1) then
+            call stat%set(FORTAI_INVALID, 'Qwen batch plan is empty')
+            return
+        end if
+        allocate (buf(need))
+        call settle(fh_batch_plan(self%handle, which, c_loc(buf), need, need), self%context, 'Qwen batch plan', stat)
+        if (.not. stat%is_ok()) return
+        allocate (character(len=int(need) - 1) :: text)
+        do i = 1, int(need) - 1
+            text(i:i) = buf(i)
+        end do
+    end subroutine batch_plan
 
 end module fortai_backend_hip

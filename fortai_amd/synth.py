@@ -98,6 +98,13 @@ CONFIGS: Dict[str, Qwen35Config] = {
                                       rope_dim=64, gdn_key_heads=16, gdn_value_heads=16,
                                       gdn_state=128, gdn_inner=2048, conv_kernel=4,
                                       vocab=16384),
+    # The mid-size model with a Q8_0 tied embedding / LM head, so that the
+    # reference's own device pipeline runs at the 0.8B layer shapes.
+    "qwen35-0.8b-short-q8emb": Qwen35Config("qwen35-0.8b-short-q8emb", hidden=1024, layers=4, ffn=3584,
+                                            heads=8, kv_heads=2, head_size=256, value_size=256,
+                                            rope_dim=64, gdn_key_heads=16, gdn_value_heads=16,
+                                            gdn_state=128, gdn_inner=2048, conv_kernel=4,
+                                            vocab=16384, embedding_q8=True),
     # BASELINE config 5 (Qwen3.5-4B shape): hidden 2560, 32 layers (24 GDN /
     # 8 attention), FFN 9216, 16 q / 4 kv heads of 256.  BASELINE leaves the
     # GDN heads open; 16 key / 32 value heads of 128 (value_heads % key_heads

@@ -203,6 +203,15 @@ def main() -> None:
             json.dump(meta, f, indent=1, sort_keys=True)
         print("wrote the 4096-step trace")
         return
+    if "--short-q8emb" in sys.argv:
+        # the 0.8B layer shapes with a Q8_0 embedding: the C-ABI boundary test
+        # of the reference's own device pipeline at those shapes
+        arrays, meta = tiny_model(ref, "qwen35-0.8b-short-q8emb")
+        np.savez_compressed(os.path.join(HERE, "short_q8emb_model.npz"), **arrays)
+        with open(os.path.join(HERE, "short_q8emb_model.json"), "w") as f:
+            json.dump(meta, f, indent=1, sort_keys=True)
+        print("wrote short_q8emb_model")
+        return
     rng = np.random.default_rng(0x60D)
     np.savez_compressed(os.path.join(HERE, "kernels.npz"), **kernels(ref, rng))
     for config, stem in (("qwen35-tiny", "tiny_model"), ("qwen35-tiny-q8emb", "tiny_q8emb_model")):

@@ -345,11 +345,12 @@ def _state_hashes(model) -> dict:
     return {k: hashlib.sha256(v.tobytes()).hexdigest() for k, v in out.items()}
 
 
-@pytest.mark.parametrize("stem", ["tiny_model", "tiny_q8emb_model"])
+@pytest.mark.parametrize("stem", ["tiny_model", "tiny_q8emb_model", "short_q8emb_model"])
 def test_tiny_model_matches_reference_golden(oracle, tmp_path, stem):
     """Greedy decode of the synthetic tiny models (F16 and Q8_0 tied
-    embedding): logits, token trace and every KV / GDN / conv state buffer
-    bit-identical to the compiled reference."""
+    embedding) and of the 0.8B layer shapes with a Q8_0 embedding: logits,
+    token trace and every KV / GDN / conv state buffer bit-identical to the
+    compiled reference."""
     from fortai_amd import synth
     from oracle.oracle import OracleModel
     arrays, meta = load_tiny_golden(stem)
