@@ -204,6 +204,43 @@ def matvec_family_roofline(model, warmup: int = 4, reps: int = 32):
             "algorithmic_bytes": algo, "us_per_step": round(us, 2), "avg_launch_us": round(us / max(launches, 1), 3)}
 
 
+def family_breakdown(model, position: int, warmup: int = 4, reps: int = 32):
+    """Where the graph-replayed step spends its time, per kernel family: a
+    decoder over the same layers in a timing-probe mode enqueues only one
+    family's kernels (the Q8_0 projections; the GDN delta rule; the attention
+    scores / softmax / output kernels; the embedding with the argmax finish
+    and the LM head), captured as a graph and replayed at a fixed position
+    (the attention kernels at `position` of the filled cache, so they read
+    position + 1 keys and values), timed with HIP events on the context
+    stream.  The families run back to back in the full step, so their sum is
+    the step's time up to the boundaries between them."""
+    from fortai_amd import backend as B
+    d, ctx = model.d, model.ctx
+    out = {"position": position}
+    for fam in ("matvec", "gdn", "attention", "head"):
+        dec = B.Decoder(model.ctx, model.recurrent, model.attention,
+                        [model.q8[f"blk.{i}.ffn_gate.weight"] for i in range(d.layers)],
+                        [model.q8[f"blk.{i}.ffn_up.weight"] for i in range(d.layers)],
+                        [model.q8[f"blk.{i}.ffn_down.weight"] for i in range(d.layers)],
+                        [n["attn"] for n in model.norms], [n["post"] for n in model.norms], model.output_norm,
+                        d.hidden, model.embedding, model.output, model.max_context, d.eps, d.vocab)
+        try:
+            dec.set_mode(only=[fam])
+            launches = len(dec.plan())
+            # the head family advances the position itself (from 0 here)
+            ctx.set_position(0 if fam == "head" else position)
+            dec.replay(warmup)
+            ctx.synchronize()
+            ctx.timer_start()
+            dec.replay(reps)
+            us = ctx.timer_stop() * 1e3 / reps
+        finally:
+            dec.free()
+        out[fam] = {"us_per_step": round(us, 2), "plan_steps": launches}
+    out["sum_us"] = round(sum(out[f]["us_per_step"] for f in ("matvec", "gdn", "attention", "head")), 2)
+    return out
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     (profiles/<name>_pmc.json, written from a committed profiling run)."""
@@ -875,6 +912,7 @@ def main() -> int:
     tok_s = args.steps / (wall_ms * 1e-3)
     roof = matvec_family_roofline(model)
     roof_lm = lm_head_roofline(model)
+    families = family_breakdown(model, args.ctx - args.steps // 2)
     mv = None if args.no_matvec else bench_matvec(model)
     kernels = None
     if not args.no_kernels:
@@ -912,6 +950,7 @@ def main() -> int:
         "trace": trace,
         "roofline": roof,
         "roofline_lm_head": roof_lm,
+        "step_by_family": families,
         "matvec": mv,
         "kernels": kernels,
         "config5": model_cfg5,

@@ -128,6 +128,7 @@ _lib: Optional[C.CDLL] = None
 # option values of include/fortai_hip_backend.h
 DECODER_DIRECT = 1
 DECODER_MATVEC_ONLY = 2
+DECODER_FAMILIES = {"matvec": 2, "gdn": 4, "attention": 8, "head": 16}
 PREFILL_MODES = {"exact": 0, "matvec": 1, "fast": 2}
 
 
@@ -439,11 +440,14 @@ class Decoder:
     def reset(self) -> None:
         self.ctx.call("fortai_hip_qwen35_decoder_reset", self.h)
 
-    def set_mode(self, direct: bool = False, matvec_only: bool = False) -> None:
+    def set_mode(self, direct: bool = False, matvec_only: bool = False, only: Sequence[str] = ()) -> None:
         """direct: enqueue the kernels every step instead of a graph replay
-        (kernel tracing); matvec_only: a timing probe of the Q8_0 projections."""
-        self.ctx.call("fortai_hip_qwen35_decoder_set_mode", self.h,
-                      (DECODER_DIRECT if direct else 0) | (DECODER_MATVEC_ONLY if matvec_only else 0))
+        (kernel tracing); matvec_only / only: timing probes that enqueue only
+        those kernel families ("matvec", "gdn", "attention", "head")."""
+        flags = (DECODER_DIRECT if direct else 0) | (DECODER_MATVEC_ONLY if matvec_only else 0)
+        for f in only:
+            flags |= DECODER_FAMILIES[f]
+        self.ctx.call("fortai_hip_qwen35_decoder_set_mode", self.h, flags)
 
     def forward(self, token: int, position: int, want_logits: bool = True) -> int:
         nxt = np.zeros(1, dtype=np.int64)

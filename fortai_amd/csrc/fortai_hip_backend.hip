@@ -112,6 +112,9 @@ struct fortai_hip_qwen35_attention {
 };
 
 constexpr int kDefaultExactMax = 8192;
+// Kernel families of a decode step.  A decoder in a timing-probe mode
+// enqueues only some of them (their values are then meaningless).
+constexpr unsigned kFamMatvec = 1, kFamGdn = 2, kFamAttention = 4, kFamHead = 8, kFamAll = 15;
 // prompt prefill projections: the exact token-block product (default), the
 // batched decode matvec (same bits), or whole-block int32 dots (not exact)
 enum class PrefillMode { EXACT = 0, MATVEC = 1, FAST = 2 };
@@ -140,11 +143,11 @@ struct fortai_hip_qwen35_decoder {
     bool use_graph = true;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
-    // FORTAI_HIP_DECODER_MATVEC_ONLY mode: a step enqueues only its Q8_0
-    // matvec launches (same kernels, weights and arguments; the other kernels
-    // are left out, so the values are meaningless) -- for timing the matvec
-    // family of a decode step
-    bool matvec_only = false;
+    // the *_ONLY timing-probe modes: a step enqueues only the selected kernel
+    // families (same kernels, weights and arguments; the others are left out,
+    // so the values are meaningless) -- for timing each family of a decode
+    // step as the graph replays it
+    unsigned families = kFamAll;  // kernel families a step enqueues (a timing probe: a subset)
     std::vector<plan_step> plan;  // the launches of one step (PlanIR steps)
 };
 
@@ -206,7 +209,8 @@ int fail(fortai_hip_q8_context *ctx, int code, const char *op, hipError_t err = 
     return code;
 }
 
-thread_local bool g_matvec_only = false;  // enqueue only the Q8_0 matvecs (decoder matvec_only)
+thread_local unsigned g_families = kFamAll;
+inline bool fam(unsigned f) { return (g_families & f) != 0; }
 // PlanIR recording (src/fortai_plan_ir.f90:7-21): while a plan is being
 // recorded, every successful launch appends (operation, kernel, batch).
 thread_local std::vector<plan_step> *g_plan = nullptr;
@@ -387,9 +391,9 @@ hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &
         segs[0].silu_end = L->conv_size + L->inner;
         count = 1;
     }
-    hipError_t e = rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream),
+    hipError_t e = !fam(kFamMatvec) ? hipSuccess : rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream),
         "GDN qkv/gate/alpha/beta projections, conv1d + SiLU");
-    if (e == hipSuccess && !g_matvec_only)
+    if (e == hipSuccess && fam(kFamGdn))
         e = rec(launch_gdn_delta(gdn_params(L, L->qkv_out, L->alpha_out, L->beta_out, L->o_raw), stream),
             "GDN L2 norms, decay/beta, delta rule");
     if (e != hipSuccess) return e;
@@ -401,6 +405,7 @@ hipError_t enqueue_recurrent(fortai_hip_qwen35_recurrent *L, const MatvecInput &
     gated.head = L->head;
     gated.width = L->inner;
     const MatvecSegment oseg = segment(L->out, out, resid);
+    if (!fam(kFamMatvec)) return hipSuccess;
     return rec(launch_q8_matvec(&oseg, 1, gated, Prologue::GATED, resid ? Epilogue::ADD : Epilogue::STORE, stream),
         "GDN gated RMSNorm, ssm_out projection + residual");
 }
@@ -426,9 +431,10 @@ hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &
         segs[0].out = A->proj;
         count = 1;
     }
-    hipError_t e = rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream), "attention q/k/v projections");
+    hipError_t e = !fam(kFamMatvec) ? hipSuccess
+        : rec(launch_q8_matvec(segs, count, in, pro, Epilogue::STORE, stream), "attention q/k/v projections");
     if (e != hipSuccess) return e;
-    if (!g_matvec_only)
+    if (fam(kFamAttention))
         e = rec(launch_attention(attention_params(A, A->q_out, A->k_out, A->v_out, A->attn_out), stream),
             "q/k norm, RoPE, KV append, softmax.V, gate");
     if (e != hipSuccess) return e;
@@ -436,6 +442,7 @@ hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &
     MatvecInput oin;
     oin.x = A->attn_out;
     oin.width = A->heads * A->value;
+    if (!fam(kFamMatvec)) return hipSuccess;
     return rec(launch_q8_matvec(&oseg, 1, oin, Prologue::F32, resid ? Epilogue::ADD : Epilogue::STORE, stream),
         "attention o projection + residual");
 }
@@ -443,6 +450,7 @@ hipError_t enqueue_attention(fortai_hip_qwen35_attention *A, const MatvecInput &
 hipError_t enqueue_ffn(const fortai_hip_q8_weights *gate, const fortai_hip_q8_weights *up,
     const fortai_hip_q8_weights *down, const MatvecInput &in, Prologue pro, void *h_q8l, float *out,
     const float *resid, hipStream_t stream) {
+    if (!fam(kFamMatvec)) return hipSuccess;
     const MatvecSegment pair = segment(gate, nullptr, nullptr, up, h_q8l);
     hipError_t e = rec(launch_q8_matvec(&pair, 1, in, pro, Epilogue::SILU_PAIR, stream),
         "FFN post-norm, gate/up projections, SiLU product");
@@ -1554,9 +1562,9 @@ ArgmaxState decoder_argmax(fortai_hip_qwen35_decoder *d, int *partials) {
     return st;
 }
 hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream) {
-    g_matvec_only = d->matvec_only;
+    g_families = d->families;
     hipError_t e = hipSuccess;
-    if (!g_matvec_only) {
+    if (fam(kFamHead)) {
         // the embedding finishes the previous step's argmax (token, trace, position)
         int parts = 0;
         const ArgmaxState st = decoder_argmax(d, &parts);
@@ -1577,9 +1585,9 @@ hipError_t enqueue_decoder_step(fortai_hip_qwen35_decoder *d, hipStream_t stream
         in.norm = L.post_norm;
         e = enqueue_ffn(L.gate, L.up, L.down, in, Prologue::RMSNORM, d->h_q8l, d->x, d->x, stream);
     }
-    const bool only = g_matvec_only;
-    g_matvec_only = false;
-    if (e != hipSuccess || only) return e;
+    const bool head = fam(kFamHead);
+    g_families = kFamAll;
+    if (e != hipSuccess || !head) return e;
     return enqueue_lm_head(d, stream);
 }
 // final RMSNorm + LM head + greedy argmax partials from d->x; the next step's
@@ -1633,7 +1641,7 @@ hipError_t run_step(fortai_hip_qwen35_decoder *d) {
 // after a call's last step: the pending argmax finish, so token, trace and
 // position are current for the host (nothing when already finished)
 hipError_t finish_decoder_steps(fortai_hip_qwen35_decoder *d) {
-    if (d->matvec_only) return hipSuccess;
+    if (!(d->families & kFamHead)) return hipSuccess;
     int parts = 0;
     const ArgmaxState st = decoder_argmax(d, &parts);
     return launch_argmax_finish(parts, st, d->context->stream);
@@ -2435,12 +2443,19 @@ int fortai_hip_qwen35_attention_set_test_options(fortai_hip_qwen35_attention *A,
 }
 
 int fortai_hip_qwen35_decoder_set_mode(fortai_hip_qwen35_decoder *d, int flags) {
-    if (!d || (flags & ~(FORTAI_HIP_DECODER_DIRECT | FORTAI_HIP_DECODER_MATVEC_ONLY))) return FORTAI_HIP_INVALID;
+    constexpr int kOnly = FORTAI_HIP_DECODER_MATVEC_ONLY | FORTAI_HIP_DECODER_GDN_ONLY |
+        FORTAI_HIP_DECODER_ATTENTION_ONLY | FORTAI_HIP_DECODER_HEAD_ONLY;
+    if (!d || (flags & ~(FORTAI_HIP_DECODER_DIRECT | kOnly))) return FORTAI_HIP_INVALID;
     auto *c = d->context;
     (void)hipSetDevice(c->device);
     hipError_t e = hipStreamSynchronize(c->stream);
     d->use_graph = !(flags & FORTAI_HIP_DECODER_DIRECT);
-    d->matvec_only = (flags & FORTAI_HIP_DECODER_MATVEC_ONLY) != 0;
+    unsigned f = 0;
+    if (flags & FORTAI_HIP_DECODER_MATVEC_ONLY) f |= kFamMatvec;
+    if (flags & FORTAI_HIP_DECODER_GDN_ONLY) f |= kFamGdn;
+    if (flags & FORTAI_HIP_DECODER_ATTENTION_ONLY) f |= kFamAttention;
+    if (flags & FORTAI_HIP_DECODER_HEAD_ONLY) f |= kFamHead;
+    d->families = f ? f : kFamAll;
     if (e == hipSuccess) e = capture_decoder(d);
     return done(c, e, "Qwen decoder mode");
 }

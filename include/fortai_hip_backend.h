@@ -434,15 +434,20 @@ int fortai_hip_qwen35_batch_logits(fortai_hip_qwen35_batch *batch_decoder, void 
  * runs the batches' wide output kernel for a single sequence too.
  * decoder_set_mode / batch_set_mode: FORTAI_HIP_DECODER_DIRECT enqueues the
  * kernels every step instead of replaying a captured graph (same kernels,
- * same results; for kernel tracing); FORTAI_HIP_DECODER_MATVEC_ONLY [timing
- * probe, decoder only] enqueues only the step's Q8_0 projections, so its
- * values are meaningless.  The step is re-captured.
+ * same results; for kernel tracing).  The *_ONLY flags [timing probes,
+ * decoder only; any combination] enqueue only those kernel families of the
+ * step -- the Q8_0 projections, the GDN delta rule, the attention kernels,
+ * the embedding and LM head -- so the values are meaningless.  The step is
+ * re-captured.
  * batch_set_prefill_mode: FORTAI_HIP_PREFILL_EXACT (default; bit-identical to
  * token-by-token decoding), _MATVEC (the batched decode matvec, 8 tokens at a
  * time; the same bits), _FAST (whole-block int32 dots on the i8 matrix cores
  * and the fp16 matrix-core attention; within 5e-2, not bit-exact). */
 #define FORTAI_HIP_DECODER_DIRECT 1
 #define FORTAI_HIP_DECODER_MATVEC_ONLY 2
+#define FORTAI_HIP_DECODER_GDN_ONLY 4
+#define FORTAI_HIP_DECODER_ATTENTION_ONLY 8
+#define FORTAI_HIP_DECODER_HEAD_ONLY 16
 #define FORTAI_HIP_PREFILL_EXACT 0
 #define FORTAI_HIP_PREFILL_MATVEC 1
 #define FORTAI_HIP_PREFILL_FAST 2
