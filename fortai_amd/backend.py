@@ -16,7 +16,9 @@ from typing import Optional, Sequence
 
 import numpy as np
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libfortai_hip.so")
+# the in-tree build; FORTAI_HIP_LIBRARY names another build of the same library
+LIB_PATH = os.environ.get("FORTAI_HIP_LIBRARY") or \
+    os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libfortai_hip.so")
 
 OK, INVALID, RUNTIME_ERROR = 0, 1, 2
 

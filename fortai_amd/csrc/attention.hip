@@ -57,6 +57,7 @@ __device__ __forceinline__ AttentionParams attention_seq(AttentionParams p, int 
 }
 
 __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const AttentionParams p_batch) {
+    FORTAI_TRACE_SCOPE(3);
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     __shared__ __align__(16) float qh[kMaxGroup * kMaxHead];
     __shared__ __align__(16) float kn[kMaxHead];
@@ -169,6 +170,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
 // long cache few workgroups load the scores and exit idle), segments holding
 // positions dispatched first.
 __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const AttentionParams p_batch) {
+    FORTAI_TRACE_SCOPE(4);
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     __shared__ __align__(16) float e_seg[ea::kSeg];
     __shared__ double dred[2 * ea::kWaves];
@@ -321,6 +323,7 @@ __device__ __forceinline__ float head_z(const AttentionParams &p, int h, int n, 
 // the cache) is issued together with the position's, in one round trip.
 constexpr int kTabRegs = kZLdsSegments * ea::kZCand / ea::kThreads;  // walk words per thread
 __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const AttentionParams p_batch) {
+    FORTAI_TRACE_SCOPE(5);
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     extern __shared__ __align__(16) float lds[];
     __shared__ MathTables mt;

@@ -14,6 +14,13 @@
 #include <stddef.h>
 #include <stdint.h>
 
+// Per-workgroup timing hook of the decode kernels (first statement of each):
+// empty in the library; a timing build defines it to record when each
+// workgroup starts and ends.
+#ifndef FORTAI_TRACE_SCOPE
+#define FORTAI_TRACE_SCOPE(id)
+#endif
+
 namespace fortai_hip {
 
 constexpr int kQ8Block = 32;       // values per Q8_0 block
@@ -220,10 +227,14 @@ __device__ __forceinline__ float softplus_ref(float v) {
 }
 
 // The expf and logf tables in LDS: a kernel whose critical path runs through
-// those functions copies them at entry (load() by every thread, no wait: the
-// copy completes before the kernel's next barrier), so that each lookup is an
-// LDS read instead of a data-dependent memory round trip.  Same values, so
-// the same results.
+// those functions keeps them there, so that each lookup is an LDS read
+// instead of a data-dependent memory round trip.  Same values, so the same
+// results.  fetch() issues the table word of threads 0..63 as the kernel's
+// first load (into a register, no wait); put() stores it once the kernel has
+// issued its own loads, so that the wait for the table word does not hold
+// them back (a load from memory followed by an LDS store of it waits for the
+// load on the spot).  The stored tables are visible after the next barrier
+// (or, for wave 0's own reads, after wave_lds_fence).
 // Cross-lane exchange through LDS within one wave: the writes of every lane
 // are ordered before the reads that follow (no workgroup barrier needed).
 __device__ __forceinline__ void wave_lds_fence() {
@@ -234,17 +245,17 @@ __device__ __forceinline__ void wave_lds_fence() {
 struct MathTables {
     uint64_t exp2[32];
     double logc[16][2];
-    __device__ __forceinline__ void load() {
-        const int t = static_cast<int>(threadIdx.x);
-        if (t < 32) exp2[t] = kExpf2Table[t];
-        else if (t < 64) logc[(t - 32) >> 1][t & 1] = kLogfTable[(t - 32) >> 1][t & 1];
+    __device__ __forceinline__ void load() { put(fetch()); }
+    // word threadIdx.x of the tables (exp2 then logc; threads past 63 re-read word 63, unused)
+    static __device__ __forceinline__ uint64_t fetch() {
+        const int t = min(static_cast<int>(threadIdx.x), 63);
+        const uint64_t *src = t < 32 ? kExpf2Table + t : reinterpret_cast<const uint64_t *>(&kLogfTable[0][0]) + (t - 32);
+        return *src;
     }
-    // load() for kernels whose tables are read only by wave 0 (threads 0..63
-    // write them all) before any workgroup barrier: a wavefront-scope fence
-    // orders the lanes' LDS writes before the reads that follow
-    __device__ __forceinline__ void load_wave0() {
-        load();
-        wave_lds_fence();
+    __device__ __forceinline__ void put(uint64_t word) {
+        static_assert(sizeof(exp2) + sizeof(logc) == 64 * sizeof(uint64_t), "64 table words");
+        const int t = static_cast<int>(threadIdx.x);
+        if (t < 64) reinterpret_cast<uint64_t *>(this)[t] = word;
     }
     __device__ __forceinline__ float expf(float x) const { return expf_libm_t(x, exp2); }
     __device__ __forceinline__ float logf(float x) const { return logf_libm_t(x, logc); }

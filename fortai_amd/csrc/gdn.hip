@@ -69,6 +69,7 @@ __device__ __forceinline__ int xcd_grouped(int b, int n) { return n % 8 == 0 ? (
 
 template <int HEAD>
 __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParams p_batch) {
+    FORTAI_TRACE_SCOPE(2);
     const GdnParams p = gdn_seq(p_batch, static_cast<int>(blockIdx.y));
     constexpr int kCols = HEAD / 8;
     __shared__ __align__(16) float qs[HEAD];
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
     __shared__ double red[2];
     __shared__ float hs[2];
     __shared__ MathTables mt;
-    mt.load();
+    const uint64_t mt_word = MathTables::fetch();  // stored after the other loads are issued
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks_per_head = HEAD / kDeltaRows;
     const int wg = xcd_grouped(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
@@ -101,6 +102,7 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
     }
     const float vrow = p.qkv[2 * p.state_size * p.key_heads + h * HEAD + row];
     const float beta_in = p.beta[h], alpha_in = p.alpha[h], ssm_a = p.ssm_a[h], ssm_dt = p.ssm_dt[h];
+    mt.put(mt_word);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = tid + k * kDeltaThreads;
@@ -176,7 +178,7 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_recurrence_kernel(const Gdn
     __shared__ double red[2];
     __shared__ float hs[2];
     __shared__ MathTables mt;  // written and read by wave 0 (thread 0 uses it)
-    mt.load_wave0();
+    const uint64_t mt_word = MathTables::fetch();  // stored after the other loads are issued
     const int tid = static_cast<int>(threadIdx.x);
     const int blocks_per_head = HEAD / kDeltaRows;
     const int wg = xcd_grouped(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
@@ -205,6 +207,8 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_recurrence_kernel(const Gdn
         const float4 f = srow[i];
         s[4 * i] = f.x; s[4 * i + 1] = f.y; s[4 * i + 2] = f.z; s[4 * i + 3] = f.w;
     }
+    mt.put(mt_word);
+    wave_lds_fence();
     const float inv_sqrt = 1.0f / sqrtf(static_cast<float>(HEAD));
     // the next step's inputs are loaded while the current one runs
     float xn[3], an = 0.0f, bn = 0.0f;

@@ -96,6 +96,7 @@ __global__ __launch_bounds__(256) void argmax_finish_kernel(int partials, Argmax
 // the next LM head writes -1 again, a finish writes the token.
 __global__ __launch_bounds__(256) void step_embedding_kernel(const uint16_t *table16, Q8Matrix table8, int rows,
     int width, ArgmaxState st, int partials, float *out) {
+    FORTAI_TRACE_SCOPE(6);
     __shared__ float sv[4];
     __shared__ int si[4];
     __shared__ int64_t chosen;
@@ -161,6 +162,7 @@ template <bool RMS, bool ARGMAX, bool FINITE, int TILE>
 __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__restrict__ w, int rows, int width,
     const float *__restrict__ x, const float *__restrict__ norm, float eps, float *__restrict__ out,
     ArgmaxState st) {
+    FORTAI_TRACE_SCOPE(7);
     constexpr int kPitch = TILE + 8;
     extern __shared__ __align__(16) unsigned char lds[];
     uint16_t *tile = reinterpret_cast<uint16_t *>(lds);

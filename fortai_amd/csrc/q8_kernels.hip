@@ -229,6 +229,7 @@ __device__ __forceinline__ void build_activation(const MatvecInput &in, int chun
 // the bytes and a wave issues a quarter of the dot work.
 template <int WAVES, int NREG, Prologue PRO, Epilogue EPI, bool MULTI, bool SPLIT>
 __global__ __launch_bounds__(WAVES * 64) void q8_matvec_kernel(const MatvecArgs args) {
+    FORTAI_TRACE_SCOPE(1);
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
     static_assert(!SPLIT || (WAVES == 4 && NREG > 0 && NREG % 4 == 0 && !MULTI && !kPair), "split form");
     constexpr int kPer = SPLIT ? NREG / 4 : NREG;  // chunks this wave loads
