@@ -175,8 +175,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     __shared__ __align__(16) float e_seg[ea::kSeg];
     __shared__ double dred[2 * ea::kWaves];
     __shared__ float fred[ea::kWaves];
-    __shared__ MathTables mt;
-    mt.load();
+    __shared__ MathTables mt;  // loaded after the scores are issued (the wait for it is theirs)
     static_assert(ea::kZCand == ea::kThreads && ea::kSeg == ea::kThreads, "one candidate and one position per thread");
     const int pos = *p.position;
     const int k0 = div(static_cast<int>(blockIdx.x), p.div_heads), h = static_cast<int>(blockIdx.x) - k0 * p.heads;
@@ -195,6 +194,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
         for (int i = 0; i < kHeld; ++i)
             if (i * ea::kThreads < cap) x[i] = sc[min(tid + i * ea::kThreads, cap - 1)];
     }
+    mt.load();  // visible after the barrier of the max below
     if (pos < 0 || pos >= p.max_context) return;
     const int n = pos + 1;
     if (n > p.exact_max) return;  // the split-K kernels cover this position
@@ -326,8 +326,8 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
     FORTAI_TRACE_SCOPE(5);
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     extern __shared__ __align__(16) float lds[];
-    __shared__ MathTables mt;
-    mt.load();
+    // sigmoid of the gate: wave 1 forms it while thread 0 resolves Z
+    __shared__ float gate_sig[ea::kDims];
     const int tid = static_cast<int>(threadIdx.x);
     FORTAI_ATT_MARK(0);
     const int pos = *p.position;
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
 #pragma unroll
     for (int r = 0; r < kTabRegs; ++r)
         tr[r] = __float_as_int(tab[static_cast<size_t>(min(r, last_row)) * ea::kZStride + ea::kZNext + tid]);
-    const float gate = tid < ea::kDims ? p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + tid] : 0.0f;
+    const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + (tid & (ea::kDims - 1))];
     const int flag = p.cache_flags[kvh];
     FORTAI_ATT_MARK(3);
     if (pos < 0 || pos >= p.max_context) return;
@@ -385,13 +385,16 @@ __global__ __launch_bounds__(ea::kThreads) void attention_output_kernel(const At
         work[0] = nseg <= kZLdsSegments
             ? ea::resolve_z(walk_lds, ea::kZCand, tab, ev, positions)
             : ea::resolve_z(reinterpret_cast<const int32_t *>(tab + ea::kZNext), ea::kZStride, tab, ev, positions);
+    // (glibc's algorithm with its table in constant memory: one lookup, off
+    // the critical path; seen by wave 0 after the output step's barriers)
+    if (tid >= 64 && tid < 64 + ea::kDims) gate_sig[tid - 64] = sigmoid_ref(gate);
     FORTAI_ATT_MARK(2);
     __syncthreads();
     const float z = work[0];
     FORTAI_ATT_MARK(5);
     const float acc = flag == 0 ? ea::attend_given_z<true>(ev, z, positions, vbase, vstride, work, v, e4)
                                 : ea::attend_given_z<false>(ev, z, positions, vbase, vstride, work, v, e4);
-    if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * mt.sigmoid(gate);
+    if (tid < ea::kDims) p.out[static_cast<size_t>(h) * VD + d0 + tid] = acc * gate_sig[tid];
     FORTAI_ATT_MARK(4);
 }
 
