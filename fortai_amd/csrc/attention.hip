@@ -27,10 +27,19 @@ constexpr int kChunk = 256;  // positions per split-K chunk (long contexts)
 
 // The per-sequence workspace behind AttentionParams::partial, in floats:
 //   scores [heads][max_context] | e values [heads][max_context] |
-//   Z tables [heads][z_segments(max_context)][kZStride]
+//   Z tables [heads][z_segments(max_context)][kZStride] |
+//   block statistics [heads][score blocks][2] (the scores kernel's per
+//   64-position block max m_b and sum of exp(s - m_b), for the softmax's
+//   estimates of the running sums)
+__host__ __device__ inline int score_blocks(int max_context) { return (max_context + ea::kPosBlock - 1) / ea::kPosBlock; }
 __host__ __device__ inline size_t workspace_floats(int heads, int max_context) {
     return static_cast<size_t>(heads) * max_context * 2 +
-        static_cast<size_t>(heads) * ea::z_segments(max_context) * ea::kZStride;
+        static_cast<size_t>(heads) * ea::z_segments(max_context) * ea::kZStride +
+        static_cast<size_t>(heads) * score_blocks(max_context) * 2;
+}
+__device__ __forceinline__ float2 *block_stats_of(const AttentionParams &p) {
+    return reinterpret_cast<float2 *>(p.partial + static_cast<size_t>(p.heads) * p.max_context * 2 +
+        static_cast<size_t>(p.heads) * ea::z_segments(p.max_context) * ea::kZStride);
 }
 __device__ __forceinline__ float *evals_of(const AttentionParams &p) {
     return p.partial + static_cast<size_t>(p.heads) * p.max_context;
@@ -150,13 +159,24 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     const bool finite = flag == 0 && overflow == 0;
     const float sqrt_head = sqrtf(static_cast<float>(HD));
     const int gi = tid >> 6, j = tid & 63;
-    if (gi < group && j < n) {
-        const float *qg = qh + gi * HD;
-        const uint16_t *kr = &ktile[j][0];
-        float sc;
-        if (finite) sc = HD == 256 ? ea::score_n<true, 256>(qg, kr, sqrt_head) : ea::score<true>(qg, kr, HD, sqrt_head);
-        else sc = ea::score<false>(qg, kr, HD, sqrt_head);
-        p.partial[static_cast<size_t>(kvh * group + gi) * p.max_context + p0 + j] = sc;
+    if (gi < group) {  // wave gi: head kvh * group + gi, positions p0 + lane
+        constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
+        float sc = kLowest;
+        if (j < n) {
+            const float *qg = qh + gi * HD;
+            const uint16_t *kr = &ktile[j][0];
+            if (finite) sc = HD == 256 ? ea::score_n<true, 256>(qg, kr, sqrt_head) : ea::score<true>(qg, kr, HD, sqrt_head);
+            else sc = ea::score<false>(qg, kr, HD, sqrt_head);
+            p.partial[static_cast<size_t>(kvh * group + gi) * p.max_context + p0 + j] = sc;
+        }
+        // the block's max and sum of exp(s - max) (a fast exp, in double): the
+        // softmax kernel's estimates start from these, not from every score
+        const float mb = wave_max(sc);
+        double t = j < n ? static_cast<double>(__expf(sc - mb)) : 0.0;
+        t = wave_sum(t);
+        if (j == 0)
+            block_stats_of(p)[static_cast<size_t>(kvh * group + gi) * score_blocks(p.max_context) + b] =
+                make_float2(mb, static_cast<float>(t));
     }
     FORTAI_ATT_MARK(20);
 }
@@ -183,75 +203,70 @@ __global__ __launch_bounds__(ea::kThreads) void attention_softmax_kernel(const A
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
     const float *sc = p.partial + static_cast<size_t>(h) * p.max_context;
     FORTAI_ATT_MARK(21);
-    // up to kHeld * 256 positions the scores are loaded in the position's
-    // round trip (clamped to the cache; those past the position are masked)
-    constexpr int kHeld = 32;
+    // the statistics of every 64-position score block (max m_b, sum of
+    // exp(s - m_b)) written by the scores kernel: one block per thread and
+    // register up to kStatRegs * 256 blocks (clamped in bounds; those past the
+    // position are masked), and the first segment's own scores
+    constexpr int kStatRegs = 2;
     const int cap = p.max_context < p.exact_max ? p.max_context : p.exact_max;
-    const bool held = cap <= kHeld * ea::kThreads;
-    float x[kHeld];
-    if (held) {
+    const int nb_cap = score_blocks(cap);
+    const float2 *bst = block_stats_of(p) + static_cast<size_t>(h) * score_blocks(p.max_context);
+    float2 st[kStatRegs];
 #pragma unroll
-        for (int i = 0; i < kHeld; ++i)
-            if (i * ea::kThreads < cap) x[i] = sc[min(tid + i * ea::kThreads, cap - 1)];
-    }
+    for (int i = 0; i < kStatRegs; ++i)
+        if (i * ea::kThreads < nb_cap) st[i] = bst[min(tid + i * ea::kThreads, nb_cap - 1)];
+    const float sv0 = sc[min(k0 * ea::kSeg + tid, cap - 1)];
     mt.load();  // visible after the barrier of the max below
     if (pos < 0 || pos >= p.max_context) return;
     const int n = pos + 1;
     if (n > p.exact_max) return;  // the split-K kernels cover this position
     if (k0 * ea::kSeg >= n) return;
-    // m = max over every score (any order gives the same value)
+    const int nb = score_blocks(n);
+    // m = max over every score = max over the blocks' maxima (any order and
+    // grouping gives the same value)
     constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
     float m = kLowest;
-    if (held) {
 #pragma unroll
-        for (int i = 0; i < kHeld; ++i)
-            if (tid + i * ea::kThreads < n) m = fmaxf(m, x[i]);
-    } else {
-        for (int i = tid; i < n; i += ea::kThreads) m = fmaxf(m, sc[i]);
-    }
+    for (int i = 0; i < kStatRegs; ++i)
+        if (tid + i * ea::kThreads < nb) m = fmaxf(m, st[i].x);
+    for (int b = tid + kStatRegs * ea::kThreads; b < nb; b += ea::kThreads) m = fmaxf(m, bst[b].x);
     m = wave_max(m);
     if (lane == 0) fred[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    // block b's share of the running sum, rescaled to m (a fast exp, in double)
+    double tb[kStatRegs];
+#pragma unroll
+    for (int i = 0; i < kStatRegs; ++i) {
+        const int b = tid + i * ea::kThreads;
+        tb[i] = b < nb ? static_cast<double>(st[i].y) * static_cast<double>(__expf(st[i].x - m)) : 0.0;
+    }
     FORTAI_ATT_MARK(22);
     for (int k = k0; k * ea::kSeg < n; k += G) {
     if (k != k0) __syncthreads();  // the previous segment's chains have read e_seg and dred
     const int p0 = k * ea::kSeg;
     const int cnt = min(ea::kSeg, n - p0);
-    // the segment's own e values, exactly as the reference computes them; the
-    // score is the held one (x[k] holds position k * kSeg + tid), selected
-    // without a dynamic register index or a second round trip to memory
-    float sv;
-    if (held) {
-        sv = x[0];
-#pragma unroll
-        for (int i = 1; i < kHeld; ++i)
-            if (i == k && i * ea::kThreads < cap) sv = x[i];
-    } else {
-        sv = sc[min(p0 + tid, n - 1)];
-    }
+    // the segment's own e values, exactly as the reference computes them
+    const float sv = k == k0 ? sv0 : sc[min(p0 + tid, n - 1)];
     const float e = tid < cnt ? mt.expf(sv - m) : -0.0f;  // -0 leaves a sum unchanged
     e_seg[tid] = e;
     if (tid < cnt) evals_of(p)[static_cast<size_t>(h) * p.max_context + p0 + tid] = e;
-    // the estimates of the running sums entering this segment and the next
-    // (a fast exp; the next segment's workgroup forms the same sum the same way)
+    // the estimates of the running sums entering this segment and the next:
+    // the blocks before it, and those before the next one (the next
+    // segment's workgroup forms the same sum in the same order)
+    const int b_in = p0 / ea::kPosBlock, b_next = (p0 + ea::kSeg) / ea::kPosBlock;
     double est = 0.0, est_next = 0.0;
-    if (held) {
 #pragma unroll
-        for (int i = 0; i < kHeld; ++i) {
-            const int q = tid + i * ea::kThreads;
-            if (q < p0 + ea::kSeg) {
-                const double t = static_cast<double>(__expf(x[i] - m));
-                if (q < p0) est += t;
-                est_next += t;
-            }
-        }
-    } else {
-        for (int q = tid; q < p0 + ea::kSeg; q += ea::kThreads) {
-            const double t = static_cast<double>(__expf(sc[q] - m));
-            if (q < p0) est += t;
-            est_next += t;
-        }
+    for (int i = 0; i < kStatRegs; ++i) {
+        const int b = tid + i * ea::kThreads;
+        if (b < b_in) est += tb[i];
+        if (b < b_next) est_next += tb[i];
+    }
+    for (int b = tid + kStatRegs * ea::kThreads; b < nb && b < b_next; b += ea::kThreads) {
+        const float2 sb = bst[b];
+        const double t = static_cast<double>(sb.y) * static_cast<double>(__expf(sb.x - m));
+        if (b < b_in) est += t;
+        est_next += t;
     }
     est = wave_sum(est);
     est_next = wave_sum(est_next);

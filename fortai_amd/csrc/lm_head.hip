@@ -289,6 +289,7 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
 // tile; x of every sequence through scalar loads; per-sequence argmax partials.
 constexpr int kBatchRows = 256;
 constexpr int kBatchTile = 64;
+constexpr int kXCols = 8;  // columns of x per scalar-load batch in the batched LM head
 constexpr int kMaxBatch = 8;
 
 // Final RMSNorm of each sequence (fortai_qwen35_cpu.f90:707), one workgroup
@@ -362,12 +363,13 @@ __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uin
     float acc[kMaxBatch];
 #pragma unroll
     for (int s = 0; s < kMaxBatch; ++s) acc[s] = 0.0f;
-    // four columns per step (32 SGPRs of x; the other waves of the SIMD
-    // cover the scalar-load latency)
-    auto xload = [&](int k, float (&xv)[4][kMaxBatch]) {
+    // kXCols columns per scalar-load round trip (8 x kXCols SGPRs of x; the
+    // wait for them is a full lgkmcnt(0), so more columns per load means
+    // fewer exposed waits; the other waves of the SIMD cover the rest)
+    auto xload = [&](int k, float (&xv)[kXCols][kMaxBatch]) {
         const float4 *src = reinterpret_cast<const float4 *>(xn + static_cast<size_t>(k) * kMaxBatch);
 #pragma unroll
-        for (int i = 0; i < 4 * kMaxBatch / 4; ++i) {
+        for (int i = 0; i < kXCols * kMaxBatch / 4; ++i) {
             const float4 v = src[i];
             xv[i / 2][(i % 2) * 4 + 0] = v.x;
             xv[i / 2][(i % 2) * 4 + 1] = v.y;
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uin
             xv[i / 2][(i % 2) * 4 + 3] = v.w;
         }
     };
-    auto step = [&](const uint16_t *mine, int c, const float (&xv)[4][kMaxBatch]) {
+    auto step = [&](const uint16_t *mine, int c, const float (&xv)[kXCols][kMaxBatch], int x0) {
         const uint2 h4 = *reinterpret_cast<const uint2 *>(mine + c * 4);
         float a[4];
         a[0] = FINITE ? half_bits_to_float(static_cast<uint16_t>(h4.x & 0xffffu))
@@ -389,17 +391,19 @@ __global__ __launch_bounds__(kBatchRows) void f16_batch_lm_head_kernel(const uin
 #pragma unroll
         for (int s = 0; s < kMaxBatch; ++s) {
             float v = acc[s];
-            v = v + a[0] * xv[0][s]; v = v + a[1] * xv[1][s]; v = v + a[2] * xv[2][s]; v = v + a[3] * xv[3][s];
+            v = v + a[0] * xv[x0][s]; v = v + a[1] * xv[x0 + 1][s]; v = v + a[2] * xv[x0 + 2][s];
+            v = v + a[3] * xv[x0 + 3][s];
             acc[s] = v;
         }
     };
     auto consume = [&](int k0) {
         const uint16_t *mine = tile + tid * kPitch;
 #pragma unroll 1
-        for (int c = 0; c < kBatchTile / 4; ++c) {
-            float xv[4][kMaxBatch];
+        for (int c = 0; c < kBatchTile / 4; c += kXCols / 4) {
+            float xv[kXCols][kMaxBatch];
             xload(k0 + c * 4, xv);
-            step(mine, c, xv);
+#pragma unroll
+            for (int u = 0; u < kXCols / 4; ++u) step(mine, c + u, xv, 4 * u);
         }
     };
     for (int t = 0; t < tiles; t += 2) {
