@@ -89,16 +89,10 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     const int group = static_cast<int>(p.div_group.d), HD = p.head, VD = p.value, NKV = p.kv_heads;
     const int half = p.rope_dim / 2;
 
-    v4u kr[kLoads];  // key rows first: the only HBM stream of this kernel
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-        const int li = tid + i * ea::kThreads;
-        const int jj = div(li, p.div_segs), sg = li - jj * static_cast<int>(p.div_segs.d);
-        const int j = min(jj, n - 1);  // rows past n re-read row n-1 (in bounds)
-        kr[i] = reinterpret_cast<const v4u *>(p.kcache + (static_cast<size_t>(p0 + j) * NKV + kvh) * HD)[sg];
-    }
-    // every other input in the same round trip (indices clamped in bounds),
-    // then the LDS stores
+    // q, k, the norm weights, v and the rope entry first (indices clamped in
+    // bounds), then the key rows: the loads complete in order, so the q/k
+    // norms and RoPE run while the key rows (the only HBM stream of this
+    // kernel) are still arriving
     float qv[kQLoads];
 #pragma unroll
     for (int i = 0; i < kQLoads; ++i) {
@@ -119,6 +113,14 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     const float vnv = p.v[static_cast<size_t>(kvh) * VD + tv];
     const float2 rsv = half > 0 ? p.rope[static_cast<size_t>(pos) * half + min(tid, half - 1)] : make_float2(0.0f, 0.0f);
     const int flag = p.cache_flags[kvh];
+    v4u kr[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int li = tid + i * ea::kThreads;
+        const int jj = div(li, p.div_segs), sg = li - jj * static_cast<int>(p.div_segs.d);
+        const int j = min(jj, n - 1);  // rows past n re-read row n-1 (in bounds)
+        kr[i] = reinterpret_cast<const v4u *>(p.kcache + (static_cast<size_t>(p0 + j) * NKV + kvh) * HD)[sg];
+    }
 #pragma unroll
     for (int i = 0; i < kQLoads; ++i)
         if (tid + i * ea::kThreads < group * HD) qh[tid + i * ea::kThreads] = qv[i];
@@ -126,17 +128,17 @@ __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const At
     if (tid < half) rs[tid] = rsv;
     if (tid == 0) overflow = 0;
     FORTAI_ATT_MARK(17);
+    __syncthreads();
+    for (int sl = wave; sl < group + (owns_new ? 1 : 0); sl += ea::kThreads / 64) {
+        if (sl < group) ea::norm_rope_regs(qh + sl * HD, HD, qwr, p.eps, rs, p.rope_dim, lane);
+        else ea::norm_rope_regs(kn, HD, kwr, p.eps, rs, p.rope_dim, lane);
+    }
+    FORTAI_ATT_MARK(18);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int li = tid + i * ea::kThreads;
         const int j = div(li, p.div_segs), sg = li - j * static_cast<int>(p.div_segs.d);
         if (j < n) *reinterpret_cast<v4u *>(&ktile[j][sg * 8]) = kr[i];
-    }
-    __syncthreads();
-    FORTAI_ATT_MARK(18);
-    for (int sl = wave; sl < group + (owns_new ? 1 : 0); sl += ea::kThreads / 64) {
-        if (sl < group) ea::norm_rope_regs(qh + sl * HD, HD, qwr, p.eps, rs, p.rope_dim, lane);
-        else ea::norm_rope_regs(kn, HD, kwr, p.eps, rs, p.rope_dim, lane);
     }
     __syncthreads();
     FORTAI_ATT_MARK(19);
