@@ -37,7 +37,7 @@ __device__ __forceinline__ void norm_rope(float *v, int head, const float *w, fl
     double ss = 0.0;
     for (int i = lane; i < head; i += 64) ss += static_cast<double>(v[i]) * static_cast<double>(v[i]);
     ss = wave_sum(ss);
-    const float inv = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(head)) + eps);
+    const float inv = 1.0f / sqrtf(static_cast<float>(div_count(ss, head)) + eps);
     for (int i = lane; i < head; i += 64) v[i] = (v[i] * inv) * w[i];
     wave_lds_fence();
     const int half = rope_dim / 2;
@@ -58,7 +58,7 @@ __device__ __forceinline__ void norm_rope_regs(float *v, int head, const float (
     double ss = 0.0;
     for (int i = lane; i < head; i += 64) ss += static_cast<double>(v[i]) * static_cast<double>(v[i]);
     ss = wave_sum(ss);
-    const float inv = 1.0f / sqrtf(static_cast<float>(ss / static_cast<double>(head)) + eps);
+    const float inv = 1.0f / sqrtf(static_cast<float>(div_count(ss, head)) + eps);
 #pragma unroll
     for (int j = 0; j < NW; ++j)
         if (lane + 64 * j < head) v[lane + 64 * j] = (v[lane + 64 * j] * inv) * wr[j];

@@ -235,6 +235,15 @@ __device__ __forceinline__ float softplus_ref(float v) {
 // them back (a load from memory followed by an LDS store of it waits for the
 // load on the spot).  The stored tables are visible after the next barrier
 // (or, for wave 0's own reads, after wave_lds_fence).
+// x / n for a double x and a count n > 0, correctly rounded.  When n = 2^k
+// the quotient is x scaled by 2^-k: ldexp rounds that same exact value the
+// same way (bit-identical, subnormal results included) in one instruction
+// instead of the division's dependent sequence.
+__device__ __forceinline__ double div_count(double x, int n) {
+    if ((n & (n - 1)) == 0) return __builtin_ldexp(x, -__builtin_ctz(static_cast<unsigned>(n)));
+    return x / static_cast<double>(n);
+}
+
 // Cross-lane exchange through LDS within one wave: the writes of every lane
 // are ordered before the reads that follow (no workgroup barrier needed).
 __device__ __forceinline__ void wave_lds_fence() {

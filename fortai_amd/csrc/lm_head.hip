@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kRows) void f16_matvec_kernel(const uint16_t *__res
         __syncthreads();
         double total = 0.0;
         for (int i = 0; i < kRows / 64; ++i) total += red[i];
-        inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+        inv = 1.0f / sqrtf(static_cast<float>(div_count(total, width)) + eps);
     }
 #pragma unroll
     for (int k = 0; k < kXRegs; ++k) {
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(128) void batch_output_norm_kernel(const float *__r
     double total = 0.0;
     total += red[0];
     total += red[1];
-    const float inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+    const float inv = 1.0f / sqrtf(static_cast<float>(div_count(total, width)) + eps);
 #pragma unroll 8
     for (int i = tid; i < width; i += 128) xnorm[static_cast<size_t>(i) * kMaxBatch + slot] = (x[base + i] * inv) * norm[i];
 }

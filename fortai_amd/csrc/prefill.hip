@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kRowThreads) void rms_quantize_tokens_kernel(const 
         __syncthreads();
         double total = 0.0;
         for (int w = 0; w < kRowThreads / 64; ++w) total += red[w];
-        inv = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+        inv = 1.0f / sqrtf(static_cast<float>(div_count(total, width)) + eps);
     }
     for (int g = tid; g < blocks_pad * 8; g += kRowThreads) {
         float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kRowThreads) void gated_quantize_tokens_kernel(cons
             static_cast<double>(y.z) * y.z + static_cast<double>(y.w) * y.w;
         ss = group_sum_up(ss, hl);
         if (in) {
-            const float nf = sqrtf(static_cast<float>(ss / static_cast<double>(head)) + eps);
+            const float nf = sqrtf(static_cast<float>(div_count(ss, head)) + eps);
             const float4 w4 = reinterpret_cast<const float4 *>(norm)[g % hl];
             const float4 z4 = reinterpret_cast<const float4 *>(zrow)[g];
             y.x = ((y.x / nf) * w4.x) * silu_poly(z4.x);

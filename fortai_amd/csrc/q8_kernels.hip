@@ -160,7 +160,7 @@ __device__ __forceinline__ void act_store(const MatvecInput &in, int chunks, con
                     ss = 0.0;
                     for (int w = 0; w < THREADS / 64; ++w) ss += red[w];
                 }
-                const float mean = static_cast<float>(ss / static_cast<double>(in.width));
+                const float mean = static_cast<float>(div_count(ss, in.width));
                 inverse_rms = 1.0f / sqrtf(mean + in.eps);
             }
             const int iters = (groups + THREADS - 1) / THREADS;
@@ -182,7 +182,7 @@ __device__ __forceinline__ void act_store(const MatvecInput &in, int chunks, con
                     ss += static_cast<double>(y.z) * static_cast<double>(y.z);
                     ss += static_cast<double>(y.w) * static_cast<double>(y.w);
                     ss = group_sum_up(ss, in.head / 4);
-                    const float nf = sqrtf(static_cast<float>(ss / static_cast<double>(in.head)) + in.eps);
+                    const float nf = sqrtf(static_cast<float>(div_count(ss, in.head)) + in.eps);
                     y.x = ((y.x / nf) * wr[k].x) * zr[k].x;
                     y.y = ((y.y / nf) * wr[k].y) * zr[k].y;
                     y.z = ((y.z / nf) * wr[k].z) * zr[k].z;
@@ -1154,7 +1154,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const flo
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     const double total = (red[0] + red[1]) + (red[2] + red[3]);
-    const float mean = static_cast<float>(total / static_cast<double>(n));
+    const float mean = static_cast<float>(div_count(total, n));
     const float inv = 1.0f / sqrtf(mean + eps);
     for (int i = tid; i < n; i += 256) out[i] = (x[i] * inv) * w[i];
 }
