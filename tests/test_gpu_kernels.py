@@ -259,7 +259,7 @@ def test_gdn_core_128_steps(ctx, oracle):
 @pytest.mark.parametrize("L,exact_max,skew", [(1, None, 0), (70, None, 0), (1024, None, 0), (4096, None, 0),
                                               (32768, None, 0), (32768, 1 << 20, 0), (70, 0, 0), (1024, 0, 0),
                                               (4095, 0, 0), (4096, None, 60), (4096, None, 1 << 20),
-                                              (8192, None, -90)])
+                                              (8192, None, -90), (8192, None, 0), (5000, None, 0)])
 def test_attention_core(ctx, oracle, L, exact_max, skew):
     """8 q / 2 kv heads x 256, fp16 cache, RoPE 1e7, append + attend at position L-1.
     Up to the layer's exact_max positions (default 8192; fortai_hip_qwen35_attention_set_exact_max) the output keeps the reference's two-pass
