@@ -910,9 +910,11 @@ def main() -> int:
     path = model_path(args)
     model, wall_ms, ev_ms, trace = bench_decode(args, path)
     tok_s = args.steps / (wall_ms * 1e-3)
-    roof = matvec_family_roofline(model)
-    roof_lm = lm_head_roofline(model)
-    families = family_breakdown(model, args.ctx - args.steps // 2)
+    # the timing probes replay graphs of their own; a --no-graph run (kernel
+    # tracing, whose profiler cannot follow graph launches) leaves them out
+    roof = None if DIRECT else matvec_family_roofline(model)
+    roof_lm = None if DIRECT else lm_head_roofline(model)
+    families = None if DIRECT else family_breakdown(model, args.ctx - args.steps // 2)
     mv = None if args.no_matvec else bench_matvec(model)
     kernels = None
     if not args.no_kernels:
