@@ -8,7 +8,7 @@
 // Q8_0, so a one-ulp change of an output flips an int8 now and then and the
 // trace drifts.  The parallel parts (the score of each position, e_p, e_p/Z,
 // every product) run on many lanes; only the left-to-right sums are chains.
-// The chains run from registers, handed from wave to wave (attend below).
+// The chains run from registers, handed from wave to wave (attend_given_z).
 #pragma once
 
 #include "fortai_hip_internal.h"
@@ -356,119 +356,9 @@ __device__ __forceinline__ void e_prefetch(const float *ev, int n, float (&e4)[k
     for (int i = 0; i < kPieces; ++i) e4[i] = ev[min(wave * kSeg + lane + 64 * i, n - 1)];
 }
 
-// Softmax weights and P.V of kDims value dims over n positions
-// (fortai_qwen35_cpu.f90:1016-1029):
-//   m = max_p s_p;  e_p = expf(s_p - m);  Z = e_0 + e_1 + ... (left to right)
-//   out_j = (e_0/Z) v_0,j + (e_1/Z) v_1,j + ... (left to right, each product
-//   rounded).
-// scores: the n scores (global memory or LDS; only read).  e_p is evaluated
-// twice, for Z and for the weights (the same value both times).  work:
-// work_floats() floats of LDS.  The value row of position p starts at
-// vbase + p * vstride (fp16 bits, kDims contiguous); v: value_prefetch of it.
-// All threads call it; the result is valid in threads 0..kDims-1.
-template <bool FINITE>
-__device__ __forceinline__ float attend(const float *scores, int n, const uint16_t *vbase, size_t vstride,
-    float *work, ValuePieces &v) {
-    static_assert(kDims == 8, "one 16-byte value piece per position");
-    const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6, lane = tid & 63;
-    float *red = work;
-    uint64_t *hand = reinterpret_cast<uint64_t *>(work + 8);
-    float *stage = work + 8 + 2 * kDims + wave * kDims * kStagePitch;
-    const int nseg = (n + kSeg - 1) / kSeg;
-    if (tid < kDims) hand[tid] = 0;
-    // the scores of the wave's next segment, a round ahead (clamped in bounds)
-    float s4[kPieces];
-    auto load_scores = [&](int k) {
-#pragma unroll
-        for (int i = 0; i < kPieces; ++i) s4[i] = scores[min(k * kSeg + lane + 64 * i, n - 1)];
-    };
-    if (wave < nseg) load_scores(wave);
-
-    // max (any order gives the same value)
-    constexpr float kLowest = -3.402823466e38f;  // -huge(1.0_real32)
-    constexpr int kUnroll = 8;
-    float m = kLowest;
-    for (int p0 = tid; p0 < n; p0 += kThreads * kUnroll) {
-        float x[kUnroll];
-#pragma unroll
-        for (int k = 0; k < kUnroll; ++k) x[k] = scores[min(p0 + k * kThreads, n - 1)];
-#pragma unroll
-        for (int k = 0; k < kUnroll; ++k) m = fmaxf(m, x[k]);  // clamped duplicates change nothing
-    }
-    m = wave_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    FORTAI_ATT_MARK(1);
-
-    // Z: each wave turns its segments' scores into e_p in its stage and sums
-    // them when its turn comes
-    f4 r[kSegVec];
-    for (int k = wave; k < nseg; k += kWaves) {
-        const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
-        float e[kPieces];
-#pragma unroll
-        for (int i = 0; i < kPieces; ++i) e[i] = p0 + lane + 64 * i < n ? expf_libm(s4[i] - m) : -0.0f;
-        if (k + kWaves < nseg) load_scores(k + kWaves);
-#pragma unroll
-        for (int i = 0; i < kPieces; ++i) stage[lane + 64 * i] = e[i];
-        seg_read(r, stage);
-        seg_held<0>(r);
-        float acc = take_turn(hand, k);
-        acc = seg_chain(r, cnt, acc);
-        if (lane == 0) pass_turn(hand, k + 1, acc);
-    }
-    __syncthreads();
-    const float z = __uint_as_float(static_cast<uint32_t>(hand[0]));
-    FORTAI_ATT_MARK(2);
-    __syncthreads();
-    if (tid < kDims) hand[tid] = 0;
-    if (wave < nseg) load_scores(wave);
-    __syncthreads();
-
-    // P.V: each wave writes its segment's products fl(fl(e_p/Z) v_p,j) to its
-    // stage [dim][position], fetches the scores and value pieces of its next
-    // segment, and lanes 0..kDims-1 sum their dim's row when the turn comes
-    float acc = 0.0f;
-    for (int k = wave; k < nseg; k += kWaves) {
-        const int p0 = k * kSeg, cnt = min(kSeg, n - p0);
-#pragma unroll
-        for (int i = 0; i < kPieces; ++i) {
-            const int j = lane + 64 * i, p = p0 + j;
-            if (p < n) {
-                const float wp = expf_libm(s4[i] - m) / z;
-                const uint32_t hw[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    stage[(2 * q) * kStagePitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] & 0xffffu));
-                    stage[(2 * q + 1) * kStagePitch + j] = wp * kv<FINITE>(static_cast<uint16_t>(hw[q] >> 16));
-                }
-            } else {
-#pragma unroll
-                for (int d = 0; d < kDims; ++d) stage[d * kStagePitch + j] = -0.0f;
-            }
-        }
-        if (k + kWaves < nseg) {
-            load_scores(k + kWaves);
-            value_fetch(vbase, vstride, n, k + kWaves, v);
-        }
-        if (lane < kDims) {
-            seg_read(r, stage + lane * kStagePitch);
-            seg_held<0>(r);
-            float a = take_turn(hand + lane, k);
-            a = seg_chain(r, cnt, a);
-            pass_turn(hand + lane, k + 1, a);
-        }
-    }
-    __syncthreads();
-    if (tid < kDims) acc = __uint_as_float(static_cast<uint32_t>(hand[tid]));
-    __syncthreads();  // hand and stage are free again when this returns
-    return acc;
-}
-
 // P.V of kDims value dims with Z given (attention_softmax_kernel's e values
 // and resolve_z): out_j = fl(e_0/Z v_0,j) + fl(e_1/Z v_1,j) + ... left to
-// right, the second half of attend().  ev: the n e values (global memory);
+// right.  ev: the n e values (global memory);
 // v and e4: the value pieces and e values of the wave's first segment
 // (value_prefetch, e_prefetch).  All threads call it; the result is valid in
 // threads 0..kDims-1.
