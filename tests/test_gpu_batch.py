@@ -116,6 +116,39 @@ def test_batch_long_trace_matches_single_sequence(model_paths, name, batch, step
         m.close()
 
 
+def test_batch_past_exact_limit_matches_single_sequence(model_paths):
+    """Attention layers whose exact limit is below the cache (exact_max 40 of
+    128): each sequence of the batch switches from the exact kernels to the
+    split-K pair when its own position passes the limit, in the same launch
+    as sequences still under it.  Split-K is held to 1e-3 against the
+    reference, but batch and single sequence run the same kernels per
+    sequence, so they must agree bit for bit.  (In this small model the
+    o-projection's Q8_0 input absorbs the split-K rounding: the logits equal
+    the exact path's too, so the test does not tell the regimes apart by
+    value; the attention-level tests do.)"""
+    m = Qwen35Hip(model_paths["qwen35-tiny"], max_context=128, batch=3, exact_max=40)
+    try:
+        starts, positions, steps = [9, 100, 4000], [0, 20, 34], 24
+        # the step's graph holds the split-K pair beside the exact kernels
+        assert any("attention_split_kernel" in step[1] for step in m.batch.plan())
+        m.batch.reset()
+        cur = np.array(starts)
+        got_logits, got_tokens = [], []
+        for k in range(steps):
+            nxt = m.batch.forward(cur, [p + k for p in positions])
+            got_logits.append(m.batch.logits.copy())
+            got_tokens.append(nxt.copy())
+            cur = nxt
+        got_logits = np.stack(got_logits)
+        for s in range(3):
+            print(f"sequence {s}: token {starts[s]} positions {positions[s]}..{positions[s] + steps - 1}", flush=True)
+            want_logits, want_tokens = run_single(m, starts[s], positions[s], steps)
+            assert np.array_equal(got_logits[:, s].view(np.uint32), want_logits.view(np.uint32)), f"sequence {s}"
+            assert [int(t[s]) for t in got_tokens] == want_tokens
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("rows,width,batch", [(3584, 1024, 8), (13, 96, 3), (2560, 9216, 8), (12352, 2560, 5),
                                               (1024, 3584, 1)])
 def test_batch_matvec_bit_identical(ctx, oracle, rows, width, batch):
