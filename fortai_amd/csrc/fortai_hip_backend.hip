@@ -1862,16 +1862,23 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
                 "GDN qkv/gate/alpha/beta projections, conv1d + SiLU");
             GdnParams gp = gdn_params(R, L.qkv, L.alpha, L.beta, L.o_raw);
             gp.state = L.state;
-            if (e == hipSuccess) e = rec(launch_gdn_delta(gp, stream, B), "GDN L2 norms, decay/beta, delta rule");
-            MatvecInput gated;
-            gated.x = L.o_raw;
-            gated.z = L.z;
-            gated.norm = R->ssm_norm;
-            gated.eps = R->eps;
-            gated.head = R->head;
-            gated.width = R->inner;
-            if (e == hipSuccess)
-                e = rec(launch_q8l_prep(gated, Prologue::GATED, b->act, B, stream), "GDN gated RMSNorm and quantize");
+            if (e == hipSuccess && (R->head == 64 || R->head == 128) && R->inner % 128 == 0) {
+                // one workgroup per (value head, sequence): the delta rule, then
+                // the gated norm and quantization for ssm_out in the same launch
+                e = rec(launch_gdn_delta_gated(gp, L.z, R->ssm_norm, R->eps, b->act, stream, B),
+                    "GDN L2 norms, decay/beta, delta rule, gated RMSNorm and quantize");
+            } else {
+                if (e == hipSuccess) e = rec(launch_gdn_delta(gp, stream, B), "GDN L2 norms, decay/beta, delta rule");
+                MatvecInput gated;
+                gated.x = L.o_raw;
+                gated.z = L.z;
+                gated.norm = R->ssm_norm;
+                gated.eps = R->eps;
+                gated.head = R->head;
+                gated.width = R->inner;
+                if (e == hipSuccess)
+                    e = rec(launch_q8l_prep(gated, Prologue::GATED, b->act, B, stream), "GDN gated RMSNorm and quantize");
+            }
             const MatvecSegment oseg = segment(R->out, b->x, b->x);
             if (e == hipSuccess)
                 e = rec(launch_q8_batch_matvec(&oseg, 1, b->act, R->inner, B, Epilogue::ADD, stream),

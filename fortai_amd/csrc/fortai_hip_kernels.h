@@ -210,6 +210,13 @@ struct GdnParams {
 hipError_t launch_gdn_recurrence(const GdnParams &p, const float *conv_w, const float *conv_in, float *conv_state,
     int conv_size, int K, int steps, hipStream_t stream);
 hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream, int batch = 1);
+// The delta rule of one whole value head per workgroup followed by the
+// head's gated RMSNorm and Q8_0 quantization into q8l [batch][q8l_bytes(width)]
+// (width = value_heads * head): the bits of launch_gdn_delta then
+// launch_q8l_prep(GATED), in one launch.  head 64 or 128, width % 128 == 0;
+// z: SiLU'd gate [batch][width]; norm: [head]; eps: the gated norm's.
+hipError_t launch_gdn_delta_gated(const GdnParams &p, const float *z, const float *norm, float eps, void *q8l,
+    hipStream_t stream, int batch);
 // Causal conv1d + SiLU of every channel of x, shifting the windows
 // conv_state[K-1][channels] (oldest first).
 hipError_t launch_conv_silu(const float *x, const float *conv_w, float *conv_state, float *out, int channels, int K,

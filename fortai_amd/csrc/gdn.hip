@@ -151,6 +151,125 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
     if (l == 0) p.out[h * HEAD + row] = qd * (1.0f / sqrtf(static_cast<float>(HEAD)));
 }
 
+// The batch decode's delta rule with the ssm_out projection's input built in
+// the same launch: one workgroup per (value head, sequence) runs every state
+// row of the head (HEAD x 8 threads, the row code of gdn_delta_kernel above,
+// operation for operation), collects the head's raw output in LDS, and then
+// wave 0 forms the head's gated RMSNorm and Q8_0 quantization with the
+// matvec's gated-prologue code (a lane per 4 values, the double sum of
+// squares by the same butterfly over the head's lanes, the same per-value
+// expression and quantizer) into the Q8L activation [batch][q8l_bytes(width)]
+// that the batched ssm_out projection reads -- the bits the separate
+// normalise-and-quantize launch would write.  width = value_heads * HEAD, a
+// multiple of 128 (no padding blocks); z: the SiLU'd gate [batch][width];
+// norm: the per-head weights [HEAD]; eps: the gated norm's epsilon.
+template <int HEAD>
+__global__ __launch_bounds__(HEAD * 8) void gdn_delta_gated_kernel(const GdnParams p_batch, const float *z_batch,
+    const float *norm, float eps, void *q8l, int width) {
+    const int seq = static_cast<int>(blockIdx.y);
+    const GdnParams p = gdn_seq(p_batch, seq);
+    constexpr int kThreads = HEAD * 8;
+    constexpr int kCols = HEAD / 8;
+    constexpr int kGroups = HEAD / 4;  // 4-value groups (lanes of wave 0) per head
+    static_assert(kGroups <= 64 && kGroups % 8 == 0, "one head's groups in whole blocks of wave 0");
+    __shared__ __align__(16) float qs[HEAD];
+    __shared__ __align__(16) float ks[HEAD];
+    __shared__ __align__(16) float os[HEAD];
+    __shared__ double red[2];
+    __shared__ float hs[2];
+    __shared__ MathTables mt;
+    const uint64_t mt_word = MathTables::fetch();  // stored after the other loads are issued
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const int h = static_cast<int>(blockIdx.x);
+    const int kh = h / (p.value_heads / p.key_heads);
+    const int row = tid >> 3, l = tid & 7;
+    float s[kCols];
+    float4 *srow = reinterpret_cast<float4 *>(p.state + ((static_cast<size_t>(h) * HEAD + row) * 8 + l) * kCols);
+#pragma unroll
+    for (int i = 0; i < kCols / 4; ++i) {
+        const float4 f = srow[i];
+        s[4 * i] = f.x; s[4 * i + 1] = f.y; s[4 * i + 2] = f.z; s[4 * i + 3] = f.w;
+    }
+    const int iq = min(tid, 2 * HEAD - 1);
+    const float qk = p.qkv[iq < HEAD ? kh * HEAD + iq : p.state_size * p.key_heads + kh * HEAD + (iq - HEAD)];
+    const float vrow = p.qkv[2 * p.state_size * p.key_heads + h * HEAD + row];
+    const float beta_in = p.beta[h], alpha_in = p.alpha[h], ssm_a = p.ssm_a[h], ssm_dt = p.ssm_dt[h];
+    // the gated norm's inputs (wave 0; lanes past the head's groups re-read its last)
+    const int t = min(lane, kGroups - 1);
+    float4 zr = make_float4(0.0f, 0.0f, 0.0f, 0.0f), wr = zr;
+    if (wave == 0) {
+        zr = reinterpret_cast<const float4 *>(z_batch + static_cast<size_t>(seq) * width)[h * kGroups + t];
+        wr = reinterpret_cast<const float4 *>(norm)[t];
+    }
+    mt.put(mt_word);
+    if (tid < HEAD) qs[tid] = qk;
+    else if (tid < 2 * HEAD) ks[tid - HEAD] = qk;
+    __syncthreads();
+    if (tid == 0) {
+        // fortai_qwen35_cpu.f90:890-894 (the tables in LDS since the barrier)
+        hs[0] = mt.sigmoid(beta_in);
+        hs[1] = mt.expf(ssm_a * mt.softplus(alpha_in + ssm_dt));
+    }
+    // L2 norms of q (wave 0) and k (wave 1), fortai_qwen35_cpu.f90:1455-1471
+    if (tid < 128) {
+        const float *v = (tid < 64) ? qs : ks;
+        double ss = 0.0;
+        for (int i = tid & 63; i < HEAD; i += 64) ss += static_cast<double>(v[i]) * static_cast<double>(v[i]);
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+    }
+    __syncthreads();
+    const float qinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[0])), p.eps);
+    const float kinv = 1.0f / fmaxf(sqrtf(static_cast<float>(red[1])), p.eps);
+    const float beta = hs[0];
+    const float decay = hs[1];
+    // delta rule (fortai_q8_dot.c:363-396), the normalized q and k read from LDS
+    float kd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) {
+        const float d = s[i] * decay;
+        s[i] = d;
+        kd = __builtin_fmaf(d, ks[8 * i + l] * kinv, kd);
+    }
+    kd = row_hsum8(kd);
+    const float delta = (vrow - kd) * beta;
+    float qd = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCols; ++i) {
+        const float u = __builtin_fmaf(delta, ks[8 * i + l] * kinv, s[i]);
+        s[i] = u;
+        qd = __builtin_fmaf(u, qs[8 * i + l] * qinv, qd);
+    }
+    qd = row_hsum8(qd);
+#pragma unroll
+    for (int i = 0; i < kCols / 4; ++i) srow[i] = make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
+    if (l == 0) os[row] = qd * (1.0f / sqrtf(static_cast<float>(HEAD)));
+    __syncthreads();
+    if (wave != 0) return;
+    // gated RMSNorm of the head, fortai_qwen35_cpu.f90:907-915, then Q8_0
+    float4 y = reinterpret_cast<const float4 *>(os)[t];
+    double ss = static_cast<double>(y.x) * static_cast<double>(y.x);
+    ss += static_cast<double>(y.y) * static_cast<double>(y.y);
+    ss += static_cast<double>(y.z) * static_cast<double>(y.z);
+    ss += static_cast<double>(y.w) * static_cast<double>(y.w);
+    ss = group_sum_up(ss, kGroups);
+    const float nf = sqrtf(static_cast<float>(div_count(ss, HEAD)) + eps);
+    y.x = ((y.x / nf) * wr.x) * zr.x;
+    y.y = ((y.y / nf) * wr.y) * zr.y;
+    y.z = ((y.z / nf) * wr.z) * zr.z;
+    y.w = ((y.w / nf) * wr.w) * zr.w;
+    float scale;
+    uint16_t bits;
+    const uint32_t packed = quantize_group(y, scale, bits);
+    if (lane < kGroups) {
+        const int g = h * kGroups + lane, b = g >> 3, lb = g & 7;
+        unsigned char *base = static_cast<unsigned char *>(q8l) + static_cast<size_t>(seq) * q8l_bytes(width);
+        reinterpret_cast<uint32_t *>(base)[((b >> 2) * 8 + lb) * 4 + (b & 3)] = packed;
+        const int chunks = width / 128;
+        if (lb == 0) reinterpret_cast<float *>(base + static_cast<size_t>(chunks) * 128)[b] = scale;
+    }
+}
+
 // ------------------------------------------------------- state-resident
 // `steps` autoregressive steps of the recurrent core in one launch: each
 // workgroup keeps its 16 state rows in registers across every step, and the
@@ -315,6 +434,21 @@ hipError_t launch_gdn_delta(const GdnParams &p, hipStream_t stream, int batch) {
     default: return hipErrorInvalidValue;
     }
     note_launch("gdn_delta_kernel<%d> grid %dx%d", p.head, grid.x, batch);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_delta_gated(const GdnParams &p, const float *z, const float *norm, float eps, void *q8l,
+    hipStream_t stream, int batch) {
+    const int width = p.value_heads * p.head;
+    if (batch < 1 || p.key_heads <= 0 || p.value_heads % p.key_heads || p.state_size != p.head || width % 128 || !q8l)
+        return hipErrorInvalidValue;
+    const dim3 grid(p.value_heads, batch);
+    switch (p.head) {
+    case 64: hipLaunchKernelGGL(gdn_delta_gated_kernel<64>, grid, dim3(64 * 8), 0, stream, p, z, norm, eps, q8l, width); break;
+    case 128: hipLaunchKernelGGL(gdn_delta_gated_kernel<128>, grid, dim3(128 * 8), 0, stream, p, z, norm, eps, q8l, width); break;
+    default: return hipErrorInvalidValue;
+    }
+    note_launch("gdn_delta_gated_kernel<%d> grid %dx%d", p.head, grid.x, batch);
     return hipGetLastError();
 }
 
