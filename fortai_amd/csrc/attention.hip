@@ -60,9 +60,32 @@ __device__ __forceinline__ AttentionParams attention_seq(AttentionParams p, int 
     p.partial += static_cast<size_t>(s) * workspace_floats(p.heads, p.max_context);
     p.cache_flags += static_cast<size_t>(s) * p.kv_heads;
     p.out += static_cast<size_t>(s) * p.heads * p.value;
+    if (p.out_q8l) p.out_q8l = static_cast<unsigned char *>(p.out_q8l) + static_cast<size_t>(s) * q8l_bytes(p.heads * p.value);
     p.position += s;
     if (p.split) p.split += static_cast<size_t>(s) * p.heads * nmax * (p.value + 2);
     return p;
+}
+
+// Wave 0 of a workgroup holding 64 consecutive outputs (lane d: output
+// h * value + d0 + d, 64-aligned): their Q8_0 quantization into p.out_q8l,
+// the two blocks as the matvec's f32 prologue forms them (lane j of 16: the
+// 4-value group j, fortai_q8_quantize's amax, scale and rounding).  lds: 64
+// floats of the caller's LDS, free for this wave.
+__device__ __forceinline__ void out_quantize64(const AttentionParams &p, int h, int d0, float val, float *lds) {
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    lds[lane] = val;
+    wave_lds_fence();
+    const float4 y = reinterpret_cast<const float4 *>(lds)[lane & 15];
+    float scale;
+    uint16_t bits;
+    const uint32_t packed = quantize_group(y, scale, bits);
+    if (lane < 16) {
+        const int g = (h * p.value + d0) / 4 + lane, b = g >> 3, l = g & 7;
+        unsigned char *base = static_cast<unsigned char *>(p.out_q8l);
+        reinterpret_cast<uint32_t *>(base)[((b >> 2) * 8 + l) * 4 + (b & 3)] = packed;
+        const int chunks = p.heads * p.value / 128;
+        if (l == 0) reinterpret_cast<float *>(base + static_cast<size_t>(chunks) * 128)[b] = scale;
+    }
 }
 
 __global__ __launch_bounds__(ea::kThreads) void attention_scores_kernel(const AttentionParams p_batch) {
@@ -581,7 +604,9 @@ __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int
     FORTAI_ATTW_MARK(5);
     if (wave == 0 && d < VD) {
         const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d];
-        p.out[static_cast<size_t>(h) * VD + d] = acc * sigmoid_ref(gate);
+        const float o = acc * sigmoid_ref(gate);
+        p.out[static_cast<size_t>(h) * VD + d] = o;
+        if (p.out_q8l) out_quantize64(p, h, d0, o, wt);  // (the tile is consumed: wt is free)
     }
 }
 
@@ -812,7 +837,9 @@ __global__ __launch_bounds__(ea::kThreads) void attention_merge_kernel(const Att
 #pragma unroll
     for (int k = 0; k < kMergeParts; ++k) sum += part[k][dl];
     const float gate = p.q[static_cast<size_t>(h) * 2 * HD + HD + d0 + dl];
-    p.out[static_cast<size_t>(h) * VD + d0 + dl] = (sum / z) * sigmoid_ref(gate);
+    const float out = (sum / z) * sigmoid_ref(gate);
+    p.out[static_cast<size_t>(h) * VD + d0 + dl] = out;
+    if (p.out_q8l) out_quantize64(p, h, d0, out, &part[1][0]);  // (wave 0 has read part)
 }
 
 }  // namespace
@@ -828,8 +855,15 @@ int softmax_groups(int positions, int batch) {
     return batch > 1 && segs > 8 ? 8 : segs;
 }
 
+bool attention_quantizes_output(const AttentionParams &p, int batch) {
+    const int exact_positions = p.max_context < p.exact_max ? p.max_context : p.exact_max;
+    const bool wide = (batch > 1 || p.force_wide) && exact_positions <= kWideMaxPositions && p.value <= ea::kThreads;
+    return wide && p.value % 64 == 0 && (p.heads * p.value) % 128 == 0;
+}
+
 hipError_t launch_attention(const AttentionParams &params, hipStream_t stream, int batch) {
     if (batch < 1) return hipErrorInvalidValue;
+    if (params.out_q8l && !attention_quantizes_output(params, batch)) return hipErrorInvalidValue;
     const int group = params.kv_heads > 0 ? params.heads / params.kv_heads : 0;
     AttentionParams p = params;
     p.div_heads = fast_div(static_cast<uint32_t>(p.heads));

@@ -1890,11 +1890,15 @@ hipError_t enqueue_batch_step(fortai_hip_qwen35_batch *b, hipStream_t stream) {
             AttentionParams ap = attention_params(A, L.q, L.k, L.v, L.attn_out);
             ap.kcache = L.kcache; ap.vcache = L.vcache; ap.partial = L.partial; ap.cache_flags = L.flags;
             ap.split = L.split; ap.position = b->positions; ap.max_context = b->max_context;
+            // the output kernels also quantize the o projection's input when they can
+            ap.out_q8l = b->act;
+            if (!attention_quantizes_output(ap, B)) ap.out_q8l = nullptr;
             if (e == hipSuccess) e = rec(launch_attention(ap, stream, B), "q/k norm, RoPE, KV append, softmax.V, gate");
             MatvecInput oin;
             oin.x = L.attn_out;
             oin.width = A->heads * A->value;
-            if (e == hipSuccess) e = rec(launch_q8l_prep(oin, Prologue::F32, b->act, B, stream), "quantize attention output");
+            if (e == hipSuccess && !ap.out_q8l)
+                e = rec(launch_q8l_prep(oin, Prologue::F32, b->act, B, stream), "quantize attention output");
             const MatvecSegment oseg = segment(A->o, b->x, b->x);
             if (e == hipSuccess)
                 e = rec(launch_q8_batch_matvec(&oseg, 1, b->act, oin.width, B, Epilogue::ADD, stream),

@@ -235,6 +235,10 @@ struct AttentionParams {
     float *partial = nullptr;       // workspace (attention_scores_floats): scores, e values, Z tables
     int *cache_flags = nullptr;     // [kv_heads]: 1 once the cache holds an exponent-31 half
     float *out = nullptr;           // [heads][value] gated output
+    // optional (batches): the same output also as the Q8L activation of the o
+    // projection, [batch][q8l_bytes(heads * value)], written by the wide and
+    // merge kernels (value % 64 == 0 and heads * value % 128 == 0)
+    void *out_q8l = nullptr;
     const int *position = nullptr;  // device position (the new token's index)
     int heads = 0, kv_heads = 0, head = 0, value = 0, max_context = 0, rope_dim = 0;
     float eps = 0.0f;
@@ -254,6 +258,9 @@ int attention_split_chunks(int max_context);
 // batch > 1: sequences along blockIdx.y, every buffer [batch][single size],
 // position[batch]
 hipError_t launch_attention(const AttentionParams &p, hipStream_t stream, int batch = 1);
+// whether launch_attention honours p.out_q8l for this shape and batch (the
+// wide output kernel and the split-K merge write it)
+bool attention_quantizes_output(const AttentionParams &p, int batch);
 size_t attention_scores_floats(int heads, int max_context);
 
 // ---- prompt prefill (prefill.hip): rows are tokens, row s * T + t ---------------
