@@ -636,8 +636,10 @@ def cpu_baseline(path, ctx_len: int, steps: int, repeats: int = 5):
         out = subprocess.run([exe, path, str(START_TOKEN), str(nsteps), str(ctx_len), str(first)], capture_output=True,
                              text=True, env=env, timeout=600)
         m = re.search(r"forward_seconds=\s*([0-9.Ee+-]+)", out.stdout)
-        if out.returncode != 0 or not m:
+        t = re.search(r"last_token=\s*(-?[0-9]+)", out.stdout)
+        if out.returncode != 0 or not m or not t:
             raise RuntimeError("reference CPU run failed: " + out.stdout[-300:] + out.stderr[-300:])
+        run.last_token = int(t.group(1))
         return nsteps / float(m.group(1))
 
     sweep = {}
@@ -651,7 +653,18 @@ def cpu_baseline(path, ctx_len: int, steps: int, repeats: int = 5):
     best = max(sweep, key=sweep.get)
     log(f"CPU baseline: {repeats} runs of {steps} steps at {best} threads")
     vals = [run(best, steps, start) for _ in range(repeats)]
+    # the timed build's own output: its greedy trace from position 0 against
+    # the golden the GPU trace is checked with (written by the -O2 build)
+    check_steps = 16
+    run(best, check_steps, 0)
+    check = {"steps_from_position_0": check_steps, "last_token": run.last_token}
+    if os.path.exists(GOLDEN_TRACE):
+        import numpy as np
+        with np.load(GOLDEN_TRACE) as z:
+            check["golden_token"] = int(z["tokens"][check_steps - 1])
+        check["matches_golden"] = check["golden_token"] == run.last_token
     return {"value": round(statistics.median(vals), 4), "unit": "tokens/s", "cores": best, "kind": "reference",
+            "output_check": check,
             "sample": f"{steps} greedy decode steps of the same 0.8B GGUF from token {START_TOKEN} at positions "
                       f"{start}..{ctx_len - 1} of a {ctx_len} context (forward + maxloc, load excluded); median of "
                       f"{repeats} runs; the reference's Fortran+C sources built with its native flags "
