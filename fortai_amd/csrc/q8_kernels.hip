@@ -584,20 +584,21 @@ __device__ __forceinline__ void scales_f(uint2 sc, float (&ws)[4]) {
 // CH > 0: exactly CH chunks, the group loop fully unrolled (a rolled loop
 // makes the compiler wait for every prefetch at its head); CH == 0: any count.
 template <Epilogue EPI, int SPLIT, int G, int WAVES, int CH>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES / 2))) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES >= 16 ? 4 : WAVES / 2))) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
     constexpr int NS = kMaxBatch / SPLIT;
     extern __shared__ __align__(16) unsigned char lds[];
     const int seq_bytes = args.chunks * 144;
     const int act_bytes = (args.batch * seq_bytes + 1023) / 1024 * 1024;  // whole 1 KiB load blocks
-    float *epi = reinterpret_cast<float *>(lds + act_bytes);  // [8][32]
+    constexpr int kSlots = WAVES / SPLIT;                      // row groups per workgroup
+    float *epi = reinterpret_cast<float *>(lds + act_bytes);  // [8][kSlots * 8]
     // the gate/up pair with one chunk per group: each wave forms the chunk's
     // scale products fl(f32(w_scale) * a_scale) once per (matrix, row,
     // sequence, block) -- four per lane -- into its own LDS table, instead of
     // every lane of a row forming all of them; LDS operations of one wave
     // read back after a wavefront-scope fence, without a workgroup barrier
     constexpr bool kTable = kPair && G == 1 && NS == 4;
-    float *ptab = epi + kMaxBatch * 32 + (static_cast<int>(threadIdx.x) >> 6) * 2 * 8 * NS * 4;  // [2][8][NS][4]
+    float *ptab = epi + kMaxBatch * kSlots * 8 + (static_cast<int>(threadIdx.x) >> 6) * 2 * 8 * NS * 4;  // [2][8][NS][4]
 
     const int wg = static_cast<int>(blockIdx.x);
     int sgi = 0;
@@ -800,25 +801,28 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVE
             const float h = row < args.pair_vector_rows ? silu_poly(acc[k]) * acc2[k]
                                                         : acc[k] / (1.0f + exp_rounded(-acc[k])) * acc2[k];
             if (writer && mine && out) out[row] = h;
-            if (seg.out_q8l && l == 0 && mine) epi[sq[k] * 32 + slot * 8 + r] = h;
+            if (seg.out_q8l && l == 0 && mine) epi[sq[k] * (kSlots * 8) + slot * 8 + r] = h;
         }
     }
     if constexpr (kPair) {
         if (seg.out_q8l) {
-            // WAVES / SPLIT == 4: the workgroup's 32 rows form one quantization
-            // block of every sequence's h
+            // every 32 rows of the workgroup (4 row groups) form one
+            // quantization block of every sequence's h
+            static_assert(kSlots % 4 == 0, "whole quantization blocks per workgroup");
+            constexpr int kBlocks = kSlots / 4;
             __syncthreads();
-            const int t = tid & 7, q = tid >> 3;
-            if (q < args.batch) {
-                const float *e = epi + q * 32;
+            const int t = tid & 7, q = tid >> 3;  // q: sequence + 8 * block
+            const int qs = q & 7, qb = q >> 3;
+            if (qs < args.batch && qb < kBlocks) {
+                const float *e = epi + qs * (kSlots * 8) + qb * 32;
                 const float4 y = make_float4(e[4 * t], e[4 * t + 1], e[4 * t + 2], e[4 * t + 3]);
                 float scale;
                 uint16_t bits;
                 const uint32_t packed = quantize_group(y, scale, bits);
-                const int b = wg - args.first_wg[sgi];
+                const int b = (wg - args.first_wg[sgi]) * kBlocks + qb;
                 const int hchunks = (seg.w.rows / kQ8Block + 3) / 4;
                 uint32_t *dq = reinterpret_cast<uint32_t *>(static_cast<unsigned char *>(seg.out_q8l) +
-                    static_cast<size_t>(q) * q8l_bytes(seg.w.rows));
+                    static_cast<size_t>(qs) * q8l_bytes(seg.w.rows));
                 dq[((b >> 2) * 8 + t) * 4 + (b & 3)] = packed;
                 if (t == 0) reinterpret_cast<float *>(dq + hchunks * 32)[b] = scale;
             }
@@ -1003,8 +1007,8 @@ hipError_t launch_batch_g(const BatchMatvecArgs &args, int grid, size_t lds, hip
     const int c = args.chunks;
     // eight-wave workgroups run two per CU with single-chunk groups (larger
     // groups exceed that register budget)
-    const int g = WAVES == 8 ? 1 : (c % 4 == 0 ? 4 : (c % 2 == 0 ? 2 : 1));
-    if constexpr (WAVES == 8) {
+    const int g = WAVES >= 8 ? 1 : (c % 4 == 0 ? 4 : (c % 2 == 0 ? 2 : 1));
+    if constexpr (WAVES >= 8) {
         // the widths of the supported shapes unrolled exactly
 #define FORTAI_PAIR(CHN) hipLaunchKernelGGL((q8_batch_matvec_kernel<EPI, SPLIT, 1, WAVES, CHN>), dim3(grid), \
         dim3(WAVES * 64), lds, stream, args)
@@ -1292,7 +1296,13 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
     args.split = split;
     args.act = q8l;
     int grid = 0;
-    const int per_wg = epilogue == Epilogue::SILU_PAIR ? 4 : 4 / split;
+    // the pair: one 32-row quantization block of h per eight-wave workgroup,
+    // or two per sixteen-wave workgroup when the blocks outnumber the CUs (a
+    // launch of, say, 288 blocks would give 32 CUs two workgroups each and
+    // end with them; 144 workgroups of two blocks each end together)
+    const bool pair_blocks2 = epilogue == Epilogue::SILU_PAIR && segments[0].w.row_groups > 4 * 256 &&
+        segments[0].w.row_groups % 8 == 0;
+    const int per_wg = epilogue == Epilogue::SILU_PAIR ? (pair_blocks2 ? 8 : 4) : 4 / split;
     for (int s = 0; s < count; ++s) {
         args.seg[s] = segments[s];
         args.first_wg[s] = grid;
@@ -1351,9 +1361,13 @@ hipError_t launch_q8_batch_matvec(const MatvecSegment *segments, int count, cons
             ns, ring_grid, seq_blocks);
         return hipGetLastError();
     }
-    // the pair's per-wave scale-product tables: 8 waves x [2][8][4][4] floats
-    if (epilogue == Epilogue::SILU_PAIR)
+    // the pair's per-wave scale-product tables: waves x [2][8][4][4] floats
+    if (epilogue == Epilogue::SILU_PAIR) {
+        if (pair_blocks2)
+            return launch_batch_g<Epilogue::SILU_PAIR, 2, 16>(args, grid, lds + kMaxBatch * 32 * 4 +
+                16 * 2 * 8 * 4 * 4 * sizeof(float), stream);
         return launch_batch_g<Epilogue::SILU_PAIR, 2, 8>(args, grid, lds + 8 * 2 * 8 * 4 * 4 * sizeof(float), stream);
+    }
     if (epilogue == Epilogue::STORE) {
         if (split == 1) return launch_batch_g<Epilogue::STORE, 1>(args, grid, lds, stream);
         if (split == 2) return launch_batch_g<Epilogue::STORE, 2>(args, grid, lds, stream);
