@@ -775,7 +775,7 @@ def bench_config5(steps: int = 32, warmup: int = 4, prompt: int = 512, batch: in
         "workload": f"Qwen3.5-4B-shaped Q8_0, batch {batch} independent sequences, context {ctx}",
         "prefill": {"tokens": tokens, "prompt_per_sequence": prompt, "ms": round(prefill_ms, 2),
                     "tokens_per_s": round(tokens / (prefill_ms * 1e-3), 1),
-                    "path": "projections in the reference's eight-lane fp32 order on v_mfma_f32_32x32x4_2b_f16 "
+                    "path": "projections in the reference's eight-lane fp32 order on v_mfma_f32_16x16x4f16 "
                             "(q8_mmq_exact_kernel); conv1d, delta rule and exact causal attention over time",
                     "fast_variant": {"ms": round(fast_ms, 2), "tokens_per_s": round(tokens / (fast_ms * 1e-3), 1),
                                      "path": "prefill mode fast: whole-block int32 dots on "

@@ -240,22 +240,27 @@ __global__ __launch_bounds__(kMmqThreads, 2) void q8_mmq_kernel(Q8Matrix w, cons
 // by block, then the horizontal sum ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)).  So
 // every output is bit-identical to the decode matvec of that token.
 //
-// The 4-byte lane dots come from v_mfma_f32_32x32x4_2b_f16: two independent
-// 32x32x4 products per instruction (lanes 0..31 feed the first, 32..63 the
-// second), so four instructions give the eight lane dots of a 32 x 32 tile
-// and block.  int8 values are exact in fp16, and the products and their
-// 4-term sums (|sum| <= 4 * 128 * 127) are exact in the fp32 accumulator, so
-// the dots arrive as exact floats and need no conversion.  The int8 operands
-// are widened to fp16 once, when a chunk (four blocks) is staged in LDS: the
-// biased byte b + 128 under the fp16 exponent of 1024 is 1024 + b + 128
-// exactly, and one packed fp16 subtraction of 1152 leaves b.
+// The 4-byte lane dots come from v_mfma_f32_16x16x4f16: four independent
+// 16x16x4 products per instruction, one per lane part (lane l feeds block
+// l / 16 with row or column l % 16; output register r of lane l is block
+// r / 4, row 4 (l / 16) + r % 4, column l % 16), so two instructions give the
+// eight lane dots of a 16 x 16 quadrant and block.  int8 values are exact in
+// fp16, and the products and their 4-term sums (|sum| <= 4 * 128 * 127) are
+// exact in the fp32 accumulator, so the dots arrive as exact floats and need
+// no conversion.  Per lane dot the 16x16 shape costs the matrix cores what
+// the 32x32x4 one does, with half the result registers, which leaves room
+// for the next instruction's result while the vector ALUs run the fmas of
+// the current one.  The int8 operands are widened to fp16 once, when a chunk
+// (four blocks) is staged in LDS: the biased byte b + 128 under the fp16
+// exponent of 1024 is 1024 + b + 128 exactly, and one packed fp16
+// subtraction of 1152 leaves b.
 //
 // Staging: per block and token (or row) the eight 4-value lane parts in the
-// order 0 2 4 6 1 3 5 7, so that a lane reads its four parts (the first or
-// the second of each pair) as 32 contiguous bytes.
+// order 0 4 1 5 2 6 3 7, so that the lane feeding block s reads parts s and
+// s + 4 (one per instruction group) as 16 contiguous bytes.
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kXTile = 64;    // tokens and rows per workgroup (4 waves of 32 x 32)
 constexpr int kXPitch = 36;   // halves per staged (block, token or row): 32 + 4 pad
@@ -268,8 +273,8 @@ struct MmqExactStage {
     float bs[4][kXTile];
 };
 
-// the staged position of lane part L (order 0 2 4 6 1 3 5 7), in halves
-__device__ __forceinline__ int part_slot(int L) { return ((L & 1) * 4 + (L >> 1)) * 4; }
+// the staged position of lane part L (order 0 4 1 5 2 6 3 7), in halves
+__device__ __forceinline__ int part_slot(int L) { return ((L & 3) * 2 + (L >> 2)) * 4; }
 
 // four signed bytes -> four fp16 values (exact)
 __device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(kXThreads, 2) void q8_mmq_exact_kernel(Q8Matrix w, 
     MmqExactStage *stage = reinterpret_cast<MmqExactStage *>(lds_raw);
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63, wave = tid >> 6;
-    const int i = lane & 31, h = lane >> 5;
+    const int i = lane & 15, s4 = lane >> 4;  // quadrant row / column, and lane part (block) s4
     const int t0 = static_cast<int>(blockIdx.y) * kXTile;
     const int r0 = static_cast<int>(blockIdx.x) * kXTile;
     const int twl = (wave & 1) * 32;   // wave's first token within the tile
@@ -367,49 +372,62 @@ __global__ __launch_bounds__(kXThreads, 2) void q8_mmq_exact_kernel(Q8Matrix w, 
         if (c + 1 < chunks) fetch(c + 1);
 #pragma unroll 1
         for (int j = 0; j < 4; ++j) {
-            // this lane's parts h, 2 + h, 4 + h, 6 + h of token twl + i and row rwl + i
-            const h4 *ap = reinterpret_cast<const h4 *>(&st.a[j][twl + i][16 * h]);
-            const h4 *bp = reinterpret_cast<const h4 *>(&st.b[j][rwl + i][16 * h]);
-            h4 av[4], bv[4];
+            // parts s4 and s4 + 4 of tokens twl + 16 th + i and rows rwl + 16 rh + i
+            h4 av[2][2], bv[2][2];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                av[k] = ap[k];
-                bv[k] = bp[k];
+            for (int q = 0; q < 2; ++q) {
+                const h4 *ap = reinterpret_cast<const h4 *>(&st.a[j][twl + 16 * q + i][8 * s4]);
+                const h4 *bp = reinterpret_cast<const h4 *>(&st.b[j][rwl + 16 * q + i][8 * s4]);
+                av[q][0] = ap[0];
+                av[q][1] = ap[1];
+                bv[q][0] = bp[0];
+                bv[q][1] = bp[1];
             }
-            // scale products of this lane's 16 tokens twl + 8 (v / 4) + 4 h + v % 4 and row rwl + i
-            const float wsc = st.bs[j][rwl + i];
-            float sc[16];
+            // scale products of this lane's outputs: tokens twl + 16 th + 4 s4 + u, rows rwl + 16 rh + i
+            float sc[2][2][4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 s4 = *reinterpret_cast<const float4 *>(&st.as[j][twl + 8 * q + 4 * h]);
-                sc[4 * q] = wsc * s4.x;
-                sc[4 * q + 1] = wsc * s4.y;
-                sc[4 * q + 2] = wsc * s4.z;
-                sc[4 * q + 3] = wsc * s4.w;
-            }
+            for (int rh = 0; rh < 2; ++rh) {
+                const float wsc = st.bs[j][rwl + 16 * rh + i];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const f32x32 zero = {};
-                const f32x32 d = __builtin_amdgcn_mfma_f32_32x32x4f16(av[k], bv[k], zero, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    acc[2 * k][v] = __builtin_fmaf(sc[v], d[v], acc[2 * k][v]);
-                    acc[2 * k + 1][v] = __builtin_fmaf(sc[v], d[16 + v], acc[2 * k + 1][v]);
+                for (int th = 0; th < 2; ++th) {
+                    const float4 a4 = *reinterpret_cast<const float4 *>(&st.as[j][twl + 16 * th + 4 * s4]);
+                    sc[th][rh][0] = wsc * a4.x;
+                    sc[th][rh][1] = wsc * a4.y;
+                    sc[th][rh][2] = wsc * a4.z;
+                    sc[th][rh][3] = wsc * a4.w;
                 }
-                // one MFMA result live at a time (the other wave of the SIMD
-                // covers the MFMA latency)
+            }
+            // eight instructions (part group g, token half th, row half rh),
+            // each issued before the fmas of the previous one
+            const f32x16 zero = {};
+            f32x16 d = __builtin_amdgcn_mfma_f32_16x16x4f16(av[0][0], bv[0][0], zero, 0, 0, 0);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const int g = m >> 2, th = (m >> 1) & 1, rh = m & 1;
+                f32x16 dn = zero;
+                if (m < 7) {
+                    const int g1 = (m + 1) >> 2, th1 = ((m + 1) >> 1) & 1, rh1 = (m + 1) & 1;
+                    dn = __builtin_amdgcn_mfma_f32_16x16x4f16(av[th1][g1], bv[rh1][g1], zero, 0, 0, 0);
+                }
                 __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float &a_ = acc[4 * g + (r >> 2)][8 * th + 4 * rh + (r & 3)];
+                    a_ = __builtin_fmaf(sc[th][rh][r & 3], d[r], a_);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                d = dn;
             }
         }
         if (c + 1 < chunks) stash(stage[(c + 1) & 1]);
         __syncthreads();
     }
-    const int row = r0 + rwl + i;
-    if (row >= w.rows) return;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-        const int t = t0 + twl + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (t >= tokens) continue;
+        // position v: token half v / 8, row half (v / 4) % 2, token 4 s4 + v % 4 of the half
+        const int row = r0 + rwl + 16 * ((v >> 2) & 1) + i;
+        const int t = t0 + twl + 16 * (v >> 3) + 4 * s4 + (v & 3);
+        if (row >= w.rows || t >= tokens) continue;
         // the horizontal sum of fortai_q8_dot.c:323-330
         const float sum = ((acc[0][v] + acc[4][v]) + (acc[2][v] + acc[6][v])) +
             ((acc[1][v] + acc[5][v]) + (acc[3][v] + acc[7][v]));
