@@ -103,11 +103,12 @@ def test_mmq_prefill_shape(ctx, oracle):
     W.free()
 
 
-@pytest.mark.parametrize("rows,width,tokens", [(13, 96, 5), (200, 1024, 37), (3584, 1024, 64), (1024, 3584, 70),
-                                               (9216, 2560, 130)])
+@pytest.mark.parametrize("rows,width,tokens", [(13, 96, 5), (200, 1024, 37), (88, 256, 21), (3584, 1024, 64),
+                                               (1024, 3584, 70), (9216, 2560, 130)])
 def test_mmq_lane_order_bit_identical(ctx, oracle, rows, width, tokens):
     """q8_mmq_exact_kernel: every output equals the reference matvec of its
-    token bit for bit (ragged rows, partial token tiles, a 4B FFN shape); the
+    token bit for bit (ragged rows, in the first or the second 16-row half of
+    a wave's rows, partial token tiles, a 4B FFN shape); the
     residual epilogue adds in place."""
     rng = np.random.default_rng(rows + 7 * width + tokens)
     w = synth.q8_blocks(rng, rows, width)
