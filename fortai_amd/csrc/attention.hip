@@ -612,6 +612,7 @@ __device__ __forceinline__ void attend_wide(const AttentionParams &p, int h, int
 
 // grid: (heads x ceil(value / 64), batch)
 __global__ __launch_bounds__(ea::kThreads) void attention_output_wide_kernel(const AttentionParams p_batch) {
+    FORTAI_TRACE_SCOPE(12);
     const AttentionParams p = attention_seq(p_batch, static_cast<int>(blockIdx.y));
     extern __shared__ __align__(16) float wide_lds[];
     __shared__ float red[8];

@@ -166,6 +166,7 @@ __global__ __launch_bounds__(kDeltaThreads) void gdn_delta_kernel(const GdnParam
 template <int HEAD>
 __global__ __launch_bounds__(HEAD * 8) void gdn_delta_gated_kernel(const GdnParams p_batch, const float *z_batch,
     const float *norm, float eps, void *q8l, int width) {
+    FORTAI_TRACE_SCOPE(11);
     const int seq = static_cast<int>(blockIdx.y);
     const GdnParams p = gdn_seq(p_batch, seq);
     constexpr int kThreads = HEAD * 8;

@@ -300,6 +300,7 @@ constexpr int kMaxBatch = 8;
 // min(s, batch - 1), so the slots past the batch repeat the last sequence.
 __global__ __launch_bounds__(128) void batch_output_norm_kernel(const float *__restrict__ x,
     const float *__restrict__ norm, float eps, int width, int batch, float *__restrict__ xnorm) {
+    FORTAI_TRACE_SCOPE(14);
     __shared__ double red[2];
     const int tid = static_cast<int>(threadIdx.x);
     const int slot = static_cast<int>(blockIdx.x);

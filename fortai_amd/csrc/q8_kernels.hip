@@ -537,6 +537,7 @@ constexpr int kPrepThreads = 512;  // activations up to 16384 wide
 
 template <Prologue PRO>
 __global__ __launch_bounds__(kPrepThreads) void q8l_prep_kernel(MatvecInput in, void *q8l) {
+    FORTAI_TRACE_SCOPE(10);
     __shared__ double red[kPrepThreads / 64];
     const int seq = static_cast<int>(blockIdx.x);
     const int chunks = (in.width / kQ8Block + 3) / 4;
@@ -585,6 +586,7 @@ __device__ __forceinline__ void scales_f(uint2 sc, float (&ws)[4]) {
 // makes the compiler wait for every prefetch at its head); CH == 0: any count.
 template <Epilogue EPI, int SPLIT, int G, int WAVES, int CH>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES >= 16 ? 4 : WAVES / 2))) void q8_batch_matvec_kernel(const BatchMatvecArgs args) {
+    FORTAI_TRACE_SCOPE(9);
     constexpr bool kPair = EPI == Epilogue::SILU_PAIR;
     constexpr int NS = kMaxBatch / SPLIT;
     extern __shared__ __align__(16) unsigned char lds[];
@@ -852,6 +854,7 @@ constexpr int kRingG = 4;  // chunks per ring group
 // single-sequence kernel's, rounding for rounding.
 template <Epilogue EPI, int GROUPS, int NS>
 __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const BatchMatvecArgs args) {
+    FORTAI_TRACE_SCOPE(8);
     constexpr int R = GROUPS < 8 ? GROUPS : 8;  // groups in flight per wave
     constexpr int kSlot = kRingG * 1024 + kRingG * 64;  // quants then scales of one group
     constexpr bool kTable = NS == 2;
@@ -972,10 +975,16 @@ __global__ __launch_bounds__(kBatchThreads) void q8_batch_ring_kernel(const Batc
     // the activations' direct-to-LDS copies were issued after the first R
     // groups: waiting for all of this wave's loads once covers both
     __builtin_amdgcn_s_waitcnt(0);
+    FORTAI_MV_MARK(0);
     // fully unrolled (the group count is a template parameter): the compiler's
     // load counters then know that group g is the oldest load in flight
 #pragma unroll
-    for (int g = 0; g < GROUPS; ++g) step(g, rq[g % R], rs[g % R]);
+    for (int g = 0; g < GROUPS; ++g) {
+        step(g, rq[g % R], rs[g % R]);
+        if (g == 0) FORTAI_MV_MARK(1);
+        if (g == GROUPS / 2) FORTAI_MV_MARK(2);
+    }
+    FORTAI_MV_MARK(3);
 #pragma unroll
     for (int k = 0; k < NS; ++k) acc[k] = row_hsum8(acc[k]);
 #pragma unroll
@@ -1133,6 +1142,7 @@ __global__ void q8_embedding_kernel(Q8Matrix w, const int64_t *token, int64_t to
 
 __global__ void f16_embedding_kernel(const uint16_t *table, int rows, int width, const int64_t *token,
     int64_t token_value, float *out) {
+    FORTAI_TRACE_SCOPE(15);
     const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
     if (i >= width) return;
     const int seq = static_cast<int>(blockIdx.y);  // batch: token[seq] -> row seq of out
