@@ -3,6 +3,8 @@
 # fortai_amd/wgtrace/libfortai_wgtrace.so: the decode kernels' sources with
 # trace.h force-included (the other objects are the library's own, so build
 # the library first: python -c "from fortai_amd import build; build.build()").
+# run.py reads the single-sequence decode step with it, run_batch.py the
+# batch-8 step.
 set -e
 HERE=$(cd "$(dirname "$0")" && pwd)
 ROOT=$(cd "$HERE/../.." && pwd)
